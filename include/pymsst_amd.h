@@ -1,0 +1,154 @@
+/*
+ * pymsst_amd: C ABI of the MI355X (gfx950) fused RoFormer layer kernels.
+ *
+ * Each entry point replaces one op of the reference's pybind11 extension
+ * (baicai-1145/pymsst src/pymsst/training/cuda/fused_band_split.cpp:731-753,
+ * kernels in fused_band_split.cu).  The cited file:line is the reference
+ * wrapper whose tensor contract the entry point implements.
+ *
+ * Conventions (all entry points):
+ *  - Plain device pointers and sizes; every tensor is dense and row-major
+ *    unless a stride argument says otherwise.  Storage dtype codes are
+ *    PMSST_F32 / PMSST_F16 / PMSST_BF16; arithmetic is fp32.
+ *  - Outputs are caller-allocated.  The library never allocates device
+ *    memory: reductions use a caller-provided workspace whose size the
+ *    matching *_workspace_size() reports for the current device.
+ *  - Work is enqueued on `stream` (a hipStream_t) and never synchronised.
+ *  - Returns PMSST_OK (0) or a negative code; pmsst_last_error() then holds
+ *    a message for the calling thread.
+ *  - Reductions over rows (dgamma, dW, dbias) are deterministic: fixed
+ *    partition, fixed summation order, no floating-point atomics.
+ */
+#ifndef PYMSST_AMD_H
+#define PYMSST_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { PMSST_F32 = 0, PMSST_F16 = 1, PMSST_BF16 = 2 };
+enum {
+  PMSST_OK = 0,
+  PMSST_EINVAL = -1,     /* bad shape, size, pointer or alignment */
+  PMSST_EDTYPE = -2,     /* unsupported dtype combination */
+  PMSST_ELAUNCH = -3,    /* HIP launch failure */
+  PMSST_EWORKSPACE = -4  /* workspace missing or too small */
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* pmsst_last_error(void);
+/* ABI revision of this header; bumped on any signature change. */
+int pmsst_abi_version(void);
+
+/* ------------------------------------------------------------------ RMSNorm
+ * y = x / max(||x||_2, 1e-12) * sqrt(dim) * gamma over the last axis of
+ * x[rows, dim].  inv_norm[rows] (fp32) = 1 / max(||x||, 1e-12).
+ * `normed` may be NULL: the normalised copy is then not written (the
+ * saved-input backward below recomputes it).
+ */
+
+/* fused_band_split.cpp:434-444 rms_norm_forward (.cu:1210-1249): x, gamma, out, normed in `dtype`. */
+int pmsst_rms_norm_forward(const void* x, const void* gamma, void* out, void* normed, float* inv_norm,
+                           int64_t rows, int64_t dim, int dtype, void* stream);
+/* fused_band_split.cpp:467-477 rms_norm_forward_fp32_gamma (.cu:1399-1438): gamma fp32, rest `dtype`. */
+int pmsst_rms_norm_forward_fp32_gamma(const void* x, const float* gamma, void* out, void* normed,
+                                      float* inv_norm, int64_t rows, int64_t dim, int dtype, void* stream);
+/* fused_band_split.cpp:500-510 rms_norm_forward_mixed (.cu:1588-1627): x `dtype`, gamma/out/normed fp32. */
+int pmsst_rms_norm_forward_mixed(const void* x, const float* gamma, float* out, float* normed, float* inv_norm,
+                                 int64_t rows, int64_t dim, int dtype, void* stream);
+
+/* Bytes of workspace every RMSNorm backward entry point needs for `dim`. */
+size_t pmsst_rms_norm_backward_workspace_size(int64_t rows, int64_t dim);
+
+/* fused_band_split.cpp:446-465 rms_norm_backward (.cu:1251-1397):
+ * grad_out, normed, gamma, grad_x, grad_gamma in `dtype`. */
+int pmsst_rms_norm_backward(const void* grad_out, const void* normed, const float* inv_norm, const void* gamma,
+                            void* grad_x, void* grad_gamma, int64_t rows, int64_t dim, int dtype, void* workspace,
+                            size_t workspace_bytes, void* stream);
+/* fused_band_split.cpp:479-498 rms_norm_backward_fp32_gamma (.cu:1440-1586): gamma/grad_gamma fp32. */
+int pmsst_rms_norm_backward_fp32_gamma(const void* grad_out, const void* normed, const float* inv_norm,
+                                       const float* gamma, void* grad_x, float* grad_gamma, int64_t rows,
+                                       int64_t dim, int dtype, void* workspace, size_t workspace_bytes,
+                                       void* stream);
+/* fused_band_split.cpp:512-534 rms_norm_backward_mixed (.cu:1629-1775): grad_out/normed/gamma/grad_gamma
+ * fp32, grad_x in `x_dtype` (the dtype of the forward input, the reference's x_meta). */
+int pmsst_rms_norm_backward_mixed(const float* grad_out, const float* normed, const float* inv_norm,
+                                  const float* gamma, void* grad_x, float* grad_gamma, int64_t rows, int64_t dim,
+                                  int x_dtype, void* workspace, size_t workspace_bytes, void* stream);
+/* Saved-input backward (no reference counterpart; same algebra as .cu:1251-1315 with
+ * normed = x * inv_norm * sqrt(dim) recomputed): lets the forward skip writing `normed`.
+ * grad_out, x, grad_x in `dtype`; gamma/grad_gamma in `gamma_dtype` (`dtype` or PMSST_F32). */
+int pmsst_rms_norm_backward_from_input(const void* grad_out, const void* x, const float* inv_norm,
+                                       const void* gamma, void* grad_x, void* grad_gamma, int64_t rows,
+                                       int64_t dim, int dtype, int gamma_dtype, void* workspace,
+                                       size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ rotary
+ * t[batch, seq, heads, dim] (bnhd); cos/sin[seq, dim/2] addressed as
+ * cos[n * cs_stride_seq + p * cs_stride_pair] (the reference's [1,N,1,D/2]
+ * table; strides let the caller pass the cos[..., ::2] view without a copy).
+ * Pair p = (t[2p], t[2p+1]) is rotated by angle (n, p).
+ */
+
+/* fused_band_split.cpp:390-410 rotary_forward (.cu:1076-1101,1130-1168). */
+int pmsst_rotary_forward(const void* t, const void* cos, const void* sin, void* out, int64_t batch, int64_t seq,
+                         int64_t heads, int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype,
+                         void* stream);
+/* fused_band_split.cpp:412-432 rotary_backward (.cu:1103-1128,1170-1208): transpose rotation. */
+int pmsst_rotary_backward(const void* grad_out, const void* cos, const void* sin, void* grad_t, int64_t batch,
+                          int64_t seq, int64_t heads, int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair,
+                          int dtype, void* stream);
+
+/* Fused q/k RMSNorm over the head dim + rotary + cast (no reference counterpart; composition of
+ * .cu:1399-1438 and .cu:1076-1101 with no intermediate round trip).  x/out/cos/sin in `dtype`,
+ * gamma[dim] in `gamma_dtype`; writes inv_norm[batch*seq*heads]. */
+int pmsst_rms_norm_rotary_forward(const void* x, const void* gamma, const void* cos, const void* sin, void* out,
+                                  float* inv_norm, int64_t batch, int64_t seq, int64_t heads, int64_t dim,
+                                  int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype, int gamma_dtype,
+                                  void* stream);
+/* Backward of the fused op from the saved input x and inv_norm. */
+size_t pmsst_rms_norm_rotary_backward_workspace_size(int64_t rows, int64_t dim);
+int pmsst_rms_norm_rotary_backward(const void* grad_out, const void* x, const float* inv_norm, const void* gamma,
+                                   const void* cos, const void* sin, void* grad_x, void* grad_gamma, int64_t batch,
+                                   int64_t seq, int64_t heads, int64_t dim, int64_t cs_stride_seq,
+                                   int64_t cs_stride_pair, int dtype, int gamma_dtype, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ band split
+ * Ragged per-band RMSNorm + Linear (BS-RoFormer / MBR front end).  Band b spans
+ * columns [off_b, off_b + I_b) of x with off = exclusive prefix sum of
+ * dim_inputs; F = sum I_b.  gamma[F]; weight = band-major concatenation of the
+ * per-band [O, I_b] Linear weights (sum_b O*I_b elements); bias[NB, O] or NULL;
+ * out[rows, NB, O]; normed[rows, F] or NULL; inv_norm[rows, NB] fp32.
+ * dim_offsets is the device copy of the NB+1 prefix sums, dim_inputs the host
+ * copy of the NB widths.  1 <= O <= 512.
+ */
+
+/* fused_band_split.cpp:271-314 band_split_ragged_forward (.cu:589-739).  With equal widths it also
+ * implements fused_band_split.cpp:141-170 band_split_forward (.cu:13-122): x_row_stride is then the
+ * row pitch of the [M, G, I] group view. */
+int pmsst_band_split_ragged_forward(const void* x, int64_t x_row_stride, const void* gamma, const void* weight,
+                                    const void* bias, const int64_t* dim_offsets, const int64_t* dim_inputs,
+                                    int64_t band_count, int64_t rows, int64_t out_features, void* out, void* normed,
+                                    float* inv_norm, int dtype, void* stream);
+size_t pmsst_band_split_ragged_backward_workspace_size(int64_t rows, int64_t total_in);
+/* fused_band_split.cpp:316-363 band_split_ragged_backward (.cu:741-1003).  With equal widths it also
+ * implements band_split_backward / _v2 / _v3 (fused_band_split.cpp:172-269, .cu:125-587).
+ * `saved` is normed[rows, F] (saved_is_input = 0) or the forward input x[rows, F] (saved_is_input = 1,
+ * normed recomputed as x * inv_norm * sqrt(I_b)).  Outputs: grad_x[rows, F], grad_gamma[F],
+ * grad_weight (packed like weight), grad_bias[NB, O] or NULL. */
+int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, int saved_is_input,
+                                     const float* inv_norm, const void* gamma, const void* weight,
+                                     const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
+                                     int64_t rows, int64_t out_features, void* grad_x, void* grad_gamma,
+                                     void* grad_weight, void* grad_bias, int dtype, void* workspace,
+                                     size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PYMSST_AMD_H */

@@ -1,0 +1,422 @@
+"""numpy restatement of the reference's fused layer kernels (test infrastructure only).
+
+Reference: baicai-1145/pymsst ``src/pymsst/training/cuda/fused_band_split.cu``
+(``.cu`` below) and ``src/pymsst/training/fused_roformer.py`` (``fr.py``).
+
+Conventions
+-----------
+* Inputs are float arrays holding values exactly representable in their
+  storage dtype ``dt`` (one of ``"f32"``, ``"f16"``, ``"bf16"``).
+* Arithmetic is float64 (``acc=np.float64``) or float32 when the oracle is
+  timed as the CPU baseline (``acc=np.float32``).
+* Every stored output is rounded to the storage dtype the reference kernel
+  writes (``static_cast<scalar_t>``); ``inv_norm`` is always fp32
+  (fused_band_split.cpp:342,459).
+* Functions suffixed ``_lean`` / ``rms_norm_rotary_*`` / ``mask_mlp_*``
+  restate fused variants this build adds; they are compositions of the
+  reference functions above them, with the intermediate left unrounded.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from .dtypes import round_to
+
+__all__ = [
+    "rms_norm_forward",
+    "rms_norm_backward",
+    "rms_norm_backward_lean",
+    "rotary_forward",
+    "rotary_backward",
+    "rotary_tables",
+    "rms_norm_rotary_forward",
+    "rms_norm_rotary_backward",
+    "band_split_forward",
+    "band_split_backward",
+    "band_split_ragged_forward",
+    "band_split_ragged_backward",
+    "band_split_ragged_backward_lean",
+    "grouped_linear_forward",
+    "grouped_linear_backward",
+    "mask_estimator_final_forward",
+    "mask_estimator_final_backward",
+    "mask_mlp_forward",
+    "mask_mlp_backward",
+    "sigmoid",
+]
+
+_EPS = 1.0e-12
+
+
+def _f(a, acc):
+    return np.asarray(a, dtype=acc)
+
+
+def _inv_out(inv, dt):
+    """``inv_norm`` is stored as fp32 by every reference kernel; kept exact when ``dt == "f64"``."""
+    return round_to(inv, "f64" if dt == "f64" else "f32")
+
+
+def _inv_norm(x, acc):
+    """``inv = 1/max(sqrt(sum x^2), 1e-12)`` over the last axis (.cu:48-50)."""
+    ss = np.sum(x * x, axis=-1)
+    return 1.0 / np.maximum(np.sqrt(ss), acc(_EPS))
+
+
+# --------------------------------------------------------------------------- RMSNorm
+
+
+def rms_norm_forward(x, gamma, dt: str, mode: str = "plain", acc=np.float64):
+    """RMSNorm forward over the last axis.
+
+    Follows .cu:1210-1249 (``mode="plain"``: gamma in ``dt``),
+    .cu:1399-1438 (``"fp32_gamma"``: gamma fp32, outputs in ``dt``) and
+    .cu:1588-1627 (``"mixed"``: gamma fp32, ``out``/``normed`` fp32).
+
+    ``n = x * inv * sqrt(D)``, ``out = n * gamma``; ``out`` is formed from the
+    unrounded ``n`` (.cu:1244-1247).  Returns ``(out, normed, inv_norm)``.
+    """
+    x = _f(x, acc)
+    gamma = _f(gamma, acc)
+    dim = x.shape[-1]
+    inv = _inv_norm(x, acc)
+    n = x * inv[..., None] * acc(math.sqrt(dim))
+    out_dt = "f32" if mode == "mixed" else dt
+    out = round_to(n * gamma, out_dt)
+    normed = round_to(n, out_dt)
+    return out, normed, _inv_out(inv, dt)
+
+
+def rms_norm_backward(grad_out, normed, inv_norm, gamma, dt: str, mode: str = "plain", acc=np.float64):
+    """RMSNorm backward from saved ``normed``/``inv_norm``.
+
+    Follows .cu:1251-1315 (plain), .cu:1440-1504 (fp32_gamma) and
+    .cu:1629-1691 (mixed: ``grad_out``/``normed`` fp32, ``grad_x`` in ``dt``):
+    ``gn = dy*gamma``, ``dot = sum(gn*normed)``,
+    ``dx = inv*(gn*sqrt(D) - normed*dot/sqrt(D))``, ``dgamma = sum_rows dy*normed``.
+    ``dgamma`` is stored in gamma's dtype (``dt`` for plain, fp32 otherwise).
+    """
+    dy = _f(grad_out, acc)
+    n = _f(normed, acc)
+    inv = _f(inv_norm, acc)
+    gamma = _f(gamma, acc)
+    dim = dy.shape[-1]
+    scale = acc(math.sqrt(dim))
+    gn = dy * gamma
+    dot = np.sum(gn * n, axis=-1, keepdims=True)
+    dx = inv.reshape(dot.shape) * (gn * scale - n * (dot / scale))
+    dgamma = np.sum((dy * n).reshape(-1, dim), axis=0)
+    g_dt = dt if mode == "plain" else "f32"
+    return round_to(dx, dt), round_to(dgamma, g_dt)
+
+
+def rms_norm_backward_lean(grad_out, x, inv_norm, gamma, dt: str, gamma_dt: str | None = None, acc=np.float64):
+    """RMSNorm backward that recomputes ``n = x*inv*sqrt(D)`` from the saved input.
+
+    Same algebra as :func:`rms_norm_backward` (.cu:1251-1315) with the saved
+    ``normed`` replaced by its unrounded value; used by this build's
+    ``_FusedRMSNorm`` fast path, which saves ``x`` instead of writing ``normed``.
+    """
+    x = _f(x, acc)
+    dim = x.shape[-1]
+    n = x * _f(inv_norm, acc).reshape(*x.shape[:-1], 1) * acc(math.sqrt(dim))
+    mode = "plain" if (gamma_dt or dt) == dt else "fp32_gamma"
+    return rms_norm_backward(grad_out, n, inv_norm, gamma, dt, mode, acc)
+
+
+# --------------------------------------------------------------------------- rotary
+
+
+def rotary_tables(seq_len: int, dim: int, theta: float = 10000.0):
+    """RoFormer tables ``cos/sin[n, p] = cos/sin(n * theta**(-2p/dim))``, shape ``[N, dim/2]``.
+
+    The reference passes ``cos[..., ::2]`` of the pairwise-repeated stock table
+    (fr.py:727), i.e. one value per adjacent pair; table construction itself
+    lives in pymss-core and is restated from the public RoFormer definition.
+    """
+    p = np.arange(0, dim, 2, dtype=np.float64)[: dim // 2]
+    inv_freq = 1.0 / (theta ** (p / dim))
+    ang = np.arange(seq_len, dtype=np.float64)[:, None] * inv_freq[None, :]
+    return np.cos(ang), np.sin(ang)
+
+
+def _rot(t, cos, sin, acc, sign):
+    t = _f(t, acc)
+    b, n, h, d = t.shape
+    c = _f(cos, acc).reshape(1, n, 1, d // 2)
+    s = _f(sin, acc).reshape(1, n, 1, d // 2) * sign
+    e = t[..., 0::2]
+    o = t[..., 1::2]
+    out = np.empty_like(t)
+    out[..., 0::2] = e * c - o * s
+    out[..., 1::2] = o * c + e * s
+    return out
+
+
+def rotary_forward(t, cos, sin, dt: str, acc=np.float64):
+    """Adjacent-pair rotation of ``t[B,N,H,D]`` (.cu:1076-1101):
+    ``(e, o) -> (e*c - o*s, o*c + e*s)`` with ``c, s = cos/sin[n, pair]``."""
+    return round_to(_rot(t, cos, sin, acc, 1.0), dt)
+
+
+def rotary_backward(grad_out, cos, sin, dt: str, acc=np.float64):
+    """Transpose rotation (.cu:1103-1128): ``(ge*c + go*s, -ge*s + go*c)``."""
+    return round_to(_rot(grad_out, cos, sin, acc, -1.0), dt)
+
+
+def rms_norm_rotary_forward(x, gamma, cos, sin, dt: str, acc=np.float64):
+    """Fused q/k RMSNorm over the head dim followed by rotary, one rounding.
+
+    Composition of .cu:1399-1438 (gamma in its own dtype) and .cu:1076-1101
+    with ``n*gamma`` kept unrounded.  Returns ``(out, inv_norm)``.
+    """
+    x = _f(x, acc)
+    dim = x.shape[-1]
+    inv = _inv_norm(x, acc)
+    y = x * inv[..., None] * acc(math.sqrt(dim)) * _f(gamma, acc)
+    return round_to(_rot(y, cos, sin, acc, 1.0), dt), _inv_out(inv, dt)
+
+
+def rms_norm_rotary_backward(grad_out, x, inv_norm, gamma, cos, sin, dt: str, gamma_dt: str, acc=np.float64):
+    """Backward of :func:`rms_norm_rotary_forward`: ``g = rot^T(dy)`` then the
+    RMSNorm backward of .cu:1251-1315 on ``g`` with ``n`` recomputed from ``x``."""
+    g = _rot(grad_out, cos, sin, acc, -1.0)
+    x = _f(x, acc)
+    dim = x.shape[-1]
+    inv = _f(inv_norm, acc).reshape(x.shape[:-1])
+    n = x * inv[..., None] * acc(math.sqrt(dim))
+    scale = acc(math.sqrt(dim))
+    gn = g * _f(gamma, acc)
+    dot = np.sum(gn * n, axis=-1, keepdims=True)
+    dx = inv[..., None] * (gn * scale - n * (dot / scale))
+    dgamma = np.sum((g * n).reshape(-1, dim), axis=0)
+    return round_to(dx, dt), round_to(dgamma, gamma_dt)
+
+
+# --------------------------------------------------------------------------- band split
+
+
+def band_split_forward(x, gamma, weight, bias, dt: str, acc=np.float64):
+    """Equal-width band group ``x[M,G,I]``, ``gamma[G,I]``, ``weight[G,O,I]``, ``bias[G,O]|None``.
+
+    .cu:13-71 / fr.py:1265-1271: ``n = x*inv*sqrt(I)``,
+    ``out = bias + sum_i (n*gamma)_i W_oi``.  Returns ``(out, normed, inv_norm)``.
+    """
+    x = _f(x, acc)
+    dim_in = x.shape[-1]
+    inv = _inv_norm(x, acc)
+    n = x * inv[..., None] * acc(math.sqrt(dim_in))
+    feat = n * _f(gamma, acc)[None]
+    out = np.einsum("mgi,goi->mgo", feat, _f(weight, acc))
+    if bias is not None:
+        out = out + _f(bias, acc)[None]
+    return round_to(out, dt), round_to(n, dt), _inv_out(inv, dt)
+
+
+def band_split_backward(grad_out, normed, inv_norm, gamma, weight, has_bias: bool, dt: str, acc=np.float64):
+    """Backward of :func:`band_split_forward` (.cu:125-247; v2/v3 .cu:314-587 compute the same values).
+
+    ``gs = dy W``, ``gn = gs*gamma``, ``dx = inv*(gn*sqrt(I) - n*(gn.n)/sqrt(I))``,
+    ``dW = sum_m dy (n*gamma)``, ``db = sum_m dy``, ``dgamma = sum_m gs*n``.
+    Returns ``(dx, dgamma, dW, db|None)``.
+    """
+    dy = _f(grad_out, acc)
+    n = _f(normed, acc)
+    inv = _f(inv_norm, acc)
+    gamma = _f(gamma, acc)
+    weight = _f(weight, acc)
+    dim_in = n.shape[-1]
+    scale = acc(math.sqrt(dim_in))
+    gs = np.einsum("mgo,goi->mgi", dy, weight)
+    gn = gs * gamma[None]
+    dot = np.sum(gn * n, axis=-1, keepdims=True)
+    dx = inv[..., None] * (gn * scale - n * (dot / scale))
+    dW = np.einsum("mgo,mgi->goi", dy, n * gamma[None])
+    db = dy.sum(axis=0) if has_bias else None
+    dgamma = np.sum(gs * n, axis=0)
+    return (
+        round_to(dx, dt),
+        round_to(dgamma, dt),
+        round_to(dW, dt),
+        round_to(db, dt) if db is not None else None,
+    )
+
+
+def _offsets(dim_inputs):
+    off = [0]
+    for d in dim_inputs:
+        off.append(off[-1] + int(d))
+    return off
+
+
+def band_split_ragged_forward(x, gammas, weights, biases, dim_inputs, dt: str, acc=np.float64):
+    """Ragged band split over ``x[M,F]`` (.cu:589-652): band ``b`` spans
+    ``offsets[b]:offsets[b+1]``.  Returns ``(out[M,NB,O], normed[M,F], inv[M,NB])``."""
+    x = _f(x, acc)
+    off = _offsets(dim_inputs)
+    outs, normed, invs = [], [], []
+    for b in range(len(dim_inputs)):
+        xb = x[:, off[b] : off[b + 1]][:, None, :]
+        o, n, i = band_split_forward(
+            xb, _f(gammas[b], acc)[None], _f(weights[b], acc)[None], _f(biases[b], acc)[None], dt, acc
+        )
+        outs.append(o[:, 0])
+        normed.append(n[:, 0])
+        invs.append(i[:, 0])
+    return np.stack(outs, axis=1), np.concatenate(normed, axis=1), np.stack(invs, axis=1)
+
+
+def band_split_ragged_backward(grad_out, normed, inv_norm, gammas, weights, dim_inputs, dt: str, acc=np.float64):
+    """Ragged backward (.cu:741-879).  Returns ``(dx[M,F], [dgamma_b], [dW_b], [db_b])``."""
+    off = _offsets(dim_inputs)
+    dy = _f(grad_out, acc)
+    n = _f(normed, acc)
+    inv = _f(inv_norm, acc)
+    dxs, dgs, dws, dbs = [], [], [], []
+    for b in range(len(dim_inputs)):
+        dx, dg, dw, db = band_split_backward(
+            dy[:, b : b + 1],
+            n[:, off[b] : off[b + 1]][:, None, :],
+            inv[:, b : b + 1],
+            _f(gammas[b], acc)[None],
+            _f(weights[b], acc)[None],
+            True,
+            dt,
+            acc,
+        )
+        dxs.append(dx[:, 0])
+        dgs.append(dg[0])
+        dws.append(dw[0])
+        dbs.append(db[0])
+    return np.concatenate(dxs, axis=1), dgs, dws, dbs
+
+
+def band_split_ragged_backward_lean(grad_out, x, inv_norm, gammas, weights, dim_inputs, dt: str, acc=np.float64):
+    """Ragged backward with ``normed`` recomputed (unrounded) from the saved input ``x``:
+    same algebra as .cu:741-879; used by this build's saved-input fast path."""
+    x = _f(x, acc)
+    inv = _f(inv_norm, acc)
+    off = _offsets(dim_inputs)
+    n = np.empty_like(x)
+    for b in range(len(dim_inputs)):
+        w = off[b + 1] - off[b]
+        n[:, off[b] : off[b + 1]] = x[:, off[b] : off[b + 1]] * inv[:, b : b + 1] * math.sqrt(w)
+    return band_split_ragged_backward(grad_out, n, inv_norm, gammas, weights, dim_inputs, dt, acc)
+
+
+# --------------------------------------------------------------------------- grouped linear
+
+
+def grouped_linear_forward(x, weight, bias, dt: str, acc=np.float64):
+    """``out[m,g,o] = bias[g,o] + sum_i x[m,g,i] W[g,o,i]`` (.cu:1005-1030; bmm form tts.py:28-37)."""
+    out = np.einsum("mgi,goi->mgo", _f(x, acc), _f(weight, acc))
+    if bias is not None:
+        out = out + _f(bias, acc)[None]
+    return round_to(out, dt)
+
+
+def grouped_linear_backward(grad_out, x, weight, has_bias: bool, dt: str, acc=np.float64):
+    """Backward of grouped linear (fr.py:1042-1048): ``dx = dy W``, ``dW = dy^T x``, ``db = sum_m dy``."""
+    dy = _f(grad_out, acc)
+    dx = np.einsum("mgo,goi->mgi", dy, _f(weight, acc))
+    dW = np.einsum("mgo,mgi->goi", dy, _f(x, acc))
+    db = dy.sum(axis=0) if has_bias else None
+    return round_to(dx, dt), round_to(dW, dt), (round_to(db, dt) if db is not None else None)
+
+
+# --------------------------------------------------------------------------- mask estimator
+
+
+def sigmoid(z):
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+def mask_estimator_final_forward(x, weights, bias, dim_inputs, dt: str, acc=np.float64):
+    """Final per-band Linear ``H -> 2*I_b`` + bias + GLU (.cu:2515-2552 direct; .cu:2283-2310 grouped).
+
+    ``x[M,NB,H]``; ``weights[b]`` is ``[2*I_b, H]``; ``bias`` is flat ``[2F]`` with band
+    ``b`` at ``[2*off_b, 2*off_b + 2*I_b)``, left half first.
+    ``pre = x W^T + bias`` (stored), ``out = left * sigmoid(gate)``.
+    Returns ``(out[M,F], pre[M,2F])``.
+    """
+    x = _f(x, acc)
+    bias = _f(bias, acc)
+    off = _offsets(dim_inputs)
+    outs, pres = [], []
+    for b, d in enumerate(dim_inputs):
+        p = x[:, b, :] @ _f(weights[b], acc).T + bias[2 * off[b] : 2 * off[b] + 2 * d]
+        left, gate = p[:, :d], p[:, d:]
+        outs.append(left * sigmoid(gate))
+        pres.append(p)
+    return round_to(np.concatenate(outs, axis=1), dt), round_to(np.concatenate(pres, axis=1), dt)
+
+
+def mask_estimator_final_backward(grad_out, x, pre, weights, dim_inputs, dt: str, acc=np.float64):
+    """Backward of :func:`mask_estimator_final_forward` (.cu:2312-2367, .cu:2585-2704).
+
+    From the saved ``pre``: ``dL = g*s``, ``dG = g*L*s*(1-s)`` with ``s = sigmoid(G)``;
+    ``dbias = sum_m dpre``, ``dx_b = dpre_b W_b``, ``dW_b = dpre_b^T x_b``.
+    Returns ``(dx[M,NB,H], dbias[2F], [dW_b])``.
+    """
+    g = _f(grad_out, acc)
+    x = _f(x, acc)
+    pre = _f(pre, acc)
+    off = _offsets(dim_inputs)
+    dx = np.empty_like(x)
+    dbias = []
+    dws = []
+    for b, d in enumerate(dim_inputs):
+        p = pre[:, 2 * off[b] : 2 * off[b] + 2 * d]
+        left, gate = p[:, :d], p[:, d:]
+        s = sigmoid(gate)
+        gb = g[:, off[b] : off[b] + d]
+        dpre = np.concatenate([gb * s, gb * left * s * (1.0 - s)], axis=1)
+        dbias.append(dpre.sum(axis=0))
+        dx[:, b, :] = dpre @ _f(weights[b], acc)
+        dws.append(round_to(dpre.T @ x[:, b, :], dt))
+    return round_to(dx, dt), round_to(np.concatenate(dbias), dt), dws
+
+
+def mask_mlp_forward(x, w1, b1, weights2, bias2, dim_inputs, dt: str, acc=np.float64):
+    """Whole per-band mask MLP (depth 2): ``h = tanh(x_b W1_b^T + b1_b)`` then the final
+    Linear + GLU of :func:`mask_estimator_final_forward`.
+
+    Hidden layer follows grouped_linear (.cu:1005-1030) + ``inference_tanh``
+    (fr.py:340,538); ``w1[NB,Hd,dim]``, ``b1[NB,Hd]``.  ``h`` is kept unrounded
+    (it never leaves the fused kernel).  Returns ``out[M,F]``.
+    """
+    h = np.tanh(np.einsum("mgi,goi->mgo", _f(x, acc), _f(w1, acc)) + _f(b1, acc)[None])
+    out, _ = mask_estimator_final_forward(h, weights2, bias2, dim_inputs, dt, acc)
+    return out
+
+
+def mask_mlp_backward(grad_out, x, w1, b1, weights2, bias2, dim_inputs, dt: str, acc=np.float64):
+    """Backward of :func:`mask_mlp_forward` with ``h`` recomputed.
+
+    Returns ``(dx[M,NB,dim], dW1[NB,Hd,dim], db1[NB,Hd], [dW2_b], dbias2[2F])``.
+    """
+    x = _f(x, acc)
+    w1 = _f(w1, acc)
+    h = np.tanh(np.einsum("mgi,goi->mgo", x, w1) + _f(b1, acc)[None])
+    pre = []
+    off = _offsets(dim_inputs)
+    b2 = _f(bias2, acc)
+    for b, d in enumerate(dim_inputs):
+        pre.append(h[:, b, :] @ _f(weights2[b], acc).T + b2[2 * off[b] : 2 * off[b] + 2 * d])
+    pre = np.concatenate(pre, axis=1)
+    # unrounded backward through the final layer
+    dh, dbias2, dws2 = mask_estimator_final_backward(grad_out, h, pre, weights2, dim_inputs, "f64", acc)
+    dz = dh * (1.0 - h * h)
+    dx = np.einsum("mgo,goi->mgi", dz, w1)
+    dW1 = np.einsum("mgo,mgi->goi", dz, x)
+    db1 = dz.sum(axis=0)
+    return (
+        round_to(dx, dt),
+        round_to(dW1, dt),
+        round_to(db1, dt),
+        [round_to(w, dt) for w in dws2],
+        round_to(dbias2, dt),
+    )

@@ -1,0 +1,518 @@
+"""Torch-facing extension object with the reference's op names, backed by the C ABI.
+
+``HipFusedExtension`` is the MI355X counterpart of the reference's pybind11
+module ``pymsst_fused_band_split`` (baicai-1145/pymsst
+``src/pymsst/training/cuda/fused_band_split.cpp:731-753``): the same op names,
+argument order, return lists and argument checks (raised as ``RuntimeError``
+with the reference's messages, ``.cpp:141-729``).  Outputs are allocated here
+with ``torch.empty`` on the input's device and every kernel is enqueued on
+torch's current stream for that device.  Ops this build adds beyond the
+reference (saved-input RMSNorm backward, fused q/k norm + rotary, ...) carry
+docstrings saying so.
+
+There is no CPU or PyTorch fallback in this module: every op runs the HIP
+kernels or raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import PmsstError, check, dtype_code
+
+
+def _req(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _ptr(t: torch.Tensor | None):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class _DeviceGuard:
+    __slots__ = ("dev", "prev")
+
+    def __init__(self, device: torch.device):
+        self.dev = device.index
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if self.dev is not None and cur != self.dev:
+            self.prev = cur
+            torch.cuda.set_device(self.dev)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+class HipFusedExtension:
+    """Duck-typed replacement for the reference's extension module (``fr.py:71`` ``extension=``)."""
+
+    def __init__(self):
+        self._lib = _lib.load_library()
+        self._band_cache = {}
+
+    # ------------------------------------------------------------------ RMSNorm
+
+    def _rms_check_fwd(self, x, gamma, fp32_gamma: bool):
+        _req(x.is_cuda, "x must be a CUDA tensor")
+        _req(gamma.is_cuda, "gamma must be a CUDA tensor")
+        _req(x.dim() >= 2, "x must have at least 2 dimensions")
+        _req(gamma.dim() == 1, "gamma must have shape [D]")
+        _req(gamma.size(0) == x.size(-1), "gamma dimension must match x last dimension")
+        if fp32_gamma:
+            _req(gamma.dtype == torch.float32, "gamma must be float32")
+        else:
+            _req(gamma.dtype == x.dtype, "gamma dtype must match x")
+
+    def _rms_fwd(self, fn_name, x, gamma, out_dtype, write_normed=True):
+        x = x.contiguous()
+        gamma = gamma.contiguous()
+        dim = x.size(-1)
+        rows = x.numel() // dim if dim else 0
+        out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+        normed = torch.empty(x.shape, dtype=out_dtype, device=x.device) if write_normed else None
+        inv = torch.empty((rows,), dtype=torch.float32, device=x.device)
+        with _DeviceGuard(x.device):
+            rc = getattr(self._lib, fn_name)(
+                _ptr(x), _ptr(gamma), _ptr(out), _ptr(normed), _ptr(inv), rows, dim, dtype_code(x.dtype),
+                _stream(x.device),
+            )
+        check(rc, fn_name)
+        return [out, normed, inv] if write_normed else [out, inv]
+
+    def _rms_check_bwd(self, grad_out, normed, inv_norm, gamma):
+        _req(grad_out.is_cuda, "grad_out must be a CUDA tensor")
+        _req(normed.is_cuda, "normed must be a CUDA tensor")
+        _req(inv_norm.is_cuda, "inv_norm must be a CUDA tensor")
+        _req(gamma.is_cuda, "gamma must be a CUDA tensor")
+        _req(grad_out.dim() >= 2, "grad_out must have at least 2 dimensions")
+        _req(normed.shape == grad_out.shape, "normed shape must match grad_out")
+        _req(gamma.dim() == 1, "gamma must have shape [D]")
+        _req(gamma.size(0) == grad_out.size(-1), "gamma dimension must match grad_out last dimension")
+        _req(inv_norm.dim() == 1, "inv_norm must have shape [M]")
+        _req(inv_norm.size(0) * gamma.size(0) == grad_out.numel(), "inv_norm length must match flattened rows")
+        _req(inv_norm.dtype == torch.float32, "inv_norm must be float32")
+
+    def _rms_bwd(self, fn_name, grad_out, nsrc, inv_norm, gamma, dx_dtype, dgamma_dtype, extra_dtype=None):
+        grad_out = grad_out.contiguous()
+        nsrc = nsrc.contiguous()
+        gamma = gamma.contiguous()
+        inv_norm = inv_norm.contiguous()
+        dim = grad_out.size(-1)
+        rows = grad_out.numel() // dim if dim else 0
+        dx = torch.empty(grad_out.shape, dtype=dx_dtype, device=grad_out.device)
+        dgamma = torch.empty((dim,), dtype=dgamma_dtype, device=grad_out.device)
+        ws_bytes = self._lib.pmsst_rms_norm_backward_workspace_size(rows, dim)
+        ws = _workspace(ws_bytes, grad_out.device)
+        args = [_ptr(grad_out), _ptr(nsrc), _ptr(inv_norm), _ptr(gamma), _ptr(dx), _ptr(dgamma), rows, dim]
+        if fn_name == "pmsst_rms_norm_backward_mixed":
+            args.append(dtype_code(dx_dtype))
+        elif fn_name == "pmsst_rms_norm_backward_from_input":
+            args += [dtype_code(grad_out.dtype), dtype_code(extra_dtype)]
+        else:
+            args.append(dtype_code(grad_out.dtype))
+        args += [_ptr(ws), ws.numel(), _stream(grad_out.device)]
+        with _DeviceGuard(grad_out.device):
+            rc = getattr(self._lib, fn_name)(*args)
+        check(rc, fn_name)
+        return [dx, dgamma]
+
+    def rms_norm_forward(self, x, gamma):
+        """``.cpp:434-444``: returns ``[out, normed, inv_norm]`` (x, gamma same dtype)."""
+        self._rms_check_fwd(x, gamma, fp32_gamma=False)
+        return self._rms_fwd("pmsst_rms_norm_forward", x, gamma, x.dtype)
+
+    def rms_norm_backward(self, grad_out, normed, inv_norm, gamma):
+        """``.cpp:446-465``: returns ``[grad_x, grad_gamma]``."""
+        self._rms_check_bwd(grad_out, normed, inv_norm, gamma)
+        _req(normed.dtype == grad_out.dtype, "normed dtype must match grad_out")
+        _req(gamma.dtype == grad_out.dtype, "gamma dtype must match grad_out")
+        return self._rms_bwd("pmsst_rms_norm_backward", grad_out, normed, inv_norm, gamma, grad_out.dtype,
+                             grad_out.dtype)
+
+    def rms_norm_forward_fp32_gamma(self, x, gamma):
+        """``.cpp:467-477``: fp32 gamma, outputs in x dtype."""
+        self._rms_check_fwd(x, gamma, fp32_gamma=True)
+        return self._rms_fwd("pmsst_rms_norm_forward_fp32_gamma", x, gamma, x.dtype)
+
+    def rms_norm_backward_fp32_gamma(self, grad_out, normed, inv_norm, gamma):
+        """``.cpp:479-498``: fp32 gamma and grad_gamma."""
+        self._rms_check_bwd(grad_out, normed, inv_norm, gamma)
+        _req(normed.dtype == grad_out.dtype, "normed dtype must match grad_out")
+        _req(gamma.dtype == torch.float32, "gamma must be float32")
+        return self._rms_bwd("pmsst_rms_norm_backward_fp32_gamma", grad_out, normed, inv_norm, gamma,
+                             grad_out.dtype, torch.float32)
+
+    def rms_norm_forward_mixed(self, x, gamma):
+        """``.cpp:500-510``: x in its dtype, fp32 gamma, fp32 ``out``/``normed``."""
+        self._rms_check_fwd(x, gamma, fp32_gamma=True)
+        return self._rms_fwd("pmsst_rms_norm_forward_mixed", x, gamma, torch.float32)
+
+    def rms_norm_backward_mixed(self, grad_out, normed, inv_norm, gamma, x_meta):
+        """``.cpp:512-534``: fp32 grad_out/normed/gamma; grad_x in ``x_meta.dtype``."""
+        self._rms_check_bwd(grad_out, normed, inv_norm, gamma)
+        _req(x_meta.is_cuda, "x_meta must be a CUDA tensor")
+        _req(grad_out.dtype == torch.float32, "grad_out must be float32")
+        _req(normed.dtype == torch.float32, "normed must be float32")
+        _req(gamma.dtype == torch.float32, "gamma must be float32")
+        return self._rms_bwd("pmsst_rms_norm_backward_mixed", grad_out, normed, inv_norm, gamma, x_meta.dtype,
+                             torch.float32)
+
+    def rms_norm_forward_lean(self, x, gamma):
+        """Build addition: RMSNorm forward that skips writing ``normed``; returns ``[out, inv_norm]``.
+
+        ``gamma`` is in x's dtype or fp32; ``out`` is in x's dtype.  Pair with
+        :meth:`rms_norm_backward_from_input`, which recomputes ``normed`` from x.
+        """
+        self._rms_check_fwd(x, gamma, fp32_gamma=gamma.dtype == torch.float32)
+        name = "pmsst_rms_norm_forward_fp32_gamma" if gamma.dtype == torch.float32 else "pmsst_rms_norm_forward"
+        return self._rms_fwd(name, x, gamma, x.dtype, write_normed=False)
+
+    def rms_norm_backward_from_input(self, grad_out, x, inv_norm, gamma):
+        """Build addition: RMSNorm backward from the saved input (``normed = x*inv*sqrt(D)`` recomputed)."""
+        self._rms_check_bwd(grad_out, x, inv_norm, gamma)
+        _req(x.dtype == grad_out.dtype, "x dtype must match grad_out")
+        _req(gamma.dtype in (grad_out.dtype, torch.float32), "gamma dtype must match grad_out or be float32")
+        return self._rms_bwd("pmsst_rms_norm_backward_from_input", grad_out, x, inv_norm, gamma, grad_out.dtype,
+                             gamma.dtype, extra_dtype=gamma.dtype)
+
+    # ------------------------------------------------------------------ rotary
+
+    @staticmethod
+    def _rot_check(t, cos, sin, tname: str):
+        _req(t.is_cuda, f"{tname} must be a CUDA tensor")
+        _req(cos.is_cuda, "cos must be a CUDA tensor")
+        _req(sin.is_cuda, "sin must be a CUDA tensor")
+        _req(t.dim() == 4, f"{tname} must have shape [B, N, H, D]")
+        _req(cos.dim() == 4, "cos must have shape [1, N, 1, D/2]")
+        _req(sin.dim() == 4, "sin must have shape [1, N, 1, D/2]")
+        _req(t.size(3) % 2 == 0, f"{tname} last dimension must be even")
+        _req(cos.size(0) == 1 and cos.size(2) == 1, "cos must broadcast over batch and heads")
+        _req(sin.size(0) == 1 and sin.size(2) == 1, "sin must broadcast over batch and heads")
+        _req(cos.size(1) == t.size(1), f"cos sequence dimension must match {tname}")
+        _req(sin.size(1) == t.size(1), f"sin sequence dimension must match {tname}")
+        _req(cos.size(3) == t.size(3) // 2, f"cos rotary dimension must match {tname}")
+        _req(sin.size(3) == t.size(3) // 2, f"sin rotary dimension must match {tname}")
+        _req(cos.dtype == t.dtype, f"cos dtype must match {tname}")
+        _req(sin.dtype == t.dtype, f"sin dtype must match {tname}")
+
+    @staticmethod
+    def _tables(cos, sin):
+        # One stride pair for both tables: make them agree if they do not.
+        if cos.stride(1) != sin.stride(1) or cos.stride(3) != sin.stride(3):
+            cos, sin = cos.contiguous(), sin.contiguous()
+        return cos, sin, cos.stride(1), cos.stride(3)
+
+    def _rotary(self, fn_name, t, cos, sin):
+        t = t.contiguous()
+        cos, sin, s_seq, s_pair = self._tables(cos, sin)
+        out = torch.empty_like(t)
+        b, n, h, d = t.shape
+        with _DeviceGuard(t.device):
+            rc = getattr(self._lib, fn_name)(
+                _ptr(t), _ptr(cos), _ptr(sin), _ptr(out), b, n, h, d, s_seq, s_pair, dtype_code(t.dtype),
+                _stream(t.device),
+            )
+        check(rc, fn_name)
+        return out
+
+    def rotary_forward(self, t, cos, sin):
+        """``.cpp:390-410``: ``t[B,N,H,D]``, ``cos/sin[1,N,1,D/2]`` (strided views accepted)."""
+        self._rot_check(t, cos, sin, "t")
+        return self._rotary("pmsst_rotary_forward", t, cos, sin)
+
+    def rotary_backward(self, grad_out, cos, sin):
+        """``.cpp:412-432``: transpose rotation of ``grad_out``."""
+        self._rot_check(grad_out, cos, sin, "grad_out")
+        return self._rotary("pmsst_rotary_backward", grad_out, cos, sin)
+
+    def rms_norm_rotary_forward(self, x, gamma, cos, sin):
+        """Build addition: fused q/k RMSNorm over the head dim + rotary + cast.
+
+        ``x[B,N,H,D]`` in bf16/f16/f32, ``gamma[D]`` in x's dtype or fp32, tables as
+        :meth:`rotary_forward`.  Returns ``[out, inv_norm[B*N*H]]``.
+        """
+        self._rot_check(x, cos, sin, "x")
+        _req(gamma.is_cuda and gamma.dim() == 1 and gamma.size(0) == x.size(3), "gamma must have shape [D]")
+        _req(gamma.dtype in (x.dtype, torch.float32), "gamma dtype must match x or be float32")
+        x = x.contiguous()
+        gamma = gamma.contiguous()
+        cos, sin, s_seq, s_pair = self._tables(cos, sin)
+        b, n, h, d = x.shape
+        out = torch.empty_like(x)
+        inv = torch.empty((b * n * h,), dtype=torch.float32, device=x.device)
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_rms_norm_rotary_forward(
+                _ptr(x), _ptr(gamma), _ptr(cos), _ptr(sin), _ptr(out), _ptr(inv), b, n, h, d, s_seq, s_pair,
+                dtype_code(x.dtype), dtype_code(gamma.dtype), _stream(x.device),
+            )
+        check(rc, "pmsst_rms_norm_rotary_forward")
+        return [out, inv]
+
+    def rms_norm_rotary_backward(self, grad_out, x, inv_norm, gamma, cos, sin):
+        """Build addition: backward of :meth:`rms_norm_rotary_forward`; returns ``[grad_x, grad_gamma]``."""
+        self._rot_check(grad_out, cos, sin, "grad_out")
+        _req(x.shape == grad_out.shape and x.dtype == grad_out.dtype, "x must match grad_out")
+        _req(inv_norm.dtype == torch.float32 and inv_norm.numel() * x.size(3) == x.numel(),
+             "inv_norm length must match flattened rows")
+        grad_out = grad_out.contiguous()
+        x = x.contiguous()
+        gamma = gamma.contiguous()
+        cos, sin, s_seq, s_pair = self._tables(cos, sin)
+        b, n, h, d = x.shape
+        dx = torch.empty_like(x)
+        dgamma = torch.empty((d,), dtype=gamma.dtype, device=x.device)
+        ws_bytes = self._lib.pmsst_rms_norm_rotary_backward_workspace_size(b * n * h, d)
+        ws = _workspace(ws_bytes, x.device)
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_rms_norm_rotary_backward(
+                _ptr(grad_out), _ptr(x), _ptr(inv_norm), _ptr(gamma), _ptr(cos), _ptr(sin), _ptr(dx), _ptr(dgamma),
+                b, n, h, d, s_seq, s_pair, dtype_code(x.dtype), dtype_code(gamma.dtype), _ptr(ws), ws.numel(),
+                _stream(x.device),
+            )
+        check(rc, "pmsst_rms_norm_rotary_backward")
+        return [dx, dgamma]
+
+
+    # ------------------------------------------------------------------ band split
+
+    def _bands(self, dim_inputs, device: torch.device):
+        """Host ctypes widths + device int64 prefix sums, cached per (widths, device)."""
+        dims = tuple(int(d) for d in dim_inputs)
+        key = (dims, device.type, device.index)
+        ent = self._band_cache.get(key)
+        if ent is None:
+            _req(len(dims) > 0 and all(d > 0 for d in dims), "dim_inputs must be positive")
+            offs = [0]
+            for d in dims:
+                offs.append(offs[-1] + d)
+            host = (ctypes.c_int64 * len(dims))(*dims)
+            dev = torch.tensor(offs, dtype=torch.int64, device=device)
+            ent = (host, dev, offs)
+            self._band_cache[key] = ent
+        return ent
+
+    def band_split_ragged_forward_packed(self, x, gamma_all, weight_all, bias_all, dim_inputs, write_normed=True,
+                                         x_row_stride=None):
+        """Ragged band split forward on packed parameters (the kernels' native layout).
+
+        ``x[M, >=F]`` (row pitch ``x_row_stride``), ``gamma_all[F]``, ``weight_all`` the
+        band-major concatenation of the ``[O, I_b]`` weights, ``bias_all[NB*O]`` or ``None``.
+        Returns ``[out[M,NB,O], normed[M,F] | None, inv_norm[M,NB]]``.
+        """
+        host, dev_offs, offs = self._bands(dim_inputs, x.device)
+        nb, total = len(offs) - 1, offs[-1]
+        m = x.size(0)
+        o = weight_all.numel() // total
+        _req(o * total == weight_all.numel(), "packed weight size must be a multiple of the total width")
+        stride = x.stride(0) if x_row_stride is None else int(x_row_stride)
+        out = torch.empty((m, nb, o), dtype=x.dtype, device=x.device)
+        normed = torch.empty((m, total), dtype=x.dtype, device=x.device) if write_normed else None
+        inv = torch.empty((m, nb), dtype=torch.float32, device=x.device)
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_band_split_ragged_forward(
+                _ptr(x), stride, _ptr(gamma_all), _ptr(weight_all), _ptr(bias_all), _ptr(dev_offs), host, nb, m, o,
+                _ptr(out), _ptr(normed), _ptr(inv), dtype_code(x.dtype), _stream(x.device),
+            )
+        check(rc, "pmsst_band_split_ragged_forward")
+        return [out, normed, inv]
+
+    def band_split_ragged_backward_packed(self, grad_out, saved, saved_is_input, inv_norm, gamma_all, weight_all,
+                                          dim_inputs, has_bias=True):
+        """Ragged band split backward on packed parameters.
+
+        ``saved`` is ``normed[M,F]`` (``saved_is_input=False``) or the forward input
+        ``x[M,F]`` (``True``; normed recomputed).  Returns packed
+        ``[grad_x[M,F], grad_gamma[F], grad_weight (packed), grad_bias[NB*O] | None]``.
+        """
+        host, dev_offs, offs = self._bands(dim_inputs, grad_out.device)
+        nb, total = len(offs) - 1, offs[-1]
+        grad_out = grad_out.contiguous()
+        saved = saved.contiguous()
+        m = grad_out.size(0)
+        o = grad_out.size(-1)
+        dev = grad_out.device
+        dx = torch.empty((m, total), dtype=grad_out.dtype, device=dev)
+        dg = torch.empty((total,), dtype=grad_out.dtype, device=dev)
+        dw = torch.empty((o * total,), dtype=grad_out.dtype, device=dev)
+        db = torch.empty((nb * o,), dtype=grad_out.dtype, device=dev) if has_bias else None
+        ws = _workspace(self._lib.pmsst_band_split_ragged_backward_workspace_size(m, total), dev)
+        with _DeviceGuard(dev):
+            rc = self._lib.pmsst_band_split_ragged_backward(
+                _ptr(grad_out), _ptr(saved), 1 if saved_is_input else 0, _ptr(inv_norm.contiguous()),
+                _ptr(gamma_all), _ptr(weight_all), _ptr(dev_offs), host, nb, m, o, _ptr(dx), _ptr(dg), _ptr(dw),
+                _ptr(db), dtype_code(grad_out.dtype), _ptr(ws), ws.numel(), _stream(dev),
+            )
+        check(rc, "pmsst_band_split_ragged_backward")
+        return [dx, dg, dw, db]
+
+    def band_split_ragged_forward(self, x, gammas, weights, biases, dim_inputs, dim_offsets):
+        """``.cpp:271-314``: ``x[M, total]``, per-band ``gamma[I]``, ``weight[O, I]``, ``bias[O]`` lists.
+
+        Returns ``[out[M,NB,O], normed[M,total], inv_norm[M,NB]]``.  ``dim_offsets`` is
+        shape-checked; the kernels use prefix sums derived from ``dim_inputs``.
+        """
+        _req(x.is_cuda, "x must be a CUDA tensor")
+        _req(dim_offsets.is_cuda, "dim_offsets must be a CUDA tensor")
+        _req(x.dim() == 2, "x must have shape [M, total]")
+        _req(dim_offsets.dim() == 1, "dim_offsets must be 1D")
+        _req(dim_offsets.dtype == torch.int64, "dim_offsets must be int64")
+        _req(len(gammas) == len(weights), "gammas length must match weights length")
+        _req(len(biases) == len(weights), "biases length must match weights length")
+        _req(len(dim_inputs) == len(weights), "dim_inputs length must match weights length")
+        _req(dim_offsets.size(0) == len(weights) + 1, "dim_offsets length must be band count + 1")
+        _req(len(weights) > 0, "weights must not be empty")
+        out_features = weights[0].size(0)
+        total = 0
+        for g, w, b, d in zip(gammas, weights, biases, dim_inputs):
+            total += int(d)
+            _req(g.is_cuda, "gamma must be a CUDA tensor")
+            _req(w.is_cuda, "weight must be a CUDA tensor")
+            _req(b.is_cuda, "bias must be a CUDA tensor")
+            _req(g.dim() == 1, "gamma must have shape [I]")
+            _req(w.dim() == 2, "weight must have shape [O, I]")
+            _req(b.dim() == 1, "bias must have shape [O]")
+            _req(g.size(0) == d, "gamma dimension must match dim_inputs")
+            _req(w.size(0) == out_features, "all weights must share output dimension")
+            _req(w.size(1) == d, "weight input dimension must match dim_inputs")
+            _req(b.size(0) == out_features, "bias output dimension must match weight")
+            _req(g.dtype == x.dtype, "gamma dtype must match x")
+            _req(w.dtype == x.dtype, "weight dtype must match x")
+            _req(b.dtype == x.dtype, "bias dtype must match x")
+            _req(g.device == x.device, "gamma device must match x")
+            _req(w.device == x.device, "weight device must match x")
+            _req(b.device == x.device, "bias device must match x")
+        _req(x.size(1) == total, "x total dimension must match dim_inputs")
+        x = x.contiguous()
+        gamma_all = torch.cat([g.reshape(-1) for g in gammas])
+        weight_all = torch.cat([w.reshape(-1) for w in weights])
+        bias_all = torch.cat([b.reshape(-1) for b in biases])
+        return self.band_split_ragged_forward_packed(x, gamma_all, weight_all, bias_all, dim_inputs, True)
+
+    def band_split_ragged_backward(self, grad_out, normed, inv_norm, gammas, weights, dim_inputs, dim_offsets):
+        """``.cpp:316-363``: returns ``[grad_x, *grad_gammas, *grad_weights, *grad_biases]``."""
+        _req(grad_out.is_cuda, "grad_out must be a CUDA tensor")
+        _req(normed.is_cuda, "normed must be a CUDA tensor")
+        _req(inv_norm.is_cuda, "inv_norm must be a CUDA tensor")
+        _req(dim_offsets.is_cuda, "dim_offsets must be a CUDA tensor")
+        _req(grad_out.dim() == 3, "grad_out must have shape [M, B, O]")
+        _req(normed.dim() == 2, "normed must have shape [M, total]")
+        _req(inv_norm.dim() == 2, "inv_norm must have shape [M, B]")
+        _req(dim_offsets.dim() == 1, "dim_offsets must be 1D")
+        _req(dim_offsets.dtype == torch.int64, "dim_offsets must be int64")
+        _req(len(gammas) == len(weights), "gammas length must match weights length")
+        _req(len(dim_inputs) == len(weights), "dim_inputs length must match weights length")
+        _req(dim_offsets.size(0) == len(weights) + 1, "dim_offsets length must be band count + 1")
+        _req(len(weights) > 0, "weights must not be empty")
+        _req(normed.size(0) == grad_out.size(0), "normed M must match grad_out")
+        _req(inv_norm.size(0) == grad_out.size(0), "inv_norm M must match grad_out")
+        _req(inv_norm.size(1) == grad_out.size(1), "inv_norm band count must match grad_out")
+        _req(len(weights) == grad_out.size(1), "weights length must match grad_out band count")
+        _req(normed.dtype == grad_out.dtype, "normed dtype must match grad_out")
+        _req(inv_norm.dtype == torch.float32, "inv_norm must be float32")
+        out_features = grad_out.size(2)
+        total = 0
+        for g, w, d in zip(gammas, weights, dim_inputs):
+            total += int(d)
+            _req(g.dim() == 1, "gamma must have shape [I]")
+            _req(w.dim() == 2, "weight must have shape [O, I]")
+            _req(g.size(0) == d, "gamma dimension must match dim_inputs")
+            _req(w.size(0) == out_features, "weight output dimension must match grad_out")
+            _req(w.size(1) == d, "weight input dimension must match dim_inputs")
+            _req(g.dtype == grad_out.dtype, "gamma dtype must match grad_out")
+            _req(w.dtype == grad_out.dtype, "weight dtype must match grad_out")
+        _req(normed.size(1) == total, "normed total dimension must match dim_inputs")
+        gamma_all = torch.cat([g.reshape(-1) for g in gammas])
+        weight_all = torch.cat([w.reshape(-1) for w in weights])
+        dx, dg, dw, db = self.band_split_ragged_backward_packed(grad_out, normed, False, inv_norm, gamma_all,
+                                                                weight_all, dim_inputs, True)
+        dims = [int(d) for d in dim_inputs]
+        o = out_features
+        dgs = list(dg.split(dims))
+        dws = [v.view(o, d) for v, d in zip(dw.split([o * d for d in dims]), dims)]
+        dbs = list(db.view(len(dims), o).unbind(0))
+        return [dx, *dgs, *dws, *dbs]
+
+    def band_split_forward(self, x, gamma, weight, bias=None):
+        """``.cpp:141-170``: equal-width group ``x[M,G,I]`` (strided view allowed), ``gamma[G,I]``,
+        ``weight[G,O,I]``, ``bias[G,O]`` or ``None``.  Returns ``[out[M,G,O], normed[M,G,I], inv_norm[M,G]]``.
+
+        Runs the ragged kernel with G equal widths; a view whose inner two dims are dense is
+        read in place with its row pitch.
+        """
+        _req(x.is_cuda, "x must be a CUDA tensor")
+        _req(gamma.is_cuda, "gamma must be a CUDA tensor")
+        _req(weight.is_cuda, "weight must be a CUDA tensor")
+        if bias is not None:
+            _req(bias.is_cuda, "bias must be a CUDA tensor")
+        _req(x.dim() == 3, "x must have shape [M, G, I]")
+        _req(gamma.dim() == 2, "gamma must have shape [G, I]")
+        _req(weight.dim() == 3, "weight must have shape [G, O, I]")
+        _req(gamma.size(0) == x.size(1), "gamma group dimension must match x")
+        _req(gamma.size(1) == x.size(2), "gamma input dimension must match x")
+        _req(weight.size(0) == x.size(1), "weight group dimension must match x")
+        _req(weight.size(2) == x.size(2), "weight input dimension must match x")
+        if bias is not None:
+            _req(bias.dim() == 2, "bias must have shape [G, O]")
+            _req(bias.size(0) == x.size(1), "bias group dimension must match x")
+            _req(bias.size(1) == weight.size(1), "bias output dimension must match weight")
+        _req(gamma.dtype == x.dtype, "gamma dtype must match x")
+        _req(weight.dtype == x.dtype, "weight dtype must match x")
+        if bias is not None:
+            _req(bias.dtype == x.dtype, "bias dtype must match x")
+        m, g, i = x.shape
+        if not (x.stride(2) == 1 and x.stride(1) == i and x.stride(0) >= g * i):
+            x = x.contiguous()
+        out, normed, inv = self.band_split_ragged_forward_packed(
+            x, gamma.contiguous().reshape(-1), weight.contiguous().reshape(-1),
+            bias.contiguous().reshape(-1) if bias is not None else None, (i,) * g, True,
+            x_row_stride=x.stride(0) if m > 0 else g * i,
+        )
+        return [out, normed.view(m, g, i), inv]
+
+    def band_split_backward(self, grad_out, normed, inv_norm, gamma, weight, has_bias):
+        """``.cpp:172-203`` (and ``_v2`` ``.cpp:205-236``, ``_v3`` ``.cpp:238-269``, same values):
+        returns ``[grad_x[M,G,I], grad_gamma[G,I], grad_weight[G,O,I], grad_bias[G,O] | None]``."""
+        _req(grad_out.is_cuda, "grad_out must be a CUDA tensor")
+        _req(normed.is_cuda, "normed must be a CUDA tensor")
+        _req(inv_norm.is_cuda, "inv_norm must be a CUDA tensor")
+        _req(grad_out.dim() == 3, "grad_out must have shape [M, G, O]")
+        _req(normed.dim() == 3, "normed must have shape [M, G, I]")
+        _req(inv_norm.dim() == 2, "inv_norm must have shape [M, G]")
+        _req(gamma.dim() == 2 and weight.dim() == 3, "gamma must have shape [G, I] and weight [G, O, I]")
+        _req(normed.size(0) == grad_out.size(0) and normed.size(1) == grad_out.size(1),
+             "normed must match grad_out in M and G")
+        _req(weight.size(1) == grad_out.size(2), "weight output dimension must match grad_out")
+        _req(inv_norm.dtype == torch.float32, "inv_norm must be float32")
+        _req(normed.dtype == grad_out.dtype and gamma.dtype == grad_out.dtype and weight.dtype == grad_out.dtype,
+             "normed, gamma and weight dtype must match grad_out")
+        m, g, i = normed.shape
+        o = grad_out.size(2)
+        dx, dg, dw, db = self.band_split_ragged_backward_packed(
+            grad_out.reshape(m, g, o), normed.reshape(m, g * i), False, inv_norm, gamma.contiguous().reshape(-1),
+            weight.contiguous().reshape(-1), (i,) * g, bool(has_bias),
+        )
+        return [dx.view(m, g, i), dg.view(g, i), dw.view(g, o, i), db.view(g, o) if db is not None else None]
+
+    band_split_backward_v2 = band_split_backward
+    band_split_backward_v3 = band_split_backward
+
+
+__all__ = ["HipFusedExtension", "PmsstError"]

@@ -1,0 +1,208 @@
+"""GPU parity: RMSNorm (plain / fp32-gamma / mixed / saved-input), rotary and fused q/k norm+rotary.
+
+Each case calls the HIP kernels through the C ABI (via ``HipFusedExtension``)
+and compares with the float64 oracle on the same seeded inputs, to the bars in
+``conftest.py``.  Shapes cover the reference configs (dim 64/192/512, head dim
+32/64), the guarded scalar path (dims not a multiple of the pack width), empty
+inputs, a single row, and all-zero rows (inv_norm = 1e12).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.conftest import assert_parity, dt_name, to_np
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def _rand(shape, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype).cuda()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,dim", [(1, 64), (257, 192), (1031, 512), (130, 64), (77, 100), (33, 8), (5, 6)])
+def test_rms_norm_plain(hip_ext, dtype, rows, dim):
+    dn = dt_name(dtype)
+    x = _rand((rows, dim), dtype, 1)
+    if rows > 3:
+        x[3].zero_()
+    gamma = (1 + 0.1 * _rand((dim,), torch.float32, 2)).to(dtype)
+    out, normed, inv = hip_ext.rms_norm_forward(x, gamma)
+    r_out, r_normed, r_inv = oracle.rms_norm_forward(to_np(x), to_np(gamma), dn, "plain")
+    assert_parity(out, r_out, dn, "out")
+    assert_parity(normed, r_normed, dn, "normed")
+    assert_parity(inv.clamp(max=1e6), np.minimum(r_inv, 1e6), "f32", "inv_norm")
+    dy = _rand((rows, dim), dtype, 3)
+    dx, dg = hip_ext.rms_norm_backward(dy, normed, inv, gamma)
+    r_dx, r_dg = oracle.rms_norm_backward(to_np(dy), to_np(normed), to_np(inv), to_np(gamma), dn, "plain")
+    if rows > 3:
+        # zero row: dx = inv * gn * sqrt(D) with inv = 1e12 -- compared relative to its own scale
+        keep = [i for i in range(rows) if i != 3]
+        assert_parity(dx[keep], r_dx[keep], dn, "dx")
+        rel = np.max(np.abs(to_np(dx[3]) - r_dx[3])) / max(np.max(np.abs(r_dx[3])), 1e-30)
+        assert rel <= (1e-5 if dn == "f32" else 2e-2), f"zero-row dx rel err {rel}"
+    else:
+        assert_parity(dx, r_dx, dn, "dx")
+    assert_parity(dg, r_dg, dn, "dgamma")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("rows,dim", [(1000, 192), (64, 64), (17, 100)])
+def test_rms_norm_fp32_gamma_and_mixed(hip_ext, dtype, rows, dim):
+    dn = dt_name(dtype)
+    x = _rand((rows, dim), dtype, 11)
+    gamma = 1 + 0.1 * _rand((dim,), torch.float32, 12)
+    out, normed, inv = hip_ext.rms_norm_forward_fp32_gamma(x, gamma)
+    assert out.dtype == dtype and normed.dtype == dtype
+    r_out, r_normed, _ = oracle.rms_norm_forward(to_np(x), to_np(gamma), dn, "fp32_gamma")
+    assert_parity(out, r_out, dn, "fp32g out")
+    assert_parity(normed, r_normed, dn, "fp32g normed")
+    dy = _rand((rows, dim), dtype, 13)
+    dx, dg = hip_ext.rms_norm_backward_fp32_gamma(dy, normed, inv, gamma)
+    assert dg.dtype == torch.float32
+    r_dx, r_dg = oracle.rms_norm_backward(to_np(dy), to_np(normed), to_np(inv), to_np(gamma), dn, "fp32_gamma")
+    assert_parity(dx, r_dx, dn, "fp32g dx")
+    assert_parity(dg, r_dg, "f32" if dn == "f32" else dn, "fp32g dgamma")
+
+    out, normed, inv = hip_ext.rms_norm_forward_mixed(x, gamma)
+    assert out.dtype == torch.float32 and normed.dtype == torch.float32
+    r_out, r_normed, _ = oracle.rms_norm_forward(to_np(x), to_np(gamma), dn, "mixed")
+    assert_parity(out, r_out, "f32", "mixed out")
+    assert_parity(normed, r_normed, "f32", "mixed normed")
+    dy32 = _rand((rows, dim), torch.float32, 14)
+    dx, dg = hip_ext.rms_norm_backward_mixed(dy32, normed, inv, gamma, x.new_empty(0))
+    assert dx.dtype == dtype
+    r_dx, r_dg = oracle.rms_norm_backward(to_np(dy32), to_np(normed), to_np(inv), to_np(gamma), dn, "mixed")
+    assert_parity(dx, r_dx, dn, "mixed dx")
+    assert_parity(dg, r_dg, "f32", "mixed dgamma")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("gamma_fp32", [False, True])
+def test_rms_norm_lean_roundtrip(hip_ext, dtype, gamma_fp32):
+    dn = dt_name(dtype)
+    rows, dim = 2049, 192
+    x = _rand((rows, dim), dtype, 21)
+    gamma = 1 + 0.1 * _rand((dim,), torch.float32, 22)
+    if not gamma_fp32:
+        gamma = gamma.to(dtype)
+    out, inv = hip_ext.rms_norm_forward_lean(x, gamma)
+    mode = "fp32_gamma" if gamma_fp32 and dtype != torch.float32 else "plain"
+    r_out, _, _ = oracle.rms_norm_forward(to_np(x), to_np(gamma), dn, mode)
+    assert_parity(out, r_out, dn, "lean out")
+    dy = _rand((rows, dim), dtype, 23)
+    dx, dg = hip_ext.rms_norm_backward_from_input(dy, x, inv, gamma)
+    gdt = "f32" if gamma.dtype == torch.float32 else dn
+    r_dx, r_dg = oracle.rms_norm_backward_lean(to_np(dy), to_np(x), to_np(inv), to_np(gamma), dn, gdt)
+    assert_parity(dx, r_dx, dn, "lean dx")
+    assert_parity(dg, r_dg, gdt, "lean dgamma")
+
+
+def test_rms_norm_empty_and_large(hip_ext):
+    x = torch.empty(0, 192, device="cuda", dtype=torch.bfloat16)
+    gamma = torch.ones(192, device="cuda", dtype=torch.bfloat16)
+    out, normed, inv = hip_ext.rms_norm_forward(x, gamma)
+    assert out.shape == (0, 192) and inv.shape == (0,)
+    dx, dg = hip_ext.rms_norm_backward(out, normed, inv, gamma)
+    assert dx.shape == (0, 192)
+    assert torch.count_nonzero(dg).item() == 0
+    # the cfg3 transformer shape: 63,984 rows x 192, fp32 (the dtype of the residual stream under autocast)
+    rows, dim = 63984, 192
+    x = _rand((rows, dim), torch.float32, 31)
+    gamma = 1 + 0.1 * _rand((dim,), torch.float32, 32)
+    out, normed, inv = hip_ext.rms_norm_forward(x, gamma)
+    dy = _rand((rows, dim), torch.float32, 33)
+    dx, dg = hip_ext.rms_norm_backward(dy, normed, inv, gamma)
+    # size-independent properties: ||normed|| = sqrt(D) per row; dx is orthogonal to normed (scale invariance)
+    nrm = normed.double().norm(dim=-1)
+    assert torch.allclose(nrm, torch.full_like(nrm, dim**0.5), rtol=1e-5)
+    ortho = (dx.double() * x.double()).sum(-1).abs().max().item()
+    assert ortho <= 1e-4 * dx.double().abs().max().item() * x.double().abs().max().item() * dim**0.5
+    # dgamma against a float64 torch reduction of the same inputs
+    ref_dg = (dy.double() * normed.double()).sum(0)
+    assert_parity(dg, ref_dg, "f32", "large dgamma")
+
+
+def test_rms_norm_rejects_bad_args(hip_ext):
+    x = torch.randn(4, 8, device="cuda")
+    with pytest.raises(RuntimeError, match="gamma dimension must match"):
+        hip_ext.rms_norm_forward(x, torch.ones(7, device="cuda"))
+    with pytest.raises(RuntimeError, match="gamma dtype must match x"):
+        hip_ext.rms_norm_forward(x, torch.ones(8, device="cuda", dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="gamma must be float32"):
+        hip_ext.rms_norm_forward_mixed(x.bfloat16(), torch.ones(8, device="cuda", dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="not supported"):
+        hip_ext.rms_norm_forward(torch.randn(2, 1001, device="cuda"), torch.ones(1001, device="cuda"))
+
+
+def _tables(n, d, dtype, sliced=True):
+    c, s = oracle.rotary_tables(n, d)
+    c = torch.from_numpy(c).to(dtype).cuda()
+    s = torch.from_numpy(s).to(dtype).cuda()
+    if sliced:
+        # the reference passes cos[..., ::2] of the pairwise-repeated [1,N,1,D] table (fused_roformer.py:727)
+        c = c.repeat_interleave(2, dim=-1).reshape(1, n, 1, d)[..., ::2]
+        s = s.repeat_interleave(2, dim=-1).reshape(1, n, 1, d)[..., ::2]
+    else:
+        c = c.reshape(1, n, 1, d // 2)
+        s = s.reshape(1, n, 1, d // 2)
+    return c, s
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(3, 65, 4, 32), (2, 62, 8, 64), (5, 7, 3, 6), (1, 1, 1, 2)])
+@pytest.mark.parametrize("sliced", [True, False])
+def test_rotary(hip_ext, dtype, shape, sliced):
+    dn = dt_name(dtype)
+    b, n, h, d = shape
+    t = _rand(shape, dtype, 41)
+    cos, sin = _tables(n, d, dtype, sliced)
+    out = hip_ext.rotary_forward(t, cos, sin)
+    r = oracle.rotary_forward(to_np(t), to_np(cos).reshape(n, d // 2), to_np(sin).reshape(n, d // 2), dn)
+    assert_parity(out, r, dn, "rotary fwd")
+    g = _rand(shape, dtype, 42)
+    dt_ = hip_ext.rotary_backward(g, cos, sin)
+    r = oracle.rotary_backward(to_np(g), to_np(cos).reshape(n, d // 2), to_np(sin).reshape(n, d // 2), dn)
+    assert_parity(dt_, r, dn, "rotary bwd")
+
+
+def test_rotary_microbench_shape_roundtrip(hip_ext):
+    # cfg2 q/k shape; forward then backward is the identity up to rounding (rotation is orthogonal)
+    shape = (248, 258, 8, 64)
+    t = _rand(shape, torch.float32, 51)
+    cos, sin = _tables(258, 64, torch.float32)
+    back = hip_ext.rotary_backward(hip_ext.rotary_forward(t, cos, sin), cos, sin)
+    assert (back - t).abs().max().item() <= 1e-5
+    nr = hip_ext.rotary_forward(t, cos, sin).double().norm(dim=-1)
+    assert torch.allclose(nr, t.double().norm(dim=-1), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("gamma_fp32", [False, True])
+@pytest.mark.parametrize("shape", [(4, 65, 4, 32), (6, 258, 8, 64), (2, 3, 1, 128)])
+def test_rms_norm_rotary_fused(hip_ext, dtype, gamma_fp32, shape):
+    dn = dt_name(dtype)
+    b, n, h, d = shape
+    x = _rand(shape, dtype, 61)
+    gamma = 1 + 0.1 * _rand((d,), torch.float32, 62)
+    if not gamma_fp32:
+        gamma = gamma.to(dtype)
+    cos, sin = _tables(n, d, dtype)
+    out, inv = hip_ext.rms_norm_rotary_forward(x, gamma, cos, sin)
+    cn, sn = to_np(cos).reshape(n, d // 2), to_np(sin).reshape(n, d // 2)
+    r_out, r_inv = oracle.rms_norm_rotary_forward(to_np(x), to_np(gamma), cn, sn, dn)
+    assert_parity(out, r_out, dn, "norm-rot out")
+    assert_parity(inv, r_inv.reshape(-1), "f32", "norm-rot inv")
+    dy = _rand(shape, dtype, 63)
+    dx, dg = hip_ext.rms_norm_rotary_backward(dy, x, inv, gamma, cos, sin)
+    gdt = "f32" if gamma.dtype == torch.float32 else dn
+    r_dx, r_dg = oracle.rms_norm_rotary_backward(to_np(dy), to_np(x), to_np(inv), to_np(gamma), cn, sn, dn, gdt)
+    assert_parity(dx, r_dx, dn, "norm-rot dx")
+    assert_parity(dg, r_dg, gdt, "norm-rot dgamma")

@@ -1,0 +1,310 @@
+"""Pin the float64 oracle (``oracle/``) against independent computations (CPU only).
+
+Each oracle function is compared with torch float64 autograd of the closed-form
+module (``tests/torch_reference.py``), with complex multiplication, with
+invariants, and at the reference tests' own seeded shapes.  A planted-mistake
+test shows the checks fail when a term of the hand-derived backward is dropped.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import torch_reference as tr
+
+TOL = 1e-10  # float64 vs float64
+
+
+def _t(a, grad=False):
+    return torch.tensor(np.asarray(a), dtype=torch.float64, requires_grad=grad)
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _close(a, b, tol=TOL, what=""):
+    a = np.asarray(a, dtype=np.float64)
+    b = b.detach().numpy() if isinstance(b, torch.Tensor) else np.asarray(b, dtype=np.float64)
+    scale = max(1.0, float(np.max(np.abs(b))) if b.size else 1.0)
+    err = float(np.max(np.abs(a - b))) if a.size else 0.0
+    assert err <= tol * scale, f"{what}: {err:.3e}"
+
+
+# ------------------------------------------------------------------ RMSNorm
+
+
+@pytest.mark.parametrize("rows,dim", [(7, 64), (5, 192), (3, 5), (1, 1)])
+def test_rms_norm_forward_backward_vs_autograd(rows, dim):
+    r = _rng(rows * 1000 + dim)
+    x = r.standard_normal((rows, dim))
+    x[0] *= 1e-3
+    gamma = 1 + 0.1 * r.standard_normal(dim)
+    dy = r.standard_normal((rows, dim))
+    out, normed, inv = oracle.rms_norm_forward(x, gamma, "f64")
+    tx, tg = _t(x, True), _t(gamma, True)
+    ref = tr.rms_norm(tx, tg)
+    _close(out, ref, what="out")
+    ref.backward(_t(dy))
+    dx, dg = oracle.rms_norm_backward(dy, normed, inv, gamma, "f64")
+    _close(dx, tx.grad, what="dx")
+    _close(dg, tg.grad, what="dgamma")
+    # saved-input variant
+    dx2, dg2 = oracle.rms_norm_backward_lean(dy, x, inv, gamma, "f64")
+    _close(dx2, tx.grad, what="lean dx")
+    _close(dg2, tg.grad, what="lean dgamma")
+
+
+def test_rms_norm_invariants_and_zero_row():
+    r = _rng(3)
+    x = r.standard_normal((6, 32))
+    x[2] = 0.0
+    gamma = np.ones(32)
+    out, normed, inv = oracle.rms_norm_forward(x, gamma, "f64")
+    norms = np.linalg.norm(normed, axis=-1)
+    assert np.allclose(np.delete(norms, 2), math.sqrt(32), rtol=1e-12)
+    assert np.all(normed[2] == 0) and inv[2] == 1e12
+    # scale invariance f(alpha x) = f(x)
+    out2, _, _ = oracle.rms_norm_forward(3.7 * x, gamma, "f64")
+    assert np.allclose(out, out2, atol=1e-12)
+    # zero-row backward: dx = inv * dy * gamma * sqrt(D)  (autograd of F.normalize's eps clamp)
+    dy = r.standard_normal((6, 32))
+    tx, tg = _t(x, True), _t(gamma, True)
+    tr.rms_norm(tx, tg).backward(_t(dy))
+    dx, _ = oracle.rms_norm_backward(dy, normed, inv, gamma, "f64")
+    rel = np.max(np.abs(dx[2] - tx.grad[2].numpy())) / np.max(np.abs(tx.grad[2].numpy()))
+    assert rel < 1e-6
+
+
+def test_rms_norm_mode_dtypes():
+    r = _rng(4)
+    x = oracle.round_to(r.standard_normal((4, 16)), "bf16")
+    gamma = 1 + 0.1 * r.standard_normal(16)
+    out, normed, _ = oracle.rms_norm_forward(x, gamma, "bf16", "mixed")
+    # mixed writes fp32, so it keeps more precision than bf16 rounding
+    assert np.any(oracle.round_to(out, "bf16") != out)
+    outb, _, _ = oracle.rms_norm_forward(x, gamma, "bf16", "fp32_gamma")
+    assert np.all(oracle.round_to(outb, "bf16") == outb)
+
+
+def test_planted_mistake_in_oracle_backward_is_caught(monkeypatch):
+    """Drop the projection term of the RMSNorm backward: the autograd check must fail."""
+    r = _rng(5)
+    x = r.standard_normal((4, 16))
+    gamma = 1 + 0.1 * r.standard_normal(16)
+    dy = r.standard_normal((4, 16))
+    _, normed, inv = oracle.rms_norm_forward(x, gamma, "f64")
+
+    def broken(grad_out, normed, inv_norm, gamma, dt, mode="plain", acc=np.float64):
+        scale = math.sqrt(grad_out.shape[-1])
+        dx = inv_norm[:, None] * (grad_out * gamma * scale)  # missing "- n * dot / scale"
+        return dx, np.sum(grad_out * normed, axis=0)
+
+    tx, tg = _t(x, True), _t(gamma, True)
+    tr.rms_norm(tx, tg).backward(_t(dy))
+    dx_bad, _ = broken(dy, normed, inv, gamma, "f64")
+    with pytest.raises(AssertionError):
+        _close(dx_bad, tx.grad, what="planted")
+
+
+# ------------------------------------------------------------------ rotary
+
+
+@pytest.mark.parametrize("shape", [(2, 5, 3, 8), (1, 65, 4, 32), (1, 3, 1, 2)])
+def test_rotary_vs_complex_multiply_and_autograd(shape):
+    b, n, h, d = shape
+    r = _rng(n * d)
+    t = r.standard_normal(shape)
+    cos, sin = oracle.rotary_tables(n, d)
+    out = oracle.rotary_forward(t, cos, sin, "f64")
+    tt = _t(t, True)
+    ref = tr.rotary(tt, _t(cos), _t(sin))
+    _close(out, ref, what="fwd")
+    g = r.standard_normal(shape)
+    ref.backward(_t(g))
+    _close(oracle.rotary_backward(g, cos, sin, "f64"), tt.grad, what="bwd")
+
+
+def test_rotary_tables_and_relative_position():
+    n, d = 16, 8
+    cos, sin = oracle.rotary_tables(n, d, theta=10000.0)
+    # closed form: angle(n, p) = n * 10000^(-2p/d)
+    ang = np.arange(n)[:, None] * (10000.0 ** (-np.arange(0, d, 2) / d))[None, :]
+    assert np.allclose(cos, np.cos(ang)) and np.allclose(sin, np.sin(ang))
+    # q(m).k(n) depends only on m - n
+    r = _rng(9)
+    q = r.standard_normal(d)
+    k = r.standard_normal(d)
+    qs = oracle.rotary_forward(np.tile(q, (1, n, 1, 1)), cos, sin, "f64")[0, :, 0]
+    ks = oracle.rotary_forward(np.tile(k, (1, n, 1, 1)), cos, sin, "f64")[0, :, 0]
+    dots = qs @ ks.T
+    for delta in range(-3, 4):
+        diag = np.diagonal(dots, offset=delta)
+        assert np.allclose(diag, diag[0], atol=1e-10)
+    # norm preservation
+    assert np.allclose(np.linalg.norm(qs, axis=-1), np.linalg.norm(q))
+
+
+@pytest.mark.parametrize("shape", [(2, 5, 3, 8), (1, 9, 2, 64)])
+def test_rms_norm_rotary_vs_autograd(shape):
+    b, n, h, d = shape
+    r = _rng(d + n)
+    x = r.standard_normal(shape)
+    x[0, 0, 0] = 0.0
+    gamma = 1 + 0.1 * r.standard_normal(d)
+    cos, sin = oracle.rotary_tables(n, d)
+    out, inv = oracle.rms_norm_rotary_forward(x, gamma, cos, sin, "f64")
+    tx, tg = _t(x, True), _t(gamma, True)
+    ref = tr.rotary(tr.rms_norm(tx, tg), _t(cos), _t(sin))
+    _close(out, ref, what="fwd")
+    g = r.standard_normal(shape)
+    ref.backward(_t(g))
+    dx, dg = oracle.rms_norm_rotary_backward(g, x, inv, gamma, cos, sin, "f64", "f64")
+    keep = np.ones(shape, bool)
+    keep[0, 0, 0] = False
+    _close(dx[keep], tx.grad.numpy()[keep], what="dx")
+    _close(dg, tg.grad, what="dgamma")
+
+
+# ------------------------------------------------------------------ band split
+
+
+@pytest.mark.parametrize("m,g,i,o,bias", [(5, 3, 8, 4, True), (4, 2, 16, 6, False), (3, 1, 7, 5, True)])
+def test_band_split_group_vs_autograd(m, g, i, o, bias):
+    r = _rng(m * g * i * o)
+    x = r.standard_normal((m, g, i))
+    gamma = 1 + 0.1 * r.standard_normal((g, i))
+    w = r.standard_normal((g, o, i)) / math.sqrt(i)
+    b = r.standard_normal((g, o)) if bias else None
+    out, normed, inv = oracle.band_split_forward(x, gamma, w, b, "f64")
+    tx, tg, tw = _t(x, True), _t(gamma, True), _t(w, True)
+    tb = _t(b, True) if bias else None
+    ref = tr.band_split_group(tx, tg, tw, tb)
+    _close(out, ref, what="out")
+    dy = r.standard_normal((m, g, o))
+    ref.backward(_t(dy))
+    dx, dg, dw, db = oracle.band_split_backward(dy, normed, inv, gamma, w, bias, "f64")
+    _close(dx, tx.grad, what="dx")
+    _close(dg, tg.grad, what="dgamma")
+    _close(dw, tw.grad, what="dW")
+    if bias:
+        _close(db, tb.grad, what="db")
+    else:
+        assert db is None
+
+
+@pytest.mark.parametrize("dim_inputs,m,o,seed", [((3, 5, 2, 7), 5, 4, 7), ((8, 8, 16, 48), 6, 12, 1)])
+def test_band_split_ragged_vs_autograd(dim_inputs, m, o, seed):
+    """Widths/seed of the reference's ragged test (tests/test_training_smoke.py:512-571)."""
+    r = _rng(seed)
+    x = r.standard_normal((m, sum(dim_inputs)))
+    gammas = [1 + 0.1 * r.standard_normal(d) for d in dim_inputs]
+    weights = [r.standard_normal((o, d)) for d in dim_inputs]
+    biases = [r.standard_normal(o) for _ in dim_inputs]
+    out, normed, inv = oracle.band_split_ragged_forward(x, gammas, weights, biases, dim_inputs, "f64")
+    tx = _t(x, True)
+    tg = [_t(v, True) for v in gammas]
+    tw = [_t(v, True) for v in weights]
+    tb = [_t(v, True) for v in biases]
+    ref = tr.band_split_ragged(tx, tg, tw, tb, dim_inputs)
+    _close(out, ref, what="out")
+    dy = r.standard_normal((m, len(dim_inputs), o))
+    ref.backward(_t(dy))
+    dx, dgs, dws, dbs = oracle.band_split_ragged_backward(dy, normed, inv, gammas, weights, dim_inputs, "f64")
+    _close(dx, tx.grad, what="dx")
+    for k in range(len(dim_inputs)):
+        _close(dgs[k], tg[k].grad, what=f"dgamma{k}")
+        _close(dws[k], tw[k].grad, what=f"dW{k}")
+        _close(dbs[k], tb[k].grad, what=f"db{k}")
+    dx2, dgs2, dws2, dbs2 = oracle.band_split_ragged_backward_lean(dy, x, inv, gammas, weights, dim_inputs, "f64")
+    _close(dx2, tx.grad, what="lean dx")
+    # ragged == concatenation of single-band group results (the reference asserts this kernel vs kernel)
+    off = np.cumsum((0,) + tuple(dim_inputs))
+    for k, d in enumerate(dim_inputs):
+        ob, _, _ = oracle.band_split_forward(
+            x[:, None, off[k] : off[k + 1]], gammas[k][None], weights[k][None], biases[k][None], "f64"
+        )
+        _close(out[:, k], ob[:, 0], what="ragged==group")
+
+
+# ------------------------------------------------------------------ grouped linear / mask estimator
+
+
+def test_grouped_linear_vs_bmm_reference():
+    r = _rng(12)
+    x = r.standard_normal((2, 5, 3, 4))
+    w = r.standard_normal((3, 6, 4))
+    b = r.standard_normal((3, 6))
+    out = oracle.grouped_linear_forward(x.reshape(-1, 3, 4), w, b, "f64")
+    tx, tw, tb = _t(x, True), _t(w, True), _t(b, True)
+    ref = tr.grouped_linear(tx, tw, tb)
+    _close(out, ref.reshape(-1, 3, 6), what="fwd")
+    dy = r.standard_normal((2, 5, 3, 6))
+    ref.backward(_t(dy))
+    dx, dw, db = oracle.grouped_linear_backward(dy.reshape(-1, 3, 6), x.reshape(-1, 3, 4), w, True, "f64")
+    _close(dx, tx.grad.reshape(-1, 3, 4), what="dx")
+    _close(dw, tw.grad, what="dW")
+    _close(db, tb.grad, what="db")
+
+
+def test_mask_final_vs_linear_glu_reference_shapes():
+    """Seed/shapes of tests/test_training_smoke.py:574-615: M=4, NB=5, hidden 16, widths (3,4,2,5,6)."""
+    r = _rng(11)
+    dim_inputs = (3, 4, 2, 5, 6)
+    m, nb, hid = 4, 5, 16
+    x = r.standard_normal((m, nb, hid))
+    weights = [r.standard_normal((2 * d, hid)) for d in dim_inputs]
+    bias = r.standard_normal(2 * sum(dim_inputs))
+    out, pre = oracle.mask_estimator_final_forward(x, weights, bias, dim_inputs, "f64")
+    tx, tb = _t(x, True), _t(bias, True)
+    tw = [_t(w, True) for w in weights]
+    ref = tr.mask_final(tx, tw, tb, dim_inputs)
+    _close(out, ref, what="out")
+    g = r.standard_normal((m, sum(dim_inputs)))
+    ref.backward(_t(g))
+    dx, dbias, dws = oracle.mask_estimator_final_backward(g, x, pre, weights, dim_inputs, "f64")
+    _close(dx, tx.grad, what="dx")
+    _close(dbias, tb.grad, what="dbias")
+    for k in range(nb):
+        _close(dws[k], tw[k].grad, what=f"dW{k}")
+
+
+def test_mask_mlp_vs_autograd():
+    r = _rng(13)
+    dim_inputs = (8, 16, 4)
+    m, nb, dim, hid = 6, 3, 12, 20
+    x = r.standard_normal((m, nb, dim))
+    w1 = r.standard_normal((nb, hid, dim)) / math.sqrt(dim)
+    b1 = r.standard_normal((nb, hid))
+    w2 = [r.standard_normal((2 * d, hid)) / math.sqrt(hid) for d in dim_inputs]
+    b2 = r.standard_normal(2 * sum(dim_inputs))
+    out = oracle.mask_mlp_forward(x, w1, b1, w2, b2, dim_inputs, "f64")
+    tx, tw1, tb1, tb2 = _t(x, True), _t(w1, True), _t(b1, True), _t(b2, True)
+    tw2 = [_t(w, True) for w in w2]
+    ref = tr.mask_mlp(tx, tw1, tb1, tw2, tb2, dim_inputs)
+    _close(out, ref, what="out")
+    g = r.standard_normal((m, sum(dim_inputs)))
+    ref.backward(_t(g))
+    dx, dw1, db1, dw2, db2 = oracle.mask_mlp_backward(g, x, w1, b1, w2, b2, dim_inputs, "f64")
+    _close(dx, tx.grad, what="dx")
+    _close(dw1, tw1.grad, what="dW1")
+    _close(db1, tb1.grad, what="db1")
+    _close(db2, tb2.grad, what="db2")
+    for k in range(nb):
+        _close(dw2[k], tw2[k].grad, what=f"dW2_{k}")
+
+
+def test_round_to_matches_torch_casts():
+    r = _rng(14)
+    a = r.standard_normal(10000) * 10 ** r.uniform(-6, 6, 10000)
+    for name, dt in (("bf16", torch.bfloat16), ("f16", torch.float16), ("f32", torch.float32)):
+        ref = torch.tensor(a, dtype=torch.float32).to(dt).double().numpy() if name != "f32" else a.astype(np.float32)
+        got = oracle.round_to(a, name)
+        if name == "f16":
+            ref = a.astype(np.float32).astype(np.float16).astype(np.float64)
+        assert np.array_equal(got, np.asarray(ref, dtype=np.float64)), name
