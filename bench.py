@@ -1,0 +1,319 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused RoFormer layer kernels on one MI355X.
+
+One "step" is one forward + backward pass of every fused layer of the kernel
+microbench, bf16, with all inputs resident in HBM:
+
+* band split: ``x[4, 258, 4100]`` (62 BS-RoFormer bands) -> ``[4, 258, 62, 192]``,
+  saved-input backward;
+* q/k RMSNorm over the head dim + rotary (theta 10000): two ``[248, 258, 8, 64]`` tensors;
+* mask estimator final layer: per band hidden 768 -> 2 * I_b, bias, GLU.
+
+``value`` is the algorithmic HBM bytes of all kernels in a step divided by the
+step time (GB/s).  Per-op average durations come from HIP events recorded on
+the launch stream inside the timed region; ``roofline`` reports the op with
+the largest share of the step.  ``cpu_baseline`` times the numpy oracle
+(``oracle/``) on a bounded sample of the same workload on the host.
+
+Usage: ``python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+if str(REPO) not in sys.path:
+    sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "fused-layer fwd+bwd HBM GB/s (% peak) + BSR train samples/s, 1 MI355X"
+BSR_WIDTHS = tuple([8] * 24 + [16] * 12 + [48] * 8 + [96] * 8 + [192] * 8 + [512, 516])
+
+
+def _args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    return ap.parse_args(argv)
+
+
+class Workload:
+    """Seeded synthetic inputs of configs[1] (the seeds of the survey's measurement plan)."""
+
+    def __init__(self, torch, ext, dtype):
+        import numpy as np
+
+        self.torch, self.ext, self.dtype = torch, ext, dtype
+        dev = torch.device("cuda:0")
+        self.dims = BSR_WIDTHS
+        self.B, self.T, self.dim, self.hidden = 4, 258, 192, 768
+        self.M = self.B * self.T
+        self.F = sum(self.dims)
+        self.NB = len(self.dims)
+        g = lambda s: torch.Generator().manual_seed(s)  # noqa: E731
+        lap = torch.distributions.Laplace(0.0, 0.05)
+        torch.manual_seed(0)
+        self.x = lap.sample((self.M, self.F)).to(dev, dtype)
+        self.qk_shape = (self.B * self.NB, self.T, 8, 64)
+        self.q = torch.randn(self.qk_shape, generator=g(1)).to(dev, dtype)
+        self.k = torch.randn(self.qk_shape, generator=g(2)).to(dev, dtype)
+        self.h = torch.randn(self.M, self.NB, self.hidden, generator=g(3)).to(dev, dtype)
+        pg = g(4)
+        self.gamma_bs = (1 + 0.1 * torch.randn(self.F, generator=pg)).to(dev, dtype)
+        self.w_bs = torch.cat([(torch.randn(self.dim, d, generator=pg) / d**0.5).reshape(-1) for d in self.dims])
+        self.w_bs = self.w_bs.to(dev, dtype)
+        self.b_bs = (0.1 * torch.randn(self.NB * self.dim, generator=pg)).to(dev, dtype)
+        self.gamma_q = (1 + 0.1 * torch.randn(64, generator=pg)).to(dev)
+        self.gamma_k = (1 + 0.1 * torch.randn(64, generator=pg)).to(dev)
+        self.w_me = torch.cat(
+            [(torch.randn(2 * d, self.hidden, generator=pg) / self.hidden**0.5).reshape(-1) for d in self.dims]
+        ).to(dev, dtype)
+        self.b_me = (0.1 * torch.randn(2 * self.F, generator=pg)).to(dev, dtype)
+        import oracle
+
+        c, s = oracle.rotary_tables(self.T, 64, 10000.0)
+        self.cos = torch.from_numpy(c).to(dev, dtype).reshape(1, self.T, 1, 32)
+        self.sin = torch.from_numpy(s).to(dev, dtype).reshape(1, self.T, 1, 32)
+        gg = g(5)
+        self.g_bs = torch.randn(self.M, self.NB, self.dim, generator=gg).to(dev, dtype)
+        self.g_q = torch.randn(self.qk_shape, generator=gg).to(dev, dtype)
+        self.g_k = torch.randn(self.qk_shape, generator=gg).to(dev, dtype)
+        self.g_me = torch.randn(self.M, self.F, generator=gg).to(dev, dtype)
+        del np
+
+    # --------------------------------------------------------------- ops (name, callable)
+    def ops(self):
+        e, w = self.ext, self
+        state = {}
+
+        def bs_fwd():
+            state["bs"] = e.band_split_ragged_forward_packed(w.x, w.gamma_bs, w.w_bs, w.b_bs, w.dims, write_normed=False)
+
+        def bs_bwd():
+            e.band_split_ragged_backward_packed(w.g_bs, w.x, True, state["bs"][2], w.gamma_bs, w.w_bs, w.dims, True)
+
+        def qk_fwd():
+            state["q"] = e.rms_norm_rotary_forward(w.q, w.gamma_q, w.cos, w.sin)
+            state["k"] = e.rms_norm_rotary_forward(w.k, w.gamma_k, w.cos, w.sin)
+
+        def qk_bwd():
+            e.rms_norm_rotary_backward(w.g_q, w.q, state["q"][1], w.gamma_q, w.cos, w.sin)
+            e.rms_norm_rotary_backward(w.g_k, w.k, state["k"][1], w.gamma_k, w.cos, w.sin)
+
+        def me_fwd():
+            state["me"] = e.mask_estimator_final_forward_packed(w.h, w.w_me, w.b_me, w.dims)
+
+        def me_bwd():
+            e.mask_estimator_final_backward_packed(w.g_me, w.h, state["me"][1], w.w_me, w.dims)
+
+        return [("band_split_fwd", bs_fwd), ("band_split_bwd", bs_bwd), ("qk_norm_rotary_fwd", qk_fwd),
+                ("qk_norm_rotary_bwd", qk_bwd), ("mask_final_fwd", me_fwd), ("mask_final_bwd", me_bwd)]
+
+    # --------------------------------------------------------------- algorithmic bytes / flops per op
+    def traffic(self):
+        s = 2 if self.dtype != self.torch.float32 else 4
+        M, F, NB, O, H = self.M, self.F, self.NB, self.dim, self.hidden
+        R = self.qk_shape[0] * self.qk_shape[1] * self.qk_shape[2]
+        D = 64
+        return {
+            # read x, gamma, W, bias; write out, inv
+            "band_split_fwd": (M * F * s + F * s + F * O * s + NB * O * s + M * NB * O * s + 4 * M * NB,
+                               2 * M * F * O),
+            # read dy, x, inv, gamma, W; write dx, dgamma, dW, dbias
+            "band_split_bwd": (M * NB * O * s + 2 * M * F * s + 4 * M * NB + 2 * F * s + 2 * F * O * s + NB * O * s,
+                               4 * M * F * O),
+            # per tensor: read x, write out, write inv (x2 tensors)
+            "qk_norm_rotary_fwd": (2 * (2 * R * D * s + 4 * R), 0),
+            # per tensor: read dy, x, inv; write dx (x2)
+            "qk_norm_rotary_bwd": (2 * (3 * R * D * s + 4 * R), 0),
+            # read x, W, bias; write pre, out
+            "mask_final_fwd": (M * NB * H * s + 2 * F * H * s + 2 * F * s + 2 * M * F * s + M * F * s,
+                               2 * M * 2 * F * H),
+            # read g, pre, x, W; write dx, dW, dbias
+            "mask_final_bwd": (M * F * s + 2 * M * F * s + 2 * M * NB * H * s + 4 * F * H * s + 2 * F * s,
+                               2 * 2 * M * 2 * F * H),
+        }
+
+
+def _cpu_baseline(budget_s: float):
+    """Time the numpy oracle (float32 arithmetic) on row slices of the same workload.
+
+    Each op runs on ``rows`` rows (a bounded sample of the M=1032 / R=511,872 rows of the
+    GPU step) and its algorithmic bytes are scaled by the same fraction; the result is
+    the oracle's GB/s over one full step's bytes, extrapolated from the sample.
+    """
+    import numpy as np
+
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([int(p.get("num_threads", 1)) for p in threadpool_info()] + [1])
+    except Exception:  # pragma: no cover
+        cores = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    dims, O, H = BSR_WIDTHS, 192, 768
+    F, NB = sum(dims), len(dims)
+    m = 64  # rows per band-split / mask sample (of 1032)
+    rq = 32 * 64 * 8  # rows per q/k sample (of 511,872), one tensor [32, 64, 8, 64]
+    acc = np.float32
+    x = (rng.laplace(0, 0.05, (m, F))).astype(acc)
+    gam = [np.ones(d, acc) for d in dims]
+    ws = [rng.standard_normal((O, d)).astype(acc) for d in dims]
+    bs = [np.zeros(O, acc) for d in dims]
+    dy = rng.standard_normal((m, NB, O)).astype(acc)
+    q = rng.standard_normal((32, 64, 8, 64)).astype(acc)
+    cos, sin = oracle.rotary_tables(64, 64)
+    gq = np.ones(64, acc)
+    h = rng.standard_normal((m, NB, H)).astype(acc)
+    w2 = [rng.standard_normal((2 * d, H)).astype(acc) for d in dims]
+    b2 = np.zeros(2 * F, acc)
+    g2 = rng.standard_normal((m, F)).astype(acc)
+    s = 4
+    sample_bytes = (
+        (m * F + F + F * O + NB * O + m * NB * O) * s + 4 * m * NB  # band split fwd
+        + (m * NB * O + 2 * m * F + 2 * F + 2 * F * O + NB * O) * s + 4 * m * NB  # band split bwd
+        + (2 * rq * 64 * s + 4 * rq) + (3 * rq * 64 * s + 4 * rq)  # one q/k tensor fwd + bwd
+        + (m * NB * H + 2 * F * H + 2 * F + 3 * m * F) * s  # mask fwd
+        + (3 * m * F + 2 * m * NB * H + 4 * F * H + 2 * F) * s  # mask bwd
+    )
+
+    def one():
+        o, n, inv = oracle.band_split_ragged_forward(x, gam, ws, bs, dims, "f32", acc)
+        oracle.band_split_ragged_backward_lean(dy, x, inv, gam, ws, dims, "f32", acc)
+        oq, iq = oracle.rms_norm_rotary_forward(q, gq, cos, sin, "f32", acc)
+        oracle.rms_norm_rotary_backward(q, q, iq, gq, cos, sin, "f32", "f32", acc)
+        out, pre = oracle.mask_estimator_final_forward(h, w2, b2, dims, "f32", acc)
+        oracle.mask_estimator_final_backward(g2, h, pre, w2, dims, "f32", acc)
+
+    one()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        one()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 50:
+            break
+    gbs = sample_bytes * reps / el / 1e9
+    return {
+        "value": round(gbs, 3),
+        "unit": "GB/s",
+        "cores": int(cores),
+        "kind": "port",
+        "sample": f"numpy oracle (fp32) on {m} of 1032 rows for band split and mask final, "
+                  f"{rq} of 511872 q/k rows (one tensor); {reps} reps in {el:.1f}s",
+    }
+
+
+def main(argv=None) -> int:
+    args = _args(argv)
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (multi-GPU runs are out of scope)"}))
+        return 2
+    import torch
+
+    from pymsst_amd.fused_extension import load_fused_band_split_extension
+
+    ext = load_fused_band_split_extension()
+    dtype = torch.bfloat16
+    w = Workload(torch, ext, dtype)
+    ops = w.ops()
+    traffic = w.traffic()
+    stream = torch.cuda.current_stream()
+
+    def step():
+        for _, fn in ops:
+            fn()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # whole-step timing
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for _ in range(args.steps):
+        step()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_per_step = t_start.elapsed_time(t_end) / args.steps
+
+    # per-op timing with events bracketing each op on the launch stream
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in ops]
+          for _ in range(args.steps)]
+    for i in range(args.steps):
+        for j, (_, fn) in enumerate(ops):
+            ev[i][j][0].record(stream)
+            fn()
+            ev[i][j][1].record(stream)
+    torch.cuda.synchronize()
+    per_op = {}
+    for j, (name, _) in enumerate(ops):
+        ms = sum(ev[i][j][0].elapsed_time(ev[i][j][1]) for i in range(args.steps)) / args.steps
+        nbytes, flops = traffic[name]
+        per_op[name] = {
+            "ms": round(ms, 5),
+            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2) if flops else None,
+        }
+    total_bytes = sum(b for b, _ in traffic.values())
+    value = total_bytes / (ms_per_step * 1e-3) / 1e9
+    dom = max(per_op, key=lambda k: per_op[k]["ms"])
+    d = per_op[dom]
+    roofline = {
+        "kernel": dom,
+        "bound": "hbm",
+        "achieved": d["GB/s"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(d["GB/s"] / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "bytes_per_launch": traffic[dom][0],
+        "avg_ms": d["ms"],
+    }
+    cpu = None if args.no_cpu_baseline else _cpu_baseline(args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "configs[1] kernel microbench: band split [4,258,4100]->192 (62 bands), "
+                        "q/k RMSNorm+rotary [248,258,8,64]x2, mask-estimator final 768->2*I_b+GLU; fwd+bwd",
+            "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+            "wall_s_timed": round(wall, 3),
+        },
+        "per_op": per_op,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

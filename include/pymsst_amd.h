@@ -147,6 +147,38 @@ int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, in
                                      void* grad_weight, void* grad_bias, int dtype, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------ grouped linear
+ * fused_band_split.cpp:365-388 grouped_linear_forward (.cu:1005-1074):
+ * out[m, g, :] = W_g x[m, g, :] + b_g for x[rows, groups, in_features] with row pitch
+ * x_row_stride (group g at column g * in_features), weight[groups, O, in_features],
+ * bias[groups, O] or NULL, out[rows, groups, O].  group_offsets is the device copy of
+ * the groups+1 prefix sums g * in_features.  Any O >= 1.
+ */
+int pmsst_grouped_linear_forward(const void* x, int64_t x_row_stride, const void* weight, const void* bias,
+                                 const int64_t* group_offsets, int64_t groups, int64_t in_features, int64_t rows,
+                                 int64_t out_features, void* out, int dtype, void* stream);
+
+/* ------------------------------------------------------------------ mask estimator final layer
+ * Per-band Linear hidden -> 2*I_b, bias, GLU.  x[rows, NB, hidden]; weight = band-major
+ * concatenation of the per-band [2*I_b, hidden] weights; bias[2F] (band b at 2*off_b);
+ * pre[rows, 2F] = x W^T + bias; out[rows, F] = left * sigmoid(gate).  dim_offsets is the
+ * device copy of the NB+1 prefix sums of dim_inputs (host copy).
+ */
+
+/* fused_band_split.cpp:589-622 mask_estimator_final_forward and :660-693
+ * mask_estimator_final_direct_forward (.cu:2283-2310, 2369-2552): both reference modes compute
+ * these values; one kernel serves both. */
+int pmsst_mask_estimator_final_forward(const void* x, const void* weight, const void* bias,
+                                       const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
+                                       int64_t rows, int64_t hidden, void* pre, void* out, int dtype, void* stream);
+/* fused_band_split.cpp:624-658 mask_estimator_final_backward and :695-729
+ * mask_estimator_final_direct_backward (.cu:2312-2367, 2585-2851): grad_out[rows, F] ->
+ * grad_x[rows, NB, hidden], grad_bias[2F], grad_weight (packed like weight). */
+int pmsst_mask_estimator_final_backward(const void* grad_out, const void* x, const void* pre, const void* weight,
+                                        const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
+                                        int64_t rows, int64_t hidden, void* grad_x, void* grad_bias,
+                                        void* grad_weight, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -331,7 +331,8 @@ def grouped_linear_backward(grad_out, x, weight, has_bias: bool, dt: str, acc=np
 
 
 def sigmoid(z):
-    return 1.0 / (1.0 + np.exp(-z))
+    """Logistic function in the overflow-free form 0.5 * (1 + tanh(z / 2))."""
+    return 0.5 * (1.0 + np.tanh(0.5 * z))
 
 
 def mask_estimator_final_forward(x, weights, bias, dim_inputs, dt: str, acc=np.float64):

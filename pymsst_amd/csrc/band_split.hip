@@ -28,6 +28,8 @@
 #include "mfma.h"
 #include "rowgeom.h"
 
+#include <vector>
+
 namespace pmsst {
 namespace {
 
@@ -47,7 +49,7 @@ struct BandArgs {
 
 // ------------------------------------------------------------------ forward
 
-template <typename T, int TO, bool WRITE_NORMED>
+template <typename T, int TO, bool WRITE_NORMED, bool NORM>
 __global__ __launch_bounds__(kThreads) void bs_fwd_kernel(const T* __restrict__ x, const T* __restrict__ gamma,
                                                           const T* __restrict__ weight, const T* __restrict__ bias,
                                                           T* __restrict__ out, T* __restrict__ normed,
@@ -60,13 +62,14 @@ __global__ __launch_bounds__(kThreads) void bs_fwd_kernel(const T* __restrict__ 
 
   const int O = a.O;
   const int band = blockIdx.y;
+  const int oc = blockIdx.z * OT;  // first output of this block's chunk
   const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBM;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rows_valid = static_cast<int>(a.M - m0 < kBM ? a.M - m0 : kBM);
   const T* xb = x + m0 * a.x_stride + off;
-  const T* wb = weight + static_cast<int64_t>(O) * off;
+  const T* wb = weight + static_cast<int64_t>(O) * off + static_cast<int64_t>(oc) * I;
 
   f32x4_t acc[TO][4];
 #pragma unroll
@@ -82,7 +85,7 @@ __global__ __launch_bounds__(kThreads) void bs_fwd_kernel(const T* __restrict__ 
     const int k = k0 + xq;
     float g[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) g[j] = (k + j < I) ? to_f32(gamma[off + k + j]) : 0.f;
+    for (int j = 0; j < 4; ++j) g[j] = (k + j < I) ? (NORM ? to_f32(gamma[off + k + j]) : 1.f) : 0.f;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const int r = xr + 32 * p;
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void bs_fwd_kernel(const T* __restrict__ 
       }
       if (p == 0) ss0 += s; else ss1 += s;
     }
-    stage_kcontig<T, OT, kThreads>(ws, wb, I, O, k0, I, a.vec4, tid);
+    stage_kcontig<T, OT, kThreads>(ws, wb, I, O - oc, k0, I, a.vec4, tid);
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < TO; ++t) {
@@ -120,15 +123,15 @@ __global__ __launch_bounds__(kThreads) void bs_fwd_kernel(const T* __restrict__ 
     for (int p = 0; p < 2; ++p) {
       const int r = xr + 32 * p;
       const float inv = 1.0f / fmaxf(sqrtf(p == 0 ? ss0 : ss1), 1.0e-12f);
-      sscale[r] = inv * root;
-      if (r < rows_valid) inv_norm[(m0 + r) * a.NB + band] = inv;
+      sscale[r] = NORM ? inv * root : 1.0f;
+      if (NORM && blockIdx.z == 0 && r < rows_valid) inv_norm[(m0 + r) * a.NB + band] = inv;
     }
   }
   __syncthreads();
 
 #pragma unroll
   for (int t = 0; t < TO; ++t) {
-    const int o = wave * 16 * TO + t * 16 + 4 * (lane >> 4);
+    const int o = oc + wave * 16 * TO + t * 16 + 4 * (lane >> 4);
     if (o >= O) continue;
     float bv[4] = {0.f, 0.f, 0.f, 0.f};
     if (bias != nullptr) {
@@ -156,7 +159,7 @@ __global__ __launch_bounds__(kThreads) void bs_fwd_kernel(const T* __restrict__ 
     }
   }
 
-  if (WRITE_NORMED) {
+  if (WRITE_NORMED && blockIdx.z == 0) {
     for (int q = tid; q < kBM * ((I + 3) / 4); q += kThreads) {
       const int r = q / ((I + 3) / 4);
       const int k = (q % ((I + 3) / 4)) * 4;
@@ -481,21 +484,24 @@ int tile_capacity(int64_t O) {
 
 bool aligned_to(const void* p, size_t bytes) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % bytes == 0; }
 
+// norm = false runs the same kernel as a plain grouped linear (gamma, normed and inv_norm unused).
 template <typename T>
 int launch_fwd(const void* x, int64_t x_stride, const void* gamma, const void* weight, const void* bias,
                const int64_t* offsets, const HostBands& hb, int64_t M, int64_t O, void* out, void* normed,
-               float* inv_norm, hipStream_t stream) {
-  const char* op = "band_split_ragged_forward";
-  PMSST_REQUIRE(x && gamma && weight && offsets && out && inv_norm, "%s: null pointer", op);
+               float* inv_norm, bool norm, hipStream_t stream) {
+  const char* op = norm ? "band_split_ragged_forward" : "grouped_linear_forward";
   PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
-  PMSST_REQUIRE(O >= 1 && O <= 512, "%s: out_features must be in [1, 512] (got %lld)", op, (long long)O);
-  PMSST_REQUIRE(x_stride >= hb.F, "%s: x row stride %lld < total features %d", op, (long long)x_stride, hb.F);
+  PMSST_REQUIRE(O >= 1 && (O <= 512 || !norm) && O < (1 << 20), "%s: bad out_features %lld", op, (long long)O);
   if (M == 0) return PMSST_OK;
+  PMSST_REQUIRE(x && weight && offsets && out && (!norm || (gamma && inv_norm)), "%s: null pointer", op);
+  PMSST_REQUIRE(x_stride >= hb.F, "%s: x row stride %lld < total features %d", op, (long long)x_stride, hb.F);
   BandArgs a{offsets, M, hb.NB, hb.F, x_stride, static_cast<int>(O), false, false};
   a.vec4 = hb.vec4 && x_stride % 4 == 0 && aligned_to(x, 4 * sizeof(T)) && aligned_to(normed, 4 * sizeof(T)) &&
            aligned_to(weight, 4 * sizeof(T));
   a.ovec4 = O % 4 == 0 && aligned_to(out, 4 * sizeof(T)) && aligned_to(bias, 4 * sizeof(T));
-  const dim3 grid(static_cast<unsigned>((M + kBM - 1) / kBM), static_cast<unsigned>(hb.NB));
+  const int cap = 64 * tile_capacity(O);
+  const dim3 grid(static_cast<unsigned>((M + kBM - 1) / kBM), static_cast<unsigned>(hb.NB),
+                  static_cast<unsigned>((O + cap - 1) / cap));
   const T* px = static_cast<const T*>(x);
   const T* pg = static_cast<const T*>(gamma);
   const T* pw = static_cast<const T*>(weight);
@@ -504,12 +510,15 @@ int launch_fwd(const void* x, int64_t x_stride, const void* gamma, const void* w
   T* pn = static_cast<T*>(normed);
 #define PMSST_BSF(TO)                                                                                            \
   do {                                                                                                           \
-    if (pn != nullptr)                                                                                           \
-      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, true>), grid, dim3(kThreads), 0, stream, px, pg, pw, pb, po, pn,  \
-                         inv_norm, a);                                                                           \
+    if (!norm)                                                                                                   \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, false>), grid, dim3(kThreads), 0, stream, px, pg, pw, pb,  \
+                         po, pn, inv_norm, a);                                                                   \
+    else if (pn != nullptr)                                                                                      \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, true, true>), grid, dim3(kThreads), 0, stream, px, pg, pw, pb,    \
+                         po, pn, inv_norm, a);                                                                   \
     else                                                                                                         \
-      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false>), grid, dim3(kThreads), 0, stream, px, pg, pw, pb, po, pn, \
-                         inv_norm, a);                                                                           \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, true>), grid, dim3(kThreads), 0, stream, px, pg, pw, pb,   \
+                         po, pn, inv_norm, a);                                                                   \
   } while (0)
   switch (tile_capacity(O)) {
     case 1: PMSST_BSF(1); break;
@@ -531,7 +540,8 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
                const void* weight, const int64_t* offsets, const HostBands& hb, int64_t M, int64_t O, void* dx,
                void* dgamma, void* dw, void* db, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const char* op = "band_split_ragged_backward";
-  PMSST_REQUIRE(dy && nsrc && inv_norm && gamma && weight && offsets && dx && dgamma && dw, "%s: null pointer", op);
+  PMSST_REQUIRE(gamma && weight && offsets && dgamma && dw && (M == 0 || (dy && nsrc && inv_norm && dx)),
+                "%s: null pointer", op);
   PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
   PMSST_REQUIRE(O >= 1 && O <= 512, "%s: out_features must be in [1, 512] (got %lld)", op, (long long)O);
   const size_t need = bwd_workspace(M, hb.F);
@@ -601,7 +611,22 @@ int pmsst_band_split_ragged_forward(const void* x, int64_t x_row_stride, const v
   return with_dtype(dtype, "band_split_ragged_forward", [&](auto tag) {
     using T = decltype(tag);
     return launch_fwd<T>(x, x_row_stride, gamma, weight, bias, dim_offsets, hb, rows, out_features, out, normed,
-                         inv_norm, static_cast<hipStream_t>(stream));
+                         inv_norm, true, static_cast<hipStream_t>(stream));
+  });
+}
+
+int pmsst_grouped_linear_forward(const void* x, int64_t x_row_stride, const void* weight, const void* bias,
+                                 const int64_t* group_offsets, int64_t groups, int64_t in_features, int64_t rows,
+                                 int64_t out_features, void* out, int dtype, void* stream) {
+  PMSST_REQUIRE(groups > 0 && groups < (1 << 16) && in_features > 0, "grouped_linear_forward: bad shape");
+  std::vector<int64_t> dims(static_cast<size_t>(groups), in_features);
+  HostBands hb;
+  int rc = check_bands("grouped_linear_forward", dims.data(), groups, &hb);
+  if (rc != PMSST_OK) return rc;
+  return with_dtype(dtype, "grouped_linear_forward", [&](auto tag) {
+    using T = decltype(tag);
+    return launch_fwd<T>(x, x_row_stride, nullptr, weight, bias, group_offsets, hb, rows, out_features, out, nullptr,
+                         nullptr, false, static_cast<hipStream_t>(stream));
   });
 }
 

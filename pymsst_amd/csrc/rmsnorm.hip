@@ -189,10 +189,10 @@ __global__ __launch_bounds__(kRowBwdThreads) void rms_bwd_kernel(const TDY* __re
 template <typename TX, typename TG, typename TO>
 int launch_fwd(const void* x, const void* gamma, void* out, void* normed, float* inv_norm, int64_t rows,
                int64_t dim, hipStream_t stream) {
-  PMSST_REQUIRE(x && gamma && out && inv_norm, "rms_norm_forward: null pointer");
   PMSST_REQUIRE(rows >= 0 && dim > 0 && dim <= (1 << 20), "rms_norm_forward: bad shape rows=%lld dim=%lld",
                 (long long)rows, (long long)dim);
   if (rows == 0) return PMSST_OK;
+  PMSST_REQUIRE(x && gamma && out && inv_norm, "rms_norm_forward: null pointer");
   constexpr int kVec = 16 / sizeof(TX);
   const void* ptrs[] = {x, gamma, out, normed};
   const size_t sizes[] = {sizeof(TX), sizeof(TG), sizeof(TO), sizeof(TO)};
@@ -235,9 +235,10 @@ template <typename TDY, typename TN, typename TG, typename TDX, bool FROM_X>
 int launch_bwd(const void* dy, const void* nsrc, const float* inv_norm, const void* gamma, void* dx,
                void* grad_gamma, int gamma_out_dtype, int64_t rows, int64_t dim, void* workspace,
                size_t workspace_bytes, hipStream_t stream) {
-  PMSST_REQUIRE(dy && nsrc && inv_norm && gamma && dx && grad_gamma, "rms_norm_backward: null pointer");
   PMSST_REQUIRE(rows >= 0 && dim > 0 && dim <= (1 << 20), "rms_norm_backward: bad shape rows=%lld dim=%lld",
                 (long long)rows, (long long)dim);
+  PMSST_REQUIRE(grad_gamma && (rows == 0 || (dy && nsrc && inv_norm && gamma && dx)),
+                "rms_norm_backward: null pointer");
   constexpr int kVec = sizeof(TDY) >= sizeof(TDX) ? 16 / sizeof(TDY) : 16 / sizeof(TDX);
   const void* ptrs[] = {dy, nsrc, gamma, dx};
   const size_t sizes[] = {sizeof(TDY), sizeof(TN), sizeof(TG), sizeof(TDX)};

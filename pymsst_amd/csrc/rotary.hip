@@ -56,12 +56,12 @@ template <typename T>
 int launch_rotary(const void* in, const void* cosv, const void* sinv, void* out, int64_t batch, int64_t seq,
                   int64_t heads, int64_t dim, int64_t cs_seq, int64_t cs_pair, bool inverse, hipStream_t stream) {
   const char* op = inverse ? "rotary_backward" : "rotary_forward";
-  PMSST_REQUIRE(in && cosv && sinv && out, "%s: null pointer", op);
   PMSST_REQUIRE(batch >= 0 && seq >= 0 && heads >= 0 && dim > 0 && dim % 2 == 0,
                 "%s: bad shape [%lld, %lld, %lld, %lld]", op, (long long)batch, (long long)seq, (long long)heads,
                 (long long)dim);
   const int64_t total = batch * seq * heads * dim;
   if (total == 0) return PMSST_OK;
+  PMSST_REQUIRE(in && cosv && sinv && out, "%s: null pointer", op);
   int vec = 16 / sizeof(T);
   auto aligned = [&](int v) {
     return dim % v == 0 && reinterpret_cast<uintptr_t>(in) % (v * sizeof(T)) == 0 &&
@@ -281,6 +281,7 @@ inline int norm_rot_check(const char* op, const NormRotArgs& a, int vec, const v
 template <typename T, typename TG>
 int launch_norm_rot_fwd(const void* x, const void* gamma, const void* cosv, const void* sinv, void* out,
                         float* inv_norm, const NormRotArgs& a, hipStream_t stream) {
+  if (a.batch * a.seq * a.heads == 0 && a.dim > 0) return PMSST_OK;
   PMSST_REQUIRE(x && gamma && cosv && sinv && out && inv_norm, "rms_norm_rotary_forward: null pointer");
   constexpr int kVec = 16 / sizeof(T);
   const void* ptrs[] = {x, gamma, out};
@@ -316,7 +317,8 @@ template <typename T, typename TG>
 int launch_norm_rot_bwd(const void* dy, const void* x, const float* inv_norm, const void* gamma, const void* cosv,
                         const void* sinv, void* dx, void* dgamma, int gamma_dtype, const NormRotArgs& a,
                         void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  PMSST_REQUIRE(dy && x && inv_norm && gamma && cosv && sinv && dx && dgamma,
+  const bool empty = a.batch * a.seq * a.heads == 0;
+  PMSST_REQUIRE(dgamma && gamma && (empty || (dy && x && inv_norm && cosv && sinv && dx)),
                 "rms_norm_rotary_backward: null pointer");
   constexpr int kVec = 16 / sizeof(T);
   const void* ptrs[] = {dy, x, gamma, dx};

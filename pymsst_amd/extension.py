@@ -514,5 +514,131 @@ class HipFusedExtension:
     band_split_backward_v2 = band_split_backward
     band_split_backward_v3 = band_split_backward
 
+    # ------------------------------------------------------------------ grouped linear
+
+    def grouped_linear_forward(self, x, weight, bias=None):
+        """``.cpp:365-388``: ``x[M,G,I]`` (strided view allowed), ``weight[G,O,I]``, ``bias[G,O]`` or ``None``
+        -> ``out[M,G,O]``."""
+        _req(x.is_cuda, "x must be a CUDA tensor")
+        _req(weight.is_cuda, "weight must be a CUDA tensor")
+        if bias is not None:
+            _req(bias.is_cuda, "bias must be a CUDA tensor")
+        _req(x.dim() == 3, "x must have shape [M, G, I]")
+        _req(weight.dim() == 3, "weight must have shape [G, O, I]")
+        _req(weight.size(0) == x.size(1), "weight group dimension must match x")
+        _req(weight.size(2) == x.size(2), "weight input dimension must match x")
+        if bias is not None:
+            _req(bias.dim() == 2, "bias must have shape [G, O]")
+            _req(bias.size(0) == x.size(1), "bias group dimension must match x")
+            _req(bias.size(1) == weight.size(1), "bias output dimension must match weight")
+        _req(weight.dtype == x.dtype, "weight dtype must match x")
+        if bias is not None:
+            _req(bias.dtype == x.dtype, "bias dtype must match x")
+        m, g, i = x.shape
+        o = weight.size(1)
+        if not (x.stride(2) == 1 and x.stride(1) == i and x.stride(0) >= g * i):
+            x = x.contiguous()
+        weight = weight.contiguous()
+        bias = bias.contiguous() if bias is not None else None
+        _, dev_offs, _ = self._bands((i,) * g, x.device)
+        out = torch.empty((m, g, o), dtype=x.dtype, device=x.device)
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_grouped_linear_forward(
+                _ptr(x), x.stride(0) if m > 0 else g * i, _ptr(weight), _ptr(bias), _ptr(dev_offs), g, i, m, o,
+                _ptr(out), dtype_code(x.dtype), _stream(x.device),
+            )
+        check(rc, "pmsst_grouped_linear_forward")
+        return out
+
+    # ------------------------------------------------------------------ mask estimator final layer
+
+    def _mask_check(self, x, weights, dim_inputs, dim_offsets):
+        _req(x.is_cuda, "x must be a CUDA tensor")
+        _req(dim_offsets.is_cuda, "dim_offsets must be a CUDA tensor")
+        _req(x.dim() == 3, "x must have shape [M, G, H]")
+        _req(dim_offsets.dim() == 1, "dim_offsets must be 1D")
+        _req(dim_offsets.dtype == torch.int64, "dim_offsets must be int64")
+        _req(len(weights) == x.size(1), "weights length must match band count")
+        _req(len(dim_inputs) == len(weights), "dim_inputs length must match weights length")
+        _req(dim_offsets.size(0) == x.size(1) + 1, "dim_offsets length must be band count + 1")
+        for w, d in zip(weights, dim_inputs):
+            _req(w.is_cuda, "weight must be a CUDA tensor")
+            _req(w.dim() == 2, "weight must have shape [2 * O, H]")
+            _req(w.size(1) == x.size(2), "weight hidden dimension must match x")
+            _req(w.size(0) == int(d) * 2, "weight output dimension must match dim_inputs")
+            _req(w.dtype == x.dtype, "weight dtype must match x")
+            _req(w.device == x.device, "weight device must match x")
+
+    def mask_estimator_final_forward_packed(self, x, weight_all, bias, dim_inputs):
+        """Final layer + GLU on packed weights; returns ``[out[M,F], pre[M,2F]]``."""
+        host, dev_offs, offs = self._bands(dim_inputs, x.device)
+        nb, total = len(offs) - 1, offs[-1]
+        x = x.contiguous()
+        m, h = x.size(0), x.size(2)
+        pre = torch.empty((m, 2 * total), dtype=x.dtype, device=x.device)
+        out = torch.empty((m, total), dtype=x.dtype, device=x.device)
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_mask_estimator_final_forward(
+                _ptr(x), _ptr(weight_all), _ptr(bias), _ptr(dev_offs), host, nb, m, h, _ptr(pre), _ptr(out),
+                dtype_code(x.dtype), _stream(x.device),
+            )
+        check(rc, "pmsst_mask_estimator_final_forward")
+        return [out, pre]
+
+    def mask_estimator_final_backward_packed(self, grad_out, x, pre, weight_all, dim_inputs):
+        """Backward on packed weights; returns ``[grad_x[M,NB,H], grad_bias[2F], grad_weight (packed)]``."""
+        host, dev_offs, offs = self._bands(dim_inputs, grad_out.device)
+        nb = len(offs) - 1
+        grad_out = grad_out.contiguous()
+        x = x.contiguous()
+        pre = pre.contiguous()
+        m, h = x.size(0), x.size(2)
+        dx = torch.empty_like(x)
+        db = torch.empty((pre.size(1),), dtype=x.dtype, device=x.device)
+        dw = torch.empty((weight_all.numel(),), dtype=x.dtype, device=x.device)
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_mask_estimator_final_backward(
+                _ptr(grad_out), _ptr(x), _ptr(pre), _ptr(weight_all), _ptr(dev_offs), host, nb, m, h, _ptr(dx),
+                _ptr(db), _ptr(dw), dtype_code(x.dtype), _stream(x.device),
+            )
+        check(rc, "pmsst_mask_estimator_final_backward")
+        return [dx, db, dw]
+
+    def mask_estimator_final_forward(self, x, weights, bias, dim_inputs, dim_offsets):
+        """``.cpp:589-622`` / ``.cpp:660-693`` (direct): ``x[M,NB,H]``, per-band ``weight[2*I_b, H]``,
+        ``bias[2F]`` -> ``[out[M,F], pre[M,2F], x_contiguous]``."""
+        self._mask_check(x, weights, dim_inputs, dim_offsets)
+        _req(bias.is_cuda, "bias must be a CUDA tensor")
+        _req(bias.dim() == 1, "bias must have shape [2 * total]")
+        _req(bias.size(0) == 2 * sum(int(d) for d in dim_inputs), "bias dimension must match dim_inputs")
+        _req(bias.dtype == x.dtype, "bias dtype must match x")
+        _req(bias.device == x.device, "bias device must match x")
+        x = x.contiguous()
+        weight_all = torch.cat([w.reshape(-1) for w in weights])
+        out, pre = self.mask_estimator_final_forward_packed(x, weight_all, bias.contiguous(), dim_inputs)
+        return [out, pre, x]
+
+    def mask_estimator_final_backward(self, grad_out, x, pre, weights, dim_inputs, dim_offsets):
+        """``.cpp:624-658`` / ``.cpp:695-729`` (direct): returns ``[grad_x, grad_bias, *grad_weights]``."""
+        self._mask_check(x, weights, dim_inputs, dim_offsets)
+        _req(grad_out.is_cuda, "grad_out must be a CUDA tensor")
+        _req(pre.is_cuda, "pre must be a CUDA tensor")
+        _req(grad_out.dim() == 2, "grad_out must have shape [M, total]")
+        _req(pre.dim() == 2, "pre must have shape [M, 2 * total]")
+        _req(grad_out.size(0) == x.size(0), "grad_out M must match x")
+        _req(pre.size(0) == x.size(0), "pre M must match x")
+        _req(pre.size(1) == grad_out.size(1) * 2, "pre total dimension must be twice grad_out")
+        _req(grad_out.dtype == x.dtype, "grad_out dtype must match x")
+        _req(pre.dtype == x.dtype, "pre dtype must match x")
+        weight_all = torch.cat([w.reshape(-1) for w in weights])
+        dx, db, dw = self.mask_estimator_final_backward_packed(grad_out, x, pre, weight_all, dim_inputs)
+        h = x.size(2)
+        dims = [int(d) for d in dim_inputs]
+        dws = [v.view(2 * d, h) for v, d in zip(dw.split([2 * d * h for d in dims]), dims)]
+        return [dx, db, *dws]
+
+    mask_estimator_final_direct_forward = mask_estimator_final_forward
+    mask_estimator_final_direct_backward = mask_estimator_final_backward
+
 
 __all__ = ["HipFusedExtension", "PmsstError"]

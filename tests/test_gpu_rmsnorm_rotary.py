@@ -46,8 +46,14 @@ def test_rms_norm_plain(hip_ext, dtype, rows, dim):
         # zero row: dx = inv * gn * sqrt(D) with inv = 1e12 -- compared relative to its own scale
         keep = [i for i in range(rows) if i != 3]
         assert_parity(dx[keep], r_dx[keep], dn, "dx")
-        rel = np.max(np.abs(to_np(dx[3]) - r_dx[3])) / max(np.max(np.abs(r_dx[3])), 1e-30)
-        assert rel <= (1e-5 if dn == "f32" else 2e-2), f"zero-row dx rel err {rel}"
+        a3, r3 = to_np(dx[3]), r_dx[3]
+        # fp16 overflows to inf here (1e12 * g): both sides must agree on which entries are infinite
+        assert np.array_equal(np.isinf(a3), np.isinf(r3))
+        assert np.array_equal(a3[np.isinf(a3)], r3[np.isinf(r3)])
+        fin = np.isfinite(r3)
+        if fin.any():
+            rel = np.max(np.abs(a3[fin] - r3[fin])) / max(np.max(np.abs(r3[fin])), 1e-30)
+            assert rel <= (1e-5 if dn == "f32" else 2e-2), f"zero-row dx rel err {rel}"
     else:
         assert_parity(dx, r_dx, dn, "dx")
     assert_parity(dg, r_dg, dn, "dgamma")
