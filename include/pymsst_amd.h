@@ -134,7 +134,9 @@ int pmsst_band_split_ragged_forward(const void* x, int64_t x_row_stride, const v
                                     const void* bias, const int64_t* dim_offsets, const int64_t* dim_inputs,
                                     int64_t band_count, int64_t rows, int64_t out_features, void* out, void* normed,
                                     float* inv_norm, int dtype, void* stream);
-size_t pmsst_band_split_ragged_backward_workspace_size(int64_t rows, int64_t total_in);
+/* Workspace bytes of the backward (dgamma / dbias reduction partials). */
+size_t pmsst_band_split_ragged_backward_workspace_size(int64_t rows, int64_t total_in, int64_t band_count,
+                                                       int64_t out_features);
 /* fused_band_split.cpp:316-363 band_split_ragged_backward (.cu:741-1003).  With equal widths it also
  * implements band_split_backward / _v2 / _v3 (fused_band_split.cpp:172-269, .cu:125-587).
  * `saved` is normed[rows, F] (saved_is_input = 0) or the forward input x[rows, F] (saved_is_input = 1,
@@ -171,13 +173,16 @@ int pmsst_grouped_linear_forward(const void* x, int64_t x_row_stride, const void
 int pmsst_mask_estimator_final_forward(const void* x, const void* weight, const void* bias,
                                        const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
                                        int64_t rows, int64_t hidden, void* pre, void* out, int dtype, void* stream);
+/* Workspace bytes of the backward: the [rows, 2*total] GLU derivative plus reduction partials. */
+size_t pmsst_mask_estimator_final_backward_workspace_size(int64_t rows, int64_t total, int dtype);
 /* fused_band_split.cpp:624-658 mask_estimator_final_backward and :695-729
  * mask_estimator_final_direct_backward (.cu:2312-2367, 2585-2851): grad_out[rows, F] ->
  * grad_x[rows, NB, hidden], grad_bias[2F], grad_weight (packed like weight). */
 int pmsst_mask_estimator_final_backward(const void* grad_out, const void* x, const void* pre, const void* weight,
                                         const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
                                         int64_t rows, int64_t hidden, void* grad_x, void* grad_bias,
-                                        void* grad_weight, int dtype, void* stream);
+                                        void* grad_weight, int dtype, void* workspace, size_t workspace_bytes,
+                                        void* stream);
 
 #ifdef __cplusplus
 }

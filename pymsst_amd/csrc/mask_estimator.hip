@@ -9,23 +9,24 @@
 //   out    [M, F]  left * sigmoid(gate)
 // F = sum_b I_b.
 //
-// Forward block (m-tile of 64, band b, chunk of 64 GLU outputs l): each wave owns
-// 16 outputs and computes both their left rows (l) and gate rows (I_b + l), so
-// the GLU is applied to two accumulators held by the same lane.
+// Forward block (128 rows of M, band b, 64 GLU outputs l): A = the 64 left rows
+// and the 64 gate rows of W_b for those outputs, B = x rows; waves split M so
+// each lane holds a left accumulator and the gate accumulator of the same
+// output, and the GLU is applied in registers.
 //
-// Backward: dpre = (g * s, g * L * s * (1 - s)) is recomputed from pre and
-// grad_out while staging MFMA operands; it is never written to HBM.
-//   dx block (m-tile, band, 256 hidden): dx^T[h][m] = W_b^T dpre^T, K = 2*I_b.
-//   dW block (band, 64 j x 64 h): dW[j][h] = sum_m dpre[m][j] x[m][b][h], K = M;
-//   blocks of the first h tile also reduce dbias.  No atomics.
+// Backward:
+//   1. me_dpre_kernel writes dpre = (g * s, g * L * s * (1 - s)), s = sigmoid(G),
+//      to a [M, 2F] workspace (one pass over pre and grad_out);
+//   2. dbias = column sums of dpre (colsum_rows_kernel + col_sum_kernel);
+//   3. dx^T[h][m] = W_b^T dpre_b^T  (K = 2*I_b), tiles 128 h x 64 m;
+//   4. dW^T[h][j] = x_b^T dpre_b    (K = M),     tiles 128 h x 64 j.
+// All reductions have a fixed order; no atomics.
 #include "common.h"
-#include "mfma.h"
+#include "gemm.h"
+#include "rowgeom.h"
 
 namespace pmsst {
 namespace {
-
-constexpr int kThreads = 256;
-constexpr int kBM = 64;
 
 struct MaskArgs {
   const int64_t* offsets;  // device [NB + 1] (prefix sums of I_b)
@@ -40,80 +41,112 @@ __device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + __ex
 
 // ------------------------------------------------------------------ forward
 
+// A operand of the forward: rows [0, 64) are left rows l0 + r of W_b, rows
+// [64, 128) the gate rows I + l0 + (r - 64); K = H contiguous.
 template <typename T>
-__global__ __launch_bounds__(kThreads) void me_fwd_kernel(const T* __restrict__ x, const T* __restrict__ weight,
-                                                          const T* __restrict__ bias, T* __restrict__ pre,
-                                                          T* __restrict__ out, int max_lchunks, MaskArgs a) {
-  constexpr int P = LdsPitch<T>::value;
-  __shared__ T wl[64 * P];
-  __shared__ T wg[64 * P];
-  __shared__ T xs[kBM * P];
+struct LeftGateLoader {
+  static constexpr int kQuads = 128 * (kChunkK / 4) / kGemmThreads;
+  struct Regs {
+    Pack<T, 4> q[kQuads];
+  };
+  const T* wb;  // band weights [2I][H]
+  int H, I, l0;
+  bool vec4;
+  __device__ __forceinline__ void fetch(int k0, Regs& g) const {
+#pragma unroll
+    for (int i = 0; i < kQuads; ++i) {
+      const int idx = threadIdx.x + i * kGemmThreads;
+      const int r = idx / (kChunkK / 4);
+      const int k = k0 + (idx % (kChunkK / 4)) * 4;
+      const int l = l0 + (r & 63);
+      const bool ok = l < I;
+      const T* p = wb + static_cast<int64_t>(r < 64 ? l : I + l) * H + k;
+      if (ok && vec4 && k + 4 <= H) {
+        g.q[i] = *reinterpret_cast<const Pack<T, 4>*>(p);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) g.q[i].v[j] = (ok && k + j < H) ? p[j] : from_f32<T>(0.f);
+      }
+    }
+  }
+  __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
+#pragma unroll
+    for (int i = 0; i < kQuads; ++i) {
+      const int idx = threadIdx.x + i * kGemmThreads;
+      const int r = idx / (kChunkK / 4);
+      const int kq = (idx % (kChunkK / 4)) * 4;
+      if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<Pack<T, 4>*>(lds + lds_index<T>(r, kq)) = g.q[i];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lds[lds_index<T>(r, kq + j)] = g.q[i].v[j];
+      }
+    }
+  }
+};
 
+constexpr int kFwdBM = 128;
+
+template <typename T>
+__global__ __launch_bounds__(kGemmThreads) void me_fwd_kernel(const T* __restrict__ x, const T* __restrict__ weight,
+                                                              const T* __restrict__ bias, T* __restrict__ pre,
+                                                              T* __restrict__ out, int max_lchunks, MaskArgs a) {
+  __shared__ T lds[gemm_lds_elems<T, 128, kFwdBM>()];
+  using S = TileShape<128, kFwdBM, 1, 4>;  // TR = 8 (4 left + 4 gate), TC = 2
   const int band = blockIdx.y / max_lchunks;
   const int l0 = (blockIdx.y % max_lchunks) * 64;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
   if (l0 >= I) return;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBM;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int rows_valid = static_cast<int>(a.M - m0 < kBM ? a.M - m0 : kBM);
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kFwdBM;
+  const int rows_valid = static_cast<int>(a.M - m0 < kFwdBM ? a.M - m0 : kFwdBM);
   const int H = a.H;
-  const T* wb = weight + static_cast<int64_t>(2) * off * H;  // [2I][H]
-  const T* xb = x + (m0 * a.NB + band) * H;                   // row m at + m * NB * H
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
-  f32x4_t accl[4], accg[4];
+  LeftGateLoader<T> la{weight + static_cast<int64_t>(2) * off * H, H, I, l0, a.vec4};
+  KRowLoader<T, kFwdBM> lb{x + (m0 * a.NB + band) * H, static_cast<int64_t>(a.NB) * H, rows_valid, H, a.vec4};
+  f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) accl[j] = accg[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < S::kTR; ++i)
+#pragma unroll
+    for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  gemm_mainloop<T, 128, kFwdBM, 1, 4>(la, lb, H, lds, acc);
 
-  for (int k0 = 0; k0 < H; k0 += kChunkK) {
-    // 3 tiles of 64 rows x 32: left weights, gate weights, x  (768 quads per tile set, 3 per thread)
-    stage_kcontig<T, 64, kThreads>(wl, wb + static_cast<int64_t>(l0) * H, H, I - l0, k0, H, a.vec4, tid);
-    stage_kcontig<T, 64, kThreads>(wg, wb + static_cast<int64_t>(I + l0) * H, H, I - l0, k0, H, a.vec4, tid);
-    stage_kcontig<T, kBM, kThreads>(xs, xb, static_cast<int64_t>(a.NB) * H, rows_valid, k0, H, a.vec4, tid);
-    __syncthreads();
-    const T* lrow = wl + (wave * 16 + (lane & 15)) * P;
-    const T* grow = wg + (wave * 16 + (lane & 15)) * P;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const T* brow = xs + (j * 16 + (lane & 15)) * P;
-      accl[j] = mfma_chunk<T>(lrow, brow, accl[j], lane);
-      accg[j] = mfma_chunk<T>(grow, brow, accg[j], lane);
-    }
-    __syncthreads();
-  }
-
-  const int l = l0 + wave * 16 + 4 * (lane >> 4);
-  if (l >= I) return;
-  float bl[4], bg[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    bl[r] = l + r < I ? to_f32(bias[2 * off + l + r]) : 0.f;
-    bg[r] = l + r < I ? to_f32(bias[2 * off + I + l + r]) : 0.f;
-  }
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = j * 16 + (lane & 15);
-    if (m >= rows_valid) continue;
-    float vl[4], vg[4], vo[4];
+  for (int i = 0; i < 4; ++i) {
+    const int l = l0 + i * 16 + 4 * (lane >> 4);
+    if (l >= I) continue;
+    float bl[4], bg[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      vl[r] = accl[j][r] + bl[r];
-      vg[r] = accg[j][r] + bg[r];
-      vo[r] = vl[r] * sigmoidf_(vg[r]);
+      bl[r] = l + r < I ? to_f32(bias[2 * off + l + r]) : 0.f;
+      bg[r] = l + r < I ? to_f32(bias[2 * off + I + l + r]) : 0.f;
     }
-    T* pl = pre + (m0 + m) * pitch2 + 2 * off + l;
-    T* pg = pl + I;
-    T* po = out + (m0 + m) * a.F + off + l;
-    if (a.vec4) {
-      store_pack<T, 4>(pl, vl);
-      store_pack<T, 4>(pg, vg);
-      store_pack<T, 4>(po, vo);
-    } else {
-      for (int r = 0; r < 4 && l + r < I; ++r) {
-        pl[r] = from_f32<T>(vl[r]);
-        pg[r] = from_f32<T>(vg[r]);
-        po[r] = from_f32<T>(vo[r]);
+#pragma unroll
+    for (int j = 0; j < S::kTC; ++j) {
+      const int m = wave * (kFwdBM / 4) + j * 16 + (lane & 15);
+      if (m >= rows_valid) continue;
+      float vl[4], vg[4], vo[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        vl[r] = acc[i][j][r] + bl[r];
+        vg[r] = acc[i + 4][j][r] + bg[r];
+        vo[r] = vl[r] * sigmoidf_(vg[r]);
+      }
+      T* pl = pre + (m0 + m) * pitch2 + 2 * off + l;
+      T* pg = pl + I;
+      T* po = out + (m0 + m) * a.F + off + l;
+      if (a.vec4) {
+        store_pack<T, 4>(pl, vl);
+        store_pack<T, 4>(pg, vg);
+        store_pack<T, 4>(po, vo);
+      } else {
+        for (int r = 0; r < 4 && l + r < I; ++r) {
+          pl[r] = from_f32<T>(vl[r]);
+          pg[r] = from_f32<T>(vg[r]);
+          po[r] = from_f32<T>(vo[r]);
+        }
       }
     }
   }
@@ -121,111 +154,100 @@ __global__ __launch_bounds__(kThreads) void me_fwd_kernel(const T* __restrict__ 
 
 // ------------------------------------------------------------------ backward
 
-// dpre for column j of band (width I) in one row: pre_row = pre + m * 2F + 2 * off,
-// g_row = grad_out + m * F + off.
-template <typename T>
-__device__ __forceinline__ float dpre_at(const T* __restrict__ pre_row, const T* __restrict__ g_row, int I, int j) {
-  const int l = j < I ? j : j - I;
-  const float left = to_f32(pre_row[l]);
-  const float gate = to_f32(pre_row[I + l]);
-  const float s = sigmoidf_(gate);
-  const float g = to_f32(g_row[l]);
-  return j < I ? g * s : g * left * s * (1.0f - s);
-}
+constexpr int kDpreRows = 64;
 
-// B tile for the dx GEMM: lds[m][k] = dpre[m0 + m][k0 + k], K-contiguous rows.
+// dpre for rows [blockIdx.x * 64, +64) of band blockIdx.y, 4 outputs per item.
 template <typename T>
-__device__ __forceinline__ void stage_dpre_rows(T* __restrict__ lds, const T* __restrict__ pre,
-                                                const T* __restrict__ gout, int64_t m0, int rows_valid, int off,
-                                                int I, int F, int k0, int tid) {
-  constexpr int P = LdsPitch<T>::value;
-  const int K = 2 * I;
-  for (int q = tid; q < kBM * (kChunkK / 4); q += kThreads) {
-    const int r = q / (kChunkK / 4);
-    const int kq = (q % (kChunkK / 4)) * 4;
-    const T* prow = pre + (m0 + r) * 2 * static_cast<int64_t>(F) + 2 * off;
-    const T* grow = gout + (m0 + r) * static_cast<int64_t>(F) + off;
+__global__ __launch_bounds__(256) void me_dpre_kernel(const T* __restrict__ gout, const T* __restrict__ pre,
+                                                      T* __restrict__ dpre, MaskArgs a) {
+  const int band = blockIdx.y;
+  const int off = static_cast<int>(a.offsets[band]);
+  const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kDpreRows;
+  const int rows = static_cast<int>(a.M - m0 < kDpreRows ? a.M - m0 : kDpreRows);
+  const int nq = (I + 3) / 4;
+  const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
+  for (int idx = threadIdx.x; idx < rows * nq; idx += 256) {
+    const int r = idx / nq;
+    const int l = (idx - r * nq) * 4;
+    const int64_t m = m0 + r;
+    const T* gp = gout + m * a.F + off + l;
+    const T* pl = pre + m * pitch2 + 2 * off + l;
+    const T* pg = pl + I;
+    T* dl = dpre + m * pitch2 + 2 * off + l;
+    T* dg = dl + I;
+    float g[4], L[4], G[4], ol[4], og[4];
+    if (a.vec4) {
+      load_pack<T, 4>(gp, g);
+      load_pack<T, 4>(pl, L);
+      load_pack<T, 4>(pg, G);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = k0 + kq + j;
-      const float v = (r < rows_valid && k < K) ? dpre_at(prow, grow, I, k) : 0.f;
-      lds[r * P + kq + j] = from_f32<T>(v);
-    }
-  }
-}
-
-// A tile of the dx GEMM: lds[h][k] = W_b[k0 + k][h0 + h] (transposed: W_b rows are contiguous in h).
-template <typename T, int ROWS>
-__device__ __forceinline__ void stage_wT(T* __restrict__ lds, const T* __restrict__ wb, int H, int h0, int K, int k0,
-                                         bool vec4, int tid) {
-  constexpr int P = LdsPitch<T>::value;
-  for (int q = tid; q < (ROWS / 4) * kChunkK; q += kThreads) {
-    const int hq = (q % (ROWS / 4)) * 4;  // consecutive threads -> consecutive h quads (coalesced)
-    const int k = q / (ROWS / 4);
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (k0 + k < K) {
-      const T* src = wb + static_cast<int64_t>(k0 + k) * H + h0 + hq;
-      if (vec4 && h0 + hq + 4 <= H) {
-        load_pack<T, 4>(src, v);
-      } else {
-        for (int j = 0; j < 4 && h0 + hq + j < H; ++j) v[j] = to_f32(src[j]);
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = l + j < I;
+        g[j] = ok ? to_f32(gp[j]) : 0.f;
+        L[j] = ok ? to_f32(pl[j]) : 0.f;
+        G[j] = ok ? to_f32(pg[j]) : 0.f;
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) lds[(hq + j) * P + k] = from_f32<T>(v[j]);
+    for (int j = 0; j < 4; ++j) {
+      const float s = sigmoidf_(G[j]);
+      ol[j] = g[j] * s;
+      og[j] = g[j] * L[j] * s * (1.0f - s);
+    }
+    if (a.vec4) {
+      store_pack<T, 4>(dl, ol);
+      store_pack<T, 4>(dg, og);
+    } else {
+      for (int j = 0; j < 4 && l + j < I; ++j) {
+        dl[j] = from_f32<T>(ol[j]);
+        dg[j] = from_f32<T>(og[j]);
+      }
+    }
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void me_bwd_dx_kernel(const T* __restrict__ gout, const T* __restrict__ pre,
-                                                             const T* __restrict__ weight, T* __restrict__ dx,
-                                                             int hchunks, MaskArgs a) {
-  constexpr int P = LdsPitch<T>::value;
-  constexpr int kBH = 256;  // hidden rows per block: 4 waves x 4 tiles x 16
-  __shared__ T ws[kBH * P];
-  __shared__ T ds[kBM * P];
+constexpr int kDxBH = 128;
+constexpr int kDxBM = 64;
 
+template <typename T>
+__global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __restrict__ dpre,
+                                                                 const T* __restrict__ weight, T* __restrict__ dx,
+                                                                 MaskArgs a) {
+  __shared__ T lds[gemm_lds_elems<T, kDxBH, kDxBM>()];
+  using S = TileShape<kDxBH, kDxBM, 2, 2>;
   const int band = blockIdx.y;
-  const int h0 = blockIdx.z * kBH;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBM;
+  const int h0 = blockIdx.z * kDxBH;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kDxBM;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
-  const int K = 2 * I;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int rows_valid = static_cast<int>(a.M - m0 < kBM ? a.M - m0 : kBM);
   const int H = a.H;
-  const T* wb = weight + static_cast<int64_t>(2) * off * H;
-  (void)hchunks;
+  const int rows_valid = static_cast<int>(a.M - m0 < kDxBM ? a.M - m0 : kDxBM);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
 
-  f32x4_t acc[4][4];
+  // A[h][j] = W_b[j][h0 + h]  (MN-contiguous in h);  B[m][j] = dpre[m0 + m][2 off + j]
+  MNLoader<T, kDxBH> la{weight + static_cast<int64_t>(2) * off * H + h0, H, H - h0, 2 * I, a.vec4};
+  KRowLoader<T, kDxBM> lb{dpre + m0 * pitch2 + 2 * off, pitch2, rows_valid, 2 * I, a.vec4};
+  f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int i = 0; i < S::kTR; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[t][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  gemm_mainloop<T, kDxBH, kDxBM, 2, 2>(la, lb, 2 * I, lds, acc);
 
-  for (int k0 = 0; k0 < K; k0 += kChunkK) {
-    stage_wT<T, kBH>(ws, wb, H, h0, K, k0, a.vec4, tid);
-    stage_dpre_rows<T>(ds, pre, gout, m0, rows_valid, off, I, a.F, k0, tid);
-    __syncthreads();
+  const int hr = (wave >> 1) * (kDxBH / 2), mc = (wave & 1) * (kDxBM / 2);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const T* arow = ws + (wave * 64 + t * 16 + (lane & 15)) * P;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[t][j] = mfma_chunk<T>(arow, ds + (j * 16 + (lane & 15)) * P, acc[t][j], lane);
-    }
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int h = h0 + wave * 64 + t * 16 + 4 * (lane >> 4);
+  for (int i = 0; i < S::kTR; ++i) {
+    const int h = h0 + hr + i * 16 + 4 * (lane >> 4);
     if (h >= H) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = j * 16 + (lane & 15);
+    for (int j = 0; j < S::kTC; ++j) {
+      const int m = mc + j * 16 + (lane & 15);
       if (m >= rows_valid) continue;
       T* dst = dx + ((m0 + m) * a.NB + band) * H + h;
-      float v[4] = {acc[t][j][0], acc[t][j][1], acc[t][j][2], acc[t][j][3]};
+      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
       if (a.vec4) {
         store_pack<T, 4>(dst, v);
       } else {
@@ -235,135 +257,53 @@ __global__ __launch_bounds__(kThreads) void me_bwd_dx_kernel(const T* __restrict
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void me_bwd_dw_kernel(const T* __restrict__ gout, const T* __restrict__ pre,
-                                                             const T* __restrict__ x, T* __restrict__ dw,
-                                                             T* __restrict__ dbias, int max_jchunks, MaskArgs a) {
-  constexpr int P = LdsPitch<T>::value;
-  __shared__ T as[64 * P];  // [j][m]
-  __shared__ T bs[64 * P];  // [h][m]
-  __shared__ float sdb[4][64];
+constexpr int kDwBH = 128;
+constexpr int kDwBJ = 64;
 
-  const int h0 = blockIdx.x * 64;
+template <typename T>
+__global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __restrict__ dpre, const T* __restrict__ x,
+                                                                 T* __restrict__ dw, int max_jchunks, MaskArgs a) {
+  __shared__ T lds[gemm_lds_elems<T, kDwBH, kDwBJ>()];
+  using S = TileShape<kDwBH, kDwBJ, 2, 2>;
+  const int h0 = blockIdx.x * kDwBH;
   const int band = blockIdx.y / max_jchunks;
-  const int j0 = (blockIdx.y % max_jchunks) * 64;
+  const int j0 = (blockIdx.y % max_jchunks) * kDwBJ;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
   const int K2 = 2 * I;
   if (j0 >= K2) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wj = (wave >> 1) * 32, wh = (wave & 1) * 32;
   const int H = a.H;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
 
-  f32x4_t acc[2][2];
+  // A[h][m] = x[m][band][h0 + h];  B[j][m] = dpre[m][2 off + j0 + j]   (both MN-contiguous, K = M)
+  MNLoader<T, kDwBH> la{x + static_cast<int64_t>(band) * H + h0, static_cast<int64_t>(a.NB) * H, H - h0,
+                        static_cast<int>(a.M), a.vec4};
+  MNLoader<T, kDwBJ> lb{dpre + 2 * off + j0, pitch2, K2 - j0, static_cast<int>(a.M), a.vec4};
+  f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
+  for (int i = 0; i < S::kTR; ++i)
 #pragma unroll
-    for (int v = 0; v < 2; ++v) acc[u][v] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float dbp0 = 0.f, dbp1 = 0.f;
-
-  for (int64_t mb = 0; mb < a.M; mb += kChunkK) {
-    const int k_valid = static_cast<int>(a.M - mb < kChunkK ? a.M - mb : kChunkK);
-    if (tid < 128) {
-      // A: lds[j][m] = dpre[mb + m][j0 + j]; thread -> j pair 2*(tid%32), m octet tid/32
-      const int jj = 2 * (tid % 32);
-      const int kb = (tid / 32) * 8;
-      float v0[8], v1[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int m = kb + q;
-        float e0 = 0.f, e1 = 0.f;
-        if (m < k_valid) {
-          const T* prow = pre + (mb + m) * pitch2 + 2 * off;
-          const T* grow = gout + (mb + m) * static_cast<int64_t>(a.F) + off;
-          if (j0 + jj < K2) e0 = dpre_at(prow, grow, I, j0 + jj);
-          if (j0 + jj + 1 < K2) e1 = dpre_at(prow, grow, I, j0 + jj + 1);
-        }
-        v0[q] = e0;
-        v1[q] = e1;
-        dbp0 += e0;
-        dbp1 += e1;
-      }
-      if constexpr (sizeof(T) == 2) {
-        store_pack<T, 8>(as + jj * P + kb, v0);
-        store_pack<T, 8>(as + (jj + 1) * P + kb, v1);
-      } else {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          as[jj * P + kb + q] = v0[q];
-          as[(jj + 1) * P + kb + q] = v1[q];
-        }
-      }
-    } else {
-      // B: lds[h][m] = x[mb + m][band][h0 + h]; thread -> h pair, m octet
-      const int t = tid - 128;
-      const int hh = 2 * (t % 32);
-      const int kb = (t / 32) * 8;
-      float v0[8], v1[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int m = kb + q;
-        float e0 = 0.f, e1 = 0.f;
-        if (m < k_valid) {
-          const T* src = x + ((mb + m) * a.NB + band) * static_cast<int64_t>(H) + h0 + hh;
-          if (h0 + hh + 2 <= H && (H % 2 == 0)) {
-            float e[2];
-            load_pack<T, 2>(src, e);
-            e0 = e[0];
-            e1 = e[1];
-          } else {
-            if (h0 + hh < H) e0 = to_f32(src[0]);
-            if (h0 + hh + 1 < H) e1 = to_f32(src[1]);
-          }
-        }
-        v0[q] = e0;
-        v1[q] = e1;
-      }
-      if constexpr (sizeof(T) == 2) {
-        store_pack<T, 8>(bs + hh * P + kb, v0);
-        store_pack<T, 8>(bs + (hh + 1) * P + kb, v1);
-      } else {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          bs[hh * P + kb + q] = v0[q];
-          bs[(hh + 1) * P + kb + q] = v1[q];
-        }
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const T* arow = as + (wj + u * 16 + (lane & 15)) * P;
-#pragma unroll
-      for (int v = 0; v < 2; ++v) acc[u][v] = mfma_chunk<T>(arow, bs + (wh + v * 16 + (lane & 15)) * P, acc[u][v], lane);
-    }
-    __syncthreads();
-  }
+    for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  gemm_mainloop<T, kDwBH, kDwBJ, 2, 2>(la, lb, static_cast<int>(a.M), lds, acc);
 
   T* dwb = dw + static_cast<int64_t>(2) * off * H;  // [2I][H]
+  const int hr = (wave >> 1) * (kDwBH / 2), jc = (wave & 1) * (kDwBJ / 2);
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int i = 0; i < S::kTR; ++i) {
+    const int h = h0 + hr + i * 16 + 4 * (lane >> 4);
+    if (h >= H) continue;
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      const int h = h0 + wh + v * 16 + (lane & 15);
-      if (h >= H) continue;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = j0 + wj + u * 16 + 4 * (lane >> 4) + r;
-        if (j < K2) dwb[static_cast<int64_t>(j) * H + h] = from_f32<T>(acc[u][v][r]);
+    for (int j = 0; j < S::kTC; ++j) {
+      const int jj = j0 + jc + j * 16 + (lane & 15);
+      if (jj >= K2) continue;
+      T* dst = dwb + static_cast<int64_t>(jj) * H + h;
+      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      if (a.vec4) {
+        store_pack<T, 4>(dst, v);
+      } else {
+        for (int r = 0; r < 4 && h + r < H; ++r) dst[r] = from_f32<T>(v[r]);
       }
-    }
-  }
-
-  if (blockIdx.x == 0) {
-    if (tid < 128) {
-      sdb[tid / 32][2 * (tid % 32)] = dbp0;
-      sdb[tid / 32][2 * (tid % 32) + 1] = dbp1;
-    }
-    __syncthreads();
-    if (tid < 64 && j0 + tid < K2) {
-      dbias[2 * off + j0 + tid] = from_f32<T>(sdb[0][tid] + sdb[1][tid] + sdb[2][tid] + sdb[3][tid]);
     }
   }
 }
@@ -407,38 +347,57 @@ int launch_me_fwd(const void* x, const void* weight, const void* bias, const int
   a.vec4 = hm.vec4 && al(x, 4 * sizeof(T)) && al(weight, 4 * sizeof(T)) && al(pre, 4 * sizeof(T)) &&
            al(out, 4 * sizeof(T));
   const int max_lchunks = (hm.max_width + 63) / 64;
-  const dim3 grid(static_cast<unsigned>((M + kBM - 1) / kBM), static_cast<unsigned>(hm.NB * max_lchunks));
-  hipLaunchKernelGGL((me_fwd_kernel<T>), grid, dim3(kThreads), 0, stream, static_cast<const T*>(x),
+  const dim3 grid(static_cast<unsigned>((M + kFwdBM - 1) / kFwdBM), static_cast<unsigned>(hm.NB * max_lchunks));
+  hipLaunchKernelGGL((me_fwd_kernel<T>), grid, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
                      static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
                      static_cast<T*>(out), max_lchunks, a);
   return check_launch("me_fwd_kernel");
 }
 
+size_t me_bwd_workspace(int64_t M, int F, size_t elem) {
+  const size_t dpre = align_up(static_cast<size_t>(M) * 2 * static_cast<size_t>(F) * elem, 256);
+  return dpre + colsum_rows_workspace(M, 2 * static_cast<int64_t>(F));
+}
+
 template <typename T>
 int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* weight, const int64_t* offsets,
-                  const HostMask& hm, int64_t M, int64_t H, void* dx, void* dbias, void* dw, hipStream_t stream) {
+                  const HostMask& hm, int64_t M, int64_t H, void* dx, void* dbias, void* dw, void* workspace,
+                  size_t workspace_bytes, hipStream_t stream) {
   const char* op = "mask_estimator_final_backward";
-  PMSST_REQUIRE(weight && offsets && dbias && dw && (M == 0 || (gout && x && pre && dx)), "%s: null pointer", op);
   PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
+  PMSST_REQUIRE(weight && offsets && dbias && dw && (M == 0 || (gout && x && pre && dx)), "%s: null pointer", op);
+  const size_t need = me_bwd_workspace(M, hm.F, sizeof(T));
+  if (workspace == nullptr || workspace_bytes < need) {
+    return fail(PMSST_EWORKSPACE, "%s: workspace of %zu bytes needed, got %zu", op, need,
+                workspace == nullptr ? size_t{0} : workspace_bytes);
+  }
   MaskArgs a{offsets, M, hm.NB, static_cast<int>(H), hm.F, false};
   a.vec4 = hm.vec4 && al(x, 4 * sizeof(T)) && al(weight, 4 * sizeof(T)) && al(pre, 4 * sizeof(T)) &&
-           al(dx, 4 * sizeof(T));
-  const T* pg = static_cast<const T*>(gout);
-  const T* pp = static_cast<const T*>(pre);
+           al(dx, 4 * sizeof(T)) && al(gout, 4 * sizeof(T)) && al(dw, 4 * sizeof(T));
+  T* dpre = static_cast<T*>(workspace);
+  float* partial = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                            align_up(static_cast<size_t>(M) * 2 * hm.F * sizeof(T), 256));
   if (M > 0) {
-    const int hchunks = static_cast<int>((H + 255) / 256);
-    const dim3 grid(static_cast<unsigned>((M + kBM - 1) / kBM), static_cast<unsigned>(hm.NB),
-                    static_cast<unsigned>(hchunks));
-    hipLaunchKernelGGL((me_bwd_dx_kernel<T>), grid, dim3(kThreads), 0, stream, pg, pp, static_cast<const T*>(weight),
-                       static_cast<T*>(dx), hchunks, a);
-    int rc = check_launch("me_bwd_dx_kernel");
+    const dim3 g1(static_cast<unsigned>((M + kDpreRows - 1) / kDpreRows), static_cast<unsigned>(hm.NB));
+    hipLaunchKernelGGL((me_dpre_kernel<T>), g1, dim3(256), 0, stream, static_cast<const T*>(gout),
+                       static_cast<const T*>(pre), dpre, a);
+    int rc = check_launch("me_dpre_kernel");
+    if (rc != PMSST_OK) return rc;
+    const dim3 g2(static_cast<unsigned>((M + kDxBM - 1) / kDxBM), static_cast<unsigned>(hm.NB),
+                  static_cast<unsigned>((H + kDxBH - 1) / kDxBH));
+    hipLaunchKernelGGL((me_bwd_dx_kernel<T>), g2, dim3(kGemmThreads), 0, stream, dpre, static_cast<const T*>(weight),
+                       static_cast<T*>(dx), a);
+    rc = check_launch("me_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
-  const int max_jchunks = (2 * hm.max_width + 63) / 64;
-  const dim3 grid(static_cast<unsigned>((H + 63) / 64), static_cast<unsigned>(hm.NB * max_jchunks));
-  hipLaunchKernelGGL((me_bwd_dw_kernel<T>), grid, dim3(kThreads), 0, stream, pg, pp, static_cast<const T*>(x),
-                     static_cast<T*>(dw), static_cast<T*>(dbias), max_jchunks, a);
-  return check_launch("me_bwd_dw_kernel");
+  const int max_jchunks = (2 * hm.max_width + kDwBJ - 1) / kDwBJ;
+  const dim3 g3(static_cast<unsigned>((H + kDwBH - 1) / kDwBH), static_cast<unsigned>(hm.NB * max_jchunks));
+  hipLaunchKernelGGL((me_bwd_dw_kernel<T>), g3, dim3(kGemmThreads), 0, stream, dpre, static_cast<const T*>(x),
+                     static_cast<T*>(dw), max_jchunks, a);
+  int rc = check_launch("me_bwd_dw_kernel");
+  if (rc != PMSST_OK) return rc;
+  return launch_colsum_rows(dpre, dtype_code<T>(), M, 2 * static_cast<int64_t>(hm.F), partial, dbias,
+                            dtype_code<T>(), stream);
 }
 
 template <typename F>
@@ -471,17 +430,23 @@ int pmsst_mask_estimator_final_forward(const void* x, const void* weight, const 
   });
 }
 
+size_t pmsst_mask_estimator_final_backward_workspace_size(int64_t rows, int64_t total, int dtype) {
+  if (rows < 0 || total <= 0 || !dtype_ok(dtype)) return 0;
+  return me_bwd_workspace(rows, static_cast<int>(total), dtype_size(dtype));
+}
+
 int pmsst_mask_estimator_final_backward(const void* grad_out, const void* x, const void* pre, const void* weight,
                                         const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
                                         int64_t rows, int64_t hidden, void* grad_x, void* grad_bias,
-                                        void* grad_weight, int dtype, void* stream) {
+                                        void* grad_weight, int dtype, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
   HostMask hm;
   int rc = check_mask("mask_estimator_final_backward", dim_inputs, band_count, hidden, &hm);
   if (rc != PMSST_OK) return rc;
   return with_dtype(dtype, "mask_estimator_final_backward", [&](auto tag) {
     using T = decltype(tag);
     return launch_me_bwd<T>(grad_out, x, pre, weight, dim_offsets, hm, rows, hidden, grad_x, grad_bias, grad_weight,
-                            static_cast<hipStream_t>(stream));
+                            workspace, workspace_bytes, static_cast<hipStream_t>(stream));
   });
 }
 

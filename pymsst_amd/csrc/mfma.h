@@ -59,32 +59,4 @@ __device__ __forceinline__ f32x4_t mfma_chunk<float>(const float* a_row, const f
   return acc;
 }
 
-// Raw 16-bit pattern of a storage value (for register transposes).
-__device__ __forceinline__ uint32_t bits16(bf16 v) { return __builtin_bit_cast(uint16_t, v); }
-__device__ __forceinline__ uint32_t bits16(f16 v) { return __builtin_bit_cast(uint16_t, v); }
-
-// Stage a K-contiguous source into lds[ROWS][pitch]: element (r, k) of the
-// chunk is src[r * stride + k0 + k]; rows >= rows_valid and k >= k_valid are zero.
-// Each thread moves 4-element groups; `vec4` selects 4-wide loads (the caller
-// guarantees 4-element alignment of every row start and of k0).
-template <typename T, int ROWS, int THREADS>
-__device__ __forceinline__ void stage_kcontig(T* __restrict__ lds, const T* __restrict__ src, int64_t stride,
-                                              int rows_valid, int k0, int k_valid, bool vec4, int tid) {
-  constexpr int P = LdsPitch<T>::value;
-  for (int q = tid; q < ROWS * (kChunkK / 4); q += THREADS) {
-    const int r = q / (kChunkK / 4);
-    const int kq = (q % (kChunkK / 4)) * 4;
-    const int k = k0 + kq;
-    float v[4];
-    if (r < rows_valid && vec4 && k + 4 <= k_valid) {
-      load_pack<T, 4>(src + r * stride + k, v);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = (r < rows_valid && k + j < k_valid) ? to_f32(src[r * stride + k + j]) : 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) lds[r * P + kq + j] = from_f32<T>(v[j]);
-  }
-}
-
 }  // namespace pmsst

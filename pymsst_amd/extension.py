@@ -353,7 +353,7 @@ class HipFusedExtension:
         dg = torch.empty((total,), dtype=grad_out.dtype, device=dev)
         dw = torch.empty((o * total,), dtype=grad_out.dtype, device=dev)
         db = torch.empty((nb * o,), dtype=grad_out.dtype, device=dev) if has_bias else None
-        ws = _workspace(self._lib.pmsst_band_split_ragged_backward_workspace_size(m, total), dev)
+        ws = _workspace(self._lib.pmsst_band_split_ragged_backward_workspace_size(m, total, nb, o), dev)
         with _DeviceGuard(dev):
             rc = self._lib.pmsst_band_split_ragged_backward(
                 _ptr(grad_out), _ptr(saved), 1 if saved_is_input else 0, _ptr(inv_norm.contiguous()),
@@ -596,10 +596,12 @@ class HipFusedExtension:
         dx = torch.empty_like(x)
         db = torch.empty((pre.size(1),), dtype=x.dtype, device=x.device)
         dw = torch.empty((weight_all.numel(),), dtype=x.dtype, device=x.device)
+        code = dtype_code(x.dtype)
+        ws = _workspace(self._lib.pmsst_mask_estimator_final_backward_workspace_size(m, offs[-1], code), x.device)
         with _DeviceGuard(x.device):
             rc = self._lib.pmsst_mask_estimator_final_backward(
                 _ptr(grad_out), _ptr(x), _ptr(pre), _ptr(weight_all), _ptr(dev_offs), host, nb, m, h, _ptr(dx),
-                _ptr(db), _ptr(dw), dtype_code(x.dtype), _stream(x.device),
+                _ptr(db), _ptr(dw), code, _ptr(ws), ws.numel(), _stream(x.device),
             )
         check(rc, "pmsst_mask_estimator_final_backward")
         return [dx, db, dw]

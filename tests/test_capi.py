@@ -40,8 +40,9 @@ def test_abi_version_and_error_string(lib):
 
 def test_workspace_queries(lib):
     assert lib.pmsst_rms_norm_backward_workspace_size(1000, 192) == 512 * 192 * 4
-    assert lib.pmsst_band_split_ragged_backward_workspace_size(1032, 4100) == 17 * 4100 * 4
-    assert lib.pmsst_band_split_ragged_backward_workspace_size(0, 4100) == 0
+    dg = -(-17 * 4100 * 4 // 256) * 256
+    assert lib.pmsst_band_split_ragged_backward_workspace_size(1032, 4100, 62, 192) == dg + 17 * 62 * 192 * 4
+    assert lib.pmsst_mask_estimator_final_backward_workspace_size(1032, 4100, 2) >= 1032 * 8200 * 2
 
 
 def test_argument_errors_need_no_device(lib):
