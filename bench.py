@@ -15,7 +15,11 @@ the launch stream inside the timed region; ``roofline`` reports the op with
 the largest share of the step.  ``cpu_baseline`` times the numpy oracle
 (``oracle/``) on a bounded sample of the same workload on the host.
 
-Usage: ``python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]``.
+``train`` reports the second half of the metric: BS-RoFormer train
+samples/s with the stock modules and with the HIP kernels patched in.
+
+Usage: ``python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]
+[--train-steps 20] [--train-warmup 3]``.
 """
 
 from __future__ import annotations
@@ -34,6 +38,14 @@ if str(REPO) not in sys.path:
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "fused-layer fwd+bwd HBM GB/s (% peak) + BSR train samples/s, 1 MI355X"
+# ops of the step that are a single kernel, launched n times per op call
+SINGLE_KERNEL_OPS = {
+    "band_split_fwd": ("bs_fwd_kernel", 1),
+    "qk_norm_rotary_fwd": ("norm_rot_fwd_kernel", 2),
+    "mask_final_fwd": ("me_fwd_kernel", 1),
+}
+# measured HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated), by kernel
+TRAFFIC_PER_LAUNCH: dict = {}
 BSR_WIDTHS = tuple([8] * 24 + [16] * 12 + [48] * 8 + [96] * 8 + [192] * 8 + [512, 516])
 
 
@@ -44,6 +56,8 @@ def _args(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--train-steps", type=int, default=20, help="timed BS-RoFormer train steps per backend (0: skip)")
+    ap.add_argument("--train-warmup", type=int, default=3)
     return ap.parse_args(argv)
 
 
@@ -79,11 +93,10 @@ class Workload:
             [(torch.randn(2 * d, self.hidden, generator=pg) / self.hidden**0.5).reshape(-1) for d in self.dims]
         ).to(dev, dtype)
         self.b_me = (0.1 * torch.randn(2 * self.F, generator=pg)).to(dev, dtype)
-        import oracle
+        from pymsst_amd.core.transformer import RotaryEmbedding
 
-        c, s = oracle.rotary_tables(self.T, 64, 10000.0)
-        self.cos = torch.from_numpy(c).to(dev, dtype).reshape(1, self.T, 1, 32)
-        self.sin = torch.from_numpy(s).to(dev, dtype).reshape(1, self.T, 1, 32)
+        cos, sin = RotaryEmbedding(64, 10000.0).tables(self.T, dev, dtype)
+        self.cos, self.sin = cos[..., ::2], sin[..., ::2]  # [1, T, 1, 32] strided views
         gg = g(5)
         self.g_bs = torch.randn(self.M, self.NB, self.dim, generator=gg).to(dev, dtype)
         self.g_q = torch.randn(self.qk_shape, generator=gg).to(dev, dtype)
@@ -216,6 +229,65 @@ def _cpu_baseline(budget_s: float):
     }
 
 
+def _train_leg(torch, steps: int, warmup: int) -> dict:
+    """BS-RoFormer dim 192, depth 6, 4 stems, batch 4 x 131584 stereo samples,
+    bf16 autocast, multi-resolution STFT loss, AdamW 5e-4.  One step = forward, backward and
+    optimizer step; train samples/s = batch / median step time, for the stock modules and for
+    the model patched onto the HIP kernels (same seed, same batch)."""
+    import statistics
+
+    from pymsst_amd import fused_roformer as fr
+    from pymsst_amd.workloads import WORKLOADS, workload_batch
+
+    wl = WORKLOADS["bsr_train"]
+    dev = torch.device("cuda:0")
+    target, mixture = workload_batch(wl, seed=0, device=dev)
+    out = {}
+    for impl in ("stock", "fused"):
+        fr.restore_stock_implementations()
+        model = wl.build_model(dev, seed=4)
+        model.train()
+        status = None
+        if impl == "fused":
+            for key, value in fr.RUNTIME_PRESETS["hip_full"].items():
+                os.environ[key] = value
+            status = fr.apply_roformer_fused_training_backend(model, "hip", rms_norm_mode="fast")
+            if status.active == "off":
+                raise RuntimeError(f"fused backend inactive: {status.reason}")
+        else:
+            os.environ[fr.CORE_GROUPED_TRAIN_ENV] = "1"
+        opt = torch.optim.AdamW(model.parameters(), lr=wl.lr)
+        times, losses = [], []
+        for i in range(warmup + steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = model(mixture, target)
+            loss.backward()
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+            torch.cuda.synchronize()
+            if i >= warmup:
+                times.append(time.perf_counter() - t0)
+                losses.append(float(loss.detach()))
+        med = statistics.median(times)
+        out[impl] = {"ms_median": round(med * 1e3, 2), "samples_per_s": round(wl.batch / med, 3),
+                     "first_loss": round(losses[0], 6), "last_loss": round(losses[-1], 6)}
+        fr.restore_stock_implementations(model)
+        del model, opt
+        torch.cuda.empty_cache()
+    return {
+        "workload": "configs[2] BS-RoFormer dim 192, depth 6, 8x64 heads, 4 stems, batch 4 x 131584 stereo "
+                    "(258 frames), bf16 autocast, multi-res STFT L1, AdamW 5e-4",
+        "steps": steps,
+        "warmup": warmup,
+        "fused_samples_per_s": out["fused"]["samples_per_s"],
+        "stock_samples_per_s": out["stock"]["samples_per_s"],
+        "speedup": round(out["fused"]["samples_per_s"] / out["stock"]["samples_per_s"], 3),
+        "detail": out,
+    }
+
+
 def main(argv=None) -> int:
     args = _args(argv)
     if args.gpus != 1:
@@ -274,19 +346,26 @@ def main(argv=None) -> int:
         }
     total_bytes = sum(b for b, _ in traffic.values())
     value = total_bytes / (ms_per_step * 1e-3) / 1e9
-    dom = max(per_op, key=lambda k: per_op[k]["ms"])
-    d = per_op[dom]
+    # roofline of the dominant single kernel: ops that are one kernel launched `n` times
+    single = {name: per_op[name]["ms"] / n for name, (_, n) in SINGLE_KERNEL_OPS.items()}
+    dom = max(single, key=single.get)
+    kname, nlaunch = SINGLE_KERNEL_OPS[dom]
+    launch_ms = single[dom]
+    launch_bytes = traffic[dom][0] / nlaunch
+    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
     roofline = {
-        "kernel": dom,
+        "kernel": kname,
+        "op": dom,
         "bound": "hbm",
-        "achieved": d["GB/s"],
+        "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
-        "frac": round(d["GB/s"] / HBM_PEAK_GBS, 4),
-        "traffic": None,
-        "bytes_per_launch": traffic[dom][0],
-        "avg_ms": d["ms"],
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": TRAFFIC_PER_LAUNCH.get(kname),
+        "bytes_per_launch": int(launch_bytes),
+        "avg_ms": round(launch_ms, 5),
     }
+    train = _train_leg(torch, args.train_steps, args.train_warmup) if args.train_steps > 0 else None
     cpu = None if args.no_cpu_baseline else _cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC,
@@ -308,6 +387,7 @@ def main(argv=None) -> int:
             "wall_s_timed": round(wall, 3),
         },
         "per_op": per_op,
+        "train": train,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

@@ -14,8 +14,10 @@ so feature packing, rotary tables and init follow the public architecture:
   table shared across depth; no output norm inside blocks, one ``final_norm``.
 * Mask estimators: per band ``MLP(dim -> hidden -> 2 * 4 * bins_b)`` + GLU; the
   masks multiply the complex STFT and iSTFT returns the separated stems.
-* Loss when ``target`` is given: waveform L1 plus the multi-resolution STFT L1
-  (windows 4096, 2048, 1024, 512, 256; hop 147; ``n_fft = max(win, 2048)``).
+* Loss when ``target`` is given (``loss=``): ``"multi_stft"`` = waveform L1 plus the
+  multi-resolution STFT L1 (windows 4096, 2048, 1024, 512, 256; hop 147;
+  ``n_fft = max(win, 2048)``); ``"l1"`` = waveform L1; ``"spec_l1"`` = L1 between the
+  estimated and the target complex spectrograms (real and imaginary parts).
 * ``checkpoint_blocks=True`` recomputes each axial block in the backward.
 """
 
@@ -60,8 +62,12 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
         multi_stft_normalized: bool = False,
         rotary_theta: float = 10000.0,
         checkpoint_blocks: bool = False,
+        loss: str = "multi_stft",
     ):
         super().__init__()
+        if loss not in ("multi_stft", "l1", "spec_l1"):
+            raise ValueError(f"unknown loss {loss!r}")
+        self.loss_type = loss
         self.stereo = stereo
         self.audio_channels = 2 if stereo else 1
         self.num_stems = num_stems
@@ -135,6 +141,8 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
         stems = mask.shape[1]
         mask = torch.view_as_complex(mask.float().reshape(b, stems, t, -1, 2).contiguous()).transpose(-1, -2)
         est = spec.unsqueeze(1) * mask  # [B, stems, F*C, T]
+        if target is not None and self.loss_type == "spec_l1":
+            return self._spec_loss(est, target, c)
         est = est.reshape(b, stems, -1, c, t).transpose(2, 3).reshape(b * stems * c, -1, t)
         recon = torch.istft(est, window=window, length=length, return_complex=False, **self.stft_kwargs)
         recon = recon.reshape(b, stems, c, length)
@@ -144,11 +152,21 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
             return recon
         return self.loss(recon, target)
 
+    def _spec_loss(self, est: torch.Tensor, target: torch.Tensor, channels: int) -> torch.Tensor:
+        """L1 on (re, im) of ``est[B, stems, F*C, T]`` against the STFT of ``target[B, stems, C, L]``."""
+        b, stems = est.shape[:2]
+        if target.ndim == 3:
+            target = target.unsqueeze(1)
+        tspec, _ = self._stft(target.reshape(b * stems, channels, -1))
+        return F.l1_loss(torch.view_as_real(est), torch.view_as_real(tspec.reshape(est.shape)))
+
     def loss(self, recon: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
         if target.ndim == recon.ndim - 1:
             target = target.unsqueeze(-2)
         target = target[..., : recon.shape[-1]]
         loss = F.l1_loss(recon, target)
+        if self.loss_type == "l1":
+            return loss
         multi = recon.new_zeros(())
         flat_r = recon.reshape(-1, recon.shape[-1]).float()
         flat_t = target.reshape(-1, target.shape[-1]).float()

@@ -1006,6 +1006,40 @@ class _FusedRMSNormMixed(torch.autograd.Function):
         return dx.reshape(ctx.input_shape), dgamma, None
 
 
+_CORE_PATCH_POINTS = (
+    # (module in pymsst_amd.core, owner attribute or None, patched name, marker of the saved original)
+    ("transformer", None, "apply_rotary_emb_fast", "_pymsst_original_apply_rotary"),
+    ("transformer", "RMSNorm", "forward", "_pymsst_original_forward"),
+    ("bands", None, "grouped_linear", "_pymsst_original_grouped_linear"),
+    ("bands", "MaskEstimator", "_forward_layer_grouped_mlp", "_pymsst_original_forward_layer_grouped_mlp"),
+    ("bands", "MaskEstimator", "_get_layer_group_params", "_pymsst_original_get_layer_group_params"),
+    ("bands", "BandSplit", "_get_group_params", "_pymsst_original_get_group_params"),
+    ("common", "RoformerRuntimeMixin", "_estimate_masks", "_pymsst_original_estimate_masks"),
+)
+
+
+def restore_stock_implementations(model: torch.nn.Module | None = None) -> None:
+    """Undo every patch ``apply_roformer_fused_training_backend`` made (this build's addition;
+    the reference has no inverse).  Module- and class-level patches are unwound to the
+    stock functions; with ``model`` its BandSplit instances get their stock
+    ``_forward_grouped`` back.  Used to run stock and fused models in one process."""
+    bands, transformer, common = _core()
+    modules = {"bands": bands, "transformer": transformer, "common": common}
+    for mod_name, owner_name, name, marker in _CORE_PATCH_POINTS:
+        owner = modules[mod_name] if owner_name is None else getattr(modules[mod_name], owner_name)
+        current = getattr(owner, name)
+        while getattr(current, marker, None) is not None:
+            current = getattr(current, marker)
+        setattr(owner, name, current)
+    if model is not None:
+        for module in model.modules():
+            if getattr(module, "_pymsst_fused_band_split", False):
+                del module._forward_grouped
+                for attr in ("_pymsst_original_forward_grouped", "_pymsst_fused_extension",
+                             "_pymsst_fused_band_split_bwd_mode", "_pymsst_fused_band_split"):
+                    module.__dict__.pop(attr, None)
+
+
 def reference_band_split_group(x, gamma, weight, bias):
     """Math statement of one band group (fr.py:1265-1271): normalise, scale, per-group Linear.
 
@@ -1026,4 +1060,5 @@ __all__ = [
     "normalize_fused_kernel_backend",
     "normalize_fused_rms_norm_mode",
     "reference_band_split_group",
+    "restore_stock_implementations",
 ]

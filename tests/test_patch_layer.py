@@ -1,0 +1,271 @@
+"""CPU tests of the patch layer (``pymsst_amd.fused_roformer``), mirroring the reference's
+switchboard tests (tests/test_training_smoke.py:236-512, 627-637): backend and mode
+normalisation, fallback when the extension is missing, duck-typed ``extension=``
+injection, bwd-mode precedence, the layout-reduce-copy helpers, the packing autograd
+Function, the pure-torch GLU Function, parameter-reference caches, and that every
+patch can be undone."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from pymsst_amd import fused_roformer as fr
+from pymsst_amd.core import bands, common, transformer
+from pymsst_amd.core.bs_roformer import BSRoformer
+
+_BANDS = (2,) * 16 + (4,) * 8 + (32,) + (33,)
+
+
+def _small_model(mask_depth: int = 2) -> BSRoformer:
+    torch.manual_seed(0)
+    return BSRoformer(dim=16, depth=1, stereo=True, num_stems=1, heads=2, dim_head=8, stft_n_fft=256,
+                      stft_hop_length=64, stft_win_length=256, freqs_per_bands=_BANDS,
+                      mask_estimator_depth=mask_depth, mlp_expansion_factor=2, loss="spec_l1")
+
+
+@pytest.fixture(autouse=True)
+def _clean(monkeypatch):
+    for name in list(fr.RUNTIME_PRESETS["hip_full"]) + [fr.EXPERIMENTAL_RMS_NORM_ENV, fr.EXPERIMENTAL_GROUPED_LINEAR_ENV,
+                                                         fr.EXPERIMENTAL_MASK_ESTIMATOR_FINAL_ENV,
+                                                         fr.EXPERIMENTAL_BAND_SPLIT_BWD_V2_ENV,
+                                                         fr.EXPERIMENTAL_TRAIN_PARAM_PACK_AUTOGRAD_ENV,
+                                                         fr.EXPERIMENTAL_ATTENTION_GATES_ENV]:
+        monkeypatch.delenv(name, raising=False)
+    monkeypatch.setenv(fr.CORE_GROUPED_TRAIN_ENV, "")
+    yield
+    fr.restore_stock_implementations()
+
+
+def test_backend_defaults_to_off():
+    status = fr.apply_roformer_fused_training_backend(_small_model(), None)
+    assert status.active == "off" and status.requested == "off" and status.reason is None
+    assert fr.normalize_fused_kernel_backend("CUDA-EXT") == "cuda_ext"
+    assert fr.normalize_fused_kernel_backend("hip") == "cuda_ext"
+    with pytest.raises(ValueError, match="fused_kernel_backend"):
+        fr.normalize_fused_kernel_backend("unknown")
+    with pytest.raises(ValueError, match="fused_rms_norm_mode"):
+        fr.normalize_fused_rms_norm_mode("unknown")
+
+
+def test_falls_back_when_extension_is_unavailable(monkeypatch):
+    def fail_load():
+        raise fr.FusedKernelUnavailable("no extension in this test")
+
+    monkeypatch.setattr(fr, "load_fused_band_split_extension", fail_load)
+    with pytest.warns(RuntimeWarning, match="no extension"):
+        status = fr.apply_roformer_fused_training_backend(_small_model(), "cuda_ext")
+    assert status.active == "off" and status.requested == "cuda_ext"
+    assert "no extension" in status.reason
+
+
+def test_real_loader_refuses_without_gpu():
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(fr.FusedKernelUnavailable):
+        fr.load_fused_band_split_extension()
+
+
+def test_can_patch_band_split_with_injected_extension():
+    model = _small_model()
+    status = fr.apply_roformer_fused_training_backend(model, "cuda_ext", extension=object())
+    assert status.active == "cuda_ext" and status.patched_band_splits == 1
+    assert model.band_split._pymsst_fused_band_split is True
+    assert status.patched_single_stem_masks is True
+    # patching twice is idempotent
+    again = fr.apply_roformer_fused_training_backend(model, "cuda_ext", extension=object())
+    assert again.patched_band_splits == 0
+
+
+def test_band_split_bwd_v3_takes_precedence_over_v2(monkeypatch):
+    class FakeExtension:
+        def band_split_backward_v2(self):
+            raise AssertionError("not called")
+
+        def band_split_backward_v3(self):
+            raise AssertionError("not called")
+
+    monkeypatch.setenv(fr.EXPERIMENTAL_BAND_SPLIT_BWD_V2_ENV, "1")
+    monkeypatch.setenv(fr.EXPERIMENTAL_BAND_SPLIT_BWD_V3_ENV, "1")
+    model = _small_model()
+    status = fr.apply_roformer_fused_training_backend(model, "cuda_ext", extension=FakeExtension())
+    assert status.patched_band_split_bwd_v2 is False and status.patched_band_split_bwd_v3 is True
+    assert model.band_split._pymsst_fused_band_split_bwd_mode == "v3"
+
+
+def test_rms_norm_bwd_v2_env_enables_fast_mode(monkeypatch):
+    assert fr.normalize_fused_rms_norm_mode(None) is None
+    monkeypatch.setenv(fr.EXPERIMENTAL_RMS_NORM_BWD_V2_ENV, "1")
+    assert fr.normalize_fused_rms_norm_mode(None) == "fast"
+    assert fr.normalize_fused_rms_norm_mode("off") is None
+    monkeypatch.setenv(fr.EXPERIMENTAL_RMS_NORM_ENV, "safe")
+    assert fr.normalize_fused_rms_norm_mode(None) == "mixed"
+
+
+def test_status_records_every_patch_with_full_extension(monkeypatch):
+    ext = type("FullExt", (), {name: object() for name in (
+        "band_split_forward", "band_split_backward", "band_split_backward_v2", "band_split_backward_v3",
+        "band_split_ragged_forward", "band_split_ragged_backward", "grouped_linear_forward", "rotary_forward",
+        "rotary_backward", "rms_norm_forward", "rms_norm_backward", "rms_norm_forward_fp32_gamma",
+        "rms_norm_backward_fp32_gamma", "rms_norm_forward_mixed", "rms_norm_backward_mixed",
+        "mask_estimator_final_forward", "mask_estimator_final_backward", "mask_estimator_final_direct_forward",
+        "mask_estimator_final_direct_backward")})()
+    for key, value in fr.RUNTIME_PRESETS["hip_full"].items():
+        monkeypatch.setenv(key, value)
+    monkeypatch.setenv(fr.EXPERIMENTAL_TRAIN_PARAM_PACK_AUTOGRAD_ENV, "1")
+    status = fr.apply_roformer_fused_training_backend(_small_model(), "hip", extension=ext)
+    assert status.patched_band_split_ragged_forward and status.patched_band_split_ragged_backward
+    assert status.patched_band_split_bwd_v3 and status.patched_rotary
+    assert status.patched_rms_norm and status.rms_norm_mode == "fast" and status.patched_rms_norm_bwd_v2
+    assert status.patched_layout_reduce_copy and status.patched_mask_final_autograd
+    assert status.patched_train_param_pack_autograd
+    assert status.patched_mask_estimator_final and status.mask_estimator_final_mode == "direct"
+    assert status.patched_attention_gates is False
+    assert getattr(transformer.apply_rotary_emb_fast, "_pymsst_fused_rotary", False)
+    assert getattr(transformer.RMSNorm.forward, "_pymsst_fused_rms_norm", False)
+
+
+def test_restore_stock_implementations_unwinds_everything(monkeypatch):
+    originals = (transformer.apply_rotary_emb_fast, transformer.RMSNorm.forward, bands.grouped_linear,
+                 bands.MaskEstimator._forward_layer_grouped_mlp, bands.MaskEstimator._get_layer_group_params,
+                 bands.BandSplit._get_group_params, common.RoformerRuntimeMixin._estimate_masks)
+    ext = type("Ext", (), {n: object() for n in ("rotary_forward", "rotary_backward", "rms_norm_forward",
+                                                  "rms_norm_backward", "grouped_linear_forward",
+                                                  "mask_estimator_final_direct_forward",
+                                                  "mask_estimator_final_direct_backward")})()
+    for key, value in fr.RUNTIME_PRESETS["hip_full"].items():
+        monkeypatch.setenv(key, value)
+    monkeypatch.setenv(fr.EXPERIMENTAL_GROUPED_LINEAR_ENV, "1")
+    model = _small_model()
+    fr.apply_roformer_fused_training_backend(model, "hip", extension=ext, rms_norm_mode="fast")
+    assert transformer.apply_rotary_emb_fast is not originals[0]
+    assert bands.grouped_linear is not originals[2]
+    fr.restore_stock_implementations(model)
+    now = (transformer.apply_rotary_emb_fast, transformer.RMSNorm.forward, bands.grouped_linear,
+           bands.MaskEstimator._forward_layer_grouped_mlp, bands.MaskEstimator._get_layer_group_params,
+           bands.BandSplit._get_group_params, common.RoformerRuntimeMixin._estimate_masks)
+    assert all(a is b for a, b in zip(originals, now))
+    assert "_forward_grouped" not in model.band_split.__dict__
+    assert not getattr(model.band_split, "_pymsst_fused_band_split", False)
+
+
+def test_layout_helpers_slice_contiguous_band_indices():
+    x = torch.arange(2 * 4 * 3, dtype=torch.float32).reshape(2, 4, 3)
+    calls = []
+
+    def index_tensor(indices, device):
+        calls.append(indices)
+        return torch.as_tensor(indices, device=device)
+
+    assert fr._contiguous_index_range((1, 2)) == (1, 3)
+    sel = fr._select_band_group(x, (1, 2), x.device, index_tensor)
+    assert not calls and torch.equal(sel, x[..., 1:3, :])
+    dst = torch.zeros_like(x)
+    fr._copy_band_group(dst, (1, 2), sel, x.device, index_tensor)
+    assert not calls and torch.equal(dst[..., 1:3, :], sel)
+
+
+def test_layout_helpers_keep_index_select_for_noncontiguous_indices():
+    x = torch.arange(2 * 4 * 3, dtype=torch.float32).reshape(2, 4, 3)
+    calls = []
+
+    def index_tensor(indices, device):
+        calls.append(indices)
+        return torch.as_tensor(indices, device=device)
+
+    assert fr._contiguous_index_range((0, 2)) is None
+    assert fr._contiguous_index_range(()) is None
+    sel = fr._select_band_group(x, (0, 2), x.device, index_tensor)
+    assert len(calls) == 1 and torch.equal(sel, x.index_select(-2, torch.tensor((0, 2))))
+    dst = torch.zeros_like(x)
+    fr._copy_band_group(dst, (0, 2), sel, x.device, index_tensor)
+    assert torch.equal(dst[..., 0, :], x[..., 0, :]) and torch.equal(dst[..., 2, :], x[..., 2, :])
+
+
+@pytest.mark.parametrize("mask_depth", [2, 3])
+def test_layout_reduce_copy_matches_original_mask_mlp(monkeypatch, mask_depth):
+    monkeypatch.setenv(fr.EXPERIMENTAL_LAYOUT_REDUCE_COPY_ENV, "1")
+    model = _small_model(mask_depth)
+    estimator = model.mask_estimators[0]
+    x = torch.randn(2, len(estimator.dim_inputs), 16)
+    reference = bands.MaskEstimator._forward_layer_grouped_mlp(estimator, x)
+    status = fr.apply_roformer_fused_training_backend(model, "cuda_ext", extension=object())
+    candidate = estimator._forward_layer_grouped_mlp(x)
+    assert status.patched_layout_reduce_copy is True
+    assert reference is not None and candidate is not None
+    assert torch.equal(candidate, reference)
+
+
+def test_train_param_pack_autograd_matches_stack_to(monkeypatch):
+    tensors = [torch.randn(2, 3, requires_grad=True) for _ in range(3)]
+    ref_tensors = [t.detach().clone().requires_grad_() for t in tensors]
+    grad = torch.randn(3, 2, 3, dtype=torch.float16)
+    monkeypatch.setenv(fr.EXPERIMENTAL_TRAIN_PARAM_PACK_AUTOGRAD_ENV, "1")
+    packed = fr._stack_converted_tensors(tensors, torch.device("cpu"), torch.float16)
+    reference = torch.stack([t.to(dtype=torch.float16) for t in ref_tensors], dim=0)
+    packed.backward(grad)
+    reference.backward(grad)
+    assert torch.equal(packed, reference)
+    for t, r in zip(tensors, ref_tensors):
+        assert torch.equal(t.grad, r.grad)
+
+
+def _reference_grouped_linear(x, weight, bias):
+    """bmm / baddbmm per group (tests/test_training_smoke.py:28-37 semantics)."""
+    g, _, i = weight.shape
+    lead = x.shape[:-2]
+    x3 = x.reshape(-1, g, i).transpose(0, 1)
+    wt = weight.transpose(1, 2).contiguous()
+    out = torch.bmm(x3, wt) if bias is None else torch.baddbmm(bias.unsqueeze(1).expand(-1, x3.shape[1], -1), x3, wt)
+    return out.transpose(0, 1).reshape(*lead, g, -1)
+
+
+def test_mask_final_grouped_linear_glu_matches_reference():
+    torch.manual_seed(3)
+    x = torch.randn(2, 5, 3, 4, requires_grad=True)
+    weight = torch.randn(3, 6, 4, requires_grad=True)
+    bias = torch.randn(3, 6, requires_grad=True)
+    rx, rw, rb = (t.detach().clone().requires_grad_() for t in (x, weight, bias))
+    grad = torch.randn(2, 5, 3, 3)
+    out = fr._MaskFinalGroupedLinearGLU.apply(x, weight, bias)
+    ref = torch.nn.functional.glu(_reference_grouped_linear(rx, rw, rb), dim=-1)
+    out.backward(grad)
+    ref.backward(grad)
+    assert torch.allclose(out, ref)
+    for a, b in ((x, rx), (weight, rw), (bias, rb)):
+        assert torch.allclose(a.grad, b.grad, atol=1e-6, rtol=1e-6)
+
+
+def test_layout_param_reference_caches_are_stable():
+    model = _small_model()
+    estimator = model.mask_estimators[0]
+    fr.apply_roformer_fused_training_backend(model, "cuda_ext", extension=object())
+    b1 = fr._band_split_group_param_refs(model.band_split, 0, 2)
+    b2 = fr._band_split_group_param_refs(model.band_split, 0, 2)
+    m1 = fr._mask_layer_param_refs(estimator, 0, (0, 1))
+    m2 = fr._mask_layer_param_refs(estimator, 0, (0, 1))
+    p1 = fr._packed_mask_layer_param_refs(estimator, (estimator,), 0, (0, 1))
+    p2 = fr._packed_mask_layer_param_refs(estimator, (estimator,), 0, (0, 1))
+    assert b1 is b2 and m1 is m2 and p1 is p2
+    assert len(b1[0]) == 2 and len(m1[0]) == 2 and len(p1[0]) == 2
+
+
+def test_cpu_inputs_take_the_stock_path_after_patching(monkeypatch):
+    """Patched functions keep the stock behaviour for inputs the kernels do not take (CPU
+    tensors): a patched CPU model computes exactly what the unpatched one does."""
+    for key, value in fr.RUNTIME_PRESETS["hip_full"].items():
+        monkeypatch.setenv(key, value)
+    ext = type("Ext", (), {n: object() for n in ("rotary_forward", "rotary_backward", "rms_norm_forward",
+                                                  "rms_norm_backward", "band_split_ragged_forward",
+                                                  "band_split_ragged_backward",
+                                                  "mask_estimator_final_direct_forward",
+                                                  "mask_estimator_final_direct_backward")})()
+    model = _small_model()
+    model.train()
+    mixture = torch.randn(1, 2, 2048) * 0.1
+    target = torch.randn(1, 1, 2, 2048) * 0.1
+    monkeypatch.setenv(fr.CORE_GROUPED_TRAIN_ENV, "1")
+    ref = model(mixture, target)
+    fr.apply_roformer_fused_training_backend(model, "hip", extension=ext, rms_norm_mode="fast")
+    got = model(mixture, target)
+    assert torch.equal(got, ref)
