@@ -30,6 +30,8 @@ extern "C" {
 #endif
 
 enum { PMSST_F32 = 0, PMSST_F16 = 1, PMSST_BF16 = 2 };
+/* Activation codes (mask-MLP hidden layer: Linear -> tanh, fr.py:340,538). */
+enum { PMSST_ACT_NONE = 0, PMSST_ACT_TANH = 1 };
 enum {
   PMSST_OK = 0,
   PMSST_EINVAL = -1,     /* bad shape, size, pointer or alignment */
@@ -87,20 +89,24 @@ int pmsst_rms_norm_backward_from_input(const void* grad_out, const void* x, cons
                                        size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ rotary
- * t[batch, seq, heads, dim] (bnhd); cos/sin[seq, dim/2] addressed as
+ * t[batch, seq, heads, dim] (bnhd shape); cos/sin[seq, dim/2] addressed as
  * cos[n * cs_stride_seq + p * cs_stride_pair] (the reference's [1,N,1,D/2]
  * table; strides let the caller pass the cos[..., ::2] view without a copy).
  * Pair p = (t[2p], t[2p+1]) is rotated by angle (n, p).
+ * *_strides: host int64[3] element strides of the batch, seq and head axes of
+ * that tensor (its last axis is contiguous), or NULL for the dense bnhd layout.
+ * They let q/k be read straight from a fused qkv buffer and written in the
+ * [B, H, N, D] layout attention consumes (the reference copies with .contiguous()).
  */
 
 /* fused_band_split.cpp:390-410 rotary_forward (.cu:1076-1101,1130-1168). */
-int pmsst_rotary_forward(const void* t, const void* cos, const void* sin, void* out, int64_t batch, int64_t seq,
-                         int64_t heads, int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype,
-                         void* stream);
+int pmsst_rotary_forward(const void* t, const int64_t* t_strides, const void* cos, const void* sin, void* out,
+                         const int64_t* out_strides, int64_t batch, int64_t seq, int64_t heads, int64_t dim,
+                         int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype, void* stream);
 /* fused_band_split.cpp:412-432 rotary_backward (.cu:1103-1128,1170-1208): transpose rotation. */
-int pmsst_rotary_backward(const void* grad_out, const void* cos, const void* sin, void* grad_t, int64_t batch,
-                          int64_t seq, int64_t heads, int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair,
-                          int dtype, void* stream);
+int pmsst_rotary_backward(const void* grad_out, const int64_t* grad_out_strides, const void* cos, const void* sin,
+                          void* grad_t, const int64_t* grad_t_strides, int64_t batch, int64_t seq, int64_t heads,
+                          int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype, void* stream);
 
 /* Fused q/k RMSNorm over the head dim + rotary + cast (no reference counterpart; composition of
  * .cu:1399-1438 and .cu:1076-1101 with no intermediate round trip).  x/out/cos/sin in `dtype`,
@@ -151,14 +157,26 @@ int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, in
 
 /* ------------------------------------------------------------------ grouped linear
  * fused_band_split.cpp:365-388 grouped_linear_forward (.cu:1005-1074):
- * out[m, g, :] = W_g x[m, g, :] + b_g for x[rows, groups, in_features] with row pitch
+ * out[m, g, :] = act(W_g x[m, g, :] + b_g) for x[rows, groups, in_features] with row pitch
  * x_row_stride (group g at column g * in_features), weight[groups, O, in_features],
  * bias[groups, O] or NULL, out[rows, groups, O].  group_offsets is the device copy of
- * the groups+1 prefix sums g * in_features.  Any O >= 1.
+ * the groups+1 prefix sums g * in_features.  Any O >= 1.  `activation` PMSST_ACT_TANH
+ * fuses the mask-MLP hidden tanh (bands.inference_tanh, fr.py:340) into the epilogue;
+ * PMSST_ACT_NONE is the reference op.
  */
 int pmsst_grouped_linear_forward(const void* x, int64_t x_row_stride, const void* weight, const void* bias,
                                  const int64_t* group_offsets, int64_t groups, int64_t in_features, int64_t rows,
-                                 int64_t out_features, void* out, int dtype, void* stream);
+                                 int64_t out_features, void* out, int activation, int dtype, void* stream);
+/* Workspace bytes of the grouped-linear backward (bias-gradient partials). */
+size_t pmsst_grouped_linear_backward_workspace_size(int64_t rows, int64_t groups, int64_t out_features);
+/* Backward of grouped_linear (the reference computes it with batched GEMMs in _FusedGroupedLinear,
+ * fr.py:1042-1048): grad_out[rows, groups, O] (the gradient of the pre-activation output),
+ * x[rows, groups * in_features] dense -> grad_x[rows, groups * in_features],
+ * grad_weight[groups, O, in_features], grad_bias[groups, O] or NULL. */
+int pmsst_grouped_linear_backward(const void* grad_out, const void* x, const void* weight,
+                                  const int64_t* group_offsets, int64_t groups, int64_t in_features, int64_t rows,
+                                  int64_t out_features, void* grad_x, void* grad_weight, void* grad_bias, int dtype,
+                                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ mask estimator final layer
  * Per-band Linear hidden -> 2*I_b, bias, GLU.  x[rows, NB, hidden]; weight = band-major
@@ -177,12 +195,15 @@ int pmsst_mask_estimator_final_forward(const void* x, const void* weight, const 
 size_t pmsst_mask_estimator_final_backward_workspace_size(int64_t rows, int64_t total, int dtype);
 /* fused_band_split.cpp:624-658 mask_estimator_final_backward and :695-729
  * mask_estimator_final_direct_backward (.cu:2312-2367, 2585-2851): grad_out[rows, F] ->
- * grad_x[rows, NB, hidden], grad_bias[2F], grad_weight (packed like weight). */
+ * grad_x[rows, NB, hidden], grad_bias[2F], grad_weight (packed like weight).
+ * input_activation PMSST_ACT_TANH: x is the tanh output of the mask-MLP hidden layer and
+ * grad_x receives the gradient of its pre-activation, (dpre W) * (1 - x^2);
+ * PMSST_ACT_NONE is the reference op. */
 int pmsst_mask_estimator_final_backward(const void* grad_out, const void* x, const void* pre, const void* weight,
                                         const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
                                         int64_t rows, int64_t hidden, void* grad_x, void* grad_bias,
-                                        void* grad_weight, int dtype, void* workspace, size_t workspace_bytes,
-                                        void* stream);
+                                        void* grad_weight, int input_activation, int dtype, void* workspace,
+                                        size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

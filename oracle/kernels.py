@@ -310,24 +310,37 @@ def band_split_ragged_backward_lean(grad_out, x, inv_norm, gammas, weights, dim_
 # --------------------------------------------------------------------------- grouped linear
 
 
-def grouped_linear_forward(x, weight, bias, dt: str, acc=np.float64):
-    """``out[m,g,o] = bias[g,o] + sum_i x[m,g,i] W[g,o,i]`` (.cu:1005-1030; bmm form tts.py:28-37)."""
-    out = np.einsum("mgi,goi->mgo", _f(x, acc), _f(weight, acc))
+def grouped_linear_forward(x, weight, bias, dt: str, acc=np.float64, act: str | None = None):
+    """``out[m,g,o] = bias[g,o] + sum_i x[m,g,i] W[g,o,i]`` (.cu:1005-1030; bmm form tts.py:28-37).
+
+    ``act="tanh"`` applies the mask-MLP hidden activation (``inference_tanh``, fr.py:340)
+    before the single rounding to ``dt``."""
+    out = np.matmul(_f(x, acc).transpose(1, 0, 2), _f(weight, acc).transpose(0, 2, 1)).transpose(1, 0, 2)
     if bias is not None:
         out = out + _f(bias, acc)[None]
+    if act == "tanh":
+        out = np.tanh(out)
+    elif act is not None:
+        raise ValueError(act)
     return round_to(out, dt)
 
 
 def grouped_linear_backward(grad_out, x, weight, has_bias: bool, dt: str, acc=np.float64):
     """Backward of grouped linear (fr.py:1042-1048): ``dx = dy W``, ``dW = dy^T x``, ``db = sum_m dy``."""
     dy = _f(grad_out, acc)
-    dx = np.einsum("mgo,goi->mgi", dy, _f(weight, acc))
-    dW = np.einsum("mgo,mgi->goi", dy, _f(x, acc))
+    dyt = dy.transpose(1, 0, 2)  # [G, M, O]
+    dx = np.matmul(dyt, _f(weight, acc)).transpose(1, 0, 2)
+    dW = np.matmul(dyt.transpose(0, 2, 1), _f(x, acc).transpose(1, 0, 2))
     db = dy.sum(axis=0) if has_bias else None
     return round_to(dx, dt), round_to(dW, dt), (round_to(db, dt) if db is not None else None)
 
 
 # --------------------------------------------------------------------------- mask estimator
+
+
+def _gmm(a, b):
+    """``out[m,g,o] = sum_i a[m,g,i] b[g,o,i]`` as one batched matmul over g."""
+    return np.matmul(a.transpose(1, 0, 2), b.transpose(0, 2, 1)).transpose(1, 0, 2)
 
 
 def sigmoid(z):
@@ -355,11 +368,14 @@ def mask_estimator_final_forward(x, weights, bias, dim_inputs, dt: str, acc=np.f
     return round_to(np.concatenate(outs, axis=1), dt), round_to(np.concatenate(pres, axis=1), dt)
 
 
-def mask_estimator_final_backward(grad_out, x, pre, weights, dim_inputs, dt: str, acc=np.float64):
+def mask_estimator_final_backward(grad_out, x, pre, weights, dim_inputs, dt: str, acc=np.float64,
+                                  input_act: str | None = None):
     """Backward of :func:`mask_estimator_final_forward` (.cu:2312-2367, .cu:2585-2704).
 
     From the saved ``pre``: ``dL = g*s``, ``dG = g*L*s*(1-s)`` with ``s = sigmoid(G)``;
     ``dbias = sum_m dpre``, ``dx_b = dpre_b W_b``, ``dW_b = dpre_b^T x_b``.
+    ``input_act="tanh"``: ``x`` is a tanh output and the first result is the gradient of its
+    pre-activation, ``dx * (1 - x^2)`` (chain rule through ``inference_tanh``).
     Returns ``(dx[M,NB,H], dbias[2F], [dW_b])``.
     """
     g = _f(grad_out, acc)
@@ -378,6 +394,10 @@ def mask_estimator_final_backward(grad_out, x, pre, weights, dim_inputs, dt: str
         dbias.append(dpre.sum(axis=0))
         dx[:, b, :] = dpre @ _f(weights[b], acc)
         dws.append(round_to(dpre.T @ x[:, b, :], dt))
+    if input_act == "tanh":
+        dx = dx * (1.0 - x * x)
+    elif input_act is not None:
+        raise ValueError(input_act)
     return round_to(dx, dt), round_to(np.concatenate(dbias), dt), dws
 
 
@@ -389,7 +409,7 @@ def mask_mlp_forward(x, w1, b1, weights2, bias2, dim_inputs, dt: str, acc=np.flo
     (fr.py:340,538); ``w1[NB,Hd,dim]``, ``b1[NB,Hd]``.  ``h`` is kept unrounded
     (it never leaves the fused kernel).  Returns ``out[M,F]``.
     """
-    h = np.tanh(np.einsum("mgi,goi->mgo", _f(x, acc), _f(w1, acc)) + _f(b1, acc)[None])
+    h = np.tanh(_gmm(_f(x, acc), _f(w1, acc)) + _f(b1, acc)[None])
     out, _ = mask_estimator_final_forward(h, weights2, bias2, dim_inputs, dt, acc)
     return out
 
@@ -401,7 +421,7 @@ def mask_mlp_backward(grad_out, x, w1, b1, weights2, bias2, dim_inputs, dt: str,
     """
     x = _f(x, acc)
     w1 = _f(w1, acc)
-    h = np.tanh(np.einsum("mgi,goi->mgo", x, w1) + _f(b1, acc)[None])
+    h = np.tanh(_gmm(x, w1) + _f(b1, acc)[None])
     pre = []
     off = _offsets(dim_inputs)
     b2 = _f(bias2, acc)
@@ -411,8 +431,9 @@ def mask_mlp_backward(grad_out, x, w1, b1, weights2, bias2, dim_inputs, dt: str,
     # unrounded backward through the final layer
     dh, dbias2, dws2 = mask_estimator_final_backward(grad_out, h, pre, weights2, dim_inputs, "f64", acc)
     dz = dh * (1.0 - h * h)
-    dx = np.einsum("mgo,goi->mgi", dz, w1)
-    dW1 = np.einsum("mgo,mgi->goi", dz, x)
+    dzt = dz.transpose(1, 0, 2)  # [G, M, Hd]
+    dx = np.matmul(dzt, w1).transpose(1, 0, 2)
+    dW1 = np.matmul(dzt.transpose(0, 2, 1), x.transpose(1, 0, 2))
     db1 = dz.sum(axis=0)
     return (
         round_to(dx, dt),

@@ -98,7 +98,7 @@ struct XGammaLoader {
   }
 };
 
-template <typename T, int TO, bool WRITE_NORMED, bool NORM>
+template <typename T, int TO, bool WRITE_NORMED, bool NORM, int ACT>
 __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restrict__ x, const T* __restrict__ gamma,
                                                               const T* __restrict__ weight,
                                                               const T* __restrict__ bias, T* __restrict__ out,
@@ -161,7 +161,10 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
       const float s = sscale[m];
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = acc[t][j][r] * s + bv[r];
+      for (int r = 0; r < 4; ++r) {
+        v[r] = acc[t][j][r] * s + bv[r];
+        if (ACT == PMSST_ACT_TANH) v[r] = tanhf(v[r]);
+      }
       T* dst = out + ((m0 + m) * a.NB + band) * O + o;
       if (a.ovec4) {
         store_pack<T, 4>(dst, v);
@@ -195,7 +198,9 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
 
 // ------------------------------------------------------------------ backward: dx + dgamma partials
 
-template <typename T, bool FROM_X>
+// NORM = false: plain grouped linear, dx = dy W_b in one pass (nsrc, inv_norm, gamma and
+// dg_partial unused).
+template <typename T, bool FROM_X, bool NORM>
 __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __restrict__ dy,
                                                                  const T* __restrict__ nsrc,
                                                                  const float* __restrict__ inv_norm,
@@ -219,11 +224,13 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
   const T* dyb = dy + (m0 * a.NB + band) * O;
   const float root = sqrtf(static_cast<float>(I));
 
-  if (tid < kBM) sinv[tid] = tid < rows_valid ? inv_norm[(m0 + tid) * a.NB + band] : 0.f;
-  __syncthreads();
+  if (NORM) {
+    if (tid < kBM) sinv[tid] = tid < rows_valid ? inv_norm[(m0 + tid) * a.NB + band] : 0.f;
+    __syncthreads();
+  }
 
   float dotp[4] = {0.f, 0.f, 0.f, 0.f};  // per m-tile j: m = 16 j + (lane & 15)
-  for (int pass = 0; pass < 2; ++pass) {
+  for (int pass = 0; pass < (NORM ? 2 : 1); ++pass) {
     if (pass == 1) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -247,6 +254,21 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
 
       // lane holds gs[m = 16 j + (lane & 15)][i = i0 + 16 wave + 4 (lane >> 4) + r]
       const int il = i0 + wave * 16 + 4 * (lane >> 4);
+      if (!NORM) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = j * 16 + (lane & 15);
+          if (m >= rows_valid || il >= I) continue;
+          float o[4] = {acc[0][j][0], acc[0][j][1], acc[0][j][2], acc[0][j][3]};
+          T* dp = dx + (m0 + m) * a.F + off + il;
+          if (a.vec4) {
+            store_pack<T, 4>(dp, o);
+          } else {
+            for (int r = 0; r < 4 && il + r < I; ++r) dp[r] = from_f32<T>(o[r]);
+          }
+        }
+        continue;
+      }
       float g[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) g[r] = il + r < I ? to_f32(gamma[off + il + r]) : 0.f;
@@ -307,7 +329,8 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
 constexpr int kDwBI = 64;
 constexpr int kDwBO = 64;
 
-template <typename T, bool FROM_X>
+// NORM = false: plain grouped linear, dW_b^T = x_b^T dy_b (no gamma / inv_norm scaling).
+template <typename T, bool FROM_X, bool NORM>
 __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __restrict__ dy,
                                                                  const T* __restrict__ nsrc,
                                                                  const float* __restrict__ inv_norm,
@@ -327,8 +350,8 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
   // A[i][m] = n[m][off + i0 + i] * gamma (MN-contiguous in i; n = x * inv * sqrt(I) when FROM_X)
   // B[o][m] = dy[m][band][o0 + o]       (MN-contiguous in o)
   MNLoader<T, kDwBI> la{nsrc + off + i0, a.F, I - i0, static_cast<int>(a.M), a.vec4};
-  la.cs = gamma + off + i0;
-  if (FROM_X) {
+  if (NORM) la.cs = gamma + off + i0;
+  if (NORM && FROM_X) {
     la.rs = inv_norm + band;
     la.rs_stride = a.NB;
     la.rs_mul = sqrtf(static_cast<float>(I));
@@ -403,8 +426,9 @@ bool aligned_to(const void* p, size_t bytes) { return p == nullptr || reinterpre
 template <typename T>
 int launch_fwd(const void* x, int64_t x_stride, const void* gamma, const void* weight, const void* bias,
                const int64_t* offsets, const HostBands& hb, int64_t M, int64_t O, void* out, void* normed,
-               float* inv_norm, bool norm, hipStream_t stream) {
+               float* inv_norm, bool norm, int act, hipStream_t stream) {
   const char* op = norm ? "band_split_ragged_forward" : "grouped_linear_forward";
+  PMSST_REQUIRE(act == PMSST_ACT_NONE || (act == PMSST_ACT_TANH && !norm), "%s: bad activation %d", op, act);
   PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
   PMSST_REQUIRE(O >= 1 && (O <= 512 || !norm) && O < (1 << 20), "%s: bad out_features %lld", op, (long long)O);
   if (M == 0) return PMSST_OK;
@@ -425,15 +449,18 @@ int launch_fwd(const void* x, int64_t x_stride, const void* gamma, const void* w
   T* pn = static_cast<T*>(normed);
 #define PMSST_BSF(TO)                                                                                              \
   do {                                                                                                             \
-    if (!norm)                                                                                                     \
-      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, false>), grid, dim3(kGemmThreads), 0, stream, px, pg, pw,    \
-                         pb, po, pn, inv_norm, a);                                                                 \
+    if (!norm && act == PMSST_ACT_TANH)                                                                            \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, false, PMSST_ACT_TANH>), grid, dim3(kGemmThreads), 0, stream, \
+                         px, pg, pw, pb, po, pn, inv_norm, a);                                                     \
+    else if (!norm)                                                                                                \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, false, PMSST_ACT_NONE>), grid, dim3(kGemmThreads), 0, stream, \
+                         px, pg, pw, pb, po, pn, inv_norm, a);                                                     \
     else if (pn != nullptr)                                                                                        \
-      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, true, true>), grid, dim3(kGemmThreads), 0, stream, px, pg, pw, pb,  \
-                         po, pn, inv_norm, a);                                                                     \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, true, true, PMSST_ACT_NONE>), grid, dim3(kGemmThreads), 0, stream,  \
+                         px, pg, pw, pb, po, pn, inv_norm, a);                                                     \
     else                                                                                                           \
-      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, true>), grid, dim3(kGemmThreads), 0, stream, px, pg, pw, pb, \
-                         po, pn, inv_norm, a);                                                                     \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, true, PMSST_ACT_NONE>), grid, dim3(kGemmThreads), 0, stream, \
+                         px, pg, pw, pb, po, pn, inv_norm, a);                                                     \
   } while (0)
   switch (tile_capacity(O)) {
     case 1: PMSST_BSF(1); break;
@@ -480,11 +507,11 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   if (M > 0) {
     const dim3 grid(static_cast<unsigned>(m_tiles), static_cast<unsigned>(hb.NB));
     if (from_x)
-      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, pg, pw,
-                         static_cast<T*>(dx), partial, a);
+      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, true, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
+                         pg, pw, static_cast<T*>(dx), partial, a);
     else
-      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, pg,
-                         pw, static_cast<T*>(dx), partial, a);
+      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
+                         pg, pw, static_cast<T*>(dx), partial, a);
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
@@ -492,11 +519,11 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
     const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
     const dim3 grid(static_cast<unsigned>((O + kDwBO - 1) / kDwBO), static_cast<unsigned>(hb.NB * max_itiles));
     if (from_x)
-      hipLaunchKernelGGL((bs_bwd_dw_kernel<T, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, pg,
-                         static_cast<T*>(dw), max_itiles, a);
+      hipLaunchKernelGGL((bs_bwd_dw_kernel<T, true, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
+                         pg, static_cast<T*>(dw), max_itiles, a);
     else
-      hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, pg,
-                         static_cast<T*>(dw), max_itiles, a);
+      hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
+                         pg, static_cast<T*>(dw), max_itiles, a);
     int rc = check_launch("bs_bwd_dw_kernel");
     if (rc != PMSST_OK) return rc;
   }
@@ -504,6 +531,46 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   if (rc != PMSST_OK || db == nullptr) return rc;
   return launch_colsum_rows(dy, dtype_code<T>(), M, static_cast<int64_t>(hb.NB) * O, db_partial, db, dtype_code<T>(),
                             stream);
+}
+
+// Grouped linear backward: the norm-free dx / dW kernels plus the bias column sums.
+template <typename T>
+int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const int64_t* offsets,
+                       const HostBands& hb, int64_t M, int64_t O, void* dx, void* dw, void* db, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
+  const char* op = "grouped_linear_backward";
+  PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
+  PMSST_REQUIRE(O >= 1 && O < (1 << 20), "%s: bad out_features %lld", op, (long long)O);
+  PMSST_REQUIRE(weight && offsets && dw && (M == 0 || (dy && x && dx)), "%s: null pointer", op);
+  const size_t need = colsum_rows_workspace(M, static_cast<int64_t>(hb.NB) * O);
+  if (db != nullptr && (workspace == nullptr || workspace_bytes < need)) {
+    return fail(PMSST_EWORKSPACE, "%s: workspace of %zu bytes needed", op, need);
+  }
+  BandArgs a{offsets, M, hb.NB, hb.F, hb.F, static_cast<int>(O), false, false};
+  a.vec4 = hb.vec4 && aligned_to(x, 4 * sizeof(T)) && aligned_to(dx, 4 * sizeof(T)) &&
+           aligned_to(weight, 4 * sizeof(T)) && aligned_to(dw, 4 * sizeof(T));
+  a.ovec4 = O % 4 == 0 && aligned_to(dy, 4 * sizeof(T));
+  const T* pdy = static_cast<const T*>(dy);
+  const T* px = static_cast<const T*>(x);
+  const T* pw = static_cast<const T*>(weight);
+  if (M > 0) {
+    const dim3 grid(static_cast<unsigned>((M + kBM - 1) / kBM), static_cast<unsigned>(hb.NB));
+    hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px, nullptr,
+                       nullptr, pw, static_cast<T*>(dx), nullptr, a);
+    int rc = check_launch("bs_bwd_dx_kernel");
+    if (rc != PMSST_OK) return rc;
+  }
+  {
+    const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
+    const dim3 grid(static_cast<unsigned>((O + kDwBO - 1) / kDwBO), static_cast<unsigned>(hb.NB * max_itiles));
+    hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px, nullptr,
+                       nullptr, static_cast<T*>(dw), max_itiles, a);
+    int rc = check_launch("bs_bwd_dw_kernel");
+    if (rc != PMSST_OK) return rc;
+  }
+  if (db == nullptr) return PMSST_OK;
+  return launch_colsum_rows(dy, dtype_code<T>(), M, static_cast<int64_t>(hb.NB) * O, static_cast<float*>(workspace),
+                            db, dtype_code<T>(), stream);
 }
 
 template <typename F>
@@ -533,13 +600,13 @@ int pmsst_band_split_ragged_forward(const void* x, int64_t x_row_stride, const v
   return with_dtype(dtype, "band_split_ragged_forward", [&](auto tag) {
     using T = decltype(tag);
     return launch_fwd<T>(x, x_row_stride, gamma, weight, bias, dim_offsets, hb, rows, out_features, out, normed,
-                         inv_norm, true, static_cast<hipStream_t>(stream));
+                         inv_norm, true, PMSST_ACT_NONE, static_cast<hipStream_t>(stream));
   });
 }
 
 int pmsst_grouped_linear_forward(const void* x, int64_t x_row_stride, const void* weight, const void* bias,
                                  const int64_t* group_offsets, int64_t groups, int64_t in_features, int64_t rows,
-                                 int64_t out_features, void* out, int dtype, void* stream) {
+                                 int64_t out_features, void* out, int activation, int dtype, void* stream) {
   PMSST_REQUIRE(groups > 0 && groups < (1 << 16) && in_features > 0, "grouped_linear_forward: bad shape");
   std::vector<int64_t> dims(static_cast<size_t>(groups), in_features);
   HostBands hb;
@@ -548,7 +615,28 @@ int pmsst_grouped_linear_forward(const void* x, int64_t x_row_stride, const void
   return with_dtype(dtype, "grouped_linear_forward", [&](auto tag) {
     using T = decltype(tag);
     return launch_fwd<T>(x, x_row_stride, nullptr, weight, bias, group_offsets, hb, rows, out_features, out, nullptr,
-                         nullptr, false, static_cast<hipStream_t>(stream));
+                         nullptr, false, activation, static_cast<hipStream_t>(stream));
+  });
+}
+
+size_t pmsst_grouped_linear_backward_workspace_size(int64_t rows, int64_t groups, int64_t out_features) {
+  if (rows < 0 || groups <= 0 || out_features <= 0) return 0;
+  return colsum_rows_workspace(rows, groups * out_features);
+}
+
+int pmsst_grouped_linear_backward(const void* grad_out, const void* x, const void* weight,
+                                  const int64_t* group_offsets, int64_t groups, int64_t in_features, int64_t rows,
+                                  int64_t out_features, void* grad_x, void* grad_weight, void* grad_bias, int dtype,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  PMSST_REQUIRE(groups > 0 && groups < (1 << 16) && in_features > 0, "grouped_linear_backward: bad shape");
+  std::vector<int64_t> dims(static_cast<size_t>(groups), in_features);
+  HostBands hb;
+  int rc = check_bands("grouped_linear_backward", dims.data(), groups, &hb);
+  if (rc != PMSST_OK) return rc;
+  return with_dtype(dtype, "grouped_linear_backward", [&](auto tag) {
+    using T = decltype(tag);
+    return launch_grouped_bwd<T>(grad_out, x, weight, group_offsets, hb, rows, out_features, grad_x, grad_weight,
+                                 grad_bias, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
   });
 }
 

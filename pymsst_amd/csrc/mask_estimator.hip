@@ -18,7 +18,8 @@
 //   1. me_dpre_kernel writes dpre = (g * s, g * L * s * (1 - s)), s = sigmoid(G),
 //      to a [M, 2F] workspace (one pass over pre and grad_out);
 //   2. dbias = column sums of dpre (colsum_rows_kernel + col_sum_kernel);
-//   3. dx^T[h][m] = W_b^T dpre_b^T  (K = 2*I_b), tiles 128 h x 64 m;
+//   3. dx^T[h][m] = W_b^T dpre_b^T  (K = 2*I_b), tiles 128 h x 64 m; with a tanh
+//      input (mask-MLP hidden layer) the epilogue writes dz = dx * (1 - x^2);
 //   4. dW^T[h][j] = x_b^T dpre_b    (K = M),     tiles 128 h x 64 j.
 // All reductions have a fixed order; no atomics.
 #include "common.h"
@@ -211,9 +212,12 @@ __global__ __launch_bounds__(256) void me_dpre_kernel(const T* __restrict__ gout
 constexpr int kDxBH = 128;
 constexpr int kDxBM = 64;
 
-template <typename T>
+// TANH_IN: the layer input x is tanh(z) of the previous layer, and the kernel writes
+// dz = (dpre W_b) * (1 - x^2) instead of dx (the hidden activation's backward, fused).
+template <typename T, bool TANH_IN>
 __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __restrict__ dpre,
-                                                                 const T* __restrict__ weight, T* __restrict__ dx,
+                                                                 const T* __restrict__ weight,
+                                                                 const T* __restrict__ x, T* __restrict__ dx,
                                                                  MaskArgs a) {
   __shared__ T lds[gemm_lds_elems<T, kDxBH, kDxBM>()];
   using S = TileShape<kDxBH, kDxBM, 2, 2>;
@@ -246,8 +250,19 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __rest
     for (int j = 0; j < S::kTC; ++j) {
       const int m = mc + j * 16 + (lane & 15);
       if (m >= rows_valid) continue;
-      T* dst = dx + ((m0 + m) * a.NB + band) * H + h;
+      const int64_t idx = ((m0 + m) * a.NB + band) * H + h;
+      T* dst = dx + idx;
       float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      if (TANH_IN) {
+        float t[4] = {0.f, 0.f, 0.f, 0.f};
+        if (a.vec4) {
+          load_pack<T, 4>(x + idx, t);
+        } else {
+          for (int r = 0; r < 4 && h + r < H; ++r) t[r] = to_f32(x[idx + r]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] *= 1.0f - t[r] * t[r];
+      }
       if (a.vec4) {
         store_pack<T, 4>(dst, v);
       } else {
@@ -361,10 +376,12 @@ size_t me_bwd_workspace(int64_t M, int F, size_t elem) {
 
 template <typename T>
 int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* weight, const int64_t* offsets,
-                  const HostMask& hm, int64_t M, int64_t H, void* dx, void* dbias, void* dw, void* workspace,
-                  size_t workspace_bytes, hipStream_t stream) {
+                  const HostMask& hm, int64_t M, int64_t H, void* dx, void* dbias, void* dw, int input_act,
+                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const char* op = "mask_estimator_final_backward";
   PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
+  PMSST_REQUIRE(input_act == PMSST_ACT_NONE || input_act == PMSST_ACT_TANH, "%s: bad input_activation %d", op,
+                input_act);
   PMSST_REQUIRE(weight && offsets && dbias && dw && (M == 0 || (gout && x && pre && dx)), "%s: null pointer", op);
   const size_t need = me_bwd_workspace(M, hm.F, sizeof(T));
   if (workspace == nullptr || workspace_bytes < need) {
@@ -385,8 +402,12 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
     if (rc != PMSST_OK) return rc;
     const dim3 g2(static_cast<unsigned>((M + kDxBM - 1) / kDxBM), static_cast<unsigned>(hm.NB),
                   static_cast<unsigned>((H + kDxBH - 1) / kDxBH));
-    hipLaunchKernelGGL((me_bwd_dx_kernel<T>), g2, dim3(kGemmThreads), 0, stream, dpre, static_cast<const T*>(weight),
-                       static_cast<T*>(dx), a);
+    if (input_act == PMSST_ACT_TANH)
+      hipLaunchKernelGGL((me_bwd_dx_kernel<T, true>), g2, dim3(kGemmThreads), 0, stream, dpre,
+                         static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), a);
+    else
+      hipLaunchKernelGGL((me_bwd_dx_kernel<T, false>), g2, dim3(kGemmThreads), 0, stream, dpre,
+                         static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), a);
     rc = check_launch("me_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
@@ -438,15 +459,15 @@ size_t pmsst_mask_estimator_final_backward_workspace_size(int64_t rows, int64_t 
 int pmsst_mask_estimator_final_backward(const void* grad_out, const void* x, const void* pre, const void* weight,
                                         const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
                                         int64_t rows, int64_t hidden, void* grad_x, void* grad_bias,
-                                        void* grad_weight, int dtype, void* workspace, size_t workspace_bytes,
-                                        void* stream) {
+                                        void* grad_weight, int input_activation, int dtype, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
   HostMask hm;
   int rc = check_mask("mask_estimator_final_backward", dim_inputs, band_count, hidden, &hm);
   if (rc != PMSST_OK) return rc;
   return with_dtype(dtype, "mask_estimator_final_backward", [&](auto tag) {
     using T = decltype(tag);
     return launch_me_bwd<T>(grad_out, x, pre, weight, dim_offsets, hm, rows, hidden, grad_x, grad_bias, grad_weight,
-                            workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                            input_activation, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
   });
 }
 

@@ -1,9 +1,11 @@
 // Rotary embedding on bnhd q/k, and the fused q/k RMSNorm + rotary + cast.
 //
 // Rotary is a pure stream: each lane moves one 16-byte pack (VEC elements,
-// VEC/2 adjacent pairs) per step.  The pack's token index and position come
-// from multiply-shift divisions; cos/sin rows (seq x dim/2, a few KB) stay in
-// L1/L2.
+// VEC/2 adjacent pairs) per step.  The pack's (batch, position, head, element)
+// come from multiply-shift divisions; cos/sin rows (seq x dim/2, a few KB) stay
+// in L1/L2.  Input and output take independent (batch, seq, head) strides, so
+// q/k are read straight out of the fused qkv projection and can be written in
+// the [B, H, N, D] layout attention consumes (no copies on either side).
 //
 // The fused kernel uses the RMSNorm row geometry: one row = one head vector
 // of `dim` elements; pairs never straddle a pack because VEC is even.
@@ -21,18 +23,27 @@ struct TableRef {
   int64_t stride_pair;
 };
 
+// Element strides of a [B, N, H, D] view whose last axis is contiguous.
+struct BnhStrides {
+  int64_t b, n, h;
+};
+
 template <typename T, int VEC, bool INVERSE>
 __global__ __launch_bounds__(kRotThreads) void rotary_kernel(const T* __restrict__ in, const T* __restrict__ cosv,
                                                              const T* __restrict__ sinv, T* __restrict__ out,
                                                              uint32_t total_packs, FastDiv packs_per_token,
-                                                             FastDiv seq, FastDiv dim, TableRef tab) {
+                                                             FastDiv seq, FastDiv dim, TableRef tab, BnhStrides si,
+                                                             BnhStrides so) {
   for (uint32_t i = blockIdx.x * kRotThreads + threadIdx.x; i < total_packs; i += gridDim.x * kRotThreads) {
     const uint32_t tok = packs_per_token.div(i);
     const uint32_t e = (i - tok * packs_per_token.d) * VEC;  // element offset inside the token
-    const uint32_t n = seq.mod(tok);
-    const uint32_t p0 = dim.mod(e) >> 1;
+    const uint32_t b = seq.div(tok);
+    const uint32_t n = tok - b * seq.d;
+    const uint32_t h = dim.div(e);
+    const uint32_t d = e - h * dim.d;
+    const uint32_t p0 = d >> 1;
     float v[VEC];
-    load_pack<T, VEC>(in + static_cast<int64_t>(i) * VEC, v);
+    load_pack<T, VEC>(in + b * si.b + n * si.n + h * si.h + d, v);
     const T* cr = cosv + n * tab.stride_seq;
     const T* sr = sinv + n * tab.stride_seq;
 #pragma unroll
@@ -48,13 +59,14 @@ __global__ __launch_bounds__(kRotThreads) void rotary_kernel(const T* __restrict
         v[2 * j + 1] = ov * c + ev * s;
       }
     }
-    store_pack<T, VEC>(out + static_cast<int64_t>(i) * VEC, v);
+    store_pack<T, VEC>(out + b * so.b + n * so.n + h * so.h + d, v);
   }
 }
 
 template <typename T>
-int launch_rotary(const void* in, const void* cosv, const void* sinv, void* out, int64_t batch, int64_t seq,
-                  int64_t heads, int64_t dim, int64_t cs_seq, int64_t cs_pair, bool inverse, hipStream_t stream) {
+int launch_rotary(const void* in, const int64_t* in_strides, const void* cosv, const void* sinv, void* out,
+                  const int64_t* out_strides, int64_t batch, int64_t seq, int64_t heads, int64_t dim, int64_t cs_seq,
+                  int64_t cs_pair, bool inverse, hipStream_t stream) {
   const char* op = inverse ? "rotary_backward" : "rotary_forward";
   PMSST_REQUIRE(batch >= 0 && seq >= 0 && heads >= 0 && dim > 0 && dim % 2 == 0,
                 "%s: bad shape [%lld, %lld, %lld, %lld]", op, (long long)batch, (long long)seq, (long long)heads,
@@ -62,10 +74,17 @@ int launch_rotary(const void* in, const void* cosv, const void* sinv, void* out,
   const int64_t total = batch * seq * heads * dim;
   if (total == 0) return PMSST_OK;
   PMSST_REQUIRE(in && cosv && sinv && out, "%s: null pointer", op);
+  const BnhStrides dense{seq * heads * dim, heads * dim, dim};
+  const BnhStrides si = in_strides ? BnhStrides{in_strides[0], in_strides[1], in_strides[2]} : dense;
+  const BnhStrides so = out_strides ? BnhStrides{out_strides[0], out_strides[1], out_strides[2]} : dense;
+  PMSST_REQUIRE(si.b >= 0 && si.n >= 0 && si.h >= 0 && so.b >= 0 && so.n >= 0 && so.h >= 0, "%s: negative stride",
+                op);
   int vec = 16 / sizeof(T);
   auto aligned = [&](int v) {
-    return dim % v == 0 && reinterpret_cast<uintptr_t>(in) % (v * sizeof(T)) == 0 &&
-           reinterpret_cast<uintptr_t>(out) % (v * sizeof(T)) == 0;
+    bool ok = dim % v == 0 && reinterpret_cast<uintptr_t>(in) % (v * sizeof(T)) == 0 &&
+              reinterpret_cast<uintptr_t>(out) % (v * sizeof(T)) == 0;
+    for (int64_t st : {si.b, si.n, si.h, so.b, so.n, so.h}) ok = ok && st % v == 0;
+    return ok;
   };
   while (vec > 2 && !aligned(vec)) vec /= 2;
   PMSST_REQUIRE(aligned(vec), "%s: tensors must be 4-byte aligned", op);
@@ -84,7 +103,7 @@ int launch_rotary(const void* in, const void* cosv, const void* sinv, void* out,
   const uint32_t np = static_cast<uint32_t>(packs);
 #define PMSST_ROT(VEC, INV)                                                                                     \
   hipLaunchKernelGGL((rotary_kernel<T, VEC, INV>), dim3(blocks), dim3(kRotThreads), 0, stream, pin, pc, ps, po, \
-                     np, ppt, fseq, fdim, tab)
+                     np, ppt, fseq, fdim, tab, si, so)
   if (inverse) {
     if (vec == 16 / (int)sizeof(T)) PMSST_ROT(16 / sizeof(T), true);
     else if (vec == 8 / (int)sizeof(T)) PMSST_ROT(8 / sizeof(T), true);
@@ -374,23 +393,23 @@ using namespace pmsst;
 
 extern "C" {
 
-int pmsst_rotary_forward(const void* t, const void* cos, const void* sin, void* out, int64_t batch, int64_t seq,
-                         int64_t heads, int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype,
-                         void* stream) {
+int pmsst_rotary_forward(const void* t, const int64_t* t_strides, const void* cos, const void* sin, void* out,
+                         const int64_t* out_strides, int64_t batch, int64_t seq, int64_t heads, int64_t dim,
+                         int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype, void* stream) {
   return with_dtype(dtype, "rotary_forward", [&](auto tag) {
     using T = decltype(tag);
-    return launch_rotary<T>(t, cos, sin, out, batch, seq, heads, dim, cs_stride_seq, cs_stride_pair, false,
-                            static_cast<hipStream_t>(stream));
+    return launch_rotary<T>(t, t_strides, cos, sin, out, out_strides, batch, seq, heads, dim, cs_stride_seq,
+                            cs_stride_pair, false, static_cast<hipStream_t>(stream));
   });
 }
 
-int pmsst_rotary_backward(const void* grad_out, const void* cos, const void* sin, void* grad_t, int64_t batch,
-                          int64_t seq, int64_t heads, int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair,
-                          int dtype, void* stream) {
+int pmsst_rotary_backward(const void* grad_out, const int64_t* grad_out_strides, const void* cos, const void* sin,
+                          void* grad_t, const int64_t* grad_t_strides, int64_t batch, int64_t seq, int64_t heads,
+                          int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype, void* stream) {
   return with_dtype(dtype, "rotary_backward", [&](auto tag) {
     using T = decltype(tag);
-    return launch_rotary<T>(grad_out, cos, sin, grad_t, batch, seq, heads, dim, cs_stride_seq, cs_stride_pair, true,
-                            static_cast<hipStream_t>(stream));
+    return launch_rotary<T>(grad_out, grad_out_strides, cos, sin, grad_t, grad_t_strides, batch, seq, heads, dim,
+                            cs_stride_seq, cs_stride_pair, true, static_cast<hipStream_t>(stream));
   });
 }
 

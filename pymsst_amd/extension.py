@@ -57,12 +57,22 @@ class _DeviceGuard:
         return False
 
 
+def _activation_code(name) -> int:
+    if name is None or name == "none":
+        return 0  # PMSST_ACT_NONE
+    if name == "tanh":
+        return 1  # PMSST_ACT_TANH
+    raise ValueError(f"unsupported activation {name!r}")
+
+
 def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
 class HipFusedExtension:
     """Duck-typed replacement for the reference's extension module (``fr.py:71`` ``extension=``)."""
+
+    rotary_out_layouts = ("bnhd", "bhnd")
 
     def __init__(self):
         self._lib = _lib.load_library()
@@ -220,26 +230,38 @@ class HipFusedExtension:
             cos, sin = cos.contiguous(), sin.contiguous()
         return cos, sin, cos.stride(1), cos.stride(3)
 
-    def _rotary(self, fn_name, t, cos, sin):
-        t = t.contiguous()
+    def _rotary(self, fn_name, t, cos, sin, out_layout="bnhd"):
+        if t.stride(3) != 1:
+            t = t.contiguous()
         cos, sin, s_seq, s_pair = self._tables(cos, sin)
-        out = torch.empty_like(t)
         b, n, h, d = t.shape
+        if out_layout == "bhnd":
+            # [B, N, H, D]-shaped view of a dense [B, H, N, D] buffer
+            out = torch.empty((b, h, n, d), dtype=t.dtype, device=t.device).transpose(1, 2)
+        elif out_layout == "bnhd":
+            out = torch.empty((b, n, h, d), dtype=t.dtype, device=t.device)
+        else:
+            raise ValueError(f"unsupported out_layout {out_layout!r}")
+        t_strides = (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+        o_strides = (ctypes.c_int64 * 3)(out.stride(0), out.stride(1), out.stride(2))
         with _DeviceGuard(t.device):
             rc = getattr(self._lib, fn_name)(
-                _ptr(t), _ptr(cos), _ptr(sin), _ptr(out), b, n, h, d, s_seq, s_pair, dtype_code(t.dtype),
-                _stream(t.device),
+                _ptr(t), t_strides, _ptr(cos), _ptr(sin), _ptr(out), o_strides, b, n, h, d, s_seq, s_pair,
+                dtype_code(t.dtype), _stream(t.device),
             )
         check(rc, fn_name)
         return out
 
-    def rotary_forward(self, t, cos, sin):
-        """``.cpp:390-410``: ``t[B,N,H,D]``, ``cos/sin[1,N,1,D/2]`` (strided views accepted)."""
+    def rotary_forward(self, t, cos, sin, out_layout="bnhd"):
+        """``.cpp:390-410``: ``t[B,N,H,D]`` (any strides with a contiguous last axis, e.g. a view
+        into a fused qkv buffer), ``cos/sin[1,N,1,D/2]`` (strided views accepted).
+        ``out_layout="bhnd"`` returns the ``[B,N,H,D]``-shaped transpose of a dense ``[B,H,N,D]``
+        buffer, the layout attention consumes."""
         self._rot_check(t, cos, sin, "t")
-        return self._rotary("pmsst_rotary_forward", t, cos, sin)
+        return self._rotary("pmsst_rotary_forward", t, cos, sin, out_layout)
 
     def rotary_backward(self, grad_out, cos, sin):
-        """``.cpp:412-432``: transpose rotation of ``grad_out``."""
+        """``.cpp:412-432``: transpose rotation of ``grad_out`` (any strides); dense bnhd result."""
         self._rot_check(grad_out, cos, sin, "grad_out")
         return self._rotary("pmsst_rotary_backward", grad_out, cos, sin)
 
@@ -519,6 +541,11 @@ class HipFusedExtension:
     def grouped_linear_forward(self, x, weight, bias=None):
         """``.cpp:365-388``: ``x[M,G,I]`` (strided view allowed), ``weight[G,O,I]``, ``bias[G,O]`` or ``None``
         -> ``out[M,G,O]``."""
+        return self.grouped_linear_forward_act(x, weight, bias, activation=None)
+
+    def grouped_linear_forward_act(self, x, weight, bias=None, activation=None):
+        """``grouped_linear_forward`` with an optional fused epilogue activation (``"tanh"``)."""
+        act = _activation_code(activation)
         _req(x.is_cuda, "x must be a CUDA tensor")
         _req(weight.is_cuda, "weight must be a CUDA tensor")
         if bias is not None:
@@ -545,10 +572,35 @@ class HipFusedExtension:
         with _DeviceGuard(x.device):
             rc = self._lib.pmsst_grouped_linear_forward(
                 _ptr(x), x.stride(0) if m > 0 else g * i, _ptr(weight), _ptr(bias), _ptr(dev_offs), g, i, m, o,
-                _ptr(out), dtype_code(x.dtype), _stream(x.device),
+                _ptr(out), act, dtype_code(x.dtype), _stream(x.device),
             )
         check(rc, "pmsst_grouped_linear_forward")
         return out
+
+    def grouped_linear_backward(self, grad_out, x, weight, has_bias=True):
+        """Backward of ``grouped_linear_forward`` (the reference's ``_FusedGroupedLinear.backward``,
+        fr.py:1042-1048): ``grad_out[M,G,O]``, ``x[M,G,I]``, ``weight[G,O,I]`` ->
+        ``[grad_x[M,G,I], grad_weight[G,O,I], grad_bias[G,O] | None]``."""
+        _req(grad_out.is_cuda and x.is_cuda and weight.is_cuda, "tensors must be CUDA tensors")
+        _req(x.dim() == 3 and weight.dim() == 3 and grad_out.dim() == 3, "x, weight, grad_out must be 3D")
+        m, g, i = x.shape
+        o = weight.size(1)
+        _req(weight.size(0) == g and weight.size(2) == i, "weight must have shape [G, O, I] matching x")
+        _req(tuple(grad_out.shape) == (m, g, o), "grad_out must have shape [M, G, O]")
+        _req(grad_out.dtype == x.dtype and weight.dtype == x.dtype, "dtypes must match x")
+        grad_out, x, weight = grad_out.contiguous(), x.contiguous(), weight.contiguous()
+        _, dev_offs, _ = self._bands((i,) * g, x.device)
+        dx = torch.empty_like(x)
+        dw = torch.empty_like(weight)
+        db = torch.empty((g, o), dtype=x.dtype, device=x.device) if has_bias else None
+        ws = _workspace(self._lib.pmsst_grouped_linear_backward_workspace_size(m, g, o) if has_bias else 0, x.device)
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_grouped_linear_backward(
+                _ptr(grad_out), _ptr(x), _ptr(weight), _ptr(dev_offs), g, i, m, o, _ptr(dx), _ptr(dw), _ptr(db),
+                dtype_code(x.dtype), _ptr(ws), ws.numel(), _stream(x.device),
+            )
+        check(rc, "pmsst_grouped_linear_backward")
+        return [dx, dw, db]
 
     # ------------------------------------------------------------------ mask estimator final layer
 
@@ -585,8 +637,11 @@ class HipFusedExtension:
         check(rc, "pmsst_mask_estimator_final_forward")
         return [out, pre]
 
-    def mask_estimator_final_backward_packed(self, grad_out, x, pre, weight_all, dim_inputs):
-        """Backward on packed weights; returns ``[grad_x[M,NB,H], grad_bias[2F], grad_weight (packed)]``."""
+    def mask_estimator_final_backward_packed(self, grad_out, x, pre, weight_all, dim_inputs, input_activation=None):
+        """Backward on packed weights; returns ``[grad_x[M,NB,H], grad_bias[2F], grad_weight (packed)]``.
+        ``input_activation="tanh"``: ``x`` is a tanh output and ``grad_x`` is the gradient of its
+        pre-activation, ``(dpre W) * (1 - x^2)``."""
+        act = _activation_code(input_activation)
         host, dev_offs, offs = self._bands(dim_inputs, grad_out.device)
         nb = len(offs) - 1
         grad_out = grad_out.contiguous()
@@ -601,7 +656,7 @@ class HipFusedExtension:
         with _DeviceGuard(x.device):
             rc = self._lib.pmsst_mask_estimator_final_backward(
                 _ptr(grad_out), _ptr(x), _ptr(pre), _ptr(weight_all), _ptr(dev_offs), host, nb, m, h, _ptr(dx),
-                _ptr(db), _ptr(dw), code, _ptr(ws), ws.numel(), _stream(x.device),
+                _ptr(db), _ptr(dw), act, code, _ptr(ws), ws.numel(), _stream(x.device),
             )
         check(rc, "pmsst_mask_estimator_final_backward")
         return [dx, db, dw]

@@ -53,6 +53,10 @@ EXPERIMENTAL_MASK_ESTIMATOR_FINAL_ENV = "PYMSST_EXPERIMENTAL_MASK_ESTIMATOR_FINA
 EXPERIMENTAL_MASK_ESTIMATOR_FINAL_DIRECT_ENV = "PYMSST_EXPERIMENTAL_MASK_ESTIMATOR_FINAL_DIRECT"
 EXPERIMENTAL_MASK_FINAL_AUTOGRAD_ENV = "PYMSST_EXPERIMENTAL_MASK_FINAL_AUTOGRAD"
 EXPERIMENTAL_TRAIN_PARAM_PACK_AUTOGRAD_ENV = "PYMSST_EXPERIMENTAL_TRAIN_PARAM_PACK_AUTOGRAD"
+# This build's addition: with the fused mask final layer, also run the hidden Linear + tanh of a
+# depth-2 mask MLP on the HIP kernels (hidden forward with a tanh epilogue; tanh' fused into the
+# final layer's dx epilogue; grouped-linear backward on the GPU).
+EXPERIMENTAL_FUSED_MASK_MLP_ENV = "PYMSST_EXPERIMENTAL_FUSED_MASK_MLP"
 
 _TRUE = {"1", "true", "yes", "on"}
 _FLOAT_TYPES = (torch.float16, torch.bfloat16, torch.float32)
@@ -71,7 +75,11 @@ RUNTIME_PRESETS: dict[str, dict[str, str]] = {
         EXPERIMENTAL_MASK_ESTIMATOR_FINAL_DIRECT_ENV: "1",
     },
 }
-RUNTIME_PRESETS["hip_full"] = {**RUNTIME_PRESETS["train_fragmentation"], EXPERIMENTAL_ROTARY_ENV: "1"}
+RUNTIME_PRESETS["hip_full"] = {
+    **RUNTIME_PRESETS["train_fragmentation"],
+    EXPERIMENTAL_ROTARY_ENV: "1",
+    EXPERIMENTAL_FUSED_MASK_MLP_ENV: "1",
+}
 
 
 def apply_runtime_preset(name: str) -> dict[str, str]:
@@ -108,6 +116,7 @@ class FusedTrainingStatus:
     patched_mask_final_autograd: bool = False
     patched_mask_estimator_final: bool = False
     mask_estimator_final_mode: str | None = None
+    patched_mask_mlp: bool = False  # this build's addition (hidden Linear + tanh fused as well)
 
 
 # ---------------------------------------------------------------------- switchboard
@@ -199,6 +208,14 @@ def _mask_estimator_final_mode(ext: Any) -> str | None:
     return None
 
 
+def _mask_mlp_enabled(ext: Any) -> bool:
+    return _flag(EXPERIMENTAL_FUSED_MASK_MLP_ENV) and all(
+        hasattr(ext, n)
+        for n in ("grouped_linear_forward_act", "grouped_linear_backward", "mask_estimator_final_forward_packed",
+                  "mask_estimator_final_backward_packed")
+    )
+
+
 def apply_roformer_fused_training_backend(
     model: torch.nn.Module,
     backend: str | None,
@@ -231,6 +248,7 @@ def apply_roformer_fused_training_backend(
     final_autograd = layout and _flag(EXPERIMENTAL_MASK_FINAL_AUTOGRAD_ENV)
     final_mode = _mask_estimator_final_mode(ext)
     final = _patch_core_mask_estimator_final(ext, final_mode) if final_mode else False
+    mask_mlp = final and _mask_mlp_enabled(ext)
 
     if not any((n_band_splits, single_stem, rotary, rms, gates, grouped_linear, layout, pack_autograd, final_autograd,
                 final)):
@@ -260,6 +278,7 @@ def apply_roformer_fused_training_backend(
         patched_mask_final_autograd=final_autograd,
         patched_mask_estimator_final=final,
         mask_estimator_final_mode=final_mode if final else None,
+        patched_mask_mlp=mask_mlp,
     )
 
 
@@ -620,6 +639,10 @@ def _patch_core_mask_estimator_final(ext: Any, mode: str) -> bool:
         plan = self._layer_grouping_plan()
         if not plan or plan[-1][0] != "linear":
             return original(self, x)
+        if _mask_mlp_enabled(ext):
+            fused = _fused_mask_mlp(self, x, plan, ext)
+            if fused is not None:
+                return fused
         h = x
         for li, (kind, groups) in enumerate(plan[:-1]):
             if kind == "tanh":
@@ -660,6 +683,36 @@ def _patch_core_mask_estimator_final(ext: Any, mode: str) -> bool:
     return True
 
 
+def _fused_mask_mlp(module, x, plan, ext):
+    """Whole depth-2 mask MLP (Linear -> tanh -> Linear -> GLU) on the kernels, or ``None`` when the
+    module does not have that shape.  Under autocast the compute dtype is the autocast dtype,
+    as for the stock grouped GEMMs."""
+    nb = len(module.to_freqs)
+    if len(plan) != 3 or plan[0][0] != "linear" or plan[1][0] != "tanh" or plan[2][0] != "linear":
+        return None
+    groups = plan[0][1]
+    if len(groups) != 1 or tuple(groups[0][1]) != tuple(range(nb)):
+        return None
+    layers = module._band_groupable_layers()
+    first = [band[0][1] for band in layers]
+    last = [band[2][1] for band in layers]
+    if any(l.bias is None for l in first) or any(l.bias is None for l in last):
+        return None
+    if first[0].in_features != x.shape[-1]:
+        return None
+    if any(l.out_features != 2 * d or l.in_features != first[0].out_features for l, d in zip(last, module.dim_inputs)):
+        return None
+    dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else x.dtype
+    lead = x.shape[:-2]
+    x3 = x.reshape(-1, nb, x.shape[-1]).to(dt)
+    w1 = torch.stack([l.weight for l in first]).to(dt)
+    b1 = torch.stack([l.bias for l in first]).to(dt)
+    w2 = torch.cat([l.weight.reshape(-1) for l in last]).to(dt)
+    b2 = torch.cat([l.bias for l in last]).to(dt)
+    out = _FusedMaskMLP.apply(x3, w1, b1, w2, b2, ext, tuple(int(d) for d in module.dim_inputs))
+    return out.reshape(*lead, module._dim_total)
+
+
 def _dim_offsets_tensor(module, device) -> torch.Tensor:
     """Device int64 copy of ``module._dim_offsets``, cached per device (fr.py:592-602, 876-885)."""
     cache = getattr(module, "_pymsst_dim_offsets_cache", None)
@@ -682,15 +735,20 @@ def _forward_grouped_band_split_cuda_ext(self, x: torch.Tensor) -> torch.Tensor:
     ext = self._pymsst_fused_extension
     bwd_mode = getattr(self, "_pymsst_fused_band_split_bwd_mode", None)
     lead = x.shape[:-1]
-    if _ragged_forward_enabled(ext):
-        gammas, weights, biases = [], [], []
-        for net in self.to_features:
-            norm, lin = net[0], net[1]
-            if lin.bias is None:
-                return self._pymsst_original_forward_grouped(x)
-            gammas.append(norm.gamma if norm.gamma.dtype == x.dtype else norm.gamma.to(x.dtype))
-            weights.append(lin.weight if lin.weight.dtype == x.dtype else lin.weight.to(x.dtype))
-            biases.append(lin.bias if lin.bias.dtype == x.dtype else lin.bias.to(x.dtype))
+    # Under autocast the stock per-band Linear runs in the autocast dtype and returns it; the
+    # fused op does the same (the reference keeps x's dtype here), so the residual stream that
+    # follows has the stock dtype.
+    ragged = _ragged_forward_enabled(ext)
+    if ragged and any(net[1].bias is None for net in self.to_features):
+        return self._pymsst_original_forward_grouped(x)
+    if torch.is_autocast_enabled("cuda"):
+        x = x.to(torch.get_autocast_dtype("cuda"))
+    if ragged:
+        gammas = [net[0].gamma for net in self.to_features]
+        weights = [net[1].weight for net in self.to_features]
+        biases = [net[1].bias for net in self.to_features]
+        if any(t.dtype != x.dtype for t in (gammas[0], weights[0], biases[0])):
+            gammas, weights, biases = _cast_band_params(gammas, weights, biases, x.dtype)
         out = _FusedBandSplitRagged.apply(
             x.reshape(-1, x.shape[-1]), _dim_offsets_tensor(self, x.device), ext,
             tuple(int(d) for d in self.dim_inputs), bwd_mode, *gammas, *weights, *biases,
@@ -703,6 +761,16 @@ def _forward_grouped_band_split_cuda_ext(self, x: torch.Tensor) -> torch.Tensor:
         y = _FusedBandSplitGroup.apply(part, gamma, weight, bias, ext, bwd_mode)
         outs.append(y.reshape(*lead, end - start, -1))
     return torch.cat(outs, dim=-2)
+
+
+def _cast_band_params(gammas, weights, biases, dtype):
+    """Per-band parameters in ``dtype`` with one cast per parameter kind: concatenate, cast, split
+    (three kernels instead of one cast per band; gradients flow back through the views)."""
+    out = []
+    for group in (gammas, weights, biases):
+        flat = torch.cat([t.reshape(-1) for t in group]).to(dtype)
+        out.append([v.view(t.shape) for v, t in zip(flat.split([t.numel() for t in group]), group)])
+    return out
 
 
 # ---------------------------------------------------------------------- autograd Functions
@@ -814,7 +882,8 @@ class _FusedBandSplitRagged(torch.autograd.Function):
 
 
 class _FusedGroupedLinear(torch.autograd.Function):
-    """``bands.grouped_linear`` forward on the kernel (fr.py:1029-1048); backward as batched GEMMs."""
+    """``bands.grouped_linear`` on the kernels (fr.py:1029-1048); the backward runs on the grouped-linear
+    backward kernels when the extension has them, else as batched GEMMs like the reference."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, extension):
@@ -823,6 +892,7 @@ class _FusedGroupedLinear(torch.autograd.Function):
         out = extension.grouped_linear_forward(x3, weight, bias)
         ctx.input_shape = tuple(x.shape)
         ctx.has_bias = bias is not None
+        ctx.extension = extension
         ctx.save_for_backward(x3, weight)
         return out.reshape(*x.shape[:-2], g, weight.shape[1])
 
@@ -830,6 +900,9 @@ class _FusedGroupedLinear(torch.autograd.Function):
     def backward(ctx, grad_out):
         x3, weight = ctx.saved_tensors
         go = grad_out.reshape(x3.shape[0], x3.shape[1], weight.shape[1])
+        if hasattr(ctx.extension, "grouped_linear_backward"):
+            dx, dw, db = ctx.extension.grouped_linear_backward(go.to(x3.dtype), x3, weight, ctx.has_bias)
+            return dx.reshape(ctx.input_shape), dw, db, None
         got = go.transpose(0, 1)  # [G, M, O]
         dx = torch.bmm(got, weight.contiguous()).transpose(0, 1).reshape(ctx.input_shape)
         dw = torch.bmm(got.transpose(1, 2).contiguous(), x3.transpose(0, 1).contiguous())
@@ -910,12 +983,43 @@ class _FusedMaskEstimatorFinal(torch.autograd.Function):
         return (res[0].reshape(ctx.input_shape), res[1], None, None, None, None, *res[2:])
 
 
+class _FusedMaskMLP(torch.autograd.Function):
+    """Depth-2 mask MLP for all bands: hidden = tanh(x W1_b^T + b1_b) (tanh in the GEMM epilogue),
+    then the final per-band Linear + GLU.  The backward fuses tanh' = 1 - h^2 into the final
+    layer's dx epilogue and runs the hidden layer's backward on the grouped-linear kernels.
+    Saves x, h and pre (the tensors the stock autograd graph keeps)."""
+
+    @staticmethod
+    def forward(ctx, x, w1, b1, w2, b2, extension, dim_inputs):
+        h = extension.grouped_linear_forward_act(x, w1, b1, activation="tanh")
+        out, pre = extension.mask_estimator_final_forward_packed(h, w2, b2, dim_inputs)
+        ctx.save_for_backward(x, w1, h, pre, w2)
+        ctx.extension = extension
+        ctx.dim_inputs = dim_inputs
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, w1, h, pre, w2 = ctx.saved_tensors
+        ext = ctx.extension
+        go = grad_out.reshape(pre.shape[0], -1).to(h.dtype).contiguous()
+        dz, db2, dw2 = ext.mask_estimator_final_backward_packed(go, h, pre, w2, ctx.dim_inputs,
+                                                                input_activation="tanh")
+        dx, dw1, db1 = ext.grouped_linear_backward(dz, x, w1, has_bias=True)
+        return dx, dw1, db1, dw2, db2, None, None
+
+
 class _FusedRotary(torch.autograd.Function):
     """fr.py:1154-1166; ``cos``/``sin`` are the ``[..., ::2]`` views (no copy is made)."""
 
     @staticmethod
     def forward(ctx, t, cos, sin, extension):
-        out = extension.rotary_forward(t, cos, sin)
+        if "bhnd" in getattr(extension, "rotary_out_layouts", ()):
+            # same values, written where attention reads them: its transpose(1, 2) + contiguous
+            # become free, and t itself (a view into the qkv projection) is read in place
+            out = extension.rotary_forward(t, cos, sin, out_layout="bhnd")
+        else:
+            out = extension.rotary_forward(t, cos, sin)
         ctx.save_for_backward(cos, sin)
         ctx.extension = extension
         return out

@@ -101,3 +101,85 @@ def test_empty_rows(hip_ext):
     res = hip_ext.mask_estimator_final_backward(out, xs, pre, weights, list(dims), _offsets(dims))
     assert res[0].shape == (0, 2, 32)
     assert all(torch.count_nonzero(t).item() == 0 for t in res[1:])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(129, 62, 192, 768), (37, 3, 6, 10), (130, 62, 64, 256), (65, 4, 512, 2048)])
+def test_grouped_linear_tanh_forward_and_backward(hip_ext, dtype, shape):
+    """Mask-MLP hidden layer: grouped linear with the tanh epilogue, and the grouped-linear backward
+    (dx, dW, db) against the oracle; odd widths (6 -> 10) take the unaligned paths."""
+    dn = dt_name(dtype)
+    m, groups, i, o = shape
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(m, groups, i, generator=g).to(dtype).cuda()
+    w = (torch.randn(groups, o, i, generator=g) / i**0.5).to(dtype).cuda()
+    b = (0.1 * torch.randn(groups, o, generator=g)).to(dtype).cuda()
+    out = hip_ext.grouped_linear_forward_act(x, w, b, activation="tanh")
+    assert_parity(out, oracle.grouped_linear_forward(to_np(x), to_np(w), to_np(b), dn, act="tanh"), dn, "tanh fwd")
+    plain = hip_ext.grouped_linear_forward(x, w, b)
+    assert torch.allclose(torch.tanh(plain.float()), out.float(), atol=2e-2 if dtype != torch.float32 else 1e-6)
+    dy = torch.randn(m, groups, o, generator=g).to(dtype).cuda()
+    for has_bias in (True, False):
+        dx, dw, db = hip_ext.grouped_linear_backward(dy, x, w, has_bias)
+        rdx, rdw, rdb = oracle.grouped_linear_backward(to_np(dy), to_np(x), to_np(w), has_bias, dn)
+        assert_parity(dx, rdx, dn, "dx")
+        assert_parity(dw, rdw, dn, "dW")
+        if has_bias:
+            assert_parity(db, rdb, dn, "db")
+        else:
+            assert db is None
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mask_final_backward_with_tanh_input(hip_ext, dtype):
+    dn = dt_name(dtype)
+    dims = BSR_WIDTHS
+    m, hidden = 130, 256
+    g = torch.Generator().manual_seed(22)
+    h = torch.tanh(torch.randn(m, len(dims), hidden, generator=g)).to(dtype).cuda()
+    w_all = torch.cat([(torch.randn(2 * d, hidden, generator=g) / hidden**0.5).reshape(-1) for d in dims])
+    w_all = w_all.to(dtype).cuda()
+    bias = (0.1 * torch.randn(2 * sum(dims), generator=g)).to(dtype).cuda()
+    out, pre = hip_ext.mask_estimator_final_forward_packed(h, w_all, bias, dims)
+    gout = torch.randn(out.shape, generator=g).to(dtype).cuda()
+    dz, db, dw = hip_ext.mask_estimator_final_backward_packed(gout, h, pre, w_all, dims, input_activation="tanh")
+    npw, off = [], 0
+    for d in dims:
+        npw.append(to_np(w_all[off : off + 2 * d * hidden]).reshape(2 * d, hidden))
+        off += 2 * d * hidden
+    r_dz, r_db, r_dw = oracle.mask_estimator_final_backward(to_np(gout), to_np(h), to_np(pre), npw, dims, dn,
+                                                            input_act="tanh")
+    assert_parity(dz, r_dz, dn, "dz")
+    assert_parity(db, r_db, dn, "dbias")
+    assert_parity(dw, np.concatenate([w.reshape(-1) for w in r_dw]), dn, "dW")
+    dx0, _, _ = hip_ext.mask_estimator_final_backward_packed(gout, h, pre, w_all, dims)
+    assert torch.allclose((dx0.float() * (1 - h.float() ** 2)), dz.float(), rtol=2e-2, atol=2e-2 * dz.abs().max().item())
+
+
+@pytest.mark.parametrize("dtype,m,dim", [(torch.float32, 65, 64), (torch.bfloat16, 1032, 192)])
+def test_fused_mask_mlp_autograd_vs_oracle(hip_ext, dtype, m, dim):
+    """The whole depth-2 mask MLP through the autograd Function the patch layer uses."""
+    from pymsst_amd.fused_roformer import _FusedMaskMLP
+
+    dn = dt_name(dtype)
+    dims = BSR_WIDTHS
+    nb, hid = len(dims), 4 * dim
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(m, nb, dim, generator=g).to(dtype).cuda().requires_grad_()
+    w1 = (torch.randn(nb, hid, dim, generator=g) / dim**0.5).to(dtype).cuda().requires_grad_()
+    b1 = (0.1 * torch.randn(nb, hid, generator=g)).to(dtype).cuda().requires_grad_()
+    w2s = [(torch.randn(2 * d, hid, generator=g) / hid**0.5).to(dtype) for d in dims]
+    w2 = torch.cat([w.reshape(-1) for w in w2s]).cuda().requires_grad_()
+    b2 = (0.1 * torch.randn(2 * sum(dims), generator=g)).to(dtype).cuda().requires_grad_()
+    out = _FusedMaskMLP.apply(x, w1, b1, w2, b2, hip_ext, dims)
+    npw2 = [to_np(w) for w in w2s]
+    ref = oracle.mask_mlp_forward(to_np(x), to_np(w1), to_np(b1), npw2, to_np(b2), dims, dn)
+    assert_parity(out, ref, dn, "mlp out")
+    gout = torch.randn(out.shape, generator=g).to(dtype).cuda()
+    out.backward(gout)
+    r = oracle.mask_mlp_backward(to_np(gout), to_np(x), to_np(w1), to_np(b1), npw2, to_np(b2), dims, dn)
+    assert_parity(x.grad, r[0], dn, "dx")
+    assert_parity(w1.grad, r[1], dn, "dW1")
+    assert_parity(b1.grad, r[2], dn, "db1")
+    assert_parity(w2.grad, np.concatenate([w.reshape(-1) for w in r[3]]), dn, "dW2")
+    assert_parity(b2.grad, r[4], dn, "db2")

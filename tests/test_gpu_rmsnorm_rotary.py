@@ -179,6 +179,32 @@ def test_rotary(hip_ext, dtype, shape, sliced):
     assert_parity(dt_, r, dn, "rotary bwd")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(3, 65, 4, 32), (2, 62, 8, 64), (5, 7, 3, 6)])
+def test_rotary_strided_qkv_view_and_bhnd_output(hip_ext, dtype, shape):
+    """q/k read in place from a fused qkv projection ([B, N, 3*H*D] viewed as [B, N, 3, H, D] and
+    unbound, as Attention does) and written as the [B,N,H,D]-shaped view of a dense [B,H,N,D]
+    buffer; the backward takes the transposed gradient SDPA hands back."""
+    dn = dt_name(dtype)
+    b, n, h, d = shape
+    qkv = _rand((b, n, 3 * h * d), dtype, 43)
+    q, k, _ = qkv.view(b, n, 3, h, d).unbind(dim=2)
+    assert not q.is_contiguous()
+    cos, sin = _tables(n, d, dtype, True)
+    cn, sn = to_np(cos).reshape(n, d // 2), to_np(sin).reshape(n, d // 2)
+    for t in (q, k):
+        for layout in ("bnhd", "bhnd"):
+            out = hip_ext.rotary_forward(t, cos, sin, out_layout=layout)
+            assert out.shape == (b, n, h, d)
+            if layout == "bhnd":
+                assert out.transpose(1, 2).is_contiguous()
+            assert_parity(out, oracle.rotary_forward(to_np(t), cn, sn, dn), dn, f"rotary fwd {layout}")
+    g = _rand((b, h, n, d), dtype, 44).transpose(1, 2)  # SDPA-style gradient, bhnd memory
+    dt_ = hip_ext.rotary_backward(g, cos, sin)
+    assert dt_.is_contiguous()
+    assert_parity(dt_, oracle.rotary_backward(to_np(g), cn, sn, dn), dn, "rotary bwd strided")
+
+
 def test_rotary_microbench_shape_roundtrip(hip_ext):
     # cfg2 q/k shape; forward then backward is the identity up to rounding (rotation is orthogonal)
     shape = (248, 258, 8, 64)

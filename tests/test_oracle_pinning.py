@@ -308,3 +308,36 @@ def test_round_to_matches_torch_casts():
         if name == "f16":
             ref = a.astype(np.float32).astype(np.float16).astype(np.float64)
         assert np.array_equal(got, np.asarray(ref, dtype=np.float64)), name
+
+
+def test_tanh_hidden_pieces_compose_to_mask_mlp_autograd():
+    """The pieces the fused mask MLP runs (grouped linear + tanh epilogue, final layer, final
+    backward with the tanh input, grouped-linear backward) chain to torch autograd of the MLP."""
+    r = _rng(14)
+    dim_inputs = (4, 8, 12, 4)
+    m, nb, dim, hid = 5, 4, 6, 10
+    x = r.standard_normal((m, nb, dim))
+    w1 = r.standard_normal((nb, hid, dim)) / math.sqrt(dim)
+    b1 = r.standard_normal((nb, hid))
+    w2 = [r.standard_normal((2 * d, hid)) / math.sqrt(hid) for d in dim_inputs]
+    b2 = r.standard_normal(2 * sum(dim_inputs))
+    h = oracle.grouped_linear_forward(x, w1, b1, "f64", act="tanh")
+    out, pre = oracle.mask_estimator_final_forward(h, w2, b2, dim_inputs, "f64")
+    tx, tw1, tb1, tb2 = _t(x, True), _t(w1, True), _t(b1, True), _t(b2, True)
+    tw2 = [_t(w, True) for w in w2]
+    ref = tr.mask_mlp(tx, tw1, tb1, tw2, tb2, dim_inputs)
+    _close(out, ref, what="out")
+    g = r.standard_normal((m, sum(dim_inputs)))
+    ref.backward(_t(g))
+    dz, db2, dw2 = oracle.mask_estimator_final_backward(g, h, pre, w2, dim_inputs, "f64", input_act="tanh")
+    dx, dw1, db1 = oracle.grouped_linear_backward(dz, x, w1, True, "f64")
+    _close(dx, tx.grad, what="dx")
+    _close(dw1, tw1.grad, what="dW1")
+    _close(db1, tb1.grad, what="db1")
+    _close(db2, tb2.grad, what="db2")
+    for k in range(nb):
+        _close(dw2[k], tw2[k].grad, what=f"dW2_{k}")
+    # without the tanh factor the chain must fail (guards against a dropped 1 - h^2 term)
+    dz_bad, _, _ = oracle.mask_estimator_final_backward(g, h, pre, w2, dim_inputs, "f64")
+    dx_bad, _, _ = oracle.grouped_linear_backward(dz_bad, x, w1, True, "f64")
+    assert np.max(np.abs(dx_bad - tx.grad.numpy())) > 1e-3
