@@ -46,13 +46,16 @@ struct BandArgs {
 
 // B operand of the forward: rows m of x (K = band features) scaled by gamma;
 // keeps the running sum of squares of the raw values of its two rows
-// (rows tid/8 and tid/8 + 32, k quad (tid%8)*4 of every chunk).
+// (rows tid/8 and tid/8 + 32, k quad (tid%8)*4 of every chunk).  gamma for the
+// thread's k quad is fetched with the chunk.
 template <typename T, bool NORM>
 struct XGammaLoader {
   static constexpr int kQuads = kBM * (kChunkK / 4) / kGemmThreads;
   static_assert(kQuads == 2, "two rows per thread");
   struct Regs {
-    Pack<T, 4> q[kQuads];
+    quad_t<T> q[kQuads];
+    quad_t<T> g;
+    uint32_t ok;
   };
   const T* base;
   int64_t stride;
@@ -61,44 +64,38 @@ struct XGammaLoader {
   int k_valid;
   bool vec4;
   mutable float ss[kQuads];
-  mutable int last_k0;
 
   __device__ __forceinline__ void fetch(int k0, Regs& g) const {
-#pragma unroll
-    for (int i = 0; i < kQuads; ++i) {
-      const int idx = threadIdx.x + i * kGemmThreads;
-      const int r = idx / (kChunkK / 4);
-      const int k = k0 + (idx % (kChunkK / 4)) * 4;
-      const T* p = base + r * stride + k;
-      if (r < rows_valid && vec4 && k + 4 <= k_valid) {
-        g.q[i] = *reinterpret_cast<const Pack<T, 4>*>(p);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) g.q[i].v[j] = (r < rows_valid && k + j < k_valid) ? p[j] : from_f32<T>(0.f);
-      }
-    }
-    last_k0 = k0;
-  }
-  __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
-    const int kq = (threadIdx.x % (kChunkK / 4)) * 4;
-    const int k = last_k0 + kq;
-    float gm[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) gm[j] = (NORM && k + j < k_valid) ? to_f32(gamma[k + j]) : 1.f;
+    const int k = k0 + (threadIdx.x % (kChunkK / 4)) * 4;
+    g.ok = 0;
 #pragma unroll
     for (int i = 0; i < kQuads; ++i) {
       const int r = (threadIdx.x + i * kGemmThreads) / (kChunkK / 4);
+      g.q[i] = fetch_quad<T>(base + r * stride + k, base, vec4, r < rows_valid, k_valid - k, g.ok, i);
+    }
+    if (NORM) g.g = fetch_quad<T>(gamma + k, gamma, vec4, true, k_valid - k, g.ok, kQuads);
+  }
+  __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
+    const int kq = (threadIdx.x % (kChunkK / 4)) * 4;
+    float gm[4] = {1.f, 1.f, 1.f, 1.f};
+    if (NORM) quad_to_f32<T>(mask_quad<T>(g.g, (g.ok >> kQuads) & 1), gm);
+#pragma unroll
+    for (int i = 0; i < kQuads; ++i) {
+      const int r = (threadIdx.x + i * kGemmThreads) / (kChunkK / 4);
+      float v[4];
+      quad_to_f32<T>(mask_quad<T>(g.q[i], (g.ok >> i) & 1), v);
+      Pack<T, 4> pk;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float v = to_f32(g.q[i].v[j]);
-        ss[i] += v * v;
-        lds[lds_index<T>(r, kq + j)] = from_f32<T>(v * gm[j]);
+        ss[i] += v[j] * v[j];
+        pk.v[j] = from_f32<T>(v[j] * gm[j]);
       }
+      commit_quad<T>(lds, r, kq, __builtin_bit_cast(quad_t<T>, pk));
     }
   }
 };
 
-template <typename T, int TO, bool WRITE_NORMED, bool NORM, int ACT>
+template <typename T, int TO, bool WRITE_NORMED, bool NORM, int ACT, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restrict__ x, const T* __restrict__ gamma,
                                                               const T* __restrict__ weight,
                                                               const T* __restrict__ bias, T* __restrict__ out,
@@ -119,8 +116,8 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
   const int rows_valid = static_cast<int>(a.M - m0 < kBM ? a.M - m0 : kBM);
   const T* xb = x + m0 * a.x_stride + off;
 
-  KRowLoader<T, OT> la{weight + static_cast<int64_t>(O) * off + static_cast<int64_t>(oc) * I, I, O - oc, I, a.vec4};
-  XGammaLoader<T, NORM> lb{xb, a.x_stride, gamma + off, rows_valid, I, a.vec4, {0.f, 0.f}, 0};
+  KRowLoader<T, OT> la{weight + static_cast<int64_t>(O) * off + static_cast<int64_t>(oc) * I, I, O - oc, I, V4};
+  XGammaLoader<T, NORM> lb{xb, a.x_stride, gamma + off, rows_valid, I, V4, {0.f, 0.f}};
   f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
   for (int i = 0; i < S::kTR; ++i)
@@ -200,7 +197,7 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
 
 // NORM = false: plain grouped linear, dx = dy W_b in one pass (nsrc, inv_norm, gamma and
 // dg_partial unused).
-template <typename T, bool FROM_X, bool NORM>
+template <typename T, bool FROM_X, bool NORM, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __restrict__ dy,
                                                                  const T* __restrict__ nsrc,
                                                                  const float* __restrict__ inv_norm,
@@ -245,8 +242,8 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
     }
     for (int i0 = 0; i0 < I; i0 += kBI) {
       // A[i][o] = W_b[o][i0 + i] (MN-contiguous in i);  B[m][o] = dy[m0 + m][band][o]
-      MNLoader<T, kBI> la{wb + i0, I, I - i0, O, a.vec4};
-      KRowLoader<T, kBM> lb{dyb, static_cast<int64_t>(a.NB) * O, rows_valid, O, a.ovec4};
+      MNLoader<T, kBI> la{wb + i0, I, I - i0, O, V4};
+      KRowLoader<T, kBM> lb{dyb, static_cast<int64_t>(a.NB) * O, rows_valid, O, V4};
       f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[0][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -330,7 +327,7 @@ constexpr int kDwBI = 64;
 constexpr int kDwBO = 64;
 
 // NORM = false: plain grouped linear, dW_b^T = x_b^T dy_b (no gamma / inv_norm scaling).
-template <typename T, bool FROM_X, bool NORM>
+template <typename T, bool FROM_X, bool NORM, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __restrict__ dy,
                                                                  const T* __restrict__ nsrc,
                                                                  const float* __restrict__ inv_norm,
@@ -349,15 +346,18 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
 
   // A[i][m] = n[m][off + i0 + i] * gamma (MN-contiguous in i; n = x * inv * sqrt(I) when FROM_X)
   // B[o][m] = dy[m][band][o0 + o]       (MN-contiguous in o)
-  MNLoader<T, kDwBI> la{nsrc + off + i0, a.F, I - i0, static_cast<int>(a.M), a.vec4};
-  if (NORM) la.cs = gamma + off + i0;
+  MNLoader<T, kDwBI> la{nsrc + off + i0, a.F, I - i0, static_cast<int>(a.M), V4};
+  if (NORM) {
+    la.cs = gamma + off + i0;
+    la.init();
+  }
   if (NORM && FROM_X) {
     la.rs = inv_norm + band;
     la.rs_stride = a.NB;
     la.rs_mul = sqrtf(static_cast<float>(I));
   }
   MNLoader<T, kDwBO> lb{dy + static_cast<int64_t>(band) * O + o0, static_cast<int64_t>(a.NB) * O, O - o0,
-                        static_cast<int>(a.M), a.ovec4};
+                        static_cast<int>(a.M), V4};
   f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
   for (int i = 0; i < S::kTR; ++i)
@@ -447,26 +447,31 @@ int launch_fwd(const void* x, int64_t x_stride, const void* gamma, const void* w
   const T* pb = static_cast<const T*>(bias);
   T* po = static_cast<T*>(out);
   T* pn = static_cast<T*>(normed);
-#define PMSST_BSF(TO)                                                                                              \
-  do {                                                                                                             \
-    if (!norm && act == PMSST_ACT_TANH)                                                                            \
-      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, false, PMSST_ACT_TANH>), grid, dim3(kGemmThreads), 0, stream, \
-                         px, pg, pw, pb, po, pn, inv_norm, a);                                                     \
-    else if (!norm)                                                                                                \
-      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, false, PMSST_ACT_NONE>), grid, dim3(kGemmThreads), 0, stream, \
-                         px, pg, pw, pb, po, pn, inv_norm, a);                                                     \
-    else if (pn != nullptr)                                                                                        \
-      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, true, true, PMSST_ACT_NONE>), grid, dim3(kGemmThreads), 0, stream,  \
-                         px, pg, pw, pb, po, pn, inv_norm, a);                                                     \
-    else                                                                                                           \
-      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, true, PMSST_ACT_NONE>), grid, dim3(kGemmThreads), 0, stream, \
-                         px, pg, pw, pb, po, pn, inv_norm, a);                                                     \
+#define PMSST_BSF(TO, V4)                                                                                           \
+  do {                                                                                                              \
+    if (!norm && act == PMSST_ACT_TANH)                                                                             \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, false, PMSST_ACT_TANH, V4>), grid, dim3(kGemmThreads), 0,      \
+                         stream, px, pg, pw, pb, po, pn, inv_norm, a);                                              \
+    else if (!norm)                                                                                                 \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, false, PMSST_ACT_NONE, V4>), grid, dim3(kGemmThreads), 0,      \
+                         stream, px, pg, pw, pb, po, pn, inv_norm, a);                                              \
+    else if (pn != nullptr)                                                                                         \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, true, true, PMSST_ACT_NONE, V4>), grid, dim3(kGemmThreads), 0, stream, \
+                         px, pg, pw, pb, po, pn, inv_norm, a);                                                      \
+    else                                                                                                            \
+      hipLaunchKernelGGL((bs_fwd_kernel<T, TO, false, true, PMSST_ACT_NONE, V4>), grid, dim3(kGemmThreads), 0,       \
+                         stream, px, pg, pw, pb, po, pn, inv_norm, a);                                              \
   } while (0)
-  switch (tile_capacity(O)) {
-    case 1: PMSST_BSF(1); break;
-    case 2: PMSST_BSF(2); break;
-    case 3: PMSST_BSF(3); break;
-    default: PMSST_BSF(4); break;
+  // Unaligned shapes (odd band widths) take one scalar-load variant with the widest tile.
+  if (!a.vec4) {
+    PMSST_BSF(4, false);
+  } else {
+    switch (tile_capacity(O)) {
+      case 1: PMSST_BSF(1, true); break;
+      case 2: PMSST_BSF(2, true); break;
+      case 3: PMSST_BSF(3, true); break;
+      default: PMSST_BSF(4, true); break;
+    }
   }
 #undef PMSST_BSF
   return check_launch("bs_fwd_kernel");
@@ -506,24 +511,32 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   const int m_tiles = static_cast<int>((M + kBM - 1) / kBM);
   if (M > 0) {
     const dim3 grid(static_cast<unsigned>(m_tiles), static_cast<unsigned>(hb.NB));
-    if (from_x)
-      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, true, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
-                         pg, pw, static_cast<T*>(dx), partial, a);
-    else
-      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
-                         pg, pw, static_cast<T*>(dx), partial, a);
+    const bool v4 = a.vec4 && a.ovec4;
+#define PMSST_BDX(FX, V4)                                                                                   \
+  hipLaunchKernelGGL((bs_bwd_dx_kernel<T, FX, true, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, \
+                     pg, pw, static_cast<T*>(dx), partial, a)
+    if (from_x) {
+      if (v4) PMSST_BDX(true, true); else PMSST_BDX(true, false);
+    } else {
+      if (v4) PMSST_BDX(false, true); else PMSST_BDX(false, false);
+    }
+#undef PMSST_BDX
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
   {
     const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
     const dim3 grid(static_cast<unsigned>((O + kDwBO - 1) / kDwBO), static_cast<unsigned>(hb.NB * max_itiles));
-    if (from_x)
-      hipLaunchKernelGGL((bs_bwd_dw_kernel<T, true, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
-                         pg, static_cast<T*>(dw), max_itiles, a);
-    else
-      hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
-                         pg, static_cast<T*>(dw), max_itiles, a);
+    const bool v4 = a.vec4 && a.ovec4;
+#define PMSST_BDW(FX, V4)                                                                                   \
+  hipLaunchKernelGGL((bs_bwd_dw_kernel<T, FX, true, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, \
+                     pg, static_cast<T*>(dw), max_itiles, a)
+    if (from_x) {
+      if (v4) PMSST_BDW(true, true); else PMSST_BDW(true, false);
+    } else {
+      if (v4) PMSST_BDW(false, true); else PMSST_BDW(false, false);
+    }
+#undef PMSST_BDW
     int rc = check_launch("bs_bwd_dw_kernel");
     if (rc != PMSST_OK) return rc;
   }
@@ -555,16 +568,24 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
   const T* pw = static_cast<const T*>(weight);
   if (M > 0) {
     const dim3 grid(static_cast<unsigned>((M + kBM - 1) / kBM), static_cast<unsigned>(hb.NB));
-    hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px, nullptr,
-                       nullptr, pw, static_cast<T*>(dx), nullptr, a);
+    if (a.vec4 && a.ovec4)
+      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
+                         nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, a);
+    else
+      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
+                         nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, a);
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
   {
     const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
     const dim3 grid(static_cast<unsigned>((O + kDwBO - 1) / kDwBO), static_cast<unsigned>(hb.NB * max_itiles));
-    hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px, nullptr,
-                       nullptr, static_cast<T*>(dw), max_itiles, a);
+    if (a.vec4 && a.ovec4)
+      hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
+                         nullptr, nullptr, static_cast<T*>(dw), max_itiles, a);
+    else
+      hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
+                         nullptr, nullptr, static_cast<T*>(dw), max_itiles, a);
     int rc = check_launch("bs_bwd_dw_kernel");
     if (rc != PMSST_OK) return rc;
   }

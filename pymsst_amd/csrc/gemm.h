@@ -21,6 +21,8 @@
 // commit(regs, lds) registers -> LDS.  Out-of-range rows and k read as zero.
 #pragma once
 
+#include <type_traits>
+
 #include "mfma.h"
 
 namespace pmsst {
@@ -50,14 +52,111 @@ __device__ __forceinline__ f32x4_t mfma_tile(const T* __restrict__ a, int ra, co
   }
 }
 
-// K-contiguous rows: element (r, k) = base[r * stride + k].  4-element groups
-// (8 bytes for 16-bit types) when `vec4` (row starts and k0 4-aligned).
+// ---------------------------------------------------------------- guarded loads
+// Loads never branch on bounds, and nothing consumes a loaded value until commit():
+// an out-of-range lane reads the tile origin (always a valid element) and records a
+// validity bit; commit() masks the value to zero.  fetch() therefore issues all of
+// its loads back to back and the MFMAs of the current chunk run while they are in
+// flight.  When a loader's `vec4` flag is set, every k / mn extent it is given is a
+// multiple of 4 (the launchers only set it then), so a quad is either fully in
+// range or fully out; without it (unaligned shapes) the loader falls back to
+// per-element loads that are masked at once.
+
+template <typename T>
+using raw_t = typename std::conditional<sizeof(T) == 2, uint16_t, uint32_t>::type;
+// 4 consecutive elements as raw bits: 8 bytes for 16-bit types, 16 for fp32.
+template <typename T>
+using quad_t = typename std::conditional<sizeof(T) == 2, uint2, uint4>::type;
+
+template <typename T>
+__device__ __forceinline__ quad_t<T> raw_quad(const T* p) {
+  return *reinterpret_cast<const quad_t<T>*>(p);
+}
+
+template <typename T>
+__device__ __forceinline__ quad_t<T> mask_quad(quad_t<T> q, bool ok) {
+  q.x = ok ? q.x : 0u;
+  q.y = ok ? q.y : 0u;
+  if constexpr (sizeof(T) == 4) {
+    q.z = ok ? q.z : 0u;
+    q.w = ok ? q.w : 0u;
+  }
+  return q;
+}
+
+// Unaligned fallback: element j is loaded when `ok && j < valid`, masked at once.
+template <typename T>
+__device__ __forceinline__ quad_t<T> load_quad_scalar(const T* p, const T* safe, bool ok, int valid) {
+  uint32_t e[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool in = ok && j < valid;
+    const raw_t<T> v = *reinterpret_cast<const raw_t<T>*>(in ? p + j : safe);
+    e[j] = in ? static_cast<uint32_t>(v) : 0u;
+  }
+  quad_t<T> q;
+  if constexpr (sizeof(T) == 2) {
+    q.x = e[0] | (e[1] << 16);
+    q.y = e[2] | (e[3] << 16);
+  } else {
+    q.x = e[0];
+    q.y = e[1];
+    q.z = e[2];
+    q.w = e[3];
+  }
+  return q;
+}
+
+// One quad: raw load (vec4) recording validity, or the masked scalar fallback.
+template <typename T>
+__device__ __forceinline__ quad_t<T> fetch_quad(const T* p, const T* safe, bool vec4, bool row_ok, int k_left,
+                                                uint32_t& okbits, int bit) {
+  if (vec4) {
+    const bool ok = row_ok && k_left > 0;
+    okbits |= static_cast<uint32_t>(ok) << bit;
+    return raw_quad<T>(ok ? p : safe);
+  }
+  okbits |= 1u << bit;
+  return load_quad_scalar<T>(p, safe, row_ok, k_left);
+}
+
+template <typename T>
+__device__ __forceinline__ void quad_to_f32(const quad_t<T>& q, float (&o)[4]) {
+  if constexpr (sizeof(T) == 2) {
+    const Pack<T, 4> pk = __builtin_bit_cast(Pack<T, 4>, q);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = to_f32(pk.v[j]);
+  } else {
+    o[0] = __uint_as_float(q.x);
+    o[1] = __uint_as_float(q.y);
+    o[2] = __uint_as_float(q.z);
+    o[3] = __uint_as_float(q.w);
+  }
+}
+
+// Stores a quad of consecutive k (kq % 4 == 0) of LDS row r.
+template <typename T>
+__device__ __forceinline__ void commit_quad(T* lds, int r, int kq, const quad_t<T>& q) {
+  if constexpr (sizeof(T) == 2) {
+    *reinterpret_cast<uint2*>(lds + lds_index<T>(r, kq)) = q;
+  } else {
+    uint32_t* row = reinterpret_cast<uint32_t*>(lds);
+    row[lds_index<T>(r, kq + 0)] = q.x;
+    row[lds_index<T>(r, kq + 1)] = q.y;
+    row[lds_index<T>(r, kq + 2)] = q.z;
+    row[lds_index<T>(r, kq + 3)] = q.w;
+  }
+}
+
+// K-contiguous rows: element (r, k) = base[r * stride + k].  Thread t moves the quad
+// (r, k) = (t / 8 + 32 i, 4 (t % 8)) of every chunk, i < ROWS / 32.
 template <typename T, int ROWS>
 struct KRowLoader {
   static constexpr int kQuads = ROWS * (kChunkK / 4) / kGemmThreads;
   static_assert(kQuads >= 1 && ROWS * (kChunkK / 4) % kGemmThreads == 0, "tile too small");
   struct Regs {
-    Pack<T, 4> q[kQuads];
+    quad_t<T> q[kQuads];
+    uint32_t ok;
   };
   const T* base;
   int64_t stride;
@@ -66,33 +165,19 @@ struct KRowLoader {
   bool vec4;
 
   __device__ __forceinline__ void fetch(int k0, Regs& g) const {
+    const int k = k0 + (threadIdx.x % (kChunkK / 4)) * 4;
+    g.ok = 0;
 #pragma unroll
     for (int i = 0; i < kQuads; ++i) {
-      const int idx = threadIdx.x + i * kGemmThreads;
-      const int r = idx / (kChunkK / 4);
-      const int k = k0 + (idx % (kChunkK / 4)) * 4;
-      const T* p = base + r * stride + k;
-      if (r < rows_valid && vec4 && k + 4 <= k_valid) {
-        g.q[i] = *reinterpret_cast<const Pack<T, 4>*>(p);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) g.q[i].v[j] = (r < rows_valid && k + j < k_valid) ? p[j] : from_f32<T>(0.f);
-      }
+      const int r = (threadIdx.x + i * kGemmThreads) / (kChunkK / 4);
+      g.q[i] = fetch_quad<T>(base + r * stride + k, base, vec4, r < rows_valid, k_valid - k, g.ok, i);
     }
   }
   __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
+    const int kq = (threadIdx.x % (kChunkK / 4)) * 4;
 #pragma unroll
-    for (int i = 0; i < kQuads; ++i) {
-      const int idx = threadIdx.x + i * kGemmThreads;
-      const int r = idx / (kChunkK / 4);
-      const int kq = (idx % (kChunkK / 4)) * 4;
-      if constexpr (sizeof(T) == 2) {
-        *reinterpret_cast<Pack<T, 4>*>(lds + lds_index<T>(r, kq)) = g.q[i];
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) lds[lds_index<T>(r, kq + j)] = g.q[i].v[j];
-      }
-    }
+    for (int i = 0; i < kQuads; ++i)
+      commit_quad<T>(lds, (threadIdx.x + i * kGemmThreads) / (kChunkK / 4), kq, mask_quad<T>(g.q[i], (g.ok >> i) & 1));
   }
 };
 
@@ -110,7 +195,9 @@ struct MNLoader {
   static_assert(KB >= 1 && KB * kQuadsPerK * (kChunkK / KB) == ROWS * kChunkK / 4, "tile shape");
   static_assert(kQuadsPerK * (kChunkK / KB) == kGemmThreads, "one block per thread");
   struct Regs {
-    float v[KB][4];
+    quad_t<T> q[KB];
+    float s[KB];
+    uint32_t ok;
   };
   const T* base;
   int64_t kstride;
@@ -121,48 +208,48 @@ struct MNLoader {
   const float* rs = nullptr;    // per-k scale, or null
   int64_t rs_stride = 1;
   float rs_mul = 1.f;
+  // per-mn scale of this thread's quad (loaded once; cs does not depend on k)
+  float c[4] = {1.f, 1.f, 1.f, 1.f};
 
+  __device__ __forceinline__ void init() {
+    if (cs != nullptr) {
+      const int mn = (threadIdx.x % kQuadsPerK) * 4;
+      quad_to_f32<T>(load_quad_scalar<T>(cs + mn, cs, true, mn_valid - mn), c);
+    }
+  }
   __device__ __forceinline__ void fetch(int k0, Regs& g) const {
     const int mn = (threadIdx.x % kQuadsPerK) * 4;
     const int kb = (threadIdx.x / kQuadsPerK) * KB;
-    float c[4] = {1.f, 1.f, 1.f, 1.f};
-    if (cs != nullptr) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) c[j] = mn + j < mn_valid ? to_f32(cs[mn + j]) : 0.f;
-    }
+    g.ok = 0;
 #pragma unroll
     for (int t = 0; t < KB; ++t) {
       const int k = k0 + kb + t;
-      float e[4] = {0.f, 0.f, 0.f, 0.f};
-      if (k < k_valid) {
-        const T* p = base + static_cast<int64_t>(k) * kstride + mn;
-        if (vec4 && mn + 4 <= mn_valid) {
-          load_pack<T, 4>(p, e);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) e[j] = mn + j < mn_valid ? to_f32(p[j]) : 0.f;
-        }
-        const float s = rs != nullptr ? rs[static_cast<int64_t>(k) * rs_stride] * rs_mul : 1.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) e[j] *= s * c[j];
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) g.v[t][j] = e[j];
+      g.q[t] = fetch_quad<T>(base + static_cast<int64_t>(k) * kstride + mn, base, vec4, k < k_valid, mn_valid - mn,
+                             g.ok, t);
+      g.s[t] = rs != nullptr ? rs[static_cast<int64_t>(k < k_valid ? k : 0) * rs_stride] : 1.f;
     }
   }
   __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
     const int mn = (threadIdx.x % kQuadsPerK) * 4;
     const int kb = (threadIdx.x / kQuadsPerK) * KB;
+    float v[KB][4];
+#pragma unroll
+    for (int t = 0; t < KB; ++t) {
+      quad_to_f32<T>(mask_quad<T>(g.q[t], (g.ok >> t) & 1), v[t]);
+      const float st = rs != nullptr ? g.s[t] * rs_mul : 1.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[t][j] *= st * c[j];
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if constexpr (sizeof(T) == 2) {
         float col[KB];
 #pragma unroll
-        for (int t = 0; t < KB; ++t) col[t] = g.v[t][j];
+        for (int t = 0; t < KB; ++t) col[t] = v[t][j];
         store_pack<T, KB>(lds + lds_index<T>(mn + j, kb), col);
       } else {
 #pragma unroll
-        for (int t = 0; t < KB; ++t) lds[lds_index<T>(mn + j, kb + t)] = g.v[t][j];
+        for (int t = 0; t < KB; ++t) lds[lds_index<T>(mn + j, kb + t)] = v[t][j];
       }
     }
   }
@@ -189,8 +276,7 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
                                                             [TileShape<BR, BC, WR, WC>::kTC]) {
   using S = TileShape<BR, BC, WR, WC>;
   constexpr int P = LdsPitch<T>::value;
-  T* abuf[2] = {lds, lds + (BR + BC) * P};
-  T* bbuf[2] = {lds + BR * P, lds + (BR + BC) * P + BR * P};
+  constexpr int kBuf = (BR + BC) * P;  // elements of one (A, B) buffer pair
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int r0 = (wave / WC) * (BR / WR);
@@ -201,11 +287,14 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
   typename LB::Regs rb;
   la.fetch(0, ra);
   lb.fetch(0, rb);
-  la.commit(ra, abuf[0]);
-  lb.commit(rb, bbuf[0]);
+  la.commit(ra, lds);
+  lb.commit(rb, lds + BR * P);
   __syncthreads();
   for (int kc = 0; kc < nk; ++kc) {
-    const int cur = kc & 1;
+    // buffer offsets computed from the __shared__ base (no pointer tables), so every
+    // access stays a ds_* instruction and waits only on the LDS counter
+    const int cur = (kc & 1) * kBuf;
+    const int nxt = kBuf - cur;
     const bool more = kc + 1 < nk;
     if (more) {
       la.fetch((kc + 1) * kChunkK, ra);
@@ -215,13 +304,13 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
     for (int i = 0; i < S::kTR; ++i) {
 #pragma unroll
       for (int j = 0; j < S::kTC; ++j) {
-        acc[i][j] = mfma_tile<T>(abuf[cur], r0 + i * 16 + (lane & 15), bbuf[cur], c0 + j * 16 + (lane & 15),
+        acc[i][j] = mfma_tile<T>(lds + cur, r0 + i * 16 + (lane & 15), lds + cur + BR * P, c0 + j * 16 + (lane & 15),
                                  acc[i][j], lane);
       }
     }
     if (more) {
-      la.commit(ra, abuf[cur ^ 1]);
-      lb.commit(rb, bbuf[cur ^ 1]);
+      la.commit(ra, lds + nxt);
+      lb.commit(rb, lds + nxt + BR * P);
     }
     __syncthreads();
   }

@@ -48,47 +48,34 @@ template <typename T>
 struct LeftGateLoader {
   static constexpr int kQuads = 128 * (kChunkK / 4) / kGemmThreads;
   struct Regs {
-    Pack<T, 4> q[kQuads];
+    quad_t<T> q[kQuads];
+    uint32_t ok;
   };
   const T* wb;  // band weights [2I][H]
   int H, I, l0;
   bool vec4;
   __device__ __forceinline__ void fetch(int k0, Regs& g) const {
+    const int k = k0 + (threadIdx.x % (kChunkK / 4)) * 4;
+    g.ok = 0;
 #pragma unroll
     for (int i = 0; i < kQuads; ++i) {
-      const int idx = threadIdx.x + i * kGemmThreads;
-      const int r = idx / (kChunkK / 4);
-      const int k = k0 + (idx % (kChunkK / 4)) * 4;
+      const int r = (threadIdx.x + i * kGemmThreads) / (kChunkK / 4);
       const int l = l0 + (r & 63);
-      const bool ok = l < I;
       const T* p = wb + static_cast<int64_t>(r < 64 ? l : I + l) * H + k;
-      if (ok && vec4 && k + 4 <= H) {
-        g.q[i] = *reinterpret_cast<const Pack<T, 4>*>(p);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) g.q[i].v[j] = (ok && k + j < H) ? p[j] : from_f32<T>(0.f);
-      }
+      g.q[i] = fetch_quad<T>(p, wb, vec4, l < I, H - k, g.ok, i);
     }
   }
   __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
+    const int kq = (threadIdx.x % (kChunkK / 4)) * 4;
 #pragma unroll
-    for (int i = 0; i < kQuads; ++i) {
-      const int idx = threadIdx.x + i * kGemmThreads;
-      const int r = idx / (kChunkK / 4);
-      const int kq = (idx % (kChunkK / 4)) * 4;
-      if constexpr (sizeof(T) == 2) {
-        *reinterpret_cast<Pack<T, 4>*>(lds + lds_index<T>(r, kq)) = g.q[i];
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) lds[lds_index<T>(r, kq + j)] = g.q[i].v[j];
-      }
-    }
+    for (int i = 0; i < kQuads; ++i)
+      commit_quad<T>(lds, (threadIdx.x + i * kGemmThreads) / (kChunkK / 4), kq, mask_quad<T>(g.q[i], (g.ok >> i) & 1));
   }
 };
 
 constexpr int kFwdBM = 128;
 
-template <typename T>
+template <typename T, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void me_fwd_kernel(const T* __restrict__ x, const T* __restrict__ weight,
                                                               const T* __restrict__ bias, T* __restrict__ pre,
                                                               T* __restrict__ out, int max_lchunks, MaskArgs a) {
@@ -104,8 +91,8 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_kernel(const T* __restric
   const int H = a.H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
-  LeftGateLoader<T> la{weight + static_cast<int64_t>(2) * off * H, H, I, l0, a.vec4};
-  KRowLoader<T, kFwdBM> lb{x + (m0 * a.NB + band) * H, static_cast<int64_t>(a.NB) * H, rows_valid, H, a.vec4};
+  LeftGateLoader<T> la{weight + static_cast<int64_t>(2) * off * H, H, I, l0, V4};
+  KRowLoader<T, kFwdBM> lb{x + (m0 * a.NB + band) * H, static_cast<int64_t>(a.NB) * H, rows_valid, H, V4};
   f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
   for (int i = 0; i < S::kTR; ++i)
@@ -214,7 +201,7 @@ constexpr int kDxBM = 64;
 
 // TANH_IN: the layer input x is tanh(z) of the previous layer, and the kernel writes
 // dz = (dpre W_b) * (1 - x^2) instead of dx (the hidden activation's backward, fused).
-template <typename T, bool TANH_IN>
+template <typename T, bool TANH_IN, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __restrict__ dpre,
                                                                  const T* __restrict__ weight,
                                                                  const T* __restrict__ x, T* __restrict__ dx,
@@ -232,8 +219,8 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __rest
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
 
   // A[h][j] = W_b[j][h0 + h]  (MN-contiguous in h);  B[m][j] = dpre[m0 + m][2 off + j]
-  MNLoader<T, kDxBH> la{weight + static_cast<int64_t>(2) * off * H + h0, H, H - h0, 2 * I, a.vec4};
-  KRowLoader<T, kDxBM> lb{dpre + m0 * pitch2 + 2 * off, pitch2, rows_valid, 2 * I, a.vec4};
+  MNLoader<T, kDxBH> la{weight + static_cast<int64_t>(2) * off * H + h0, H, H - h0, 2 * I, V4};
+  KRowLoader<T, kDxBM> lb{dpre + m0 * pitch2 + 2 * off, pitch2, rows_valid, 2 * I, V4};
   f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
   for (int i = 0; i < S::kTR; ++i)
@@ -275,7 +262,7 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __rest
 constexpr int kDwBH = 128;
 constexpr int kDwBJ = 64;
 
-template <typename T>
+template <typename T, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __restrict__ dpre, const T* __restrict__ x,
                                                                  T* __restrict__ dw, int max_jchunks, MaskArgs a) {
   __shared__ T lds[gemm_lds_elems<T, kDwBH, kDwBJ>()];
@@ -293,8 +280,8 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __rest
 
   // A[h][m] = x[m][band][h0 + h];  B[j][m] = dpre[m][2 off + j0 + j]   (both MN-contiguous, K = M)
   MNLoader<T, kDwBH> la{x + static_cast<int64_t>(band) * H + h0, static_cast<int64_t>(a.NB) * H, H - h0,
-                        static_cast<int>(a.M), a.vec4};
-  MNLoader<T, kDwBJ> lb{dpre + 2 * off + j0, pitch2, K2 - j0, static_cast<int>(a.M), a.vec4};
+                        static_cast<int>(a.M), V4};
+  MNLoader<T, kDwBJ> lb{dpre + 2 * off + j0, pitch2, K2 - j0, static_cast<int>(a.M), V4};
   f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
   for (int i = 0; i < S::kTR; ++i)
@@ -363,9 +350,14 @@ int launch_me_fwd(const void* x, const void* weight, const void* bias, const int
            al(out, 4 * sizeof(T));
   const int max_lchunks = (hm.max_width + 63) / 64;
   const dim3 grid(static_cast<unsigned>((M + kFwdBM - 1) / kFwdBM), static_cast<unsigned>(hm.NB * max_lchunks));
-  hipLaunchKernelGGL((me_fwd_kernel<T>), grid, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
-                     static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
-                     static_cast<T*>(out), max_lchunks, a);
+  if (a.vec4)
+    hipLaunchKernelGGL((me_fwd_kernel<T, true>), grid, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
+                       static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
+                       static_cast<T*>(out), max_lchunks, a);
+  else
+    hipLaunchKernelGGL((me_fwd_kernel<T, false>), grid, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
+                       static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
+                       static_cast<T*>(out), max_lchunks, a);
   return check_launch("me_fwd_kernel");
 }
 
@@ -402,19 +394,26 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
     if (rc != PMSST_OK) return rc;
     const dim3 g2(static_cast<unsigned>((M + kDxBM - 1) / kDxBM), static_cast<unsigned>(hm.NB),
                   static_cast<unsigned>((H + kDxBH - 1) / kDxBH));
-    if (input_act == PMSST_ACT_TANH)
-      hipLaunchKernelGGL((me_bwd_dx_kernel<T, true>), g2, dim3(kGemmThreads), 0, stream, dpre,
-                         static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), a);
-    else
-      hipLaunchKernelGGL((me_bwd_dx_kernel<T, false>), g2, dim3(kGemmThreads), 0, stream, dpre,
-                         static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), a);
+#define PMSST_MDX(TANH, V4)                                                                                    \
+  hipLaunchKernelGGL((me_bwd_dx_kernel<T, TANH, V4>), g2, dim3(kGemmThreads), 0, stream, dpre,                   \
+                     static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), a)
+    if (input_act == PMSST_ACT_TANH) {
+      if (a.vec4) PMSST_MDX(true, true); else PMSST_MDX(true, false);
+    } else {
+      if (a.vec4) PMSST_MDX(false, true); else PMSST_MDX(false, false);
+    }
+#undef PMSST_MDX
     rc = check_launch("me_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
   const int max_jchunks = (2 * hm.max_width + kDwBJ - 1) / kDwBJ;
   const dim3 g3(static_cast<unsigned>((H + kDwBH - 1) / kDwBH), static_cast<unsigned>(hm.NB * max_jchunks));
-  hipLaunchKernelGGL((me_bwd_dw_kernel<T>), g3, dim3(kGemmThreads), 0, stream, dpre, static_cast<const T*>(x),
-                     static_cast<T*>(dw), max_jchunks, a);
+  if (a.vec4)
+    hipLaunchKernelGGL((me_bwd_dw_kernel<T, true>), g3, dim3(kGemmThreads), 0, stream, dpre, static_cast<const T*>(x),
+                       static_cast<T*>(dw), max_jchunks, a);
+  else
+    hipLaunchKernelGGL((me_bwd_dw_kernel<T, false>), g3, dim3(kGemmThreads), 0, stream, dpre,
+                       static_cast<const T*>(x), static_cast<T*>(dw), max_jchunks, a);
   int rc = check_launch("me_bwd_dw_kernel");
   if (rc != PMSST_OK) return rc;
   return launch_colsum_rows(dpre, dtype_code<T>(), M, 2 * static_cast<int64_t>(hm.F), partial, dbias,
