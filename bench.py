@@ -113,7 +113,8 @@ class Workload:
             state["bs"] = e.band_split_ragged_forward_packed(w.x, w.gamma_bs, w.w_bs, w.b_bs, w.dims, write_normed=False)
 
         def bs_bwd():
-            e.band_split_ragged_backward_packed(w.g_bs, w.x, True, state["bs"][2], w.gamma_bs, w.w_bs, w.dims, True)
+            e.band_split_ragged_backward_packed(w.g_bs, w.x, True, state["bs"][2], w.gamma_bs, w.w_bs, w.dims, True,
+                                                out=state["bs"][0].reshape(w.M, -1), bias_all=w.b_bs)
 
         def qk_fwd():
             state["q"] = e.rms_norm_rotary_forward(w.q, w.gamma_q, w.cos, w.sin)
@@ -142,7 +143,9 @@ class Workload:
             # read x, gamma, W, bias; write out, inv
             "band_split_fwd": (M * F * s + F * s + F * O * s + NB * O * s + M * NB * O * s + 4 * M * NB,
                                2 * M * F * O),
-            # read dy, x, inv, gamma, W; write dx, dgamma, dW, dbias
+            # algorithmic (the op's own inputs and outputs): read dy, x, inv, gamma, W; write dx, dgamma,
+            # dW, dbias.  The kernels also read the forward output for the per-row dots; that read is
+            # this implementation's choice and is not counted.
             "band_split_bwd": (M * NB * O * s + 2 * M * F * s + 4 * M * NB + 2 * F * s + 2 * F * O * s + NB * O * s,
                                4 * M * F * O),
             # per tensor: read x, write out, write inv (x2 tensors)

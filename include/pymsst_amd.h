@@ -147,12 +147,16 @@ size_t pmsst_band_split_ragged_backward_workspace_size(int64_t rows, int64_t tot
  * implements band_split_backward / _v2 / _v3 (fused_band_split.cpp:172-269, .cu:125-587).
  * `saved` is normed[rows, F] (saved_is_input = 0) or the forward input x[rows, F] (saved_is_input = 1,
  * normed recomputed as x * inv_norm * sqrt(I_b)).  Outputs: grad_x[rows, F], grad_gamma[F],
- * grad_weight (packed like weight), grad_bias[NB, O] or NULL. */
+ * grad_weight (packed like weight), grad_bias[NB, O] or NULL.
+ * `out` (the forward output [rows, NB, O]) and `bias` (the forward bias or NULL) are optional: with
+ * `out` the per-row dots of the normalisation backward come from sum_o grad_out * (out - bias)
+ * (= sum_i gs gamma n) and every 64-wide input chunk of every band is an independent block;
+ * with out = NULL each (rows, band) block makes two passes over its band (the reference's form). */
 int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, int saved_is_input,
-                                     const float* inv_norm, const void* gamma, const void* weight,
-                                     const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
-                                     int64_t rows, int64_t out_features, void* grad_x, void* grad_gamma,
-                                     void* grad_weight, void* grad_bias, int dtype, void* workspace,
+                                     const float* inv_norm, const void* gamma, const void* weight, const void* out,
+                                     const void* bias, const int64_t* dim_offsets, const int64_t* dim_inputs,
+                                     int64_t band_count, int64_t rows, int64_t out_features, void* grad_x,
+                                     void* grad_gamma, void* grad_weight, void* grad_bias, int dtype, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ grouped linear

@@ -195,26 +195,69 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
 
 // ------------------------------------------------------------------ backward: dx + dgamma partials
 
-// NORM = false: plain grouped linear, dx = dy W_b in one pass (nsrc, inv_norm, gamma and
-// dg_partial unused).
-template <typename T, bool FROM_X, bool NORM, bool V4>
+// Per-row dots of the band-split backward from the forward output:
+//   dot[m][b] = sum_i gs[m][i] gamma_i n[m][i] = sum_o dy[m][b][o] (out[m][b][o] - bias[b][o]),
+// since out - bias = (n * gamma) W_b^T.  One 32-lane group per (m, b) row.
+template <typename T, bool V4>
+__global__ __launch_bounds__(256) void bs_dots_kernel(const T* __restrict__ dy, const T* __restrict__ out,
+                                                      const T* __restrict__ bias, float* __restrict__ dots,
+                                                      int64_t rows, int NB, int O) {
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / 32;
+  const int l = threadIdx.x & 31;
+  float acc = 0.f;
+  if (row < rows) {
+    const int b = static_cast<int>(row % NB);
+    const T* pd = dy + row * O;
+    const T* po = out + row * O;
+    const T* pb = bias != nullptr ? bias + static_cast<int64_t>(b) * O : nullptr;
+    if (V4) {
+      for (int q = l * 4; q < O; q += 128) {
+        float d[4], o[4], c[4] = {0.f, 0.f, 0.f, 0.f};
+        load_pack<T, 4>(pd + q, d);
+        load_pack<T, 4>(po + q, o);
+        if (pb != nullptr) load_pack<T, 4>(pb + q, c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc += d[j] * (o[j] - c[j]);
+      }
+    } else {
+      for (int q = l; q < O; q += 32) acc += to_f32(pd[q]) * (to_f32(po[q]) - (pb != nullptr ? to_f32(pb[q]) : 0.f));
+    }
+  }
+  acc = group_sum(acc, 32);
+  if (l == 0 && row < rows) dots[row] = acc;
+}
+
+// dx for one (64-row tile, band) block, or one (64-row tile, band, 64-wide input chunk)
+// block when SPLIT.  gs^T[i][m] = W_b^T dy^T per 64-wide input chunk (K = O), then
+//   NORM:  dx = inv (gs gamma sqrt(I) - n dot / sqrt(I)), dgamma partials sum_m gs n;
+//   !NORM: dx = gs (plain grouped linear; nsrc, inv_norm, gamma, dg_partial unused).
+// With NORM and !SPLIT the block makes two passes over the band (dots, then dx); with
+// NORM and SPLIT the per-row dots come precomputed (`dots`, from bs_dots_kernel) and
+// every block makes one pass over its chunk.
+template <typename T, bool FROM_X, bool NORM, bool SPLIT, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __restrict__ dy,
                                                                  const T* __restrict__ nsrc,
                                                                  const float* __restrict__ inv_norm,
                                                                  const T* __restrict__ gamma,
                                                                  const T* __restrict__ weight, T* __restrict__ dx,
-                                                                 float* __restrict__ dg_partial, BandArgs a) {
+                                                                 float* __restrict__ dg_partial,
+                                                                 const float* __restrict__ dots, int max_ichunks,
+                                                                 BandArgs a) {
   constexpr int kBI = 64;
+  constexpr int kPasses = (NORM && !SPLIT) ? 2 : 1;
   __shared__ T lds[gemm_lds_elems<T, kBI, kBM>()];
   __shared__ float sinv[kBM];
   __shared__ float sdot[4][kBM];
   using S = TileShape<kBI, kBM, 4, 1>;  // TR = 1, TC = 4
 
   const int O = a.O;
-  const int band = blockIdx.y;
+  const int band = SPLIT ? static_cast<int>(blockIdx.y) / max_ichunks : static_cast<int>(blockIdx.y);
   const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBM;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  const int i_begin = SPLIT ? (static_cast<int>(blockIdx.y) % max_ichunks) * kBI : 0;
+  if (i_begin >= I) return;  // uniform over the block
+  const int i_end = SPLIT ? (i_begin + kBI < I ? i_begin + kBI : I) : I;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rows_valid = static_cast<int>(a.M - m0 < kBM ? a.M - m0 : kBM);
   const T* wb = weight + static_cast<int64_t>(O) * off;  // [O][I]
@@ -222,13 +265,16 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
   const float root = sqrtf(static_cast<float>(I));
 
   if (NORM) {
-    if (tid < kBM) sinv[tid] = tid < rows_valid ? inv_norm[(m0 + tid) * a.NB + band] : 0.f;
+    if (tid < kBM) {
+      sinv[tid] = tid < rows_valid ? inv_norm[(m0 + tid) * a.NB + band] : 0.f;
+      if (SPLIT) sdot[0][tid] = tid < rows_valid ? dots[(m0 + tid) * a.NB + band] : 0.f;
+    }
     __syncthreads();
   }
 
   float dotp[4] = {0.f, 0.f, 0.f, 0.f};  // per m-tile j: m = 16 j + (lane & 15)
-  for (int pass = 0; pass < (NORM ? 2 : 1); ++pass) {
-    if (pass == 1) {
+  for (int pass = 0; pass < kPasses; ++pass) {
+    if (NORM && !SPLIT && pass == 1) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float v = dotp[j];
@@ -240,7 +286,11 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
       if (tid < kBM) sdot[0][tid] = sdot[0][tid] + sdot[1][tid] + sdot[2][tid] + sdot[3][tid];
       __syncthreads();
     }
-    for (int i0 = 0; i0 < I; i0 += kBI) {
+    // dot partials are gathered in pass 0 of the two-pass form; dx is written in the last pass;
+    // dgamma partials in pass 0 of every NORM form
+    const bool gather_dot = NORM && !SPLIT && pass == 0;
+    const bool write_dx = pass == kPasses - 1;
+    for (int i0 = i_begin; i0 < i_end; i0 += kBI) {
       // A[i][o] = W_b[o][i0 + i] (MN-contiguous in i);  B[m][o] = dy[m0 + m][band][o]
       MNLoader<T, kBI> la{wb + i0, I, I - i0, O, V4};
       KRowLoader<T, kBM> lb{dyb, static_cast<int64_t>(a.NB) * O, rows_valid, O, V4};
@@ -290,15 +340,16 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
         if (pass == 0) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            dotp[j] += acc[0][j][r] * g[r] * n[r];
+            if (gather_dot) dotp[j] += acc[0][j][r] * g[r] * n[r];
             dgp[r] += acc[0][j][r] * n[r];
           }
-        } else {
+        }
+        if (write_dx) {
           const float inv = sinv[m];
-          const float dots = sdot[0][m] / root;
+          const float dots_m = sdot[0][m] / root;
           float o[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = inv * (acc[0][j][r] * g[r] * root - n[r] * dots);
+          for (int r = 0; r < 4; ++r) o[r] = inv * (acc[0][j][r] * g[r] * root - n[r] * dots_m);
           T* dp = dx + (m0 + m) * a.F + off + il;
           if (a.vec4) {
             store_pack<T, 4>(dp, o);
@@ -481,14 +532,18 @@ size_t dg_partial_bytes(int64_t M, int F) {
   return align_up(static_cast<size_t>((M + kBM - 1) / kBM) * static_cast<size_t>(F) * sizeof(float), 256);
 }
 
+size_t dots_bytes(int64_t M, int NB) { return align_up(static_cast<size_t>(M) * NB * sizeof(float), 256); }
+
+// [dgamma partials | dots | dbias partials]
 size_t bwd_workspace(int64_t M, int F, int NB, int O) {
-  return dg_partial_bytes(M, F) + colsum_rows_workspace(M, static_cast<int64_t>(NB) * O);
+  return dg_partial_bytes(M, F) + dots_bytes(M, NB) + colsum_rows_workspace(M, static_cast<int64_t>(NB) * O);
 }
 
 template <typename T>
 int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_norm, const void* gamma,
-               const void* weight, const int64_t* offsets, const HostBands& hb, int64_t M, int64_t O, void* dx,
-               void* dgamma, void* dw, void* db, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+               const void* weight, const void* out, const void* bias, const int64_t* offsets, const HostBands& hb,
+               int64_t M, int64_t O, void* dx, void* dgamma, void* dw, void* db, void* workspace,
+               size_t workspace_bytes, hipStream_t stream) {
   const char* op = "band_split_ragged_backward";
   PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
   PMSST_REQUIRE(O >= 1 && O <= 512, "%s: out_features must be in [1, 512] (got %lld)", op, (long long)O);
@@ -507,18 +562,42 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   const T* pg = static_cast<const T*>(gamma);
   const T* pw = static_cast<const T*>(weight);
   float* partial = static_cast<float*>(workspace);
-  float* db_partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + dg_partial_bytes(M, hb.F));
+  float* dots = reinterpret_cast<float*>(static_cast<char*>(workspace) + dg_partial_bytes(M, hb.F));
+  float* db_partial = reinterpret_cast<float*>(reinterpret_cast<char*>(dots) + dots_bytes(M, hb.NB));
   const int m_tiles = static_cast<int>((M + kBM - 1) / kBM);
   if (M > 0) {
-    const dim3 grid(static_cast<unsigned>(m_tiles), static_cast<unsigned>(hb.NB));
     const bool v4 = a.vec4 && a.ovec4;
-#define PMSST_BDX(FX, V4)                                                                                   \
-  hipLaunchKernelGGL((bs_bwd_dx_kernel<T, FX, true, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, \
-                     pg, pw, static_cast<T*>(dx), partial, a)
-    if (from_x) {
-      if (v4) PMSST_BDX(true, true); else PMSST_BDX(true, false);
+    const bool split = out != nullptr;  // dots from the forward output: one pass per 64-wide chunk
+    const int max_ichunks = (hb.max_width + 63) / 64;
+    if (split) {
+      const bool dv4 = a.ovec4 && aligned_to(out, 4 * sizeof(T)) && aligned_to(bias, 4 * sizeof(T));
+      const int64_t rows = M * hb.NB;
+      const dim3 gd(static_cast<unsigned>((rows * 32 + 255) / 256));
+      if (dv4)
+        hipLaunchKernelGGL((bs_dots_kernel<T, true>), gd, dim3(256), 0, stream, pdy, static_cast<const T*>(out),
+                           static_cast<const T*>(bias), dots, rows, hb.NB, static_cast<int>(O));
+      else
+        hipLaunchKernelGGL((bs_dots_kernel<T, false>), gd, dim3(256), 0, stream, pdy, static_cast<const T*>(out),
+                           static_cast<const T*>(bias), dots, rows, hb.NB, static_cast<int>(O));
+      int rc = check_launch("bs_dots_kernel");
+      if (rc != PMSST_OK) return rc;
+    }
+    const dim3 grid(static_cast<unsigned>(m_tiles), static_cast<unsigned>(hb.NB * (split ? max_ichunks : 1)));
+#define PMSST_BDX(FX, SPLIT, V4)                                                                               \
+  hipLaunchKernelGGL((bs_bwd_dx_kernel<T, FX, true, SPLIT, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, \
+                     inv_norm, pg, pw, static_cast<T*>(dx), partial, dots, max_ichunks, a)
+    if (split) {
+      if (from_x) {
+        if (v4) PMSST_BDX(true, true, true); else PMSST_BDX(true, true, false);
+      } else {
+        if (v4) PMSST_BDX(false, true, true); else PMSST_BDX(false, true, false);
+      }
     } else {
-      if (v4) PMSST_BDX(false, true); else PMSST_BDX(false, false);
+      if (from_x) {
+        if (v4) PMSST_BDX(true, false, true); else PMSST_BDX(true, false, false);
+      } else {
+        if (v4) PMSST_BDX(false, false, true); else PMSST_BDX(false, false, false);
+      }
     }
 #undef PMSST_BDX
     int rc = check_launch("bs_bwd_dx_kernel");
@@ -567,13 +646,14 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
   const T* px = static_cast<const T*>(x);
   const T* pw = static_cast<const T*>(weight);
   if (M > 0) {
-    const dim3 grid(static_cast<unsigned>((M + kBM - 1) / kBM), static_cast<unsigned>(hb.NB));
+    const int max_ichunks = (hb.max_width + 63) / 64;
+    const dim3 grid(static_cast<unsigned>((M + kBM - 1) / kBM), static_cast<unsigned>(hb.NB * max_ichunks));
     if (a.vec4 && a.ovec4)
-      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
-                         nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, a);
+      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true, true>), grid, dim3(kGemmThreads), 0, stream, pdy,
+                         px, nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, max_ichunks, a);
     else
-      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
-                         nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, a);
+      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true, false>), grid, dim3(kGemmThreads), 0, stream, pdy,
+                         px, nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, max_ichunks, a);
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
@@ -669,8 +749,9 @@ size_t pmsst_band_split_ragged_backward_workspace_size(int64_t rows, int64_t tot
 }
 
 int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, int saved_is_input,
-                                     const float* inv_norm, const void* gamma, const void* weight,
-                                     const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
+                                     const float* inv_norm, const void* gamma, const void* weight, const void* out,
+                                     const void* bias, const int64_t* dim_offsets, const int64_t* dim_inputs,
+                                     int64_t band_count,
                                      int64_t rows, int64_t out_features, void* grad_x, void* grad_gamma,
                                      void* grad_weight, void* grad_bias, int dtype, void* workspace,
                                      size_t workspace_bytes, void* stream) {
@@ -679,8 +760,8 @@ int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, in
   if (rc != PMSST_OK) return rc;
   return with_dtype(dtype, "band_split_ragged_backward", [&](auto tag) {
     using T = decltype(tag);
-    return launch_bwd<T>(grad_out, saved, saved_is_input != 0, inv_norm, gamma, weight, dim_offsets, hb, rows,
-                         out_features, grad_x, grad_gamma, grad_weight, grad_bias, workspace, workspace_bytes,
+    return launch_bwd<T>(grad_out, saved, saved_is_input != 0, inv_norm, gamma, weight, out, bias, dim_offsets, hb,
+                         rows, out_features, grad_x, grad_gamma, grad_weight, grad_bias, workspace, workspace_bytes,
                          static_cast<hipStream_t>(stream));
   });
 }

@@ -2,8 +2,8 @@
 //
 // A block computes C[BR x BC] += A[BR x K] * B[BC x K]^T with both operands
 // staged in LDS as [rows][pitch] (K contiguous) in chunks of 32.  Two LDS
-// buffers and a register copy of the next chunk overlap the global loads of
-// chunk k+1 with the MFMAs of chunk k; one barrier per chunk.
+// buffers and one or two register copies keep the global loads of the next one
+// or two chunks in flight during the MFMAs of chunk k; one barrier per chunk.
 //
 // LDS layout (16-bit types): row r, element k of a chunk lives at
 //   r * pitch + 8 * ((k / 8) ^ ((r / 16) % 4)) + k % 8,
@@ -270,10 +270,19 @@ constexpr int gemm_lds_elems() {
 }
 
 // Runs the K loop; `acc` is accumulated (callers zero it).
-template <typename T, int BR, int BC, int WR, int WC, class LA, class LB>
+//
+// DEPTH = 1: chunk c + 1 is fetched into registers while chunk c is multiplied and
+// committed to the other LDS buffer afterwards.  DEPTH = 2: chunk c is fetched into
+// register set R[c % 2] two iterations ahead, so two chunks of global loads are in
+// flight during the MFMAs of a third, at the cost of a second register set (the
+// loop is unrolled by two so the sets stay fixed registers).  Buffer offsets are
+// computed from the __shared__ base (no pointer tables), so every LDS access stays
+// a ds_* instruction and waits only on the LDS counter.
+template <typename T, int BR, int BC, int WR, int WC, int DEPTH = 1, class LA, class LB>
 __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K, T* lds,
                                               f32x4_t (&acc)[TileShape<BR, BC, WR, WC>::kTR]
                                                             [TileShape<BR, BC, WR, WC>::kTC]) {
+  static_assert(DEPTH == 1 || DEPTH == 2, "prefetch depth 1 or 2");
   using S = TileShape<BR, BC, WR, WC>;
   constexpr int P = LdsPitch<T>::value;
   constexpr int kBuf = (BR + BC) * P;  // elements of one (A, B) buffer pair
@@ -283,23 +292,8 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
   const int c0 = (wave % WC) * (BC / WC);
   const int nk = (K + kChunkK - 1) / kChunkK;
   if (nk == 0) return;
-  typename LA::Regs ra;
-  typename LB::Regs rb;
-  la.fetch(0, ra);
-  lb.fetch(0, rb);
-  la.commit(ra, lds);
-  lb.commit(rb, lds + BR * P);
-  __syncthreads();
-  for (int kc = 0; kc < nk; ++kc) {
-    // buffer offsets computed from the __shared__ base (no pointer tables), so every
-    // access stays a ds_* instruction and waits only on the LDS counter
-    const int cur = (kc & 1) * kBuf;
-    const int nxt = kBuf - cur;
-    const bool more = kc + 1 < nk;
-    if (more) {
-      la.fetch((kc + 1) * kChunkK, ra);
-      lb.fetch((kc + 1) * kChunkK, rb);
-    }
+
+  auto mma = [&](int cur) {
 #pragma unroll
     for (int i = 0; i < S::kTR; ++i) {
 #pragma unroll
@@ -308,11 +302,60 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
                                  acc[i][j], lane);
       }
     }
-    if (more) {
-      la.commit(ra, lds + nxt);
-      lb.commit(rb, lds + nxt + BR * P);
-    }
+  };
+
+  typename LA::Regs ra0;
+  typename LB::Regs rb0;
+  la.fetch(0, ra0);
+  lb.fetch(0, rb0);
+  if constexpr (DEPTH == 1) {
+    la.commit(ra0, lds);
+    lb.commit(rb0, lds + BR * P);
     __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+      const int cur = (kc & 1) * kBuf;
+      const bool more = kc + 1 < nk;
+      if (more) {
+        la.fetch((kc + 1) * kChunkK, ra0);
+        lb.fetch((kc + 1) * kChunkK, rb0);
+      }
+      mma(cur);
+      if (more) {
+        la.commit(ra0, lds + kBuf - cur);
+        lb.commit(rb0, lds + kBuf - cur + BR * P);
+      }
+      __syncthreads();
+    }
+  } else {
+    typename LA::Regs ra1;
+    typename LB::Regs rb1;
+    if (nk > 1) {
+      la.fetch(kChunkK, ra1);
+      lb.fetch(kChunkK, rb1);
+    }
+    la.commit(ra0, lds);
+    lb.commit(rb0, lds + BR * P);
+    __syncthreads();
+    // `rc` held chunk kc (already in LDS) and is refilled with kc + 2; `rn` holds
+    // chunk kc + 1 and is committed after the MFMAs of chunk kc.
+    auto step = [&](int kc, typename LA::Regs& rca, typename LB::Regs& rcb, typename LA::Regs& rna,
+                    typename LB::Regs& rnb) {
+      const int cur = (kc & 1) * kBuf;
+      if (kc + 2 < nk) {
+        la.fetch((kc + 2) * kChunkK, rca);
+        lb.fetch((kc + 2) * kChunkK, rcb);
+      }
+      mma(cur);
+      if (kc + 1 < nk) {
+        la.commit(rna, lds + kBuf - cur);
+        lb.commit(rnb, lds + kBuf - cur + BR * P);
+      }
+      __syncthreads();
+    };
+    for (int kc = 0; kc < nk; kc += 2) {
+      step(kc, ra0, rb0, ra1, rb1);
+      if (kc + 1 < nk) step(kc + 1, ra1, rb1, ra0, rb0);
+    }
   }
 }
 

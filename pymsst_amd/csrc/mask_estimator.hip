@@ -98,7 +98,7 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_kernel(const T* __restric
   for (int i = 0; i < S::kTR; ++i)
 #pragma unroll
     for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  gemm_mainloop<T, 128, kFwdBM, 1, 4>(la, lb, H, lds, acc);
+  gemm_mainloop<T, 128, kFwdBM, 1, 4, 2>(la, lb, H, lds, acc);
 
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
 #pragma unroll

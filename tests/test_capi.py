@@ -41,7 +41,8 @@ def test_abi_version_and_error_string(lib):
 def test_workspace_queries(lib):
     assert lib.pmsst_rms_norm_backward_workspace_size(1000, 192) == 512 * 192 * 4
     dg = -(-17 * 4100 * 4 // 256) * 256
-    assert lib.pmsst_band_split_ragged_backward_workspace_size(1032, 4100, 62, 192) == dg + 17 * 62 * 192 * 4
+    dots = -(-1032 * 62 * 4 // 256) * 256
+    assert lib.pmsst_band_split_ragged_backward_workspace_size(1032, 4100, 62, 192) == dg + dots + 17 * 62 * 192 * 4
     assert lib.pmsst_mask_estimator_final_backward_workspace_size(1032, 4100, 2) >= 1032 * 8200 * 2
 
 

@@ -115,6 +115,35 @@ def test_saved_input_backward(hip_ext, dtype):
     assert_parity(db, np.concatenate(r_db), dn, "dbias")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dims,m,o,has_bias", [((3, 5, 2, 7), 5, 4, True), (BSR_WIDTHS, 1032, 192, True),
+                                               (BSR_WIDTHS, 130, 64, False), ((12, 520, 36), 77, 100, True)])
+def test_backward_from_output(hip_ext, dtype, dims, m, o, has_bias):
+    """Backward with the per-row dots taken from the forward output (sum_o dy * (out - bias)) and one
+    block per 64-wide input chunk, from the saved input and from normed; against the oracle."""
+    dn = dt_name(dtype)
+    g = torch.Generator().manual_seed(31)
+    x = (0.05 * torch.randn(m, sum(dims), generator=g)).to(dtype).cuda()
+    gammas, weights, biases = _params(dims, o, dtype, 32)
+    ga = torch.cat(gammas)
+    wa = torch.cat([w.reshape(-1) for w in weights])
+    ba = torch.cat(biases) if has_bias else None
+    out, normed, inv = hip_ext.band_split_ragged_forward_packed(x, ga, wa, ba, dims, write_normed=True)
+    dy = torch.randn(out.shape, generator=g).to(dtype).cuda()
+    r_dx, r_dg, r_dw, r_db = oracle.band_split_ragged_backward_lean(
+        to_np(dy), to_np(x), to_np(inv), [to_np(v) for v in gammas], [to_np(v) for v in weights], dims, dn
+    )
+    for saved, is_input in ((x, True), (normed, False)):
+        dx, dg, dw, db = hip_ext.band_split_ragged_backward_packed(dy, saved, is_input, inv, ga, wa, dims, has_bias,
+                                                                   out=out.reshape(m, -1), bias_all=ba)
+        tag = "x" if is_input else "normed"
+        assert_parity(dx, r_dx, dn, f"dx from {tag}")
+        assert_parity(dg, np.concatenate(r_dg), dn, f"dgamma from {tag}")
+        assert_parity(dw, np.concatenate([w.reshape(-1) for w in r_dw]), dn, f"dW from {tag}")
+        if has_bias:
+            assert_parity(db, np.concatenate(r_db), dn, f"dbias from {tag}")
+
+
 @pytest.mark.parametrize("has_bias", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_group_view(hip_ext, has_bias, dtype):
