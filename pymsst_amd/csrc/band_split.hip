@@ -383,7 +383,7 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
                                                                  const T* __restrict__ nsrc,
                                                                  const float* __restrict__ inv_norm,
                                                                  const T* __restrict__ gamma, T* __restrict__ dw,
-                                                                 int max_itiles, BandArgs a) {
+                                                                 T* __restrict__ db, int max_itiles, BandArgs a) {
   __shared__ T lds[gemm_lds_elems<T, kDwBI, kDwBO>()];
   using S = TileShape<kDwBI, kDwBO, 2, 2>;
   const int O = a.O;
@@ -409,12 +409,15 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
   }
   MNLoader<T, kDwBO> lb{dy + static_cast<int64_t>(band) * O + o0, static_cast<int64_t>(a.NB) * O, O - o0,
                         static_cast<int>(a.M), V4};
+  // the first input tile of each (band, output tile) also sums dy over the rows: dbias
+  lb.colsum = db != nullptr && i0 == 0;
   f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
   for (int i = 0; i < S::kTR; ++i)
 #pragma unroll
     for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   gemm_mainloop<T, kDwBI, kDwBO, 2, 2>(la, lb, static_cast<int>(a.M), lds, acc);
+  if (lb.colsum) reduce_colsum<T, kDwBO>(lb, lds, db + static_cast<int64_t>(band) * O + o0);
 
   T* dwb = dw + static_cast<int64_t>(O) * off;  // [O][I]
   const int ir = (wave >> 1) * (kDwBI / 2), oc = (wave & 1) * (kDwBO / 2);
@@ -609,7 +612,7 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
     const bool v4 = a.vec4 && a.ovec4;
 #define PMSST_BDW(FX, V4)                                                                                   \
   hipLaunchKernelGGL((bs_bwd_dw_kernel<T, FX, true, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, \
-                     pg, static_cast<T*>(dw), max_itiles, a)
+                     pg, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, a)
     if (from_x) {
       if (v4) PMSST_BDW(true, true); else PMSST_BDW(true, false);
     } else {
@@ -619,10 +622,9 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
     int rc = check_launch("bs_bwd_dw_kernel");
     if (rc != PMSST_OK) return rc;
   }
-  int rc = launch_col_sum(partial, m_tiles, hb.F, dgamma, dtype_code<T>(), stream);
-  if (rc != PMSST_OK || db == nullptr) return rc;
-  return launch_colsum_rows(dy, dtype_code<T>(), M, static_cast<int64_t>(hb.NB) * O, db_partial, db, dtype_code<T>(),
-                            stream);
+  // dbias was summed by the dW kernel (which also runs for M == 0 and then writes zeros)
+  (void)db_partial;
+  return launch_col_sum(partial, m_tiles, hb.F, dgamma, dtype_code<T>(), stream);
 }
 
 // Grouped linear backward: the norm-free dx / dW kernels plus the bias column sums.
@@ -662,16 +664,17 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
     const dim3 grid(static_cast<unsigned>((O + kDwBO - 1) / kDwBO), static_cast<unsigned>(hb.NB * max_itiles));
     if (a.vec4 && a.ovec4)
       hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
-                         nullptr, nullptr, static_cast<T*>(dw), max_itiles, a);
+                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, a);
     else
       hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
-                         nullptr, nullptr, static_cast<T*>(dw), max_itiles, a);
+                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, a);
     int rc = check_launch("bs_bwd_dw_kernel");
     if (rc != PMSST_OK) return rc;
   }
-  if (db == nullptr) return PMSST_OK;
-  return launch_colsum_rows(dy, dtype_code<T>(), M, static_cast<int64_t>(hb.NB) * O, static_cast<float*>(workspace),
-                            db, dtype_code<T>(), stream);
+  // dbias was summed by the dW kernel (which also runs for M == 0 and then writes zeros)
+  (void)workspace;
+  (void)workspace_bytes;
+  return PMSST_OK;
 }
 
 template <typename F>

@@ -210,6 +210,10 @@ struct MNLoader {
   float rs_mul = 1.f;
   // per-mn scale of this thread's quad (loaded once; cs does not depend on k)
   float c[4] = {1.f, 1.f, 1.f, 1.f};
+  // with `colsum` set, commit() also accumulates the unscaled values of the thread's mn
+  // quad over its k rows (column sums over K, e.g. a bias gradient); see reduce_colsum()
+  bool colsum = false;
+  mutable float csum[4] = {0.f, 0.f, 0.f, 0.f};
 
   __device__ __forceinline__ void init() {
     if (cs != nullptr) {
@@ -236,6 +240,10 @@ struct MNLoader {
 #pragma unroll
     for (int t = 0; t < KB; ++t) {
       quad_to_f32<T>(mask_quad<T>(g.q[t], (g.ok >> t) & 1), v[t]);
+      if (colsum) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) csum[j] += v[t][j];
+      }
       const float st = rs != nullptr ? g.s[t] * rs_mul : 1.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[t][j] *= st * c[j];
@@ -254,6 +262,27 @@ struct MNLoader {
     }
   }
 };
+
+// Column sums gathered by a `colsum` MNLoader: the 256 threads hold partial sums of
+// 4 consecutive mn each (thread t: mn = 4 (t % ROWS/4)); they are combined in a fixed
+// order through LDS and written as dst[mn] for mn < mn_valid.  Call after the main loop
+// (which ends with a barrier), with every thread of the block.
+template <typename T, int ROWS>
+__device__ __forceinline__ void reduce_colsum(const MNLoader<T, ROWS>& ld, T* lds, T* __restrict__ dst) {
+  constexpr int kQ = ROWS / 4;                  // mn quads
+  constexpr int kGroups = kGemmThreads / kQ;    // threads per quad
+  float* red = reinterpret_cast<float*>(lds);   // [kGroups][ROWS]
+  const int q = threadIdx.x % kQ, grp = threadIdx.x / kQ;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) red[grp * ROWS + 4 * q + j] = ld.csum[j];
+  __syncthreads();
+  if (threadIdx.x < ROWS && static_cast<int>(threadIdx.x) < ld.mn_valid) {
+    float s = 0.f;
+#pragma unroll 4
+    for (int g2 = 0; g2 < kGroups; ++g2) s += red[g2 * ROWS + threadIdx.x];
+    dst[threadIdx.x] = from_f32<T>(s);
+  }
+}
 
 template <int BR, int BC, int WR, int WC>
 struct TileShape {

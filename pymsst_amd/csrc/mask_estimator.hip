@@ -143,6 +143,59 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_kernel(const T* __restric
 // ------------------------------------------------------------------ backward
 
 constexpr int kDpreRows = 64;
+constexpr int kDpreFlatRows = 8;
+constexpr int kDpreFlatMaxBands = 4096;
+constexpr int kDpreFlatMaxQuads = 16384;  // LDS table <= 48 KB per block
+
+// dpre over whole rows (aligned case): block = kDpreFlatRows rows x all F/4 column quads, so
+// every band's columns are spread evenly over the threads whatever the band widths.  The
+// block first builds a quad -> band table in LDS (band offsets are multiples of 4, so a quad
+// lies in one band); consecutive threads then take consecutive quads of a row (coalesced).
+template <typename T>
+__global__ __launch_bounds__(256) void me_dpre_flat_kernel(const T* __restrict__ gout, const T* __restrict__ pre,
+                                                           T* __restrict__ dpre, MaskArgs a) {
+  extern __shared__ int smem[];
+  int* soff = smem;                                                   // [NB + 1]
+  uint16_t* sband = reinterpret_cast<uint16_t*>(smem + a.NB + 1);    // [F / 4]
+  const int nq = a.F / 4;
+  for (int b = threadIdx.x; b <= a.NB; b += 256) soff[b] = static_cast<int>(a.offsets[b]);
+  __syncthreads();
+  for (int q = threadIdx.x; q < nq; q += 256) {
+    int lo = 0, hi = a.NB - 1;  // last band with soff[b] <= 4q
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (soff[mid] <= 4 * q) lo = mid; else hi = mid - 1;
+    }
+    sband[q] = static_cast<uint16_t>(lo);
+  }
+  __syncthreads();
+  const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kDpreFlatRows;
+  for (int rr = 0; rr < kDpreFlatRows; ++rr) {
+    const int64_t m = r0 + rr;
+    if (m >= a.M) break;
+    for (int q = threadIdx.x; q < nq; q += 256) {
+      const int b = sband[q];
+      const int off = soff[b];
+      const int I = soff[b + 1] - off;
+      const int l = 4 * q - off;
+      const T* pl = pre + m * pitch2 + 2 * off + l;
+      float g[4], L[4], G[4], ol[4], og[4];
+      load_pack<T, 4>(gout + m * a.F + 4 * q, g);
+      load_pack<T, 4>(pl, L);
+      load_pack<T, 4>(pl + I, G);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float sg = sigmoidf_(G[j]);
+        ol[j] = g[j] * sg;
+        og[j] = g[j] * L[j] * sg * (1.0f - sg);
+      }
+      T* dl = dpre + m * pitch2 + 2 * off + l;
+      store_pack<T, 4>(dl, ol);
+      store_pack<T, 4>(dl + I, og);
+    }
+  }
+}
 
 // dpre for rows [blockIdx.x * 64, +64) of band blockIdx.y, 4 outputs per item.
 template <typename T>
@@ -264,7 +317,8 @@ constexpr int kDwBJ = 64;
 
 template <typename T, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __restrict__ dpre, const T* __restrict__ x,
-                                                                 T* __restrict__ dw, int max_jchunks, MaskArgs a) {
+                                                                 T* __restrict__ dw, T* __restrict__ dbias,
+                                                                 int max_jchunks, MaskArgs a) {
   __shared__ T lds[gemm_lds_elems<T, kDwBH, kDwBJ>()];
   using S = TileShape<kDwBH, kDwBJ, 2, 2>;
   const int h0 = blockIdx.x * kDwBH;
@@ -282,12 +336,15 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __rest
   MNLoader<T, kDwBH> la{x + static_cast<int64_t>(band) * H + h0, static_cast<int64_t>(a.NB) * H, H - h0,
                         static_cast<int>(a.M), V4};
   MNLoader<T, kDwBJ> lb{dpre + 2 * off + j0, pitch2, K2 - j0, static_cast<int>(a.M), V4};
+  // the first hidden tile of each (band, j chunk) also sums dpre over the rows: dbias
+  lb.colsum = h0 == 0;
   f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
   for (int i = 0; i < S::kTR; ++i)
 #pragma unroll
     for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   gemm_mainloop<T, kDwBH, kDwBJ, 2, 2>(la, lb, static_cast<int>(a.M), lds, acc);
+  if (lb.colsum) reduce_colsum<T, kDwBJ>(lb, lds, dbias + 2 * off + j0);
 
   T* dwb = dw + static_cast<int64_t>(2) * off * H;  // [2I][H]
   const int hr = (wave >> 1) * (kDwBH / 2), jc = (wave & 1) * (kDwBJ / 2);
@@ -388,6 +445,11 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
                                             align_up(static_cast<size_t>(M) * 2 * hm.F * sizeof(T), 256));
   if (M > 0) {
     const dim3 g1(static_cast<unsigned>((M + kDpreRows - 1) / kDpreRows), static_cast<unsigned>(hm.NB));
+    if (a.vec4 && hm.NB < kDpreFlatMaxBands && hm.F / 4 <= kDpreFlatMaxQuads) {
+      const size_t shm = static_cast<size_t>(hm.NB + 1) * sizeof(int) + static_cast<size_t>(hm.F / 4) * 2;
+      hipLaunchKernelGGL((me_dpre_flat_kernel<T>), dim3(static_cast<unsigned>((M + kDpreFlatRows - 1) / kDpreFlatRows)),
+                         dim3(256), shm, stream, static_cast<const T*>(gout), static_cast<const T*>(pre), dpre, a);
+    } else
     hipLaunchKernelGGL((me_dpre_kernel<T>), g1, dim3(256), 0, stream, static_cast<const T*>(gout),
                        static_cast<const T*>(pre), dpre, a);
     int rc = check_launch("me_dpre_kernel");
@@ -410,14 +472,15 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
   const dim3 g3(static_cast<unsigned>((H + kDwBH - 1) / kDwBH), static_cast<unsigned>(hm.NB * max_jchunks));
   if (a.vec4)
     hipLaunchKernelGGL((me_bwd_dw_kernel<T, true>), g3, dim3(kGemmThreads), 0, stream, dpre, static_cast<const T*>(x),
-                       static_cast<T*>(dw), max_jchunks, a);
+                       static_cast<T*>(dw), static_cast<T*>(dbias), max_jchunks, a);
   else
     hipLaunchKernelGGL((me_bwd_dw_kernel<T, false>), g3, dim3(kGemmThreads), 0, stream, dpre,
-                       static_cast<const T*>(x), static_cast<T*>(dw), max_jchunks, a);
+                       static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(dbias), max_jchunks, a);
   int rc = check_launch("me_bwd_dw_kernel");
   if (rc != PMSST_OK) return rc;
-  return launch_colsum_rows(dpre, dtype_code<T>(), M, 2 * static_cast<int64_t>(hm.F), partial, dbias,
-                            dtype_code<T>(), stream);
+  // dbias was summed by the dW kernel (which also runs for M == 0 and then writes zeros)
+  (void)partial;
+  return PMSST_OK;
 }
 
 template <typename F>
