@@ -97,6 +97,9 @@ int pmsst_rms_norm_backward_from_input(const void* grad_out, const void* x, cons
  * that tensor (its last axis is contiguous), or NULL for the dense bnhd layout.
  * They let q/k be read straight from a fused qkv buffer and written in the
  * [B, H, N, D] layout attention consumes (the reference copies with .contiguous()).
+ * With cs_stride_pair == 2 (the [..., ::2] view of a pair-repeated table) the
+ * kernels read the table rows 16 bytes at a time, so every element
+ * cos[n * cs_stride_seq + k], k < dim, must be readable (as it is for such a view).
  */
 
 /* fused_band_split.cpp:390-410 rotary_forward (.cu:1076-1101,1130-1168). */

@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_kernel(const T* __restric
 // ------------------------------------------------------------------ backward
 
 constexpr int kDpreRows = 64;
-constexpr int kDpreFlatRows = 8;
+constexpr int kDpreFlatRows = 2;
 constexpr int kDpreFlatMaxBands = 4096;
 constexpr int kDpreFlatMaxQuads = 16384;  // LDS table <= 48 KB per block
 

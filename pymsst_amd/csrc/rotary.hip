@@ -28,7 +28,36 @@ struct BnhStrides {
   int64_t b, n, h;
 };
 
-template <typename T, int VEC, bool INVERSE>
+// Table access modes: 1 = one value per pair, contiguous; 2 = the pair-repeated
+// [.., D] table read through its [..., ::2] view (stride 2): one 16-byte load covers
+// the pairs of a pack and the even elements are used; 0 = any strides, scalar loads.
+enum { kTabAny = 0, kTabDense = 1, kTabRepeated = 2 };
+
+// cos or sin of pairs p0 .. p0 + NP - 1 of one table row `r`.
+template <typename T, int NP, int TS>
+__device__ __forceinline__ void load_table(const T* __restrict__ r, int p0, int64_t stride_pair, float (&o)[NP]) {
+  if constexpr (TS == kTabDense) {
+    load_pack<T, NP>(r + p0, o);
+  } else if constexpr (TS == kTabRepeated) {
+    float tmp[2 * NP];
+    load_pack<T, 2 * NP>(r + 2 * p0, tmp);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) o[j] = tmp[2 * j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) o[j] = to_f32(r[(p0 + j) * stride_pair]);
+  }
+}
+
+// Fastest table mode the strides and alignment allow for packs of `vec` elements.
+inline int table_mode(const void* cosv, const void* sinv, int64_t cs_seq, int64_t cs_pair, int vec, size_t elem) {
+  auto al = [&](const void* p, int64_t n) { return reinterpret_cast<uintptr_t>(p) % (n * elem) == 0; };
+  if (cs_pair == 2 && cs_seq % vec == 0 && al(cosv, vec) && al(sinv, vec)) return kTabRepeated;
+  if (vec >= 4 && cs_pair == 1 && cs_seq % (vec / 2) == 0 && al(cosv, vec / 2) && al(sinv, vec / 2)) return kTabDense;
+  return kTabAny;
+}
+
+template <typename T, int VEC, bool INVERSE, int TS>
 __global__ __launch_bounds__(kRotThreads) void rotary_kernel(const T* __restrict__ in, const T* __restrict__ cosv,
                                                              const T* __restrict__ sinv, T* __restrict__ out,
                                                              uint32_t total_packs, FastDiv packs_per_token,
@@ -44,12 +73,13 @@ __global__ __launch_bounds__(kRotThreads) void rotary_kernel(const T* __restrict
     const uint32_t p0 = d >> 1;
     float v[VEC];
     load_pack<T, VEC>(in + b * si.b + n * si.n + h * si.h + d, v);
-    const T* cr = cosv + n * tab.stride_seq;
-    const T* sr = sinv + n * tab.stride_seq;
+    float cv[VEC / 2], sv[VEC / 2];
+    load_table<T, VEC / 2, TS>(cosv + n * tab.stride_seq, p0, tab.stride_pair, cv);
+    load_table<T, VEC / 2, TS>(sinv + n * tab.stride_seq, p0, tab.stride_pair, sv);
 #pragma unroll
     for (int j = 0; j < VEC / 2; ++j) {
-      const float c = to_f32(cr[(p0 + j) * tab.stride_pair]);
-      const float s = to_f32(sr[(p0 + j) * tab.stride_pair]);
+      const float c = cv[j];
+      const float s = sv[j];
       const float ev = v[2 * j], ov = v[2 * j + 1];
       if (INVERSE) {
         v[2 * j] = ev * c + ov * s;
@@ -101,9 +131,16 @@ int launch_rotary(const void* in, const int64_t* in_strides, const void* cosv, c
   const T* ps = static_cast<const T*>(sinv);
   T* po = static_cast<T*>(out);
   const uint32_t np = static_cast<uint32_t>(packs);
-#define PMSST_ROT(VEC, INV)                                                                                     \
-  hipLaunchKernelGGL((rotary_kernel<T, VEC, INV>), dim3(blocks), dim3(kRotThreads), 0, stream, pin, pc, ps, po, \
+  const int ts = table_mode(cosv, sinv, cs_seq, cs_pair, vec, sizeof(T));
+#define PMSST_ROT1(VEC, INV, TS)                                                                                    \
+  hipLaunchKernelGGL((rotary_kernel<T, VEC, INV, TS>), dim3(blocks), dim3(kRotThreads), 0, stream, pin, pc, ps, po, \
                      np, ppt, fseq, fdim, tab, si, so)
+#define PMSST_ROT(VEC, INV)                                  \
+  do {                                                       \
+    if (ts == kTabRepeated) PMSST_ROT1(VEC, INV, kTabRepeated); \
+    else if (ts == kTabDense) PMSST_ROT1(VEC, INV, kTabDense);  \
+    else PMSST_ROT1(VEC, INV, kTabAny);                         \
+  } while (0)
   if (inverse) {
     if (vec == 16 / (int)sizeof(T)) PMSST_ROT(16 / sizeof(T), true);
     else if (vec == 8 / (int)sizeof(T)) PMSST_ROT(8 / sizeof(T), true);
@@ -114,12 +151,17 @@ int launch_rotary(const void* in, const int64_t* in_strides, const void* cosv, c
     else PMSST_ROT(2, false);
   }
 #undef PMSST_ROT
+#undef PMSST_ROT1
   return check_launch("rotary_kernel");
 }
 
 // ------------------------------------------------------------------ fused q/k RMSNorm + rotary
 
-template <typename T, typename TG, int VEC, int NV>
+// Rows per lane slot in flight: the loads of kRowsPerSlot rows are issued before any
+// reduction, so each lane keeps several 16-byte packs outstanding.
+constexpr int kRowsPerSlot = 2;
+
+template <typename T, typename TG, int VEC, int NV, int TS>
 __global__ __launch_bounds__(kNormRotThreads) void norm_rot_fwd_kernel(
     const T* __restrict__ x, const TG* __restrict__ gamma, const T* __restrict__ cosv, const T* __restrict__ sinv,
     T* __restrict__ out, float* __restrict__ inv_norm, int64_t rows, int tpr_log2, float scale, FastDiv heads,
@@ -137,52 +179,57 @@ __global__ __launch_bounds__(kNormRotThreads) void norm_rot_fwd_kernel(
 #pragma unroll
   for (int v = 0; v < NV; ++v) load_pack<TG, VEC>(gamma + (v * tpr + t) * VEC, g[v]);
 
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block; base < rows;
-       base += static_cast<int64_t>(gridDim.x) * rows_per_block) {
-    const int64_t row = base + wave * rows_per_wave + slot;
-    const bool valid = row < rows;
-    float xv[NV][VEC];
-    float ss = 0.f;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block * kRowsPerSlot; base < rows;
+       base += static_cast<int64_t>(gridDim.x) * rows_per_block * kRowsPerSlot) {
+    float xv[kRowsPerSlot][NV][VEC];
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      if (valid) {
-        load_pack<T, VEC>(x + row * dim + (v * tpr + t) * VEC, xv[v]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) xv[v][i] = 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) ss += xv[v][i] * xv[v][i];
-    }
-    ss = group_sum(ss, tpr);
-    const float inv = 1.0f / fmaxf(sqrtf(ss), 1.0e-12f);
-    if (valid) {
-      const uint32_t n = seq.mod(heads.div(static_cast<uint32_t>(row)));
-      const T* cr = cosv + n * tab.stride_seq;
-      const T* sr = sinv + n * tab.stride_seq;
-      const float s = inv * scale;
+    for (int u = 0; u < kRowsPerSlot; ++u) {
+      const int64_t row = base + u * rows_per_block + wave * rows_per_wave + slot;
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        const int col = (v * tpr + t) * VEC;
-        float o[VEC];
+        if (row < rows) {
+          load_pack<T, VEC>(x + row * dim + (v * tpr + t) * VEC, xv[u][v]);
+        } else {
 #pragma unroll
-        for (int j = 0; j < VEC / 2; ++j) {
-          const int p = col / 2 + j;
-          const float c = to_f32(cr[p * tab.stride_pair]);
-          const float sn = to_f32(sr[p * tab.stride_pair]);
-          const float ev = xv[v][2 * j] * s * g[v][2 * j];
-          const float ov = xv[v][2 * j + 1] * s * g[v][2 * j + 1];
-          o[2 * j] = ev * c - ov * sn;
-          o[2 * j + 1] = ov * c + ev * sn;
+          for (int i = 0; i < VEC; ++i) xv[u][v][i] = 0.f;
         }
-        store_pack<T, VEC>(out + row * dim + col, o);
       }
-      if (t == 0) inv_norm[row] = inv;
+    }
+#pragma unroll
+    for (int u = 0; u < kRowsPerSlot; ++u) {
+      const int64_t row = base + u * rows_per_block + wave * rows_per_wave + slot;
+      float ss = 0.f;
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) ss += xv[u][v][i] * xv[u][v][i];
+      ss = group_sum(ss, tpr);
+      const float inv = 1.0f / fmaxf(sqrtf(ss), 1.0e-12f);
+      if (row < rows) {
+        const uint32_t n = seq.mod(heads.div(static_cast<uint32_t>(row)));
+        const float s = inv * scale;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          const int col = (v * tpr + t) * VEC;
+          float cv[VEC / 2], sv[VEC / 2], o[VEC];
+          load_table<T, VEC / 2, TS>(cosv + n * tab.stride_seq, col / 2, tab.stride_pair, cv);
+          load_table<T, VEC / 2, TS>(sinv + n * tab.stride_seq, col / 2, tab.stride_pair, sv);
+#pragma unroll
+          for (int j = 0; j < VEC / 2; ++j) {
+            const float ev = xv[u][v][2 * j] * s * g[v][2 * j];
+            const float ov = xv[u][v][2 * j + 1] * s * g[v][2 * j + 1];
+            o[2 * j] = ev * cv[j] - ov * sv[j];
+            o[2 * j + 1] = ov * cv[j] + ev * sv[j];
+          }
+          store_pack<T, VEC>(out + row * dim + col, o);
+        }
+        if (t == 0) inv_norm[row] = inv;
+      }
     }
   }
 }
 
-template <typename T, typename TG, int VEC, int NV>
+template <typename T, typename TG, int VEC, int NV, int TS>
 __global__ __launch_bounds__(kRowBwdThreads) void norm_rot_bwd_kernel(
     const T* __restrict__ dy, const T* __restrict__ x, const float* __restrict__ inv_norm,
     const TG* __restrict__ gamma, const T* __restrict__ cosv, const T* __restrict__ sinv, T* __restrict__ dx,
@@ -207,54 +254,65 @@ __global__ __launch_bounds__(kRowBwdThreads) void norm_rot_bwd_kernel(
   }
   const float inv_scale = 1.0f / scale;
 
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block; base < rows;
-       base += static_cast<int64_t>(gridDim.x) * rows_per_block) {
-    const int64_t row = base + wave * rows_per_wave + slot;
-    const bool valid = row < rows;
-    float gr[NV][VEC], n[NV][VEC];
-    float dot = 0.f;
-    const float inv = valid ? inv_norm[row] : 0.f;
-    const float ns = inv * scale;
-    const uint32_t pos = valid ? seq.mod(heads.div(static_cast<uint32_t>(row))) : 0u;
-    const T* cr = cosv + pos * tab.stride_seq;
-    const T* sr = sinv + pos * tab.stride_seq;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block * kRowsPerSlot; base < rows;
+       base += static_cast<int64_t>(gridDim.x) * rows_per_block * kRowsPerSlot) {
+    // loads of all kRowsPerSlot rows first
+    float d[kRowsPerSlot][NV][VEC], n[kRowsPerSlot][NV][VEC], inv[kRowsPerSlot];
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int col = (v * tpr + t) * VEC;
-      if (valid) {
-        float d[VEC];
-        load_pack<T, VEC>(dy + row * dim + col, d);
-        load_pack<T, VEC>(x + row * dim + col, n[v]);
-#pragma unroll
-        for (int j = 0; j < VEC / 2; ++j) {
-          const int p = col / 2 + j;
-          const float c = to_f32(cr[p * tab.stride_pair]);
-          const float sn = to_f32(sr[p * tab.stride_pair]);
-          gr[v][2 * j] = d[2 * j] * c + d[2 * j + 1] * sn;
-          gr[v][2 * j + 1] = d[2 * j + 1] * c - d[2 * j] * sn;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) gr[v][i] = n[v][i] = 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        n[v][i] *= ns;
-        dot += gr[v][i] * g[v][i] * n[v][i];
-      }
-    }
-    dot = group_sum(dot, tpr);
-    if (valid) {
-      const float dot_s = dot * inv_scale;
+    for (int u = 0; u < kRowsPerSlot; ++u) {
+      const int64_t row = base + u * rows_per_block + wave * rows_per_wave + slot;
+      const bool valid = row < rows;
+      inv[u] = valid ? inv_norm[row] : 0.f;
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        float o[VEC];
+        const int col = (v * tpr + t) * VEC;
+        if (valid) {
+          load_pack<T, VEC>(dy + row * dim + col, d[u][v]);
+          load_pack<T, VEC>(x + row * dim + col, n[u][v]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) d[u][v][i] = n[u][v][i] = 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRowsPerSlot; ++u) {
+      const int64_t row = base + u * rows_per_block + wave * rows_per_wave + slot;
+      const bool valid = row < rows;
+      const float ns = inv[u] * scale;
+      const uint32_t pos = valid ? seq.mod(heads.div(static_cast<uint32_t>(row))) : 0u;
+      float gr[NV][VEC];
+      float dot = 0.f;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int col = (v * tpr + t) * VEC;
+        float cv[VEC / 2], sv[VEC / 2];
+        load_table<T, VEC / 2, TS>(cosv + pos * tab.stride_seq, col / 2, tab.stride_pair, cv);
+        load_table<T, VEC / 2, TS>(sinv + pos * tab.stride_seq, col / 2, tab.stride_pair, sv);
+#pragma unroll
+        for (int j = 0; j < VEC / 2; ++j) {
+          gr[v][2 * j] = d[u][v][2 * j] * cv[j] + d[u][v][2 * j + 1] * sv[j];
+          gr[v][2 * j + 1] = d[u][v][2 * j + 1] * cv[j] - d[u][v][2 * j] * sv[j];
+        }
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          o[i] = inv * (gr[v][i] * g[v][i] * scale - n[v][i] * dot_s);
-          acc[v][i] += gr[v][i] * n[v][i];
+          n[u][v][i] *= ns;
+          dot += gr[v][i] * g[v][i] * n[u][v][i];
         }
-        store_pack<T, VEC>(dx + row * dim + (v * tpr + t) * VEC, o);
+      }
+      dot = group_sum(dot, tpr);
+      if (valid) {
+        const float dot_s = dot * inv_scale;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          float o[VEC];
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            o[i] = inv[u] * (gr[v][i] * g[v][i] * scale - n[u][v][i] * dot_s);
+            acc[v][i] += gr[v][i] * n[u][v][i];
+          }
+          store_pack<T, VEC>(dx + row * dim + (v * tpr + t) * VEC, o);
+        }
       }
     }
   }
@@ -310,17 +368,24 @@ int launch_norm_rot_fwd(const void* x, const void* gamma, const void* cosv, cons
   if (rc != PMSST_OK) return rc;
   const int64_t rows = a.batch * a.seq * a.heads;
   if (rows == 0) return PMSST_OK;
-  const int rpb = (kWave >> geo.tpr_log2) * (kNormRotThreads / kWave);
+  const int rpb = (kWave >> geo.tpr_log2) * (kNormRotThreads / kWave) * kRowsPerSlot;
   const int64_t blocks64 = (rows + rpb - 1) / rpb;
   const int blocks = static_cast<int>(blocks64 < 65536 ? blocks64 : 65536);
   const float scale = sqrtf(static_cast<float>(a.dim));
   const FastDiv fh(static_cast<uint32_t>(a.heads)), fs(static_cast<uint32_t>(a.seq));
   const TableRef tab{a.cs_seq, a.cs_pair};
-#define PMSST_NRF(NV)                                                                                        \
-  hipLaunchKernelGGL((norm_rot_fwd_kernel<T, TG, kVec, NV>), dim3(blocks), dim3(kNormRotThreads), 0, stream, \
-                     static_cast<const T*>(x), static_cast<const TG*>(gamma), static_cast<const T*>(cosv),    \
-                     static_cast<const T*>(sinv), static_cast<T*>(out), inv_norm, rows, geo.tpr_log2, scale, \
+  const int ts = table_mode(cosv, sinv, a.cs_seq, a.cs_pair, kVec, sizeof(T));
+#define PMSST_NRF1(NV, TS)                                                                                        \
+  hipLaunchKernelGGL((norm_rot_fwd_kernel<T, TG, kVec, NV, TS>), dim3(blocks), dim3(kNormRotThreads), 0, stream, \
+                     static_cast<const T*>(x), static_cast<const TG*>(gamma), static_cast<const T*>(cosv),        \
+                     static_cast<const T*>(sinv), static_cast<T*>(out), inv_norm, rows, geo.tpr_log2, scale,     \
                      fh, fs, tab)
+#define PMSST_NRF(NV)                                          \
+  do {                                                         \
+    if (ts == kTabRepeated) PMSST_NRF1(NV, kTabRepeated);      \
+    else if (ts == kTabDense) PMSST_NRF1(NV, kTabDense);       \
+    else PMSST_NRF1(NV, kTabAny);                              \
+  } while (0)
   switch (geo.nv) {
     case 1: PMSST_NRF(1); break;
     case 2: PMSST_NRF(2); break;
@@ -329,6 +394,7 @@ int launch_norm_rot_fwd(const void* x, const void* gamma, const void* cosv, cons
     default: return fail(PMSST_EINVAL, "rms_norm_rotary_forward: internal geometry error");
   }
 #undef PMSST_NRF
+#undef PMSST_NRF1
   return check_launch("norm_rot_fwd_kernel");
 }
 
@@ -357,11 +423,18 @@ int launch_norm_rot_bwd(const void* dy, const void* x, const float* inv_norm, co
   const TableRef tab{a.cs_seq, a.cs_pair};
   const size_t shmem = sizeof(float) * (kRowBwdThreads / kWave) * static_cast<size_t>(a.dim);
   if (parts > 0) {
-#define PMSST_NRB(NV)                                                                                          \
-  hipLaunchKernelGGL((norm_rot_bwd_kernel<T, TG, kVec, NV>), dim3(parts), dim3(kRowBwdThreads), shmem, stream, \
-                     static_cast<const T*>(dy), static_cast<const T*>(x), inv_norm, static_cast<const TG*>(gamma), \
-                     static_cast<const T*>(cosv), static_cast<const T*>(sinv), static_cast<T*>(dx), partial,     \
+    const int ts = table_mode(cosv, sinv, a.cs_seq, a.cs_pair, kVec, sizeof(T));
+#define PMSST_NRB1(NV, TS)                                                                                           \
+  hipLaunchKernelGGL((norm_rot_bwd_kernel<T, TG, kVec, NV, TS>), dim3(parts), dim3(kRowBwdThreads), shmem, stream, \
+                     static_cast<const T*>(dy), static_cast<const T*>(x), inv_norm, static_cast<const TG*>(gamma),     \
+                     static_cast<const T*>(cosv), static_cast<const T*>(sinv), static_cast<T*>(dx), partial,         \
                      rows, geo.tpr_log2, scale, fh, fs, tab)
+#define PMSST_NRB(NV)                                          \
+  do {                                                         \
+    if (ts == kTabRepeated) PMSST_NRB1(NV, kTabRepeated);      \
+    else if (ts == kTabDense) PMSST_NRB1(NV, kTabDense);       \
+    else PMSST_NRB1(NV, kTabAny);                              \
+  } while (0)
     switch (geo.nv) {
       case 1: PMSST_NRB(1); break;
       case 2: PMSST_NRB(2); break;
@@ -370,6 +443,7 @@ int launch_norm_rot_bwd(const void* dy, const void* x, const float* inv_norm, co
       default: return fail(PMSST_EINVAL, "rms_norm_rotary_backward: internal geometry error");
     }
 #undef PMSST_NRB
+#undef PMSST_NRB1
     rc = check_launch("norm_rot_bwd_kernel");
     if (rc != PMSST_OK) return rc;
   }

@@ -228,6 +228,15 @@ class HipFusedExtension:
         # One stride pair for both tables: make them agree if they do not.
         if cos.stride(1) != sin.stride(1) or cos.stride(3) != sin.stride(3):
             cos, sin = cos.contiguous(), sin.contiguous()
+
+        def repeated_view_ok(t):
+            # the kernels read a [..., ::2] table 16 bytes at a time, odd elements included:
+            # they must lie inside the tensor's storage (true for a view of a [.., D] table)
+            last = t.storage_offset() + (t.size(1) - 1) * t.stride(1) + 2 * t.size(3)
+            return last * t.element_size() <= t.untyped_storage().nbytes()
+
+        if cos.stride(3) == 2 and not (repeated_view_ok(cos) and repeated_view_ok(sin)):
+            cos, sin = cos.contiguous(), sin.contiguous()
         return cos, sin, cos.stride(1), cos.stride(3)
 
     def _rotary(self, fn_name, t, cos, sin, out_layout="bnhd"):
