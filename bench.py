@@ -58,6 +58,8 @@ def _args(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--train-steps", type=int, default=20, help="timed BS-RoFormer train steps per backend (0: skip)")
     ap.add_argument("--train-warmup", type=int, default=3)
+    ap.add_argument("--train-impl", choices=("both", "fused", "stock"), default="both",
+                    help="which train-step legs to run (profiling one implementation at a time)")
     return ap.parse_args(argv)
 
 
@@ -232,7 +234,7 @@ def _cpu_baseline(budget_s: float):
     }
 
 
-def _train_leg(torch, steps: int, warmup: int) -> dict:
+def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused")) -> dict:
     """BS-RoFormer dim 192, depth 6, 4 stems, batch 4 x 131584 stereo samples,
     bf16 autocast, multi-resolution STFT loss, AdamW 5e-4.  One step = forward, backward and
     optimizer step; train samples/s = batch / median step time, for the stock modules and for
@@ -246,7 +248,7 @@ def _train_leg(torch, steps: int, warmup: int) -> dict:
     dev = torch.device("cuda:0")
     target, mixture = workload_batch(wl, seed=0, device=dev)
     out = {}
-    for impl in ("stock", "fused"):
+    for impl in impls:
         fr.restore_stock_implementations()
         model = wl.build_model(dev, seed=4)
         model.train()
@@ -279,16 +281,18 @@ def _train_leg(torch, steps: int, warmup: int) -> dict:
         fr.restore_stock_implementations(model)
         del model, opt
         torch.cuda.empty_cache()
-    return {
+    res = {
         "workload": "configs[2] BS-RoFormer dim 192, depth 6, 8x64 heads, 4 stems, batch 4 x 131584 stereo "
                     "(258 frames), bf16 autocast, multi-res STFT L1, AdamW 5e-4",
         "steps": steps,
         "warmup": warmup,
-        "fused_samples_per_s": out["fused"]["samples_per_s"],
-        "stock_samples_per_s": out["stock"]["samples_per_s"],
-        "speedup": round(out["fused"]["samples_per_s"] / out["stock"]["samples_per_s"], 3),
         "detail": out,
     }
+    for impl in impls:
+        res[f"{impl}_samples_per_s"] = out[impl]["samples_per_s"]
+    if "fused" in out and "stock" in out:
+        res["speedup"] = round(out["fused"]["samples_per_s"] / out["stock"]["samples_per_s"], 3)
+    return res
 
 
 def main(argv=None) -> int:
@@ -368,7 +372,21 @@ def main(argv=None) -> int:
         "bytes_per_launch": int(launch_bytes),
         "avg_ms": round(launch_ms, 5),
     }
-    train = _train_leg(torch, args.train_steps, args.train_warmup) if args.train_steps > 0 else None
+    # achievable streaming rate on this GPU: a plain elementwise copy of 1 GiB (read + write)
+    src = torch.empty(1 << 29, dtype=torch.bfloat16, device="cuda").uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record(stream)
+    for _ in range(10):
+        torch.mul(src, 1.0, out=dst)
+    c1.record(stream)
+    torch.cuda.synchronize()
+    copy_gbs = 2 * src.numel() * src.element_size() * 10 / (c0.elapsed_time(c1) * 1e-3) / 1e9
+    del src, dst
+    impls = ("stock", "fused") if args.train_impl == "both" else (args.train_impl,)
+    train = _train_leg(torch, args.train_steps, args.train_warmup, impls) if args.train_steps > 0 else None
     cpu = None if args.no_cpu_baseline else _cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC,
@@ -387,6 +405,7 @@ def main(argv=None) -> int:
             "workload": "configs[1] kernel microbench: band split [4,258,4100]->192 (62 bands), "
                         "q/k RMSNorm+rotary [248,258,8,64]x2, mask-estimator final 768->2*I_b+GLU; fwd+bwd",
             "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+            "hbm_copy_GBps_measured": round(copy_gbs, 1),
             "wall_s_timed": round(wall, 3),
         },
         "per_op": per_op,

@@ -242,7 +242,7 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
                                                                  const T* __restrict__ weight, T* __restrict__ dx,
                                                                  float* __restrict__ dg_partial,
                                                                  const float* __restrict__ dots, int max_ichunks,
-                                                                 BandArgs a) {
+                                                                 XcdGrid xg, BandArgs a) {
   constexpr int kBI = 64;
   constexpr int kPasses = (NORM && !SPLIT) ? 2 : 1;
   __shared__ T lds[gemm_lds_elems<T, kBI, kBM>()];
@@ -251,11 +251,25 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
   using S = TileShape<kBI, kBM, 4, 1>;  // TR = 1, TC = 4
 
   const int O = a.O;
-  const int band = SPLIT ? static_cast<int>(blockIdx.y) / max_ichunks : static_cast<int>(blockIdx.y);
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBM;
+  // SPLIT: 1-D XCD-ordered grid, group = (band, input chunk), member = row tile (the weight
+  // chunk is shared in L2); otherwise grid (row tile, band)
+  int band, ichunk;
+  int64_t mtile;
+  if (SPLIT) {
+    uint32_t grp, mt;
+    if (!xcd_block(xg, grp, mt)) return;
+    band = static_cast<int>(grp) / max_ichunks;
+    ichunk = static_cast<int>(grp) % max_ichunks;
+    mtile = mt;
+  } else {
+    band = static_cast<int>(blockIdx.y);
+    ichunk = 0;
+    mtile = blockIdx.x;
+  }
+  const int64_t m0 = mtile * kBM;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
-  const int i_begin = SPLIT ? (static_cast<int>(blockIdx.y) % max_ichunks) * kBI : 0;
+  const int i_begin = ichunk * kBI;
   if (i_begin >= I) return;  // uniform over the block
   const int i_end = SPLIT ? (i_begin + kBI < I ? i_begin + kBI : I) : I;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -362,7 +376,7 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
 #pragma unroll
         for (int r = 0; r < 4; ++r) dgp[r] = group_sum(dgp[r], 16);
         if ((lane & 15) == 0) {
-          float* dst = dg_partial + static_cast<int64_t>(blockIdx.x) * a.F + off;
+          float* dst = dg_partial + mtile * a.F + off;
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             if (il + r < I) dst[il + r] = dgp[r];
@@ -383,13 +397,16 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
                                                                  const T* __restrict__ nsrc,
                                                                  const float* __restrict__ inv_norm,
                                                                  const T* __restrict__ gamma, T* __restrict__ dw,
-                                                                 T* __restrict__ db, int max_itiles, BandArgs a) {
+                                                                 T* __restrict__ db, int max_itiles, XcdGrid xg,
+                                                                 BandArgs a) {
   __shared__ T lds[gemm_lds_elems<T, kDwBI, kDwBO>()];
   using S = TileShape<kDwBI, kDwBO, 2, 2>;
   const int O = a.O;
-  const int o0 = blockIdx.x * kDwBO;
-  const int band = blockIdx.y / max_itiles;
-  const int i0 = (blockIdx.y % max_itiles) * kDwBI;
+  uint32_t grp, ot;  // group = (band, input tile), member = output tile: the input slab shared in L2
+  if (!xcd_block(xg, grp, ot)) return;
+  const int o0 = static_cast<int>(ot) * kDwBO;
+  const int band = static_cast<int>(grp) / max_itiles;
+  const int i0 = (static_cast<int>(grp) % max_itiles) * kDwBI;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
   if (i0 >= I) return;
@@ -585,10 +602,11 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
       int rc = check_launch("bs_dots_kernel");
       if (rc != PMSST_OK) return rc;
     }
-    const dim3 grid(static_cast<unsigned>(m_tiles), static_cast<unsigned>(hb.NB * (split ? max_ichunks : 1)));
+    const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_ichunks), static_cast<uint32_t>(m_tiles)};
+    const dim3 grid = split ? dim3(xg.blocks()) : dim3(static_cast<unsigned>(m_tiles), static_cast<unsigned>(hb.NB));
 #define PMSST_BDX(FX, SPLIT, V4)                                                                               \
   hipLaunchKernelGGL((bs_bwd_dx_kernel<T, FX, true, SPLIT, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, \
-                     inv_norm, pg, pw, static_cast<T*>(dx), partial, dots, max_ichunks, a)
+                     inv_norm, pg, pw, static_cast<T*>(dx), partial, dots, max_ichunks, xg, a)
     if (split) {
       if (from_x) {
         if (v4) PMSST_BDX(true, true, true); else PMSST_BDX(true, true, false);
@@ -608,11 +626,12 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   }
   {
     const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
-    const dim3 grid(static_cast<unsigned>((O + kDwBO - 1) / kDwBO), static_cast<unsigned>(hb.NB * max_itiles));
+    const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_itiles), static_cast<uint32_t>((O + kDwBO - 1) / kDwBO)};
+    const dim3 grid(xg.blocks());
     const bool v4 = a.vec4 && a.ovec4;
 #define PMSST_BDW(FX, V4)                                                                                   \
   hipLaunchKernelGGL((bs_bwd_dw_kernel<T, FX, true, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, \
-                     pg, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, a)
+                     pg, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, a)
     if (from_x) {
       if (v4) PMSST_BDW(true, true); else PMSST_BDW(true, false);
     } else {
@@ -649,25 +668,27 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
   const T* pw = static_cast<const T*>(weight);
   if (M > 0) {
     const int max_ichunks = (hb.max_width + 63) / 64;
-    const dim3 grid(static_cast<unsigned>((M + kBM - 1) / kBM), static_cast<unsigned>(hb.NB * max_ichunks));
+    const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_ichunks), static_cast<uint32_t>((M + kBM - 1) / kBM)};
+    const dim3 grid(xg.blocks());
     if (a.vec4 && a.ovec4)
       hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true, true>), grid, dim3(kGemmThreads), 0, stream, pdy,
-                         px, nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, max_ichunks, a);
+                         px, nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, max_ichunks, xg, a);
     else
       hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true, false>), grid, dim3(kGemmThreads), 0, stream, pdy,
-                         px, nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, max_ichunks, a);
+                         px, nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, max_ichunks, xg, a);
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
   {
     const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
-    const dim3 grid(static_cast<unsigned>((O + kDwBO - 1) / kDwBO), static_cast<unsigned>(hb.NB * max_itiles));
+    const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_itiles), static_cast<uint32_t>((O + kDwBO - 1) / kDwBO)};
+    const dim3 grid(xg.blocks());
     if (a.vec4 && a.ovec4)
       hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
-                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, a);
+                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, a);
     else
       hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
-                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, a);
+                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, a);
     int rc = check_launch("bs_bwd_dw_kernel");
     if (rc != PMSST_OK) return rc;
   }

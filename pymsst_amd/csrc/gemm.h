@@ -284,6 +284,29 @@ __device__ __forceinline__ void reduce_colsum(const MNLoader<T, ROWS>& ld, T* ld
   }
 }
 
+// ---------------------------------------------------------------- XCD-aware block order
+// MI355X has 8 XCDs (32 CUs and one L2 each); the hardware dispatches 1-D block b to
+// XCD b % 8.  Kernels whose blocks fall into groups that read the same operand tile
+// (e.g. the m-tiles of one band's weight chunk) number their blocks so that all
+// `members` blocks of a group land on one XCD and are dispatched close together:
+//   block b -> group (b / 8 / members) * 8 + b % 8, member (b / 8) % members.
+// The grid is padded to whole groups of 8; padding blocks exit at once.
+constexpr uint32_t kXcds = 8;
+
+struct XcdGrid {
+  uint32_t groups;
+  uint32_t members;
+  uint32_t blocks() const { return ((groups + kXcds - 1) / kXcds) * kXcds * members; }
+};
+
+__device__ __forceinline__ bool xcd_block(const XcdGrid& xg, uint32_t& group, uint32_t& member) {
+  const uint32_t b = blockIdx.x;
+  const uint32_t r = b / kXcds;
+  member = r % xg.members;
+  group = (r / xg.members) * kXcds + b % kXcds;
+  return group < xg.groups;
+}
+
 template <int BR, int BC, int WR, int WC>
 struct TileShape {
   static constexpr int kTR = BR / WR / 16;

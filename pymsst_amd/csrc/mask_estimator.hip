@@ -78,15 +78,18 @@ constexpr int kFwdBM = 128;
 template <typename T, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void me_fwd_kernel(const T* __restrict__ x, const T* __restrict__ weight,
                                                               const T* __restrict__ bias, T* __restrict__ pre,
-                                                              T* __restrict__ out, int max_lchunks, MaskArgs a) {
+                                                              T* __restrict__ out, int max_lchunks, XcdGrid xg,
+                                                              MaskArgs a) {
   __shared__ T lds[gemm_lds_elems<T, 128, kFwdBM>()];
   using S = TileShape<128, kFwdBM, 1, 4>;  // TR = 8 (4 left + 4 gate), TC = 2
-  const int band = blockIdx.y / max_lchunks;
-  const int l0 = (blockIdx.y % max_lchunks) * 64;
+  uint32_t grp, mt;  // group = (band, 64-output chunk), member = row tile: weight chunk shared in L2
+  if (!xcd_block(xg, grp, mt)) return;
+  const int band = static_cast<int>(grp) / max_lchunks;
+  const int l0 = (static_cast<int>(grp) % max_lchunks) * 64;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
   if (l0 >= I) return;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kFwdBM;
+  const int64_t m0 = static_cast<int64_t>(mt) * kFwdBM;
   const int rows_valid = static_cast<int>(a.M - m0 < kFwdBM ? a.M - m0 : kFwdBM);
   const int H = a.H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -258,12 +261,14 @@ template <typename T, bool TANH_IN, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __restrict__ dpre,
                                                                  const T* __restrict__ weight,
                                                                  const T* __restrict__ x, T* __restrict__ dx,
-                                                                 MaskArgs a) {
+                                                                 int hchunks, XcdGrid xg, MaskArgs a) {
   __shared__ T lds[gemm_lds_elems<T, kDxBH, kDxBM>()];
   using S = TileShape<kDxBH, kDxBM, 2, 2>;
-  const int band = blockIdx.y;
-  const int h0 = blockIdx.z * kDxBH;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kDxBM;
+  uint32_t grp, mt;  // group = (band, hidden chunk), member = row tile: weight chunk shared in L2
+  if (!xcd_block(xg, grp, mt)) return;
+  const int band = static_cast<int>(grp) / hchunks;
+  const int h0 = (static_cast<int>(grp) % hchunks) * kDxBH;
+  const int64_t m0 = static_cast<int64_t>(mt) * kDxBM;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
   const int H = a.H;
@@ -318,12 +323,14 @@ constexpr int kDwBJ = 64;
 template <typename T, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __restrict__ dpre, const T* __restrict__ x,
                                                                  T* __restrict__ dw, T* __restrict__ dbias,
-                                                                 int max_jchunks, MaskArgs a) {
+                                                                 int htiles, XcdGrid xg, MaskArgs a) {
   __shared__ T lds[gemm_lds_elems<T, kDwBH, kDwBJ>()];
   using S = TileShape<kDwBH, kDwBJ, 2, 2>;
-  const int h0 = blockIdx.x * kDwBH;
-  const int band = blockIdx.y / max_jchunks;
-  const int j0 = (blockIdx.y % max_jchunks) * kDwBJ;
+  uint32_t grp, jchunk;  // group = (band, hidden tile), member = j chunk: the x slab shared in L2
+  if (!xcd_block(xg, grp, jchunk)) return;
+  const int band = static_cast<int>(grp) / htiles;
+  const int h0 = (static_cast<int>(grp) % htiles) * kDwBH;
+  const int j0 = static_cast<int>(jchunk) * kDwBJ;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
   const int K2 = 2 * I;
@@ -406,15 +413,16 @@ int launch_me_fwd(const void* x, const void* weight, const void* bias, const int
   a.vec4 = hm.vec4 && al(x, 4 * sizeof(T)) && al(weight, 4 * sizeof(T)) && al(pre, 4 * sizeof(T)) &&
            al(out, 4 * sizeof(T));
   const int max_lchunks = (hm.max_width + 63) / 64;
-  const dim3 grid(static_cast<unsigned>((M + kFwdBM - 1) / kFwdBM), static_cast<unsigned>(hm.NB * max_lchunks));
+  const XcdGrid xg{static_cast<uint32_t>(hm.NB * max_lchunks), static_cast<uint32_t>((M + kFwdBM - 1) / kFwdBM)};
+  const dim3 grid(xg.blocks());
   if (a.vec4)
     hipLaunchKernelGGL((me_fwd_kernel<T, true>), grid, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
                        static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
-                       static_cast<T*>(out), max_lchunks, a);
+                       static_cast<T*>(out), max_lchunks, xg, a);
   else
     hipLaunchKernelGGL((me_fwd_kernel<T, false>), grid, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
                        static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
-                       static_cast<T*>(out), max_lchunks, a);
+                       static_cast<T*>(out), max_lchunks, xg, a);
   return check_launch("me_fwd_kernel");
 }
 
@@ -454,11 +462,12 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
                        static_cast<const T*>(pre), dpre, a);
     int rc = check_launch("me_dpre_kernel");
     if (rc != PMSST_OK) return rc;
-    const dim3 g2(static_cast<unsigned>((M + kDxBM - 1) / kDxBM), static_cast<unsigned>(hm.NB),
-                  static_cast<unsigned>((H + kDxBH - 1) / kDxBH));
+    const int hchunks = static_cast<int>((H + kDxBH - 1) / kDxBH);
+    const XcdGrid xg2{static_cast<uint32_t>(hm.NB * hchunks), static_cast<uint32_t>((M + kDxBM - 1) / kDxBM)};
+    const dim3 g2(xg2.blocks());
 #define PMSST_MDX(TANH, V4)                                                                                    \
   hipLaunchKernelGGL((me_bwd_dx_kernel<T, TANH, V4>), g2, dim3(kGemmThreads), 0, stream, dpre,                   \
-                     static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), a)
+                     static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), hchunks, xg2, a)
     if (input_act == PMSST_ACT_TANH) {
       if (a.vec4) PMSST_MDX(true, true); else PMSST_MDX(true, false);
     } else {
@@ -469,13 +478,15 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
     if (rc != PMSST_OK) return rc;
   }
   const int max_jchunks = (2 * hm.max_width + kDwBJ - 1) / kDwBJ;
-  const dim3 g3(static_cast<unsigned>((H + kDwBH - 1) / kDwBH), static_cast<unsigned>(hm.NB * max_jchunks));
+  const int htiles = static_cast<int>((H + kDwBH - 1) / kDwBH);
+  const XcdGrid xg3{static_cast<uint32_t>(hm.NB * htiles), static_cast<uint32_t>(max_jchunks)};
+  const dim3 g3(xg3.blocks());
   if (a.vec4)
     hipLaunchKernelGGL((me_bwd_dw_kernel<T, true>), g3, dim3(kGemmThreads), 0, stream, dpre, static_cast<const T*>(x),
-                       static_cast<T*>(dw), static_cast<T*>(dbias), max_jchunks, a);
+                       static_cast<T*>(dw), static_cast<T*>(dbias), htiles, xg3, a);
   else
     hipLaunchKernelGGL((me_bwd_dw_kernel<T, false>), g3, dim3(kGemmThreads), 0, stream, dpre,
-                       static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(dbias), max_jchunks, a);
+                       static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(dbias), htiles, xg3, a);
   int rc = check_launch("me_bwd_dw_kernel");
   if (rc != PMSST_OK) return rc;
   // dbias was summed by the dW kernel (which also runs for M == 0 and then writes zeros)

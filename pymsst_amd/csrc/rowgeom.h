@@ -8,7 +8,7 @@ namespace pmsst {
 
 constexpr int kRowBwdThreads = 512;
 // Upper bound on backward blocks; the dgamma workspace is kRowBwdMaxParts * dim fp32.
-constexpr int kRowBwdMaxParts = 512;
+constexpr int kRowBwdMaxParts = 1024;
 
 struct RowGeom {
   int vec;       // elements per pack (1 = scalar path with column guards)
