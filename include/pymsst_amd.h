@@ -212,6 +212,30 @@ int pmsst_mask_estimator_final_backward(const void* grad_out, const void* x, con
                                         void* grad_weight, int input_activation, int dtype, void* workspace,
                                         size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------ attention output gate
+ * gate[m, h] = sigmoid(x[m] . W[h] + b[h]) stored in the tensor dtype; out[m, h*Dh + d] =
+ * attn[m, h, d] * gate[m, h].  Rows m = b * seq + n.  attn is [batch, seq, heads, dim_head]
+ * with element strides attn_strides = {batch, seq, head} (NULL = dense) and a contiguous last
+ * axis: the SDPA output is read through its transposed view.  x[rows, dim], weight[heads, dim],
+ * bias[heads], out[rows, heads * dim_head] and gate[rows, heads] are dense.
+ */
+
+/* fused_band_split.cpp:536-557 attention_gate_forward (.cu:1777-1826, 1922-1971). */
+int pmsst_attention_gate_forward(const void* attn, const int64_t* attn_strides, const void* x, const void* weight,
+                                 const void* bias, void* out, void* gate, int64_t batch, int64_t seq, int64_t heads,
+                                 int64_t dim_head, int64_t dim, int dtype, void* stream);
+/* Workspace bytes of the backward: the stored gate pre-activation gradient plus grad_weight /
+ * grad_bias partials over row chunks. */
+size_t pmsst_attention_gate_backward_workspace_size(int64_t rows, int64_t heads, int64_t dim);
+/* fused_band_split.cpp:559-587 attention_gate_backward (.cu:1828-1920, 1973-2036):
+ * grad_out[rows, heads * dim_head] dense -> grad_attn (strides grad_attn_strides like attn's,
+ * NULL = dense), grad_x[rows, dim], grad_weight[heads, dim], grad_bias[heads]. */
+int pmsst_attention_gate_backward(const void* grad_out, const void* attn, const int64_t* attn_strides, const void* x,
+                                  const void* weight, const void* gate, void* grad_attn,
+                                  const int64_t* grad_attn_strides, void* grad_x, void* grad_weight, void* grad_bias,
+                                  int64_t batch, int64_t seq, int64_t heads, int64_t dim_head, int64_t dim, int dtype,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

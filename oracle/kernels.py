@@ -45,6 +45,8 @@ __all__ = [
     "mask_estimator_final_backward",
     "mask_mlp_forward",
     "mask_mlp_backward",
+    "attention_gate_forward",
+    "attention_gate_backward",
     "sigmoid",
 ]
 
@@ -442,3 +444,37 @@ def mask_mlp_backward(grad_out, x, w1, b1, weights2, bias2, dim_inputs, dt: str,
         [round_to(w, dt) for w in dws2],
         round_to(dbias2, dt),
     )
+
+
+def attention_gate_forward(attn, x, weight, bias, dt: str, acc=np.float64):
+    """Attention output gate (.cu:1777-1826; fr.py:1228-1250).
+
+    ``attn[M,H,Dh]``, ``x[M,D]``, ``weight[H,D]``, ``bias[H]``.
+    ``gate = sigmoid(x W^T + b)`` is stored in the storage dtype (.cu:1805) and the stored
+    value scales the attention output: ``out[m, h*Dh + d] = attn[m,h,d] * gate[m,h]`` (.cu:1823).
+    Returns ``(out[M, H*Dh], gate[M,H])``.
+    """
+    attn = _f(attn, acc)
+    gate = round_to(sigmoid(_f(x, acc) @ _f(weight, acc).T + _f(bias, acc)), dt)
+    out = attn * _f(gate, acc)[:, :, None]
+    return round_to(out.reshape(attn.shape[0], -1), dt), gate
+
+
+def attention_gate_backward(grad_out, attn, x, weight, gate, dt: str, acc=np.float64):
+    """Backward of :func:`attention_gate_forward` (.cu:1828-1920, .cu:1973-2036).
+
+    ``grad_attn = g * gate``; ``gpre = (sum_d g * attn) * gate * (1 - gate)`` stored in the
+    storage dtype (.cu:1862) and used as stored for ``grad_x = gpre W``,
+    ``grad_weight = gpre^T x`` and ``grad_bias = sum_m gpre``.
+    Returns ``(grad_attn[M,H,Dh], grad_x[M,D], grad_weight[H,D], grad_bias[H])``.
+    """
+    attn = _f(attn, acc)
+    m, h, dh = attn.shape
+    g = _f(grad_out, acc).reshape(m, h, dh)
+    gt = _f(gate, acc)
+    grad_attn = g * gt[:, :, None]
+    gpre = _f(round_to((g * attn).sum(axis=2) * gt * (1.0 - gt), dt), acc)
+    grad_x = gpre @ _f(weight, acc)
+    grad_w = gpre.T @ _f(x, acc)
+    grad_b = gpre.sum(axis=0)
+    return round_to(grad_attn, dt), round_to(grad_x, dt), round_to(grad_w, dt), round_to(grad_b, dt)

@@ -84,6 +84,10 @@ __global__ __launch_bounds__(kFwdThreads) void rms_fwd_kernel(const TX* __restri
   }
 }
 
+#ifndef PMSST_RMS_BWD_HALFVEC
+#define PMSST_RMS_BWD_HALFVEC 1
+#endif
+
 // FROM_X: `nsrc` is the forward input x and n = x * inv * scale is recomputed;
 // otherwise `nsrc` is the saved normalised tensor.
 template <typename TDY, typename TN, typename TG, typename TDX, int VEC, int NV, bool GUARD, bool FROM_X>
@@ -245,6 +249,20 @@ int launch_bwd(const void* dy, const void* nsrc, const float* inv_norm, const vo
   RowGeom geo = pick_row_geom(dim, kVec, ptrs, sizes, 4);
   PMSST_REQUIRE(geo.ok, "rms_norm_backward: dim=%lld is not supported (needs dim %% %d == 0 or dim <= 512)",
                 (long long)dim, kVec);
+#if PMSST_RMS_BWD_HALFVEC
+  // Three packs per lane (dim = 3 * 2^k) keep 4 x 3 x kVec fp32 values live per lane, which
+  // caps occupancy at 3 waves per SIMD: half-width packs on twice the lanes halve that.
+  bool half = false;
+  if (geo.vec == kVec && geo.nv == 3 && kVec >= 4) {
+    const RowGeom h = pick_row_geom(dim, kVec / 2, ptrs, sizes, 4);
+    if (h.ok && h.vec == kVec / 2 && h.nv == 3 && h.tpr_log2 == geo.tpr_log2 + 1) {
+      geo = h;
+      half = true;
+    }
+  }
+#else
+  const bool half = false;
+#endif
   const int parts = row_bwd_parts(rows, geo.tpr_log2);
   const size_t need = row_bwd_workspace(dim);
   if (workspace == nullptr || workspace_bytes < need) {
@@ -264,7 +282,9 @@ int launch_bwd(const void* dy, const void* nsrc, const float* inv_norm, const vo
   hipLaunchKernelGGL((rms_bwd_kernel<TDY, TN, TG, TDX, VEC, NV, GUARD, FROM_X>), dim3(parts),             \
                      dim3(kRowBwdThreads), shmem, stream, pdy, pn, inv_norm, pg, pdx, partial, rows,        \
                      static_cast<int>(dim), geo.tpr_log2, scale)
-    if (geo.vec == kVec) {
+    if (half) {
+      PMSST_BWD(kVec / 2, 3, false);
+    } else if (geo.vec == kVec) {
       switch (geo.nv) {
         case 1: PMSST_BWD(kVec, 1, false); break;
         case 2: PMSST_BWD(kVec, 2, false); break;

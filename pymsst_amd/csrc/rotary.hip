@@ -57,39 +57,61 @@ inline int table_mode(const void* cosv, const void* sinv, int64_t cs_seq, int64_
   return kTabAny;
 }
 
+#ifndef PMSST_ROT_UNROLL
+#define PMSST_ROT_UNROLL 1
+#endif
+// Packs per lane per loop trip: all loads of a trip are issued before any use,
+// so each lane keeps kRotUnroll 16-byte packs in flight.
+constexpr int kRotUnroll = PMSST_ROT_UNROLL;
+
 template <typename T, int VEC, bool INVERSE, int TS>
 __global__ __launch_bounds__(kRotThreads) void rotary_kernel(const T* __restrict__ in, const T* __restrict__ cosv,
                                                              const T* __restrict__ sinv, T* __restrict__ out,
                                                              uint32_t total_packs, FastDiv packs_per_token,
                                                              FastDiv seq, FastDiv dim, TableRef tab, BnhStrides si,
                                                              BnhStrides so) {
-  for (uint32_t i = blockIdx.x * kRotThreads + threadIdx.x; i < total_packs; i += gridDim.x * kRotThreads) {
-    const uint32_t tok = packs_per_token.div(i);
-    const uint32_t e = (i - tok * packs_per_token.d) * VEC;  // element offset inside the token
-    const uint32_t b = seq.div(tok);
-    const uint32_t n = tok - b * seq.d;
-    const uint32_t h = dim.div(e);
-    const uint32_t d = e - h * dim.d;
-    const uint32_t p0 = d >> 1;
-    float v[VEC];
-    load_pack<T, VEC>(in + b * si.b + n * si.n + h * si.h + d, v);
-    float cv[VEC / 2], sv[VEC / 2];
-    load_table<T, VEC / 2, TS>(cosv + n * tab.stride_seq, p0, tab.stride_pair, cv);
-    load_table<T, VEC / 2, TS>(sinv + n * tab.stride_seq, p0, tab.stride_pair, sv);
+  constexpr int U = kRotUnroll;
+  const uint32_t trip = gridDim.x * kRotThreads * U;
+  for (uint32_t i0 = blockIdx.x * kRotThreads * U + threadIdx.x; i0 < total_packs; i0 += trip) {
+    float v[U][VEC], cv[U][VEC / 2], sv[U][VEC / 2];
+    int64_t dst[U];
 #pragma unroll
-    for (int j = 0; j < VEC / 2; ++j) {
-      const float c = cv[j];
-      const float s = sv[j];
-      const float ev = v[2 * j], ov = v[2 * j + 1];
-      if (INVERSE) {
-        v[2 * j] = ev * c + ov * s;
-        v[2 * j + 1] = ov * c - ev * s;
+    for (int u = 0; u < U; ++u) {
+      const uint32_t i = i0 + u * kRotThreads;
+      if (i < total_packs) {
+        const uint32_t tok = packs_per_token.div(i);
+        const uint32_t e = (i - tok * packs_per_token.d) * VEC;  // element offset inside the token
+        const uint32_t b = seq.div(tok);
+        const uint32_t n = tok - b * seq.d;
+        const uint32_t h = dim.div(e);
+        const uint32_t d = e - h * dim.d;
+        const uint32_t p0 = d >> 1;
+        load_pack<T, VEC>(in + b * si.b + n * si.n + h * si.h + d, v[u]);
+        load_table<T, VEC / 2, TS>(cosv + n * tab.stride_seq, p0, tab.stride_pair, cv[u]);
+        load_table<T, VEC / 2, TS>(sinv + n * tab.stride_seq, p0, tab.stride_pair, sv[u]);
+        dst[u] = b * so.b + n * so.n + h * so.h + d;
       } else {
-        v[2 * j] = ev * c - ov * s;
-        v[2 * j + 1] = ov * c + ev * s;
+        dst[u] = -1;
       }
     }
-    store_pack<T, VEC>(out + b * so.b + n * so.n + h * so.h + d, v);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (dst[u] < 0) continue;
+#pragma unroll
+      for (int j = 0; j < VEC / 2; ++j) {
+        const float c = cv[u][j];
+        const float s = sv[u][j];
+        const float ev = v[u][2 * j], ov = v[u][2 * j + 1];
+        if (INVERSE) {
+          v[u][2 * j] = ev * c + ov * s;
+          v[u][2 * j + 1] = ov * c - ev * s;
+        } else {
+          v[u][2 * j] = ev * c - ov * s;
+          v[u][2 * j + 1] = ov * c + ev * s;
+        }
+      }
+      store_pack<T, VEC>(out + dst[u], v[u]);
+    }
   }
 }
 
@@ -124,7 +146,7 @@ int launch_rotary(const void* in, const int64_t* in_strides, const void* cosv, c
   const FastDiv fseq(static_cast<uint32_t>(seq));
   const FastDiv fdim(static_cast<uint32_t>(dim));
   const TableRef tab{cs_seq, cs_pair};
-  const int64_t blocks64 = (packs + kRotThreads - 1) / kRotThreads;
+  const int64_t blocks64 = (packs + kRotThreads * kRotUnroll - 1) / (kRotThreads * kRotUnroll);
   const int blocks = static_cast<int>(blocks64 < 65536 ? blocks64 : 65536);
   const T* pin = static_cast<const T*>(in);
   const T* pc = static_cast<const T*>(cosv);
@@ -159,7 +181,10 @@ int launch_rotary(const void* in, const int64_t* in_strides, const void* cosv, c
 
 // Rows per lane slot in flight: the loads of kRowsPerSlot rows are issued before any
 // reduction, so each lane keeps several 16-byte packs outstanding.
-constexpr int kRowsPerSlot = 2;
+#ifndef PMSST_NR_ROWS
+#define PMSST_NR_ROWS 2
+#endif
+constexpr int kRowsPerSlot = PMSST_NR_ROWS;
 
 template <typename T, typename TG, int VEC, int NV, int TS>
 __global__ __launch_bounds__(kNormRotThreads) void norm_rot_fwd_kernel(

@@ -6,9 +6,15 @@
 
 namespace pmsst {
 
-constexpr int kRowBwdThreads = 512;
+#ifndef PMSST_ROW_BWD_THREADS
+#define PMSST_ROW_BWD_THREADS 512
+#endif
+constexpr int kRowBwdThreads = PMSST_ROW_BWD_THREADS;
 // Upper bound on backward blocks; the dgamma workspace is kRowBwdMaxParts * dim fp32.
-constexpr int kRowBwdMaxParts = 1024;
+#ifndef PMSST_ROW_BWD_MAX_PARTS
+#define PMSST_ROW_BWD_MAX_PARTS 1024
+#endif
+constexpr int kRowBwdMaxParts = PMSST_ROW_BWD_MAX_PARTS;
 
 struct RowGeom {
   int vec;       // elements per pack (1 = scalar path with column guards)

@@ -322,6 +322,118 @@ class HipFusedExtension:
         return [dx, dgamma]
 
 
+    # ------------------------------------------------------------------ attention gate
+
+    @staticmethod
+    def _gate_common_checks(attn, x, weight):
+        _req(attn.size(-2) == weight.size(0), "attn heads must match weight")
+        _req(weight.size(1) == x.size(1), "weight input dimension must match x")
+        _req(x.dtype == attn.dtype, "x dtype must match attn")
+        _req(weight.dtype == attn.dtype, "weight dtype must match attn")
+
+    def _gate_fwd(self, attn4, x, weight, bias):
+        if attn4.stride(3) != 1:
+            attn4 = attn4.contiguous()
+        x, weight, bias = x.contiguous(), weight.contiguous(), bias.contiguous()
+        b, n, h, dh = attn4.shape
+        out = torch.empty((b * n, h * dh), dtype=attn4.dtype, device=attn4.device)
+        gate = torch.empty((b * n, h), dtype=attn4.dtype, device=attn4.device)
+        st = (ctypes.c_int64 * 3)(attn4.stride(0), attn4.stride(1), attn4.stride(2))
+        with _DeviceGuard(attn4.device):
+            rc = self._lib.pmsst_attention_gate_forward(
+                _ptr(attn4), st, _ptr(x), _ptr(weight), _ptr(bias), _ptr(out), _ptr(gate), b, n, h, dh, x.size(1),
+                dtype_code(attn4.dtype), _stream(attn4.device),
+            )
+        check(rc, "pmsst_attention_gate_forward")
+        return out, gate, attn4, x
+
+    def _gate_bwd(self, grad_out, attn4, x, weight, gate, out_layout):
+        if attn4.stride(3) != 1:
+            attn4 = attn4.contiguous()
+        grad_out, x, weight, gate = grad_out.contiguous(), x.contiguous(), weight.contiguous(), gate.contiguous()
+        b, n, h, dh = attn4.shape
+        if out_layout == "bhnd":
+            grad_attn = torch.empty((b, h, n, dh), dtype=attn4.dtype, device=attn4.device).transpose(1, 2)
+        else:
+            grad_attn = torch.empty((b, n, h, dh), dtype=attn4.dtype, device=attn4.device)
+        grad_x = torch.empty_like(x)
+        grad_weight = torch.empty_like(weight)
+        grad_bias = torch.empty((h,), dtype=attn4.dtype, device=attn4.device)
+        ws = _workspace(self._lib.pmsst_attention_gate_backward_workspace_size(b * n, h, x.size(1)), attn4.device)
+        ast = (ctypes.c_int64 * 3)(attn4.stride(0), attn4.stride(1), attn4.stride(2))
+        gst = (ctypes.c_int64 * 3)(grad_attn.stride(0), grad_attn.stride(1), grad_attn.stride(2))
+        with _DeviceGuard(attn4.device):
+            rc = self._lib.pmsst_attention_gate_backward(
+                _ptr(grad_out), _ptr(attn4), ast, _ptr(x), _ptr(weight), _ptr(gate), _ptr(grad_attn), gst,
+                _ptr(grad_x), _ptr(grad_weight), _ptr(grad_bias), b, n, h, dh, x.size(1), dtype_code(attn4.dtype),
+                _ptr(ws), ws.numel(), _stream(attn4.device),
+            )
+        check(rc, "pmsst_attention_gate_backward")
+        return grad_attn, grad_x, grad_weight, grad_bias
+
+    def attention_gate_forward(self, attn, x, weight, bias):
+        """``.cpp:536-557``: ``attn[M,H,Dh]``, ``x[M,D]``, ``weight[H,D]``, ``bias[H]`` ->
+        ``[out[M, H*Dh], gate[M,H], attn, x]`` (the last two are what backward takes)."""
+        _req(attn.is_cuda, "attn must be a CUDA tensor")
+        _req(x.is_cuda, "x must be a CUDA tensor")
+        _req(weight.is_cuda, "weight must be a CUDA tensor")
+        _req(bias.is_cuda, "bias must be a CUDA tensor")
+        _req(attn.dim() == 3, "attn must have shape [M, H, DH]")
+        _req(x.dim() == 2, "x must have shape [M, D]")
+        _req(weight.dim() == 2, "weight must have shape [H, D]")
+        _req(bias.dim() == 1, "bias must have shape [H]")
+        _req(attn.size(0) == x.size(0), "attn and x row counts must match")
+        self._gate_common_checks(attn, x, weight)
+        _req(bias.size(0) == weight.size(0), "bias heads must match weight")
+        _req(bias.dtype == attn.dtype, "bias dtype must match attn")
+        out, gate, a4, xs = self._gate_fwd(attn.unsqueeze(0), x, weight, bias)
+        return [out, gate, a4.squeeze(0), xs]
+
+    def attention_gate_backward(self, grad_out, attn, x, weight, gate):
+        """``.cpp:559-587``: returns ``[grad_attn[M,H,Dh], grad_x[M,D], grad_weight[H,D], grad_bias[H]]``."""
+        _req(grad_out.is_cuda, "grad_out must be a CUDA tensor")
+        _req(attn.is_cuda, "attn must be a CUDA tensor")
+        _req(x.is_cuda, "x must be a CUDA tensor")
+        _req(weight.is_cuda, "weight must be a CUDA tensor")
+        _req(gate.is_cuda, "gate must be a CUDA tensor")
+        _req(grad_out.dim() == 2, "grad_out must have shape [M, H*DH]")
+        _req(attn.dim() == 3, "attn must have shape [M, H, DH]")
+        _req(x.dim() == 2, "x must have shape [M, D]")
+        _req(weight.dim() == 2, "weight must have shape [H, D]")
+        _req(gate.dim() == 2, "gate must have shape [M, H]")
+        _req(grad_out.size(0) == attn.size(0), "grad_out rows must match attn")
+        _req(grad_out.size(1) == attn.size(1) * attn.size(2), "grad_out columns must match flattened attn")
+        _req(attn.size(0) == x.size(0), "attn and x row counts must match")
+        _req(gate.size(0) == attn.size(0), "gate rows must match attn")
+        _req(gate.size(1) == attn.size(1), "gate heads must match attn")
+        _req(attn.dtype == grad_out.dtype, "attn dtype must match grad_out")
+        self._gate_common_checks(attn, x, weight)
+        _req(gate.dtype == grad_out.dtype, "gate dtype must match grad_out")
+        ga, gx, gw, gb = self._gate_bwd(grad_out, attn.unsqueeze(0), x, weight, gate, "bnhd")
+        return [ga.squeeze(0), gx, gw, gb]
+
+    def attention_gate_forward_bnhd(self, attn, x, weight, bias):
+        """Build addition: :meth:`attention_gate_forward` on ``attn[B,N,H,Dh]`` with any strides and a
+        contiguous last axis (the transposed SDPA output, read in place); ``x[B*N, D]``."""
+        _req(attn.is_cuda and attn.dim() == 4, "attn must be a CUDA tensor of shape [B, N, H, DH]")
+        _req(x.is_cuda and x.dim() == 2 and x.size(0) == attn.size(0) * attn.size(1), "x must have shape [B*N, D]")
+        _req(weight.is_cuda and weight.dim() == 2 and bias.is_cuda and bias.dim() == 1, "bad weight/bias")
+        self._gate_common_checks(attn, x, weight)
+        _req(bias.size(0) == weight.size(0) and bias.dtype == attn.dtype, "bias must be [H] in attn's dtype")
+        return list(self._gate_fwd(attn, x, weight, bias))
+
+    def attention_gate_backward_bnhd(self, grad_out, attn, x, weight, gate, out_layout="bhnd"):
+        """Build addition: backward of :meth:`attention_gate_forward_bnhd`; ``grad_attn`` comes back
+        ``[B,N,H,Dh]``-shaped, by default as the transpose of a dense ``[B,H,N,Dh]`` buffer (the layout
+        SDPA's backward reads)."""
+        _req(grad_out.is_cuda and grad_out.dim() == 2, "grad_out must have shape [B*N, H*DH]")
+        _req(grad_out.size(0) == attn.size(0) * attn.size(1) and grad_out.size(1) == attn.size(2) * attn.size(3),
+             "grad_out must match attn")
+        _req(gate.dtype == grad_out.dtype == attn.dtype, "gate/grad_out dtype must match attn")
+        self._gate_common_checks(attn, x, weight)
+        _req(out_layout in ("bhnd", "bnhd"), f"unsupported out_layout {out_layout!r}")
+        return list(self._gate_bwd(grad_out, attn, x, weight, gate, out_layout))
+
     # ------------------------------------------------------------------ band split
 
     def _bands(self, dim_inputs, device: torch.device):

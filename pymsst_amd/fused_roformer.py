@@ -79,6 +79,7 @@ RUNTIME_PRESETS["hip_full"] = {
     **RUNTIME_PRESETS["train_fragmentation"],
     EXPERIMENTAL_ROTARY_ENV: "1",
     EXPERIMENTAL_FUSED_MASK_MLP_ENV: "1",
+    EXPERIMENTAL_ATTENTION_GATES_ENV: "1",
 }
 
 
@@ -391,9 +392,46 @@ def _patch_core_rms_norm(ext: Any, mode: str, *, use_bwd_v2: bool = False) -> bo
 
 
 def _patch_core_attention_gates(ext: Any, mode: str) -> bool:
-    """The reference's attention-gate fusion (fr.py:776-824) is outside this build's kernel set,
-    so the flag is accepted and reported as not patched."""
-    return False
+    """Class-level ``Attention.forward`` replacement (fr.py:776-824): the gate Linear, sigmoid and
+    multiply after SDPA run as one fused op; the rest of the block is the stock forward."""
+    if mode != "full":
+        return False
+    if any(not hasattr(ext, name) for name in ("attention_gate_forward", "attention_gate_backward")):
+        return False
+    _, transformer, _ = _core()
+    if getattr(transformer.Attention.forward, "_pymsst_fused_attention_gates", False):
+        return True
+    original = transformer.Attention.forward
+
+    def attention_forward_cuda_ext(self, x):
+        if (
+            not self.training
+            or x.device.type != "cuda"
+            or x.dtype not in _FLOAT_TYPES
+            or self.to_gates.bias is None
+        ):
+            return original(self, x)
+        x = self.norm(x)
+        q, k, v = transformer.qkv_to_bnhd(self.to_qkv(x), self.heads)
+        if self.rotary_embed is not None:
+            q, k = transformer.rotate_qk_fast_bnhd(self.rotary_embed, q, k)
+        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        out = self._attention(q, k, v).transpose(1, 2)
+        gate_dtype = out.dtype
+        gated = _FusedAttentionGate.apply(
+            out,
+            x.to(dtype=gate_dtype),
+            self.to_gates.weight.to(dtype=gate_dtype),
+            self.to_gates.bias.to(dtype=gate_dtype),
+            ext,
+        )
+        return self.to_out(gated)
+
+    attention_forward_cuda_ext._pymsst_fused_attention_gates = True
+    attention_forward_cuda_ext._pymsst_fused_attention_gate_mode = mode
+    attention_forward_cuda_ext._pymsst_original_forward = original
+    transformer.Attention.forward = attention_forward_cuda_ext
+    return True
 
 
 def _patch_core_grouped_linear(ext: Any) -> bool:
@@ -1012,6 +1050,45 @@ class _FusedMaskMLP(torch.autograd.Function):
         return dx, dw1, db1, dw2, db2, None, None
 
 
+class _FusedAttentionGate(torch.autograd.Function):
+    """fr.py:1228-1262.  With an extension that reads ``[B,N,H,Dh]`` views in place
+    (``attention_gate_forward_bnhd``), the transposed SDPA output is not copied and the attn
+    gradient comes back in the ``[B,H,N,Dh]`` layout SDPA's backward reads."""
+
+    @staticmethod
+    def forward(ctx, attn, x, weight, bias, extension):
+        heads, dim_head = attn.shape[-2], attn.shape[-1]
+        x_2d = x.reshape(-1, x.shape[-1])
+        bnhd = attn.dim() == 4 and hasattr(extension, "attention_gate_forward_bnhd")
+        if bnhd:
+            out, gate, saved_attn, saved_x = extension.attention_gate_forward_bnhd(attn, x_2d, weight, bias)
+        else:
+            out, gate, saved_attn, saved_x = extension.attention_gate_forward(
+                attn.reshape(-1, heads, dim_head), x_2d, weight, bias
+            )
+        ctx.attn_shape = tuple(attn.shape)
+        ctx.x_shape = tuple(x.shape)
+        ctx.bnhd = bnhd
+        ctx.save_for_backward(saved_attn, saved_x, weight, gate)
+        ctx.extension = extension
+        return out.reshape(*x.shape[:-1], heads * dim_head)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        saved_attn, saved_x, weight, gate = ctx.saved_tensors
+        rows = gate.shape[0]
+        grad_out_2d = grad_out.reshape(rows, -1)
+        if ctx.bnhd:
+            grad_attn, grad_x, grad_weight, grad_bias = ctx.extension.attention_gate_backward_bnhd(
+                grad_out_2d, saved_attn, saved_x, weight, gate
+            )
+        else:
+            grad_attn, grad_x, grad_weight, grad_bias = ctx.extension.attention_gate_backward(
+                grad_out_2d, saved_attn, saved_x, weight, gate
+            )
+        return grad_attn.reshape(ctx.attn_shape), grad_x.reshape(ctx.x_shape), grad_weight, grad_bias, None
+
+
 class _FusedRotary(torch.autograd.Function):
     """fr.py:1154-1166; ``cos``/``sin`` are the ``[..., ::2]`` views (no copy is made)."""
 
@@ -1117,6 +1194,7 @@ _CORE_PATCH_POINTS = (
     # (module in pymsst_amd.core, owner attribute or None, patched name, marker of the saved original)
     ("transformer", None, "apply_rotary_emb_fast", "_pymsst_original_apply_rotary"),
     ("transformer", "RMSNorm", "forward", "_pymsst_original_forward"),
+    ("transformer", "Attention", "forward", "_pymsst_original_forward"),
     ("bands", None, "grouped_linear", "_pymsst_original_grouped_linear"),
     ("bands", "MaskEstimator", "_forward_layer_grouped_mlp", "_pymsst_original_forward_layer_grouped_mlp"),
     ("bands", "MaskEstimator", "_get_layer_group_params", "_pymsst_original_get_layer_group_params"),

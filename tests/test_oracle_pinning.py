@@ -341,3 +341,48 @@ def test_tanh_hidden_pieces_compose_to_mask_mlp_autograd():
     dz_bad, _, _ = oracle.mask_estimator_final_backward(g, h, pre, w2, dim_inputs, "f64")
     dx_bad, _, _ = oracle.grouped_linear_backward(dz_bad, x, w1, True, "f64")
     assert np.max(np.abs(dx_bad - tx.grad.numpy())) > 1e-3
+
+
+@pytest.mark.parametrize("m,h,dh,d", [(7, 8, 64, 192), (5, 4, 32, 64), (3, 3, 5, 7)])
+def test_attention_gate_vs_autograd(m, h, dh, d):
+    r = _rng(15)
+    attn = r.standard_normal((m, h, dh))
+    x = r.standard_normal((m, d))
+    w = r.standard_normal((h, d)) / math.sqrt(d)
+    b = r.standard_normal(h)
+    out, gate = oracle.attention_gate_forward(attn, x, w, b, "f64")
+    ta, tx, tw, tb = _t(attn, True), _t(x, True), _t(w, True), _t(b, True)
+    ref = tr.attention_gate(ta, tx, tw, tb)
+    _close(out, ref, what="out")
+    g = r.standard_normal((m, h * dh))
+    ref.backward(_t(g))
+    ga, gx, gw, gb = oracle.attention_gate_backward(g, attn, x, w, gate, "f64")
+    _close(ga, ta.grad, what="grad_attn")
+    _close(gx, tx.grad, what="grad_x")
+    _close(gw, tw.grad, what="grad_weight")
+    _close(gb, tb.grad, what="grad_bias")
+
+
+def test_attention_gate_rounding_points():
+    """bf16: the stored gate (not the fp32 sigmoid) scales attn, and the stored gate
+    pre-activation gradient feeds grad_x/grad_weight/grad_bias.  A planted variant that
+    rounds only the outputs differs from the oracle on these inputs, so the check has teeth."""
+    r = _rng(16)
+    m, h, dh, d = 64, 8, 64, 192
+    attn = oracle.round_to(r.standard_normal((m, h, dh)), "bf16")
+    x = oracle.round_to(r.standard_normal((m, d)), "bf16")
+    w = oracle.round_to(r.standard_normal((h, d)) / math.sqrt(d), "bf16")
+    b = oracle.round_to(r.standard_normal(h), "bf16")
+    out, gate = oracle.attention_gate_forward(attn, x, w, b, "bf16")
+    # the stored gate is a bf16 value and out is exactly round(attn * gate)
+    assert np.array_equal(gate, oracle.round_to(gate, "bf16"))
+    assert np.array_equal(out, oracle.round_to((attn * gate[:, :, None]).reshape(m, -1), "bf16"))
+    exact = oracle.sigmoid(x @ w.T + b)
+    planted = oracle.round_to((attn * exact[:, :, None]).reshape(m, -1), "bf16")
+    assert not np.array_equal(planted, out)
+    g = oracle.round_to(r.standard_normal((m, h * dh)), "bf16")
+    ga, gx, gw, gb = oracle.attention_gate_backward(g, attn, x, w, gate, "bf16")
+    gpre = oracle.round_to((g.reshape(m, h, dh) * attn).sum(2) * gate * (1 - gate), "bf16")
+    assert np.array_equal(gb, oracle.round_to(gpre.sum(0), "bf16"))
+    unrounded = ((g.reshape(m, h, dh) * attn).sum(2) * gate * (1 - gate)).sum(0)
+    assert not np.array_equal(oracle.round_to(unrounded, "bf16"), gb)

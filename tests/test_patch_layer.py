@@ -269,3 +269,72 @@ def test_cpu_inputs_take_the_stock_path_after_patching(monkeypatch):
     fr.apply_roformer_fused_training_backend(model, "hip", extension=ext, rms_norm_mode="fast")
     got = model(mixture, target)
     assert torch.equal(got, ref)
+
+
+class _OracleGateExt:
+    """CPU stand-in with the attention-gate op names, computing through the numpy oracle."""
+
+    def __init__(self, bnhd: bool):
+        if bnhd:
+            self.attention_gate_forward_bnhd = self._fwd4
+            self.attention_gate_backward_bnhd = self._bwd4
+
+    @staticmethod
+    def _np(t):
+        return t.detach().double().numpy()
+
+    def attention_gate_forward(self, attn, x, weight, bias):
+        import oracle
+
+        out, gate = oracle.attention_gate_forward(self._np(attn), self._np(x), self._np(weight), self._np(bias), "f64")
+        return [torch.from_numpy(out), torch.from_numpy(gate), attn, x]
+
+    def attention_gate_backward(self, grad_out, attn, x, weight, gate):
+        import oracle
+
+        res = oracle.attention_gate_backward(self._np(grad_out), self._np(attn), self._np(x), self._np(weight),
+                                             self._np(gate), "f64")
+        return [torch.from_numpy(r) for r in res]
+
+    def _fwd4(self, attn, x, weight, bias):
+        out, gate, _, _ = self.attention_gate_forward(attn.reshape(-1, *attn.shape[2:]), x, weight, bias)
+        return [out, gate, attn, x]
+
+    def _bwd4(self, grad_out, attn, x, weight, gate):
+        ga, gx, gw, gb = self.attention_gate_backward(grad_out, attn.reshape(-1, *attn.shape[2:]), x, weight, gate)
+        return [ga.reshape(attn.shape), gx, gw, gb]
+
+
+@pytest.mark.parametrize("bnhd", [False, True])
+def test_fused_attention_gate_function_matches_autograd(bnhd):
+    from tests import torch_reference as tr
+
+    g = torch.Generator().manual_seed(3)
+    b, n, h, dh, d = 2, 5, 4, 8, 12
+    attn = torch.randn(b, h, n, dh, generator=g, dtype=torch.float64).transpose(1, 2).requires_grad_()
+    x = torch.randn(b, n, d, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(h, d, generator=g, dtype=torch.float64, requires_grad=True)
+    bias = torch.randn(h, generator=g, dtype=torch.float64, requires_grad=True)
+    out = fr._FusedAttentionGate.apply(attn, x, w, bias, _OracleGateExt(bnhd))
+    assert out.shape == (b, n, h * dh)
+    gout = torch.randn(out.shape, generator=g, dtype=torch.float64)
+    grads = torch.autograd.grad(out, (attn, x, w, bias), gout)
+    ref = tr.attention_gate(attn.reshape(b * n, h, dh), x.reshape(b * n, d), w, bias).reshape(b, n, -1)
+    torch.testing.assert_close(out, ref)
+    rgrads = torch.autograd.grad(ref, (attn, x, w, bias), gout)
+    for got, want in zip(grads, rgrads):
+        torch.testing.assert_close(got, want)
+
+
+def test_attention_gate_patch_and_restore(monkeypatch):
+    original = transformer.Attention.forward
+    ext = _OracleGateExt(True)
+    monkeypatch.setenv(fr.EXPERIMENTAL_ATTENTION_GATES_ENV, "gate")
+    status = fr.apply_roformer_fused_training_backend(_small_model(), "hip", extension=ext)
+    assert status.patched_attention_gates and status.attention_gate_mode == "full"
+    assert getattr(transformer.Attention.forward, "_pymsst_fused_attention_gates", False)
+    fr.restore_stock_implementations()
+    assert transformer.Attention.forward is original
+    monkeypatch.setenv(fr.EXPERIMENTAL_ATTENTION_GATES_ENV, "off")
+    status = fr.apply_roformer_fused_training_backend(_small_model(), "hip", extension=ext)
+    assert not status.patched_attention_gates and status.attention_gate_mode is None

@@ -11,6 +11,8 @@ hand-derived backward:
 * Grouped linear: ``_reference_grouped_linear`` bmm/baddbmm (tests/test_training_smoke.py:28-37).
 * Mask final: per-band ``F.linear`` + ``F.glu`` (tests/test_training_smoke.py:574-615).
 * Rotary: multiplication of ``t[2p] + i t[2p+1]`` by ``exp(i angle)``.
+* Attention gate: the stock ``Attention`` tail, ``out * to_gates(x).sigmoid().unsqueeze(-1)``
+  with ``to_gates = nn.Linear(dim, heads)`` (fused_roformer.py:776-824 patches it).
 """
 
 from __future__ import annotations
@@ -72,3 +74,9 @@ def mask_final(x, weights, bias, dim_inputs):
 def mask_mlp(x, w1, b1, weights2, bias2, dim_inputs):
     h = torch.tanh(grouped_linear(x, w1, b1))
     return mask_final(h, weights2, bias2, dim_inputs)
+
+
+def attention_gate(attn, x, weight, bias):
+    """``attn[M,H,Dh] * sigmoid(F.linear(x, weight, bias))[..., None]`` flattened to ``[M, H*Dh]``."""
+    gates = torch.sigmoid(F.linear(x, weight, bias))
+    return (attn * gates.unsqueeze(-1)).reshape(attn.shape[0], -1)
