@@ -111,6 +111,21 @@ int pmsst_rotary_backward(const void* grad_out, const int64_t* grad_out_strides,
                           void* grad_t, const int64_t* grad_t_strides, int64_t batch, int64_t seq, int64_t heads,
                           int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype, void* stream);
 
+/* No reference counterpart: q, k and v of one fused qkv projection in one launch (the
+ * reference's rotary patch, fr.py:710-732, rotates q and k in two calls and leaves the split
+ * and the gradient stacking of qkv_to_bnhd to torch).  q and k are rotated, v is copied.
+ * in_strides / out_strides: three {batch, seq, head} element-stride triples (q, k, v order;
+ * NULL = dense bnhd).  The backward applies the transpose rotation to grad_q / grad_k and copies
+ * grad_v, typically into the three slices of the qkv gradient. */
+int pmsst_rotary_qkv_forward(const void* q, const void* k, const void* v, const int64_t* in_strides, const void* cos,
+                             const void* sin, void* q_out, void* k_out, void* v_out, const int64_t* out_strides,
+                             int64_t batch, int64_t seq, int64_t heads, int64_t dim, int64_t cs_stride_seq,
+                             int64_t cs_stride_pair, int dtype, void* stream);
+int pmsst_rotary_qkv_backward(const void* grad_q, const void* grad_k, const void* grad_v, const int64_t* grad_strides,
+                              const void* cos, const void* sin, void* grad_q_in, void* grad_k_in, void* grad_v_in,
+                              const int64_t* grad_in_strides, int64_t batch, int64_t seq, int64_t heads, int64_t dim,
+                              int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype, void* stream);
+
 /* Fused q/k RMSNorm over the head dim + rotary + cast (no reference counterpart; composition of
  * .cu:1399-1438 and .cu:1076-1101 with no intermediate round trip).  x/out/cos/sin in `dtype`,
  * gamma[dim] in `gamma_dtype`; writes inv_norm[batch*seq*heads]. */

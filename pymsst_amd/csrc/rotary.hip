@@ -1,7 +1,9 @@
 // Rotary embedding on bnhd q/k, and the fused q/k RMSNorm + rotary + cast.
 //
 // Rotary is a pure stream: each lane moves one 16-byte pack (VEC elements,
-// VEC/2 adjacent pairs) per step.  The pack's (batch, position, head, element)
+// VEC/2 adjacent pairs) per step.  One launch can carry q, k and v of a fused qkv
+// projection (v copied): the split into the attention layout, and in the backward
+// the stacking of the three gradients back into the qkv gradient, cost no extra pass.  The pack's (batch, position, head, element)
 // come from multiply-shift divisions; cos/sin rows (seq x dim/2, a few KB) stay
 // in L1/L2.  Input and output take independent (batch, seq, head) strides, so
 // q/k are read straight out of the fused qkv projection and can be written in
@@ -57,85 +59,93 @@ inline int table_mode(const void* cosv, const void* sinv, int64_t cs_seq, int64_
   return kTabAny;
 }
 
-#ifndef PMSST_ROT_UNROLL
-#define PMSST_ROT_UNROLL 1
-#endif
-// Packs per lane per loop trip: all loads of a trip are issued before any use,
-// so each lane keeps kRotUnroll 16-byte packs in flight.
-constexpr int kRotUnroll = PMSST_ROT_UNROLL;
+// Up to three [B, N, H, D] tensors per launch, one per blockIdx.y: parts [0, rotated) are
+// rotated, the others copied (v next to q and k when a fused qkv buffer is split).
+template <typename T>
+struct RotParts {
+  const T* in[3];
+  T* out[3];
+  BnhStrides si[3];
+  BnhStrides so[3];
+  int rotated;
+};
 
 template <typename T, int VEC, bool INVERSE, int TS>
-__global__ __launch_bounds__(kRotThreads) void rotary_kernel(const T* __restrict__ in, const T* __restrict__ cosv,
-                                                             const T* __restrict__ sinv, T* __restrict__ out,
-                                                             uint32_t total_packs, FastDiv packs_per_token,
-                                                             FastDiv seq, FastDiv dim, TableRef tab, BnhStrides si,
-                                                             BnhStrides so) {
-  constexpr int U = kRotUnroll;
-  const uint32_t trip = gridDim.x * kRotThreads * U;
-  for (uint32_t i0 = blockIdx.x * kRotThreads * U + threadIdx.x; i0 < total_packs; i0 += trip) {
-    float v[U][VEC], cv[U][VEC / 2], sv[U][VEC / 2];
-    int64_t dst[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t i = i0 + u * kRotThreads;
-      if (i < total_packs) {
-        const uint32_t tok = packs_per_token.div(i);
-        const uint32_t e = (i - tok * packs_per_token.d) * VEC;  // element offset inside the token
-        const uint32_t b = seq.div(tok);
-        const uint32_t n = tok - b * seq.d;
-        const uint32_t h = dim.div(e);
-        const uint32_t d = e - h * dim.d;
-        const uint32_t p0 = d >> 1;
-        load_pack<T, VEC>(in + b * si.b + n * si.n + h * si.h + d, v[u]);
-        load_table<T, VEC / 2, TS>(cosv + n * tab.stride_seq, p0, tab.stride_pair, cv[u]);
-        load_table<T, VEC / 2, TS>(sinv + n * tab.stride_seq, p0, tab.stride_pair, sv[u]);
-        dst[u] = b * so.b + n * so.n + h * so.h + d;
-      } else {
-        dst[u] = -1;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (dst[u] < 0) continue;
+__global__ __launch_bounds__(kRotThreads) void rotary_kernel(RotParts<T> io, const T* __restrict__ cosv,
+                                                             const T* __restrict__ sinv, uint32_t part_packs,
+                                                             FastDiv packs_per_token, FastDiv seq, FastDiv dim,
+                                                             TableRef tab) {
+  const int part = blockIdx.y;
+  const T* __restrict__ in = io.in[part];
+  T* __restrict__ out = io.out[part];
+  const BnhStrides si = io.si[part];
+  const BnhStrides so = io.so[part];
+  const bool rotate = part < io.rotated;
+  for (uint32_t i = blockIdx.x * kRotThreads + threadIdx.x; i < part_packs; i += gridDim.x * kRotThreads) {
+    const uint32_t tok = packs_per_token.div(i);
+    const uint32_t e = (i - tok * packs_per_token.d) * VEC;  // element offset inside the token
+    const uint32_t b = seq.div(tok);
+    const uint32_t n = tok - b * seq.d;
+    const uint32_t h = dim.div(e);
+    const uint32_t d = e - h * dim.d;
+    float v[VEC];
+    load_pack<T, VEC>(in + b * si.b + n * si.n + h * si.h + d, v);
+    if (rotate) {
+      float cv[VEC / 2], sv[VEC / 2];
+      load_table<T, VEC / 2, TS>(cosv + n * tab.stride_seq, d >> 1, tab.stride_pair, cv);
+      load_table<T, VEC / 2, TS>(sinv + n * tab.stride_seq, d >> 1, tab.stride_pair, sv);
 #pragma unroll
       for (int j = 0; j < VEC / 2; ++j) {
-        const float c = cv[u][j];
-        const float s = sv[u][j];
-        const float ev = v[u][2 * j], ov = v[u][2 * j + 1];
+        const float c = cv[j];
+        const float s = sv[j];
+        const float ev = v[2 * j], ov = v[2 * j + 1];
         if (INVERSE) {
-          v[u][2 * j] = ev * c + ov * s;
-          v[u][2 * j + 1] = ov * c - ev * s;
+          v[2 * j] = ev * c + ov * s;
+          v[2 * j + 1] = ov * c - ev * s;
         } else {
-          v[u][2 * j] = ev * c - ov * s;
-          v[u][2 * j + 1] = ov * c + ev * s;
+          v[2 * j] = ev * c - ov * s;
+          v[2 * j + 1] = ov * c + ev * s;
         }
       }
-      store_pack<T, VEC>(out + dst[u], v[u]);
     }
+    store_pack<T, VEC>(out + b * so.b + n * so.n + h * so.h + d, v);
   }
 }
 
+// `nparts` tensors of one [batch, seq, heads, dim] shape; strides are {b, n, h} triples (NULL
+// = dense bnhd); the first `rotated` parts are rotated, the rest copied.
 template <typename T>
-int launch_rotary(const void* in, const int64_t* in_strides, const void* cosv, const void* sinv, void* out,
-                  const int64_t* out_strides, int64_t batch, int64_t seq, int64_t heads, int64_t dim, int64_t cs_seq,
-                  int64_t cs_pair, bool inverse, hipStream_t stream) {
-  const char* op = inverse ? "rotary_backward" : "rotary_forward";
+int launch_rotary_parts(const char* op, int nparts, int rotated, const void* const* in,
+                        const int64_t* const* in_strides, const void* cosv, const void* sinv, void* const* out,
+                        const int64_t* const* out_strides, int64_t batch, int64_t seq, int64_t heads, int64_t dim,
+                        int64_t cs_seq, int64_t cs_pair, bool inverse, hipStream_t stream) {
   PMSST_REQUIRE(batch >= 0 && seq >= 0 && heads >= 0 && dim > 0 && dim % 2 == 0,
                 "%s: bad shape [%lld, %lld, %lld, %lld]", op, (long long)batch, (long long)seq, (long long)heads,
                 (long long)dim);
   const int64_t total = batch * seq * heads * dim;
   if (total == 0) return PMSST_OK;
-  PMSST_REQUIRE(in && cosv && sinv && out, "%s: null pointer", op);
+  PMSST_REQUIRE(cosv && sinv, "%s: null pointer", op);
+  RotParts<T> io{};
+  io.rotated = rotated;
   const BnhStrides dense{seq * heads * dim, heads * dim, dim};
-  const BnhStrides si = in_strides ? BnhStrides{in_strides[0], in_strides[1], in_strides[2]} : dense;
-  const BnhStrides so = out_strides ? BnhStrides{out_strides[0], out_strides[1], out_strides[2]} : dense;
-  PMSST_REQUIRE(si.b >= 0 && si.n >= 0 && si.h >= 0 && so.b >= 0 && so.n >= 0 && so.h >= 0, "%s: negative stride",
-                op);
+  for (int p = 0; p < nparts; ++p) {
+    PMSST_REQUIRE(in[p] && out[p], "%s: null pointer", op);
+    io.in[p] = static_cast<const T*>(in[p]);
+    io.out[p] = static_cast<T*>(out[p]);
+    io.si[p] = in_strides[p] ? BnhStrides{in_strides[p][0], in_strides[p][1], in_strides[p][2]} : dense;
+    io.so[p] = out_strides[p] ? BnhStrides{out_strides[p][0], out_strides[p][1], out_strides[p][2]} : dense;
+    PMSST_REQUIRE(io.si[p].b >= 0 && io.si[p].n >= 0 && io.si[p].h >= 0 && io.so[p].b >= 0 && io.so[p].n >= 0 &&
+                      io.so[p].h >= 0,
+                  "%s: negative stride", op);
+  }
   int vec = 16 / sizeof(T);
   auto aligned = [&](int v) {
-    bool ok = dim % v == 0 && reinterpret_cast<uintptr_t>(in) % (v * sizeof(T)) == 0 &&
-              reinterpret_cast<uintptr_t>(out) % (v * sizeof(T)) == 0;
-    for (int64_t st : {si.b, si.n, si.h, so.b, so.n, so.h}) ok = ok && st % v == 0;
+    bool ok = dim % v == 0;
+    for (int p = 0; p < nparts; ++p) {
+      ok = ok && reinterpret_cast<uintptr_t>(in[p]) % (v * sizeof(T)) == 0 &&
+           reinterpret_cast<uintptr_t>(out[p]) % (v * sizeof(T)) == 0;
+      for (int64_t st : {io.si[p].b, io.si[p].n, io.si[p].h, io.so[p].b, io.so[p].n, io.so[p].h}) ok = ok && st % v == 0;
+    }
     return ok;
   };
   while (vec > 2 && !aligned(vec)) vec /= 2;
@@ -146,19 +156,16 @@ int launch_rotary(const void* in, const int64_t* in_strides, const void* cosv, c
   const FastDiv fseq(static_cast<uint32_t>(seq));
   const FastDiv fdim(static_cast<uint32_t>(dim));
   const TableRef tab{cs_seq, cs_pair};
-  const int64_t blocks64 = (packs + kRotThreads * kRotUnroll - 1) / (kRotThreads * kRotUnroll);
-  const int blocks = static_cast<int>(blocks64 < 65536 ? blocks64 : 65536);
-  const T* pin = static_cast<const T*>(in);
-  const T* pc = static_cast<const T*>(cosv);
-  const T* ps = static_cast<const T*>(sinv);
-  T* po = static_cast<T*>(out);
+  const int64_t blocks64 = (packs + kRotThreads - 1) / kRotThreads;
+  const dim3 grid(static_cast<unsigned>(blocks64 < 65536 ? blocks64 : 65536), static_cast<unsigned>(nparts));
   const uint32_t np = static_cast<uint32_t>(packs);
   const int ts = table_mode(cosv, sinv, cs_seq, cs_pair, vec, sizeof(T));
-#define PMSST_ROT1(VEC, INV, TS)                                                                                    \
-  hipLaunchKernelGGL((rotary_kernel<T, VEC, INV, TS>), dim3(blocks), dim3(kRotThreads), 0, stream, pin, pc, ps, po, \
-                     np, ppt, fseq, fdim, tab, si, so)
-#define PMSST_ROT(VEC, INV)                                  \
-  do {                                                       \
+  const T* pc = static_cast<const T*>(cosv);
+  const T* ps = static_cast<const T*>(sinv);
+#define PMSST_ROT1(VEC, INV, TS) \
+  hipLaunchKernelGGL((rotary_kernel<T, VEC, INV, TS>), grid, dim3(kRotThreads), 0, stream, io, pc, ps, np, ppt, fseq, fdim, tab)
+#define PMSST_ROT(VEC, INV)                                     \
+  do {                                                          \
     if (ts == kTabRepeated) PMSST_ROT1(VEC, INV, kTabRepeated); \
     else if (ts == kTabDense) PMSST_ROT1(VEC, INV, kTabDense);  \
     else PMSST_ROT1(VEC, INV, kTabAny);                         \
@@ -175,6 +182,18 @@ int launch_rotary(const void* in, const int64_t* in_strides, const void* cosv, c
 #undef PMSST_ROT
 #undef PMSST_ROT1
   return check_launch("rotary_kernel");
+}
+
+template <typename T>
+int launch_rotary(const void* in, const int64_t* in_strides, const void* cosv, const void* sinv, void* out,
+                  const int64_t* out_strides, int64_t batch, int64_t seq, int64_t heads, int64_t dim, int64_t cs_seq,
+                  int64_t cs_pair, bool inverse, hipStream_t stream) {
+  const void* ins[] = {in};
+  void* outs[] = {out};
+  const int64_t* sis[] = {in_strides};
+  const int64_t* sos[] = {out_strides};
+  return launch_rotary_parts<T>(inverse ? "rotary_backward" : "rotary_forward", 1, 1, ins, sis, cosv, sinv, outs, sos,
+                                batch, seq, heads, dim, cs_seq, cs_pair, inverse, stream);
 }
 
 // ------------------------------------------------------------------ fused q/k RMSNorm + rotary
@@ -509,6 +528,40 @@ int pmsst_rotary_backward(const void* grad_out, const int64_t* grad_out_strides,
     using T = decltype(tag);
     return launch_rotary<T>(grad_out, grad_out_strides, cos, sin, grad_t, grad_t_strides, batch, seq, heads, dim,
                             cs_stride_seq, cs_stride_pair, true, static_cast<hipStream_t>(stream));
+  });
+}
+
+int pmsst_rotary_qkv_forward(const void* q, const void* k, const void* v, const int64_t* in_strides, const void* cos,
+                             const void* sin, void* q_out, void* k_out, void* v_out, const int64_t* out_strides,
+                             int64_t batch, int64_t seq, int64_t heads, int64_t dim, int64_t cs_stride_seq,
+                             int64_t cs_stride_pair, int dtype, void* stream) {
+  return with_dtype(dtype, "rotary_qkv_forward", [&](auto tag) {
+    using T = decltype(tag);
+    const void* ins[] = {q, k, v};
+    void* outs[] = {q_out, k_out, v_out};
+    const int64_t* sis[] = {in_strides ? in_strides : nullptr, in_strides ? in_strides + 3 : nullptr,
+                            in_strides ? in_strides + 6 : nullptr};
+    const int64_t* sos[] = {out_strides ? out_strides : nullptr, out_strides ? out_strides + 3 : nullptr,
+                            out_strides ? out_strides + 6 : nullptr};
+    return launch_rotary_parts<T>("rotary_qkv_forward", 3, 2, ins, sis, cos, sin, outs, sos, batch, seq, heads, dim,
+                                  cs_stride_seq, cs_stride_pair, false, static_cast<hipStream_t>(stream));
+  });
+}
+
+int pmsst_rotary_qkv_backward(const void* grad_q, const void* grad_k, const void* grad_v, const int64_t* grad_strides,
+                              const void* cos, const void* sin, void* grad_q_in, void* grad_k_in, void* grad_v_in,
+                              const int64_t* grad_in_strides, int64_t batch, int64_t seq, int64_t heads, int64_t dim,
+                              int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype, void* stream) {
+  return with_dtype(dtype, "rotary_qkv_backward", [&](auto tag) {
+    using T = decltype(tag);
+    const void* ins[] = {grad_q, grad_k, grad_v};
+    void* outs[] = {grad_q_in, grad_k_in, grad_v_in};
+    const int64_t* sis[] = {grad_strides ? grad_strides : nullptr, grad_strides ? grad_strides + 3 : nullptr,
+                            grad_strides ? grad_strides + 6 : nullptr};
+    const int64_t* sos[] = {grad_in_strides ? grad_in_strides : nullptr, grad_in_strides ? grad_in_strides + 3 : nullptr,
+                            grad_in_strides ? grad_in_strides + 6 : nullptr};
+    return launch_rotary_parts<T>("rotary_qkv_backward", 3, 2, ins, sis, cos, sin, outs, sos, batch, seq, heads, dim,
+                                  cs_stride_seq, cs_stride_pair, true, static_cast<hipStream_t>(stream));
   });
 }
 

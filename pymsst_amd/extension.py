@@ -274,6 +274,55 @@ class HipFusedExtension:
         self._rot_check(grad_out, cos, sin, "grad_out")
         return self._rotary("pmsst_rotary_backward", grad_out, cos, sin)
 
+    def rotary_qkv_forward(self, qkv, heads, cos, sin):
+        """Build addition: split a fused ``qkv[B, N, 3*H*D]`` projection and rotate q and k in one
+        launch.  Returns ``(q, k, v)``, each the ``[B,N,H,D]``-shaped transpose of a dense
+        ``[B,H,N,D]`` buffer (the layout attention reads); v is copied unrotated."""
+        _req(qkv.is_cuda and qkv.dim() == 3, "qkv must be a CUDA tensor of shape [B, N, 3*H*D]")
+        _req(qkv.size(2) % (3 * heads) == 0, "qkv last dimension must be 3 * heads * dim_head")
+        if qkv.stride(2) != 1:
+            qkv = qkv.contiguous()
+        b, n, _ = qkv.shape
+        d = qkv.size(2) // (3 * heads)
+        q, k, v = qkv.view(b, n, 3, heads, d).unbind(2)
+        self._rot_check(q, cos, sin, "q")
+        cos, sin, s_seq, s_pair = self._tables(cos, sin)
+        outs = [torch.empty((b, heads, n, d), dtype=qkv.dtype, device=qkv.device).transpose(1, 2) for _ in range(3)]
+        ist = (ctypes.c_int64 * 9)(*[st for t in (q, k, v) for st in (t.stride(0), t.stride(1), t.stride(2))])
+        ost = (ctypes.c_int64 * 9)(*[st for t in outs for st in (t.stride(0), t.stride(1), t.stride(2))])
+        with _DeviceGuard(qkv.device):
+            rc = self._lib.pmsst_rotary_qkv_forward(
+                _ptr(q), _ptr(k), _ptr(v), ist, _ptr(cos), _ptr(sin), _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]),
+                ost, b, n, heads, d, s_seq, s_pair, dtype_code(qkv.dtype), _stream(qkv.device),
+            )
+        check(rc, "pmsst_rotary_qkv_forward")
+        return tuple(outs)
+
+    def rotary_qkv_backward(self, grad_q, grad_k, grad_v, cos, sin):
+        """Build addition: backward of :meth:`rotary_qkv_forward`.  ``grad_q/k/v`` are
+        ``[B,N,H,D]``-shaped with any strides and a contiguous last axis; returns the dense
+        ``[B, N, 3*H*D]`` qkv gradient (q and k rotated back, v copied) from one launch."""
+        grads = []
+        for t in (grad_q, grad_k, grad_v):
+            _req(t.is_cuda and t.dim() == 4 and t.shape == grad_q.shape and t.dtype == grad_q.dtype,
+                 "grad_q, grad_k and grad_v must be CUDA tensors of one [B, N, H, D] shape and dtype")
+            grads.append(t if t.stride(3) == 1 else t.contiguous())
+        self._rot_check(grads[0], cos, sin, "grad_q")
+        cos, sin, s_seq, s_pair = self._tables(cos, sin)
+        b, n, h, d = grads[0].shape
+        dqkv = torch.empty((b, n, 3 * h * d), dtype=grads[0].dtype, device=grads[0].device)
+        parts = dqkv.view(b, n, 3, h, d).unbind(2)
+        ist = (ctypes.c_int64 * 9)(*[st for t in grads for st in (t.stride(0), t.stride(1), t.stride(2))])
+        ost = (ctypes.c_int64 * 9)(*[st for t in parts for st in (t.stride(0), t.stride(1), t.stride(2))])
+        with _DeviceGuard(dqkv.device):
+            rc = self._lib.pmsst_rotary_qkv_backward(
+                _ptr(grads[0]), _ptr(grads[1]), _ptr(grads[2]), ist, _ptr(cos), _ptr(sin), _ptr(parts[0]),
+                _ptr(parts[1]), _ptr(parts[2]), ost, b, n, h, d, s_seq, s_pair, dtype_code(dqkv.dtype),
+                _stream(dqkv.device),
+            )
+        check(rc, "pmsst_rotary_qkv_backward")
+        return dqkv
+
     def rms_norm_rotary_forward(self, x, gamma, cos, sin):
         """Build addition: fused q/k RMSNorm over the head dim + rotary + cast.
 

@@ -412,9 +412,15 @@ def _patch_core_attention_gates(ext: Any, mode: str) -> bool:
         ):
             return original(self, x)
         x = self.norm(x)
-        q, k, v = transformer.qkv_to_bnhd(self.to_qkv(x), self.heads)
-        if self.rotary_embed is not None:
-            q, k = transformer.rotate_qk_fast_bnhd(self.rotary_embed, q, k)
+        qkv = self.to_qkv(x)
+        if self.rotary_embed is not None and _fused_qkv_split_ok(ext, qkv):
+            # rotary patch active too: split + rotate (+ gradient stacking) in one op each way
+            cos, sin = self.rotary_embed.tables(qkv.shape[1], qkv.device, qkv.dtype)
+            q, k, v = _FusedQKVRotary.apply(qkv, cos[..., ::2], sin[..., ::2], self.heads, ext)
+        else:
+            q, k, v = transformer.qkv_to_bnhd(qkv, self.heads)
+            if self.rotary_embed is not None:
+                q, k = transformer.rotate_qk_fast_bnhd(self.rotary_embed, q, k)
         q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
         out = self._attention(q, k, v).transpose(1, 2)
         gate_dtype = out.dtype
@@ -1048,6 +1054,40 @@ class _FusedMaskMLP(torch.autograd.Function):
                                                                 input_activation="tanh")
         dx, dw1, db1 = ext.grouped_linear_backward(dz, x, w1, has_bias=True)
         return dx, dw1, db1, dw2, db2, None, None
+
+
+def _fused_qkv_split_ok(ext: Any, qkv: torch.Tensor) -> bool:
+    """The fused q/k/v split + rotary runs where the stock path would call the patched rotary."""
+    _, transformer, _ = _core()
+    return (
+        getattr(transformer.apply_rotary_emb_fast, "_pymsst_fused_rotary", False)
+        and hasattr(ext, "rotary_qkv_forward")
+        and hasattr(ext, "rotary_qkv_backward")
+        and qkv.device.type == "cuda"
+        and qkv.dtype in _FLOAT_TYPES
+        and qkv.dim() == 3
+    )
+
+
+class _FusedQKVRotary(torch.autograd.Function):
+    """``qkv_to_bnhd`` + ``rotate_qk_fast_bnhd`` as one op (no reference counterpart: the reference
+    rotates q and k through ``_FusedRotary``, fr.py:1154-1166, and leaves the split to torch).
+    Forward writes q (rotated), k (rotated) and v in the layout attention reads; backward writes
+    the qkv gradient directly, replacing the two inverse rotations and the stack of the split."""
+
+    @staticmethod
+    def forward(ctx, qkv, cos, sin, heads, extension):
+        q, k, v = extension.rotary_qkv_forward(qkv, heads, cos, sin)
+        ctx.save_for_backward(cos, sin)
+        ctx.extension = extension
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, grad_q, grad_k, grad_v):
+        cos, sin = ctx.saved_tensors
+        ref = next(g for g in (grad_q, grad_k, grad_v) if g is not None)
+        grads = [torch.zeros_like(ref) if g is None else g for g in (grad_q, grad_k, grad_v)]
+        return ctx.extension.rotary_qkv_backward(*grads, cos, sin), None, None, None, None
 
 
 class _FusedAttentionGate(torch.autograd.Function):

@@ -205,6 +205,56 @@ def test_rotary_strided_qkv_view_and_bhnd_output(hip_ext, dtype, shape):
     assert_parity(dt_, oracle.rotary_backward(to_np(g), cn, sn, dn), dn, "rotary bwd strided")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(2, 7, 3, 16), (248, 258, 8, 64), (1032, 62, 8, 64), (3, 5, 2, 6)])
+def test_rotary_qkv_split_forward_backward(hip_ext, dtype, shape):
+    """One launch splits a fused qkv projection into rotated q, rotated k and v (dense [B,H,N,D]
+    storage); the backward writes the qkv gradient (q, k rotated back, v copied) in one launch."""
+    dn = dt_name(dtype)
+    b, n, h, d = shape
+    qkv = _rand((b, n, 3 * h * d), dtype, 45)
+    cos, sin = _tables(n, d, dtype, True)
+    cn, sn = to_np(cos).reshape(n, d // 2), to_np(sin).reshape(n, d // 2)
+    q, k, v = hip_ext.rotary_qkv_forward(qkv, h, cos, sin)
+    parts = qkv.view(b, n, 3, h, d).unbind(2)
+    for name, out, src, rot in (("q", q, parts[0], True), ("k", k, parts[1], True), ("v", v, parts[2], False)):
+        assert out.shape == (b, n, h, d) and out.transpose(1, 2).is_contiguous()
+        if rot:
+            assert_parity(out, oracle.rotary_forward(to_np(src), cn, sn, dn), dn, f"qkv fwd {name}")
+        else:
+            assert torch.equal(out, src)
+    gq, gk, gv = (_rand((b, h, n, d), dtype, 46 + i).transpose(1, 2) for i in range(3))
+    dqkv = hip_ext.rotary_qkv_backward(gq, gk, gv, cos, sin)
+    assert dqkv.shape == qkv.shape and dqkv.is_contiguous()
+    dparts = dqkv.view(b, n, 3, h, d).unbind(2)
+    assert_parity(dparts[0], oracle.rotary_backward(to_np(gq), cn, sn, dn), dn, "qkv bwd q")
+    assert_parity(dparts[1], oracle.rotary_backward(to_np(gk), cn, sn, dn), dn, "qkv bwd k")
+    assert torch.equal(dparts[2], gv)
+    # same values as the single-tensor ops
+    assert torch.equal(q, hip_ext.rotary_forward(parts[0], cos, sin))
+    assert torch.equal(dparts[1], hip_ext.rotary_backward(gk, cos, sin))
+
+
+def test_fused_qkv_rotary_autograd(hip_ext):
+    from pymsst_amd.fused_roformer import _FusedQKVRotary
+
+    b, n, h, d = 4, 62, 8, 64
+    qkv = _rand((b, n, 3 * h * d), torch.float32, 47).requires_grad_()
+    cos, sin = _tables(n, d, torch.float32, True)
+    q, k, v = _FusedQKVRotary.apply(qkv, cos, sin, h, hip_ext)
+    loss = (q * 1.5).sum() + (k * k).sum() + (v * 0.5).sum()
+    loss.backward()
+    cn, sn = to_np(cos).reshape(n, d // 2), to_np(sin).reshape(n, d // 2)
+    gq = torch.full_like(q, 1.5)
+    gk = 2 * k.detach()
+    expect = torch.cat([
+        torch.from_numpy(oracle.rotary_backward(to_np(gq), cn, sn, "f32")).float().cuda().reshape(b, n, 1, h, d),
+        torch.from_numpy(oracle.rotary_backward(to_np(gk), cn, sn, "f32")).float().cuda().reshape(b, n, 1, h, d),
+        torch.full((b, n, 1, h, d), 0.5, device="cuda"),
+    ], dim=2).reshape(b, n, -1)
+    assert_parity(qkv.grad, to_np(expect), "f32", "dqkv")
+
+
 def test_rotary_microbench_shape_roundtrip(hip_ext):
     # cfg2 q/k shape; forward then backward is the identity up to rounding (rotation is orthogonal)
     shape = (248, 258, 8, 64)
