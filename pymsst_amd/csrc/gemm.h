@@ -345,7 +345,10 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
   const int nk = (K + kChunkK - 1) / kChunkK;
   if (nk == 0) return;
 
+  // The scheduler would otherwise hoist the LDS commit of the next chunk (independent
+  // addresses) above the MFMAs, making them wait for the in-flight loads it commits.
   auto mma = [&](int cur) {
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < S::kTR; ++i) {
 #pragma unroll
@@ -354,30 +357,33 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
                                  acc[i][j], lane);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   typename LA::Regs ra0;
   typename LB::Regs rb0;
   la.fetch(0, ra0);
   lb.fetch(0, rb0);
+  // The steady-state loops below fetch unconditionally: with every trip issuing the
+  // same loads into the same registers, the wait-count analysis can see that a
+  // register set's previous loads retired before it is refilled, and no conditional
+  // path splits the accumulators' live ranges.
   if constexpr (DEPTH == 1) {
     la.commit(ra0, lds);
     lb.commit(rb0, lds + BR * P);
     __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
+    int kc = 0;
+    for (; kc + 1 < nk; ++kc) {
       const int cur = (kc & 1) * kBuf;
-      const bool more = kc + 1 < nk;
-      if (more) {
-        la.fetch((kc + 1) * kChunkK, ra0);
-        lb.fetch((kc + 1) * kChunkK, rb0);
-      }
+      la.fetch((kc + 1) * kChunkK, ra0);
+      lb.fetch((kc + 1) * kChunkK, rb0);
       mma(cur);
-      if (more) {
-        la.commit(ra0, lds + kBuf - cur);
-        lb.commit(rb0, lds + kBuf - cur + BR * P);
-      }
+      la.commit(ra0, lds + kBuf - cur);
+      lb.commit(rb0, lds + kBuf - cur + BR * P);
       __syncthreads();
     }
+    mma((kc & 1) * kBuf);
+    __syncthreads();
   } else {
     typename LA::Regs ra1;
     typename LB::Regs rb1;
@@ -388,26 +394,48 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
     la.commit(ra0, lds);
     lb.commit(rb0, lds + BR * P);
     __syncthreads();
-    // `rc` held chunk kc (already in LDS) and is refilled with kc + 2; `rn` holds
-    // chunk kc + 1 and is committed after the MFMAs of chunk kc.
-    auto step = [&](int kc, typename LA::Regs& rca, typename LB::Regs& rcb, typename LA::Regs& rna,
-                    typename LB::Regs& rnb) {
+    // Entering each trip: chunk kc is in LDS buffer (kc & 1) and its registers (set 0)
+    // are free; chunk kc + 1 is in flight into set 1.
+    int kc = 0;
+    for (; kc + 3 < nk; kc += 2) {
       const int cur = (kc & 1) * kBuf;
-      if (kc + 2 < nk) {
-        la.fetch((kc + 2) * kChunkK, rca);
-        lb.fetch((kc + 2) * kChunkK, rcb);
-      }
+      la.fetch((kc + 2) * kChunkK, ra0);
+      lb.fetch((kc + 2) * kChunkK, rb0);
       mma(cur);
-      if (kc + 1 < nk) {
-        la.commit(rna, lds + kBuf - cur);
-        lb.commit(rnb, lds + kBuf - cur + BR * P);
-      }
+      la.commit(ra1, lds + kBuf - cur);
+      lb.commit(rb1, lds + kBuf - cur + BR * P);
       __syncthreads();
-    };
-    for (int kc = 0; kc < nk; kc += 2) {
-      step(kc, ra0, rb0, ra1, rb1);
-      if (kc + 1 < nk) step(kc + 1, ra1, rb1, ra0, rb0);
+      la.fetch((kc + 3) * kChunkK, ra1);
+      lb.fetch((kc + 3) * kChunkK, rb1);
+      mma(kBuf - cur);
+      la.commit(ra0, lds + cur);
+      lb.commit(rb0, lds + cur + BR * P);
+      __syncthreads();
     }
+    // 1 to 3 chunks left: kc (in LDS), kc + 1 (set 1, in flight), kc + 2 (not fetched)
+    const int cur = (kc & 1) * kBuf;
+    if (kc + 2 < nk) {
+      la.fetch((kc + 2) * kChunkK, ra0);
+      lb.fetch((kc + 2) * kChunkK, rb0);
+      mma(cur);
+      la.commit(ra1, lds + kBuf - cur);
+      lb.commit(rb1, lds + kBuf - cur + BR * P);
+      __syncthreads();
+      mma(kBuf - cur);
+      la.commit(ra0, lds + cur);
+      lb.commit(rb0, lds + cur + BR * P);
+      __syncthreads();
+      mma(cur);
+    } else if (kc + 1 < nk) {
+      mma(cur);
+      la.commit(ra1, lds + kBuf - cur);
+      lb.commit(rb1, lds + kBuf - cur + BR * P);
+      __syncthreads();
+      mma(kBuf - cur);
+    } else {
+      mma(cur);
+    }
+    __syncthreads();
   }
 }
 
