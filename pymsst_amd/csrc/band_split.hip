@@ -47,8 +47,9 @@ struct BandArgs {
 // B operand of the forward: rows m of x (K = band features) scaled by gamma;
 // keeps the running sum of squares of the raw values of its two rows
 // (rows tid/8 and tid/8 + 32, k quad (tid%8)*4 of every chunk).  gamma for the
-// thread's k quad is fetched with the chunk.
-template <typename T, bool NORM>
+// thread's k quad is fetched with the chunk.  Rows past rows_valid are clamped to the
+// last valid row in interior chunks (their outputs and sums are discarded).
+template <typename T, bool NORM, bool V4>
 struct XGammaLoader {
   static constexpr int kQuads = kBM * (kChunkK / 4) / kGemmThreads;
   static_assert(kQuads == 2, "two rows per thread");
@@ -62,37 +63,66 @@ struct XGammaLoader {
   const T* gamma;  // band gamma (k indexed)
   int rows_valid;
   int k_valid;
-  bool vec4;
-  mutable float ss[kQuads];
+  mutable float ss[kQuads] = {0.f, 0.f};
+  int64_t src_row[kQuads] = {};
+  uint32_t off[kQuads] = {};
 
-  __device__ __forceinline__ void fetch(int k0, Regs& g) const {
-    const int k = k0 + (threadIdx.x % (kChunkK / 4)) * 4;
+  static __device__ __forceinline__ int tile_row(int i) {
+    return (static_cast<int>(threadIdx.x) + i * kGemmThreads) / (kChunkK / 4);
+  }
+  static __device__ __forceinline__ int lane_k() { return (threadIdx.x % (kChunkK / 4)) * 4; }
+
+  __device__ __forceinline__ void prepare() {
+#pragma unroll
+    for (int i = 0; i < kQuads; ++i) {
+      const int r = tile_row(i);
+      src_row[i] = r < rows_valid ? r : rows_valid - 1;
+      off[i] = static_cast<uint32_t>((src_row[i] * stride + lane_k()) * static_cast<int64_t>(sizeof(T)));
+    }
+  }
+  __device__ __forceinline__ void fetch_edge(int k0, Regs& g) const {
+    const int k = k0 + lane_k();
     g.ok = 0;
 #pragma unroll
-    for (int i = 0; i < kQuads; ++i) {
-      const int r = (threadIdx.x + i * kGemmThreads) / (kChunkK / 4);
-      g.q[i] = fetch_quad<T>(base + r * stride + k, base, vec4, r < rows_valid, k_valid - k, g.ok, i);
-    }
-    if (NORM) g.g = fetch_quad<T>(gamma + k, gamma, vec4, true, k_valid - k, g.ok, kQuads);
+    for (int i = 0; i < kQuads; ++i)
+      g.q[i] = fetch_quad_k<T, V4>(base + src_row[i] * stride + k, base, tile_row(i) < rows_valid, k, k_valid, g.ok, i);
+    if (NORM) g.g = fetch_quad_k<T, V4>(gamma + k, gamma, true, k, k_valid, g.ok, kQuads);
   }
-  __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
-    const int kq = (threadIdx.x % (kChunkK / 4)) * 4;
-    float gm[4] = {1.f, 1.f, 1.f, 1.f};
-    if (NORM) quad_to_f32<T>(mask_quad<T>(g.g, (g.ok >> kQuads) & 1), gm);
+  __device__ __forceinline__ void fetch(int k0, Regs& g) const {
+    if constexpr (V4) {
+#pragma unroll
+      for (int i = 0; i < kQuads; ++i) g.q[i] = quad_at<T>(base + k0, off[i]);
+      if (NORM) g.g = quad_at<T>(gamma + k0, static_cast<uint32_t>(lane_k() * sizeof(T)));
+    } else {
+      fetch_edge(k0, g);
+    }
+  }
+  __device__ __forceinline__ void commit_impl(const Regs& g, T* lds, bool masked) const {
+    const int kq = lane_k();
+    if constexpr (!NORM) {
+      // plain grouped linear: no gamma, no sums of squares
+#pragma unroll
+      for (int i = 0; i < kQuads; ++i)
+        commit_quad<T>(lds, tile_row(i), kq, masked ? mask_quad<T>(g.q[i], (g.ok >> i) & 1) : g.q[i]);
+      return;
+    }
+    float gm[4];
+    quad_to_f32<T>(masked ? mask_quad<T>(g.g, (g.ok >> kQuads) & 1) : g.g, gm);
 #pragma unroll
     for (int i = 0; i < kQuads; ++i) {
-      const int r = (threadIdx.x + i * kGemmThreads) / (kChunkK / 4);
       float v[4];
-      quad_to_f32<T>(mask_quad<T>(g.q[i], (g.ok >> i) & 1), v);
+      quad_to_f32<T>(masked ? mask_quad<T>(g.q[i], (g.ok >> i) & 1) : g.q[i], v);
       Pack<T, 4> pk;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         ss[i] += v[j] * v[j];
         pk.v[j] = from_f32<T>(v[j] * gm[j]);
       }
-      commit_quad<T>(lds, r, kq, __builtin_bit_cast(quad_t<T>, pk));
+      commit_quad<T>(lds, tile_row(i), kq, __builtin_bit_cast(quad_t<T>, pk));
     }
   }
+  __device__ __forceinline__ void commit_edge(const Regs& g, T* lds) const { commit_impl(g, lds, true); }
+  __device__ __forceinline__ void commit(const Regs& g, T* lds) const { commit_impl(g, lds, !V4); }
 };
 
 template <typename T, int TO, bool WRITE_NORMED, bool NORM, int ACT, bool V4>
@@ -116,8 +146,8 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
   const int rows_valid = static_cast<int>(a.M - m0 < kBM ? a.M - m0 : kBM);
   const T* xb = x + m0 * a.x_stride + off;
 
-  KRowLoader<T, OT> la{weight + static_cast<int64_t>(O) * off + static_cast<int64_t>(oc) * I, I, O - oc, I, V4};
-  XGammaLoader<T, NORM> lb{xb, a.x_stride, gamma + off, rows_valid, I, V4, {0.f, 0.f}};
+  KRowLoader<T, OT, V4> la{weight + static_cast<int64_t>(O) * off + static_cast<int64_t>(oc) * I, I, O - oc, I};
+  XGammaLoader<T, NORM, V4> lb{xb, a.x_stride, gamma + off, rows_valid, I};
   f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
   for (int i = 0; i < S::kTR; ++i)
@@ -306,8 +336,8 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
     const bool write_dx = pass == kPasses - 1;
     for (int i0 = i_begin; i0 < i_end; i0 += kBI) {
       // A[i][o] = W_b[o][i0 + i] (MN-contiguous in i);  B[m][o] = dy[m0 + m][band][o]
-      MNLoader<T, kBI> la{wb + i0, I, I - i0, O, V4};
-      KRowLoader<T, kBM> lb{dyb, static_cast<int64_t>(a.NB) * O, rows_valid, O, V4};
+      MNLoader<T, kBI, V4> la{wb + i0, I, I - i0, O};
+      KRowLoader<T, kBM, V4> lb{dyb, static_cast<int64_t>(a.NB) * O, rows_valid, O};
       f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[0][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -414,18 +444,15 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
 
   // A[i][m] = n[m][off + i0 + i] * gamma (MN-contiguous in i; n = x * inv * sqrt(I) when FROM_X)
   // B[o][m] = dy[m][band][o0 + o]       (MN-contiguous in o)
-  MNLoader<T, kDwBI> la{nsrc + off + i0, a.F, I - i0, static_cast<int>(a.M), V4};
-  if (NORM) {
-    la.cs = gamma + off + i0;
-    la.init();
-  }
+  MNLoader<T, kDwBI, V4> la{nsrc + off + i0, a.F, I - i0, static_cast<int>(a.M)};
+  if (NORM) la.cs = gamma + off + i0;
   if (NORM && FROM_X) {
     la.rs = inv_norm + band;
     la.rs_stride = a.NB;
     la.rs_mul = sqrtf(static_cast<float>(I));
   }
-  MNLoader<T, kDwBO> lb{dy + static_cast<int64_t>(band) * O + o0, static_cast<int64_t>(a.NB) * O, O - o0,
-                        static_cast<int>(a.M), V4};
+  MNLoader<T, kDwBO, V4> lb{dy + static_cast<int64_t>(band) * O + o0, static_cast<int64_t>(a.NB) * O, O - o0,
+                            static_cast<int>(a.M)};
   // the first input tile of each (band, output tile) also sums dy over the rows: dbias
   lb.colsum = db != nullptr && i0 == 0;
   f32x4_t acc[S::kTR][S::kTC];
@@ -434,7 +461,7 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
 #pragma unroll
     for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   gemm_mainloop<T, kDwBI, kDwBO, 2, 2>(la, lb, static_cast<int>(a.M), lds, acc);
-  if (lb.colsum) reduce_colsum<T, kDwBO>(lb, lds, db + static_cast<int64_t>(band) * O + o0);
+  if (lb.colsum) reduce_colsum<T, kDwBO, V4>(lb, lds, db + static_cast<int64_t>(band) * O + o0);
 
   T* dwb = dw + static_cast<int64_t>(O) * off;  // [O][I]
   const int ir = (wave >> 1) * (kDwBI / 2), oc = (wave & 1) * (kDwBO / 2);
@@ -505,6 +532,8 @@ int launch_fwd(const void* x, int64_t x_stride, const void* gamma, const void* w
   if (M == 0) return PMSST_OK;
   PMSST_REQUIRE(x && weight && offsets && out && (!norm || (gamma && inv_norm)), "%s: null pointer", op);
   PMSST_REQUIRE(x_stride >= hb.F, "%s: x row stride %lld < total features %d", op, (long long)x_stride, hb.F);
+  PMSST_REQUIRE(gemm_stride_ok(x_stride, sizeof(T)) && gemm_stride_ok(int64_t{hb.NB} * O, sizeof(T)),
+                "%s: rows too long for 32-bit tile offsets", op);
   BandArgs a{offsets, M, hb.NB, hb.F, x_stride, static_cast<int>(O), false, false};
   a.vec4 = hb.vec4 && x_stride % 4 == 0 && aligned_to(x, 4 * sizeof(T)) && aligned_to(normed, 4 * sizeof(T)) &&
            aligned_to(weight, 4 * sizeof(T));
@@ -569,6 +598,8 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   PMSST_REQUIRE(O >= 1 && O <= 512, "%s: out_features must be in [1, 512] (got %lld)", op, (long long)O);
   PMSST_REQUIRE(gamma && weight && offsets && dgamma && dw && (M == 0 || (dy && nsrc && inv_norm && dx)),
                 "%s: null pointer", op);
+  PMSST_REQUIRE(gemm_stride_ok(hb.F, sizeof(T)) && gemm_stride_ok(int64_t{hb.NB} * O, sizeof(T)),
+                "%s: rows too long for 32-bit tile offsets", op);
   const size_t need = bwd_workspace(M, hb.F, hb.NB, static_cast<int>(O));
   if (workspace == nullptr || workspace_bytes < need) {
     return fail(PMSST_EWORKSPACE, "%s: workspace of %zu bytes needed", op, need);
@@ -655,6 +686,8 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
   PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
   PMSST_REQUIRE(O >= 1 && O < (1 << 20), "%s: bad out_features %lld", op, (long long)O);
   PMSST_REQUIRE(weight && offsets && dw && (M == 0 || (dy && x && dx)), "%s: null pointer", op);
+  PMSST_REQUIRE(gemm_stride_ok(hb.F, sizeof(T)) && gemm_stride_ok(int64_t{hb.NB} * O, sizeof(T)),
+                "%s: rows too long for 32-bit tile offsets", op);
   const size_t need = colsum_rows_workspace(M, static_cast<int64_t>(hb.NB) * O);
   if (db != nullptr && (workspace == nullptr || workspace_bytes < need)) {
     return fail(PMSST_EWORKSPACE, "%s: workspace of %zu bytes needed", op, need);

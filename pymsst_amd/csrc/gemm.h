@@ -18,7 +18,8 @@
 //   C[row0 + 16 i + 4 (l / 16) + r][col0 + 16 j + (l % 16)],  r = 0..3.
 //
 // Loaders move one 32-wide K chunk:  fetch(k0, regs) global -> registers,
-// commit(regs, lds) registers -> LDS.  Out-of-range rows and k read as zero.
+// commit(regs, lds) registers -> LDS (fetch_edge / commit_edge for a partial chunk);
+// prepare() runs once before the first chunk.
 #pragma once
 
 #include <type_traits>
@@ -52,15 +53,18 @@ __device__ __forceinline__ f32x4_t mfma_tile(const T* __restrict__ a, int ra, co
   }
 }
 
-// ---------------------------------------------------------------- guarded loads
-// Loads never branch on bounds, and nothing consumes a loaded value until commit():
-// an out-of-range lane reads the tile origin (always a valid element) and records a
-// validity bit; commit() masks the value to zero.  fetch() therefore issues all of
-// its loads back to back and the MFMAs of the current chunk run while they are in
-// flight.  When a loader's `vec4` flag is set, every k / mn extent it is given is a
-// multiple of 4 (the launchers only set it then), so a quad is either fully in
-// range or fully out; without it (unaligned shapes) the loader falls back to
-// per-element loads that are masked at once.
+// ---------------------------------------------------------------- loads
+// K is walked in chunks of 32 that END at K: chunk c covers k in [kbeg + 32 c, kbeg + 32 c + 32)
+// with kbeg = K - 32 ceil(K / 32) <= 0, so only chunk 0 can be partial (k < 0 masked).
+// Loaders therefore have two paths:
+//  * interior chunks (fetch / commit): rows / columns outside the tile's valid range are
+//    CLAMPED to a valid one when the loader is prepared (their products only reach outputs
+//    the epilogue discards), every k is in range, and each load is a uniform chunk base plus a
+//    per-lane 32-bit byte offset computed once -- no per-chunk address arithmetic or masking;
+//  * the partial chunk 0 (fetch_edge / commit_edge): loads never branch on bounds (an
+//    out-of-range lane reads a valid element and records a bit) and commit_edge zeroes them.
+// With V4 false (widths or strides not multiples of 4 elements) every chunk takes the
+// element-wise guarded path.
 
 template <typename T>
 using raw_t = typename std::conditional<sizeof(T) == 2, uint16_t, uint32_t>::type;
@@ -71,6 +75,12 @@ using quad_t = typename std::conditional<sizeof(T) == 2, uint2, uint4>::type;
 template <typename T>
 __device__ __forceinline__ quad_t<T> raw_quad(const T* p) {
   return *reinterpret_cast<const quad_t<T>*>(p);
+}
+
+// Quad at a uniform base plus a per-lane byte offset (global_load with an SGPR base).
+template <typename T>
+__device__ __forceinline__ quad_t<T> quad_at(const T* base, uint32_t byte_off) {
+  return *reinterpret_cast<const quad_t<T>*>(reinterpret_cast<const char*>(base) + byte_off);
 }
 
 template <typename T>
@@ -84,13 +94,13 @@ __device__ __forceinline__ quad_t<T> mask_quad(quad_t<T> q, bool ok) {
   return q;
 }
 
-// Unaligned fallback: element j is loaded when `ok && j < valid`, masked at once.
+// Element-wise guarded quad: element j is loaded when `ok` and lo <= j < hi, else zero.
 template <typename T>
-__device__ __forceinline__ quad_t<T> load_quad_scalar(const T* p, const T* safe, bool ok, int valid) {
+__device__ __forceinline__ quad_t<T> load_quad_scalar(const T* p, const T* safe, bool ok, int lo, int hi) {
   uint32_t e[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const bool in = ok && j < valid;
+    const bool in = ok && j >= lo && j < hi;
     const raw_t<T> v = *reinterpret_cast<const raw_t<T>*>(in ? p + j : safe);
     e[j] = in ? static_cast<uint32_t>(v) : 0u;
   }
@@ -107,17 +117,19 @@ __device__ __forceinline__ quad_t<T> load_quad_scalar(const T* p, const T* safe,
   return q;
 }
 
-// One quad: raw load (vec4) recording validity, or the masked scalar fallback.
-template <typename T>
-__device__ __forceinline__ quad_t<T> fetch_quad(const T* p, const T* safe, bool vec4, bool row_ok, int k_left,
-                                                uint32_t& okbits, int bit) {
-  if (vec4) {
-    const bool ok = row_ok && k_left > 0;
+// Edge-path quad of elements k .. k+3 of a row (valid range [0, k_valid)): with V4 the quad is
+// wholly in or out (raw load recording a validity bit, masked at commit); otherwise element-wise.
+template <typename T, bool V4>
+__device__ __forceinline__ quad_t<T> fetch_quad_k(const T* p, const T* safe, bool row_ok, int k, int k_valid,
+                                                  uint32_t& okbits, int bit) {
+  if constexpr (V4) {
+    const bool ok = row_ok && k >= 0 && k < k_valid;
     okbits |= static_cast<uint32_t>(ok) << bit;
     return raw_quad<T>(ok ? p : safe);
+  } else {
+    okbits |= 1u << bit;
+    return load_quad_scalar<T>(p, safe, row_ok, -k, k_valid - k);
   }
-  okbits |= 1u << bit;
-  return load_quad_scalar<T>(p, safe, row_ok, k_left);
 }
 
 template <typename T>
@@ -148,9 +160,10 @@ __device__ __forceinline__ void commit_quad(T* lds, int r, int kq, const quad_t<
   }
 }
 
-// K-contiguous rows: element (r, k) = base[r * stride + k].  Thread t moves the quad
-// (r, k) = (t / 8 + 32 i, 4 (t % 8)) of every chunk, i < ROWS / 32.
-template <typename T, int ROWS>
+// K-contiguous rows: element (r, k) = base[row(r) * stride + k].  Thread t moves the quad
+// (r, k) = (t / 8 + 32 i, 4 (t % 8)) of every chunk, i < ROWS / 32.  By default row(r) = r for
+// r < rows_valid; prepare_rows() lets a kernel map tile rows to other source rows.
+template <typename T, int ROWS, bool V4>
 struct KRowLoader {
   static constexpr int kQuads = ROWS * (kChunkK / 4) / kGemmThreads;
   static_assert(kQuads >= 1 && ROWS * (kChunkK / 4) % kGemmThreads == 0, "tile too small");
@@ -162,33 +175,71 @@ struct KRowLoader {
   int64_t stride;
   int rows_valid;
   int k_valid;
-  bool vec4;
+  int64_t src_row[kQuads] = {};  // source row of each of the thread's tile rows (clamped)
+  uint32_t off[kQuads] = {};     // byte offset of (src_row, k = 4 (t % 8)) from base
+  uint32_t rowok = 0;            // bit i: tile row i of this thread is a real row
 
-  __device__ __forceinline__ void fetch(int k0, Regs& g) const {
-    const int k = k0 + (threadIdx.x % (kChunkK / 4)) * 4;
-    g.ok = 0;
+  static __device__ __forceinline__ int tile_row(int i) {
+    return (static_cast<int>(threadIdx.x) + i * kGemmThreads) / (kChunkK / 4);
+  }
+  static __device__ __forceinline__ int lane_k() { return (threadIdx.x % (kChunkK / 4)) * 4; }
+
+  __device__ __forceinline__ void prepare() {
+    rowok = 0;
 #pragma unroll
     for (int i = 0; i < kQuads; ++i) {
-      const int r = (threadIdx.x + i * kGemmThreads) / (kChunkK / 4);
-      g.q[i] = fetch_quad<T>(base + r * stride + k, base, vec4, r < rows_valid, k_valid - k, g.ok, i);
+      const int r = tile_row(i);
+      src_row[i] = r < rows_valid ? r : rows_valid - 1;
+      rowok |= static_cast<uint32_t>(r < rows_valid) << i;
+    }
+    finish_prepare();
+  }
+  // Call after filling src_row and rowok (custom row maps).
+  __device__ __forceinline__ void finish_prepare() {
+#pragma unroll
+    for (int i = 0; i < kQuads; ++i)
+      off[i] = static_cast<uint32_t>((src_row[i] * stride + lane_k()) * static_cast<int64_t>(sizeof(T)));
+  }
+  __device__ __forceinline__ bool row_ok(int i) const { return (rowok >> i) & 1; }
+
+  __device__ __forceinline__ void fetch_edge(int k0, Regs& g) const {
+    const int k = k0 + lane_k();
+    g.ok = 0;
+#pragma unroll
+    for (int i = 0; i < kQuads; ++i)
+      g.q[i] = fetch_quad_k<T, V4>(base + src_row[i] * stride + k, base, row_ok(i), k, k_valid, g.ok, i);
+  }
+  __device__ __forceinline__ void commit_edge(const Regs& g, T* lds) const {
+#pragma unroll
+    for (int i = 0; i < kQuads; ++i) commit_quad<T>(lds, tile_row(i), lane_k(), mask_quad<T>(g.q[i], (g.ok >> i) & 1));
+  }
+  __device__ __forceinline__ void fetch(int k0, Regs& g) const {
+    if constexpr (V4) {
+#pragma unroll
+      for (int i = 0; i < kQuads; ++i) g.q[i] = quad_at<T>(base + k0, off[i]);
+    } else {
+      fetch_edge(k0, g);
     }
   }
   __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
-    const int kq = (threadIdx.x % (kChunkK / 4)) * 4;
+    if constexpr (V4) {
 #pragma unroll
-    for (int i = 0; i < kQuads; ++i)
-      commit_quad<T>(lds, (threadIdx.x + i * kGemmThreads) / (kChunkK / 4), kq, mask_quad<T>(g.q[i], (g.ok >> i) & 1));
+      for (int i = 0; i < kQuads; ++i) commit_quad<T>(lds, tile_row(i), lane_k(), g.q[i]);
+    } else {
+      commit_edge(g, lds);
+    }
   }
 };
 
-// MN-contiguous source: element (k, mn) = base[k * kstride + mn], staged
-// transposed into lds[mn][k].  A thread owns a block of KB consecutive k rows x 4
-// consecutive mn (consecutive threads take consecutive mn quads, so each global
-// load is coalesced along mn), transposes it in registers and stores KB
-// consecutive k values per mn row.  KB = ROWS / 32 so one block per thread
-// covers the chunk.  Optional scales: per-mn `cs[mn]`, per-k
-// `rs[k * rs_stride] * rs_mul` (both global and cache-resident).
-template <typename T, int ROWS>
+// MN-contiguous source: element (k, mn) = base[k * kstride + mn], staged transposed into
+// lds[mn][k].  A thread owns a block of KB consecutive k rows x 4 consecutive mn
+// (consecutive threads take consecutive mn quads, so each global load is coalesced along mn),
+// transposes it in registers and stores KB consecutive k values per mn row.  KB = ROWS / 32 so
+// one block per thread covers the chunk.  Optional scales: per-mn `cs[mn]`, per-k
+// `rs[k * rs_stride] * rs_mul`; `colsum` also sums the unscaled values of the thread's mn quad
+// over its k rows (e.g. a bias gradient, see reduce_colsum).  Unscaled 16-bit interior chunks
+// are transposed as raw bits (byte permutes, no conversions).
+template <typename T, int ROWS, bool V4>
 struct MNLoader {
   static constexpr int kQuadsPerK = ROWS / 4;
   static constexpr int KB = ROWS / 32;
@@ -203,43 +254,67 @@ struct MNLoader {
   int64_t kstride;
   int mn_valid;
   int k_valid;
-  bool vec4;
   const T* cs = nullptr;        // per-mn scale, or null
   const float* rs = nullptr;    // per-k scale, or null
   int64_t rs_stride = 1;
   float rs_mul = 1.f;
-  // per-mn scale of this thread's quad (loaded once; cs does not depend on k)
-  float c[4] = {1.f, 1.f, 1.f, 1.f};
-  // with `colsum` set, commit() also accumulates the unscaled values of the thread's mn
-  // quad over its k rows (column sums over K, e.g. a bias gradient); see reduce_colsum()
   bool colsum = false;
+  float c[4] = {1.f, 1.f, 1.f, 1.f};       // per-mn scale of this thread's quad
   mutable float csum[4] = {0.f, 0.f, 0.f, 0.f};
+  int mn_src = 0;                          // this thread's (clamped) mn quad start
+  uint32_t off[KB] = {};                   // byte offset of (kb + t, mn_src) from a chunk base
 
-  __device__ __forceinline__ void init() {
-    if (cs != nullptr) {
-      const int mn = (threadIdx.x % kQuadsPerK) * 4;
-      quad_to_f32<T>(load_quad_scalar<T>(cs + mn, cs, true, mn_valid - mn), c);
-    }
+  static __device__ __forceinline__ int lane_mn() { return (threadIdx.x % kQuadsPerK) * 4; }
+  static __device__ __forceinline__ int lane_kb() { return (threadIdx.x / kQuadsPerK) * KB; }
+
+  __device__ __forceinline__ void prepare() {
+    const int mn = lane_mn();
+    mn_src = (V4 && mn >= mn_valid) ? mn_valid - 4 : mn;
+#pragma unroll
+    for (int t = 0; t < KB; ++t)
+      off[t] = static_cast<uint32_t>(((lane_kb() + t) * kstride + mn_src) * static_cast<int64_t>(sizeof(T)));
+    if (cs != nullptr) quad_to_f32<T>(load_quad_scalar<T>(cs + mn, cs, true, 0, mn_valid - mn), c);
   }
-  __device__ __forceinline__ void fetch(int k0, Regs& g) const {
-    const int mn = (threadIdx.x % kQuadsPerK) * 4;
-    const int kb = (threadIdx.x / kQuadsPerK) * KB;
+
+  __device__ __forceinline__ void fetch_edge(int k0, Regs& g) const {
+    const int mn = lane_mn();
     g.ok = 0;
 #pragma unroll
     for (int t = 0; t < KB; ++t) {
-      const int k = k0 + kb + t;
-      g.q[t] = fetch_quad<T>(base + static_cast<int64_t>(k) * kstride + mn, base, vec4, k < k_valid, mn_valid - mn,
-                             g.ok, t);
-      g.s[t] = rs != nullptr ? rs[static_cast<int64_t>(k < k_valid ? k : 0) * rs_stride] : 1.f;
+      const int k = k0 + lane_kb() + t;
+      const bool kok = k >= 0 && k < k_valid;
+      const int kc = kok ? k : 0;
+      if constexpr (V4) {
+        g.ok |= static_cast<uint32_t>(kok) << t;
+        g.q[t] = raw_quad<T>(kok ? base + static_cast<int64_t>(k) * kstride + mn_src : base);
+      } else {
+        g.ok |= 1u << t;
+        g.q[t] = load_quad_scalar<T>(base + static_cast<int64_t>(kc) * kstride + mn, base, kok, 0, mn_valid - mn);
+      }
+      g.s[t] = rs != nullptr ? rs[static_cast<int64_t>(kc) * rs_stride] : 1.f;
     }
   }
-  __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
-    const int mn = (threadIdx.x % kQuadsPerK) * 4;
-    const int kb = (threadIdx.x / kQuadsPerK) * KB;
+  __device__ __forceinline__ void fetch(int k0, Regs& g) const {
+    if constexpr (V4) {
+      const T* kb = base + static_cast<int64_t>(k0) * kstride;
+#pragma unroll
+      for (int t = 0; t < KB; ++t) {
+        g.q[t] = quad_at<T>(kb, off[t]);
+        g.s[t] = rs != nullptr ? rs[static_cast<int64_t>(k0 + lane_kb() + t) * rs_stride] : 1.f;
+      }
+    } else {
+      fetch_edge(k0, g);
+    }
+  }
+
+  // Float path: optional masking of k rows (edge), column sums, scales.
+  __device__ __forceinline__ void commit_f32(const Regs& g, T* lds, bool masked) const {
+    const int mn = lane_mn();
+    const int kb = lane_kb();
     float v[KB][4];
 #pragma unroll
     for (int t = 0; t < KB; ++t) {
-      quad_to_f32<T>(mask_quad<T>(g.q[t], (g.ok >> t) & 1), v[t]);
+      quad_to_f32<T>(masked ? mask_quad<T>(g.q[t], (g.ok >> t) & 1) : g.q[t], v[t]);
       if (colsum) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) csum[j] += v[t][j];
@@ -261,14 +336,54 @@ struct MNLoader {
       }
     }
   }
+  // Raw transpose of 16-bit values: element j of quad t is the 16-bit half (j & 1) of word
+  // (j >> 1); pairs of k rows are merged into one 32-bit word per mn with a byte permute.
+  __device__ __forceinline__ void commit_raw16(const Regs& g, T* lds) const {
+    const int mn = lane_mn();
+    const int kb = lane_kb();
+    constexpr uint32_t kLo = 0x05040100u, kHi = 0x07060302u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w[(KB + 1) / 2];
+#pragma unroll
+      for (int t = 0; t + 1 < KB; t += 2) {
+        const uint32_t a = (j >> 1) ? g.q[t].y : g.q[t].x;
+        const uint32_t b = (j >> 1) ? g.q[t + 1].y : g.q[t + 1].x;
+        w[t / 2] = __builtin_amdgcn_perm(b, a, (j & 1) ? kHi : kLo);
+      }
+      if constexpr (KB == 1) {
+        const uint32_t a = (j >> 1) ? g.q[0].y : g.q[0].x;
+        *reinterpret_cast<uint16_t*>(lds + lds_index<T>(mn + j, kb)) = static_cast<uint16_t>((j & 1) ? a >> 16 : a);
+      } else if constexpr (KB == 2) {
+        *reinterpret_cast<uint32_t*>(lds + lds_index<T>(mn + j, kb)) = w[0];
+      } else {
+        static_assert(KB == 4, "KB in {1, 2, 4}");
+        *reinterpret_cast<uint2*>(lds + lds_index<T>(mn + j, kb)) = make_uint2(w[0], w[1]);
+      }
+    }
+  }
+  __device__ __forceinline__ void commit_edge(const Regs& g, T* lds) const { commit_f32(g, lds, true); }
+  __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
+    if constexpr (!V4) {
+      commit_f32(g, lds, true);
+    } else if constexpr (sizeof(T) == 2) {
+      if (cs == nullptr && rs == nullptr && !colsum) {
+        commit_raw16(g, lds);
+      } else {
+        commit_f32(g, lds, false);
+      }
+    } else {
+      commit_f32(g, lds, false);
+    }
+  }
 };
 
 // Column sums gathered by a `colsum` MNLoader: the 256 threads hold partial sums of
 // 4 consecutive mn each (thread t: mn = 4 (t % ROWS/4)); they are combined in a fixed
 // order through LDS and written as dst[mn] for mn < mn_valid.  Call after the main loop
 // (which ends with a barrier), with every thread of the block.
-template <typename T, int ROWS>
-__device__ __forceinline__ void reduce_colsum(const MNLoader<T, ROWS>& ld, T* lds, T* __restrict__ dst) {
+template <typename T, int ROWS, bool V4>
+__device__ __forceinline__ void reduce_colsum(const MNLoader<T, ROWS, V4>& ld, T* lds, T* __restrict__ dst) {
   constexpr int kQ = ROWS / 4;                  // mn quads
   constexpr int kGroups = kGemmThreads / kQ;    // threads per quad
   float* red = reinterpret_cast<float*>(lds);   // [kGroups][ROWS]
@@ -282,6 +397,12 @@ __device__ __forceinline__ void reduce_colsum(const MNLoader<T, ROWS>& ld, T* ld
     for (int g2 = 0; g2 < kGroups; ++g2) s += red[g2 * ROWS + threadIdx.x];
     dst[threadIdx.x] = from_f32<T>(s);
   }
+}
+
+// Host check: loaders address a tile as a uniform base plus 32-bit per-lane byte offsets that
+// span at most 256 rows of `stride` elements.
+inline bool gemm_stride_ok(int64_t stride, size_t esz) {
+  return stride >= 0 && (stride + 1) * 256 * static_cast<int64_t>(esz) < (int64_t{1} << 31);
 }
 
 // ---------------------------------------------------------------- XCD-aware block order
@@ -331,7 +452,7 @@ constexpr int gemm_lds_elems() {
 // computed from the __shared__ base (no pointer tables), so every LDS access stays
 // a ds_* instruction and waits only on the LDS counter.
 template <typename T, int BR, int BC, int WR, int WC, int DEPTH = 1, class LA, class LB>
-__device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K, T* lds,
+__device__ __forceinline__ void gemm_mainloop(LA& la, LB& lb, int K, T* lds,
                                               f32x4_t (&acc)[TileShape<BR, BC, WR, WC>::kTR]
                                                             [TileShape<BR, BC, WR, WC>::kTC]) {
   static_assert(DEPTH == 1 || DEPTH == 2, "prefetch depth 1 or 2");
@@ -360,23 +481,41 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
     __builtin_amdgcn_sched_barrier(0);
   };
 
+  // chunk c covers k in [kbeg + 32 c, kbeg + 32 c + 32); only chunk 0 can be partial
+  const int kbeg = K - nk * kChunkK;
+  const bool edge0 = kbeg < 0;
+  la.prepare();
+  lb.prepare();
   typename LA::Regs ra0;
   typename LB::Regs rb0;
-  la.fetch(0, ra0);
-  lb.fetch(0, rb0);
+  if (edge0) {
+    la.fetch_edge(kbeg, ra0);
+    lb.fetch_edge(kbeg, rb0);
+  } else {
+    la.fetch(kbeg, ra0);
+    lb.fetch(kbeg, rb0);
+  }
+  auto commit0 = [&]() {
+    if (edge0) {
+      la.commit_edge(ra0, lds);
+      lb.commit_edge(rb0, lds + BR * P);
+    } else {
+      la.commit(ra0, lds);
+      lb.commit(rb0, lds + BR * P);
+    }
+  };
   // The steady-state loops below fetch unconditionally: with every trip issuing the
   // same loads into the same registers, the wait-count analysis can see that a
   // register set's previous loads retired before it is refilled, and no conditional
   // path splits the accumulators' live ranges.
   if constexpr (DEPTH == 1) {
-    la.commit(ra0, lds);
-    lb.commit(rb0, lds + BR * P);
+    commit0();
     __syncthreads();
     int kc = 0;
     for (; kc + 1 < nk; ++kc) {
       const int cur = (kc & 1) * kBuf;
-      la.fetch((kc + 1) * kChunkK, ra0);
-      lb.fetch((kc + 1) * kChunkK, rb0);
+      la.fetch(kbeg + (kc + 1) * kChunkK, ra0);
+      lb.fetch(kbeg + (kc + 1) * kChunkK, rb0);
       mma(cur);
       la.commit(ra0, lds + kBuf - cur);
       lb.commit(rb0, lds + kBuf - cur + BR * P);
@@ -388,25 +527,24 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
     typename LA::Regs ra1;
     typename LB::Regs rb1;
     if (nk > 1) {
-      la.fetch(kChunkK, ra1);
-      lb.fetch(kChunkK, rb1);
+      la.fetch(kbeg + kChunkK, ra1);
+      lb.fetch(kbeg + kChunkK, rb1);
     }
-    la.commit(ra0, lds);
-    lb.commit(rb0, lds + BR * P);
+    commit0();
     __syncthreads();
     // Entering each trip: chunk kc is in LDS buffer (kc & 1) and its registers (set 0)
     // are free; chunk kc + 1 is in flight into set 1.
     int kc = 0;
     for (; kc + 3 < nk; kc += 2) {
       const int cur = (kc & 1) * kBuf;
-      la.fetch((kc + 2) * kChunkK, ra0);
-      lb.fetch((kc + 2) * kChunkK, rb0);
+      la.fetch(kbeg + (kc + 2) * kChunkK, ra0);
+      lb.fetch(kbeg + (kc + 2) * kChunkK, rb0);
       mma(cur);
       la.commit(ra1, lds + kBuf - cur);
       lb.commit(rb1, lds + kBuf - cur + BR * P);
       __syncthreads();
-      la.fetch((kc + 3) * kChunkK, ra1);
-      lb.fetch((kc + 3) * kChunkK, rb1);
+      la.fetch(kbeg + (kc + 3) * kChunkK, ra1);
+      lb.fetch(kbeg + (kc + 3) * kChunkK, rb1);
       mma(kBuf - cur);
       la.commit(ra0, lds + cur);
       lb.commit(rb0, lds + cur + BR * P);
@@ -415,8 +553,8 @@ __device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, int K,
     // 1 to 3 chunks left: kc (in LDS), kc + 1 (set 1, in flight), kc + 2 (not fetched)
     const int cur = (kc & 1) * kBuf;
     if (kc + 2 < nk) {
-      la.fetch((kc + 2) * kChunkK, ra0);
-      lb.fetch((kc + 2) * kChunkK, rb0);
+      la.fetch(kbeg + (kc + 2) * kChunkK, ra0);
+      lb.fetch(kbeg + (kc + 2) * kChunkK, rb0);
       mma(cur);
       la.commit(ra1, lds + kBuf - cur);
       lb.commit(rb1, lds + kBuf - cur + BR * P);

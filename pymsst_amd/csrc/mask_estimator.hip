@@ -43,40 +43,40 @@ __device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + __ex
 // ------------------------------------------------------------------ forward
 
 // A operand of the forward: rows [0, 64) are left rows l0 + r of W_b, rows
-// [64, 128) the gate rows I + l0 + (r - 64); K = H contiguous.
-template <typename T>
-struct LeftGateLoader {
-  static constexpr int kQuads = 128 * (kChunkK / 4) / kGemmThreads;
-  struct Regs {
-    quad_t<T> q[kQuads];
-    uint32_t ok;
-  };
-  const T* wb;  // band weights [2I][H]
-  int H, I, l0;
-  bool vec4;
-  __device__ __forceinline__ void fetch(int k0, Regs& g) const {
-    const int k = k0 + (threadIdx.x % (kChunkK / 4)) * 4;
-    g.ok = 0;
+// [64, 128) the gate rows I + l0 + (r - 64); K = H contiguous.  Outputs l >= I are
+// clamped to l = I - 1 in interior chunks (discarded by the epilogue).
+template <typename T, bool V4>
+struct LeftGateLoader : KRowLoader<T, 128, V4> {
+  using Base = KRowLoader<T, 128, V4>;
+  int I, l0;
+  __device__ __forceinline__ LeftGateLoader(const T* wb, int H, int I_, int l0_) : Base{wb, H, 128, H}, I(I_), l0(l0_) {}
+  __device__ __forceinline__ void prepare() {
+    this->rowok = 0;
 #pragma unroll
-    for (int i = 0; i < kQuads; ++i) {
-      const int r = (threadIdx.x + i * kGemmThreads) / (kChunkK / 4);
+    for (int i = 0; i < Base::kQuads; ++i) {
+      const int r = Base::tile_row(i);
       const int l = l0 + (r & 63);
-      const T* p = wb + static_cast<int64_t>(r < 64 ? l : I + l) * H + k;
-      g.q[i] = fetch_quad<T>(p, wb, vec4, l < I, H - k, g.ok, i);
+      const int lc = l < I ? l : I - 1;
+      this->src_row[i] = r < 64 ? lc : I + lc;
+      this->rowok |= static_cast<uint32_t>(l < I) << i;
     }
-  }
-  __device__ __forceinline__ void commit(const Regs& g, T* lds) const {
-    const int kq = (threadIdx.x % (kChunkK / 4)) * 4;
-#pragma unroll
-    for (int i = 0; i < kQuads; ++i)
-      commit_quad<T>(lds, (threadIdx.x + i * kGemmThreads) / (kChunkK / 4), kq, mask_quad<T>(g.q[i], (g.ok >> i) & 1));
+    this->finish_prepare();
   }
 };
 
+// Forward tile: 128 rows of M x (64 left + 64 gate outputs).  One chunk of prefetch in
+// registers and a register budget of 3 waves per SIMD (the compiler fits 4) measured faster
+// than two chunks in flight at 2 waves per SIMD: 52 vs 60 us at configs[1] shapes.
+#ifndef PMSST_ME_FWD_DEPTH
+#define PMSST_ME_FWD_DEPTH 1
+#endif
+#ifndef PMSST_ME_FWD_WAVES
+#define PMSST_ME_FWD_WAVES 3
+#endif
 constexpr int kFwdBM = 128;
 
 template <typename T, bool V4>
-__global__ __launch_bounds__(kGemmThreads) void me_fwd_kernel(const T* __restrict__ x, const T* __restrict__ weight,
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(PMSST_ME_FWD_WAVES))) void me_fwd_kernel(const T* __restrict__ x, const T* __restrict__ weight,
                                                               const T* __restrict__ bias, T* __restrict__ pre,
                                                               T* __restrict__ out, int max_lchunks, XcdGrid xg,
                                                               MaskArgs a) {
@@ -94,14 +94,14 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_kernel(const T* __restric
   const int H = a.H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
-  LeftGateLoader<T> la{weight + static_cast<int64_t>(2) * off * H, H, I, l0, V4};
-  KRowLoader<T, kFwdBM> lb{x + (m0 * a.NB + band) * H, static_cast<int64_t>(a.NB) * H, rows_valid, H, V4};
+  LeftGateLoader<T, V4> la(weight + static_cast<int64_t>(2) * off * H, H, I, l0);
+  KRowLoader<T, kFwdBM, V4> lb{x + (m0 * a.NB + band) * H, static_cast<int64_t>(a.NB) * H, rows_valid, H};
   f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
   for (int i = 0; i < S::kTR; ++i)
 #pragma unroll
     for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  gemm_mainloop<T, 128, kFwdBM, 1, 4, 2>(la, lb, H, lds, acc);
+  gemm_mainloop<T, 128, kFwdBM, 1, 4, PMSST_ME_FWD_DEPTH>(la, lb, H, lds, acc);
 
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
 #pragma unroll
@@ -277,8 +277,8 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __rest
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
 
   // A[h][j] = W_b[j][h0 + h]  (MN-contiguous in h);  B[m][j] = dpre[m0 + m][2 off + j]
-  MNLoader<T, kDxBH> la{weight + static_cast<int64_t>(2) * off * H + h0, H, H - h0, 2 * I, V4};
-  KRowLoader<T, kDxBM> lb{dpre + m0 * pitch2 + 2 * off, pitch2, rows_valid, 2 * I, V4};
+  MNLoader<T, kDxBH, V4> la{weight + static_cast<int64_t>(2) * off * H + h0, H, H - h0, 2 * I};
+  KRowLoader<T, kDxBM, V4> lb{dpre + m0 * pitch2 + 2 * off, pitch2, rows_valid, 2 * I};
   f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
   for (int i = 0; i < S::kTR; ++i)
@@ -340,9 +340,9 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __rest
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
 
   // A[h][m] = x[m][band][h0 + h];  B[j][m] = dpre[m][2 off + j0 + j]   (both MN-contiguous, K = M)
-  MNLoader<T, kDwBH> la{x + static_cast<int64_t>(band) * H + h0, static_cast<int64_t>(a.NB) * H, H - h0,
-                        static_cast<int>(a.M), V4};
-  MNLoader<T, kDwBJ> lb{dpre + 2 * off + j0, pitch2, K2 - j0, static_cast<int>(a.M), V4};
+  MNLoader<T, kDwBH, V4> la{x + static_cast<int64_t>(band) * H + h0, static_cast<int64_t>(a.NB) * H, H - h0,
+                            static_cast<int>(a.M)};
+  MNLoader<T, kDwBJ, V4> lb{dpre + 2 * off + j0, pitch2, K2 - j0, static_cast<int>(a.M)};
   // the first hidden tile of each (band, j chunk) also sums dpre over the rows: dbias
   lb.colsum = h0 == 0;
   f32x4_t acc[S::kTR][S::kTC];
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __rest
 #pragma unroll
     for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   gemm_mainloop<T, kDwBH, kDwBJ, 2, 2>(la, lb, static_cast<int>(a.M), lds, acc);
-  if (lb.colsum) reduce_colsum<T, kDwBJ>(lb, lds, dbias + 2 * off + j0);
+  if (lb.colsum) reduce_colsum<T, kDwBJ, V4>(lb, lds, dbias + 2 * off + j0);
 
   T* dwb = dw + static_cast<int64_t>(2) * off * H;  // [2I][H]
   const int hr = (wave >> 1) * (kDwBH / 2), jc = (wave & 1) * (kDwBJ / 2);
@@ -393,6 +393,8 @@ int check_mask(const char* op, const int64_t* dim_inputs, int64_t band_count, in
     maxw = dim_inputs[b] > maxw ? dim_inputs[b] : maxw;
   }
   PMSST_REQUIRE(total < (int64_t{1} << 29), "%s: too many features", op);
+  PMSST_REQUIRE(gemm_stride_ok(band_count * H, 4) && gemm_stride_ok(2 * total, 4),
+                "%s: rows too long for 32-bit tile offsets", op);
   hm->NB = static_cast<int>(band_count);
   hm->F = static_cast<int>(total);
   hm->max_width = static_cast<int>(maxw);
