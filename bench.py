@@ -66,6 +66,9 @@ def _args(argv=None):
     ap.add_argument("--train-warmup", type=int, default=3)
     ap.add_argument("--train-impl", choices=("both", "fused", "stock"), default="both",
                     help="which train-step legs to run (profiling one implementation at a time)")
+    ap.add_argument("--train-workload", default="bsr_train",
+                    help="training configuration of the train leg (pymsst_amd.workloads.WORKLOADS key; "
+                         "bsr_train = configs[2])")
     return ap.parse_args(argv)
 
 
@@ -240,8 +243,16 @@ def _cpu_baseline(budget_s: float):
     }
 
 
-def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused")) -> dict:
-    """BS-RoFormer dim 192, depth 6, 4 stems, batch 4 x 131584 stereo samples,
+_TRAIN_DESCRIPTIONS = {
+    "bsr_train": "configs[2] BS-RoFormer dim 192, depth 6, 8x64 heads, 4 stems, batch 4 x 131584 stereo "
+                 "(258 frames), bf16 autocast, multi-res STFT L1, AdamW 5e-4",
+    "bsr_large": "configs[4] BS-RoFormer dim 512, depth 12, 8x64 heads, 1 stem, batch 2 x 485100 stereo "
+                 "(948 frames), activation checkpointing per axial block, bf16 autocast, L1, AdamW 5e-4",
+}
+
+
+def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused"), workload: str = "bsr_train") -> dict:
+    """Default configs[2]: BS-RoFormer dim 192, depth 6, 4 stems, batch 4 x 131584 stereo samples,
     bf16 autocast, multi-resolution STFT loss, AdamW 5e-4.  One step = forward, backward and
     optimizer step; train samples/s = batch / median step time, for the stock modules and for
     the model patched onto the HIP kernels (same seed, same batch)."""
@@ -250,7 +261,7 @@ def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused")) -> dict
     from pymsst_amd import fused_roformer as fr
     from pymsst_amd.workloads import WORKLOADS, workload_batch
 
-    wl = WORKLOADS["bsr_train"]
+    wl = WORKLOADS[workload]
     dev = torch.device("cuda:0")
     target, mixture = workload_batch(wl, seed=0, device=dev)
     out = {}
@@ -270,9 +281,10 @@ def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused")) -> dict
         opt = torch.optim.AdamW(model.parameters(), lr=wl.lr)
         times, losses = [], []
         for i in range(warmup + steps):
+            print(f"[train] {workload} {impl} step {i}", file=sys.stderr, flush=True)
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            with torch.autocast("cuda", dtype=torch.bfloat16):
+            with torch.autocast("cuda", dtype=wl.amp_dtype or torch.float32, enabled=wl.amp_dtype is not None):
                 loss = model(mixture, target)
             loss.backward()
             opt.step()
@@ -288,8 +300,7 @@ def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused")) -> dict
         del model, opt
         torch.cuda.empty_cache()
     res = {
-        "workload": "configs[2] BS-RoFormer dim 192, depth 6, 8x64 heads, 4 stems, batch 4 x 131584 stereo "
-                    "(258 frames), bf16 autocast, multi-res STFT L1, AdamW 5e-4",
+        "workload": _TRAIN_DESCRIPTIONS.get(workload, workload),
         "steps": steps,
         "warmup": warmup,
         "detail": out,
@@ -392,7 +403,8 @@ def main(argv=None) -> int:
     copy_gbs = 2 * src.numel() * src.element_size() * 10 / (c0.elapsed_time(c1) * 1e-3) / 1e9
     del src, dst
     impls = ("stock", "fused") if args.train_impl == "both" else (args.train_impl,)
-    train = _train_leg(torch, args.train_steps, args.train_warmup, impls) if args.train_steps > 0 else None
+    train = (_train_leg(torch, args.train_steps, args.train_warmup, impls, args.train_workload)
+             if args.train_steps > 0 else None)
     cpu = None if args.no_cpu_baseline else _cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC,

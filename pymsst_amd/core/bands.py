@@ -40,21 +40,44 @@ def inference_tanh(x: torch.Tensor) -> torch.Tensor:
     return torch.tanh(x)
 
 
-def grouped_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
-    """Per-group Linear over the second-to-last axis via one batched GEMM.
+class _GroupedLinearBmm(torch.autograd.Function):
+    """bmm / baddbmm grouped Linear with an explicit backward.
 
-    The right operand is made contiguous before the product (16-bit batched GEMMs
-    with a transposed right operand are avoided on this platform).
+    Autograd's own bmm backward multiplies by transposed views of the saved operands
+    (``grad @ W^T``, ``X^T @ grad``); 16-bit batched GEMMs whose right operand is such a
+    transposed view have faulted GPUs of this platform, so every product here, forward and
+    backward, takes contiguous operands.
     """
-    groups, out_features, in_features = weight.shape
-    lead = x.shape[:-2]
-    xt = x.reshape(-1, groups, in_features).transpose(0, 1)
-    wt = weight.transpose(1, 2).contiguous()
-    if bias is None:
-        out = torch.bmm(xt, wt)
-    else:
-        out = torch.baddbmm(bias.unsqueeze(1), xt, wt)
-    return out.transpose(0, 1).reshape(*lead, groups, out_features)
+
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        groups, out_features, in_features = weight.shape
+        lead = x.shape[:-2]
+        xt = x.reshape(-1, groups, in_features).transpose(0, 1).contiguous()  # [G, M, I]
+        wt = weight.transpose(1, 2).contiguous()                               # [G, I, O]
+        out = torch.bmm(xt, wt) if bias is None else torch.baddbmm(bias.unsqueeze(1), xt, wt)
+        ctx.save_for_backward(xt, weight)
+        ctx.lead = lead
+        ctx.has_bias = bias is not None
+        return out.transpose(0, 1).reshape(*lead, groups, out_features)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        xt, weight = ctx.saved_tensors
+        groups, out_features, in_features = weight.shape
+        g = grad_out.reshape(-1, groups, out_features).transpose(0, 1).contiguous()  # [G, M, O]
+        grad_x = torch.bmm(g, weight.contiguous())                                   # [G, M, I]
+        grad_w = torch.bmm(g.transpose(1, 2).contiguous(), xt)                        # [G, O, I]
+        grad_b = g.sum(dim=1) if ctx.has_bias else None
+        grad_x = grad_x.transpose(0, 1).reshape(*ctx.lead, groups, in_features)
+        return grad_x, grad_w, grad_b
+
+
+def grouped_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    """Per-group Linear over the second-to-last axis via one batched GEMM (bmm / baddbmm semantics,
+    tests/test_training_smoke.py:28-37).  Operands of every product are contiguous (see
+    ``_GroupedLinearBmm``)."""
+    return _GroupedLinearBmm.apply(x, weight, bias)
 
 
 def _prefix(widths):

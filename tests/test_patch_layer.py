@@ -338,3 +338,20 @@ def test_attention_gate_patch_and_restore(monkeypatch):
     monkeypatch.setenv(fr.EXPERIMENTAL_ATTENTION_GATES_ENV, "off")
     status = fr.apply_roformer_fused_training_backend(_small_model(), "hip", extension=ext)
     assert not status.patched_attention_gates and status.attention_gate_mode is None
+
+
+@pytest.mark.parametrize("bias", [True, False])
+def test_stock_grouped_linear_explicit_backward_matches_autograd(bias):
+    """The stock grouped_linear's hand-written backward (contiguous operands for every batched
+    product) equals autograd of the same per-group Linear."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 5, 4, 6, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(4, 7, 6, generator=g, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(4, 7, generator=g, dtype=torch.float64, requires_grad=True) if bias else None
+    out = bands.grouped_linear(x, w, b)
+    ref = torch.stack([x[..., k, :] @ w[k].T + (b[k] if bias else 0) for k in range(4)], dim=-2)
+    torch.testing.assert_close(out, ref)
+    gout = torch.randn(out.shape, generator=g, dtype=torch.float64)
+    inputs = [t for t in (x, w, b) if t is not None]
+    for got, want in zip(torch.autograd.grad(out, inputs, gout), torch.autograd.grad(ref, inputs, gout)):
+        torch.testing.assert_close(got, want)
