@@ -53,24 +53,29 @@ class _GroupedLinearBmm(torch.autograd.Function):
     def forward(ctx, x, weight, bias):
         groups, out_features, in_features = weight.shape
         lead = x.shape[:-2]
-        xt = x.reshape(-1, groups, in_features).transpose(0, 1).contiguous()  # [G, M, I]
-        wt = weight.transpose(1, 2).contiguous()                               # [G, I, O]
-        out = torch.bmm(xt, wt) if bias is None else torch.baddbmm(bias.unsqueeze(1), xt, wt)
-        ctx.save_for_backward(xt, weight)
+        # the dtype autocast would give bmm / baddbmm; the backward computes in it too
+        dt = torch.get_autocast_dtype(x.device.type) if torch.is_autocast_enabled(x.device.type) else x.dtype
+        ctx.dtypes = (x.dtype, weight.dtype, bias.dtype if bias is not None else None)
+        xt = x.reshape(-1, groups, in_features).transpose(0, 1).to(dt).contiguous()  # [G, M, I]
+        wc = weight.to(dt)
+        wt = wc.transpose(1, 2).contiguous()                                         # [G, I, O]
+        with torch.autocast(x.device.type, enabled=False):
+            out = torch.bmm(xt, wt) if bias is None else torch.baddbmm(bias.to(dt).unsqueeze(1), xt, wt)
+        ctx.save_for_backward(xt, wc)
         ctx.lead = lead
-        ctx.has_bias = bias is not None
         return out.transpose(0, 1).reshape(*lead, groups, out_features)
 
     @staticmethod
     def backward(ctx, grad_out):
-        xt, weight = ctx.saved_tensors
-        groups, out_features, in_features = weight.shape
-        g = grad_out.reshape(-1, groups, out_features).transpose(0, 1).contiguous()  # [G, M, O]
-        grad_x = torch.bmm(g, weight.contiguous())                                   # [G, M, I]
-        grad_w = torch.bmm(g.transpose(1, 2).contiguous(), xt)                        # [G, O, I]
-        grad_b = g.sum(dim=1) if ctx.has_bias else None
-        grad_x = grad_x.transpose(0, 1).reshape(*ctx.lead, groups, in_features)
-        return grad_x, grad_w, grad_b
+        xt, wc = ctx.saved_tensors
+        groups, out_features, in_features = wc.shape
+        x_dt, w_dt, b_dt = ctx.dtypes
+        g = grad_out.to(xt.dtype).reshape(-1, groups, out_features).transpose(0, 1).contiguous()  # [G, M, O]
+        grad_x = torch.bmm(g, wc.contiguous())                                                    # [G, M, I]
+        grad_w = torch.bmm(g.transpose(1, 2).contiguous(), xt)                                     # [G, O, I]
+        grad_b = g.sum(dim=1).to(b_dt) if b_dt is not None else None
+        grad_x = grad_x.transpose(0, 1).reshape(*ctx.lead, groups, in_features).to(x_dt)
+        return grad_x, grad_w.to(w_dt), grad_b
 
 
 def grouped_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
