@@ -248,6 +248,8 @@ _TRAIN_DESCRIPTIONS = {
                  "(258 frames), bf16 autocast, multi-res STFT L1, AdamW 5e-4",
     "bsr_large": "configs[4] BS-RoFormer dim 512, depth 12, 8x64 heads, 1 stem, batch 2 x 485100 stereo "
                  "(948 frames), activation checkpointing per axial block, bf16 autocast, L1, AdamW 5e-4",
+    "mbr_train": "configs[3] Mel-band RoFormer dim 192, depth 8, 8x64 heads, 4 stems, 60 mel bands, batch 4 x "
+                 "352800 stereo (690 frames), bf16 autocast, L1, AdamW 5e-4",
 }
 
 

@@ -251,6 +251,28 @@ int pmsst_attention_gate_backward(const void* grad_out, const void* attn, const 
                                   int64_t batch, int64_t seq, int64_t heads, int64_t dim_head, int64_t dim, int dtype,
                                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------ Mel-band RoFormer band rows
+ * No reference counterpart (the band gather and the overlap-averaged mask scatter live in
+ * pymss-core, absent from the reference; the Mel-band model calls them around the band split and
+ * the mask estimators).  The spectrum is packed [batch, num_rows, frames, 2] (frequency x channel
+ * rows, re/im) and a band layout selects num_sel rows: rows[j] (device int64), bands in order.
+ * row_start (device int64 [num_rows + 1]) and sources (device int64 [num_sel]) list, for every
+ * row, the selections j that point at it (a CSR of rows[], ascending j); the caller builds and
+ * validates both (0 <= rows[j] < num_rows).
+ */
+
+/* out[b, t, j, :] = in[b, rows[j], t, :] / divisor[j] (divisor: device fp32 [num_sel], NULL = no
+ * division); out is [batch, frames, num_sel, 2].  in_dtype / out_dtype may differ. */
+int pmsst_band_rows_gather(const void* in, int in_dtype, const int64_t* rows, const float* divisor, void* out,
+                           int out_dtype, int64_t batch, int64_t num_rows, int64_t frames, int64_t num_sel,
+                           void* stream);
+/* out[b, r, t, :] = sum_{j in sources[row_start[r] .. row_start[r+1])} in[b, t, j, :], divided by the
+ * count when mean is nonzero (rows no band selects get 0); in is [batch, frames, num_sel, 2], out
+ * [batch, num_rows, frames, 2]. */
+int pmsst_band_rows_scatter(const void* in, int in_dtype, const int64_t* row_start, const int64_t* sources, int mean,
+                            void* out, int out_dtype, int64_t batch, int64_t num_rows, int64_t frames,
+                            int64_t num_sel, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,6 +47,8 @@ __all__ = [
     "mask_mlp_backward",
     "attention_gate_forward",
     "attention_gate_backward",
+    "band_rows_gather",
+    "band_rows_scatter",
     "sigmoid",
 ]
 
@@ -478,3 +480,29 @@ def attention_gate_backward(grad_out, attn, x, weight, gate, dt: str, acc=np.flo
     grad_w = gpre.T @ _f(x, acc)
     grad_b = gpre.sum(axis=0)
     return round_to(grad_attn, dt), round_to(grad_x, dt), round_to(grad_w, dt), round_to(grad_b, dt)
+
+
+def band_rows_gather(x, rows, divisor=None):
+    """Mel band gather (no reference counterpart; pymss-core's Mel-band model indexes the spectrum
+    rows of each band in band order): ``x[B, R, T, 2]`` -> ``out[B, T, J, 2]``,
+    ``out[b, t, j] = x[b, rows[j], t] / divisor[j]``.  float64 results."""
+    x = np.asarray(x, dtype=np.float64)
+    out = x[:, np.asarray(rows), :, :].transpose(0, 2, 1, 3)
+    if divisor is not None:
+        out = out / np.asarray(divisor, dtype=np.float64)[None, None, :, None]
+    return out
+
+
+def band_rows_scatter(x, rows, num_rows: int, mean: bool = True):
+    """Overlap-averaged mask scatter (no reference counterpart; the Mel-band model's scatter_add
+    + division by the number of bands per bin): ``x[B, T, J, 2]`` -> ``out[B, R, T, 2]`` with each
+    row the sum (``mean``: the average) of the selections pointing at it; unselected rows are 0."""
+    x = np.asarray(x, dtype=np.float64)
+    rows = np.asarray(rows)
+    b, t, j, _ = x.shape
+    out = np.zeros((b, num_rows, t, 2))
+    np.add.at(out, (slice(None), rows), x.transpose(0, 2, 1, 3))
+    if mean:
+        counts = np.bincount(rows, minlength=num_rows).astype(np.float64)
+        out = out / np.maximum(counts, 1.0)[None, :, None, None]
+    return out

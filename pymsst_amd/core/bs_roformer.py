@@ -63,6 +63,7 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
         rotary_theta: float = 10000.0,
         checkpoint_blocks: bool = False,
         loss: str = "multi_stft",
+        _check_cover: bool = True,
     ):
         super().__init__()
         if loss not in ("multi_stft", "l1", "spec_l1"):
@@ -92,7 +93,7 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
                                 normalized=stft_normalized)
         self.stft_win_length = stft_win_length
         n_freqs = stft_n_fft // 2 + 1
-        if sum(freqs_per_bands) != n_freqs:
+        if _check_cover and sum(freqs_per_bands) != n_freqs:
             raise ValueError(f"freqs_per_bands must sum to {n_freqs}, got {sum(freqs_per_bands)}")
         self.freqs_per_bands = tuple(int(f) for f in freqs_per_bands)
         dims_in = tuple(2 * f * self.audio_channels for f in self.freqs_per_bands)
@@ -115,6 +116,17 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
         f, t = spec.shape[-2:]
         return spec.reshape(b, c, f, t).transpose(1, 2).reshape(b, f * c, t), window
 
+    def _band_features(self, spec: torch.Tensor) -> torch.Tensor:
+        """Complex ``spec[B, F*C, T]`` -> band-split input ``[B, T, F*C*2]`` (bands are contiguous runs of
+        frequencies, so the features are the spectrum itself)."""
+        b, _, t = spec.shape
+        return torch.view_as_real(spec).permute(0, 2, 1, 3).reshape(b, t, -1)
+
+    def _spectral_mask(self, mask: torch.Tensor) -> torch.Tensor:
+        """Mask-estimator output ``[B, stems, T, F*C*2]`` -> complex mask ``[B, stems, F*C, T]``."""
+        b, stems, t = mask.shape[:3]
+        return torch.view_as_complex(mask.float().reshape(b, stems, t, -1, 2).contiguous()).transpose(-1, -2)
+
     def _axial(self, x: torch.Tensor, time_tf: Transformer, freq_tf: Transformer) -> torch.Tensor:
         b, t, nb, d = x.shape
         x = time_tf(x.transpose(1, 2).reshape(b * nb, t, d)).reshape(b, nb, t, d).transpose(1, 2)
@@ -129,7 +141,7 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
         b, c, length = raw_audio.shape
         spec, window = self._stft(raw_audio)  # [B, F*C, T] complex
         t = spec.shape[-1]
-        x = torch.view_as_real(spec).permute(0, 2, 1, 3).reshape(b, t, -1)  # [B, T, F*C*2]
+        x = self._band_features(spec)  # [B, T, features]
         x = self.band_split(x)  # [B, T, NB, dim]
         for time_tf, freq_tf in self.layers:
             if self.checkpoint_blocks and self.training:
@@ -137,9 +149,9 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
             else:
                 x = self._axial(x, time_tf, freq_tf)
         x = self.final_norm(x)
-        mask = self._estimate_masks(x)  # [B, stems, T, F*C*2]
+        mask = self._estimate_masks(x)  # [B, stems, T, features]
         stems = mask.shape[1]
-        mask = torch.view_as_complex(mask.float().reshape(b, stems, t, -1, 2).contiguous()).transpose(-1, -2)
+        mask = self._spectral_mask(mask)  # [B, stems, F*C, T] complex
         est = spec.unsqueeze(1) * mask  # [B, stems, F*C, T]
         if target is not None and self.loss_type == "spec_l1":
             return self._spec_loss(est, target, c)

@@ -17,11 +17,23 @@ kernels or raises.
 from __future__ import annotations
 
 import ctypes
+from typing import NamedTuple
 
 import torch
 
 from . import _lib
 from ._lib import PmsstError, check, dtype_code
+
+
+class BandRowsPlan(NamedTuple):
+    """Device tables of a mel band layout (see ``HipFusedExtension.band_rows_plan``)."""
+
+    rows: torch.Tensor
+    row_start: torch.Tensor
+    sources: torch.Tensor
+    divisor: torch.Tensor
+    num_rows: int
+    num_sel: int
 
 
 def _req(cond: bool, msg: str) -> None:
@@ -482,6 +494,58 @@ class HipFusedExtension:
         self._gate_common_checks(attn, x, weight)
         _req(out_layout in ("bhnd", "bnhd"), f"unsupported out_layout {out_layout!r}")
         return list(self._gate_bwd(grad_out, attn, x, weight, gate, out_layout))
+
+    # ------------------------------------------------------------------ mel band rows
+
+    @staticmethod
+    def band_rows_plan(rows, num_rows: int, device):
+        """Build-addition helper: device tables of a band layout (``rows[j]`` = spectrum row of
+        selection ``j``, bands in order) for :meth:`band_rows_gather` / :meth:`band_rows_scatter`:
+        the rows, their CSR by row (``row_start[num_rows + 1]``, ``sources`` = selections of each
+        row in ascending order) and each selection's row count (fp32 divisor).  Validated here."""
+        r = torch.as_tensor(rows, dtype=torch.int64).detach().cpu().reshape(-1)
+        _req(num_rows > 0, "num_rows must be positive")
+        _req(r.numel() == 0 or (int(r.min()) >= 0 and int(r.max()) < num_rows), "rows must lie in [0, num_rows)")
+        counts = torch.bincount(r, minlength=num_rows)
+        row_start = torch.zeros(num_rows + 1, dtype=torch.int64)
+        row_start[1:] = torch.cumsum(counts, 0)
+        sources = torch.argsort(r, stable=True)
+        divisor = counts[r].to(torch.float32)
+        dev = torch.device(device)
+        return BandRowsPlan(r.to(dev), row_start.to(dev), sources.to(dev), divisor.to(dev), int(num_rows),
+                            int(r.numel()))
+
+    def band_rows_gather(self, x, plan, divide=False, out_dtype=None):
+        """``x[B, R, T, 2]`` -> ``[B, T, J, 2]`` with ``out[b, t, j] = x[b, rows[j], t]`` (divided by the
+        row's band count when ``divide``)."""
+        _req(x.is_cuda and x.dim() == 4 and x.size(3) == 2 and x.size(1) == plan.num_rows,
+             "x must be a CUDA tensor of shape [B, num_rows, T, 2]")
+        x = x.contiguous()
+        b, _, t, _ = x.shape
+        out = torch.empty((b, t, plan.num_sel, 2), dtype=out_dtype or x.dtype, device=x.device)
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_band_rows_gather(
+                _ptr(x), dtype_code(x.dtype), _ptr(plan.rows), _ptr(plan.divisor) if divide else None, _ptr(out),
+                dtype_code(out.dtype), b, plan.num_rows, t, plan.num_sel, _stream(x.device),
+            )
+        check(rc, "pmsst_band_rows_gather")
+        return out
+
+    def band_rows_scatter(self, x, plan, mean=True, out_dtype=torch.float32):
+        """``x[B, T, J, 2]`` -> ``[B, R, T, 2]``: per row the sum of its selections (the mean when
+        ``mean``); rows no band selects are zero."""
+        _req(x.is_cuda and x.dim() == 4 and x.size(3) == 2 and x.size(2) == plan.num_sel,
+             "x must be a CUDA tensor of shape [B, T, num_sel, 2]")
+        x = x.contiguous()
+        b, t = x.shape[:2]
+        out = torch.empty((b, plan.num_rows, t, 2), dtype=out_dtype, device=x.device)
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_band_rows_scatter(
+                _ptr(x), dtype_code(x.dtype), _ptr(plan.row_start), _ptr(plan.sources), int(bool(mean)), _ptr(out),
+                dtype_code(out.dtype), b, plan.num_rows, t, plan.num_sel, _stream(x.device),
+            )
+        check(rc, "pmsst_band_rows_scatter")
+        return out
 
     # ------------------------------------------------------------------ band split
 

@@ -57,6 +57,9 @@ EXPERIMENTAL_TRAIN_PARAM_PACK_AUTOGRAD_ENV = "PYMSST_EXPERIMENTAL_TRAIN_PARAM_PA
 # depth-2 mask MLP on the HIP kernels (hidden forward with a tanh epilogue; tanh' fused into the
 # final layer's dx epilogue; grouped-linear backward on the GPU).
 EXPERIMENTAL_FUSED_MASK_MLP_ENV = "PYMSST_EXPERIMENTAL_FUSED_MASK_MLP"
+# This build's addition: the Mel-band RoFormer's band gather and overlap-averaged mask scatter on
+# the HIP band-row kernels.
+EXPERIMENTAL_FUSED_MEL_BANDS_ENV = "PYMSST_EXPERIMENTAL_FUSED_MEL_BANDS"
 
 _TRUE = {"1", "true", "yes", "on"}
 _FLOAT_TYPES = (torch.float16, torch.bfloat16, torch.float32)
@@ -80,6 +83,7 @@ RUNTIME_PRESETS["hip_full"] = {
     EXPERIMENTAL_ROTARY_ENV: "1",
     EXPERIMENTAL_FUSED_MASK_MLP_ENV: "1",
     EXPERIMENTAL_ATTENTION_GATES_ENV: "1",
+    EXPERIMENTAL_FUSED_MEL_BANDS_ENV: "1",
 }
 
 
@@ -118,6 +122,7 @@ class FusedTrainingStatus:
     patched_mask_estimator_final: bool = False
     mask_estimator_final_mode: str | None = None
     patched_mask_mlp: bool = False  # this build's addition (hidden Linear + tanh fused as well)
+    patched_mel_bands: bool = False  # this build's addition (Mel-band gather / mask scatter)
 
 
 # ---------------------------------------------------------------------- switchboard
@@ -250,9 +255,10 @@ def apply_roformer_fused_training_backend(
     final_mode = _mask_estimator_final_mode(ext)
     final = _patch_core_mask_estimator_final(ext, final_mode) if final_mode else False
     mask_mlp = final and _mask_mlp_enabled(ext)
+    mel_bands = _patch_mel_bands(ext) if _flag(EXPERIMENTAL_FUSED_MEL_BANDS_ENV) else False
 
     if not any((n_band_splits, single_stem, rotary, rms, gates, grouped_linear, layout, pack_autograd, final_autograd,
-                final)):
+                final, mel_bands)):
         reason = "no compatible BandSplit modules were found"
         warnings.warn(reason, RuntimeWarning, stacklevel=2)
         return FusedTrainingStatus(requested=normalized, active="off", reason=reason)
@@ -280,6 +286,7 @@ def apply_roformer_fused_training_backend(
         patched_mask_estimator_final=final,
         mask_estimator_final_mode=final_mode if final else None,
         patched_mask_mlp=mask_mlp,
+        patched_mel_bands=mel_bands,
     )
 
 
@@ -437,6 +444,49 @@ def _patch_core_attention_gates(ext: Any, mode: str) -> bool:
     attention_forward_cuda_ext._pymsst_fused_attention_gate_mode = mode
     attention_forward_cuda_ext._pymsst_original_forward = original
     transformer.Attention.forward = attention_forward_cuda_ext
+    return True
+
+
+def _mel_plan(module, ext: Any, device: torch.device):
+    plan = getattr(module, "_pymsst_mel_plan", None)
+    if plan is None or plan.rows.device != device:
+        plan = ext.band_rows_plan(module.band_rows, module.num_rows, device)
+        module._pymsst_mel_plan = plan
+    return plan
+
+
+def _patch_mel_bands(ext: Any) -> bool:
+    """Class-level ``MelBandRoformer._band_features`` / ``_spectral_mask`` replacement (no reference
+    counterpart: pymss-core's Mel-band model does the gather with indexing and the average with
+    scatter_add + division)."""
+    if any(not hasattr(ext, n) for n in ("band_rows_plan", "band_rows_gather", "band_rows_scatter")):
+        return False
+    from .core import mel_band_roformer as mbr
+
+    cls = mbr.MelBandRoformer
+    if getattr(cls._band_features, "_pymsst_fused_mel_bands", False):
+        return True
+    orig_features, orig_mask = cls._band_features, cls._spectral_mask
+
+    def band_features_cuda_ext(self, spec):
+        if not spec.is_cuda or spec.dtype != torch.complex64:
+            return orig_features(self, spec)
+        plan = _mel_plan(self, ext, spec.device)
+        b, _, t = spec.shape
+        return _FusedBandGather.apply(torch.view_as_real(spec), plan, ext).reshape(b, t, -1)
+
+    def spectral_mask_cuda_ext(self, mask):
+        if not mask.is_cuda or mask.dtype not in _FLOAT_TYPES:
+            return orig_mask(self, mask)
+        plan = _mel_plan(self, ext, mask.device)
+        return torch.view_as_complex(_FusedMaskScatterMean.apply(mask, plan, ext))
+
+    band_features_cuda_ext._pymsst_fused_mel_bands = True
+    band_features_cuda_ext._pymsst_original_band_features = orig_features
+    spectral_mask_cuda_ext._pymsst_fused_mel_bands = True
+    spectral_mask_cuda_ext._pymsst_original_spectral_mask = orig_mask
+    cls._band_features = band_features_cuda_ext
+    cls._spectral_mask = spectral_mask_cuda_ext
     return True
 
 
@@ -1090,6 +1140,41 @@ class _FusedQKVRotary(torch.autograd.Function):
         return ctx.extension.rotary_qkv_backward(*grads, cos, sin), None, None, None, None
 
 
+class _FusedBandGather(torch.autograd.Function):
+    """Mel band gather: ``spec[B, R, T, 2]`` -> band-split input ``[B, T, J, 2]`` (one HIP pass; the
+    backward sums the selections of each row back onto it)."""
+
+    @staticmethod
+    def forward(ctx, spec, plan, extension):
+        ctx.plan, ctx.extension, ctx.dtype = plan, extension, spec.dtype
+        return extension.band_rows_gather(spec, plan)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        if not ctx.needs_input_grad[0]:
+            return None, None, None
+        return ctx.extension.band_rows_scatter(grad_out, ctx.plan, mean=False, out_dtype=ctx.dtype), None, None
+
+
+class _FusedMaskScatterMean(torch.autograd.Function):
+    """Mel mask average: ``mask[B, stems, T, J*2]`` -> fp32 ``[B, stems, R, T, 2]``, each spectrum row
+    the mean of the band values that cover it (one HIP pass each way)."""
+
+    @staticmethod
+    def forward(ctx, mask, plan, extension):
+        b, stems, t = mask.shape[:3]
+        ctx.plan, ctx.extension, ctx.shape, ctx.dtype = plan, extension, mask.shape, mask.dtype
+        out = extension.band_rows_scatter(mask.reshape(b * stems, t, plan.num_sel, 2), plan, mean=True)
+        return out.view(b, stems, plan.num_rows, t, 2)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        b, stems, t = ctx.shape[:3]
+        g = grad_out.reshape(b * stems, ctx.plan.num_rows, t, 2)
+        grad = ctx.extension.band_rows_gather(g, ctx.plan, divide=True, out_dtype=ctx.dtype)
+        return grad.reshape(ctx.shape), None, None
+
+
 class _FusedAttentionGate(torch.autograd.Function):
     """fr.py:1228-1262.  With an extension that reads ``[B,N,H,Dh]`` views in place
     (``attention_gate_forward_bnhd``), the transposed SDPA output is not copied and the attn
@@ -1240,6 +1325,8 @@ _CORE_PATCH_POINTS = (
     ("bands", "MaskEstimator", "_get_layer_group_params", "_pymsst_original_get_layer_group_params"),
     ("bands", "BandSplit", "_get_group_params", "_pymsst_original_get_group_params"),
     ("common", "RoformerRuntimeMixin", "_estimate_masks", "_pymsst_original_estimate_masks"),
+    ("mel_band_roformer", "MelBandRoformer", "_band_features", "_pymsst_original_band_features"),
+    ("mel_band_roformer", "MelBandRoformer", "_spectral_mask", "_pymsst_original_spectral_mask"),
 )
 
 
@@ -1248,8 +1335,10 @@ def restore_stock_implementations(model: torch.nn.Module | None = None) -> None:
     the reference has no inverse).  Module- and class-level patches are unwound to the
     stock functions; with ``model`` its BandSplit instances get their stock
     ``_forward_grouped`` back.  Used to run stock and fused models in one process."""
+    from .core import mel_band_roformer
+
     bands, transformer, common = _core()
-    modules = {"bands": bands, "transformer": transformer, "common": common}
+    modules = {"bands": bands, "transformer": transformer, "common": common, "mel_band_roformer": mel_band_roformer}
     for mod_name, owner_name, name, marker in _CORE_PATCH_POINTS:
         owner = modules[mod_name] if owner_name is None else getattr(modules[mod_name], owner_name)
         current = getattr(owner, name)

@@ -10,6 +10,10 @@ batch shape, sample length, stems, loss) for the restated stock models in
   stereo 131584 samples (258 frames); multi-resolution STFT L1; AdamW 5e-4.
 * ``bsr_large`` - BS-RoFormer dim 512, depth 12, 1 stem; batch 2 of stereo 485100
   samples (948 frames); L1; activation checkpointing per axial block.
+* ``mbr_train`` - Mel-band RoFormer dim 192, depth 8, 8 heads x 64, 4 stems, 60 mel bands;
+  batch 4 of stereo 352800 samples (690 frames); L1 (configs[3]; transformer depths 1 and
+  mask-estimator depth 2 chosen as for the BS-RoFormer configs).
+* ``mbr_tiny`` - Mel-band RoFormer dim 32, depth 1, 12 bands, 2 stems (tests).
 
 Audio: every source is i.i.d. N(0, 0.1^2) clipped to [-1, 1], drawn from its own
 ``torch.Generator``; the mixture is the sum of the sources and the target their
@@ -23,6 +27,7 @@ from dataclasses import dataclass, field
 import torch
 
 from .core.bs_roformer import BSRoformer
+from .core.mel_band_roformer import MelBandRoformer
 
 
 @dataclass(frozen=True)
@@ -35,10 +40,11 @@ class TrainWorkload:
     lr: float = 5e-4
     amp_dtype: torch.dtype | None = torch.bfloat16
     extra: dict = field(default_factory=dict)
+    family: str = "bsr"  # "bsr" (BS-RoFormer) or "mbr" (Mel-band RoFormer)
 
     def build_model(self, device=None, seed: int = 4) -> BSRoformer:
         torch.manual_seed(seed)
-        model = BSRoformer(**self.model)
+        model = (MelBandRoformer if self.family == "mbr" else BSRoformer)(**self.model)
         return model.to(device) if device is not None else model
 
 
@@ -61,6 +67,18 @@ WORKLOADS = {
                    heads=8, dim_head=64, mask_estimator_depth=2, mlp_expansion_factor=4, loss="l1",
                    checkpoint_blocks=True),
         batch=2, length=485100, stems=1,
+    ),
+    "mbr_train": TrainWorkload(
+        name="mbr_train",
+        model=dict(dim=192, depth=8, stereo=True, num_stems=4, time_transformer_depth=1, freq_transformer_depth=1,
+                   heads=8, dim_head=64, num_bands=60, mask_estimator_depth=2, mlp_expansion_factor=4, loss="l1"),
+        batch=4, length=352800, stems=4, family="mbr",
+    ),
+    "mbr_tiny": TrainWorkload(
+        name="mbr_tiny",
+        model=dict(dim=32, depth=1, stereo=True, num_stems=2, time_transformer_depth=1, freq_transformer_depth=1,
+                   heads=2, dim_head=32, num_bands=12, mask_estimator_depth=2, mlp_expansion_factor=2, loss="l1"),
+        batch=2, length=16384, stems=2, amp_dtype=None, family="mbr",
     ),
 }
 

@@ -386,3 +386,29 @@ def test_attention_gate_rounding_points():
     assert np.array_equal(gb, oracle.round_to(gpre.sum(0), "bf16"))
     unrounded = ((g.reshape(m, h, dh) * attn).sum(2) * gate * (1 - gate)).sum(0)
     assert not np.array_equal(oracle.round_to(unrounded, "bf16"), gb)
+
+
+def test_band_rows_gather_scatter_vs_torch_index_ops():
+    """The Mel-band gather / averaged scatter against torch index_select / scatter_add_ (the library
+    routines the stock model uses), an all-ones mask averaging to ones on covered rows, and the
+    scatter being the gather's adjoint (<gather(x), y> = <x, scatter(y)>)."""
+    r = _rng(17)
+    b, R, t = 2, 11, 5
+    rows = np.array([0, 1, 2, 2, 3, 4, 5, 5, 6, 8, 9, 10, 10])  # rows 2, 5, 10 twice; row 7 never
+    x = r.standard_normal((b, R, t, 2))
+    got = oracle.band_rows_gather(x, rows)
+    ref = torch.from_numpy(x).index_select(1, torch.from_numpy(rows)).permute(0, 2, 1, 3).numpy()
+    _close(got, torch.from_numpy(ref), what="gather")
+    y = r.standard_normal((b, t, rows.size, 2))
+    vals = torch.from_numpy(y).permute(0, 2, 1, 3)
+    idx = torch.from_numpy(rows).view(1, -1, 1, 1).expand(b, -1, t, 2)
+    summed = torch.zeros(b, R, t, 2, dtype=torch.float64).scatter_add_(1, idx, vals)
+    counts = torch.bincount(torch.from_numpy(rows), minlength=R).clamp(min=1).double()
+    _close(oracle.band_rows_scatter(y, rows, R, mean=False), summed, what="scatter sum")
+    _close(oracle.band_rows_scatter(y, rows, R, mean=True), summed / counts.view(1, -1, 1, 1), what="scatter mean")
+    ones = oracle.band_rows_scatter(np.ones((b, t, rows.size, 2)), rows, R, mean=True)
+    covered = np.bincount(rows, minlength=R) > 0
+    assert np.allclose(ones[:, covered], 1.0) and np.allclose(ones[:, ~covered], 0.0)
+    lhs = (oracle.band_rows_gather(x, rows) * y).sum()
+    rhs = (x * oracle.band_rows_scatter(y, rows, R, mean=False)).sum()
+    assert abs(lhs - rhs) <= 1e-9 * max(1.0, abs(lhs))
