@@ -42,15 +42,15 @@ METRIC = "fused-layer fwd+bwd HBM GB/s (% peak) + BSR train samples/s, 1 MI355X"
 SINGLE_KERNEL_OPS = {
     "band_split_fwd": ("bs_fwd_kernel", 1),
     "qk_norm_rotary_fwd": ("norm_rot_fwd_kernel", 2),
-    "mask_final_fwd": ("me_fwd_kernel", 1),
+    "mask_final_fwd": ("me_fwd_dma_kernel", 1),
 }
 # measured HBM bytes per launch, by kernel: rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (KiB per
 # dispatch x 1024).  The factors are what the same counters read for a 1 GiB bf16 copy (torch.mul) in
 # the same runs: FETCH_SIZE 524310 KiB for 1048576 KiB read, WRITE_SIZE 1048576 KiB for 1048576 written.
 TRAFFIC_PER_LAUNCH: dict = {
-    "me_fwd_kernel": (84255 * 2 + 34423) * 1024,
-    "norm_rot_fwd_kernel": (32271 * 2 + 65984) * 1024,
-    "bs_fwd_kernel": (14201 * 2 + 32301) * 1024,
+    "me_fwd_dma_kernel": (57461 * 2 + 31359) * 1024,
+    "norm_rot_fwd_kernel": (32278 * 2 + 65984) * 1024,
+    "bs_fwd_kernel": (14210 * 2 + 32755) * 1024,
 }
 BSR_WIDTHS = tuple([8] * 24 + [16] * 12 + [48] * 8 + [96] * 8 + [192] * 8 + [512, 516])
 

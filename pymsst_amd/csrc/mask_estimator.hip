@@ -10,9 +10,11 @@
 // F = sum_b I_b.
 //
 // Forward block (128 rows of M, band b, 64 GLU outputs l): A = the 64 left rows
-// and the 64 gate rows of W_b for those outputs, B = x rows; waves split M so
-// each lane holds a left accumulator and the gate accumulator of the same
-// output, and the GLU is applied in registers.
+// and the 64 gate rows of W_b for those outputs, B = x rows; each lane holds a
+// left accumulator and the gate accumulator of the same output, and the GLU is
+// applied in registers.  16-bit inputs with 4-aligned widths run me_fwd_dma_kernel
+// (global -> LDS DMA ring, XCD-grouped block schedule); other cases run
+// me_fwd_kernel (register-staged main loop of gemm.h).
 //
 // Backward:
 //   1. me_dpre_kernel writes dpre = (g * s, g * L * s * (1 - s)), s = sigmoid(G),
@@ -139,6 +141,220 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(PM
           po[r] = from_f32<T>(vo[r]);
         }
       }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ forward, DMA pipeline
+//
+// The register-staged main loop keeps one 16 KB chunk per block in flight, and at three
+// blocks per CU the forward is bound by load latency, not by HBM, LDS or MFMA throughput.
+// This kernel moves the chunks with global -> LDS DMA (global_load_lds_dwordx4: 16 bytes per
+// lane into LDS at M0 + 16 * lane, no registers involved), so S - 1 chunks of both operands are
+// in flight per block (a ring of S LDS stages of 16 KB), with one barrier per chunk.
+//
+// Tile: 128 rows of M x 64 GLU outputs of one band.  A stage holds 128 weight rows then 128 x
+// rows, 64 bytes (one 32-wide K chunk) per row.  Weight rows are ordered in 16-row blocks left,
+// gate, left, gate, ...: tile row R is output l0 + 16 (R / 32) + R % 16, gate when (R / 16) is
+// odd.  The four 16-byte units of a row are stored XOR-swizzled (mef_swz) so MFMA fragment
+// reads are free of bank conflicts.
+//
+// Waves are 2 x 2: wave (wr, wc) multiplies weight rows 64 wr .. + 64 (4 fragments = 32
+// outputs, left and gate of each) by x rows 64 wc .. + 64 (4 fragments), so each lane ends
+// with 4 consecutive outputs and their gates (in-register GLU).  A wave whose 32 outputs lie
+// past the band skips its reads and MFMAs.  DMA: wave w moves tile rows 64 w .. + 64 (waves
+// 0-1 weight rows, 2-3 x rows), one dwordx4 per lane per 16 rows.
+//
+// The LDS reads are inline ds_read_b128 followed by an explicit lgkmcnt wait that the MFMA
+// operands depend on; the DMA completion wait (vmcnt) and the barrier are explicit too.  This
+// keeps the compiler from waiting for every DMA in flight before each LDS read (it cannot tell
+// the ring's stages apart).  Chunk 0 (the only partial one: K is walked in chunks that end at
+// H) is loaded through registers with the out-of-range units zeroed.
+#ifndef PMSST_MEF_STAGES
+#define PMSST_MEF_STAGES 4
+#endif
+constexpr int kMefStage = 16384;  // bytes of one LDS stage
+
+// Block schedule of the forward: the blocks in canonical order (band, row tile, 64-output
+// chunk) are cut into kXcds contiguous ranges of whole (band, row tile) units, balanced by
+// block count, and range x runs on XCD x (hardware places block i on XCD i % 8).  The chunks
+// of one row tile -- which read the same x rows -- and the row tiles of one band -- which read
+// the same weights -- then share that XCD's L2, and neighbouring narrow bands, which write
+// neighbouring columns of pre and out, write them through the same L2.
+constexpr int kSchedMaxBands = 256;
+struct MefSched {
+  uint32_t gs[kXcds + 1];                // canonical block range [gs[x], gs[x+1]) of XCD x
+  uint32_t cumb[kSchedMaxBands + 1];     // canonical index of each band's first block
+  uint32_t bstart[kXcds];                // band of XCD x's first block
+  uint32_t m_tiles;                      // row tiles; 0: no schedule, use the XcdGrid map
+};
+
+// Unit swizzle of a stage row (by its index r mod 16).  An MFMA fragment read is 16 rows x one
+// 16-byte unit; with the swizzle the rows of every 8-lane half (128 bytes, 32 banks) and of the
+// whole 16 lanes (256 bytes, 64 banks) land on distinct bank groups: rows of equal parity in
+// each half, and rows equal mod 4, get distinct units.
+__device__ __forceinline__ int mef_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+template <typename T>
+__device__ __forceinline__ f32x4_t mfma_raw(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+  if constexpr (std::is_same<T, bf16>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kGemmThreads) void me_fwd_dma_kernel(const T* __restrict__ x,
+                                                                  const T* __restrict__ weight,
+                                                                  const T* __restrict__ bias, T* __restrict__ pre,
+                                                                  T* __restrict__ out, int max_lchunks, XcdGrid xg,
+                                                                  MaskArgs a, MefSched sc) {
+  constexpr int S = PMSST_MEF_STAGES;
+  static_assert(S >= 2 && S <= 8, "stages");
+  __shared__ __attribute__((aligned(1024))) char lds[S * kMefStage];
+  int band, l0;
+  uint32_t mt;
+  if (sc.m_tiles != 0) {
+    const uint32_t xcd = blockIdx.x % kXcds;
+    const uint32_t gb = sc.gs[xcd] + blockIdx.x / kXcds;
+    if (gb >= sc.gs[xcd + 1]) return;
+    uint32_t b = sc.bstart[xcd];
+    while (gb >= sc.cumb[b + 1]) ++b;
+    const uint32_t nch = (sc.cumb[b + 1] - sc.cumb[b]) / sc.m_tiles;
+    const uint32_t within = gb - sc.cumb[b];
+    band = static_cast<int>(b);
+    mt = within / nch;
+    l0 = static_cast<int>(within % nch) * 64;
+  } else {
+    uint32_t grp;  // group = (band, 64-output chunk), member = row tile: weight chunk shared in L2
+    if (!xcd_block(xg, grp, mt)) return;
+    band = static_cast<int>(grp) / max_lchunks;
+    l0 = (static_cast<int>(grp) % max_lchunks) * 64;
+  }
+  const int off = static_cast<int>(a.offsets[band]);
+  const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  if (l0 >= I) return;
+  const int64_t m0 = static_cast<int64_t>(mt) * kFwdBM;
+  const int rows_valid = static_cast<int>(a.M - m0 < kFwdBM ? a.M - m0 : kFwdBM);
+  const int H = a.H;
+  const int lane = threadIdx.x & 63, g = lane >> 4, rr = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int wr = wave >> 1, wc = wave & 1;
+  const bool active = l0 + 32 * wr < I;  // wave-uniform
+
+  // DMA pieces of this lane: instruction t moves tile row R = 64 wave + 16 t + lane / 4
+  // (R % 16 = lane / 4), physical unit lane % 4, i.e. logical K unit u = (lane % 4) ^ swz(lane / 4)
+  const uint32_t u = static_cast<uint32_t>((lane & 3) ^ mef_swz(lane >> 2));
+  uint32_t soff[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int R = 64 * wave + 16 * t + (lane >> 2);
+    if (wave < 2) {
+      const int l = l0 + 16 * (R >> 5) + (R & 15);
+      const int lc = l < I ? l : I - 1;
+      soff[t] = static_cast<uint32_t>(((R >> 4) & 1) ? I + lc : lc) * static_cast<uint32_t>(H) * 2u + 16u * u;
+    } else {
+      const int m = R - 128 < rows_valid ? R - 128 : rows_valid - 1;
+      soff[t] = static_cast<uint32_t>(m) * static_cast<uint32_t>(a.NB) * static_cast<uint32_t>(H) * 2u + 16u * u;
+    }
+  }
+  const char* gbase = wave < 2 ? reinterpret_cast<const char*>(weight + static_cast<int64_t>(2) * off * H)
+                               : reinterpret_cast<const char*>(x + (m0 * a.NB + band) * static_cast<int64_t>(H));
+  const int nk = (H + kChunkK - 1) / kChunkK;  // >= 2 (host check)
+  const int kbeg = H - nk * kChunkK;           // chunk c covers k in [kbeg + 32 c, +32)
+  char* my_lds = lds + (4 * wave) * 1024;      // this wave's 4 KB of a stage
+
+  auto dma = [&](int c, int stage) {  // chunk c >= 1 into `stage`
+    const char* src = gbase + 2 * (kbeg + kChunkK * c);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      __builtin_amdgcn_global_load_lds(src + soff[t], my_lds + stage * kMefStage + t * 1024, 16, 0, 0);
+  };
+
+  // chunk 0 through registers: units with k < 0 are zero (they load k = 0 of the row)
+  {
+    const bool ok = kbeg + 8 * static_cast<int>(u) >= 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t o = ok ? soff[t] + static_cast<uint32_t>(2 * kbeg) : soff[t] - 16u * u;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(gbase + o);
+      *reinterpret_cast<u32x4_t*>(my_lds + t * 1024 + lane * 16) = ok ? v : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int c = 1; c < S - 1; ++c) dma(c < nk ? c : nk - 1, c);
+
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // fragment read addresses inside a stage: row R, logical unit g -> R * 64 + 16 (g ^ swz(R % 16))
+  const uint32_t sw = 16u * static_cast<uint32_t>(g ^ mef_swz(rr));
+  const uint32_t abase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)) +
+                         static_cast<uint32_t>((64 * wr + rr) * 64) + sw;
+  const uint32_t bbase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)) + 8192u +
+                         static_cast<uint32_t>((64 * wc + rr) * 64) + sw;
+
+  for (int c = 0; c < nk; ++c) {
+    // chunk c landed: the DMAs issued after it are chunks c + 1 .. c + S - 2
+    if (c > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (S - 2)) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // refill the stage chunk c - 1 used (every wave is past its reads); clamped at the end
+    dma(c + S - 1 < nk ? c + S - 1 : nk - 1, (c + S - 1) % S);
+    if (active) {
+      const uint32_t st = static_cast<uint32_t>((c % S) * kMefStage);
+      u32x4_t af[4], bf[4];
+      const uint32_t pa = abase + st, pb = bbase + st;
+      asm volatile("ds_read_b128 %0, %1 offset:0" : "=v"(af[0]) : "v"(pa));
+      asm volatile("ds_read_b128 %0, %1 offset:1024" : "=v"(af[1]) : "v"(pa));
+      asm volatile("ds_read_b128 %0, %1 offset:2048" : "=v"(af[2]) : "v"(pa));
+      asm volatile("ds_read_b128 %0, %1 offset:3072" : "=v"(af[3]) : "v"(pa));
+      asm volatile("ds_read_b128 %0, %1 offset:0" : "=v"(bf[0]) : "v"(pb));
+      asm volatile("ds_read_b128 %0, %1 offset:1024" : "=v"(bf[1]) : "v"(pb));
+      asm volatile("ds_read_b128 %0, %1 offset:2048" : "=v"(bf[2]) : "v"(pb));
+      asm volatile("ds_read_b128 %0, %1 offset:3072" : "=v"(bf[3]) : "v"(pb));
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(af[0]), "+v"(af[1]), "+v"(af[2]), "+v"(af[3]), "+v"(bf[0]), "+v"(bf[1]), "+v"(bf[2]),
+                     "+v"(bf[3]));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_raw<T>(af[i], bf[j], acc[i][j]);
+    }
+  }
+  // no DMA may still be writing this block's LDS when its waves end
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (!active) return;
+
+  // epilogue: fragment pair (2h, 2h + 1) = (left, gate) of outputs l0 + 32 wr + 16 h + 4 g + r
+  const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int l = l0 + 32 * wr + 16 * h + 4 * g;
+    if (l >= I) continue;  // I_b is a multiple of 4 on this path: the 4 outputs are all valid
+    float bl[4], bgt[4];
+    load_pack<T, 4>(bias + 2 * off + l, bl);
+    load_pack<T, 4>(bias + 2 * off + I + l, bgt);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = 64 * wc + 16 * j + rr;
+      if (m >= rows_valid) continue;
+      float vl[4], vg[4], vo[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        vl[r] = acc[2 * h][j][r] + bl[r];
+        vg[r] = acc[2 * h + 1][j][r] + bgt[r];
+        vo[r] = vl[r] * sigmoidf_(vg[r]);
+      }
+      T* pl = pre + (m0 + m) * pitch2 + 2 * off + l;
+      store_pack<T, 4>(pl, vl);
+      store_pack<T, 4>(pl + I, vg);
+      store_pack<T, 4>(out + (m0 + m) * a.F + off + l, vo);
     }
   }
 }
@@ -381,6 +597,70 @@ struct HostMask {
   bool vec4;
 };
 
+#ifndef PMSST_ME_FWD_DMA
+#define PMSST_ME_FWD_DMA 1
+#endif
+#ifndef PMSST_ME_FWD_SCHED
+#define PMSST_ME_FWD_SCHED 1
+#endif
+
+// Contiguous split of the (band, row tile) units (chunks_b blocks each, canonical order) into
+// kXcds ranges with the smallest maximum block count (binary search on the cap, greedy fill).
+// Returns false (no schedule) when the band count exceeds the table.
+bool build_mef_sched(const int64_t* dim_inputs, int NB, int64_t m_tiles, MefSched* sc, uint32_t* per_xcd) {
+  sc->m_tiles = 0;
+  if (!PMSST_ME_FWD_SCHED || NB > kSchedMaxBands || m_tiles <= 0) return false;
+  int64_t total = 0, unit_max = 0;
+  sc->cumb[0] = 0;
+  for (int b = 0; b < NB; ++b) {
+    const int64_t ch = (dim_inputs[b] + 63) / 64;
+    unit_max = ch > unit_max ? ch : unit_max;
+    total += ch * m_tiles;
+    if (total >= (int64_t{1} << 31)) return false;
+    sc->cumb[b + 1] = static_cast<uint32_t>(total);
+  }
+  auto ranges = [&](int64_t cap, bool fill) {
+    int x = 0;
+    int64_t acc = 0, g = 0;
+    if (fill) {
+      sc->gs[0] = 0;
+      sc->bstart[0] = 0;
+    }
+    for (int b = 0; b < NB; ++b) {
+      const int64_t ch = (sc->cumb[b + 1] - sc->cumb[b]) / m_tiles;
+      for (int64_t t = 0; t < m_tiles; ++t, g += ch) {
+        if (acc + ch > cap) {
+          ++x;
+          acc = 0;
+          if (fill && x < static_cast<int>(kXcds)) {
+            sc->gs[x] = static_cast<uint32_t>(g);
+            sc->bstart[x] = static_cast<uint32_t>(b);
+          }
+        }
+        acc += ch;
+      }
+    }
+    if (fill)
+      for (int y = x + 1; y <= static_cast<int>(kXcds); ++y) {
+        sc->gs[y] = static_cast<uint32_t>(total);
+        if (y < static_cast<int>(kXcds)) sc->bstart[y] = static_cast<uint32_t>(NB - 1);
+      }
+    return x + 1;
+  };
+  int64_t lo = unit_max, hi = total > unit_max ? total : unit_max;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) / 2;
+    if (ranges(mid, false) <= static_cast<int>(kXcds)) hi = mid;
+    else lo = mid + 1;
+  }
+  ranges(lo, true);
+  uint32_t mx = 0;
+  for (uint32_t y = 0; y < kXcds; ++y) mx = sc->gs[y + 1] - sc->gs[y] > mx ? sc->gs[y + 1] - sc->gs[y] : mx;
+  sc->m_tiles = static_cast<uint32_t>(m_tiles);
+  *per_xcd = mx;
+  return true;
+}
+
 int check_mask(const char* op, const int64_t* dim_inputs, int64_t band_count, int64_t H, HostMask* hm) {
   PMSST_REQUIRE(dim_inputs != nullptr && band_count > 0 && band_count < (1 << 16), "%s: bad band count", op);
   PMSST_REQUIRE(H > 0 && H < (1 << 20), "%s: bad hidden size %lld", op, (long long)H);
@@ -405,8 +685,9 @@ int check_mask(const char* op, const int64_t* dim_inputs, int64_t band_count, in
 bool al(const void* p, size_t b) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % b == 0; }
 
 template <typename T>
-int launch_me_fwd(const void* x, const void* weight, const void* bias, const int64_t* offsets, const HostMask& hm,
-                  int64_t M, int64_t H, void* pre, void* out, hipStream_t stream) {
+int launch_me_fwd(const void* x, const void* weight, const void* bias, const int64_t* offsets,
+                  const int64_t* dim_inputs, const HostMask& hm, int64_t M, int64_t H, void* pre, void* out,
+                  hipStream_t stream) {
   const char* op = "mask_estimator_final_forward";
   PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
   if (M == 0) return PMSST_OK;
@@ -417,6 +698,22 @@ int launch_me_fwd(const void* x, const void* weight, const void* bias, const int
   const int max_lchunks = (hm.max_width + 63) / 64;
   const XcdGrid xg{static_cast<uint32_t>(hm.NB * max_lchunks), static_cast<uint32_t>((M + kFwdBM - 1) / kFwdBM)};
   const dim3 grid(xg.blocks());
+  // 16-bit, 4-aligned widths and bias, hidden a multiple of 8 (whole 16-byte K units), at least
+  // two K chunks, 16-byte aligned rows: the DMA-pipelined kernel
+  if constexpr (sizeof(T) == 2) {
+    if (PMSST_ME_FWD_DMA && a.vec4 && H % 8 == 0 && H > kChunkK && al(x, 16) && al(weight, 16) &&
+        al(bias, 4 * sizeof(T)) && (2 * static_cast<int64_t>(hm.max_width) + 1) * H * 2 < (int64_t{1} << 31) &&
+        (static_cast<int64_t>(kFwdBM) * hm.NB + 1) * H * 2 < (int64_t{1} << 31)) {
+      MefSched sc;
+      uint32_t per_xcd = 0;
+      const bool sched = build_mef_sched(dim_inputs, hm.NB, (M + kFwdBM - 1) / kFwdBM, &sc, &per_xcd);
+      const dim3 g(sched ? per_xcd * kXcds : grid.x);
+      hipLaunchKernelGGL((me_fwd_dma_kernel<T>), g, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
+                         static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
+                         static_cast<T*>(out), max_lchunks, xg, a, sc);
+      return check_launch("me_fwd_dma_kernel");
+    }
+  }
   if (a.vec4)
     hipLaunchKernelGGL((me_fwd_kernel<T, true>), grid, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
                        static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
@@ -521,7 +818,7 @@ int pmsst_mask_estimator_final_forward(const void* x, const void* weight, const 
   if (rc != PMSST_OK) return rc;
   return with_dtype(dtype, "mask_estimator_final_forward", [&](auto tag) {
     using T = decltype(tag);
-    return launch_me_fwd<T>(x, weight, bias, dim_offsets, hm, rows, hidden, pre, out,
+    return launch_me_fwd<T>(x, weight, bias, dim_offsets, dim_inputs, hm, rows, hidden, pre, out,
                             static_cast<hipStream_t>(stream));
   });
 }

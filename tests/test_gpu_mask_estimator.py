@@ -72,6 +72,16 @@ def test_mel_style_widths(hip_ext):
     _check(hip_ext, widths, 77, 100, torch.bfloat16, 6)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,hidden", [(77, 200), (64, 768), (1, 144), (300, 216)])
+def test_register_direct_forward_classes(hip_ext, dtype, m, hidden):
+    """16-bit forward with every width a multiple of 4 and hidden % 8 == 0 (the register-direct
+    kernel): widths of each output class (<= 8, <= 16, 32-chunks with a partial last chunk),
+    a first K step that is partly below zero (hidden % 32 != 0), and M not a multiple of the tile."""
+    widths = (4, 8, 12, 16, 20, 24, 32, 36, 48, 96, 100, 516, 8, 4)
+    _check(hip_ext, widths, m, hidden, dtype, 17 + m)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("has_bias", [True, False])
 def test_grouped_linear(hip_ext, dtype, has_bias):
