@@ -19,6 +19,10 @@ using f16 = _Float16;
 
 constexpr int kWave = 64;
 
+// 16 raw bytes in one vector register quad (a whole-register load / store that the compiler
+// does not slice).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 // ------------------------------------------------------------------ errors
 
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));

@@ -48,12 +48,17 @@ __global__ __launch_bounds__(kFwdThreads) void rms_fwd_kernel(const TX* __restri
        base += static_cast<int64_t>(gridDim.x) * rows_per_block) {
     const int64_t row = base + wave * rows_per_wave + slot;
     const bool valid = row < rows;
+    // unguarded packs load from a clamped row without a branch (a load inside a branch is
+    // waited for at the join, which would serialize the packs of a lane)
+    const int64_t rl = valid ? row : rows - 1;
     float xv[NV][VEC];
     float ss = 0.f;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int col = (v * tpr + t) * VEC;
-      if (valid && (!GUARD || col < dim)) {
+      if (!GUARD) {
+        load_pack<TX, VEC>(x + rl * dim + col, xv[v]);
+      } else if (valid && col < dim) {
         load_pack<TX, VEC>(x + row * dim + col, xv[v]);
       } else {
 #pragma unroll
@@ -126,14 +131,20 @@ __global__ __launch_bounds__(kRowBwdThreads) void rms_bwd_kernel(const TDY* __re
        base += static_cast<int64_t>(gridDim.x) * rows_per_block) {
     const int64_t row = base + wave * rows_per_wave + slot;
     const bool valid = row < rows;
+    // unguarded packs load from a clamped row without a branch, so all packs of the lane are in
+    // flight together; a row past the end only reduces within its own lanes and stores nothing
+    const int64_t rl = valid ? row : rows - 1;
     float d[NV][VEC], n[NV][VEC];
-    const float inv = valid ? inv_norm[row] : 0.f;
+    const float inv = inv_norm[rl];
     const float nscale = FROM_X ? inv * scale : 1.0f;
     float dot = 0.f;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int col = (v * tpr + t) * VEC;
-      if (valid && (!GUARD || col < dim)) {
+      if (!GUARD) {
+        load_pack<TDY, VEC>(dy + rl * dim + col, d[v]);
+        load_pack<TN, VEC>(nsrc + rl * dim + col, n[v]);
+      } else if (valid && col < dim) {
         load_pack<TDY, VEC>(dy + row * dim + col, d[v]);
         load_pack<TN, VEC>(nsrc + row * dim + col, n[v]);
       } else {

@@ -18,6 +18,10 @@ namespace pmsst {
 namespace {
 
 constexpr int kRotThreads = 256;
+#ifndef PMSST_ROT_UNROLL
+#define PMSST_ROT_UNROLL 2
+#endif
+constexpr int kRotUnroll = PMSST_ROT_UNROLL;  // packs per thread per trip
 constexpr int kNormRotThreads = 256;
 
 struct TableRef {
@@ -41,15 +45,71 @@ __device__ __forceinline__ void load_table(const T* __restrict__ r, int p0, int6
   if constexpr (TS == kTabDense) {
     load_pack<T, NP>(r + p0, o);
   } else if constexpr (TS == kTabRepeated) {
-    float tmp[2 * NP];
-    load_pack<T, 2 * NP>(r + 2 * p0, tmp);
+    if constexpr (sizeof(T) == 2 && NP == 4) {
+      // one 16-byte load; the even elements (low halves of the 4 words) are gathered with byte
+      // permutes, which keeps the compiler from splitting the load into 4 two-byte loads
+      const uint4 w = *reinterpret_cast<const uint4*>(r + 2 * p0);
+      const uint2 ev{__builtin_amdgcn_perm(w.y, w.x, 0x05040100u), __builtin_amdgcn_perm(w.w, w.z, 0x05040100u)};
+      const Pack<T, 4> pk = __builtin_bit_cast(Pack<T, 4>, ev);
 #pragma unroll
-    for (int j = 0; j < NP; ++j) o[j] = tmp[2 * j];
+      for (int j = 0; j < 4; ++j) o[j] = to_f32(pk.v[j]);
+    } else {
+      float tmp[2 * NP];
+      load_pack<T, 2 * NP>(r + 2 * p0, tmp);
+#pragma unroll
+      for (int j = 0; j < NP; ++j) o[j] = tmp[2 * j];
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < NP; ++j) o[j] = to_f32(r[(p0 + j) * stride_pair]);
   }
 }
+
+// A raw 16-byte pack (VEC = 16 / sizeof(T) elements) as fp32, converted from the bits (a
+// vector register keeps the compiler from slicing the load into pieces).
+template <typename T>
+__device__ __forceinline__ void raw_to_f32(const u32x4_t& w, float (&o)[16 / sizeof(T)]) {
+  if constexpr (std::is_same<T, bf16>::value) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[2 * k] = __uint_as_float(w[k] << 16);
+      o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+  } else if constexpr (std::is_same<T, f16>::value) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[2 * k] = static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(w[k] & 0xffffu)));
+      o[2 * k + 1] = static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(w[k] >> 16)));
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = __uint_as_float(w[k]);
+  }
+}
+
+// A table piece held as loaded until the arithmetic: the 16-byte repeated-table piece stays raw
+// (converted by get() after every load of a trip has issued); other modes convert at load.
+template <typename T, int NP, int TS>
+struct TabPiece {
+  static constexpr bool kRaw = TS == kTabRepeated && sizeof(T) == 2 && NP == 4;
+  u32x4_t w;
+  float f[NP];
+  __device__ __forceinline__ void load(const T* __restrict__ r, int p0, int64_t stride_pair) {
+    if constexpr (kRaw) w = *reinterpret_cast<const u32x4_t*>(r + 2 * p0);
+    else load_table<T, NP, TS>(r, p0, stride_pair, f);
+  }
+  __device__ __forceinline__ void get(float (&o)[NP]) const {
+    if constexpr (kRaw) {
+      const uint2 ev{__builtin_amdgcn_perm(w.y, w.x, 0x05040100u), __builtin_amdgcn_perm(w.w, w.z, 0x05040100u)};
+      const Pack<T, 4> pk = __builtin_bit_cast(Pack<T, 4>, ev);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = to_f32(pk.v[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NP; ++j) o[j] = f[j];
+    }
+  }
+};
 
 // Fastest table mode the strides and alignment allow for packs of `vec` elements.
 inline int table_mode(const void* cosv, const void* sinv, int64_t cs_seq, int64_t cs_pair, int vec, size_t elem) {
@@ -80,36 +140,71 @@ __global__ __launch_bounds__(kRotThreads) void rotary_kernel(RotParts<T> io, con
   T* __restrict__ out = io.out[part];
   const BnhStrides si = io.si[part];
   const BnhStrides so = io.so[part];
-  const bool rotate = part < io.rotated;
-  for (uint32_t i = blockIdx.x * kRotThreads + threadIdx.x; i < part_packs; i += gridDim.x * kRotThreads) {
-    const uint32_t tok = packs_per_token.div(i);
-    const uint32_t e = (i - tok * packs_per_token.d) * VEC;  // element offset inside the token
-    const uint32_t b = seq.div(tok);
-    const uint32_t n = tok - b * seq.d;
-    const uint32_t h = dim.div(e);
-    const uint32_t d = e - h * dim.d;
-    float v[VEC];
-    load_pack<T, VEC>(in + b * si.b + n * si.n + h * si.h + d, v);
-    if (rotate) {
-      float cv[VEC / 2], sv[VEC / 2];
-      load_table<T, VEC / 2, TS>(cosv + n * tab.stride_seq, d >> 1, tab.stride_pair, cv);
-      load_table<T, VEC / 2, TS>(sinv + n * tab.stride_seq, d >> 1, tab.stride_pair, sv);
+  // kRotUnroll packs per thread per trip, all loads issued first; 16-byte packs are moved raw in
+  // a vector register (the copied part is stored as loaded).  Packs past the end redo the last
+  // pack.  The rotate / copy choice is made once per block, outside the loop: no load sits in a
+  // branch (a load inside a branch, or used only inside one, is waited for at the join).
+  constexpr bool kRaw = VEC * sizeof(T) == 16;
+  const uint32_t stride = gridDim.x * kRotThreads;
+  auto run = [&](auto rot_tag) {
+    constexpr bool ROT = decltype(rot_tag)::value;
+    for (uint32_t i0 = blockIdx.x * kRotThreads * kRotUnroll + threadIdx.x; i0 < part_packs;
+         i0 += stride * kRotUnroll) {
+      u32x4_t raw[kRotUnroll];
+      float v[kRotUnroll][VEC];
+      float cv[kRotUnroll][VEC / 2], sv[kRotUnroll][VEC / 2];
+      int64_t oo[kRotUnroll];
 #pragma unroll
-      for (int j = 0; j < VEC / 2; ++j) {
-        const float c = cv[j];
-        const float s = sv[j];
-        const float ev = v[2 * j], ov = v[2 * j + 1];
-        if (INVERSE) {
-          v[2 * j] = ev * c + ov * s;
-          v[2 * j + 1] = ov * c - ev * s;
-        } else {
-          v[2 * j] = ev * c - ov * s;
-          v[2 * j + 1] = ov * c + ev * s;
+      for (int u = 0; u < kRotUnroll; ++u) {
+        const uint32_t iu = i0 + u * kRotThreads;
+        const uint32_t i = iu < part_packs ? iu : part_packs - 1;
+        const uint32_t tok = packs_per_token.div(i);
+        const uint32_t e = (i - tok * packs_per_token.d) * VEC;  // element offset inside the token
+        const uint32_t b = seq.div(tok);
+        const uint32_t n = tok - b * seq.d;
+        const uint32_t h = dim.div(e);
+        const uint32_t d = e - h * dim.d;
+        const T* src = in + b * si.b + n * si.n + h * si.h + d;
+        if constexpr (kRaw) raw[u] = *reinterpret_cast<const u32x4_t*>(src);
+        else load_pack<T, VEC>(src, v[u]);
+        if constexpr (ROT) {
+          load_table<T, VEC / 2, TS>(cosv + n * tab.stride_seq, d >> 1, tab.stride_pair, cv[u]);
+          load_table<T, VEC / 2, TS>(sinv + n * tab.stride_seq, d >> 1, tab.stride_pair, sv[u]);
+        }
+        oo[u] = b * so.b + n * so.n + h * so.h + d;
+      }
+#pragma unroll
+      for (int u = 0; u < kRotUnroll; ++u) {
+        if constexpr (!(kRaw && !ROT)) {
+          if constexpr (kRaw) raw_to_f32<T>(raw[u], v[u]);
+          if constexpr (ROT) {
+#pragma unroll
+            for (int j = 0; j < VEC / 2; ++j) {
+              const float c = cv[u][j];
+              const float s = sv[u][j];
+              const float ev = v[u][2 * j], ov = v[u][2 * j + 1];
+              if (INVERSE) {
+                v[u][2 * j] = ev * c + ov * s;
+                v[u][2 * j + 1] = ov * c - ev * s;
+              } else {
+                v[u][2 * j] = ev * c - ov * s;
+                v[u][2 * j + 1] = ov * c + ev * s;
+              }
+            }
+          }
         }
       }
+      // a pack past the end recomputes the last pack from the same input and position, so its
+      // store writes the same bits the last pack's own store writes: no guard is needed
+#pragma unroll
+      for (int u = 0; u < kRotUnroll; ++u) {
+        if constexpr (kRaw && !ROT) *reinterpret_cast<u32x4_t*>(out + oo[u]) = raw[u];
+        else store_pack<T, VEC>(out + oo[u], v[u]);
+      }
     }
-    store_pack<T, VEC>(out + b * so.b + n * so.n + h * so.h + d, v);
-  }
+  };
+  if (part < io.rotated) run(std::true_type{});
+  else run(std::false_type{});
 }
 
 // `nparts` tensors of one [batch, seq, heads, dim] shape; strides are {b, n, h} triples (NULL
@@ -156,7 +251,7 @@ int launch_rotary_parts(const char* op, int nparts, int rotated, const void* con
   const FastDiv fseq(static_cast<uint32_t>(seq));
   const FastDiv fdim(static_cast<uint32_t>(dim));
   const TableRef tab{cs_seq, cs_pair};
-  const int64_t blocks64 = (packs + kRotThreads - 1) / kRotThreads;
+  const int64_t blocks64 = (packs + kRotThreads * kRotUnroll - 1) / (kRotThreads * kRotUnroll);
   const dim3 grid(static_cast<unsigned>(blocks64 < 65536 ? blocks64 : 65536), static_cast<unsigned>(nparts));
   const uint32_t np = static_cast<uint32_t>(packs);
   const int ts = table_mode(cosv, sinv, cs_seq, cs_pair, vec, sizeof(T));
@@ -204,6 +299,10 @@ int launch_rotary(const void* in, const int64_t* in_strides, const void* cosv, c
 #define PMSST_NR_ROWS 2
 #endif
 constexpr int kRowsPerSlot = PMSST_NR_ROWS;
+// Forward grid: 0 = one trip per block; N = at most N blocks per CU, each looping over trips.
+#ifndef PMSST_NR_GRID
+#define PMSST_NR_GRID 0
+#endif
 
 template <typename T, typename TG, int VEC, int NV, int TS>
 __global__ __launch_bounds__(kNormRotThreads) void norm_rot_fwd_kernel(
@@ -225,50 +324,60 @@ __global__ __launch_bounds__(kNormRotThreads) void norm_rot_fwd_kernel(
 
   for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block * kRowsPerSlot; base < rows;
        base += static_cast<int64_t>(gridDim.x) * rows_per_block * kRowsPerSlot) {
-    float xv[kRowsPerSlot][NV][VEC];
+    // every load of the trip (x packs and the cos / sin of each row's position) is issued
+    // before the first reduction; the packs stay raw until then
+    u32x4_t xr[kRowsPerSlot][NV];
+    TabPiece<T, VEC / 2, TS> ct[kRowsPerSlot][NV], st[kRowsPerSlot][NV];
 #pragma unroll
     for (int u = 0; u < kRowsPerSlot; ++u) {
+      // rows past the end load the last row (no branch around the loads: a load inside a
+      // branch is waited for at the join, which would serialize the rows of the trip)
       const int64_t row = base + u * rows_per_block + wave * rows_per_wave + slot;
+      const int64_t rl = row < rows ? row : rows - 1;
+      const uint32_t n = seq.mod(heads.div(static_cast<uint32_t>(rl)));
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        if (row < rows) {
-          load_pack<T, VEC>(x + row * dim + (v * tpr + t) * VEC, xv[u][v]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) xv[u][v][i] = 0.f;
-        }
+        const int col = (v * tpr + t) * VEC;
+        xr[u][v] = *reinterpret_cast<const u32x4_t*>(x + rl * dim + col);
+        ct[u][v].load(cosv + n * tab.stride_seq, col / 2, tab.stride_pair);
+        st[u][v].load(sinv + n * tab.stride_seq, col / 2, tab.stride_pair);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // all loads of the trip issue before the first wait
+    // a row past the end recomputes the last row from the same data, so its stores write the
+    // bits the last row's own stores write: the arithmetic and stores need no guard (a load
+    // used only under a guard would be moved into it and waited for there)
 #pragma unroll
     for (int u = 0; u < kRowsPerSlot; ++u) {
       const int64_t row = base + u * rows_per_block + wave * rows_per_wave + slot;
+      const int64_t rl = row < rows ? row : rows - 1;
+      float xv[NV][VEC];
       float ss = 0.f;
 #pragma unroll
-      for (int v = 0; v < NV; ++v)
+      for (int v = 0; v < NV; ++v) {
+        raw_to_f32<T>(xr[u][v], xv[v]);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) ss += xv[u][v][i] * xv[u][v][i];
+        for (int i = 0; i < VEC; ++i) ss += xv[v][i] * xv[v][i];
+      }
       ss = group_sum(ss, tpr);
       const float inv = 1.0f / fmaxf(sqrtf(ss), 1.0e-12f);
-      if (row < rows) {
-        const uint32_t n = seq.mod(heads.div(static_cast<uint32_t>(row)));
-        const float s = inv * scale;
+      const float s = inv * scale;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          const int col = (v * tpr + t) * VEC;
-          float cv[VEC / 2], sv[VEC / 2], o[VEC];
-          load_table<T, VEC / 2, TS>(cosv + n * tab.stride_seq, col / 2, tab.stride_pair, cv);
-          load_table<T, VEC / 2, TS>(sinv + n * tab.stride_seq, col / 2, tab.stride_pair, sv);
+      for (int v = 0; v < NV; ++v) {
+        const int col = (v * tpr + t) * VEC;
+        float cv[VEC / 2], sv[VEC / 2], o[VEC];
+        ct[u][v].get(cv);
+        st[u][v].get(sv);
 #pragma unroll
-          for (int j = 0; j < VEC / 2; ++j) {
-            const float ev = xv[u][v][2 * j] * s * g[v][2 * j];
-            const float ov = xv[u][v][2 * j + 1] * s * g[v][2 * j + 1];
-            o[2 * j] = ev * cv[j] - ov * sv[j];
-            o[2 * j + 1] = ov * cv[j] + ev * sv[j];
-          }
-          store_pack<T, VEC>(out + row * dim + col, o);
+        for (int j = 0; j < VEC / 2; ++j) {
+          const float ev = xv[v][2 * j] * s * g[v][2 * j];
+          const float ov = xv[v][2 * j + 1] * s * g[v][2 * j + 1];
+          o[2 * j] = ev * cv[j] - ov * sv[j];
+          o[2 * j + 1] = ov * cv[j] + ev * sv[j];
         }
-        if (t == 0) inv_norm[row] = inv;
+        store_pack<T, VEC>(out + rl * dim + col, o);
       }
+      if (t == 0) inv_norm[rl] = inv;
     }
   }
 }
@@ -300,63 +409,66 @@ __global__ __launch_bounds__(kRowBwdThreads) void norm_rot_bwd_kernel(
 
   for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block * kRowsPerSlot; base < rows;
        base += static_cast<int64_t>(gridDim.x) * rows_per_block * kRowsPerSlot) {
-    // loads of all kRowsPerSlot rows first
-    float d[kRowsPerSlot][NV][VEC], n[kRowsPerSlot][NV][VEC], inv[kRowsPerSlot];
+    // loads of all kRowsPerSlot rows first, held raw until every load of the trip has issued.
+    // Rows past the end load the last row (no branch around the loads) and recompute it: their
+    // dx stores write the bits the last row's own stores write, and only the dgamma
+    // accumulation excludes them.
+    u32x4_t dr[kRowsPerSlot][NV], xr[kRowsPerSlot][NV];
+    TabPiece<T, VEC / 2, TS> ct[kRowsPerSlot][NV], st[kRowsPerSlot][NV];
+    float inv[kRowsPerSlot];
 #pragma unroll
     for (int u = 0; u < kRowsPerSlot; ++u) {
       const int64_t row = base + u * rows_per_block + wave * rows_per_wave + slot;
-      const bool valid = row < rows;
-      inv[u] = valid ? inv_norm[row] : 0.f;
+      const int64_t rl = row < rows ? row : rows - 1;
+      inv[u] = inv_norm[rl];
+      const uint32_t pos = seq.mod(heads.div(static_cast<uint32_t>(rl)));
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
         const int col = (v * tpr + t) * VEC;
-        if (valid) {
-          load_pack<T, VEC>(dy + row * dim + col, d[u][v]);
-          load_pack<T, VEC>(x + row * dim + col, n[u][v]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) d[u][v][i] = n[u][v][i] = 0.f;
-        }
+        dr[u][v] = *reinterpret_cast<const u32x4_t*>(dy + rl * dim + col);
+        xr[u][v] = *reinterpret_cast<const u32x4_t*>(x + rl * dim + col);
+        ct[u][v].load(cosv + pos * tab.stride_seq, col / 2, tab.stride_pair);
+        st[u][v].load(sinv + pos * tab.stride_seq, col / 2, tab.stride_pair);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // all loads of the trip issue before the first wait
 #pragma unroll
     for (int u = 0; u < kRowsPerSlot; ++u) {
       const int64_t row = base + u * rows_per_block + wave * rows_per_wave + slot;
       const bool valid = row < rows;
+      const int64_t rl = valid ? row : rows - 1;
       const float ns = inv[u] * scale;
-      const uint32_t pos = valid ? seq.mod(heads.div(static_cast<uint32_t>(row))) : 0u;
-      float gr[NV][VEC];
+      float gr[NV][VEC], n[NV][VEC];
       float dot = 0.f;
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        const int col = (v * tpr + t) * VEC;
-        float cv[VEC / 2], sv[VEC / 2];
-        load_table<T, VEC / 2, TS>(cosv + pos * tab.stride_seq, col / 2, tab.stride_pair, cv);
-        load_table<T, VEC / 2, TS>(sinv + pos * tab.stride_seq, col / 2, tab.stride_pair, sv);
+        float d[VEC], cv[VEC / 2], sv[VEC / 2];
+        raw_to_f32<T>(dr[u][v], d);
+        raw_to_f32<T>(xr[u][v], n[v]);
+        ct[u][v].get(cv);
+        st[u][v].get(sv);
 #pragma unroll
         for (int j = 0; j < VEC / 2; ++j) {
-          gr[v][2 * j] = d[u][v][2 * j] * cv[j] + d[u][v][2 * j + 1] * sv[j];
-          gr[v][2 * j + 1] = d[u][v][2 * j + 1] * cv[j] - d[u][v][2 * j] * sv[j];
+          gr[v][2 * j] = d[2 * j] * cv[j] + d[2 * j + 1] * sv[j];
+          gr[v][2 * j + 1] = d[2 * j + 1] * cv[j] - d[2 * j] * sv[j];
         }
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          n[u][v][i] *= ns;
-          dot += gr[v][i] * g[v][i] * n[u][v][i];
+          n[v][i] *= ns;
+          dot += gr[v][i] * g[v][i] * n[v][i];
         }
       }
       dot = group_sum(dot, tpr);
-      if (valid) {
-        const float dot_s = dot * inv_scale;
+      const float dot_s = dot * inv_scale;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          float o[VEC];
+      for (int v = 0; v < NV; ++v) {
+        float o[VEC];
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) {
-            o[i] = inv[u] * (gr[v][i] * g[v][i] * scale - n[u][v][i] * dot_s);
-            acc[v][i] += gr[v][i] * n[u][v][i];
-          }
-          store_pack<T, VEC>(dx + row * dim + (v * tpr + t) * VEC, o);
+        for (int i = 0; i < VEC; ++i) {
+          o[i] = inv[u] * (gr[v][i] * g[v][i] * scale - n[v][i] * dot_s);
+          acc[v][i] += valid ? gr[v][i] * n[v][i] : 0.f;
         }
+        store_pack<T, VEC>(dx + rl * dim + (v * tpr + t) * VEC, o);
       }
     }
   }
@@ -413,7 +525,9 @@ int launch_norm_rot_fwd(const void* x, const void* gamma, const void* cosv, cons
   const int64_t rows = a.batch * a.seq * a.heads;
   if (rows == 0) return PMSST_OK;
   const int rpb = (kWave >> geo.tpr_log2) * (kNormRotThreads / kWave) * kRowsPerSlot;
-  const int64_t blocks64 = (rows + rpb - 1) / rpb;
+  int64_t blocks64 = (rows + rpb - 1) / rpb;
+  if (PMSST_NR_GRID > 0 && blocks64 > static_cast<int64_t>(PMSST_NR_GRID) * num_cus())
+    blocks64 = static_cast<int64_t>(PMSST_NR_GRID) * num_cus();
   const int blocks = static_cast<int>(blocks64 < 65536 ? blocks64 : 65536);
   const float scale = sqrtf(static_cast<float>(a.dim));
   const FastDiv fh(static_cast<uint32_t>(a.heads)), fs(static_cast<uint32_t>(a.seq));
