@@ -25,6 +25,7 @@
 //   4. dW^T[h][j] = x_b^T dpre_b    (K = M),     tiles 128 h x 64 j.
 // All reductions have a fixed order; no atomics.
 #include "common.h"
+#include "dma_gemm.h"
 #include "gemm.h"
 #include "rowgeom.h"
 
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(PM
 // Tile: 128 rows of M x 64 GLU outputs of one band.  A stage holds 128 weight rows then 128 x
 // rows, 64 bytes (one 32-wide K chunk) per row.  Weight rows are ordered in 16-row blocks left,
 // gate, left, gate, ...: tile row R is output l0 + 16 (R / 32) + R % 16, gate when (R / 16) is
-// odd.  The four 16-byte units of a row are stored XOR-swizzled (mef_swz) so MFMA fragment
+// odd.  The four 16-byte units of a row are stored XOR-swizzled (swz_k) so MFMA fragment
 // reads are free of bank conflicts.
 //
 // Waves are 2 x 2: wave (wr, wc) multiplies weight rows 64 wr .. + 64 (4 fragments = 32
@@ -175,58 +176,22 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(PM
 #endif
 constexpr int kMefStage = 16384;  // bytes of one LDS stage
 
-// Block schedule of the forward: the blocks in canonical order (band, row tile, 64-output
-// chunk) are cut into kXcds contiguous ranges of whole (band, row tile) units, balanced by
-// block count, and range x runs on XCD x (hardware places block i on XCD i % 8).  The chunks
-// of one row tile -- which read the same x rows -- and the row tiles of one band -- which read
-// the same weights -- then share that XCD's L2, and neighbouring narrow bands, which write
-// neighbouring columns of pre and out, write them through the same L2.
-constexpr int kSchedMaxBands = 256;
-struct MefSched {
-  uint32_t gs[kXcds + 1];                // canonical block range [gs[x], gs[x+1]) of XCD x
-  uint32_t cumb[kSchedMaxBands + 1];     // canonical index of each band's first block
-  uint32_t bstart[kXcds];                // band of XCD x's first block
-  uint32_t m_tiles;                      // row tiles; 0: no schedule, use the XcdGrid map
-};
-
-// Unit swizzle of a stage row (by its index r mod 16).  An MFMA fragment read is 16 rows x one
-// 16-byte unit; with the swizzle the rows of every 8-lane half (128 bytes, 32 banks) and of the
-// whole 16 lanes (256 bytes, 64 banks) land on distinct bank groups: rows of equal parity in
-// each half, and rows equal mod 4, get distinct units.
-__device__ __forceinline__ int mef_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
-
-template <typename T>
-__device__ __forceinline__ f32x4_t mfma_raw(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
-  if constexpr (std::is_same<T, bf16>::value)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                   c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
-                                                  0, 0, 0);
-}
 
 template <typename T>
 __global__ __launch_bounds__(kGemmThreads) void me_fwd_dma_kernel(const T* __restrict__ x,
                                                                   const T* __restrict__ weight,
                                                                   const T* __restrict__ bias, T* __restrict__ pre,
                                                                   T* __restrict__ out, int max_lchunks, XcdGrid xg,
-                                                                  MaskArgs a, MefSched sc) {
+                                                                  MaskArgs a, BandSched sc) {
   constexpr int S = PMSST_MEF_STAGES;
   static_assert(S >= 2 && S <= 8, "stages");
   __shared__ __attribute__((aligned(1024))) char lds[S * kMefStage];
   int band, l0;
   uint32_t mt;
   if (sc.m_tiles != 0) {
-    const uint32_t xcd = blockIdx.x % kXcds;
-    const uint32_t gb = sc.gs[xcd] + blockIdx.x / kXcds;
-    if (gb >= sc.gs[xcd + 1]) return;
-    uint32_t b = sc.bstart[xcd];
-    while (gb >= sc.cumb[b + 1]) ++b;
-    const uint32_t nch = (sc.cumb[b + 1] - sc.cumb[b]) / sc.m_tiles;
-    const uint32_t within = gb - sc.cumb[b];
-    band = static_cast<int>(b);
-    mt = within / nch;
-    l0 = static_cast<int>(within % nch) * 64;
+    uint32_t chunk, nch;
+    if (!sched_block(sc, band, mt, chunk, nch)) return;
+    l0 = static_cast<int>(chunk) * 64;
   } else {
     uint32_t grp;  // group = (band, 64-output chunk), member = row tile: weight chunk shared in L2
     if (!xcd_block(xg, grp, mt)) return;
@@ -246,7 +211,7 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_dma_kernel(const T* __res
 
   // DMA pieces of this lane: instruction t moves tile row R = 64 wave + 16 t + lane / 4
   // (R % 16 = lane / 4), physical unit lane % 4, i.e. logical K unit u = (lane % 4) ^ swz(lane / 4)
-  const uint32_t u = static_cast<uint32_t>((lane & 3) ^ mef_swz(lane >> 2));
+  const uint32_t u = static_cast<uint32_t>((lane & 3) ^ swz_k(lane >> 2));
   uint32_t soff[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -293,7 +258,7 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_dma_kernel(const T* __res
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // fragment read addresses inside a stage: row R, logical unit g -> R * 64 + 16 (g ^ swz(R % 16))
-  const uint32_t sw = 16u * static_cast<uint32_t>(g ^ mef_swz(rr));
+  const uint32_t sw = 16u * static_cast<uint32_t>(g ^ swz_k(rr));
   const uint32_t abase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)) +
                          static_cast<uint32_t>((64 * wr + rr) * 64) + sw;
   const uint32_t bbase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)) + 8192u +
@@ -327,34 +292,58 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_dma_kernel(const T* __res
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma_raw<T>(af[i], bf[j], acc[i][j]);
     }
   }
-  // no DMA may still be writing this block's LDS when its waves end
+  // no DMA may still be writing this block's LDS when its waves end or the epilogue reuses it
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (!active) return;
 
-  // epilogue: fragment pair (2h, 2h + 1) = (left, gate) of outputs l0 + 32 wr + 16 h + 4 g + r
-  const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
+  // epilogue through LDS: fragment pair (2h, 2h + 1) = (left, gate) of outputs
+  // l0 + 32 wr + 16 h + 4 g + r of rows m = 64 wc + 16 j + rr (8-byte runs of 16 rows per
+  // instruction).  The three result tiles (pre left, pre gate, out) are staged as [128 m][64 l]
+  // (row pitch 144 bytes) and written back row by row, 16 lanes x 8 bytes = 128 contiguous
+  // bytes per row, so HBM sees whole lines.
+  __syncthreads();  // every wave is done with the ring
+  constexpr int kOP = 72;  // staged row pitch in elements
+  T* ol = reinterpret_cast<T*>(lds);
+  T* og = ol + kFwdBM * kOP;
+  T* oo = og + kFwdBM * kOP;
+  if (active) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int l = l0 + 32 * wr + 16 * h + 4 * g;
-    if (l >= I) continue;  // I_b is a multiple of 4 on this path: the 4 outputs are all valid
-    float bl[4], bgt[4];
-    load_pack<T, 4>(bias + 2 * off + l, bl);
-    load_pack<T, 4>(bias + 2 * off + I + l, bgt);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = 64 * wc + 16 * j + rr;
-      if (m >= rows_valid) continue;
-      float vl[4], vg[4], vo[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        vl[r] = acc[2 * h][j][r] + bl[r];
-        vg[r] = acc[2 * h + 1][j][r] + bgt[r];
-        vo[r] = vl[r] * sigmoidf_(vg[r]);
+    for (int h = 0; h < 2; ++h) {
+      const int lt = 32 * wr + 16 * h + 4 * g;  // tile column
+      const int l = l0 + lt;
+      float bl[4] = {0.f, 0.f, 0.f, 0.f}, bgt[4] = {0.f, 0.f, 0.f, 0.f};
+      if (l < I) {  // I_b is a multiple of 4 on this path: the 4 outputs are all valid or none
+        load_pack<T, 4>(bias + 2 * off + l, bl);
+        load_pack<T, 4>(bias + 2 * off + I + l, bgt);
       }
-      T* pl = pre + (m0 + m) * pitch2 + 2 * off + l;
-      store_pack<T, 4>(pl, vl);
-      store_pack<T, 4>(pl + I, vg);
-      store_pack<T, 4>(out + (m0 + m) * a.F + off + l, vo);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = 64 * wc + 16 * j + rr;
+        float vl[4], vg[4], vo[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          vl[r] = acc[2 * h][j][r] + bl[r];
+          vg[r] = acc[2 * h + 1][j][r] + bgt[r];
+          vo[r] = vl[r] * sigmoidf_(vg[r]);
+        }
+        store_pack<T, 4>(ol + m * kOP + lt, vl);
+        store_pack<T, 4>(og + m * kOP + lt, vg);
+        store_pack<T, 4>(oo + m * kOP + lt, vo);
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
+  const int c4 = (static_cast<int>(threadIdx.x) & 15) * 4;  // tile column of this thread's piece
+  if (l0 + c4 < I) {
+#pragma unroll
+    for (int p = 0; p < kFwdBM / 16; ++p) {
+      const int m = static_cast<int>(threadIdx.x >> 4) + 16 * p;
+      if (m >= rows_valid) break;
+      T* pl = pre + (m0 + m) * pitch2 + 2 * off + l0 + c4;
+      *reinterpret_cast<u32x2_t*>(pl) = *reinterpret_cast<const u32x2_t*>(ol + m * kOP + c4);
+      *reinterpret_cast<u32x2_t*>(pl + I) = *reinterpret_cast<const u32x2_t*>(og + m * kOP + c4);
+      *reinterpret_cast<u32x2_t*>(out + (m0 + m) * a.F + off + l0 + c4) =
+          *reinterpret_cast<const u32x2_t*>(oo + m * kOP + c4);
     }
   }
 }
@@ -533,6 +522,178 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __rest
   }
 }
 
+// dx on the DMA ring (16-bit, 4-aligned widths, H % 128 == 0).  Tile 128 h x 128 m: per K
+// chunk, A = W_b^T as stored (32 K-rows j x 128 h, 8 KB, transpose-read fragments) and
+// B = dpre rows (128 m x 32 j, 8 KB).  The bound is the L2 -> CU traffic of the re-read
+// operand tiles, so the tile is as large as one block's registers allow (every weight chunk
+// is read once per 128 rows).  Chunk 0 of K is the partial one (K chunks end at 2 I_b);
+// its pieces with j < 0 are read from row / column 0 and zeroed in LDS once the DMA has
+// landed.  DMA: 16 dwordx4 per stage, wave w moves weight K-rows 4w .. 4w + 3 and
+// 16 + 4w .. 16 + 4w + 3 and dpre rows 16w .. 16w + 15 and 64 + 16w .. 64 + 16w + 15.
+// The block schedule balances the XCDs by K steps and starts the long (wide-band) blocks
+// first.
+#ifndef PMSST_ME_DX_DMA
+#define PMSST_ME_DX_DMA 1
+#endif
+#ifndef PMSST_ME_DX_STAGES
+#define PMSST_ME_DX_STAGES 4
+#endif
+constexpr int kDxStage = 16384;
+constexpr int kDxHC = 128;  // hidden columns per block
+constexpr int kDxBMd = 128;  // rows per block
+
+template <typename T, bool TANH_IN>
+__global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_dma_kernel(const T* __restrict__ dpre,
+                                                                     const T* __restrict__ weight,
+                                                                     const T* __restrict__ x, T* __restrict__ dx,
+                                                                     BandSched sc, MaskArgs a) {
+  constexpr int S = PMSST_ME_DX_STAGES;
+  static_assert(S >= 3 && S <= 8, "stages");
+  __shared__ __attribute__((aligned(1024))) char lds[S * kDxStage];
+  int band;
+  uint32_t mt, hc, nhc_u;
+  if (!sched_block<true>(sc, band, mt, hc, nhc_u)) return;
+  const int off = static_cast<int>(a.offsets[band]);
+  const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  const int H = a.H, K = 2 * I;
+  const int64_t m0 = static_cast<int64_t>(mt) * kDxBMd;
+  const int rows_valid = static_cast<int>(a.M - m0 < kDxBMd ? a.M - m0 : kDxBMd);
+  const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int wr = wave >> 1, wc = wave & 1;
+  const int nk = (K + kChunkK - 1) / kChunkK;
+  const int kbeg = K - nk * kChunkK;  // multiple of 8 (I % 4 == 0)
+
+  // DMA pieces of this lane: t = 0, 1 weight K-rows (unit ua), t = 0, 1 dpre rows (unit ub)
+  uint32_t aoff[2], aoff0[2], boff[2], boff0[2];  // byte offsets from the chunk's bases (full / chunk 0)
+  bool aok0[2], bok0;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int kr = 4 * (wave + 4 * t) + (lane >> 4);
+    const int ua = (lane & 15) ^ swz_mn(kr);
+    aoff[t] = static_cast<uint32_t>((kr * H + 8 * ua) * 2);
+    aok0[t] = kbeg + kr >= 0;
+    aoff0[t] = aok0[t] ? aoff[t] : static_cast<uint32_t>((-kbeg * H + 8 * ua) * 2);  // row j = 0
+  }
+  {
+    const int ub = (lane & 3) ^ swz_k((lane >> 2) & 15);  // rows 16 w + lane / 4 (+ 64): same swizzle
+    bok0 = kbeg + 8 * ub >= 0;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int mr = 64 * t + 16 * wave + (lane >> 2);
+      const int mrc = mr < rows_valid ? mr : rows_valid - 1;
+      boff[t] = static_cast<uint32_t>((mrc * pitch2 + 8 * ub) * 2);
+      boff0[t] = bok0 ? boff[t] : static_cast<uint32_t>((mrc * pitch2 - kbeg) * 2);  // column j = 0
+    }
+  }
+  const char* wsrc0 = reinterpret_cast<const char*>(weight + static_cast<int64_t>(2) * off * H +
+                                                    static_cast<int64_t>(kbeg) * H + hc * kDxHC);
+  const char* dsrc0 = reinterpret_cast<const char*>(dpre + m0 * pitch2 + 2 * off + kbeg);
+  const uint32_t lds0 = lds_addr(lds);
+
+  auto dma = [&](int kc, int stage) {  // K chunk kc into `stage`
+    const char* wsrc = wsrc0 + static_cast<int64_t>(kc) * kChunkK * H * 2;
+    const char* dsrc = dsrc0 + kc * kChunkK * 2;
+    char* st = lds + stage * kDxStage;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      __builtin_amdgcn_global_load_lds(wsrc + (kc == 0 ? aoff0[t] : aoff[t]), st + (wave + 4 * t) * 1024, 16, 0,
+                                       0);
+      __builtin_amdgcn_global_load_lds(dsrc + (kc == 0 ? boff0[t] : boff[t]),
+                                       st + 8192 + (wave + 4 * t) * 1024, 16, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) dma(s, s);
+
+  uint32_t fa[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) fa[i] = frag_mn_addr(lds0, 64 * wr + 16 * i, 2 * kDxHC, lane);
+  const uint32_t fb = frag_k_addr(lds0 + 8192, 64 * wc, lane);
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int s = 0; s < nk; ++s) {
+    // chunk s landed once at most 4 nd DMAs are outstanding, nd = chunks issued after it
+    // (s + 1 .. s + S - 2 that exist); the loop issues no other memory operation
+    const int nd = nk - 1 - s < S - 2 ? nk - 1 - s : S - 2;
+    static_assert(S - 2 <= 6, "wait table");
+    switch (nd) {
+      case 0: vm_wait<0>(); break;
+      case 1: vm_wait<4>(); break;
+      case 2: vm_wait<8>(); break;
+      case 3: vm_wait<12>(); break;
+      case 4: vm_wait<16>(); break;
+      case 5: vm_wait<20>(); break;
+      default: vm_wait<24>(); break;
+    }
+    if (s == 0 && kbeg < 0) {
+      // zero this lane's pieces of chunk 0 that lie below j = 0
+      const u32x4_t z{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (!aok0[t]) *reinterpret_cast<u32x4_t*>(lds + (wave + 4 * t) * 1024 + lane * 16) = z;
+        if (!bok0) *reinterpret_cast<u32x4_t*>(lds + 8192 + (wave + 4 * t) * 1024 + lane * 16) = z;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (s + S - 1 < nk) dma(s + S - 1, (s + S - 1) % S);  // into the stage chunk s - 1 used
+    const uint32_t so = static_cast<uint32_t>((s % S) * kDxStage);
+    u32x4_t af[4], bfr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = lds_read_tr_pair(fa[i] + so, 4 * 2 * kDxHC);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bfr[j] = lds_read_b128(fb + so + 1024 * j);
+    lds_wait(af, bfr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma_raw<T>(af[i], bfr[j], acc[i][j]);
+  }
+
+  // epilogue through LDS: lane holds h = 64 wr + 16 i + 4 (lane / 16) + r of rows
+  // m = 64 wc + 16 j + lane % 16 (8-byte runs of 16 rows per instruction); the tile is staged as
+  // [128 m][128 h] (row pitch 272 bytes) and written back as 16-byte pieces, 256 contiguous
+  // bytes per row, so HBM sees whole lines.  With a tanh input the factor 1 - x^2 is applied
+  // before staging (x read at the lane's own positions), so dx is rounded once.
+  __syncthreads();  // every wave is done with the ring (its last wait was vmcnt(0))
+  constexpr int kOP = 136;  // staged row pitch in elements
+  T* ot = reinterpret_cast<T*>(lds);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = 64 * wc + 16 * j + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 64 * wr + 16 * i + 4 * (lane >> 4);
+      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      if (TANH_IN) {
+        const int mc = m < rows_valid ? m : rows_valid - 1;
+        float tx[4];
+        load_pack<T, 4>(x + ((m0 + mc) * a.NB + band) * H + hc * kDxHC + h, tx);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] *= 1.0f - tx[r] * tx[r];
+      }
+      store_pack<T, 4>(ot + m * kOP + h, v);
+    }
+  }
+  __syncthreads();
+  const int c8 = (threadIdx.x & 15) * 8;
+#pragma unroll
+  for (int p = 0; p < kDxBMd / 16; ++p) {
+    const int row = static_cast<int>(threadIdx.x >> 4) + 16 * p;
+    if (row < rows_valid)
+      *reinterpret_cast<u32x4_t*>(dx + ((m0 + row) * a.NB + band) * H + hc * kDxHC + c8) =
+          *reinterpret_cast<const u32x4_t*>(ot + row * kOP + c8);
+  }
+}
+
 constexpr int kDwBH = 128;
 constexpr int kDwBJ = 64;
 
@@ -604,62 +765,6 @@ struct HostMask {
 #define PMSST_ME_FWD_SCHED 1
 #endif
 
-// Contiguous split of the (band, row tile) units (chunks_b blocks each, canonical order) into
-// kXcds ranges with the smallest maximum block count (binary search on the cap, greedy fill).
-// Returns false (no schedule) when the band count exceeds the table.
-bool build_mef_sched(const int64_t* dim_inputs, int NB, int64_t m_tiles, MefSched* sc, uint32_t* per_xcd) {
-  sc->m_tiles = 0;
-  if (!PMSST_ME_FWD_SCHED || NB > kSchedMaxBands || m_tiles <= 0) return false;
-  int64_t total = 0, unit_max = 0;
-  sc->cumb[0] = 0;
-  for (int b = 0; b < NB; ++b) {
-    const int64_t ch = (dim_inputs[b] + 63) / 64;
-    unit_max = ch > unit_max ? ch : unit_max;
-    total += ch * m_tiles;
-    if (total >= (int64_t{1} << 31)) return false;
-    sc->cumb[b + 1] = static_cast<uint32_t>(total);
-  }
-  auto ranges = [&](int64_t cap, bool fill) {
-    int x = 0;
-    int64_t acc = 0, g = 0;
-    if (fill) {
-      sc->gs[0] = 0;
-      sc->bstart[0] = 0;
-    }
-    for (int b = 0; b < NB; ++b) {
-      const int64_t ch = (sc->cumb[b + 1] - sc->cumb[b]) / m_tiles;
-      for (int64_t t = 0; t < m_tiles; ++t, g += ch) {
-        if (acc + ch > cap) {
-          ++x;
-          acc = 0;
-          if (fill && x < static_cast<int>(kXcds)) {
-            sc->gs[x] = static_cast<uint32_t>(g);
-            sc->bstart[x] = static_cast<uint32_t>(b);
-          }
-        }
-        acc += ch;
-      }
-    }
-    if (fill)
-      for (int y = x + 1; y <= static_cast<int>(kXcds); ++y) {
-        sc->gs[y] = static_cast<uint32_t>(total);
-        if (y < static_cast<int>(kXcds)) sc->bstart[y] = static_cast<uint32_t>(NB - 1);
-      }
-    return x + 1;
-  };
-  int64_t lo = unit_max, hi = total > unit_max ? total : unit_max;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) / 2;
-    if (ranges(mid, false) <= static_cast<int>(kXcds)) hi = mid;
-    else lo = mid + 1;
-  }
-  ranges(lo, true);
-  uint32_t mx = 0;
-  for (uint32_t y = 0; y < kXcds; ++y) mx = sc->gs[y + 1] - sc->gs[y] > mx ? sc->gs[y + 1] - sc->gs[y] : mx;
-  sc->m_tiles = static_cast<uint32_t>(m_tiles);
-  *per_xcd = mx;
-  return true;
-}
 
 int check_mask(const char* op, const int64_t* dim_inputs, int64_t band_count, int64_t H, HostMask* hm) {
   PMSST_REQUIRE(dim_inputs != nullptr && band_count > 0 && band_count < (1 << 16), "%s: bad band count", op);
@@ -704,9 +809,12 @@ int launch_me_fwd(const void* x, const void* weight, const void* bias, const int
     if (PMSST_ME_FWD_DMA && a.vec4 && H % 8 == 0 && H > kChunkK && al(x, 16) && al(weight, 16) &&
         al(bias, 4 * sizeof(T)) && (2 * static_cast<int64_t>(hm.max_width) + 1) * H * 2 < (int64_t{1} << 31) &&
         (static_cast<int64_t>(kFwdBM) * hm.NB + 1) * H * 2 < (int64_t{1} << 31)) {
-      MefSched sc;
+      BandSched sc;
       uint32_t per_xcd = 0;
-      const bool sched = build_mef_sched(dim_inputs, hm.NB, (M + kFwdBM - 1) / kFwdBM, &sc, &per_xcd);
+      const bool sched =
+          PMSST_ME_FWD_SCHED && build_band_sched(
+                                    hm.NB, (M + kFwdBM - 1) / kFwdBM,
+                                    [&](int b) { return (dim_inputs[b] + 63) / 64; }, &sc, &per_xcd);
       const dim3 g(sched ? per_xcd * kXcds : grid.x);
       hipLaunchKernelGGL((me_fwd_dma_kernel<T>), g, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
                          static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
@@ -732,8 +840,8 @@ size_t me_bwd_workspace(int64_t M, int F, size_t elem) {
 
 template <typename T>
 int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* weight, const int64_t* offsets,
-                  const HostMask& hm, int64_t M, int64_t H, void* dx, void* dbias, void* dw, int input_act,
-                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                  const int64_t* dim_inputs, const HostMask& hm, int64_t M, int64_t H, void* dx, void* dbias,
+                  void* dw, int input_act, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const char* op = "mask_estimator_final_backward";
   PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
   PMSST_REQUIRE(input_act == PMSST_ACT_NONE || input_act == PMSST_ACT_TANH, "%s: bad input_activation %d", op,
@@ -761,20 +869,49 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
                        static_cast<const T*>(pre), dpre, a);
     int rc = check_launch("me_dpre_kernel");
     if (rc != PMSST_OK) return rc;
-    const int hchunks = static_cast<int>((H + kDxBH - 1) / kDxBH);
-    const XcdGrid xg2{static_cast<uint32_t>(hm.NB * hchunks), static_cast<uint32_t>((M + kDxBM - 1) / kDxBM)};
-    const dim3 g2(xg2.blocks());
+    BandSched dsc;
+    uint32_t dx_per_xcd = 0;
+    const int nhc = static_cast<int>(H / kDxHC);
+    const bool dx_dma = sizeof(T) == 2 && PMSST_ME_DX_DMA && a.vec4 && H % kDxHC == 0 && al(weight, 16) &&
+                        al(dx, 16) &&
+                        (static_cast<int64_t>(kChunkK) * H + H) * 2 < (int64_t{1} << 31) &&
+                        (kDxBMd * 2 * static_cast<int64_t>(hm.F) + 64) * 2 < (int64_t{1} << 31) &&
+                        build_band_sched(
+                            hm.NB, (M + kDxBMd - 1) / kDxBMd,
+                            [&](int) { return static_cast<int64_t>(nhc); },  // hidden chunks
+                            [&](int b) {  // K steps per block (+2 for its prologue and epilogue)
+                              return (2 * dim_inputs[b] + kChunkK - 1) / kChunkK + 2;
+                            },
+                            &dsc, &dx_per_xcd);
+    if constexpr (sizeof(T) == 2) {
+      if (dx_dma) {
+        const dim3 gd(dx_per_xcd * kXcds);
+        if (input_act == PMSST_ACT_TANH)
+          hipLaunchKernelGGL((me_bwd_dx_dma_kernel<T, true>), gd, dim3(kGemmThreads), 0, stream, dpre,
+                             static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), dsc, a);
+        else
+          hipLaunchKernelGGL((me_bwd_dx_dma_kernel<T, false>), gd, dim3(kGemmThreads), 0, stream, dpre,
+                             static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), dsc, a);
+        rc = check_launch("me_bwd_dx_dma_kernel");
+        if (rc != PMSST_OK) return rc;
+      }
+    }
+    if (!dx_dma) {
+      const int hchunks = static_cast<int>((H + kDxBH - 1) / kDxBH);
+      const XcdGrid xg2{static_cast<uint32_t>(hm.NB * hchunks), static_cast<uint32_t>((M + kDxBM - 1) / kDxBM)};
+      const dim3 g2(xg2.blocks());
 #define PMSST_MDX(TANH, V4)                                                                                    \
   hipLaunchKernelGGL((me_bwd_dx_kernel<T, TANH, V4>), g2, dim3(kGemmThreads), 0, stream, dpre,                   \
                      static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), hchunks, xg2, a)
-    if (input_act == PMSST_ACT_TANH) {
-      if (a.vec4) PMSST_MDX(true, true); else PMSST_MDX(true, false);
-    } else {
-      if (a.vec4) PMSST_MDX(false, true); else PMSST_MDX(false, false);
-    }
+      if (input_act == PMSST_ACT_TANH) {
+        if (a.vec4) PMSST_MDX(true, true); else PMSST_MDX(true, false);
+      } else {
+        if (a.vec4) PMSST_MDX(false, true); else PMSST_MDX(false, false);
+      }
 #undef PMSST_MDX
-    rc = check_launch("me_bwd_dx_kernel");
-    if (rc != PMSST_OK) return rc;
+      rc = check_launch("me_bwd_dx_kernel");
+      if (rc != PMSST_OK) return rc;
+    }
   }
   const int max_jchunks = (2 * hm.max_width + kDwBJ - 1) / kDwBJ;
   const int htiles = static_cast<int>((H + kDwBH - 1) / kDwBH);
@@ -838,7 +975,8 @@ int pmsst_mask_estimator_final_backward(const void* grad_out, const void* x, con
   if (rc != PMSST_OK) return rc;
   return with_dtype(dtype, "mask_estimator_final_backward", [&](auto tag) {
     using T = decltype(tag);
-    return launch_me_bwd<T>(grad_out, x, pre, weight, dim_offsets, hm, rows, hidden, grad_x, grad_bias, grad_weight,
+    return launch_me_bwd<T>(grad_out, x, pre, weight, dim_offsets, dim_inputs, hm, rows, hidden, grad_x, grad_bias,
+                            grad_weight,
                             input_activation, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
   });
 }

@@ -73,11 +73,12 @@ def test_mel_style_widths(hip_ext):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m,hidden", [(77, 200), (64, 768), (1, 144), (300, 216)])
+@pytest.mark.parametrize("m,hidden", [(77, 200), (64, 768), (1, 144), (300, 216), (130, 256), (3, 384)])
 def test_register_direct_forward_classes(hip_ext, dtype, m, hidden):
-    """16-bit forward with every width a multiple of 4 and hidden % 8 == 0 (the register-direct
-    kernel): widths of each output class (<= 8, <= 16, 32-chunks with a partial last chunk),
-    a first K step that is partly below zero (hidden % 32 != 0), and M not a multiple of the tile."""
+    """16-bit forward and backward with every width a multiple of 4 (the DMA-ring kernels when
+    hidden % 8 == 0, and for dx when hidden % 128 == 0): narrow and wide bands, partial first K
+    chunks of the forward (hidden % 32 != 0) and of dx (2 I_b % 32 != 0), M not a multiple of
+    the row tiles."""
     widths = (4, 8, 12, 16, 20, 24, 32, 36, 48, 96, 100, 516, 8, 4)
     _check(hip_ext, widths, m, hidden, dtype, 17 + m)
 
