@@ -42,6 +42,8 @@ struct BandArgs {
   int O;              // out_features
   bool vec4;          // all offsets, pitches and widths are multiples of 4 elements
   bool ovec4;         // O % 4 == 0 and out / bias / grad_out are 4-element aligned
+  bool ovec8;         // 16-bit, O % 8 == 0, out 16-byte aligned and bias 4-element aligned:
+                      // the forward stages its output tile through LDS
 };
 
 // B operand of the forward: rows m of x (K = band features) scaled by gamma;
@@ -137,7 +139,9 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
   using S = TileShape<OT, kBM, 4, 1>;  // TR = TO, TC = 4
 
   const int O = a.O;
-  const int band = blockIdx.y;
+  // widest bands (highest index in the usual layouts) first: their long K loops start at once
+  // instead of forming the tail
+  const int band = a.NB - 1 - static_cast<int>(blockIdx.y);
   const int oc = blockIdx.z * OT;
   const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBM;
   const int off = static_cast<int>(a.offsets[band]);
@@ -169,34 +173,72 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
   }
   __syncthreads();
 
+  if (a.ovec8) {
+    // epilogue through LDS: lane holds 4 consecutive outputs of one row (8-byte runs of 16 rows
+    // per instruction); the tile is staged as [64 m][OT o] (row pitch OT + 8 elements) and
+    // written back as 16-byte pieces, 2 OT contiguous bytes per row, so HBM sees whole lines
+    constexpr int kOP = OT + 8;
+    T* ot = lds;  // the main loop's buffers are free after its last barrier
 #pragma unroll
-  for (int t = 0; t < S::kTR; ++t) {
-    const int o = oc + wave * 16 * TO + t * 16 + 4 * (lane >> 4);
-    if (o >= O) continue;
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (bias != nullptr) {
-      if (a.ovec4) {
-        load_pack<T, 4>(bias + static_cast<int64_t>(band) * O + o, bv);
-      } else {
-        for (int r = 0; r < 4 && o + r < O; ++r) bv[r] = to_f32(bias[static_cast<int64_t>(band) * O + o + r]);
+    for (int t = 0; t < S::kTR; ++t) {
+      const int ol = wave * 16 * TO + t * 16 + 4 * (lane >> 4);
+      const int o = oc + ol;
+      if (o >= O) continue;
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias != nullptr) load_pack<T, 4>(bias + static_cast<int64_t>(band) * O + o, bv);
+#pragma unroll
+      for (int j = 0; j < S::kTC; ++j) {
+        const int m = j * 16 + (lane & 15);
+        const float s = sscale[m];
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          v[r] = acc[t][j][r] * s + bv[r];
+          if (ACT == PMSST_ACT_TANH) v[r] = tanhf(v[r]);
+        }
+        store_pack<T, 4>(ot + m * kOP + ol, v);
       }
     }
+    __syncthreads();
+    const int ov = O - oc < OT ? O - oc : OT;  // valid outputs of this tile (a multiple of 8)
+    const int pieces = kBM * (ov / 8);
+    for (int q = tid; q < pieces; q += kGemmThreads) {
+      const int m = q / (ov / 8);
+      const int c = (q - m * (ov / 8)) * 8;
+      if (m < rows_valid)
+        *reinterpret_cast<u32x4_t*>(out + ((m0 + m) * a.NB + band) * O + oc + c) =
+            *reinterpret_cast<const u32x4_t*>(ot + m * kOP + c);
+    }
+  } else {
 #pragma unroll
-    for (int j = 0; j < S::kTC; ++j) {
-      const int m = j * 16 + (lane & 15);
-      if (m >= rows_valid) continue;
-      const float s = sscale[m];
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        v[r] = acc[t][j][r] * s + bv[r];
-        if (ACT == PMSST_ACT_TANH) v[r] = tanhf(v[r]);
+    for (int t = 0; t < S::kTR; ++t) {
+      const int o = oc + wave * 16 * TO + t * 16 + 4 * (lane >> 4);
+      if (o >= O) continue;
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias != nullptr) {
+        if (a.ovec4) {
+          load_pack<T, 4>(bias + static_cast<int64_t>(band) * O + o, bv);
+        } else {
+          for (int r = 0; r < 4 && o + r < O; ++r) bv[r] = to_f32(bias[static_cast<int64_t>(band) * O + o + r]);
+        }
       }
-      T* dst = out + ((m0 + m) * a.NB + band) * O + o;
-      if (a.ovec4) {
-        store_pack<T, 4>(dst, v);
-      } else {
-        for (int r = 0; r < 4 && o + r < O; ++r) dst[r] = from_f32<T>(v[r]);
+#pragma unroll
+      for (int j = 0; j < S::kTC; ++j) {
+        const int m = j * 16 + (lane & 15);
+        if (m >= rows_valid) continue;
+        const float s = sscale[m];
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          v[r] = acc[t][j][r] * s + bv[r];
+          if (ACT == PMSST_ACT_TANH) v[r] = tanhf(v[r]);
+        }
+        T* dst = out + ((m0 + m) * a.NB + band) * O + o;
+        if (a.ovec4) {
+          store_pack<T, 4>(dst, v);
+        } else {
+          for (int r = 0; r < 4 && o + r < O; ++r) dst[r] = from_f32<T>(v[r]);
+        }
       }
     }
   }
@@ -288,11 +330,11 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
   if (SPLIT) {
     uint32_t grp, mt;
     if (!xcd_block(xg, grp, mt)) return;
-    band = static_cast<int>(grp) / max_ichunks;
+    band = a.NB - 1 - static_cast<int>(grp) / max_ichunks;  // widest bands first
     ichunk = static_cast<int>(grp) % max_ichunks;
     mtile = mt;
   } else {
-    band = static_cast<int>(blockIdx.y);
+    band = a.NB - 1 - static_cast<int>(blockIdx.y);
     ichunk = 0;
     mtile = blockIdx.x;
   }
@@ -534,10 +576,11 @@ int launch_fwd(const void* x, int64_t x_stride, const void* gamma, const void* w
   PMSST_REQUIRE(x_stride >= hb.F, "%s: x row stride %lld < total features %d", op, (long long)x_stride, hb.F);
   PMSST_REQUIRE(gemm_stride_ok(x_stride, sizeof(T)) && gemm_stride_ok(int64_t{hb.NB} * O, sizeof(T)),
                 "%s: rows too long for 32-bit tile offsets", op);
-  BandArgs a{offsets, M, hb.NB, hb.F, x_stride, static_cast<int>(O), false, false};
+  BandArgs a{offsets, M, hb.NB, hb.F, x_stride, static_cast<int>(O), false, false, false};
   a.vec4 = hb.vec4 && x_stride % 4 == 0 && aligned_to(x, 4 * sizeof(T)) && aligned_to(normed, 4 * sizeof(T)) &&
            aligned_to(weight, 4 * sizeof(T));
   a.ovec4 = O % 4 == 0 && aligned_to(out, 4 * sizeof(T)) && aligned_to(bias, 4 * sizeof(T));
+  a.ovec8 = sizeof(T) == 2 && a.ovec4 && O % 8 == 0 && aligned_to(out, 16);
   const int cap = 64 * tile_capacity(O);
   const dim3 grid(static_cast<unsigned>((M + kBM - 1) / kBM), static_cast<unsigned>(hb.NB),
                   static_cast<unsigned>((O + cap - 1) / cap));
@@ -604,7 +647,7 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   if (workspace == nullptr || workspace_bytes < need) {
     return fail(PMSST_EWORKSPACE, "%s: workspace of %zu bytes needed", op, need);
   }
-  BandArgs a{offsets, M, hb.NB, hb.F, hb.F, static_cast<int>(O), false, false};
+  BandArgs a{offsets, M, hb.NB, hb.F, hb.F, static_cast<int>(O), false, false, false};
   a.vec4 = hb.vec4 && aligned_to(nsrc, 4 * sizeof(T)) && aligned_to(dx, 4 * sizeof(T)) &&
            aligned_to(weight, 4 * sizeof(T)) && aligned_to(dw, 4 * sizeof(T));
   a.ovec4 = O % 4 == 0 && aligned_to(dy, 4 * sizeof(T));
@@ -692,7 +735,7 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
   if (db != nullptr && (workspace == nullptr || workspace_bytes < need)) {
     return fail(PMSST_EWORKSPACE, "%s: workspace of %zu bytes needed", op, need);
   }
-  BandArgs a{offsets, M, hb.NB, hb.F, hb.F, static_cast<int>(O), false, false};
+  BandArgs a{offsets, M, hb.NB, hb.F, hb.F, static_cast<int>(O), false, false, false};
   a.vec4 = hb.vec4 && aligned_to(x, 4 * sizeof(T)) && aligned_to(dx, 4 * sizeof(T)) &&
            aligned_to(weight, 4 * sizeof(T)) && aligned_to(dw, 4 * sizeof(T));
   a.ovec4 = O % 4 == 0 && aligned_to(dy, 4 * sizeof(T));
