@@ -213,7 +213,8 @@ int pmsst_grouped_linear_backward(const void* grad_out, const void* x, const voi
 int pmsst_mask_estimator_final_forward(const void* x, const void* weight, const void* bias,
                                        const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
                                        int64_t rows, int64_t hidden, void* pre, void* out, int dtype, void* stream);
-/* Workspace bytes of the backward: the [rows, 2*total] GLU derivative plus reduction partials. */
+/* Workspace bytes of the backward: the [rows, 2*total] GLU derivative (0 when rows == 0; a
+ * zero-byte workspace may be null). */
 size_t pmsst_mask_estimator_final_backward_workspace_size(int64_t rows, int64_t total, int dtype);
 /* fused_band_split.cpp:624-658 mask_estimator_final_backward and :695-729
  * mask_estimator_final_direct_backward (.cu:2312-2367, 2585-2851): grad_out[rows, F] ->

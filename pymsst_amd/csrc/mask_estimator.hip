@@ -751,6 +751,184 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __rest
   }
 }
 
+// dW on the DMA ring (16-bit, 4-aligned widths, H % 128 == 0): dW_b^T[h][j] =
+// sum_m x[m][b][h] dpre[m][2 off + j], K = M.  Tile 128 h x 128 j per block (band, hidden
+// tile, j chunk); both operands are moved as stored (32 K-rows m x 128 columns, 8 KB each) and
+// read as transposed fragments, so each x row slab is re-read once per 128 columns of dpre
+// instead of once per 64.  K chunks end at M; chunk 0's rows m < 0 are read from row 0 and
+// zeroed in LDS once the DMA has landed.  DMA: 16 dwordx4 per stage, wave w moves x K-rows
+// 4w .. + 3 and 16 + 4w .. + 3 and the same dpre K-rows.  dbias[j] = sum_m dpre[m][j] comes
+// from the blocks of hidden tile 0: their two top waves add 4 MFMAs per chunk with an all-ones
+// A fragment.  The tile leaves through LDS: rows j of dW_b, 256 contiguous bytes each.  Three
+// stages (48 KB) let three blocks share a CU.
+#ifndef PMSST_ME_DW_DMA
+#define PMSST_ME_DW_DMA 1
+#endif
+#ifndef PMSST_ME_DW_STAGES
+#define PMSST_ME_DW_STAGES 3
+#endif
+constexpr int kDwStage = 16384;
+constexpr int kDwT = 128;  // hidden and j columns per block
+
+template <typename T>
+__global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_dma_kernel(const T* __restrict__ dpre,
+                                                                     const T* __restrict__ x, T* __restrict__ dw,
+                                                                     T* __restrict__ dbias, BandSched sc,
+                                                                     MaskArgs a) {
+  constexpr int S = PMSST_ME_DW_STAGES;
+  static_assert(S >= 3 && S <= 8, "stages");
+  __shared__ __attribute__((aligned(1024))) char lds[S * kDwStage];
+  int band;
+  uint32_t mt0, sub, per_unit;
+  if (!sched_block(sc, band, mt0, sub, per_unit)) return;
+  const int H = a.H;
+  const int htiles = H / kDwT;
+  const int h0 = static_cast<int>(sub % htiles) * kDwT;
+  const int j0 = static_cast<int>(sub / htiles) * kDwT;
+  const int off = static_cast<int>(a.offsets[band]);
+  const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  const int K2 = 2 * I;
+  const int M = static_cast<int>(a.M);
+  const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
+  const int64_t xstride = static_cast<int64_t>(a.NB) * H;  // elements between rows m of x
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int wr = wave >> 1, wc = wave & 1;
+  const int nk = (M + kChunkK - 1) / kChunkK;
+  const int kbeg = M - nk * kChunkK;
+
+  // DMA pieces: t = 0, 1 -> K-row kr[t] of both tiles; x unit ua, dpre unit ub (clamped to the
+  // band's last 8 columns past 2 I)
+  uint32_t aoff[2], aoff0[2], boff[2], boff0[2];
+  bool ok0[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int kr = 4 * (wave + 4 * t) + (lane >> 4);
+    const int u = (lane & 15) ^ swz_mn(kr);
+    const int jc = j0 + 8 * u < K2 ? j0 + 8 * u : K2 - 8;
+    aoff[t] = static_cast<uint32_t>((kr * xstride + 8 * u) * 2);
+    boff[t] = static_cast<uint32_t>((kr * pitch2 + jc) * 2);
+    ok0[t] = kbeg + kr >= 0;
+    aoff0[t] = ok0[t] ? aoff[t] : static_cast<uint32_t>((-kbeg * xstride + 8 * u) * 2);  // row m = 0
+    boff0[t] = ok0[t] ? boff[t] : static_cast<uint32_t>((-kbeg * pitch2 + jc) * 2);
+  }
+  const char* xsrc0 = reinterpret_cast<const char*>(x + (static_cast<int64_t>(kbeg) * a.NB + band) * H + h0);
+  const char* dsrc0 = reinterpret_cast<const char*>(dpre + static_cast<int64_t>(kbeg) * pitch2 + 2 * off);
+  const uint32_t lds0 = lds_addr(lds);
+
+  auto dma = [&](int kc, int stage) {  // K chunk kc into `stage`
+    const char* xs = xsrc0 + static_cast<int64_t>(kc) * kChunkK * xstride * 2;
+    const char* ds = dsrc0 + static_cast<int64_t>(kc) * kChunkK * pitch2 * 2;
+    char* st = lds + stage * kDwStage;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      __builtin_amdgcn_global_load_lds(xs + (kc == 0 ? aoff0[t] : aoff[t]), st + (wave + 4 * t) * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(ds + (kc == 0 ? boff0[t] : boff[t]), st + 8192 + (wave + 4 * t) * 1024, 16,
+                                       0, 0);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) dma(s, s);
+
+  uint32_t fa[4], fb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    fa[i] = frag_mn_addr(lds0, 64 * wr + 16 * i, 2 * kDwT, lane);
+    fb[i] = frag_mn_addr(lds0 + 8192, 64 * wc + 16 * i, 2 * kDwT, lane);
+  }
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // dbias = ones^T dpre: the two waves of the first hidden tile's top half also multiply their
+  // dpre fragments by an all-ones A fragment (every row of the product is the column sum)
+  const bool do_bias = h0 == 0 && wr == 0;
+  const uint32_t one2 = std::is_same<T, bf16>::value ? 0x3F803F80u : 0x3C003C00u;
+  const u32x4_t ones{one2, one2, one2, one2};
+  f32x4_t accb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) accb[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int s = 0; s < nk; ++s) {
+    // chunk s landed once at most 4 nd DMAs are outstanding, nd = chunks issued after it
+    const int nd = nk - 1 - s < S - 2 ? nk - 1 - s : S - 2;
+    static_assert(S - 2 <= 6, "wait table");
+    switch (nd) {
+      case 0: vm_wait<0>(); break;
+      case 1: vm_wait<4>(); break;
+      case 2: vm_wait<8>(); break;
+      case 3: vm_wait<12>(); break;
+      case 4: vm_wait<16>(); break;
+      case 5: vm_wait<20>(); break;
+      default: vm_wait<24>(); break;
+    }
+    if (s == 0 && kbeg < 0) {
+      const u32x4_t z{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        if (!ok0[t]) {
+          *reinterpret_cast<u32x4_t*>(lds + (wave + 4 * t) * 1024 + lane * 16) = z;
+          *reinterpret_cast<u32x4_t*>(lds + 8192 + (wave + 4 * t) * 1024 + lane * 16) = z;
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (s + S - 1 < nk) dma(s + S - 1, (s + S - 1) % S);  // into the stage chunk s - 1 used
+    const uint32_t so = static_cast<uint32_t>((s % S) * kDwStage);
+    u32x4_t af[4], bfr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = lds_read_tr_pair(fa[i] + so, 4 * 2 * kDwT);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bfr[j] = lds_read_tr_pair(fb[j] + so, 4 * 2 * kDwT);
+    lds_wait(af, bfr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma_raw<T>(af[i], bfr[j], acc[i][j]);
+    if (do_bias) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) accb[j] = mfma_raw<T>(ones, bfr[j], accb[j]);
+    }
+  }
+
+  const int jv = K2 - j0 < kDwT ? K2 - j0 : kDwT;
+  if (do_bias && lane < 16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int jj = 64 * wc + 16 * j + lane;
+      if (jj < jv) dbias[2 * off + j0 + jj] = from_f32<T>(accb[j][0]);
+    }
+  }
+
+  // epilogue through LDS: lane holds h = 64 wr + 16 i + 4 (lane / 16) + r of columns
+  // j = 64 wc + 16 jj + lane % 16; staged as [128 j][128 h] (row pitch 272 bytes)
+  __syncthreads();  // every wave is done with the ring (its last wait was vmcnt(0))
+  constexpr int kOP = kDwT + 8;
+  T* ot = reinterpret_cast<T*>(lds);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int jj = 64 * wc + 16 * j + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      store_pack<T, 4>(ot + jj * kOP + 64 * wr + 16 * i + 4 * (lane >> 4), v);
+    }
+  }
+  __syncthreads();
+  T* dwb = dw + (static_cast<int64_t>(2) * off + j0) * H + h0;  // rows j of dW_b
+  const int c8 = (threadIdx.x & 15) * 8;
+#pragma unroll
+  for (int p = 0; p < kDwT / 16; ++p) {
+    const int jj = static_cast<int>(threadIdx.x >> 4) + 16 * p;
+    if (jj < jv)
+      *reinterpret_cast<u32x4_t*>(dwb + static_cast<int64_t>(jj) * H + c8) =
+          *reinterpret_cast<const u32x4_t*>(ot + jj * kOP + c8);
+  }
+}
+
 // ------------------------------------------------------------------ host side
 
 struct HostMask {
@@ -835,7 +1013,7 @@ int launch_me_fwd(const void* x, const void* weight, const void* bias, const int
 
 size_t me_bwd_workspace(int64_t M, int F, size_t elem) {
   const size_t dpre = align_up(static_cast<size_t>(M) * 2 * static_cast<size_t>(F) * elem, 256);
-  return dpre + colsum_rows_workspace(M, 2 * static_cast<int64_t>(F));
+  return dpre;
 }
 
 template <typename T>
@@ -848,7 +1026,7 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
                 input_act);
   PMSST_REQUIRE(weight && offsets && dbias && dw && (M == 0 || (gout && x && pre && dx)), "%s: null pointer", op);
   const size_t need = me_bwd_workspace(M, hm.F, sizeof(T));
-  if (workspace == nullptr || workspace_bytes < need) {
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     return fail(PMSST_EWORKSPACE, "%s: workspace of %zu bytes needed, got %zu", op, need,
                 workspace == nullptr ? size_t{0} : workspace_bytes);
   }
@@ -856,8 +1034,6 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
   a.vec4 = hm.vec4 && al(x, 4 * sizeof(T)) && al(weight, 4 * sizeof(T)) && al(pre, 4 * sizeof(T)) &&
            al(dx, 4 * sizeof(T)) && al(gout, 4 * sizeof(T)) && al(dw, 4 * sizeof(T));
   T* dpre = static_cast<T*>(workspace);
-  float* partial = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                            align_up(static_cast<size_t>(M) * 2 * hm.F * sizeof(T), 256));
   if (M > 0) {
     const dim3 g1(static_cast<unsigned>((M + kDpreRows - 1) / kDpreRows), static_cast<unsigned>(hm.NB));
     if (a.vec4 && hm.NB < kDpreFlatMaxBands && hm.F / 4 <= kDpreFlatMaxQuads) {
@@ -913,6 +1089,21 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
       if (rc != PMSST_OK) return rc;
     }
   }
+  if constexpr (sizeof(T) == 2) {
+    BandSched wsc;
+    uint32_t dw_per_xcd = 0;
+    const int htl = static_cast<int>(H / kDwT);
+    if (PMSST_ME_DW_DMA && M >= kChunkK && a.vec4 && H % kDwT == 0 && al(x, 16) && al(dw, 16) &&
+        (static_cast<int64_t>(kChunkK) * hm.NB * H + H) * 2 < (int64_t{1} << 31) &&
+        (static_cast<int64_t>(kChunkK) * 2 * hm.F + 2 * hm.F) * 2 < (int64_t{1} << 31) &&
+        build_band_sched(hm.NB, 1,
+                         [&](int b) { return static_cast<int64_t>(htl) * ((2 * dim_inputs[b] + kDwT - 1) / kDwT); },
+                         &wsc, &dw_per_xcd)) {
+      hipLaunchKernelGGL((me_bwd_dw_dma_kernel<T>), dim3(dw_per_xcd * kXcds), dim3(kGemmThreads), 0, stream, dpre,
+                         static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(dbias), wsc, a);
+      return check_launch("me_bwd_dw_dma_kernel");  // dbias summed by the kernel
+    }
+  }
   const int max_jchunks = (2 * hm.max_width + kDwBJ - 1) / kDwBJ;
   const int htiles = static_cast<int>((H + kDwBH - 1) / kDwBH);
   const XcdGrid xg3{static_cast<uint32_t>(hm.NB * htiles), static_cast<uint32_t>(max_jchunks)};
@@ -926,7 +1117,6 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
   int rc = check_launch("me_bwd_dw_kernel");
   if (rc != PMSST_OK) return rc;
   // dbias was summed by the dW kernel (which also runs for M == 0 and then writes zeros)
-  (void)partial;
   return PMSST_OK;
 }
 

@@ -33,28 +33,41 @@ __global__ __launch_bounds__(kColsPerBlock* kGroups) void col_sum_kernel(const f
   if (grp == 0 && c < dim) out[c] = from_f32<TO>(red[0][cl]);
 }
 
-// partial[blockIdx.y][c] = sum of src[r][c] over the block's 64 rows; 4 columns per thread.
+// partial[pb][c] = sum of src[r][c] over row block pb (kColsumRowBlock rows, ascending), for
+// row blocks pb = blockIdx.y, blockIdx.y + gridDim.y, ...; 4 columns per thread.  A whole row
+// block issues all its loads before the first add.
 template <typename T>
 __global__ __launch_bounds__(256) void colsum_rows_kernel(const T* __restrict__ src, int64_t rows, int64_t cols,
                                                           bool vec4, float* __restrict__ partial) {
   const int64_t c = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (c >= cols) return;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kColsumRowBlock;
-  const int64_t r1 = r0 + kColsumRowBlock < rows ? r0 + kColsumRowBlock : rows;
-  float s[4] = {0.f, 0.f, 0.f, 0.f};
-  if (vec4 && c + 4 <= cols) {
-    for (int64_t r = r0; r < r1; ++r) {
-      float v[4];
-      load_pack<T, 4>(src + r * cols + c, v);
+  const int64_t parts = (rows + kColsumRowBlock - 1) / kColsumRowBlock;
+  for (int64_t pb = blockIdx.y; pb < parts; pb += gridDim.y) {
+    const int64_t r0 = pb * kColsumRowBlock;
+    const int64_t r1 = r0 + kColsumRowBlock < rows ? r0 + kColsumRowBlock : rows;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    if (vec4 && c + 4 <= cols && r1 - r0 == kColsumRowBlock) {
+      float v[kColsumRowBlock][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) s[j] += v[j];
+      for (int r = 0; r < kColsumRowBlock; ++r) load_pack<T, 4>(src + (r0 + r) * cols + c, v[r]);
+#pragma unroll
+      for (int r = 0; r < kColsumRowBlock; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] += v[r][j];
+    } else if (vec4 && c + 4 <= cols) {
+      for (int64_t r = r0; r < r1; ++r) {
+        float v[4];
+        load_pack<T, 4>(src + r * cols + c, v);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] += v[j];
+      }
+    } else {
+      for (int64_t r = r0; r < r1; ++r)
+        for (int j = 0; j < 4 && c + j < cols; ++j) s[j] += to_f32(src[r * cols + c + j]);
     }
-  } else {
-    for (int64_t r = r0; r < r1; ++r)
-      for (int j = 0; j < 4 && c + j < cols; ++j) s[j] += to_f32(src[r * cols + c + j]);
+    float* dst = partial + pb * cols + c;
+    for (int j = 0; j < 4 && c + j < cols; ++j) dst[j] = s[j];
   }
-  float* dst = partial + static_cast<int64_t>(blockIdx.y) * cols + c;
-  for (int j = 0; j < 4 && c + j < cols; ++j) dst[j] = s[j];
 }
 
 }  // namespace
@@ -63,11 +76,11 @@ int launch_colsum_rows(const void* src, int src_dtype, int64_t rows, int64_t col
                        int out_dtype, hipStream_t stream) {
   PMSST_REQUIRE(cols > 0 && cols < (int64_t{1} << 31) && rows >= 0, "colsum_rows: bad shape");
   const int64_t parts = (rows + kColsumRowBlock - 1) / kColsumRowBlock;
-  PMSST_REQUIRE(parts < 65536, "colsum_rows: too many rows");
+  PMSST_REQUIRE(parts < (int64_t{1} << 31), "colsum_rows: too many rows");
   if (parts > 0) {
     const size_t esz = src_dtype == PMSST_F32 ? 4 : 2;
     const bool vec4 = cols % 4 == 0 && reinterpret_cast<uintptr_t>(src) % (4 * esz) == 0;
-    const dim3 grid(static_cast<unsigned>((cols + 1023) / 1024), static_cast<unsigned>(parts));
+    const dim3 grid(static_cast<unsigned>((cols + 1023) / 1024), static_cast<unsigned>(parts < 65535 ? parts : 65535));
     switch (src_dtype) {
       case PMSST_F32:
         hipLaunchKernelGGL(colsum_rows_kernel<float>, grid, dim3(256), 0, stream, static_cast<const float*>(src),

@@ -60,9 +60,9 @@ inline size_t row_bwd_workspace(int64_t dim) {
 int launch_col_sum(const float* partial, int parts, int dim, void* out, int out_dtype, hipStream_t stream);
 
 // Column sums of a row-major src[rows, cols] (storage `src_dtype`) into out[cols]
-// (`out_dtype`): fp32 partials per 64-row block in `partial` (colsum_rows_workspace
+// (`out_dtype`): fp32 partials per 16-row block in `partial` (colsum_rows_workspace
 // bytes), then launch_col_sum.  Deterministic.
-constexpr int kColsumRowBlock = 64;
+constexpr int kColsumRowBlock = 16;
 inline size_t colsum_rows_workspace(int64_t rows, int64_t cols) {
   const int64_t parts = (rows + kColsumRowBlock - 1) / kColsumRowBlock;
   return static_cast<size_t>(parts > 0 ? parts : 1) * static_cast<size_t>(cols) * sizeof(float);
