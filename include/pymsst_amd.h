@@ -158,7 +158,8 @@ int pmsst_band_split_ragged_forward(const void* x, int64_t x_row_stride, const v
                                     const void* bias, const int64_t* dim_offsets, const int64_t* dim_inputs,
                                     int64_t band_count, int64_t rows, int64_t out_features, void* out, void* normed,
                                     float* inv_norm, int dtype, void* stream);
-/* Workspace bytes of the backward (dgamma / dbias reduction partials). */
+/* Workspace bytes of the backward: per-row-tile dgamma partials and the per-(row, band) dots
+ * (0 when rows == 0; a zero-byte workspace may be null). */
 size_t pmsst_band_split_ragged_backward_workspace_size(int64_t rows, int64_t total_in, int64_t band_count,
                                                        int64_t out_features);
 /* fused_band_split.cpp:316-363 band_split_ragged_backward (.cu:741-1003).  With equal widths it also

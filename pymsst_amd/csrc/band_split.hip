@@ -23,10 +23,22 @@
 // writes dx.  dW block (band, 64 i x 64 o): dW^T[i][o] = sum_m n[m][i] gamma_i
 // dy[m][o], K = M.  dbias = column sums of dy.  No atomics anywhere.
 #include "common.h"
+#include "dma_gemm.h"
 #include "gemm.h"
 #include "rowgeom.h"
 
 #include <vector>
+
+// K-loop prefetch depth (chunks in registers ahead of the one in use) of each kernel
+#ifndef PMSST_BS_FWD_DEPTH
+#define PMSST_BS_FWD_DEPTH 2
+#endif
+#ifndef PMSST_BS_DX_DEPTH
+#define PMSST_BS_DX_DEPTH 1
+#endif
+#ifndef PMSST_BS_DW_DEPTH
+#define PMSST_BS_DW_DEPTH 1
+#endif
 
 namespace pmsst {
 namespace {
@@ -157,7 +169,7 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
   for (int i = 0; i < S::kTR; ++i)
 #pragma unroll
     for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  gemm_mainloop<T, OT, kBM, 4, 1>(la, lb, I, lds, acc);
+  gemm_mainloop<T, OT, kBM, 4, 1, PMSST_BS_FWD_DEPTH>(la, lb, I, lds, acc);
 
   const float root = sqrtf(static_cast<float>(I));
   const float ss0 = group_sum(lb.ss[0], 8);
@@ -383,7 +395,7 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
       f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[0][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      gemm_mainloop<T, kBI, kBM, 4, 1>(la, lb, O, lds, acc);
+      gemm_mainloop<T, kBI, kBM, 4, 1, PMSST_BS_DX_DEPTH>(la, lb, O, lds, acc);
 
       // lane holds gs[m = 16 j + (lane & 15)][i = i0 + 16 wave + 4 (lane >> 4) + r]
       const int il = i0 + wave * 16 + 4 * (lane >> 4);
@@ -502,7 +514,7 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
   for (int i = 0; i < S::kTR; ++i)
 #pragma unroll
     for (int j = 0; j < S::kTC; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  gemm_mainloop<T, kDwBI, kDwBO, 2, 2>(la, lb, static_cast<int>(a.M), lds, acc);
+  gemm_mainloop<T, kDwBI, kDwBO, 2, 2, PMSST_BS_DW_DEPTH>(la, lb, static_cast<int>(a.M), lds, acc);
   if (lb.colsum) reduce_colsum<T, kDwBO, V4>(lb, lds, db + static_cast<int64_t>(band) * O + o0);
 
   T* dwb = dw + static_cast<int64_t>(O) * off;  // [O][I]
@@ -523,6 +535,276 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
         for (int r = 0; r < 4 && i + r < I; ++r) dst[r] = from_f32<T>(e[r]);
       }
     }
+  }
+}
+
+// ------------------------------------------------------------------ backward: dW on the DMA ring
+// 16-bit, 4-aligned widths, O % 8 == 0:
+//   dW_b^T[i][o] = gamma_i s_b sum_m n'[m][i] dy[m][b][o],
+// n' = x * inv with s_b = sqrt(I_b) from the saved input (FROM_X), n' = normed with s_b = 1.
+// Block = (band, 64-wide input tile, 64-wide output tile); K = the rows, walked in steps of
+// KR = 32 KS rows.  Both operands move as stored (KR rows x 64 columns each
+// per step) into a ring of S LDS stages: x by 4-byte DMA (its rows are only 8-byte aligned), dy
+// by 16-byte DMA; both are read as transposed fragments (ds_read_b64_tr_b16, swz_mn swizzle).
+// Wave w moves rows KR/4 w .. + KR/4 - 1 of both tiles.  From the saved input each landed x tile
+// is scaled by inv in LDS (KS 16-byte units per thread, of its own wave's rows; inv of the
+// block's rows sits in LDS in windows of kBdWinRows rows).  Columns past the band or past O are
+// clamped reads whose products land in discarded outputs; step 0's rows before the range start
+// are read from its first row and zeroed.  dbias: the two top waves of input tile 0 also
+// multiply their dy fragments by an all-ones A fragment (every row of that product is the
+// column sum).  The tile leaves through LDS as rows o of dW_b.
+constexpr int kBdT = 64;
+constexpr int kBdWinRows = 2048;
+#ifndef PMSST_BS_DW_DMA
+#define PMSST_BS_DW_DMA 1
+#endif
+#ifndef PMSST_BS_DWD_STAGES
+#define PMSST_BS_DWD_STAGES 3
+#endif
+#ifndef PMSST_BS_DWD_KS
+#define PMSST_BS_DWD_KS 2
+#endif
+
+template <typename T>
+__device__ __forceinline__ u32x4_t scale8(const u32x4_t& v, float sc) {
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  const v8 e = __builtin_bit_cast(v8, v);
+  v8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = static_cast<T>(static_cast<float>(e[j]) * sc);
+  return __builtin_bit_cast(u32x4_t, r);
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait_steps(int nd) {  // at most N nd DMAs outstanding, nd <= 6
+  switch (nd) {
+    case 0: vm_wait<0>(); break;
+    case 1: vm_wait<N>(); break;
+    case 2: vm_wait<2 * N>(); break;
+    case 3: vm_wait<3 * N>(); break;
+    case 4: vm_wait<4 * N>(); break;
+    case 5: vm_wait<5 * N>(); break;
+    default: vm_wait<6 * N>(); break;
+  }
+}
+
+template <typename T, bool FROM_X>
+__global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_dma_kernel(
+    const T* __restrict__ dy, const T* __restrict__ nsrc, const float* __restrict__ inv_norm,
+    const T* __restrict__ gamma, T* __restrict__ dw, T* __restrict__ db, BandSched sc, BandArgs a, int otiles) {
+  constexpr int S = PMSST_BS_DWD_STAGES;
+  constexpr int KS = PMSST_BS_DWD_KS;
+  constexpr int KR = KS * kChunkK;             // rows per step
+  constexpr int kTile = KR * 2 * kBdT;          // bytes of one operand tile
+  constexpr int kStage = 2 * kTile;
+  constexpr int kWR = KR / 4;                   // rows per wave
+  constexpr int kXI = kWR / 2;                  // 4-byte x DMAs per wave and step
+  constexpr int kDI = kWR / 8;                  // 16-byte dy DMAs per wave and step
+  constexpr int kWinSteps = kBdWinRows / KR;
+  static_assert(KS == 1 || KS == 2 || KS == 4, "rows per step");
+  static_assert(S >= 3 && (S - 2) <= 6 && (S - 2) * (kXI + kDI) <= 63, "stages (wait table)");
+  __shared__ __attribute__((aligned(1024))) char lds[S * kStage];
+  __shared__ float sinv[FROM_X ? kBdWinRows : 1];
+  int band;
+  uint32_t mt, sub, per_unit;
+  if (!sched_block(sc, band, mt, sub, per_unit)) return;
+  const int i0 = static_cast<int>(sub) / otiles * kBdT;
+  const int o0 = static_cast<int>(sub) % otiles * kBdT;
+  const int off = static_cast<int>(a.offsets[band]);
+  const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  const int O = a.O;
+  const int NB = a.NB;
+  const int K = static_cast<int>(a.M);
+  const int nk = (K + KR - 1) / KR;
+  const int kbeg = K - nk * KR;  // step c covers rows kbeg + KR c .. + KR - 1
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int wr = wave >> 1, wc = wave & 1;
+  const int64_t dstride = static_cast<int64_t>(NB) * O;  // elements between rows of dy
+  const int64_t xstride = a.F;
+
+  // DMA pieces.  dy instruction t: row kWR wave + 8 t + lane / 8, LDS unit lane % 8 <- unit
+  // (lane % 8) ^ swz_mn(row).  x instruction t: row kWR wave + 2 t + lane / 32, 4-byte word
+  // lane % 32 of the row: LDS unit (lane % 32) / 4 <- unit ((lane % 32) / 4) ^ swz_mn(row).
+  uint32_t doff[kDI], doff0[kDI], xoff[kXI], xoff0[kXI];
+#pragma unroll
+  for (int t = 0; t < kDI; ++t) {
+    const int r = kWR * wave + 8 * t + (lane >> 3);
+    int col = o0 + 8 * ((lane & 7) ^ swz_mn(r));
+    col = col <= O - 8 ? col : O - 8;
+    doff[t] = static_cast<uint32_t>((r * dstride + col) * 2);
+    doff0[t] = kbeg + r >= 0 ? doff[t] : static_cast<uint32_t>((-kbeg * dstride + col) * 2);
+  }
+#pragma unroll
+  for (int t = 0; t < kXI; ++t) {
+    const int r = kWR * wave + 2 * t + (lane >> 5);
+    int i = i0 + 8 * (((lane & 31) >> 2) ^ swz_mn(r)) + 2 * (lane & 3);
+    i = i <= I - 2 ? i : I - 2;
+    xoff[t] = static_cast<uint32_t>((r * xstride + i) * 2);
+    xoff0[t] = kbeg + r >= 0 ? xoff[t] : static_cast<uint32_t>((-kbeg * xstride + i) * 2);
+  }
+  const char* xsrc0 = reinterpret_cast<const char*>(nsrc + static_cast<int64_t>(kbeg) * xstride + off);
+  const char* dsrc0 = reinterpret_cast<const char*>(dy + (static_cast<int64_t>(kbeg) * NB + band) * O);
+  const uint32_t lds0 = lds_addr(lds);
+
+  auto dma = [&](int c, int stage) {  // step c into `stage`
+    const char* xs = xsrc0 + static_cast<int64_t>(c) * KR * xstride * 2;
+    const char* ds = dsrc0 + static_cast<int64_t>(c) * KR * dstride * 2;
+    char* st = lds + stage * kStage;
+#pragma unroll
+    for (int t = 0; t < kXI; ++t)
+      __builtin_amdgcn_global_load_lds(xs + (c == 0 ? xoff0[t] : xoff[t]), st + 128 * (kWR * wave + 2 * t), 4, 0,
+                                       0);
+#pragma unroll
+    for (int t = 0; t < kDI; ++t)
+      __builtin_amdgcn_global_load_lds(ds + (c == 0 ? doff0[t] : doff[t]), st + kTile + 128 * (kWR * wave + 8 * t),
+                                       16, 0, 0);
+  };
+  // inv of the rows of steps c0 .. c0 + kWinSteps - 1 (0 before row 0)
+  auto load_inv = [&](int c0) {
+    const int64_t r0 = kbeg + static_cast<int64_t>(c0) * KR;
+    const int64_t rows = static_cast<int64_t>(nk - c0) * KR;
+    const int n = static_cast<int>(rows < kBdWinRows ? rows : kBdWinRows);
+    for (int j = threadIdx.x; j < n; j += kGemmThreads) {
+      const int64_t rr = r0 + j;
+      sinv[j] = rr >= 0 ? inv_norm[rr * NB + band] : 0.f;
+    }
+  };
+  if constexpr (FROM_X) {
+    load_inv(0);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) dma(s, s);
+
+  uint32_t fa[2], fb[2];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    fa[f] = frag_mn_addr(0, 32 * wr + 16 * f, 2 * kBdT, lane);
+    fb[f] = frag_mn_addr(kTile, 32 * wc + 16 * f, 2 * kBdT, lane);
+  }
+  f32x4_t acc[2][2], accb[2];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    accb[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < 2; ++g) acc[f][g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const bool do_bias = db != nullptr && i0 == 0 && wr == 0;
+  const uint32_t one2 = std::is_same<T, bf16>::value ? 0x3F803F80u : 0x3C003C00u;
+  const u32x4_t ones{one2, one2, one2, one2};
+  // this thread's units of a tile (rows of its own wave): row kWR wave + 8 j + lane / 8, unit lane % 8
+  const int urow = kWR * wave + (lane >> 3);
+  const uint32_t uoff = static_cast<uint32_t>(urow * 2 * kBdT + 16 * (lane & 7));
+  const uint32_t sinv0 = lds_addr(sinv);
+
+  for (int s = 0; s < nk; ++s) {
+    // step s landed once at most (kXI + kDI) nd DMAs of this wave are outstanding
+    const int nd = nk - 1 - s < S - 2 ? nk - 1 - s : S - 2;
+    vm_wait_steps<kXI + kDI>(nd);
+    if (s == 0 && kbeg < 0) {
+      const u32x4_t z{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int j = 0; j < KS; ++j)
+        if (kbeg + urow + 8 * j < 0) {
+          lds_write_b128(lds0 + uoff + 8 * j * 128, z);
+          lds_write_b128(lds0 + kTile + uoff + 8 * j * 128, z);
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if constexpr (FROM_X) {
+      if (s > 0 && s % kWinSteps == 0) {  // next window of inv (every DMA in flight drains)
+        vm_wait<0>();
+        load_inv(s);
+        __syncthreads();
+      }
+    }
+    if (s + S - 1 < nk) dma(s + S - 1, (s + S - 1) % S);  // into the stage step s - 1 used
+    const uint32_t so = lds0 + static_cast<uint32_t>((s % S) * kStage);
+    if constexpr (FROM_X) {
+      u32x4_t v[KS];
+      float scl[KS];
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        v[j] = lds_read_b128(so + uoff + 8 * j * 128);
+        scl[j] = lds_read_f32(sinv0 + 4u * static_cast<uint32_t>((s % kWinSteps) * KR + urow + 8 * j));
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        asm volatile("" : "+v"(v[j]), "+v"(scl[j]));
+        lds_write_b128(so + uoff + 8 * j * 128, scale8<T>(v[j], scl[j]));
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      u32x4_t af[2], bfr[2];
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        af[f] = lds_read_tr_pair(so + fa[f] + kk * 32 * 128, 4 * 2 * kBdT);
+        bfr[f] = lds_read_tr_pair(so + fb[f] + kk * 32 * 128, 4 * 2 * kBdT);
+      }
+      lds_wait(af, bfr);
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int g = 0; g < 2; ++g) acc[f][g] = mfma_raw<T>(af[f], bfr[g], acc[f][g]);
+      if (do_bias) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) accb[g] = mfma_raw<T>(ones, bfr[g], accb[g]);
+      }
+    }
+  }
+
+  // lane holds i = 32 wr + 16 f + 4 (lane / 16) + r, o = 32 wc + 16 g + lane % 16 of the tile
+  const float sb = FROM_X ? sqrtf(static_cast<float>(I)) : 1.f;
+  float gsc[2][4];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const int i = i0 + 32 * wr + 16 * f + 4 * (lane >> 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {  // clamped loads outside any branch: issued together
+      const float gv = to_f32(gamma[off + (i + r < I ? i + r : I - 1)]);
+      gsc[f][r] = i + r < I ? gv * sb : 0.f;
+    }
+  }
+  if (do_bias && lane < 16) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int o = o0 + 32 * wc + 16 * g + lane;
+      if (o < O) db[static_cast<int64_t>(band) * O + o] = from_f32<T>(accb[g][0]);
+    }
+  }
+  const int64_t wbase = static_cast<int64_t>(O) * off;  // dW_b is [O][I]
+  // staged as [64 o][64 i] (row pitch 144 bytes), then rows o of dW_b, 8 bytes per lane
+  __syncthreads();  // every wave is done with the ring (its last wait was vmcnt(0))
+  constexpr int kOP = kBdT + 8;
+  static_assert(kBdT * kOP * 2 <= S * kStage, "staging tile");
+  T* ot = reinterpret_cast<T*>(lds);
+#pragma unroll
+  for (int f = 0; f < 2; ++f)
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = acc[f][g][r] * gsc[f][r];
+      store_pack<T, 4>(ot + (32 * wc + 16 * g + (lane & 15)) * kOP + 32 * wr + 16 * f + 4 * (lane >> 4), v);
+    }
+  __syncthreads();
+  const int iv = I - i0 < kBdT ? I - i0 : kBdT;
+  const int q = static_cast<int>(threadIdx.x & 15);
+#pragma unroll
+  for (int p = 0; p < kBdT / 16; ++p) {
+    const int ol = static_cast<int>(threadIdx.x >> 4) + 16 * p;
+    if (o0 + ol < O && 4 * q < iv)
+      *reinterpret_cast<u32x2_t*>(dw + wbase + static_cast<int64_t>(o0 + ol) * I + i0 + 4 * q) =
+          *reinterpret_cast<const u32x2_t*>(ot + ol * kOP + 4 * q);
   }
 }
 
@@ -626,14 +908,16 @@ size_t dg_partial_bytes(int64_t M, int F) {
 
 size_t dots_bytes(int64_t M, int NB) { return align_up(static_cast<size_t>(M) * NB * sizeof(float), 256); }
 
-// [dgamma partials | dots | dbias partials]
+// [dgamma partials | dots]
 size_t bwd_workspace(int64_t M, int F, int NB, int O) {
-  return dg_partial_bytes(M, F) + dots_bytes(M, NB) + colsum_rows_workspace(M, static_cast<int64_t>(NB) * O);
+  (void)O;
+  return dg_partial_bytes(M, F) + dots_bytes(M, NB);
 }
 
 template <typename T>
 int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_norm, const void* gamma,
-               const void* weight, const void* out, const void* bias, const int64_t* offsets, const HostBands& hb,
+               const void* weight, const void* out, const void* bias, const int64_t* offsets,
+               const int64_t* dim_inputs, const HostBands& hb,
                int64_t M, int64_t O, void* dx, void* dgamma, void* dw, void* db, void* workspace,
                size_t workspace_bytes, hipStream_t stream) {
   const char* op = "band_split_ragged_backward";
@@ -644,7 +928,7 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   PMSST_REQUIRE(gemm_stride_ok(hb.F, sizeof(T)) && gemm_stride_ok(int64_t{hb.NB} * O, sizeof(T)),
                 "%s: rows too long for 32-bit tile offsets", op);
   const size_t need = bwd_workspace(M, hb.F, hb.NB, static_cast<int>(O));
-  if (workspace == nullptr || workspace_bytes < need) {
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     return fail(PMSST_EWORKSPACE, "%s: workspace of %zu bytes needed", op, need);
   }
   BandArgs a{offsets, M, hb.NB, hb.F, hb.F, static_cast<int>(O), false, false, false};
@@ -657,7 +941,6 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   const T* pw = static_cast<const T*>(weight);
   float* partial = static_cast<float*>(workspace);
   float* dots = reinterpret_cast<float*>(static_cast<char*>(workspace) + dg_partial_bytes(M, hb.F));
-  float* db_partial = reinterpret_cast<float*>(reinterpret_cast<char*>(dots) + dots_bytes(M, hb.NB));
   const int m_tiles = static_cast<int>((M + kBM - 1) / kBM);
   if (M > 0) {
     const bool v4 = a.vec4 && a.ovec4;
@@ -698,7 +981,31 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
-  {
+  bool dw_done = false;
+  if constexpr (sizeof(T) == 2) {
+    // DMA-ring dW: 16-bit, 4-aligned widths and pointers, O % 8 == 0 with 16-byte aligned dy rows
+    constexpr int KR = PMSST_BS_DWD_KS * kChunkK;
+    const int otiles = static_cast<int>((O + kBdT - 1) / kBdT);
+    BandSched sc;
+    uint32_t per_xcd = 0;
+    if (PMSST_BS_DW_DMA && M >= KR && a.vec4 && O % 8 == 0 && aligned_to(dy, 16) &&
+        (static_cast<int64_t>(KR) * hb.F + hb.F) * 2 < (int64_t{1} << 31) &&
+        (static_cast<int64_t>(KR) * hb.NB * O + O) * 2 < (int64_t{1} << 31) &&
+        build_band_sched(hb.NB, 1, [&](int b) { return (dim_inputs[b] + kBdT - 1) / kBdT * otiles; }, &sc,
+                         &per_xcd)) {
+      const dim3 grid(per_xcd * kXcds);
+      if (from_x)
+        hipLaunchKernelGGL((bs_bwd_dw_dma_kernel<T, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
+                           pg, static_cast<T*>(dw), static_cast<T*>(db), sc, a, otiles);
+      else
+        hipLaunchKernelGGL((bs_bwd_dw_dma_kernel<T, false>), grid, dim3(kGemmThreads), 0, stream, pdy, pn,
+                           inv_norm, pg, static_cast<T*>(dw), static_cast<T*>(db), sc, a, otiles);
+      const int rc = check_launch("bs_bwd_dw_dma_kernel");
+      if (rc != PMSST_OK) return rc;
+      dw_done = true;
+    }
+  }
+  if (!dw_done) {
     const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
     const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_itiles), static_cast<uint32_t>((O + kDwBO - 1) / kDwBO)};
     const dim3 grid(xg.blocks());
@@ -715,8 +1022,7 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
     int rc = check_launch("bs_bwd_dw_kernel");
     if (rc != PMSST_OK) return rc;
   }
-  // dbias was summed by the dW kernel (which also runs for M == 0 and then writes zeros)
-  (void)db_partial;
+  // dbias was summed by the dW kernel (the fallback one also runs for M == 0 and then writes zeros)
   return launch_col_sum(partial, m_tiles, hb.F, dgamma, dtype_code<T>(), stream);
 }
 
@@ -860,7 +1166,8 @@ int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, in
   if (rc != PMSST_OK) return rc;
   return with_dtype(dtype, "band_split_ragged_backward", [&](auto tag) {
     using T = decltype(tag);
-    return launch_bwd<T>(grad_out, saved, saved_is_input != 0, inv_norm, gamma, weight, out, bias, dim_offsets, hb,
+    return launch_bwd<T>(grad_out, saved, saved_is_input != 0, inv_norm, gamma, weight, out, bias, dim_offsets,
+                         dim_inputs, hb,
                          rows, out_features, grad_x, grad_gamma, grad_weight, grad_bias, workspace, workspace_bytes,
                          static_cast<hipStream_t>(stream));
   });

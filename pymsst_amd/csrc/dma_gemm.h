@@ -69,6 +69,16 @@ __device__ __forceinline__ u32x4_t lds_read_b128(uint32_t addr) {
   return v;
 }
 
+__device__ __forceinline__ void lds_write_b128(uint32_t addr, const u32x4_t& v) {
+  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+
+__device__ __forceinline__ float lds_read_f32(uint32_t addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
 // ds_read_b64_tr_b16 at addr and addr + step (the two K halves of an MN fragment).
 __device__ __forceinline__ u32x4_t lds_read_tr_pair(uint32_t addr, uint32_t step) {
   u32x2_t lo, hi;
@@ -89,6 +99,8 @@ __device__ __forceinline__ void lds_wait(u32x4_t (&a)[NA], u32x4_t (&b)[NB]) {
                  : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
   else if constexpr (NA == 2 && NB == 4)
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+  else if constexpr (NA == 2 && NB == 2)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
   else
     static_assert(NA < 0, "add the operand list for this shape");
 }

@@ -89,10 +89,24 @@ def test_mel_style_widths(hip_ext, o):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_saved_input_backward(hip_ext, dtype):
+def test_odd_widths_long_rows(hip_ext, dtype):
+    # odd widths take the scalar (non-4-aligned) loads and stores of every kernel; 777 rows
+    r = np.random.default_rng(12)
+    widths = tuple(int(w) for w in r.integers(1, 90, size=13))
+    _check_ragged(hip_ext, widths, 777, 100, dtype, 13)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_long_rows_from_normed(hip_ext, dtype):
+    # 2500 rows, 40 outputs (O % 8 == 0, one ragged 64-wide output tile), from normed
+    _check_ragged(hip_ext, (4, 68, 200, 12), 2500, 40, dtype, 14)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("dims,m,o", [(BSR_WIDTHS, 300, 192), ((8, 64, 132, 4), 4500, 64)])
+def test_saved_input_backward(hip_ext, dtype, dims, m, o):
+    # 4500 rows: the 16-bit dW kernel stages inv for its rows in LDS windows of 2048 rows
     dn = dt_name(dtype)
-    dims = BSR_WIDTHS
-    m, o = 300, 192
     g = torch.Generator().manual_seed(21)
     x = (0.05 * torch.randn(m, sum(dims), generator=g)).to(dtype).cuda()
     gammas, weights, biases = _params(dims, o, dtype, 22)
