@@ -311,6 +311,41 @@ __global__ __launch_bounds__(256) void bs_dots_kernel(const T* __restrict__ dy, 
   if (l == 0 && row < rows) dots[row] = acc;
 }
 
+// The same dots for 16-bit rows with O % 8 == 0 and 16-byte aligned dy / out: 8 lanes per
+// (m, b) row, U 16-byte units of dy, out and bias per lane (O = 64 U), every load issued before the
+// first product (rows past the end are clamped reads whose sums are not stored).
+template <typename T, int U>
+__global__ __launch_bounds__(256) void bs_dots16_kernel(const T* __restrict__ dy, const T* __restrict__ out,
+                                                        const T* __restrict__ bias, float* __restrict__ dots,
+                                                        int64_t rows, int NB, int O) {
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / 8;
+  const int l = threadIdx.x & 7;
+  const int64_t rc = row < rows ? row : rows - 1;
+  const int b = static_cast<int>(rc % NB);
+  u32x4_t vd[U], vo[U], vb[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = 8 * (l + 8 * u);
+    const int cc = c < O ? c : O - 8;
+    vd[u] = *reinterpret_cast<const u32x4_t*>(dy + rc * O + cc);
+    vo[u] = *reinterpret_cast<const u32x4_t*>(out + rc * O + cc);
+    vb[u] = bias != nullptr ? *reinterpret_cast<const u32x4_t*>(bias + static_cast<int64_t>(b) * O + cc)
+                            : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const v8 d = __builtin_bit_cast(v8, vd[u]), o = __builtin_bit_cast(v8, vo[u]), c = __builtin_bit_cast(v8, vb[u]);
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) part += static_cast<float>(d[j]) * (static_cast<float>(o[j]) - static_cast<float>(c[j]));
+    acc += 8 * (l + 8 * u) < O ? part : 0.f;
+  }
+  acc = group_sum(acc, 8);
+  if (l == 0 && row < rows) dots[row] = acc;
+}
+
 // dx for one (64-row tile, band) block, or one (64-row tile, band, 64-wide input chunk)
 // block when SPLIT.  gs^T[i][m] = W_b^T dy^T per 64-wide input chunk (K = O), then
 //   NORM:  dx = inv (gs gamma sqrt(I) - n dot / sqrt(I)), dgamma partials sum_m gs n;
@@ -950,12 +985,36 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
       const bool dv4 = a.ovec4 && aligned_to(out, 4 * sizeof(T)) && aligned_to(bias, 4 * sizeof(T));
       const int64_t rows = M * hb.NB;
       const dim3 gd(static_cast<unsigned>((rows * 32 + 255) / 256));
-      if (dv4)
-        hipLaunchKernelGGL((bs_dots_kernel<T, true>), gd, dim3(256), 0, stream, pdy, static_cast<const T*>(out),
-                           static_cast<const T*>(bias), dots, rows, hb.NB, static_cast<int>(O));
-      else
-        hipLaunchKernelGGL((bs_dots_kernel<T, false>), gd, dim3(256), 0, stream, pdy, static_cast<const T*>(out),
-                           static_cast<const T*>(bias), dots, rows, hb.NB, static_cast<int>(O));
+      bool d16 = false;  // 16-bit rows, O % 8 == 0, 16-byte aligned: 8 lanes per row, 16-byte loads
+      if constexpr (sizeof(T) == 2) {
+        d16 = O % 8 == 0 && aligned_to(dy, 16) && aligned_to(out, 16) && aligned_to(bias, 16) &&
+              (rows * 8 + 255) / 256 < (int64_t{1} << 31);
+        if (d16) {
+          const dim3 g16(static_cast<unsigned>((rows * 8 + 255) / 256));
+#define PMSST_DOTS16(UU)                                                                                       \
+  hipLaunchKernelGGL((bs_dots16_kernel<T, UU>), g16, dim3(256), 0, stream, pdy, static_cast<const T*>(out), \
+                     static_cast<const T*>(bias), dots, rows, hb.NB, static_cast<int>(O))
+          switch ((O + 63) / 64) {
+            case 1: PMSST_DOTS16(1); break;
+            case 2: PMSST_DOTS16(2); break;
+            case 3: PMSST_DOTS16(3); break;
+            case 4: PMSST_DOTS16(4); break;
+            case 5: PMSST_DOTS16(5); break;
+            case 6: PMSST_DOTS16(6); break;
+            case 7: PMSST_DOTS16(7); break;
+            default: PMSST_DOTS16(8); break;
+          }
+#undef PMSST_DOTS16
+        }
+      }
+      if (!d16) {
+        if (dv4)
+          hipLaunchKernelGGL((bs_dots_kernel<T, true>), gd, dim3(256), 0, stream, pdy, static_cast<const T*>(out),
+                             static_cast<const T*>(bias), dots, rows, hb.NB, static_cast<int>(O));
+        else
+          hipLaunchKernelGGL((bs_dots_kernel<T, false>), gd, dim3(256), 0, stream, pdy, static_cast<const T*>(out),
+                             static_cast<const T*>(bias), dots, rows, hb.NB, static_cast<int>(O));
+      }
       int rc = check_launch("bs_dots_kernel");
       if (rc != PMSST_OK) return rc;
     }

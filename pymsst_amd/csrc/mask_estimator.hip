@@ -351,54 +351,53 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_dma_kernel(const T* __res
 // ------------------------------------------------------------------ backward
 
 constexpr int kDpreRows = 64;
-constexpr int kDpreFlatRows = 2;
-constexpr int kDpreFlatMaxBands = 4096;
-constexpr int kDpreFlatMaxQuads = 16384;  // LDS table <= 48 KB per block
+constexpr int kDpreFlatRows = 8;
+constexpr int kDpreFlatMaxBands = 4096;  // band offsets in LDS, 16 KB
 
-// dpre over whole rows (aligned case): block = kDpreFlatRows rows x all F/4 column quads, so
-// every band's columns are spread evenly over the threads whatever the band widths.  The
-// block first builds a quad -> band table in LDS (band offsets are multiples of 4, so a quad
-// lies in one band); consecutive threads then take consecutive quads of a row (coalesced).
+// dpre over whole rows (aligned case): thread t takes column quad t % (F / 4) of the
+// kDpreFlatRows rows of row group t / (F / 4), so consecutive threads read consecutive quads of
+// the same rows whatever the band widths (band offsets are multiples of 4, so a quad lies in one
+// band, found by binary search over the offsets staged in LDS).  The rows past M are clamped
+// reads (issued with the others, no branch before the arithmetic) whose results are not stored.
 template <typename T>
 __global__ __launch_bounds__(256) void me_dpre_flat_kernel(const T* __restrict__ gout, const T* __restrict__ pre,
                                                            T* __restrict__ dpre, MaskArgs a) {
-  extern __shared__ int smem[];
-  int* soff = smem;                                                   // [NB + 1]
-  uint16_t* sband = reinterpret_cast<uint16_t*>(smem + a.NB + 1);    // [F / 4]
-  const int nq = a.F / 4;
+  __shared__ int soff[kDpreFlatMaxBands + 1];
   for (int b = threadIdx.x; b <= a.NB; b += 256) soff[b] = static_cast<int>(a.offsets[b]);
   __syncthreads();
-  for (int q = threadIdx.x; q < nq; q += 256) {
-    int lo = 0, hi = a.NB - 1;  // last band with soff[b] <= 4q
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (soff[mid] <= 4 * q) lo = mid; else hi = mid - 1;
-    }
-    sband[q] = static_cast<uint16_t>(lo);
+  const int nq = a.F / 4;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t m0 = t / nq * kDpreFlatRows;
+  if (m0 >= a.M) return;
+  const int q = static_cast<int>(t % nq);
+  int lo = 0, hi = a.NB - 1;  // last band with soff[b] <= 4q
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (soff[mid] <= 4 * q) lo = mid; else hi = mid - 1;
   }
-  __syncthreads();
+  const int off = soff[lo];
+  const int I = soff[lo + 1] - off;
+  const int l = 4 * q - off;
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kDpreFlatRows;
-  for (int rr = 0; rr < kDpreFlatRows; ++rr) {
-    const int64_t m = r0 + rr;
-    if (m >= a.M) break;
-    for (int q = threadIdx.x; q < nq; q += 256) {
-      const int b = sband[q];
-      const int off = soff[b];
-      const int I = soff[b + 1] - off;
-      const int l = 4 * q - off;
-      const T* pl = pre + m * pitch2 + 2 * off + l;
-      float g[4], L[4], G[4], ol[4], og[4];
-      load_pack<T, 4>(gout + m * a.F + 4 * q, g);
-      load_pack<T, 4>(pl, L);
-      load_pack<T, 4>(pl + I, G);
+  float g[kDpreFlatRows][4], L[kDpreFlatRows][4], G[kDpreFlatRows][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float sg = sigmoidf_(G[j]);
-        ol[j] = g[j] * sg;
-        og[j] = g[j] * L[j] * sg * (1.0f - sg);
-      }
-      T* dl = dpre + m * pitch2 + 2 * off + l;
+  for (int r = 0; r < kDpreFlatRows; ++r) {
+    const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;
+    load_pack<T, 4>(gout + m * a.F + 4 * q, g[r]);
+    load_pack<T, 4>(pre + m * pitch2 + 2 * off + l, L[r]);
+    load_pack<T, 4>(pre + m * pitch2 + 2 * off + l + I, G[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < kDpreFlatRows; ++r) {
+    float ol[4], og[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float sg = sigmoidf_(G[r][j]);
+      ol[j] = g[r][j] * sg;
+      og[j] = g[r][j] * L[r][j] * sg * (1.0f - sg);
+    }
+    if (m0 + r < a.M) {
+      T* dl = dpre + (m0 + r) * pitch2 + 2 * off + l;
       store_pack<T, 4>(dl, ol);
       store_pack<T, 4>(dl + I, og);
     }
@@ -1036,10 +1035,10 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
   T* dpre = static_cast<T*>(workspace);
   if (M > 0) {
     const dim3 g1(static_cast<unsigned>((M + kDpreRows - 1) / kDpreRows), static_cast<unsigned>(hm.NB));
-    if (a.vec4 && hm.NB < kDpreFlatMaxBands && hm.F / 4 <= kDpreFlatMaxQuads) {
-      const size_t shm = static_cast<size_t>(hm.NB + 1) * sizeof(int) + static_cast<size_t>(hm.F / 4) * 2;
-      hipLaunchKernelGGL((me_dpre_flat_kernel<T>), dim3(static_cast<unsigned>((M + kDpreFlatRows - 1) / kDpreFlatRows)),
-                         dim3(256), shm, stream, static_cast<const T*>(gout), static_cast<const T*>(pre), dpre, a);
+    const int64_t flat_threads = (M + kDpreFlatRows - 1) / kDpreFlatRows * (hm.F / 4);
+    if (a.vec4 && hm.NB <= kDpreFlatMaxBands && (flat_threads + 255) / 256 < (int64_t{1} << 31)) {
+      hipLaunchKernelGGL((me_dpre_flat_kernel<T>), dim3(static_cast<unsigned>((flat_threads + 255) / 256)), dim3(256),
+                         0, stream, static_cast<const T*>(gout), static_cast<const T*>(pre), dpre, a);
     } else
     hipLaunchKernelGGL((me_dpre_kernel<T>), g1, dim3(256), 0, stream, static_cast<const T*>(gout),
                        static_cast<const T*>(pre), dpre, a);

@@ -15,16 +15,20 @@ __global__ __launch_bounds__(kColsPerBlock* kGroups) void col_sum_kernel(const f
   const int cl = threadIdx.x % kColsPerBlock;
   const int grp = threadIdx.x / kColsPerBlock;
   const int c = blockIdx.x * kColsPerBlock + cl;
-  float s0 = 0.f, s1 = 0.f;
+  // 8 independent loads in flight per trip (a serial chain of round trips otherwise sets the time)
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (c < dim) {
     int p = grp;
-    for (; p + kGroups < parts; p += 2 * kGroups) {
-      s0 += partial[static_cast<int64_t>(p) * dim + c];
-      s1 += partial[static_cast<int64_t>(p + kGroups) * dim + c];
+    for (; p + 7 * kGroups < parts; p += 8 * kGroups) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = partial[static_cast<int64_t>(p + u * kGroups) * dim + c];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[u] += v[u];
     }
-    if (p < parts) s0 += partial[static_cast<int64_t>(p) * dim + c];
+    for (; p < parts; p += kGroups) acc[0] += partial[static_cast<int64_t>(p) * dim + c];
   }
-  red[grp][cl] = s0 + s1;
+  red[grp][cl] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
   for (int stride = kGroups / 2; stride > 0; stride >>= 1) {
     if (grp < stride) red[grp][cl] += red[grp + stride][cl];
