@@ -275,6 +275,27 @@ int pmsst_band_rows_scatter(const void* in, int in_dtype, const int64_t* row_sta
                             void* out, int out_dtype, int64_t batch, int64_t num_rows, int64_t frames,
                             int64_t num_sel, void* stream);
 
+/* ---------------------------------------------------------------- mask application / iSTFT layout
+ * No kernel counterpart in the reference: the stock model multiplies the complex spectrum by the
+ * masks (after a float cast and a transposed complex view) and permutes the product into the iSTFT
+ * input, which the reference's cached-zero iSTFT then consumes (cuda_graph.py:140-158, including its
+ * zero_dc index_fill of frequency bin 0).  One pass each way here:
+ *   est[b, s, c, f, t] = spec[b, f*C + c, t] * mask_s[b, t, f*C + c]   (complex)
+ * spec: complex64 [batch, freqs*channels, frames] (re, im fp32 pairs), 8-byte aligned.
+ * mask: (re, im) pairs of dtype mask_dtype; element (b, s, t, k) at
+ *       b * mask_batch_stride + s * mask_stem_stride + t * 2*freqs*channels + k (even strides).
+ * est:  complex64 [batch, stems, channels, freqs, frames] = the iSTFT input [B*S*C, F, T].
+ * zero_dc nonzero: est (and both gradients) are 0 at f = 0. */
+int pmsst_mask_apply_forward(const void* spec, const void* mask, int64_t mask_batch_stride, int64_t mask_stem_stride,
+                             int64_t batch, int64_t stems, int64_t channels, int64_t freqs, int64_t frames,
+                             int zero_dc, void* est, int mask_dtype, void* stream);
+/* grad_mask (mask_dtype, contiguous [batch, stems, frames, 2*freqs*channels]) = grad_est * conj(spec);
+ * grad_spec (complex64 like spec, NULL to skip) = sum over stems of grad_est * conj(mask). */
+int pmsst_mask_apply_backward(const void* grad_est, const void* spec, const void* mask, int64_t mask_batch_stride,
+                              int64_t mask_stem_stride, int64_t batch, int64_t stems, int64_t channels, int64_t freqs,
+                              int64_t frames, int zero_dc, void* grad_mask, void* grad_spec, int mask_dtype,
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif

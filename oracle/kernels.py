@@ -49,6 +49,8 @@ __all__ = [
     "attention_gate_backward",
     "band_rows_gather",
     "band_rows_scatter",
+    "mask_apply_forward",
+    "mask_apply_backward",
     "sigmoid",
 ]
 
@@ -506,3 +508,42 @@ def band_rows_scatter(x, rows, num_rows: int, mean: bool = True):
         counts = np.bincount(rows, minlength=num_rows).astype(np.float64)
         out = out / np.maximum(counts, 1.0)[None, :, None, None]
     return out
+
+
+def mask_apply_forward(spec, mask, channels: int, zero_dc: bool = False):
+    """Complex mask application in the iSTFT layout (no reference kernel; the stock model's
+    ``spec.unsqueeze(1) * mask`` followed by the permute the cached-zero iSTFT consumes,
+    cuda_graph.py:140-158, with its optional zero-DC fill): ``spec`` complex ``[B, F*C, T]``,
+    ``mask`` real ``[B, S, T, F*C*2]`` ((re, im) pairs) -> complex128 ``[B*S*C, F, T]``."""
+    spec = np.asarray(spec, dtype=np.complex128)
+    mask = np.asarray(mask, dtype=np.float64)
+    b, fc, t = spec.shape
+    s = mask.shape[1]
+    f = fc // channels
+    m = mask[..., 0::2] + 1j * mask[..., 1::2]                       # [B, S, T, FC]
+    est = spec[:, None, :, :] * m.transpose(0, 1, 3, 2)              # [B, S, FC, T]
+    est = est.reshape(b, s, f, channels, t).transpose(0, 1, 3, 2, 4)  # [B, S, C, F, T]
+    if zero_dc:
+        est = est.copy()
+        est[:, :, :, 0, :] = 0
+    return est.reshape(b * s * channels, f, t)
+
+
+def mask_apply_backward(grad_est, spec, mask, channels: int, zero_dc: bool = False):
+    """Gradients of :func:`mask_apply_forward` in PyTorch's complex convention (for a product
+    ``est = spec * m`` the gradient of ``m`` is ``grad * conj(spec)``): returns
+    ``(grad_mask [B, S, T, F*C*2] real (re, im) pairs, grad_spec complex [B, F*C, T])``."""
+    spec = np.asarray(spec, dtype=np.complex128)
+    mask = np.asarray(mask, dtype=np.float64)
+    b, fc, t = spec.shape
+    s = mask.shape[1]
+    f = fc // channels
+    g = np.asarray(grad_est, dtype=np.complex128).reshape(b, s, channels, f, t).copy()
+    if zero_dc:
+        g[:, :, :, 0, :] = 0
+    g = g.transpose(0, 1, 3, 2, 4).reshape(b, s, fc, t)                 # [B, S, FC, T]
+    gm = (g * np.conj(spec)[:, None]).transpose(0, 1, 3, 2)             # [B, S, T, FC]
+    grad_mask = np.stack([gm.real, gm.imag], axis=-1).reshape(b, s, t, 2 * fc)
+    m = (mask[..., 0::2] + 1j * mask[..., 1::2]).transpose(0, 1, 3, 2)  # [B, S, FC, T]
+    grad_spec = (g * np.conj(m)).sum(axis=1)
+    return grad_mask, grad_spec

@@ -63,6 +63,7 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
         rotary_theta: float = 10000.0,
         checkpoint_blocks: bool = False,
         loss: str = "multi_stft",
+        zero_dc: bool = False,
         _check_cover: bool = True,
     ):
         super().__init__()
@@ -73,6 +74,7 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
         self.audio_channels = 2 if stereo else 1
         self.num_stems = num_stems
         self.checkpoint_blocks = checkpoint_blocks
+        self.zero_dc = zero_dc  # zero frequency bin 0 of the masked spectrum before the iSTFT
         time_rotary = RotaryEmbedding(dim_head, rotary_theta)
         freq_rotary = RotaryEmbedding(dim_head, rotary_theta)
         kw = dict(dim=dim, heads=heads, dim_head=dim_head, attn_dropout=attn_dropout, ff_dropout=ff_dropout,
@@ -127,6 +129,18 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
         b, stems, t = mask.shape[:3]
         return torch.view_as_complex(mask.float().reshape(b, stems, t, -1, 2).contiguous()).transpose(-1, -2)
 
+    def _masked_spectrum(self, spec: torch.Tensor, mask: torch.Tensor, channels: int) -> torch.Tensor:
+        """Complex ``spec[B, F*C, T]`` times the stems' masks (mask-estimator output
+        ``[B, stems, T, F*C*2]``) in the layout iSTFT consumes, ``[B * stems * C, F, T]``; frequency bin 0
+        is zeroed when ``zero_dc`` (the layout and fill of pymsst's cached-zero iSTFT,
+        ``cuda_graph.py:140-158``)."""
+        b, stems, t = mask.shape[:3]
+        est = spec.unsqueeze(1) * self._spectral_mask(mask)  # [B, stems, F*C, T]
+        est = est.reshape(b, stems, -1, channels, t).transpose(2, 3).reshape(b * stems * channels, -1, t)
+        if self.zero_dc:
+            est = est.index_fill(1, torch.zeros(1, dtype=torch.long, device=est.device), 0.0)
+        return est
+
     def _axial(self, x: torch.Tensor, time_tf: Transformer, freq_tf: Transformer) -> torch.Tensor:
         b, t, nb, d = x.shape
         x = time_tf(x.transpose(1, 2).reshape(b * nb, t, d)).reshape(b, nb, t, d).transpose(1, 2)
@@ -151,11 +165,9 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
         x = self.final_norm(x)
         mask = self._estimate_masks(x)  # [B, stems, T, features]
         stems = mask.shape[1]
-        mask = self._spectral_mask(mask)  # [B, stems, F*C, T] complex
-        est = spec.unsqueeze(1) * mask  # [B, stems, F*C, T]
         if target is not None and self.loss_type == "spec_l1":
-            return self._spec_loss(est, target, c)
-        est = est.reshape(b, stems, -1, c, t).transpose(2, 3).reshape(b * stems * c, -1, t)
+            return self._spec_loss(spec.unsqueeze(1) * self._spectral_mask(mask), target, c)
+        est = self._masked_spectrum(spec, mask, c)  # [B * stems * C, F, T], the iSTFT input
         recon = torch.istft(est, window=window, length=length, return_complex=False, **self.stft_kwargs)
         recon = recon.reshape(b, stems, c, length)
         if stems == 1:

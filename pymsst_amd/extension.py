@@ -547,6 +547,55 @@ class HipFusedExtension:
         check(rc, "pmsst_band_rows_scatter")
         return out
 
+    # ------------------------------------------------------------------ mask application
+
+    def mask_apply_forward(self, spec, mask, channels: int, zero_dc: bool = False):
+        """Build-addition op: complex ``spec[B, F*C, T]`` times the per-stem masks
+        ``mask[B, S, T, F*C*2]`` ((re, im) pairs), returned in the iSTFT layout: complex64
+        ``[B*S*C, F, T]`` (frequency bin 0 zeroed when ``zero_dc``)."""
+        _req(spec.is_cuda and spec.dtype == torch.complex64 and spec.dim() == 3, "spec must be CUDA complex64 [B, F*C, T]")
+        _req(mask.is_cuda and mask.dim() == 4 and mask.dtype in (torch.float32, torch.float16, torch.bfloat16),
+             "mask must be a CUDA float tensor [B, S, T, F*C*2]")
+        b, fc, t = spec.shape
+        _req(channels > 0 and fc % channels == 0, "channels must divide the spectrum rows")
+        _req(mask.shape[0] == b and mask.shape[2] == t and mask.shape[3] == 2 * fc, "mask shape does not match spec")
+        spec = spec.contiguous()
+        if mask.stride(3) != 1 or mask.stride(2) != 2 * fc:
+            mask = mask.contiguous()
+        s = mask.shape[1]
+        f = fc // channels
+        est = torch.empty((b * s * channels, f, t), dtype=torch.complex64, device=spec.device)
+        with _DeviceGuard(spec.device):
+            rc = self._lib.pmsst_mask_apply_forward(
+                _ptr(spec), _ptr(mask), mask.stride(0), mask.stride(1), b, s, channels, f, t, int(bool(zero_dc)),
+                _ptr(est), dtype_code(mask.dtype), _stream(spec.device),
+            )
+        check(rc, "pmsst_mask_apply_forward")
+        return est
+
+    def mask_apply_backward(self, grad_est, spec, mask, channels: int, zero_dc: bool = False, need_spec_grad=False):
+        """Gradients of :meth:`mask_apply_forward`: ``(grad_mask [B, S, T, F*C*2] in the mask dtype,
+        grad_spec complex64 [B, F*C, T] or None)``."""
+        b, fc, t = spec.shape
+        s = mask.shape[1]
+        f = fc // channels
+        _req(grad_est.is_cuda and grad_est.dtype == torch.complex64 and tuple(grad_est.shape) == (b * s * channels, f, t),
+             "grad_est must be CUDA complex64 [B*S*C, F, T]")
+        grad_est = grad_est.contiguous()
+        spec = spec.contiguous()
+        if mask.stride(3) != 1 or mask.stride(2) != 2 * fc:
+            mask = mask.contiguous()
+        grad_mask = torch.empty((b, s, t, 2 * fc), dtype=mask.dtype, device=spec.device)
+        grad_spec = torch.empty_like(spec) if need_spec_grad else None
+        with _DeviceGuard(spec.device):
+            rc = self._lib.pmsst_mask_apply_backward(
+                _ptr(grad_est), _ptr(spec), _ptr(mask), mask.stride(0), mask.stride(1), b, s, channels, f, t,
+                int(bool(zero_dc)), _ptr(grad_mask), _ptr(grad_spec) if grad_spec is not None else None,
+                dtype_code(mask.dtype), _stream(spec.device),
+            )
+        check(rc, "pmsst_mask_apply_backward")
+        return grad_mask, grad_spec
+
     # ------------------------------------------------------------------ band split
 
     def _bands(self, dim_inputs, device: torch.device):

@@ -60,6 +60,9 @@ EXPERIMENTAL_FUSED_MASK_MLP_ENV = "PYMSST_EXPERIMENTAL_FUSED_MASK_MLP"
 # This build's addition: the Mel-band RoFormer's band gather and overlap-averaged mask scatter on
 # the HIP band-row kernels.
 EXPERIMENTAL_FUSED_MEL_BANDS_ENV = "PYMSST_EXPERIMENTAL_FUSED_MEL_BANDS"
+# This build's addition: the complex mask product and the iSTFT-layout permute (plus the zero-DC
+# fill) of the BS-RoFormer output in one HIP pass each way.
+EXPERIMENTAL_FUSED_MASK_APPLY_ENV = "PYMSST_EXPERIMENTAL_FUSED_MASK_APPLY"
 
 _TRUE = {"1", "true", "yes", "on"}
 _FLOAT_TYPES = (torch.float16, torch.bfloat16, torch.float32)
@@ -84,6 +87,7 @@ RUNTIME_PRESETS["hip_full"] = {
     EXPERIMENTAL_FUSED_MASK_MLP_ENV: "1",
     EXPERIMENTAL_ATTENTION_GATES_ENV: "1",
     EXPERIMENTAL_FUSED_MEL_BANDS_ENV: "1",
+    EXPERIMENTAL_FUSED_MASK_APPLY_ENV: "1",
 }
 
 
@@ -123,6 +127,7 @@ class FusedTrainingStatus:
     mask_estimator_final_mode: str | None = None
     patched_mask_mlp: bool = False  # this build's addition (hidden Linear + tanh fused as well)
     patched_mel_bands: bool = False  # this build's addition (Mel-band gather / mask scatter)
+    patched_mask_apply: bool = False  # this build's addition (mask product in the iSTFT layout)
 
 
 # ---------------------------------------------------------------------- switchboard
@@ -256,9 +261,10 @@ def apply_roformer_fused_training_backend(
     final = _patch_core_mask_estimator_final(ext, final_mode) if final_mode else False
     mask_mlp = final and _mask_mlp_enabled(ext)
     mel_bands = _patch_mel_bands(ext) if _flag(EXPERIMENTAL_FUSED_MEL_BANDS_ENV) else False
+    mask_apply = _patch_mask_apply(ext) if _flag(EXPERIMENTAL_FUSED_MASK_APPLY_ENV) else False
 
     if not any((n_band_splits, single_stem, rotary, rms, gates, grouped_linear, layout, pack_autograd, final_autograd,
-                final, mel_bands)):
+                final, mel_bands, mask_apply)):
         reason = "no compatible BandSplit modules were found"
         warnings.warn(reason, RuntimeWarning, stacklevel=2)
         return FusedTrainingStatus(requested=normalized, active="off", reason=reason)
@@ -287,6 +293,7 @@ def apply_roformer_fused_training_backend(
         mask_estimator_final_mode=final_mode if final else None,
         patched_mask_mlp=mask_mlp,
         patched_mel_bands=mel_bands,
+        patched_mask_apply=mask_apply,
     )
 
 
@@ -487,6 +494,33 @@ def _patch_mel_bands(ext: Any) -> bool:
     spectral_mask_cuda_ext._pymsst_original_spectral_mask = orig_mask
     cls._band_features = band_features_cuda_ext
     cls._spectral_mask = spectral_mask_cuda_ext
+    return True
+
+
+def _patch_mask_apply(ext: Any) -> bool:
+    """Class-level ``BSRoformer._masked_spectrum`` replacement (no reference kernel: the stock model
+    multiplies the spectrum by the float-cast masks through a transposed complex view and permutes
+    the product for the iSTFT, cuda_graph.py:140-158).  Models whose ``_spectral_mask`` is not the
+    BS-RoFormer one (the Mel-band model averages band masks first) keep the stock method."""
+    if any(not hasattr(ext, n) for n in ("mask_apply_forward", "mask_apply_backward")):
+        return False
+    from .core import bs_roformer
+
+    cls = bs_roformer.BSRoformer
+    if getattr(cls._masked_spectrum, "_pymsst_fused_mask_apply", False):
+        return True
+    original = cls._masked_spectrum
+    stock_spectral_mask = cls._spectral_mask
+
+    def masked_spectrum_cuda_ext(self, spec, mask, channels):
+        if (type(self)._spectral_mask is not stock_spectral_mask or not spec.is_cuda
+                or spec.dtype != torch.complex64 or mask.dtype not in _FLOAT_TYPES or mask.dim() != 4):
+            return original(self, spec, mask, channels)
+        return _FusedMaskApply.apply(spec, mask, channels, bool(getattr(self, "zero_dc", False)), ext)
+
+    masked_spectrum_cuda_ext._pymsst_fused_mask_apply = True
+    masked_spectrum_cuda_ext._pymsst_original_masked_spectrum = original
+    cls._masked_spectrum = masked_spectrum_cuda_ext
     return True
 
 
@@ -1175,6 +1209,25 @@ class _FusedMaskScatterMean(torch.autograd.Function):
         return grad.reshape(ctx.shape), None, None
 
 
+class _FusedMaskApply(torch.autograd.Function):
+    """``spec[B, F*C, T]`` (complex64) times the masks ``mask[B, stems, T, F*C*2]`` in the iSTFT layout
+    ``[B*stems*C, F, T]`` (one HIP pass each way; the mask gradient comes back in the mask's dtype
+    like the stock float cast's backward)."""
+
+    @staticmethod
+    def forward(ctx, spec, mask, channels, zero_dc, extension):
+        ctx.channels, ctx.zero_dc, ctx.extension = channels, zero_dc, extension
+        ctx.save_for_backward(spec, mask)
+        return extension.mask_apply_forward(spec, mask, channels, zero_dc)
+
+    @staticmethod
+    def backward(ctx, grad_est):
+        spec, mask = ctx.saved_tensors
+        grad_mask, grad_spec = ctx.extension.mask_apply_backward(
+            grad_est, spec, mask, ctx.channels, ctx.zero_dc, need_spec_grad=ctx.needs_input_grad[0])
+        return grad_spec, grad_mask if ctx.needs_input_grad[1] else None, None, None, None
+
+
 class _FusedAttentionGate(torch.autograd.Function):
     """fr.py:1228-1262.  With an extension that reads ``[B,N,H,Dh]`` views in place
     (``attention_gate_forward_bnhd``), the transposed SDPA output is not copied and the attn
@@ -1327,6 +1380,7 @@ _CORE_PATCH_POINTS = (
     ("common", "RoformerRuntimeMixin", "_estimate_masks", "_pymsst_original_estimate_masks"),
     ("mel_band_roformer", "MelBandRoformer", "_band_features", "_pymsst_original_band_features"),
     ("mel_band_roformer", "MelBandRoformer", "_spectral_mask", "_pymsst_original_spectral_mask"),
+    ("bs_roformer", "BSRoformer", "_masked_spectrum", "_pymsst_original_masked_spectrum"),
 )
 
 
@@ -1335,10 +1389,11 @@ def restore_stock_implementations(model: torch.nn.Module | None = None) -> None:
     the reference has no inverse).  Module- and class-level patches are unwound to the
     stock functions; with ``model`` its BandSplit instances get their stock
     ``_forward_grouped`` back.  Used to run stock and fused models in one process."""
-    from .core import mel_band_roformer
+    from .core import bs_roformer, mel_band_roformer
 
     bands, transformer, common = _core()
-    modules = {"bands": bands, "transformer": transformer, "common": common, "mel_band_roformer": mel_band_roformer}
+    modules = {"bands": bands, "transformer": transformer, "common": common, "mel_band_roformer": mel_band_roformer,
+               "bs_roformer": bs_roformer}
     for mod_name, owner_name, name, marker in _CORE_PATCH_POINTS:
         owner = modules[mod_name] if owner_name is None else getattr(modules[mod_name], owner_name)
         current = getattr(owner, name)

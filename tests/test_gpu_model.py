@@ -66,6 +66,7 @@ def test_fused_model_matches_stock_fp32(hip_env):
     assert status.active == "cuda_ext"
     assert status.patched_band_splits == 1 and status.patched_band_split_ragged_backward
     assert status.patched_rotary and status.patched_rms_norm and status.patched_mask_estimator_final
+    assert status.patched_mask_apply
     assert set(gs) == set(gf)
     assert abs(lf - ls) <= 1e-5 * abs(ls), (lf, ls)
     worst_abs, worst_rel = 0.0, 0.0

@@ -412,3 +412,34 @@ def test_band_rows_gather_scatter_vs_torch_index_ops():
     lhs = (oracle.band_rows_gather(x, rows) * y).sum()
     rhs = (x * oracle.band_rows_scatter(y, rows, R, mean=False)).sum()
     assert abs(lhs - rhs) <= 1e-9 * max(1.0, abs(lhs))
+
+
+@pytest.mark.parametrize("zero_dc", [False, True])
+def test_mask_apply_vs_torch_complex_autograd(zero_dc):
+    """The stock model's mask product and iSTFT permute in torch (CPU complex autograd) against the
+    oracle, plus an explicit-loop check of the layout on the same inputs."""
+    g = torch.Generator().manual_seed(5)
+    b, s, c, f, t = 2, 3, 2, 5, 7
+    spec = torch.complex(torch.randn(b, f * c, t, generator=g, dtype=torch.float64),
+                         torch.randn(b, f * c, t, generator=g, dtype=torch.float64)).requires_grad_(True)
+    mask = torch.randn(b, s, t, f * c * 2, generator=g, dtype=torch.float64, requires_grad=True)
+    m = torch.view_as_complex(mask.reshape(b, s, t, f * c, 2)).transpose(-1, -2)
+    est = (spec.unsqueeze(1) * m).reshape(b, s, f, c, t).transpose(2, 3).reshape(b * s * c, f, t)
+    if zero_dc:
+        est = est.index_fill(1, torch.zeros(1, dtype=torch.long), 0.0)
+    ge = torch.complex(torch.randn(est.shape, generator=g, dtype=torch.float64),
+                       torch.randn(est.shape, generator=g, dtype=torch.float64))
+    (est * ge.conj()).real.sum().backward()   # d/d(est) of Re<est, ge> is ge
+    ri = lambda z: np.stack([np.real(z), np.imag(z)], axis=-1)  # noqa: E731  (compare re and im)
+    got = oracle.mask_apply_forward(spec.detach().numpy(), mask.detach().numpy(), c, zero_dc)
+    _close(ri(got), ri(est.detach().numpy()), what="est")
+    gm, gs = oracle.mask_apply_backward(ge.numpy(), spec.detach().numpy(), mask.detach().numpy(), c, zero_dc)
+    _close(gm, mask.grad.numpy(), what="grad_mask")
+    _close(ri(gs), ri(spec.grad.numpy()), what="grad_spec")
+    sp, mk = spec.detach().numpy(), mask.detach().numpy()
+    for (bi, si, ci, fi, ti) in [(0, 0, 0, 1, 0), (1, 2, 1, 4, 6), (1, 1, 0, 2, 3)]:
+        r = fi * c + ci
+        want = sp[bi, r, ti] * complex(mk[bi, si, ti, 2 * r], mk[bi, si, ti, 2 * r + 1])
+        assert abs(got[(bi * s + si) * c + ci, fi, ti] - want) < 1e-12
+    if zero_dc:
+        assert np.all(got[:, 0, :] == 0) and np.all(gm.reshape(b, s, t, f, c, 2)[:, :, :, 0] == 0)
