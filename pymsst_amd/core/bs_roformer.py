@@ -154,7 +154,13 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
             raw_audio = raw_audio.unsqueeze(1)
         b, c, length = raw_audio.shape
         spec, window = self._stft(raw_audio)  # [B, F*C, T] complex
-        t = spec.shape[-1]
+        if target is not None and self.loss_type == "spec_l1":
+            return self._spec_loss(spec.unsqueeze(1) * self._spectral_mask(self._masks(spec)), target, c)
+        return self._finish(self._mask_core(spec, c), window, b, c, length, target)
+
+    def _masks(self, spec: torch.Tensor) -> torch.Tensor:
+        """Complex ``spec[B, F*C, T]`` -> the stems' masks ``[B, stems, T, features]`` (band features,
+        band split, axial blocks, final norm, mask estimators)."""
         x = self._band_features(spec)  # [B, T, features]
         x = self.band_split(x)  # [B, T, NB, dim]
         for time_tf, freq_tf in self.layers:
@@ -162,14 +168,20 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
                 x = checkpoint(self._axial, x, time_tf, freq_tf, use_reentrant=False)
             else:
                 x = self._axial(x, time_tf, freq_tf)
-        x = self.final_norm(x)
-        mask = self._estimate_masks(x)  # [B, stems, T, features]
-        stems = mask.shape[1]
-        if target is not None and self.loss_type == "spec_l1":
-            return self._spec_loss(spec.unsqueeze(1) * self._spectral_mask(mask), target, c)
-        est = self._masked_spectrum(spec, mask, c)  # [B * stems * C, F, T], the iSTFT input
+        return self._estimate_masks(self.final_norm(x))
+
+    def _mask_core(self, spec: torch.Tensor, channels: int) -> torch.Tensor:
+        """The part between STFT and iSTFT (pymsst's "mask core"): complex ``spec[B, F*C, T]`` -> masked
+        spectrum in the iSTFT layout ``[B * stems * C, F, T]``."""
+        return self._masked_spectrum(spec, self._masks(spec), channels)
+
+    def _finish(self, est: torch.Tensor, window: torch.Tensor, batch: int, channels: int, length: int,
+                target: torch.Tensor | None = None):
+        """iSTFT of the masked spectrum -> audio ``[B, stems, C, L]`` (stems squeezed when 1), or the loss
+        against ``target``."""
         recon = torch.istft(est, window=window, length=length, return_complex=False, **self.stft_kwargs)
-        recon = recon.reshape(b, stems, c, length)
+        stems = est.shape[0] // (batch * channels)
+        recon = recon.reshape(batch, stems, channels, length)
         if stems == 1:
             recon = recon[:, 0]
         if target is None:
