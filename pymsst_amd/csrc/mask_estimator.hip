@@ -174,6 +174,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(PM
 #ifndef PMSST_MEF_STAGES
 #define PMSST_MEF_STAGES 4
 #endif
+#ifndef PMSST_MEF_BAND_DMA
+#define PMSST_MEF_BAND_DMA 1
+#endif
 constexpr int kMefStage = 16384;  // bytes of one LDS stage
 
 
@@ -231,11 +234,20 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_dma_kernel(const T* __res
   const int kbeg = H - nk * kChunkK;           // chunk c covers k in [kbeg + 32 c, +32)
   char* my_lds = lds + (4 * wave) * 1024;      // this wave's 4 KB of a stage
 
+  // Weight waves move only the 16-output groups inside the band (instruction t of wave w holds
+  // outputs l0 + 32 w + 16 (t / 2) ..; the groups past the band would re-read its clamped last row
+  // and only feed outputs that are never stored): nv = 4, 2 or 0 DMAs per chunk, wave-uniform.
+#if PMSST_MEF_BAND_DMA
+  const int nv = wave >= 2 ? 4 : (l0 + 32 * wave + 16 < I ? 4 : (l0 + 32 * wave < I ? 2 : 0));
+#else
+  const int nv = 4;
+#endif
   auto dma = [&](int c, int stage) {  // chunk c >= 1 into `stage`
     const char* src = gbase + 2 * (kbeg + kChunkK * c);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-      __builtin_amdgcn_global_load_lds(src + soff[t], my_lds + stage * kMefStage + t * 1024, 16, 0, 0);
+      if (t < nv)
+        __builtin_amdgcn_global_load_lds(src + soff[t], my_lds + stage * kMefStage + t * 1024, 16, 0, 0);
   };
 
   // chunk 0 through registers: units with k < 0 are zero (they load k = 0 of the row)
@@ -265,8 +277,11 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_dma_kernel(const T* __res
                          static_cast<uint32_t>((64 * wc + rr) * 64) + sw;
 
   for (int c = 0; c < nk; ++c) {
-    // chunk c landed: the DMAs issued after it are chunks c + 1 .. c + S - 2
-    if (c > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (S - 2)) : "memory");
+    // chunk c landed: the DMAs issued after it are chunks c + 1 .. c + S - 2 (nv per chunk)
+    if (c > 0) {
+      if (nv == 4) vm_wait<4 * (S - 2)>();
+      else if (nv == 2) vm_wait<2 * (S - 2)>();
+    }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     // refill the stage chunk c - 1 used (every wave is past its reads); clamped at the end
