@@ -190,7 +190,8 @@ int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, in
 int pmsst_grouped_linear_forward(const void* x, int64_t x_row_stride, const void* weight, const void* bias,
                                  const int64_t* group_offsets, int64_t groups, int64_t in_features, int64_t rows,
                                  int64_t out_features, void* out, int activation, int dtype, void* stream);
-/* Workspace bytes of the grouped-linear backward (bias-gradient partials). */
+/* Workspace bytes of the grouped-linear backward: 0 (kept for the op's calling convention; the
+ * workspace arguments of pmsst_grouped_linear_backward may be NULL / 0). */
 size_t pmsst_grouped_linear_backward_workspace_size(int64_t rows, int64_t groups, int64_t out_features);
 /* Backward of grouped_linear (the reference computes it with batched GEMMs in _FusedGroupedLinear,
  * fr.py:1042-1048): grad_out[rows, groups, O] (the gradient of the pre-activation output),

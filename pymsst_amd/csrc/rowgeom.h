@@ -59,15 +59,4 @@ inline size_t row_bwd_workspace(int64_t dim) {
 // parts == 0 writes zeros.
 int launch_col_sum(const float* partial, int parts, int dim, void* out, int out_dtype, hipStream_t stream);
 
-// Column sums of a row-major src[rows, cols] (storage `src_dtype`) into out[cols]
-// (`out_dtype`): fp32 partials per 16-row block in `partial` (colsum_rows_workspace
-// bytes), then launch_col_sum.  Deterministic.
-constexpr int kColsumRowBlock = 16;
-inline size_t colsum_rows_workspace(int64_t rows, int64_t cols) {
-  const int64_t parts = (rows + kColsumRowBlock - 1) / kColsumRowBlock;
-  return static_cast<size_t>(parts > 0 ? parts : 1) * static_cast<size_t>(cols) * sizeof(float);
-}
-int launch_colsum_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, float* partial, void* out,
-                       int out_dtype, hipStream_t stream);
-
 }  // namespace pmsst

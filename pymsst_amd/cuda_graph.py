@@ -18,10 +18,12 @@ With a target, ``forward`` returns the model's loss: the waveform losses after t
 spectrogram loss (``loss="spec_l1"``) from the graphed masked spectrum permuted back to
 ``[B, stems, F*C, T]``.
 
-``capture`` checks two replays of the recorded forward and backward against the eager region on
-the capture sample and stays inactive (eager ``forward``) when they disagree: on this ROCm stack the
-backward of torch's bias / normalisation reductions records memset nodes that only hold on the
-first replay, which leaves the training graph inactive with that reason.
+On ROCm (``torch.version.hip``) a training capture (parameters that require gradients) is refused by
+default and ``forward`` runs eagerly: on ROCm 7.2 with torch 2.10 the captured backward of torch's
+bias / normalisation reductions records memset nodes that hold on the first replay only, so later
+replays return wrong gradients, and not always on the second replay (a capture-time check passed
+two replays and a later one failed).  ``allow_hip_training_graphs=True`` captures anyway and still
+checks two replays against eager before using the graph.
 
 The model is this build's restated BS-RoFormer (``pymsst_amd.core``): its ``_stft`` / ``_mask_core``
 / ``_finish`` split stands in for pymss-core's ``stft_roformer`` / ``_mask_stft_repr`` /
@@ -41,7 +43,13 @@ from typing import Callable
 import torch
 from torch import nn
 
-__all__ = ["CudaGraphRuntimeStatus", "RoformerTrainingCudaGraph", "normalize_cuda_graph_mode"]
+__all__ = ["CudaGraphRuntimeStatus", "HIP_TRAINING_GRAPH_REASON", "RoformerTrainingCudaGraph",
+           "normalize_cuda_graph_mode"]
+
+HIP_TRAINING_GRAPH_REASON = (
+    "HIP graph replays of the training backward are not reliable on this ROCm stack (memset nodes recorded by "
+    "library reductions hold on the first replay only); pass allow_hip_training_graphs=True to capture anyway"
+)
 
 
 @dataclass
@@ -96,12 +104,14 @@ class _STFTMaskCoreModule(nn.Module):
 class RoformerTrainingCudaGraph:
     """``cuda_graph.py:29-103`` over this build's BS-RoFormer (mixture ``[B, C, L]``)."""
 
-    def __init__(self, model: nn.Module, mode: str = "mask_core", amp_dtype: torch.dtype = torch.float16) -> None:
+    def __init__(self, model: nn.Module, mode: str = "mask_core", amp_dtype: torch.dtype = torch.float16,
+                 allow_hip_training_graphs: bool = False) -> None:
         self.mode = normalize_cuda_graph_mode(mode)
         if self.mode == "off":
             raise ValueError("RoformerTrainingCudaGraph requires an active graph mode")
         self.model = model
         self.amp_dtype = amp_dtype
+        self.allow_hip_training_graphs = allow_hip_training_graphs
         self.status = CudaGraphRuntimeStatus(requested=self.mode, active="off")
         self._graph_call: Callable[[torch.Tensor], torch.Tensor] | None = None
         self._input_shape: tuple[int, ...] | None = None
@@ -118,6 +128,10 @@ class RoformerTrainingCudaGraph:
             return self.status
         if sample_mixture.ndim == 2:
             sample_mixture = sample_mixture.unsqueeze(1)
+        training = any(p.requires_grad for p in self.model.parameters())
+        if torch.version.hip is not None and training and not self.allow_hip_training_graphs:
+            self.status = CudaGraphRuntimeStatus(self.mode, "off", HIP_TRAINING_GRAPH_REASON)
+            return self.status
         try:
             if self.mode == "stft_mask_core":
                 graph_module = _STFTMaskCoreModule(self.model)

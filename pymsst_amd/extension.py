@@ -880,11 +880,12 @@ class HipFusedExtension:
         dx = torch.empty_like(x)
         dw = torch.empty_like(weight)
         db = torch.empty((g, o), dtype=x.dtype, device=x.device) if has_bias else None
-        ws = _workspace(self._lib.pmsst_grouped_linear_backward_workspace_size(m, g, o) if has_bias else 0, x.device)
+        ws_bytes = int(self._lib.pmsst_grouped_linear_backward_workspace_size(m, g, o))  # 0 on this build
+        ws = _workspace(ws_bytes, x.device) if ws_bytes else None
         with _DeviceGuard(x.device):
             rc = self._lib.pmsst_grouped_linear_backward(
                 _ptr(grad_out), _ptr(x), _ptr(weight), _ptr(dev_offs), g, i, m, o, _ptr(dx), _ptr(dw), _ptr(db),
-                dtype_code(x.dtype), _ptr(ws), ws.numel(), _stream(x.device),
+                dtype_code(x.dtype), _ptr(ws), ws_bytes, _stream(x.device),
             )
         check(rc, "pmsst_grouped_linear_backward")
         return [dx, dw, db]

@@ -46,6 +46,7 @@ def test_workspace_queries(lib):
     assert lib.pmsst_band_split_ragged_backward_workspace_size(0, 4100, 62, 192) == 0
     assert lib.pmsst_mask_estimator_final_backward_workspace_size(1032, 4100, 2) == -(-1032 * 8200 * 2 // 256) * 256
     assert lib.pmsst_mask_estimator_final_backward_workspace_size(0, 4100, 2) == 0
+    assert lib.pmsst_grouped_linear_backward_workspace_size(1032, 62, 768) == 0
 
 
 def test_argument_errors_need_no_device(lib):

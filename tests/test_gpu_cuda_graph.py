@@ -1,6 +1,8 @@
-"""GPU: HIP-graph capture of the RoFormer mask core (``pymsst_amd.cuda_graph``, after pymsst's
-``cuda_graph.py``) gives the eager model's results: either its graphs replay forward and backward
-exactly, or its own two-replay check at capture finds them wrong and ``forward`` runs eagerly.
+"""GPU: the RoFormer mask-core graph wrapper (``pymsst_amd.cuda_graph``, after pymsst's
+``cuda_graph.py``) gives the eager model's results.  On ROCm it refuses training captures by default
+(replays of the captured backward after the first return wrong gradients on this stack), so the
+training cases check the eager fallback and its stated reason; the opt-in capture is exercised for
+its status only.
 
 Each case captures once, then for three fresh batches runs the eager model and the graphed model on
 the same parameters and compares loss and every parameter gradient; the eager runs between the
@@ -11,13 +13,11 @@ loss and the iSTFT + multi-resolution STFT loss.
 
 from __future__ import annotations
 
-import sys
-
 import pytest
 import torch
 
 from pymsst_amd import fused_roformer as fr
-from pymsst_amd.cuda_graph import RoformerTrainingCudaGraph, normalize_cuda_graph_mode
+from pymsst_amd.cuda_graph import HIP_TRAINING_GRAPH_REASON, RoformerTrainingCudaGraph, normalize_cuda_graph_mode
 from pymsst_amd.workloads import WORKLOADS, TrainWorkload, workload_batch
 
 # bsr_tiny trains on the spectrogram loss; this variant (2 stems) goes through the iSTFT and the
@@ -43,7 +43,9 @@ def _loss_grads(fn, model):
 @pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("amp", [None, torch.bfloat16])
 @pytest.mark.parametrize("wl", [WORKLOADS["bsr_tiny"], _ISTFT_WL], ids=["spec_l1", "istft"])
-def test_graph_replays_match_eager(monkeypatch, hip_ext, mode, fused, amp, wl):
+def test_training_graph_matches_eager(monkeypatch, hip_ext, mode, fused, amp, wl):
+    """The wrapper's training forward gives the eager model's loss and gradients on three batches.  On
+    ROCm it refuses the capture by default (and says why), so this checks the eager fallback there."""
     if fused:
         for key, value in fr.RUNTIME_PRESETS["hip_full"].items():
             monkeypatch.setenv(key, value)
@@ -59,11 +61,10 @@ def test_graph_replays_match_eager(monkeypatch, hip_ext, mode, fused, amp, wl):
         _, sample = workload_batch(wl, seed=0, device="cuda")
         st = graph.capture(sample, use_amp=use_amp)
         assert all(p.grad is None for p in model.parameters())
-        # active, or inactive because its own replay check found the graph wrong (then forward is eager)
-        assert st.active == mode or "replay" in (st.reason or ""), st.reason
-        sys.stderr.write(f"[graph] {mode}: active={st.active} reason={st.reason}\n")
-        # fp32: the mask core replays bitwise-equal kernels; with the STFT inside the graph the FFTs
-        # run from the captured plan and differ from the eager ones by rounding (bar 1e-4)
+        if torch.version.hip is not None:
+            assert st.active == "off" and st.reason == HIP_TRAINING_GRAPH_REASON
+        else:
+            assert st.active == mode or "replay" in (st.reason or ""), st.reason
         tol = (1e-5 if mode == "mask_core" else 1e-4) if amp is None else 2e-2
         for seed in (1, 2, 3):
             target, mixture = workload_batch(wl, seed=seed, device="cuda")
@@ -76,21 +77,26 @@ def test_graph_replays_match_eager(monkeypatch, hip_ext, mode, fused, amp, wl):
             lg, gg = _loss_grads(lambda: graph.forward(mixture, target, use_amp=use_amp), model)
             assert abs(lg - le) <= tol * abs(le), (seed, lg, le)
             assert set(gg) == set(ge)
-            worst = 0.0
             for name, ref in ge.items():
                 diff = (gg[name] - ref).abs().max().item()
-                worst = max(worst, diff / max(1.0, ref.abs().max().item()))
-                assert diff <= tol * max(1.0, ref.abs().max().item()), f"replay {seed} {name}: {diff:.3e}"
-            sys.stderr.write(f"[graph] replay {seed}: loss {lg:.8f} vs {le:.8f}, worst grad diff {worst:.3e}\n")
-        # another shape runs eagerly
-        _, other = workload_batch(wl, seed=4, device="cuda")
-        other = other[:1]
-        with torch.no_grad():
-            out = graph.forward(other, use_amp=use_amp)
-        assert out.shape[0] == 1
+                assert diff <= tol * max(1.0, ref.abs().max().item()), f"call {seed} {name}: {diff:.3e}"
     finally:
         fr.restore_stock_implementations(model)
         fr.restore_stock_implementations()
+
+
+@pytest.mark.gpu
+def test_opt_in_capture_reports_a_status(hip_ext):
+    """With the opt-in the capture runs (warm-up, recording, two checked replays) and reports active or
+    the replay disagreement; the graph is not used for training here."""
+    wl = WORKLOADS["bsr_tiny"]
+    model = wl.build_model("cuda", seed=4)
+    model.train()
+    graph = RoformerTrainingCudaGraph(model, "mask_core", allow_hip_training_graphs=True)
+    _, sample = workload_batch(wl, seed=0, device="cuda")
+    st = graph.capture(sample, use_amp=False)
+    assert st.active == "mask_core" or "replay" in (st.reason or ""), st.reason
+    assert all(p.grad is None for p in model.parameters())
 
 
 def test_mode_names():
