@@ -105,6 +105,13 @@ __device__ __forceinline__ void lds_wait(u32x4_t (&a)[NA], u32x4_t (&b)[NB]) {
     static_assert(NA < 0, "add the operand list for this shape");
 }
 
+// One 16-byte-per-lane global -> LDS DMA (to lds + 16 * lane).  Kernel templates with a non-type
+// parameter call it instead of the builtin: hipcc (ROCm 7.2) drops the host launch stub of such a
+// kernel template when its body calls __builtin_amdgcn_global_load_lds directly.
+__device__ __forceinline__ void dma_lds16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
 template <int N>
 __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");

@@ -552,18 +552,29 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __rest
 #ifndef PMSST_ME_DX_STAGES
 #define PMSST_ME_DX_STAGES 4
 #endif
-constexpr int kDxStage = 16384;
-constexpr int kDxHC = 128;  // hidden columns per block
+#ifndef PMSST_ME_DX256_STAGES
+#define PMSST_ME_DX256_STAGES 3
+#endif
+// Hidden columns per block: 256 (8 waves) when the hidden size allows, else 128 (4 waves).
+#ifndef PMSST_ME_DX_HC
+#define PMSST_ME_DX_HC 256
+#endif
 constexpr int kDxBMd = 128;  // rows per block
 
-template <typename T, bool TANH_IN>
-__global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_dma_kernel(const T* __restrict__ dpre,
-                                                                     const T* __restrict__ weight,
-                                                                     const T* __restrict__ x, T* __restrict__ dx,
-                                                                     BandSched sc, MaskArgs a) {
-  constexpr int S = PMSST_ME_DX_STAGES;
+template <typename T, bool TANH_IN, int HC>
+__global__ __launch_bounds__(512) void me_bwd_dx_dma_kernel(const T* __restrict__ dpre,
+                                                              const T* __restrict__ weight,
+                                                              const T* __restrict__ x, T* __restrict__ dx,
+                                                              BandSched sc, MaskArgs a) {
+  constexpr int S = HC == 128 ? PMSST_ME_DX_STAGES : PMSST_ME_DX256_STAGES;
   static_assert(S >= 3 && S <= 8, "stages");
-  __shared__ __attribute__((aligned(1024))) char lds[S * kDxStage];
+  constexpr int NW = HC / 32;              // waves: (HC / 64) x 2
+  constexpr int kU = HC / 8;               // 16-byte units per weight K-row
+  constexpr int kWTile = kChunkK * HC * 2;  // weight tile bytes; the dpre tile (8 KB) follows
+  constexpr int kStage = kWTile + 8192;
+  constexpr int kDI = 8 / NW;               // dpre DMAs per wave and stage (2 weight DMAs each)
+  static_assert(HC == 128 || HC == 256, "hidden columns per block");
+  __shared__ __attribute__((aligned(1024))) char lds[S * kStage];
   int band;
   uint32_t mt, hc, nhc_u;
   if (!sched_block<true>(sc, band, mt, hc, nhc_u)) return;
@@ -575,48 +586,48 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_dma_kernel(const T* __
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int wr = wave >> 1, wc = wave & 1;
+  const int wr = wave >> 1, wc = wave & 1;  // hidden columns 64 wr .., rows 64 wc ..
   const int nk = (K + kChunkK - 1) / kChunkK;
   const int kbeg = K - nk * kChunkK;  // multiple of 8 (I % 4 == 0)
 
-  // DMA pieces of this lane: t = 0, 1 weight K-rows (unit ua), t = 0, 1 dpre rows (unit ub)
-  uint32_t aoff[2], aoff0[2], boff[2], boff0[2];  // byte offsets from the chunk's bases (full / chunk 0)
+  // DMA pieces of this lane.  Weight instruction t (of 2) of wave w is q = w + NW t: K-rows
+  // (64 / kU) q + lane / kU, unit lane % kU of the row (logical unit ^ swz_mn).  dpre instruction
+  // t (of kDI) is q = w + NW t: rows 16 q + lane / 4, unit (lane % 4) ^ swz_k.
+  uint32_t aoff[2], aoff0[2], boff[kDI], boff0[kDI];  // byte offsets from the chunk's bases (full / chunk 0)
   bool aok0[2], bok0;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int kr = 4 * (wave + 4 * t) + (lane >> 4);
-    const int ua = (lane & 15) ^ swz_mn(kr);
+    const int kr = (64 / kU) * (wave + NW * t) + lane / kU;
+    const int ua = (lane % kU) ^ swz_mn(kr);
     aoff[t] = static_cast<uint32_t>((kr * H + 8 * ua) * 2);
     aok0[t] = kbeg + kr >= 0;
     aoff0[t] = aok0[t] ? aoff[t] : static_cast<uint32_t>((-kbeg * H + 8 * ua) * 2);  // row j = 0
   }
   {
-    const int ub = (lane & 3) ^ swz_k((lane >> 2) & 15);  // rows 16 w + lane / 4 (+ 64): same swizzle
+    const int ub = (lane & 3) ^ swz_k((lane >> 2) & 15);  // rows 16 q + lane / 4: same swizzle
     bok0 = kbeg + 8 * ub >= 0;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int mr = 64 * t + 16 * wave + (lane >> 2);
+    for (int t = 0; t < kDI; ++t) {
+      const int mr = 16 * (wave + NW * t) + (lane >> 2);
       const int mrc = mr < rows_valid ? mr : rows_valid - 1;
       boff[t] = static_cast<uint32_t>((mrc * pitch2 + 8 * ub) * 2);
       boff0[t] = bok0 ? boff[t] : static_cast<uint32_t>((mrc * pitch2 - kbeg) * 2);  // column j = 0
     }
   }
   const char* wsrc0 = reinterpret_cast<const char*>(weight + static_cast<int64_t>(2) * off * H +
-                                                    static_cast<int64_t>(kbeg) * H + hc * kDxHC);
+                                                    static_cast<int64_t>(kbeg) * H + hc * HC);
   const char* dsrc0 = reinterpret_cast<const char*>(dpre + m0 * pitch2 + 2 * off + kbeg);
   const uint32_t lds0 = lds_addr(lds);
 
   auto dma = [&](int kc, int stage) {  // K chunk kc into `stage`
     const char* wsrc = wsrc0 + static_cast<int64_t>(kc) * kChunkK * H * 2;
     const char* dsrc = dsrc0 + kc * kChunkK * 2;
-    char* st = lds + stage * kDxStage;
+    char* st = lds + stage * kStage;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      __builtin_amdgcn_global_load_lds(wsrc + (kc == 0 ? aoff0[t] : aoff[t]), st + (wave + 4 * t) * 1024, 16, 0,
-                                       0);
-      __builtin_amdgcn_global_load_lds(dsrc + (kc == 0 ? boff0[t] : boff[t]),
-                                       st + 8192 + (wave + 4 * t) * 1024, 16, 0, 0);
-    }
+    for (int t = 0; t < 2; ++t) dma_lds16(wsrc + (kc == 0 ? aoff0[t] : aoff[t]), st + (wave + NW * t) * 1024);
+#pragma unroll
+    for (int t = 0; t < kDI; ++t)
+      dma_lds16(dsrc + (kc == 0 ? boff0[t] : boff[t]), st + kWTile + (wave + NW * t) * 1024);
   };
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
@@ -624,8 +635,8 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_dma_kernel(const T* __
 
   uint32_t fa[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) fa[i] = frag_mn_addr(lds0, 64 * wr + 16 * i, 2 * kDxHC, lane);
-  const uint32_t fb = frag_k_addr(lds0 + 8192, 64 * wc, lane);
+  for (int i = 0; i < 4; ++i) fa[i] = frag_mn_addr(lds0, 64 * wr + 16 * i, 2 * HC, lane);
+  const uint32_t fb = frag_k_addr(lds0 + kWTile, 64 * wc, lane);
   f32x4_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -633,36 +644,37 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_dma_kernel(const T* __
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int s = 0; s < nk; ++s) {
-    // chunk s landed once at most 4 nd DMAs are outstanding, nd = chunks issued after it
+    // chunk s landed once at most (2 + kDI) nd DMAs are outstanding, nd = chunks issued after it
     // (s + 1 .. s + S - 2 that exist); the loop issues no other memory operation
     const int nd = nk - 1 - s < S - 2 ? nk - 1 - s : S - 2;
     static_assert(S - 2 <= 6, "wait table");
     switch (nd) {
       case 0: vm_wait<0>(); break;
-      case 1: vm_wait<4>(); break;
-      case 2: vm_wait<8>(); break;
-      case 3: vm_wait<12>(); break;
-      case 4: vm_wait<16>(); break;
-      case 5: vm_wait<20>(); break;
-      default: vm_wait<24>(); break;
+      case 1: vm_wait<2 + kDI>(); break;
+      case 2: vm_wait<2 * (2 + kDI)>(); break;
+      case 3: vm_wait<3 * (2 + kDI)>(); break;
+      case 4: vm_wait<4 * (2 + kDI)>(); break;
+      case 5: vm_wait<5 * (2 + kDI)>(); break;
+      default: vm_wait<6 * (2 + kDI)>(); break;
     }
     if (s == 0 && kbeg < 0) {
       // zero this lane's pieces of chunk 0 that lie below j = 0
       const u32x4_t z{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if (!aok0[t]) *reinterpret_cast<u32x4_t*>(lds + (wave + 4 * t) * 1024 + lane * 16) = z;
-        if (!bok0) *reinterpret_cast<u32x4_t*>(lds + 8192 + (wave + 4 * t) * 1024 + lane * 16) = z;
-      }
+      for (int t = 0; t < 2; ++t)
+        if (!aok0[t]) *reinterpret_cast<u32x4_t*>(lds + (wave + NW * t) * 1024 + lane * 16) = z;
+#pragma unroll
+      for (int t = 0; t < kDI; ++t)
+        if (!bok0) *reinterpret_cast<u32x4_t*>(lds + kWTile + (wave + NW * t) * 1024 + lane * 16) = z;
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (s + S - 1 < nk) dma(s + S - 1, (s + S - 1) % S);  // into the stage chunk s - 1 used
-    const uint32_t so = static_cast<uint32_t>((s % S) * kDxStage);
+    const uint32_t so = static_cast<uint32_t>((s % S) * kStage);
     u32x4_t af[4], bfr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = lds_read_tr_pair(fa[i] + so, 4 * 2 * kDxHC);
+    for (int i = 0; i < 4; ++i) af[i] = lds_read_tr_pair(fa[i] + so, 4 * 2 * HC);
 #pragma unroll
     for (int j = 0; j < 4; ++j) bfr[j] = lds_read_b128(fb + so + 1024 * j);
     lds_wait(af, bfr);
@@ -674,11 +686,12 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_dma_kernel(const T* __
 
   // epilogue through LDS: lane holds h = 64 wr + 16 i + 4 (lane / 16) + r of rows
   // m = 64 wc + 16 j + lane % 16 (8-byte runs of 16 rows per instruction); the tile is staged as
-  // [128 m][128 h] (row pitch 272 bytes) and written back as 16-byte pieces, 256 contiguous
+  // [128 m][HC h] (row pitch 2 HC + 16 bytes) and written back as 16-byte pieces, 2 HC contiguous
   // bytes per row, so HBM sees whole lines.  With a tanh input the factor 1 - x^2 is applied
   // before staging (x read at the lane's own positions), so dx is rounded once.
   __syncthreads();  // every wave is done with the ring (its last wait was vmcnt(0))
-  constexpr int kOP = 136;  // staged row pitch in elements
+  constexpr int kOP = HC + 8;  // staged row pitch in elements
+  static_assert(kDxBMd * kOP * 2 <= S * kStage, "staging tile");
   T* ot = reinterpret_cast<T*>(lds);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -690,7 +703,7 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_dma_kernel(const T* __
       if (TANH_IN) {
         const int mc = m < rows_valid ? m : rows_valid - 1;
         float tx[4];
-        load_pack<T, 4>(x + ((m0 + mc) * a.NB + band) * H + hc * kDxHC + h, tx);
+        load_pack<T, 4>(x + ((m0 + mc) * a.NB + band) * H + hc * HC + h, tx);
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] *= 1.0f - tx[r] * tx[r];
       }
@@ -698,12 +711,12 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_dma_kernel(const T* __
     }
   }
   __syncthreads();
-  const int c8 = (threadIdx.x & 15) * 8;
+  const int c8 = static_cast<int>(threadIdx.x % kU) * 8;
 #pragma unroll
   for (int p = 0; p < kDxBMd / 16; ++p) {
-    const int row = static_cast<int>(threadIdx.x >> 4) + 16 * p;
+    const int row = static_cast<int>(threadIdx.x / kU) + 16 * p;
     if (row < rows_valid)
-      *reinterpret_cast<u32x4_t*>(dx + ((m0 + row) * a.NB + band) * H + hc * kDxHC + c8) =
+      *reinterpret_cast<u32x4_t*>(dx + ((m0 + row) * a.NB + band) * H + hc * HC + c8) =
           *reinterpret_cast<const u32x4_t*>(ot + row * kOP + c8);
   }
 }
@@ -1061,8 +1074,9 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
     if (rc != PMSST_OK) return rc;
     BandSched dsc;
     uint32_t dx_per_xcd = 0;
-    const int nhc = static_cast<int>(H / kDxHC);
-    const bool dx_dma = sizeof(T) == 2 && PMSST_ME_DX_DMA && a.vec4 && H % kDxHC == 0 && al(weight, 16) &&
+    const int dx_hc = PMSST_ME_DX_HC == 256 && H % 256 == 0 ? 256 : 128;
+    const int nhc = static_cast<int>(H / dx_hc);
+    const bool dx_dma = sizeof(T) == 2 && PMSST_ME_DX_DMA && a.vec4 && H % dx_hc == 0 && al(weight, 16) &&
                         al(dx, 16) &&
                         (static_cast<int64_t>(kChunkK) * H + H) * 2 < (int64_t{1} << 31) &&
                         (kDxBMd * 2 * static_cast<int64_t>(hm.F) + 64) * 2 < (int64_t{1} << 31) &&
@@ -1076,12 +1090,18 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
     if constexpr (sizeof(T) == 2) {
       if (dx_dma) {
         const dim3 gd(dx_per_xcd * kXcds);
-        if (input_act == PMSST_ACT_TANH)
-          hipLaunchKernelGGL((me_bwd_dx_dma_kernel<T, true>), gd, dim3(kGemmThreads), 0, stream, dpre,
-                             static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), dsc, a);
+        const T* wp = static_cast<const T*>(weight);
+        const T* xp = static_cast<const T*>(x);
+        T* dxp = static_cast<T*>(dx);
+        const bool tanh_in = input_act == PMSST_ACT_TANH;
+        if (dx_hc == 256 && tanh_in)
+          me_bwd_dx_dma_kernel<T, true, 256><<<gd, dim3(512), 0, stream>>>(dpre, wp, xp, dxp, dsc, a);
+        else if (dx_hc == 256)
+          me_bwd_dx_dma_kernel<T, false, 256><<<gd, dim3(512), 0, stream>>>(dpre, wp, xp, dxp, dsc, a);
+        else if (tanh_in)
+          me_bwd_dx_dma_kernel<T, true, 128><<<gd, dim3(256), 0, stream>>>(dpre, wp, xp, dxp, dsc, a);
         else
-          hipLaunchKernelGGL((me_bwd_dx_dma_kernel<T, false>), gd, dim3(kGemmThreads), 0, stream, dpre,
-                             static_cast<const T*>(weight), static_cast<const T*>(x), static_cast<T*>(dx), dsc, a);
+          me_bwd_dx_dma_kernel<T, false, 128><<<gd, dim3(256), 0, stream>>>(dpre, wp, xp, dxp, dsc, a);
         rc = check_launch("me_bwd_dx_dma_kernel");
         if (rc != PMSST_OK) return rc;
       }
