@@ -778,39 +778,53 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __rest
   }
 }
 
-// dW on the DMA ring (16-bit, 4-aligned widths, H % 128 == 0): dW_b^T[h][j] =
-// sum_m x[m][b][h] dpre[m][2 off + j], K = M.  Tile 128 h x 128 j per block (band, hidden
-// tile, j chunk); both operands are moved as stored (32 K-rows m x 128 columns, 8 KB each) and
-// read as transposed fragments, so each x row slab is re-read once per 128 columns of dpre
-// instead of once per 64.  K chunks end at M; chunk 0's rows m < 0 are read from row 0 and
-// zeroed in LDS once the DMA has landed.  DMA: 16 dwordx4 per stage, wave w moves x K-rows
-// 4w .. + 3 and 16 + 4w .. + 3 and the same dpre K-rows.  dbias[j] = sum_m dpre[m][j] comes
-// from the blocks of hidden tile 0: their two top waves add 4 MFMAs per chunk with an all-ones
-// A fragment.  The tile leaves through LDS: rows j of dW_b, 256 contiguous bytes each.  Three
-// stages (48 KB) let three blocks share a CU.
+// dW on the DMA ring (16-bit, 4-aligned widths, H % HT == 0): dW_b^T[h][j] =
+// sum_m x[m][b][h] dpre[m][2 off + j], K = M.  Tile HT h x 128 j per block (band, hidden tile,
+// j chunk), HT = 128 on 4 waves (2 x 2 of 64 x 64; 256 on 8 waves is built too: at configs[1] it
+// measured 102 us of mask backward against 94.5 us with 128, whose 48 KB ring keeps three blocks
+// per CU); both
+// operands are moved as stored (32 K-rows m x HT or 128 columns) and read as transposed
+// fragments, so each x row slab is re-read once per 128 columns of dpre and each dpre slab once
+// per HT hidden columns.  K chunks end at M; chunk 0's rows m < 0 are read from row 0 and zeroed
+// in LDS once the DMA has landed.  DMA per wave and stage: 2 x pieces and 8 / waves dpre pieces.
+// dbias[j] = sum_m dpre[m][j] comes from the blocks of hidden tile 0: their two waves of hidden
+// columns 0 .. 63 add 4 MFMAs per chunk with an all-ones A fragment.  The tile leaves through
+// LDS as rows j of dW_b, 2 HT contiguous bytes each.  Three stages (48 or 72 KB) keep two or three
+// blocks per CU.
 #ifndef PMSST_ME_DW_DMA
 #define PMSST_ME_DW_DMA 1
 #endif
 #ifndef PMSST_ME_DW_STAGES
 #define PMSST_ME_DW_STAGES 3
 #endif
-constexpr int kDwStage = 16384;
-constexpr int kDwT = 128;  // hidden and j columns per block
+#ifndef PMSST_ME_DW256_STAGES
+#define PMSST_ME_DW256_STAGES 3
+#endif
+// Hidden columns per block: 128 (4 waves), or 256 (8 waves) when the hidden size allows.
+#ifndef PMSST_ME_DW_HT
+#define PMSST_ME_DW_HT 128
+#endif
+constexpr int kDwT = 128;  // j columns per block
 
-template <typename T>
-__global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_dma_kernel(const T* __restrict__ dpre,
-                                                                     const T* __restrict__ x, T* __restrict__ dw,
-                                                                     T* __restrict__ dbias, BandSched sc,
-                                                                     MaskArgs a) {
-  constexpr int S = PMSST_ME_DW_STAGES;
+template <typename T, int HT>
+__global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict__ dpre, const T* __restrict__ x,
+                                                           T* __restrict__ dw, T* __restrict__ dbias, BandSched sc,
+                                                           MaskArgs a) {
+  constexpr int S = HT == 128 ? PMSST_ME_DW_STAGES : PMSST_ME_DW256_STAGES;
   static_assert(S >= 3 && S <= 8, "stages");
-  __shared__ __attribute__((aligned(1024))) char lds[S * kDwStage];
+  static_assert(HT == 128 || HT == 256, "hidden columns per block");
+  constexpr int NW = HT / 32;              // waves: (HT / 64) x 2
+  constexpr int kU = HT / 8;               // 16-byte units per x K-row
+  constexpr int kXTile = kChunkK * HT * 2;  // x tile bytes; the dpre tile (32 K-rows x 128 j) follows
+  constexpr int kStage = kXTile + 8192;
+  constexpr int kDI = 8 / NW;               // dpre DMAs per wave and stage (2 x DMAs each)
+  __shared__ __attribute__((aligned(1024))) char lds[S * kStage];
   int band;
   uint32_t mt0, sub, per_unit;
   if (!sched_block(sc, band, mt0, sub, per_unit)) return;
   const int H = a.H;
-  const int htiles = H / kDwT;
-  const int h0 = static_cast<int>(sub % htiles) * kDwT;
+  const int htiles = H / HT;
+  const int h0 = static_cast<int>(sub % htiles) * HT;
   const int j0 = static_cast<int>(sub / htiles) * kDwT;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
@@ -820,24 +834,31 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_dma_kernel(const T* __
   const int64_t xstride = static_cast<int64_t>(a.NB) * H;  // elements between rows m of x
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int wr = wave >> 1, wc = wave & 1;
+  const int wr = wave >> 1, wc = wave & 1;  // hidden columns 64 wr .., j columns 64 wc ..
   const int nk = (M + kChunkK - 1) / kChunkK;
   const int kbeg = M - nk * kChunkK;
 
-  // DMA pieces: t = 0, 1 -> K-row kr[t] of both tiles; x unit ua, dpre unit ub (clamped to the
-  // band's last 8 columns past 2 I)
-  uint32_t aoff[2], aoff0[2], boff[2], boff0[2];
-  bool ok0[2];
+  // DMA pieces.  x instruction t (of 2) of wave w is q = w + NW t: K-rows (64 / kU) q + lane / kU,
+  // unit lane % kU of the row (logical unit ^ swz_mn).  dpre instruction t (of kDI) is q = w + NW t:
+  // K-rows 4 q + lane / 16, unit lane % 16 (columns past 2 I clamped to the band's last 8).
+  uint32_t aoff[2], aoff0[2], boff[kDI], boff0[kDI];
+  bool aok0[2], bok0[kDI];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int kr = 4 * (wave + 4 * t) + (lane >> 4);
+    const int kr = (64 / kU) * (wave + NW * t) + lane / kU;
+    const int u = (lane % kU) ^ swz_mn(kr);
+    aoff[t] = static_cast<uint32_t>((kr * xstride + 8 * u) * 2);
+    aok0[t] = kbeg + kr >= 0;
+    aoff0[t] = aok0[t] ? aoff[t] : static_cast<uint32_t>((-kbeg * xstride + 8 * u) * 2);  // row m = 0
+  }
+#pragma unroll
+  for (int t = 0; t < kDI; ++t) {
+    const int kr = 4 * (wave + NW * t) + (lane >> 4);
     const int u = (lane & 15) ^ swz_mn(kr);
     const int jc = j0 + 8 * u < K2 ? j0 + 8 * u : K2 - 8;
-    aoff[t] = static_cast<uint32_t>((kr * xstride + 8 * u) * 2);
     boff[t] = static_cast<uint32_t>((kr * pitch2 + jc) * 2);
-    ok0[t] = kbeg + kr >= 0;
-    aoff0[t] = ok0[t] ? aoff[t] : static_cast<uint32_t>((-kbeg * xstride + 8 * u) * 2);  // row m = 0
-    boff0[t] = ok0[t] ? boff[t] : static_cast<uint32_t>((-kbeg * pitch2 + jc) * 2);
+    bok0[t] = kbeg + kr >= 0;
+    boff0[t] = bok0[t] ? boff[t] : static_cast<uint32_t>((-kbeg * pitch2 + jc) * 2);
   }
   const char* xsrc0 = reinterpret_cast<const char*>(x + (static_cast<int64_t>(kbeg) * a.NB + band) * H + h0);
   const char* dsrc0 = reinterpret_cast<const char*>(dpre + static_cast<int64_t>(kbeg) * pitch2 + 2 * off);
@@ -846,13 +867,12 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_dma_kernel(const T* __
   auto dma = [&](int kc, int stage) {  // K chunk kc into `stage`
     const char* xs = xsrc0 + static_cast<int64_t>(kc) * kChunkK * xstride * 2;
     const char* ds = dsrc0 + static_cast<int64_t>(kc) * kChunkK * pitch2 * 2;
-    char* st = lds + stage * kDwStage;
+    char* st = lds + stage * kStage;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      __builtin_amdgcn_global_load_lds(xs + (kc == 0 ? aoff0[t] : aoff[t]), st + (wave + 4 * t) * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(ds + (kc == 0 ? boff0[t] : boff[t]), st + 8192 + (wave + 4 * t) * 1024, 16,
-                                       0, 0);
-    }
+    for (int t = 0; t < 2; ++t) dma_lds16(xs + (kc == 0 ? aoff0[t] : aoff[t]), st + (wave + NW * t) * 1024);
+#pragma unroll
+    for (int t = 0; t < kDI; ++t)
+      dma_lds16(ds + (kc == 0 ? boff0[t] : boff[t]), st + kXTile + (wave + NW * t) * 1024);
   };
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
@@ -861,16 +881,16 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_dma_kernel(const T* __
   uint32_t fa[4], fb[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    fa[i] = frag_mn_addr(lds0, 64 * wr + 16 * i, 2 * kDwT, lane);
-    fb[i] = frag_mn_addr(lds0 + 8192, 64 * wc + 16 * i, 2 * kDwT, lane);
+    fa[i] = frag_mn_addr(lds0, 64 * wr + 16 * i, 2 * HT, lane);
+    fb[i] = frag_mn_addr(lds0 + kXTile, 64 * wc + 16 * i, 2 * kDwT, lane);
   }
   f32x4_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // dbias = ones^T dpre: the two waves of the first hidden tile's top half also multiply their
-  // dpre fragments by an all-ones A fragment (every row of the product is the column sum)
+  // dbias = ones^T dpre: the two waves of the first hidden tile's first 64 columns also multiply
+  // their dpre fragments by an all-ones A fragment (every row of the product is the column sum)
   const bool do_bias = h0 == 0 && wr == 0;
   const uint32_t one2 = std::is_same<T, bf16>::value ? 0x3F803F80u : 0x3C003C00u;
   const u32x4_t ones{one2, one2, one2, one2};
@@ -879,35 +899,35 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_dma_kernel(const T* __
   for (int j = 0; j < 4; ++j) accb[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int s = 0; s < nk; ++s) {
-    // chunk s landed once at most 4 nd DMAs are outstanding, nd = chunks issued after it
+    // chunk s landed once at most (2 + kDI) nd DMAs are outstanding, nd = chunks issued after it
     const int nd = nk - 1 - s < S - 2 ? nk - 1 - s : S - 2;
     static_assert(S - 2 <= 6, "wait table");
     switch (nd) {
       case 0: vm_wait<0>(); break;
-      case 1: vm_wait<4>(); break;
-      case 2: vm_wait<8>(); break;
-      case 3: vm_wait<12>(); break;
-      case 4: vm_wait<16>(); break;
-      case 5: vm_wait<20>(); break;
-      default: vm_wait<24>(); break;
+      case 1: vm_wait<2 + kDI>(); break;
+      case 2: vm_wait<2 * (2 + kDI)>(); break;
+      case 3: vm_wait<3 * (2 + kDI)>(); break;
+      case 4: vm_wait<4 * (2 + kDI)>(); break;
+      case 5: vm_wait<5 * (2 + kDI)>(); break;
+      default: vm_wait<6 * (2 + kDI)>(); break;
     }
-    if (s == 0 && kbeg < 0) {
+    if (s == 0 && kbeg < 0) {  // zero this wave's own pieces of chunk 0 that lie before row 0
       const u32x4_t z{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int t = 0; t < 2; ++t)
-        if (!ok0[t]) {
-          *reinterpret_cast<u32x4_t*>(lds + (wave + 4 * t) * 1024 + lane * 16) = z;
-          *reinterpret_cast<u32x4_t*>(lds + 8192 + (wave + 4 * t) * 1024 + lane * 16) = z;
-        }
+        if (!aok0[t]) *reinterpret_cast<u32x4_t*>(lds + (wave + NW * t) * 1024 + lane * 16) = z;
+#pragma unroll
+      for (int t = 0; t < kDI; ++t)
+        if (!bok0[t]) *reinterpret_cast<u32x4_t*>(lds + kXTile + (wave + NW * t) * 1024 + lane * 16) = z;
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (s + S - 1 < nk) dma(s + S - 1, (s + S - 1) % S);  // into the stage chunk s - 1 used
-    const uint32_t so = static_cast<uint32_t>((s % S) * kDwStage);
+    const uint32_t so = static_cast<uint32_t>((s % S) * kStage);
     u32x4_t af[4], bfr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = lds_read_tr_pair(fa[i] + so, 4 * 2 * kDwT);
+    for (int i = 0; i < 4; ++i) af[i] = lds_read_tr_pair(fa[i] + so, 4 * 2 * HT);
 #pragma unroll
     for (int j = 0; j < 4; ++j) bfr[j] = lds_read_tr_pair(fb[j] + so, 4 * 2 * kDwT);
     lds_wait(af, bfr);
@@ -931,9 +951,10 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_dma_kernel(const T* __
   }
 
   // epilogue through LDS: lane holds h = 64 wr + 16 i + 4 (lane / 16) + r of columns
-  // j = 64 wc + 16 jj + lane % 16; staged as [128 j][128 h] (row pitch 272 bytes)
+  // j = 64 wc + 16 jj + lane % 16; staged as [128 j][HT h] (row pitch 2 HT + 16 bytes)
   __syncthreads();  // every wave is done with the ring (its last wait was vmcnt(0))
-  constexpr int kOP = kDwT + 8;
+  constexpr int kOP = HT + 8;
+  static_assert(kDwT * kOP * 2 <= S * kStage, "staging tile");
   T* ot = reinterpret_cast<T*>(lds);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -946,10 +967,10 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_dma_kernel(const T* __
   }
   __syncthreads();
   T* dwb = dw + (static_cast<int64_t>(2) * off + j0) * H + h0;  // rows j of dW_b
-  const int c8 = (threadIdx.x & 15) * 8;
+  const int c8 = static_cast<int>(threadIdx.x % kU) * 8;
 #pragma unroll
   for (int p = 0; p < kDwT / 16; ++p) {
-    const int jj = static_cast<int>(threadIdx.x >> 4) + 16 * p;
+    const int jj = static_cast<int>(threadIdx.x / kU) + 16 * p;
     if (jj < jv)
       *reinterpret_cast<u32x4_t*>(dwb + static_cast<int64_t>(jj) * H + c8) =
           *reinterpret_cast<const u32x4_t*>(ot + jj * kOP + c8);
@@ -1126,15 +1147,20 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
   if constexpr (sizeof(T) == 2) {
     BandSched wsc;
     uint32_t dw_per_xcd = 0;
-    const int htl = static_cast<int>(H / kDwT);
-    if (PMSST_ME_DW_DMA && M >= kChunkK && a.vec4 && H % kDwT == 0 && al(x, 16) && al(dw, 16) &&
+    const int dw_ht = PMSST_ME_DW_HT == 256 && H % 256 == 0 ? 256 : 128;
+    const int htl = static_cast<int>(H / dw_ht);
+    if (PMSST_ME_DW_DMA && M >= kChunkK && a.vec4 && H % dw_ht == 0 && al(x, 16) && al(dw, 16) &&
         (static_cast<int64_t>(kChunkK) * hm.NB * H + H) * 2 < (int64_t{1} << 31) &&
         (static_cast<int64_t>(kChunkK) * 2 * hm.F + 2 * hm.F) * 2 < (int64_t{1} << 31) &&
         build_band_sched(hm.NB, 1,
                          [&](int b) { return static_cast<int64_t>(htl) * ((2 * dim_inputs[b] + kDwT - 1) / kDwT); },
                          &wsc, &dw_per_xcd)) {
-      hipLaunchKernelGGL((me_bwd_dw_dma_kernel<T>), dim3(dw_per_xcd * kXcds), dim3(kGemmThreads), 0, stream, dpre,
-                         static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(dbias), wsc, a);
+      if (dw_ht == 256)
+        hipLaunchKernelGGL((me_bwd_dw_dma_kernel<T, 256>), dim3(dw_per_xcd * kXcds), dim3(512), 0, stream, dpre,
+                           static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(dbias), wsc, a);
+      else
+        hipLaunchKernelGGL((me_bwd_dw_dma_kernel<T, 128>), dim3(dw_per_xcd * kXcds), dim3(256), 0, stream, dpre,
+                           static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(dbias), wsc, a);
       return check_launch("me_bwd_dw_dma_kernel");  // dbias summed by the kernel
     }
   }
