@@ -73,7 +73,7 @@ def _args(argv=None):
 
 
 class Workload:
-    """Seeded synthetic inputs of configs[1] (the seeds of the survey's measurement plan)."""
+    """Seeded synthetic inputs of configs[1] (fixed seeds, so every run times the same data)."""
 
     def __init__(self, torch, ext, dtype):
         import numpy as np

@@ -1,5 +1,5 @@
-"""CPU tests of the Mel-band RoFormer restatement: the mel band layout (pinned against the
-survey's independent computation: 60 bands at 44.1 kHz / n_fft 2048 give 6 to 130 bins per band,
+"""CPU tests of the Mel-band RoFormer restatement: the mel band layout (pinned against figures
+computed independently of this code from the mel scale: 60 bands at 44.1 kHz / n_fft 2048 give 6 to 130 bins per band,
 1979 (bin, band) pairs, 38 distinct widths, every bin in one or two bands), the model's stock
 gather / average against the oracle, and the fused autograd Functions through a CPU stand-in of the
 extension computing with the oracle."""
@@ -15,7 +15,7 @@ from pymsst_amd import fused_roformer as fr
 from pymsst_amd.core.mel_band_roformer import MelBandRoformer, mel_band_bins, mel_filterbank
 
 
-def test_mel_band_layout_matches_survey_figures():
+def test_mel_band_layout_matches_independent_figures():
     bins = mel_band_bins(44100, 2048, 60)
     widths = [b.size for b in bins]
     assert len(bins) == 60 and min(widths) == 6 and max(widths) == 130
