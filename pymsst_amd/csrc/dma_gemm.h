@@ -17,8 +17,9 @@
 //    ds_read_b64_tr_b16 (gfx950 transpose read: in each 16-lane group, lane i receives
 //    element i % 4 of the 4 elements lane 4 k + i / 4 addressed, k = 0..3), which hand
 //    lane i of the group the 4 K values of column c0 + i.
-// Both swizzles keep every fragment read free of bank conflicts for a 32-bank (8 lanes
-// per pass) and a 64-bank (16 lanes per pass) LDS.
+// On gfx950 the swizzled fragment reads of K-contiguous tiles still take 4 LDS bank-conflict
+// cycles per ds_read_b128 (SQ_LDS_BANK_CONFLICT on a probe kernel; contiguous 16-byte reads take
+// none); the transpose reads at a 512-byte pitch take 2 with swz_mn.
 #pragma once
 
 #include <type_traits>
@@ -31,6 +32,15 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ int swz_k(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 __device__ __forceinline__ int swz_mn(int k) { return 2 * (k & 3); }
+// swz_mn for a 512-byte K-row pitch: a transpose read covers K-rows 8 g + 0..3 (g = 0..3), which
+// start on the same bank at this pitch; spreading them over 16 unit pairs makes the read
+// conflict-free (0 conflict cycles against 2 for swz_mn, measured on a probe kernel).  Rows k
+// and k + 4 keep the same swizzle, as the second read of a fragment needs.
+template <int PITCH>
+__device__ __forceinline__ int swz_mn_p(int k) {
+  if constexpr (PITCH == 512) return 2 * ((k & 3) | (((k >> 3) & 3) << 2));
+  else return swz_mn(k);
+}
 
 template <typename T>
 __device__ __forceinline__ f32x4_t mfma_raw(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
@@ -61,6 +71,15 @@ __device__ __forceinline__ uint32_t frag_mn_addr(uint32_t region, int c0, int pi
   const int col = c0 + 4 * (j & 3);
   const int unit = col >> 3;
   return region + static_cast<uint32_t>(k * pitch + 16 * (unit ^ swz_mn(k)) + 2 * (col & 7));
+}
+
+template <int PITCH>
+__device__ __forceinline__ uint32_t frag_mn_addr_p(uint32_t region, int c0, int lane) {
+  const int j = lane & 15, g = lane >> 4;
+  const int k = 8 * g + (j >> 2);
+  const int col = c0 + 4 * (j & 3);
+  const int unit = col >> 3;
+  return region + static_cast<uint32_t>(k * PITCH + 16 * (unit ^ swz_mn_p<PITCH>(k)) + 2 * (col & 7));
 }
 
 __device__ __forceinline__ u32x4_t lds_read_b128(uint32_t addr) {

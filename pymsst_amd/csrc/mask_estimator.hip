@@ -215,10 +215,11 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_dma_kernel(const T* __res
   // DMA pieces of this lane: instruction t moves tile row R = 64 wave + 16 t + lane / 4
   // (R % 16 = lane / 4), physical unit lane % 4, i.e. logical K unit u = (lane % 4) ^ swz(lane / 4)
   const uint32_t u = static_cast<uint32_t>((lane & 3) ^ swz_k(lane >> 2));
+  const int rsub = lane >> 2;
   uint32_t soff[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const int R = 64 * wave + 16 * t + (lane >> 2);
+    const int R = 64 * wave + 16 * t + rsub;
     if (wave < 2) {
       const int l = l0 + 16 * (R >> 5) + (R & 15);
       const int lc = l < I ? l : I - 1;
@@ -598,7 +599,7 @@ __global__ __launch_bounds__(512) void me_bwd_dx_dma_kernel(const T* __restrict_
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int kr = (64 / kU) * (wave + NW * t) + lane / kU;
-    const int ua = (lane % kU) ^ swz_mn(kr);
+    const int ua = (lane % kU) ^ swz_mn_p<2 * HC>(kr);
     aoff[t] = static_cast<uint32_t>((kr * H + 8 * ua) * 2);
     aok0[t] = kbeg + kr >= 0;
     aoff0[t] = aok0[t] ? aoff[t] : static_cast<uint32_t>((-kbeg * H + 8 * ua) * 2);  // row j = 0
@@ -635,7 +636,7 @@ __global__ __launch_bounds__(512) void me_bwd_dx_dma_kernel(const T* __restrict_
 
   uint32_t fa[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) fa[i] = frag_mn_addr(lds0, 64 * wr + 16 * i, 2 * HC, lane);
+  for (int i = 0; i < 4; ++i) fa[i] = frag_mn_addr_p<2 * HC>(lds0, 64 * wr + 16 * i, lane);
   const uint32_t fb = frag_k_addr(lds0 + kWTile, 64 * wc, lane);
   f32x4_t acc[4][4];
 #pragma unroll
