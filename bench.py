@@ -48,9 +48,9 @@ SINGLE_KERNEL_OPS = {
 # dispatch x 1024).  The factors are what the same counters read for a 1 GiB bf16 copy (torch.mul) in
 # the same runs: FETCH_SIZE 524310 KiB for 1048576 KiB read, WRITE_SIZE 1048576 KiB for 1048576 written.
 TRAFFIC_PER_LAUNCH: dict = {
-    "me_fwd_dma_kernel": (57630 * 2 + 26692) * 1024,
+    "me_fwd_dma_kernel": (57624 * 2 + 26676) * 1024,
     "norm_rot_fwd_kernel": (32278 * 2 + 65984) * 1024,
-    "bs_fwd_kernel": (14256 * 2 + 26454) * 1024,
+    "bs_fwd_kernel": (14253 * 2 + 26452) * 1024,
 }
 BSR_WIDTHS = tuple([8] * 24 + [16] * 12 + [48] * 8 + [96] * 8 + [192] * 8 + [512, 516])
 
