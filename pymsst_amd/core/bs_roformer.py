@@ -197,6 +197,10 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
         return F.l1_loss(torch.view_as_real(est), torch.view_as_real(tspec.reshape(est.shape)))
 
     def loss(self, recon: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+        # one stem: recon is [B, C, L] (stem axis squeezed) and a stacked target [B, 1, C, L] drops
+        # its singleton stem axis, so the loss compares item with item instead of broadcasting
+        if target.ndim == recon.ndim + 1 and target.shape[1] == 1:
+            target = target[:, 0]
         if target.ndim == recon.ndim - 1:
             target = target.unsqueeze(-2)
         target = target[..., : recon.shape[-1]]

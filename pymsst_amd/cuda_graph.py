@@ -18,12 +18,12 @@ With a target, ``forward`` returns the model's loss: the waveform losses after t
 spectrogram loss (``loss="spec_l1"``) from the graphed masked spectrum permuted back to
 ``[B, stems, F*C, T]``.
 
-On ROCm (``torch.version.hip``) a training capture (parameters that require gradients) is refused by
-default and ``forward`` runs eagerly: on ROCm 7.2 with torch 2.10 the captured backward of torch's
-bias / normalisation reductions records memset nodes that hold on the first replay only, so later
-replays return wrong gradients, and not always on the second replay (a capture-time check passed
-two replays and a later one failed).  ``allow_hip_training_graphs=True`` captures anyway and still
-checks two replays against eager before using the graph.
+On ROCm (``torch.version.hip``) a training capture (parameters that require gradients) is refused and
+``forward`` runs eagerly: on ROCm 7.2 with torch 2.10 the captured backward of torch's bias /
+normalisation reductions records memset nodes, and memset nodes in a HIP graph hold on the first
+replay only, so later replays return wrong gradients.  There is no opt-in:
+``allow_hip_training_graphs=True`` raises ``ValueError`` on ROCm.  Captures without gradients
+(frozen parameters) are unaffected.
 
 The model is this build's restated BS-RoFormer (``pymsst_amd.core``): its ``_stft`` / ``_mask_core``
 / ``_finish`` split stands in for pymss-core's ``stft_roformer`` / ``_mask_stft_repr`` /
@@ -43,12 +43,12 @@ from typing import Callable
 import torch
 from torch import nn
 
-__all__ = ["CudaGraphRuntimeStatus", "HIP_TRAINING_GRAPH_REASON", "RoformerTrainingCudaGraph",
+__all__ = ["CudaGraphRuntimeStatus", "HIP_TRAINING_GRAPH_REASON", "RoformerTrainingCudaGraph", "capture_refusal",
            "normalize_cuda_graph_mode"]
 
 HIP_TRAINING_GRAPH_REASON = (
     "HIP graph replays of the training backward are not reliable on this ROCm stack (memset nodes recorded by "
-    "library reductions hold on the first replay only); pass allow_hip_training_graphs=True to capture anyway"
+    "library reductions hold on the first replay only); training captures are refused on ROCm"
 )
 
 
@@ -71,6 +71,17 @@ def normalize_cuda_graph_mode(value: str | None) -> str:
     if mode in {"stft_mask", "stft_mask_core", "roformer_stft_mask_core"}:
         return "stft_mask_core"
     raise ValueError("cuda_graph_mode must be one of: off, mask_core, stft_mask_core")
+
+
+def capture_refusal(device_type: str, training: bool, hip_version: str | None) -> str | None:
+    """Why a capture is not attempted (``None``: capture).  Non-CUDA tensors are refused as in
+    ``cuda_graph.py:44-46``; on ROCm a region whose parameters require gradients is refused because
+    its captured backward would hold memset nodes."""
+    if device_type != "cuda":
+        return "CUDA graph requires CUDA tensors"
+    if hip_version is not None and training:
+        return HIP_TRAINING_GRAPH_REASON
+    return None
 
 
 def _autocast(enabled: bool, dtype: torch.dtype):
@@ -109,6 +120,8 @@ class RoformerTrainingCudaGraph:
         self.mode = normalize_cuda_graph_mode(mode)
         if self.mode == "off":
             raise ValueError("RoformerTrainingCudaGraph requires an active graph mode")
+        if allow_hip_training_graphs and torch.version.hip is not None:
+            raise ValueError("allow_hip_training_graphs is not supported on ROCm: " + HIP_TRAINING_GRAPH_REASON)
         self.model = model
         self.amp_dtype = amp_dtype
         self.allow_hip_training_graphs = allow_hip_training_graphs
@@ -123,15 +136,13 @@ class RoformerTrainingCudaGraph:
 
     def capture(self, sample_mixture: torch.Tensor, *, use_amp: bool) -> CudaGraphRuntimeStatus:
         """Warm up and record the graphs on ``sample_mixture``'s shape (``cuda_graph.py:44-84``)."""
-        if sample_mixture.device.type != "cuda":
-            self.status = CudaGraphRuntimeStatus(self.mode, "off", "CUDA graph requires CUDA tensors")
+        training = any(p.requires_grad for p in self.model.parameters())
+        refusal = capture_refusal(sample_mixture.device.type, training, torch.version.hip)
+        if refusal is not None:
+            self.status = CudaGraphRuntimeStatus(self.mode, "off", refusal)
             return self.status
         if sample_mixture.ndim == 2:
             sample_mixture = sample_mixture.unsqueeze(1)
-        training = any(p.requires_grad for p in self.model.parameters())
-        if torch.version.hip is not None and training and not self.allow_hip_training_graphs:
-            self.status = CudaGraphRuntimeStatus(self.mode, "off", HIP_TRAINING_GRAPH_REASON)
-            return self.status
         try:
             if self.mode == "stft_mask_core":
                 graph_module = _STFTMaskCoreModule(self.model)
@@ -175,7 +186,8 @@ class RoformerTrainingCudaGraph:
             out_r = torch.view_as_real(out) if out.is_complex() else out
             w = torch.randn(out_r.shape, generator=gen.manual_seed(0), device=out.device, dtype=torch.float32)
             (out_r.float() * w).sum().backward()
-            torch.cuda.synchronize()
+            if sample.is_cuda:
+                torch.cuda.synchronize()
             return out_r.detach().float().clone(), [None if p.grad is None else p.grad.detach().float().clone()
                                                     for p in params]
 

@@ -1,8 +1,9 @@
 """GPU: the RoFormer mask-core graph wrapper (``pymsst_amd.cuda_graph``, after pymsst's
 ``cuda_graph.py``) gives the eager model's results.  On ROCm it refuses training captures by default
 (replays of the captured backward after the first return wrong gradients on this stack), so the
-training cases check the eager fallback and its stated reason; the opt-in capture is exercised for
-its status only.
+training cases check the eager fallback and its stated reason.  No GPU test records a training graph
+on ROCm (its captured backward would hold memset nodes); the capture / refusal logic and the replay
+check are tested on the CPU below with a stand-in for the graphed callable.
 
 Each case captures once, then for three fresh batches runs the eager model and the graphed model on
 the same parameters and compares loss and every parameter gradient; the eager runs between the
@@ -85,23 +86,71 @@ def test_training_graph_matches_eager(monkeypatch, hip_ext, mode, fused, amp, wl
         fr.restore_stock_implementations()
 
 
-@pytest.mark.gpu
-def test_opt_in_capture_reports_a_status(hip_ext):
-    """With the opt-in the capture runs (warm-up, recording, two checked replays) and reports active or
-    the replay disagreement; the graph is not used for training here."""
-    wl = WORKLOADS["bsr_tiny"]
-    model = wl.build_model("cuda", seed=4)
-    model.train()
-    graph = RoformerTrainingCudaGraph(model, "mask_core", allow_hip_training_graphs=True)
-    _, sample = workload_batch(wl, seed=0, device="cuda")
-    st = graph.capture(sample, use_amp=False)
-    assert st.active == "mask_core" or "replay" in (st.reason or ""), st.reason
-    assert all(p.grad is None for p in model.parameters())
-
-
 def test_mode_names():
     assert normalize_cuda_graph_mode(None) == "off"
     assert normalize_cuda_graph_mode("mask") == "mask_core"
     assert normalize_cuda_graph_mode("roformer-stft-mask-core") == "stft_mask_core"
     with pytest.raises(ValueError):
         normalize_cuda_graph_mode("everything")
+
+
+def test_capture_refusal_reasons():
+    from pymsst_amd.cuda_graph import capture_refusal
+
+    assert capture_refusal("cpu", False, None) == "CUDA graph requires CUDA tensors"
+    assert capture_refusal("cuda", True, "7.2") == HIP_TRAINING_GRAPH_REASON
+    assert capture_refusal("cuda", False, "7.2") is None
+    assert capture_refusal("cuda", True, None) is None
+
+
+def test_training_capture_opt_in_raises_on_rocm(monkeypatch):
+    model = WORKLOADS["bsr_tiny"].build_model(None, seed=4)
+    monkeypatch.setattr(torch.version, "hip", "7.2.0", raising=False)
+    with pytest.raises(ValueError, match="not supported on ROCm"):
+        RoformerTrainingCudaGraph(model, "mask_core", allow_hip_training_graphs=True)
+    graph = RoformerTrainingCudaGraph(model, "mask_core")
+    st = graph.capture(torch.zeros(1, 2, 4096), use_amp=False)  # CPU tensor: refused before any capture
+    assert st.active == "off" and not graph.active
+
+
+class _Lin(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.lin = torch.nn.Linear(6, 5)
+
+    def forward(self, x):
+        return self.lin(x).tanh()
+
+
+def test_replay_check_flags_a_replay_that_disagrees():
+    """``_validate`` compares two replays with eager: a stand-in graph whose second replay returns a wrong
+    bias gradient (the failure mode of a memset node that holds once) is rejected with that reason."""
+    torch.manual_seed(0)
+    mod = _Lin()
+    graph = RoformerTrainingCudaGraph(mod, "mask_core")
+    sample = torch.randn(4, 6)
+    calls = {"n": 0}
+
+    class _Replay(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x, w, b):
+            ctx.save_for_backward(x, w, b)
+            return torch.nn.functional.linear(x, w, b).tanh()
+
+        @staticmethod
+        def backward(ctx, g):
+            x, w, b = ctx.saved_tensors
+            y = torch.nn.functional.linear(x, w, b).tanh()
+            gz = g * (1 - y * y)
+            db = gz.sum(0)
+            calls["n"] += 1
+            if calls["n"] >= 2:
+                db = db * 0  # the replay after the first loses the bias reduction
+            return gz @ w, gz.t() @ x, db
+
+    graph._graph_call = lambda x: _Replay.apply(x, mod.lin.weight, mod.lin.bias)
+    reason = graph._validate(mod, sample, use_amp=False)
+    assert reason is not None and "replay 2 gradients" in reason
+
+    calls["n"] = -10**6  # every replay right: accepted
+    assert graph._validate(mod, sample, use_amp=False) is None

@@ -1,18 +1,18 @@
 """CPU tests of the training harness: loss-curve CSV, curve comparison, threshold summary,
-the seeded manual loop and the restated losses (mirroring the reference's
-tests/test_comparison.py:127-222 and tests/test_training_smoke.py:660-668)."""
+the seeded manual loop and the model's waveform loss (mirroring the reference's
+tests/test_comparison.py:127-222)."""
 
 from __future__ import annotations
 
 import csv
 import json
+import warnings
 
 import pytest
 import torch
 from pytest import approx
 
 from pymsst_amd import direct_compare as dc
-from pymsst_amd.losses import compute_loss, masked_loss
 from pymsst_amd.workloads import TrainWorkload, noise_sources, synthetic_batches, workload_batch
 
 
@@ -81,22 +81,26 @@ def test_should_record_loss():
     assert not any(dc.should_record_loss(s, 10, 0) for s in range(1, 11))
 
 
-def test_masked_loss_known_answers():
-    prediction = torch.arange(18, dtype=torch.float32).reshape(3, 2, 3)
-    target = prediction[:, None].clone()
-    assert masked_loss(prediction, target) == 0
-    assert masked_loss(prediction, target, original_shape_compat=True) > 0
-    # q-quantile masking: per-item errors 0, 1, 4, 9 (coarse means over [C, L]); the 0.5
-    # quantile is 2.5, so only the items with error < 2.5 contribute: (0 + 1) / 4
-    p = torch.tensor([0.0, 1.0, 2.0, 3.0]).reshape(4, 1, 1)
-    t = torch.zeros(4, 1, 1)
-    assert masked_loss(p, t, q=0.5).item() == approx(0.25)
-    assert compute_loss(p, t, loss_name="l1_loss").item() == approx(1.5)
-    assert compute_loss(p, t, loss_name="mse_loss").item() == approx(3.5)
-    with pytest.raises(ValueError, match="unsupported loss"):
-        compute_loss(p, t, loss_name="nope")
-    with pytest.raises(ValueError, match="does not match"):
-        compute_loss(p, torch.zeros(3, 1, 1), loss_name="l1_loss")
+def test_one_stem_waveform_loss_is_per_item():
+    """One stem: recon is [B, C, L] and the stacked target [B, 1, C, L]; the L1 compares each item with
+    its own target (no broadcast over [B, B, C, L]); the multi-resolution term likewise."""
+    import torch.nn.functional as F
+
+    from pymsst_amd.workloads import WORKLOADS
+
+    torch.manual_seed(0)
+    for loss in ("l1", "multi_stft"):
+        model = WORKLOADS["bsr_tiny"].build_model(None, seed=4)
+        model.loss_type = loss
+        recon = torch.randn(2, 2, 4096)
+        target = torch.randn(2, 1, 2, 4096)
+        with warnings.catch_warnings():
+            warnings.simplefilter("error")  # torch warns when l1_loss broadcasts mismatched sizes
+            got = model.loss(recon, target)
+            ref = model.loss(recon, target[:, 0])
+        assert got.item() == approx(ref.item(), rel=1e-6)
+        if loss == "l1":
+            assert got.item() == approx(F.l1_loss(recon, target[:, 0]).item(), rel=1e-6)
 
 
 def test_noise_sources_law_and_seeding():
