@@ -1,0 +1,1095 @@
+"""CPU replay of the address arithmetic of the HIP kernels (test infrastructure, no GPU).
+
+Each ``replay_*`` function restates, for one C-ABI entry point, what the host side launches (the
+variant, grid and block schedule the dispatch code picks for the given shapes) and every global
+load, store and global->LDS DMA those kernels issue, plus their LDS reads and writes, as byte
+offsets.  The offsets are computed with numpy over all threads of a block; over the blocks, the
+schedule decode is evaluated for every block (each (band, row tile, sub-tile) unit must be hit
+exactly once) and the memory accesses for every band and sub-tile at the first and last row tile.
+K loops move a per-lane offset by a fixed stride per step, so their extremes are the first two
+steps and the last one, which are the steps evaluated.
+
+``Bounds.violations()`` lists every buffer whose touched byte range leaves the buffer the caller
+allocates for the entry point (sizes from the C-ABI contract in include/pymsst_amd.h).  Every
+formula below cites the kernel source it restates (pymsst_amd/csrc/<file>:<kernel>).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+WAVE = 64
+XCDS = 8
+CHUNK_K = 32
+GEMM_THREADS = 256
+LDS_PITCH16 = CHUNK_K + 8  # 16-bit LDS row pitch of gemm.h (elements)
+LDS_PITCH32 = CHUNK_K + 1
+
+
+# ----------------------------------------------------------------------------- recorder
+
+
+@dataclass
+class Bounds:
+    sizes: dict
+    lo: dict = field(default_factory=dict)
+    hi: dict = field(default_factory=dict)
+    notes: list = field(default_factory=list)
+
+    def touch(self, buf: str, off, width: int, mask=None) -> None:
+        """Accesses of ``width`` bytes at byte offsets ``off`` (where ``mask``) of buffer ``buf``."""
+        off = np.asarray(off, dtype=np.int64)
+        if mask is not None:
+            off = off[np.broadcast_to(np.asarray(mask, dtype=bool), off.shape)]
+        if off.size == 0:
+            return
+        lo, hi = int(off.min()), int(off.max()) + int(width)
+        self.lo[buf] = min(self.lo.get(buf, lo), lo)
+        self.hi[buf] = max(self.hi.get(buf, hi), hi)
+
+    def fail(self, msg: str) -> None:
+        self.notes.append(msg)
+
+    def violations(self) -> list[str]:
+        out = list(self.notes)
+        for buf in self.lo:
+            size = self.sizes[buf]
+            if self.lo[buf] < 0 or self.hi[buf] > size:
+                out.append(f"{buf}: bytes [{self.lo[buf]}, {self.hi[buf]}) outside [0, {size})")
+        return out
+
+
+def steps(nk: int) -> list[int]:
+    """K-loop steps whose offsets bound every step's: 0, 1 and the last."""
+    return sorted({c for c in (0, 1, nk - 1) if 0 <= c < nk})
+
+
+def cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+# ----------------------------------------------------------------------------- device helpers
+
+
+def swz_k(r):  # dma_gemm.h
+    return ((r >> 1) ^ (r >> 3)) & 3
+
+
+def swz_mn(k):  # dma_gemm.h
+    return 2 * (k & 3)
+
+
+def swz_mn_p(pitch: int, k):  # dma_gemm.h swz_mn_p<PITCH>
+    if pitch == 512:
+        return 2 * ((k & 3) | (((k >> 3) & 3) << 2))
+    return swz_mn(k)
+
+
+def frag_mn_addr(region, c0, pitch, lane, p512=False):  # dma_gemm.h frag_mn_addr / frag_mn_addr_p
+    j, g = lane & 15, lane >> 4
+    k = 8 * g + (j >> 2)
+    col = c0 + 4 * (j & 3)
+    unit = col >> 3
+    sw = swz_mn_p(pitch, k) if p512 else swz_mn(k)
+    return region + k * pitch + 16 * (unit ^ sw) + 2 * (col & 7)
+
+
+def frag_k_addr(region, r0, lane):  # dma_gemm.h
+    rr, g = lane & 15, lane >> 4
+    return region + (r0 + rr) * 64 + 16 * (g ^ swz_k(rr))
+
+
+def lds_index16(r, k):  # gemm.h lds_index for 16-bit types (elements)
+    return r * LDS_PITCH16 + ((((k >> 3) ^ ((r >> 4) & 3)) << 3) | (k & 7))
+
+
+def xcd_decode(groups: int, members: int):
+    """gemm.h XcdGrid: blocks() and xcd_block(); returns (group, member, valid) per block."""
+    nblocks = cdiv(groups, XCDS) * XCDS * members
+    b = np.arange(nblocks, dtype=np.int64)
+    r = b // XCDS
+    member = r % members
+    group = (r // members) * XCDS + b % XCDS
+    return group, member, group < groups
+
+
+@dataclass
+class BandSched:
+    gs: list
+    cumb: list
+    bstart: list
+    m_tiles: int
+    per_xcd: int
+
+
+def build_band_sched(nb: int, m_tiles: int, units, cost=lambda b: 1):
+    """dma_gemm.h build_band_sched (returns None where the host falls back)."""
+    if nb > 256 or m_tiles <= 0:
+        return None
+    cumb = [0]
+    total = total_cost = ucmax = 0
+    for b in range(nb):
+        u = int(units(b))
+        uc = u * int(cost(b))
+        ucmax = max(ucmax, uc)
+        total += u * m_tiles
+        total_cost += uc * m_tiles
+        if total >= 1 << 31:
+            return None
+        cumb.append(total)
+
+    def ranges(cap, fill, gs, bstart):
+        x = 0
+        acc = g = 0
+        if fill:
+            gs[0] = 0
+            bstart[0] = 0
+        for b in range(nb):
+            ch = (cumb[b + 1] - cumb[b]) // m_tiles
+            uc = ch * int(cost(b))
+            for _ in range(m_tiles):
+                if acc + uc > cap:
+                    x += 1
+                    acc = 0
+                    if fill and x < XCDS:
+                        gs[x] = g
+                        bstart[x] = b
+                acc += uc
+                g += ch
+        if fill:
+            for y in range(x + 1, XCDS + 1):
+                gs[y] = total
+                if y < XCDS:
+                    bstart[y] = nb - 1
+        return x + 1
+
+    lo, hi = ucmax, max(total_cost, ucmax)
+    while lo < hi:
+        mid = (lo + hi) // 2
+        if ranges(mid, False, None, None) <= XCDS:
+            hi = mid
+        else:
+            lo = mid + 1
+    gs = [0] * (XCDS + 1)
+    bstart = [0] * XCDS
+    ranges(lo, True, gs, bstart)
+    per_xcd = max(gs[y + 1] - gs[y] for y in range(XCDS))
+    return BandSched(gs, cumb, bstart, m_tiles, per_xcd)
+
+
+def sched_decode(sc: BandSched, nb: int, units, last_first: bool, bnd: Bounds, what: str):
+    """dma_gemm.h sched_block over every block of the grid; checks that the units are covered once
+    and that the forward band search starting at bstart finds each block's band."""
+    nblocks = sc.per_xcd * XCDS
+    seen = np.zeros(sc.cumb[-1], dtype=np.int64)
+    out = []
+    for blk in range(nblocks):
+        xcd, local = blk % XCDS, blk // XCDS
+        if sc.gs[xcd] + local >= sc.gs[xcd + 1]:
+            continue
+        gb = sc.gs[xcd + 1] - 1 - local if last_first else sc.gs[xcd] + local
+        b = sc.bstart[xcd]
+        if b >= nb or sc.cumb[b] > gb:
+            bnd.fail(f"{what}: block {blk} starts its band search past its band")
+            continue
+        while gb >= sc.cumb[b + 1]:
+            b += 1
+            if b >= nb:
+                break
+        if b >= nb:
+            bnd.fail(f"{what}: block {blk} decodes past the last band")
+            continue
+        per_unit = (sc.cumb[b + 1] - sc.cumb[b]) // sc.m_tiles
+        within = gb - sc.cumb[b]
+        mt, sub = within // per_unit, within % per_unit
+        if per_unit != units(b) or not (0 <= mt < sc.m_tiles):
+            bnd.fail(f"{what}: block {blk} decodes to band {b} row tile {mt} unit size {per_unit}")
+        seen[gb] += 1
+        out.append((b, mt, sub))
+    if seen.size and (seen.min() != 1 or seen.max() != 1):
+        bnd.fail(f"{what}: {int((seen != 1).sum())} schedule units not covered exactly once")
+    return out
+
+
+# ----------------------------------------------------------------------------- gemm.h loaders
+
+
+def krow_loader(bnd, buf, esz, base_el, stride, rows_valid, k_valid, rows, v4, kbeg, nk, tid):
+    """gemm.h KRowLoader: thread t moves quads (r, k) = ((t + 256 i) / 8, 4 (t % 8)) of every chunk;
+    rows past rows_valid are clamped (interior) or masked (edge chunk)."""
+    kq = rows * (CHUNK_K // 4) // GEMM_THREADS
+    i = np.arange(kq)
+    r = (tid[:, None] + i[None, :] * GEMM_THREADS) // (CHUNK_K // 4)
+    lane_k = (tid % (CHUNK_K // 4)) * 4
+    src = np.minimum(r, rows_valid - 1)
+    row_ok = r < rows_valid
+    for c in steps(nk):
+        k = kbeg + CHUNK_K * c + lane_k[:, None]
+        edge = (c == 0 and kbeg < 0) or not v4
+        if not edge:
+            bnd.touch(buf, (base_el + src * stride + k) * esz, 4 * esz)
+        elif v4:
+            ok = row_ok & (k >= 0) & (k < k_valid)
+            bnd.touch(buf, np.where(ok, base_el + src * stride + k, base_el) * esz, 4 * esz)
+        else:
+            for j in range(4):
+                ok = row_ok & (k + j >= 0) & (k + j < k_valid)
+                bnd.touch(buf, np.where(ok, base_el + src * stride + k + j, base_el) * esz, esz)
+
+
+def mn_loader(bnd, buf, esz, base_el, kstride, mn_valid, k_valid, rows, v4, kbeg, nk, tid):
+    """gemm.h MNLoader: element (k, mn) = base[k * kstride + mn]; thread t owns mn quad 4 (t % (ROWS/4))
+    and k rows (t / (ROWS/4)) * KB .. + KB - 1 of each chunk (KB = ROWS / 32)."""
+    qpk = rows // 4
+    kb_n = rows // 32
+    mn = (tid % qpk) * 4
+    kb = (tid // qpk) * kb_n
+    mn_src = np.where(v4 & (mn >= mn_valid), mn_valid - 4, mn)
+    for c in steps(nk):
+        for t in range(kb_n):
+            k = kbeg + CHUNK_K * c + kb + t
+            edge = (c == 0 and kbeg < 0) or not v4
+            if not edge:
+                bnd.touch(buf, (base_el + k * kstride + mn_src) * esz, 4 * esz)
+            elif v4:
+                kok = (k >= 0) & (k < k_valid)
+                bnd.touch(buf, np.where(kok, base_el + k * kstride + mn_src, base_el) * esz, 4 * esz)
+            else:
+                kok = (k >= 0) & (k < k_valid)
+                kc = np.where(kok, k, 0)
+                for j in range(4):
+                    ok = kok & (mn + j < mn_valid)
+                    bnd.touch(buf, np.where(ok, base_el + kc * kstride + mn + j, base_el) * esz, esz)
+
+
+def gemm_lds_bytes(esz, br, bc):
+    return 2 * (br + bc) * (LDS_PITCH16 if esz == 2 else LDS_PITCH32) * esz
+
+
+# ----------------------------------------------------------------------------- band split
+
+
+def _offs(widths):
+    return np.concatenate([[0], np.cumsum(widths)]).astype(np.int64)
+
+
+def tile_capacity(o):
+    return min(4, cdiv(o, 64))
+
+
+def replay_band_split_forward(widths, M, O, esz, *, norm=True, x_stride=None, has_bias=True, act_tanh=False):
+    """band_split.hip launch_fwd + bs_fwd_kernel (also the grouped linear forward when norm=False)."""
+    nb, F = len(widths), int(sum(widths))
+    x_stride = F if x_stride is None else x_stride
+    offs = _offs(widths)
+    sizes = {"x": ((M - 1) * x_stride + F) * esz, "gamma": F * esz, "weight": O * F * esz,
+             "bias": nb * O * esz, "out": M * nb * O * esz, "inv_norm": M * nb * 4, "offsets": (nb + 1) * 8,
+             "lds": 0}
+    bnd = Bounds(sizes)
+    vec4 = all(w % 4 == 0 for w in widths) and x_stride % 4 == 0
+    ovec4 = O % 4 == 0
+    ovec8 = esz == 2 and ovec4 and O % 8 == 0
+    TO = tile_capacity(O) if vec4 else 4
+    OT = 64 * TO
+    cap = 64 * tile_capacity(O)
+    sizes["lds"] = gemm_lds_bytes(esz, OT, 64) + 64 * 4
+    mtiles, oz = cdiv(M, 64), cdiv(O, cap)
+    tid = np.arange(GEMM_THREADS)
+    lane, wave = tid & 63, tid >> 6
+    for by in range(nb):
+        band = nb - 1 - by
+        bnd.touch("offsets", np.array([band, band + 1]) * 8, 8)
+        off, I = int(offs[band]), int(widths[band])
+        nk = cdiv(I, CHUNK_K)
+        kbeg = I - nk * CHUNK_K
+        for bx in sorted({0, mtiles - 1}):
+            m0 = bx * 64
+            rv = min(M - m0, 64)
+            for bz in range(oz):
+                oc = bz * OT
+                # A: weight rows oc .. of band b ([O, I_b] at O * off), K = I
+                krow_loader(bnd, "weight", esz, O * off + oc * I, I, O - oc, I, OT, vec4, kbeg, nk, tid)
+                # B: x rows (clamped) of the band; gamma of the thread's k quad
+                krow_loader(bnd, "x", esz, m0 * x_stride + off, x_stride, rv, I, 64, vec4, kbeg, nk, tid)
+                if norm:
+                    for c in steps(nk):
+                        k = kbeg + CHUNK_K * c + (tid % 8) * 4
+                        if (c == 0 and kbeg < 0) or not vec4:
+                            for j in range(4):
+                                ok = (k + j >= 0) & (k + j < I)
+                                bnd.touch("gamma", np.where(ok, off + k + j, off) * esz, esz)
+                        else:
+                            bnd.touch("gamma", (off + k) * esz, 4 * esz)
+                    r = np.arange(64)
+                    if bz == 0:
+                        bnd.touch("inv_norm", ((m0 + r) * nb + band) * 4, 4, r < rv)
+                # epilogue
+                for t in range(TO):
+                    o = oc + wave * 16 * TO + t * 16 + 4 * (lane >> 4)
+                    ok = o < O
+                    if has_bias:
+                        if ovec4:
+                            bnd.touch("bias", (band * O + o) * esz, 4 * esz, ok)
+                        else:
+                            for rr in range(4):
+                                bnd.touch("bias", (band * O + o + rr) * esz, esz, ok & (o + rr < O))
+                    if ovec8:
+                        kop = OT + 8
+                        ol = wave * 16 * TO + t * 16 + 4 * (lane >> 4)
+                        for j in range(4):
+                            m = j * 16 + (lane & 15)
+                            bnd.touch("lds", (m * kop + ol) * esz, 4 * esz, ok)
+                    else:
+                        for j in range(4):
+                            m = j * 16 + (lane & 15)
+                            okm = ok & (m < rv)
+                            if ovec4:
+                                bnd.touch("out", (((m0 + m) * nb + band) * O + o) * esz, 4 * esz, okm)
+                            else:
+                                for rr in range(4):
+                                    bnd.touch("out", (((m0 + m) * nb + band) * O + o + rr) * esz, esz,
+                                              okm & (o + rr < O))
+                if ovec8:
+                    kop = OT + 8
+                    ov = min(O - oc, OT)
+                    q = np.arange(64 * (ov // 8))
+                    m, cc = q // (ov // 8), (q % (ov // 8)) * 8
+                    okm = m < rv
+                    bnd.touch("lds", (m * kop + cc) * esz, 16, okm)
+                    bnd.touch("out", (((m0 + m) * nb + band) * O + oc + cc) * esz, 16, okm)
+    return bnd
+
+
+def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=False):
+    """band_split.hip launch_bwd (saved input, forward output given: the per-row dots kernel, the split
+    dx kernel, the DMA-ring or register dW kernel, col_sum) or launch_grouped_bwd (grouped=True)."""
+    nb, F = len(widths), int(sum(widths))
+    offs = _offs(widths)
+    m_tiles = cdiv(M, 64)
+    dgp = cdiv(m_tiles * F * 4, 256) * 256
+    sizes = {"dy": M * nb * O * esz, "x": M * F * esz, "inv_norm": M * nb * 4, "gamma": F * esz,
+             "weight": O * F * esz, "out": M * nb * O * esz, "bias": nb * O * esz, "dx": M * F * esz,
+             "dgamma": F * esz, "dw": O * F * esz, "db": nb * O * esz, "offsets": (nb + 1) * 8,
+             "workspace": 0 if grouped else dgp + cdiv(M * nb * 4, 256) * 256, "lds": 0}
+    bnd = Bounds(sizes)
+    vec4 = all(w % 4 == 0 for w in widths)
+    ovec4 = O % 4 == 0
+    tid = np.arange(GEMM_THREADS)
+    lane, wave = tid & 63, tid >> 6
+    norm = not grouped
+    # -- per-row dots (launch_bwd, split form)
+    if norm and M > 0:
+        rows = M * nb
+        if esz == 2 and O % 8 == 0:
+            U = min(8, cdiv(O, 64))
+            nblk = cdiv(rows * 8, 256)
+            for blk in sorted({0, nblk - 1}):
+                row = (blk * 256 + tid) // 8
+                l8 = tid & 7
+                rc = np.minimum(row, rows - 1)
+                b = rc % nb
+                for u in range(U):
+                    cc0 = 8 * (l8 + 8 * u)
+                    cc = np.where(cc0 < O, cc0, O - 8)
+                    bnd.touch("dy", (rc * O + cc) * esz, 16)
+                    bnd.touch("out", (rc * O + cc) * esz, 16)
+                    if has_bias:
+                        bnd.touch("bias", (b * O + cc) * esz, 16)
+                bnd.touch("workspace", dgp + row * 4, 4, (l8 == 0) & (row < rows))
+        else:
+            nblk = cdiv(rows * 32, 256)
+            for blk in sorted({0, nblk - 1}):
+                row = (blk * 256 + tid) // 32
+                l32 = tid & 31
+                ok = row < rows
+                b = row % nb
+                step = 4 if (ovec4 and vec4) else 1
+                for q0 in range(0, O, 128 if step == 4 else 32):
+                    q = q0 + l32 * step
+                    okq = ok & (q < O)
+                    bnd.touch("dy", (row * O + q) * esz, step * esz, okq)
+                    bnd.touch("out", (row * O + q) * esz, step * esz, okq)
+                    if has_bias:
+                        bnd.touch("bias", (b * O + q) * esz, step * esz, okq)
+                bnd.touch("workspace", dgp + row * 4, 4, (l32 == 0) & ok)
+    # -- dx (split: one block per (band, 64-wide input chunk, 64 rows))
+    max_ich = cdiv(max(widths), 64)
+    sizes["lds"] = gemm_lds_bytes(esz, 64, 64) + 64 * 4 + 4 * 64 * 4
+    if M > 0:
+        grp, mt, valid = xcd_decode(nb * max_ich, m_tiles)
+        if np.any(mt[valid] >= m_tiles):
+            bnd.fail("dx: member out of range")
+        v4 = vec4 and ovec4
+        for band in range(nb):
+            off, I = int(offs[band]), int(widths[band])
+            for ich in range(max_ich):
+                i0 = ich * 64
+                if i0 >= I:
+                    continue
+                for mtile in sorted({0, m_tiles - 1}):
+                    m0 = mtile * 64
+                    rv = min(M - m0, 64)
+                    r64 = np.arange(64)
+                    if norm:
+                        bnd.touch("inv_norm", ((m0 + r64) * nb + band) * 4, 4, r64 < rv)
+                        bnd.touch("workspace", dgp + ((m0 + r64) * nb + band) * 4, 4, r64 < rv)
+                    nk = cdiv(O, CHUNK_K)
+                    kbeg = O - nk * CHUNK_K
+                    mn_loader(bnd, "weight", esz, O * off + i0, I, I - i0, O, 64, v4, kbeg, nk, tid)
+                    krow_loader(bnd, "dy", esz, (m0 * nb + band) * O, nb * O, rv, O, 64, v4, kbeg, nk, tid)
+                    il = i0 + wave * 16 + 4 * (lane >> 4)
+                    for j in range(4):
+                        m = j * 16 + (lane & 15)
+                        ok = (m < rv) & (il < I)
+                        if norm:
+                            for r in range(4):
+                                gi = np.where(il + r < I, off + il + r, off)
+                                bnd.touch("gamma", gi * esz, esz, il + r < I)
+                        if vec4:
+                            if norm:
+                                bnd.touch("x", ((m0 + m) * F + off + il) * esz, 4 * esz, ok)
+                            bnd.touch("dx", ((m0 + m) * F + off + il) * esz, 4 * esz, ok)
+                        else:
+                            for r in range(4):
+                                okr = ok & (il + r < I)
+                                if norm:
+                                    bnd.touch("x", ((m0 + m) * F + off + il + r) * esz, esz, okr)
+                                bnd.touch("dx", ((m0 + m) * F + off + il + r) * esz, esz, okr)
+                    if norm:
+                        for r in range(4):
+                            bnd.touch("workspace", (mtile * F + off + il + r) * 4, 4,
+                                      ((lane & 15) == 0) & (il + r < I))
+    # -- dW
+    dma = (not grouped) and esz == 2 and M >= 64 and vec4 and O % 8 == 0
+    if dma:
+        _replay_bs_dw_dma(bnd, widths, offs, M, O, esz, has_bias)
+    else:
+        _replay_bs_dw_reg(bnd, widths, offs, M, O, esz, has_bias, norm, vec4 and ovec4)
+    if norm:
+        # col_sum_kernel over the m_tiles x F partials -> dgamma
+        _replay_col_sum(bnd, "workspace", m_tiles, F, "dgamma", esz)
+    return bnd
+
+
+def _replay_col_sum(bnd, pbuf, parts, dim, obuf, osz, poff=0):
+    """reduce.hip col_sum_kernel: 16 columns x 64 groups per block."""
+    tid = np.arange(1024)
+    cl, grp = tid % 16, tid // 16
+    for blk in sorted({0, cdiv(dim, 16) - 1}):
+        c = blk * 16 + cl
+        ok = c < dim
+        for p0 in sorted({0, max(parts - 1, 0)}):
+            p = np.full_like(c, p0)
+            bnd.touch(pbuf, poff + (p * dim + c) * 4, 4, ok & (p < parts))
+        bnd.touch(obuf, c * osz, osz, ok & (grp == 0))
+    _ = grp
+
+
+def _replay_bs_dw_dma(bnd, widths, offs, M, O, esz, has_bias):
+    """band_split.hip bs_bwd_dw_dma_kernel (S = 3 stages, KS = 2: 64 rows per step)."""
+    S, KS = 3, 2
+    KR = KS * CHUNK_K
+    kTile = KR * 2 * 64
+    kStage = 2 * kTile
+    kWR = KR // 4
+    kXI, kDI = kWR // 2, kWR // 8
+    nb, F = len(widths), int(sum(widths))
+    otiles = cdiv(O, 64)
+    units = lambda b: cdiv(widths[b], 64) * otiles  # noqa: E731
+    sc = build_band_sched(nb, 1, units)
+    if sc is None:
+        bnd.fail("dw dma: no schedule")
+        return
+    bnd.sizes["lds"] = max(bnd.sizes["lds"], S * kStage + 2048 * 4)
+    decoded = sched_decode(sc, nb, units, False, bnd, "bs_bwd_dw_dma")
+    tid = np.arange(GEMM_THREADS)
+    lane, wave = tid & 63, tid >> 6
+    wr, wc = wave >> 1, wave & 1
+    nk = cdiv(M, KR)
+    kbeg = M - nk * KR
+    dstride = nb * O
+    for band, _mt, sub in sorted(set(decoded)):
+        i0, o0 = sub // otiles * 64, sub % otiles * 64
+        off, I = int(offs[band]), int(widths[band])
+        for c in steps(nk):
+            stage = (c % S) * kStage
+            for t in range(kDI):
+                r = kWR * wave + 8 * t + (lane >> 3)
+                col = np.minimum(o0 + 8 * ((lane & 7) ^ swz_mn(r)), O - 8)
+                row = kbeg + c * KR + r
+                row = np.where((c == 0) & (row < 0), 0, row)
+                bnd.touch("dy", (row * dstride + band * O + col) * esz, 16)
+                bnd.touch("lds", stage + kTile + 128 * (kWR * wave + 8 * t) + 16 * lane, 16)
+            for t in range(kXI):
+                r = kWR * wave + 2 * t + (lane >> 5)
+                i = np.minimum(i0 + 8 * (((lane & 31) >> 2) ^ swz_mn(r)) + 2 * (lane & 3), I - 2)
+                row = kbeg + c * KR + r
+                row = np.where((c == 0) & (row < 0), 0, row)
+                bnd.touch("x", (row * F + off + i) * esz, 4)
+                bnd.touch("lds", stage + 128 * (kWR * wave + 2 * t) + 4 * lane, 4)
+            # inv window, scaling pass and fragment reads
+            urow = kWR * wave + (lane >> 3)
+            uoff = urow * 2 * 64 + 16 * (lane & 7)
+            for j in range(KS):
+                bnd.touch("lds", stage + uoff + 8 * j * 128, 16)
+            for kk in range(KS):
+                for f in range(2):
+                    fa = frag_mn_addr(0, 32 * wr + 16 * f, 2 * 64, lane) + stage + kk * 32 * 128
+                    fb = frag_mn_addr(kTile, 32 * wc + 16 * f, 2 * 64, lane) + stage + kk * 32 * 128
+                    for a in (fa, fb):
+                        bnd.touch("lds", a, 8)
+                        bnd.touch("lds", a + 4 * 2 * 64, 8)
+        for c0 in range(0, nk, 2048 // KR):
+            j = np.arange(min((nk - c0) * KR, 2048))
+            rr = kbeg + c0 * KR + j
+            bnd.touch("inv_norm", (rr * nb + band) * 4, 4, rr >= 0)
+        for f in range(2):
+            i = i0 + 32 * wr + 16 * f + 4 * (lane >> 4)
+            for r in range(4):
+                bnd.touch("gamma", (off + np.minimum(i + r, I - 1)) * esz, esz)
+        if has_bias and i0 == 0:
+            for g in range(2):
+                o = o0 + 32 * wc + 16 * g + lane
+                bnd.touch("db", (band * O + o) * esz, esz, (wr == 0) & (lane < 16) & (o < O))
+        kop = 64 + 8
+        for f in range(2):
+            for g in range(2):
+                bnd.touch("lds", ((32 * wc + 16 * g + (lane & 15)) * kop + 32 * wr + 16 * f + 4 * (lane >> 4)) * esz,
+                          4 * esz)
+        iv = min(I - i0, 64)
+        q = tid & 15
+        for p in range(4):
+            ol = (tid >> 4) + 16 * p
+            ok = (o0 + ol < O) & (4 * q < iv)
+            bnd.touch("lds", (ol * kop + 4 * q) * esz, 8, ok)
+            bnd.touch("dw", (O * off + (o0 + ol) * I + i0 + 4 * q) * esz, 8, ok)
+
+
+def _replay_bs_dw_reg(bnd, widths, offs, M, O, esz, has_bias, norm, v4):
+    """band_split.hip bs_bwd_dw_kernel (register-staged main loop; also the grouped linear's dW)."""
+    nb, F = len(widths), int(sum(widths))
+    max_it = cdiv(max(widths), 64)
+    grp, ot, valid = xcd_decode(nb * max_it, cdiv(O, 64))
+    tid = np.arange(GEMM_THREADS)
+    lane, wave = tid & 63, tid >> 6
+    nk = cdiv(M, CHUNK_K)
+    kbeg = M - nk * CHUNK_K
+    bnd.sizes["lds"] = max(bnd.sizes["lds"], gemm_lds_bytes(esz, 64, 64))
+    for g_, o_ in zip(grp[valid], ot[valid]):
+        band, i0 = int(g_) // max_it, (int(g_) % max_it) * 64
+        o0 = int(o_) * 64
+        off, I = int(offs[band]), int(widths[band])
+        if i0 >= I or M == 0:
+            continue
+        mn_loader(bnd, "x", esz, off + i0, F, I - i0, M, 64, v4, kbeg, nk, tid)
+        if norm:
+            bnd.touch("inv_norm", (np.arange(M) * nb + band) * 4, 4)
+        mn_loader(bnd, "dy", esz, band * O + o0, nb * O, O - o0, M, 64, v4, kbeg, nk, tid)
+        if has_bias and i0 == 0:
+            t64 = np.arange(GEMM_THREADS)
+            bnd.touch("db", (band * O + o0 + t64) * esz, esz, (t64 < 64) & (t64 < O - o0))
+        ir, oc = (wave >> 1) * 32, (wave & 1) * 32
+        for u in range(2):
+            i = i0 + ir + u * 16 + 4 * (lane >> 4)
+            for v in range(2):
+                o = o0 + oc + v * 16 + (lane & 15)
+                ok = (i < I) & (o < O)
+                if v4:
+                    bnd.touch("dw", (O * off + o * I + i) * esz, 4 * esz, ok)
+                else:
+                    for r in range(4):
+                        bnd.touch("dw", (O * off + o * I + i + r) * esz, esz, ok & (i + r < I))
+
+
+# ----------------------------------------------------------------------------- mask estimator
+
+
+def replay_mask_final_forward(widths, M, H, esz):
+    """mask_estimator.hip launch_me_fwd: me_fwd_dma_kernel on the band schedule (16-bit, aligned), else
+    me_fwd_kernel."""
+    nb, F = len(widths), int(sum(widths))
+    offs = _offs(widths)
+    sizes = {"x": M * nb * H * esz, "weight": 2 * F * H * esz, "bias": 2 * F * esz, "pre": M * 2 * F * esz,
+             "out": M * F * esz, "offsets": (nb + 1) * 8, "lds": 4 * 16384}
+    bnd = Bounds(sizes)
+    vec4 = all(w % 4 == 0 for w in widths) and H % 4 == 0
+    mtiles = cdiv(M, 128)
+    if not (esz == 2 and vec4 and H % 8 == 0 and H > CHUNK_K):
+        bnd.fail("mask forward: register path not modelled")
+        return bnd
+    units = lambda b: cdiv(widths[b], 64)  # noqa: E731
+    sc = build_band_sched(nb, mtiles, units)
+    decoded = sched_decode(sc, nb, units, False, bnd, "me_fwd_dma")
+    S, kStage = 4, 16384
+    tid = np.arange(GEMM_THREADS)
+    lane, wave = tid & 63, tid >> 6
+    g, rr = lane >> 4, lane & 15
+    wr, wc = wave >> 1, wave & 1
+    u = (lane & 3) ^ swz_k(lane >> 2)
+    rsub = lane >> 2
+    nk = cdiv(H, CHUNK_K)
+    kbeg = H - nk * CHUNK_K
+    for band, mt, chunk in sorted({(b, m, s) for b, m, s in decoded if m in (0, mtiles - 1)}):
+        l0 = chunk * 64
+        off, I = int(offs[band]), int(widths[band])
+        m0 = mt * 128
+        rv = min(M - m0, 128)
+        active = l0 + 32 * wr < I
+        nv = np.where(wave >= 2, 4, np.where(l0 + 32 * wave + 16 < I, 4, np.where(l0 + 32 * wave < I, 2, 0)))
+        for t in range(4):
+            R = 64 * wave + 16 * t + rsub
+            l = l0 + 16 * (R >> 5) + (R & 15)
+            lc = np.minimum(l, I - 1)
+            wrow = np.where(((R >> 4) & 1) == 1, I + lc, lc)
+            m = np.minimum(R - 128, rv - 1)
+            is_w = wave < 2
+            gb_w = 2 * off * H
+            gb_x = (m0 * nb + band) * H
+            # chunk 0 through registers: units with k < 0 read k = 0 of the row
+            ok0 = kbeg + 8 * u >= 0
+            kel = np.where(ok0, kbeg + 8 * u, 0)
+            bnd.touch("weight", (gb_w + wrow * H + kel) * esz, 16, is_w)
+            bnd.touch("x", (gb_x + m * nb * H + kel) * esz, 16, ~is_w)
+            bnd.touch("lds", 4 * wave * 1024 + t * 1024 + lane * 16, 16)
+            for c in steps(nk):
+                if c == 0:
+                    continue
+                cc = min(c, nk - 1)
+                k = kbeg + CHUNK_K * cc + 8 * u
+                live = t < nv
+                bnd.touch("weight", (gb_w + wrow * H + k) * esz, 16, is_w & live)
+                bnd.touch("x", (gb_x + m * nb * H + k) * esz, 16, (~is_w) & live)
+                bnd.touch("lds", 4 * wave * 1024 + (cc % S) * kStage + t * 1024 + lane * 16, 16, live)
+        sw = 16 * (g ^ swz_k(rr))
+        for st in {0, (S - 1) * kStage}:
+            for q in range(4):
+                bnd.touch("lds", (64 * wr + rr) * 64 + sw + st + 1024 * q, 16, active)
+                bnd.touch("lds", 8192 + (64 * wc + rr) * 64 + sw + st + 1024 * q, 16, active)
+        kop = 72
+        for h in range(2):
+            lt = 32 * wr + 16 * h + 4 * g
+            l = l0 + lt
+            okl = active & (l < I)
+            bnd.touch("bias", (2 * off + l) * esz, 4 * esz, okl)
+            bnd.touch("bias", (2 * off + I + l) * esz, 4 * esz, okl)
+            for j in range(4):
+                m = 64 * wc + 16 * j + rr
+                for base in (0, 128 * kop, 2 * 128 * kop):
+                    bnd.touch("lds", (base + m * kop + lt) * esz, 4 * esz, active)
+        c4 = (tid & 15) * 4
+        for p in range(8):
+            m = (tid >> 4) + 16 * p
+            ok = (l0 + c4 < I) & (m < rv)
+            bnd.touch("pre", ((m0 + m) * 2 * F + 2 * off + l0 + c4) * esz, 8, ok)
+            bnd.touch("pre", ((m0 + m) * 2 * F + 2 * off + l0 + c4 + I) * esz, 8, ok)
+            bnd.touch("out", ((m0 + m) * F + off + l0 + c4) * esz, 8, ok)
+    bnd.touch("offsets", np.arange(nb + 1) * 8, 8)
+    return bnd
+
+
+def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
+    """mask_estimator.hip launch_me_bwd: me_dpre_flat_kernel, me_bwd_dx_dma_kernel (HC = 256 when
+    H % 256 == 0, else 128), me_bwd_dw_dma_kernel (HT = 128)."""
+    nb, F = len(widths), int(sum(widths))
+    offs = _offs(widths)
+    sizes = {"gout": M * F * esz, "x": M * nb * H * esz, "pre": M * 2 * F * esz, "weight": 2 * F * H * esz,
+             "dx": M * nb * H * esz, "dbias": 2 * F * esz, "dw": 2 * F * H * esz,
+             "workspace": cdiv(M * 2 * F * esz, 256) * 256, "offsets": (nb + 1) * 8, "lds": 0,
+             "lds_flat": (4096 + 1) * 4}
+    bnd = Bounds(sizes)
+    vec4 = all(w % 4 == 0 for w in widths) and H % 4 == 0
+    if not (esz == 2 and vec4 and H % 128 == 0 and M >= CHUNK_K):
+        bnd.fail("mask backward: register paths not modelled")
+        return bnd
+    # -- dpre over whole rows
+    nq = F // 4
+    flat_threads = cdiv(M, 8) * nq
+    nblk = cdiv(flat_threads, 256)
+    tid = np.arange(256)
+    for blk in sorted({0, 1, nblk - 1}):
+        t = blk * 256 + tid
+        m0 = t // nq * 8
+        live = m0 < M
+        q = t % nq
+        band = np.searchsorted(offs[:-1], 4 * q, side="right") - 1
+        off = offs[band]
+        I = offs[band + 1] - off
+        l = 4 * q - off
+        for r in range(8):
+            m = np.minimum(m0 + r, M - 1)
+            bnd.touch("gout", (m * F + 4 * q) * esz, 4 * esz, live)
+            bnd.touch("pre", (m * 2 * F + 2 * off + l) * esz, 4 * esz, live)
+            bnd.touch("pre", (m * 2 * F + 2 * off + l + I) * esz, 4 * esz, live)
+            okw = live & (m0 + r < M)
+            bnd.touch("workspace", ((m0 + r) * 2 * F + 2 * off + l) * esz, 4 * esz, okw)
+            bnd.touch("workspace", ((m0 + r) * 2 * F + 2 * off + l + I) * esz, 4 * esz, okw)
+    bnd.touch("lds_flat", np.arange(nb + 1) * 4, 4)
+    # -- dx on the DMA ring
+    HC = 256 if H % 256 == 0 else 128
+    S = 3 if HC == 256 else 4
+    NW = HC // 32
+    kU = HC // 8
+    kWTile = CHUNK_K * HC * 2
+    kStage = kWTile + 8192
+    kDI = 8 // NW
+    bnd.sizes["lds"] = S * kStage
+    nhc = H // HC
+    mt_dx = cdiv(M, 128)
+    units = lambda b: nhc  # noqa: E731
+    sc = build_band_sched(nb, mt_dx, units, lambda b: cdiv(2 * widths[b], CHUNK_K) + 2)
+    decoded = sched_decode(sc, nb, units, True, bnd, "me_bwd_dx_dma")
+    tid = np.arange(NW * 64)
+    lane, wave = tid & 63, tid >> 6
+    wr, wc = wave >> 1, wave & 1
+    for band, mt, hc in sorted({(b, m, s) for b, m, s in decoded if m in (0, mt_dx - 1)}):
+        off, I = int(offs[band]), int(widths[band])
+        K = 2 * I
+        m0 = mt * 128
+        rv = min(M - m0, 128)
+        nk = cdiv(K, CHUNK_K)
+        kbeg = K - nk * CHUNK_K
+        ub = (lane & 3) ^ swz_k((lane >> 2) & 15)
+        bok0 = kbeg + 8 * ub >= 0
+        for c in steps(nk):
+            st = (c % S) * kStage
+            for t in range(2):
+                kr = (64 // kU) * (wave + NW * t) + lane // kU
+                ua = (lane % kU) ^ swz_mn_p(2 * HC, kr)
+                row = kbeg + c * CHUNK_K + kr
+                row = np.where((c == 0) & (row < 0), 0, row)
+                bnd.touch("weight", ((2 * off + row) * H + hc * HC + 8 * ua) * esz, 16)
+                bnd.touch("lds", st + (wave + NW * t) * 1024 + 16 * lane, 16)
+            for t in range(kDI):
+                mr = 16 * (wave + NW * t) + (lane >> 2)
+                mrc = np.minimum(mr, rv - 1)
+                col = kbeg + c * CHUNK_K + 8 * ub
+                col = np.where((c == 0) & ~bok0, 0, col)
+                bnd.touch("workspace", ((m0 + mrc) * 2 * F + 2 * off + col) * esz, 16)
+                bnd.touch("lds", st + kWTile + (wave + NW * t) * 1024 + 16 * lane, 16)
+            for i in range(4):
+                fa = frag_mn_addr(0, 64 * wr + 16 * i, 2 * HC, lane, p512=True) + st
+                bnd.touch("lds", fa, 8)
+                bnd.touch("lds", fa + 4 * 2 * HC, 8)
+            fb = frag_k_addr(kWTile, 64 * wc, lane) + st
+            for j in range(4):
+                bnd.touch("lds", fb + 1024 * j, 16)
+        kop = HC + 8
+        for j in range(4):
+            m = 64 * wc + 16 * j + (lane & 15)
+            for i in range(4):
+                h = 64 * wr + 16 * i + 4 * (lane >> 4)
+                if tanh_in:
+                    mc = np.minimum(m, rv - 1)
+                    bnd.touch("x", (((m0 + mc) * nb + band) * H + hc * HC + h) * esz, 4 * esz)
+                bnd.touch("lds", (m * kop + h) * esz, 4 * esz)
+        c8 = (tid % kU) * 8
+        for p in range(128 // 16):
+            row = tid // kU + 16 * p
+            ok = row < rv
+            bnd.touch("lds", (row * kop + c8) * esz, 16, ok)
+            bnd.touch("dx", (((m0 + row) * nb + band) * H + hc * HC + c8) * esz, 16, ok)
+    # -- dW on the DMA ring
+    HT, kDwT = 128, 128
+    S2 = 3
+    NW2 = HT // 32
+    kU2 = HT // 8
+    kXTile = CHUNK_K * HT * 2
+    kStage2 = kXTile + 8192
+    kDI2 = 8 // NW2
+    bnd.sizes["lds"] = max(bnd.sizes["lds"], S2 * kStage2)
+    htl = H // HT
+    units2 = lambda b: htl * cdiv(2 * widths[b], kDwT)  # noqa: E731
+    sc2 = build_band_sched(nb, 1, units2)
+    decoded2 = sched_decode(sc2, nb, units2, False, bnd, "me_bwd_dw_dma")
+    tid = np.arange(NW2 * 64)
+    lane, wave = tid & 63, tid >> 6
+    wr, wc = wave >> 1, wave & 1
+    nk = cdiv(M, CHUNK_K)
+    kbeg = M - nk * CHUNK_K
+    xstride = nb * H
+    for band, _mt, sub in sorted(set(decoded2)):
+        off, I = int(offs[band]), int(widths[band])
+        K2 = 2 * I
+        h0 = (sub % htl) * HT
+        j0 = (sub // htl) * kDwT
+        for c in steps(nk):
+            st = (c % S2) * kStage2
+            for t in range(2):
+                kr = (64 // kU2) * (wave + NW2 * t) + lane // kU2
+                uu = (lane % kU2) ^ swz_mn(kr)
+                row = kbeg + c * CHUNK_K + kr
+                row = np.where((c == 0) & (row < 0), 0, row)
+                bnd.touch("x", (row * xstride + band * H + h0 + 8 * uu) * esz, 16)
+                bnd.touch("lds", st + (wave + NW2 * t) * 1024 + 16 * lane, 16)
+            for t in range(kDI2):
+                kr = 4 * (wave + NW2 * t) + (lane >> 4)
+                uu = (lane & 15) ^ swz_mn(kr)
+                jc = np.minimum(j0 + 8 * uu, K2 - 8)
+                row = kbeg + c * CHUNK_K + kr
+                row = np.where((c == 0) & (row < 0), 0, row)
+                bnd.touch("workspace", (row * 2 * F + 2 * off + jc) * esz, 16)
+                bnd.touch("lds", st + kXTile + (wave + NW2 * t) * 1024 + 16 * lane, 16)
+            for i in range(4):
+                fa = frag_mn_addr(0, 64 * wr + 16 * i, 2 * HT, lane) + st
+                fb = frag_mn_addr(kXTile, 64 * wc + 16 * i, 2 * kDwT, lane) + st
+                for a, p in ((fa, 2 * HT), (fb, 2 * kDwT)):
+                    bnd.touch("lds", a, 8)
+                    bnd.touch("lds", a + 4 * p, 8)
+        jv = min(K2 - j0, kDwT)
+        for j in range(4):
+            jj = 64 * wc + 16 * j + lane
+            bnd.touch("dbias", (2 * off + j0 + jj) * esz, esz, (h0 == 0) & (wr == 0) & (lane < 16) & (jj < jv))
+        kop = HT + 8
+        for j in range(4):
+            jj = 64 * wc + 16 * j + (lane & 15)
+            for i in range(4):
+                bnd.touch("lds", (jj * kop + 64 * wr + 16 * i + 4 * (lane >> 4)) * esz, 4 * esz)
+        c8 = (tid % kU2) * 8
+        for p in range(kDwT // 16):
+            jj = tid // kU2 + 16 * p
+            ok = jj < jv
+            bnd.touch("lds", (jj * kop + c8) * esz, 16, ok)
+            bnd.touch("dw", ((2 * off + j0 + jj) * H + h0 + c8) * esz, 16, ok)
+    bnd.touch("offsets", np.arange(nb + 1) * 8, 8)
+    return bnd
+
+
+# ----------------------------------------------------------------------------- row kernels
+
+
+def _row_geom(dim: int, vec: int):
+    """rowgeom.h pick_row_geom for aligned pointers."""
+    if dim % vec == 0:
+        nvec = dim // vec
+        tl = 0
+        while tl < 6 and nvec % (2 << tl) == 0:
+            tl += 1
+        nv = nvec >> tl
+        if 1 <= nv <= 4:
+            return vec, nv, tl
+    if dim <= 512:
+        need = cdiv(dim, WAVE)
+        nv = 1 if need <= 1 else 2 if need <= 2 else 4 if need <= 4 else 8
+        return 1, nv, 6
+    return None
+
+
+def replay_rms_norm(rows: int, dim: int, esz: int):
+    """rmsnorm.hip rms_fwd_kernel and rms_bwd_kernel (saved input), col_sum_kernel."""
+    sizes = {"x": rows * dim * esz, "gamma": dim * esz, "out": rows * dim * esz, "inv_norm": rows * 4,
+             "dy": rows * dim * esz, "dx": rows * dim * esz, "dgamma": dim * esz,
+             "workspace": 1024 * dim * 4, "red": 8 * dim * 4}
+    bnd = Bounds(sizes)
+    geo = _row_geom(dim, 16 // esz)
+    if geo is None:
+        bnd.fail("rms: unsupported dim")
+        return bnd
+    vec, nv, tl = geo
+    half = False
+    if vec == 16 // esz and nv == 3 and vec >= 4:
+        h = _row_geom(dim, vec // 2)
+        if h is not None and h[0] == vec // 2 and h[1] == 3 and h[2] == tl + 1:
+            vec, nv, tl, half = h[0], h[1], h[2], True
+    guard = vec == 1
+    for threads, kind in ((256, "fwd"), (512, "bwd")):
+        tid = np.arange(threads)
+        lane, wave = tid & 63, tid >> 6
+        tpr = 1 << tl
+        t, slot = lane & (tpr - 1), lane >> tl
+        rpw = WAVE >> tl
+        rpb = rpw * (threads // WAVE)
+        nblk = cdiv(rows, rpb)
+        grid = min(nblk, 65536) if kind == "fwd" else min(nblk, 1024)
+        for base in sorted({0, (nblk - 1) * rpb}):
+            row = base + wave * rpw + slot
+            valid = row < rows
+            rl = np.where(valid, row, rows - 1)
+            for v in range(nv):
+                col = (v * tpr + t) * vec
+                okc = col < dim
+                ld = okc if guard else np.ones_like(okc)
+                srcs = ("x",) if kind == "fwd" else ("dy", "x")
+                for b in srcs:
+                    bnd.touch(b, (rl * dim + col) * esz, vec * esz, ld & (valid if guard else True))
+                bnd.touch("gamma", col * esz, vec * esz, okc)
+                dst = "out" if kind == "fwd" else "dx"
+                bnd.touch(dst, (row * dim + col) * esz, vec * esz, valid & okc)
+                if kind == "bwd":
+                    bnd.touch("red", (wave * dim + col) * 4, vec * 4, (slot == 0) & okc)
+            if kind == "fwd":
+                bnd.touch("inv_norm", row * 4, 4, valid & (t == 0))
+            else:
+                bnd.touch("inv_norm", rl * 4, 4)
+        if kind == "bwd":
+            parts = grid
+            for blk in sorted({0, parts - 1}):
+                c = np.arange(dim)
+                bnd.touch("workspace", (blk * dim + c) * 4, 4)
+            _replay_col_sum(bnd, "workspace", parts, dim, "dgamma", esz)
+    _ = half
+    return bnd
+
+
+def replay_rotary_qkv(B: int, N: int, H: int, D: int, esz: int, backward: bool):
+    """rotary.hip rotary_kernel with the three parts of a fused qkv projection (extension.py
+    rotary_qkv_forward / _backward strides); tables are the [..., ::2] views of [1, N, 1, D]."""
+    HD = H * D
+    sizes = {"qkv": B * N * 3 * HD * esz, "o0": B * N * HD * esz, "o1": B * N * HD * esz,
+             "o2": B * N * HD * esz, "cos": N * D * esz, "sin": N * D * esz}
+    bnd = Bounds(sizes)
+    dense_bhnd = (H * N * D, D, N * D)  # [B, H, N, D] buffer seen as [B, N, H, D]
+    qkv = (N * 3 * HD, 3 * HD, D)
+    if not backward:
+        ins = [("qkv", p * HD, qkv) for p in range(3)]
+        outs = [(f"o{p}", 0, dense_bhnd) for p in range(3)]
+    else:
+        ins = [(f"o{p}", 0, dense_bhnd) for p in range(3)]
+        outs = [("qkv", p * HD, qkv) for p in range(3)]
+    vec = 16 // esz
+    while vec > 2 and any(s % vec for _, _, st in ins + outs for s in st):
+        vec //= 2
+    packs = B * N * H * D // vec
+    # the grid-stride loop visits every pack index (packs past the end redo the last one); a pack's
+    # addresses depend on its index only and grow with (b, n, h, d), so the first and the last
+    # 64K packs hold every extreme
+    span = min(packs, 1 << 16)
+    i = np.unique(np.concatenate([np.arange(span), np.arange(packs - span, packs)])).astype(np.int64)
+    ppt = HD // vec
+    tok = i // ppt
+    e = (i - tok * ppt) * vec
+    b, n = tok // N, tok % N
+    h, d = e // D, e % D
+    cs_seq = D
+    for part in range(3):
+        ib, ioff, si = ins[part]
+        ob, ooff, so = outs[part]
+        bnd.touch(ib, (ioff + b * si[0] + n * si[1] + h * si[2] + d) * esz, vec * esz)
+        if part < 2:
+            for tb in ("cos", "sin"):
+                # repeated-table mode: 16 bytes from element 2 * (d / 2) of the position's row
+                bnd.touch(tb, (n * cs_seq + 2 * (d >> 1)) * esz, vec * esz)
+        bnd.touch(ob, (ooff + b * so[0] + n * so[1] + h * so[2] + d) * esz, vec * esz)
+    return bnd
+
+
+def replay_attention_gate(B: int, N: int, H: int, Dh: int, dim: int, esz: int):
+    """attn_gate.hip gate_fwd_kernel / gate_bwd_kernel (fast path) with attn and grad_attn the
+    [B, N, H, Dh] views of dense [B, H, N, Dh] SDPA buffers, col_sum of the partials."""
+    rows = B * N
+    HD = H * Dh
+    sizes = {"attn": B * N * HD * esz, "x": rows * dim * esz, "weight": H * dim * esz, "bias": H * esz,
+             "out": rows * HD * esz, "gate": rows * H * esz, "grad_out": rows * HD * esz,
+             "grad_attn": B * N * HD * esz, "grad_x": rows * dim * esz, "grad_weight": H * dim * esz,
+             "grad_bias": H * esz, "lds": (2 * H * dim + H) * 4}
+    chunks_per = 64
+    while cdiv(rows, chunks_per) > 2048:
+        chunks_per *= 2
+    parts_ws = max(cdiv(rows, chunks_per), 1024)
+    ws_gpre = cdiv(rows * H * 4, 256) * 256
+    ws_pw = cdiv(parts_ws * H * dim * 4, 256) * 256
+    sizes["workspace"] = ws_gpre + ws_pw + cdiv(parts_ws * H * 4, 256) * 256
+    bnd = Bounds(sizes)
+    E = HD // WAVE
+    logh = H.bit_length() - 1
+    jx = cdiv(dim, WAVE)
+    jx = jx if jx <= 4 else 8
+    fast = (1 << logh) == H and 1 <= logh <= 4 and HD % WAVE == 0 and E in (2, 4, 8) and cdiv(dim, WAVE) <= 8 \
+        and H * jx <= 64 and (2 * H * dim + H) * 4 <= 48 * 1024
+    if not fast:
+        bnd.fail("gate: generic path not modelled")
+        return bnd
+    sb, sn, sh = HD * N, Dh, N * Dh  # transposed view of [B, H, N, Dh]
+    LPH = WAVE // H
+    tid = np.arange(256)
+    lane, wave = tid & 63, tid >> 6
+    head, sub = lane // LPH, lane % LPH
+    k = np.arange(H * dim)
+    bnd.touch("weight", k * esz, esz)
+    bnd.touch("lds", ((k % dim) * H + k // dim) * 4, 4)
+    for kind, maxb in (("fwd", 4096), ("bwd", 1024)):
+        nblk = min(cdiv(rows, 4 * 2), maxb)
+        for blk in sorted({0, nblk - 1}):
+            # a wave's rows: m0 = (block * 4 + wave) * 2 + trip * (grid * 8) while m0 < rows
+            first = (blk * 4 + wave) * 2
+            trips = np.where(first < rows, (rows - 1 - first) // (nblk * 8), -1)
+            for m0, live in ((first, first < rows), (first + np.maximum(trips, 0) * nblk * 8, trips >= 0)):
+                for r in range(2):
+                    m = m0 + r
+                    ok = live & (m < rows)
+                    bb, nn = m // N, m % N
+                    tok = bb * sb + nn * sn + head * sh + sub * E
+                    bnd.touch("attn", tok * esz, E * esz, ok)
+                    for j in range(jx):
+                        i = lane + j * WAVE
+                        bnd.touch("x", (m * dim + i) * esz, esz, ok & (i < dim))
+                        if kind == "bwd":
+                            bnd.touch("grad_x", (m * dim + i) * esz, esz, ok & (i < dim))
+                            bnd.touch("lds", (i * H + head) * 4, 4, ok & (i < dim))
+                    if kind == "fwd":
+                        bnd.touch("gate", (m * H + head) * esz, esz, ok & (sub == 0))
+                        bnd.touch("out", (m * HD + lane * E) * esz, E * esz, ok)
+                    else:
+                        bnd.touch("grad_out", (m * HD + lane * E) * esz, E * esz, ok)
+                        bnd.touch("gate", (m * H + head) * esz, esz, ok)
+                        bnd.touch("grad_attn", tok * esz, E * esz, ok)
+        if kind == "bwd":
+            for j in range(jx):
+                i = lane + j * WAVE
+                for h in range(H):
+                    bnd.touch("lds", (H * dim + h * dim + i) * 4, 4, i < dim)
+            bnd.touch("lds", (H * dim + H * dim + head) * 4, 4, sub == 0)
+            c = np.arange(H * dim)
+            for blk in sorted({0, nblk - 1}):
+                bnd.touch("workspace", ws_gpre + (blk * H * dim + c) * 4, 4)
+                bnd.touch("workspace", ws_gpre + ws_pw + (blk * H + np.arange(H)) * 4, 4)
+            _replay_col_sum(bnd, "workspace", nblk, H * dim, "grad_weight", esz, poff=ws_gpre)
+            _replay_col_sum(bnd, "workspace", nblk, H, "grad_bias", esz, poff=ws_gpre + ws_pw)
+    bnd.touch("bias", head * esz, esz)
+    return bnd
+
+
+# ----------------------------------------------------------------------------- configs
+
+
+BSR_WIDTHS = tuple([8] * 24 + [16] * 12 + [48] * 8 + [96] * 8 + [192] * 8 + [512, 516])
+
+# (name, band widths, rows M = B * T, model dim, mask hidden, q/k shapes (B*NB, T) and (B*T, NB))
+CONFIG_SHAPES = {
+    "configs0": (BSR_WIDTHS, 130, 64, 256, (124, 65, 4, 32), (130, 62, 4, 32)),
+    "configs1": (BSR_WIDTHS, 1032, 192, 768, (248, 258, 8, 64), (1032, 62, 8, 64)),
+    "configs4": (BSR_WIDTHS, 1896, 512, 2048, (124, 948, 8, 64), (1896, 62, 8, 64)),
+}
+
+
+def mel_widths():
+    """The 60-band Mel layout (4 * bins per band) of configs[3], from the restated model."""
+    from pymsst_amd.core.mel_band_roformer import mel_band_bins
+
+    return tuple(4 * len(b) for b in mel_band_bins(44100, 2048, 60))
+
+
+def all_replays(name: str, esz: int):
+    """Every kernel replay of one configuration's fused train step (band split fwd/bwd, grouped
+    linear fwd/bwd of the mask hidden layer, mask final fwd/bwd, RMSNorm at the model dim, fused qkv
+    rotary and the attention output gate on both attention axes); yields (label, Bounds)."""
+    if name == "configs3":
+        widths, M, dim, hidden = mel_widths(), 2760, 192, 768
+        qk = [(240, 690, 8, 64), (2760, 60, 8, 64)]
+    else:
+        widths, M, dim, hidden, qk_t, qk_f = CONFIG_SHAPES[name]
+        qk = [qk_t, qk_f]
+    nb = len(widths)
+    yield "band_split_fwd", replay_band_split_forward(widths, M, dim, esz)
+    yield "band_split_bwd", replay_band_split_backward(widths, M, dim, esz)
+    yield "grouped_linear_fwd", replay_band_split_forward([dim] * nb, M, hidden, esz, norm=False, act_tanh=True)
+    yield "grouped_linear_bwd", replay_band_split_backward([dim] * nb, M, hidden, esz, grouped=True)
+    if esz == 2:
+        yield "mask_final_fwd", replay_mask_final_forward(widths, M, hidden, esz)
+        yield "mask_final_bwd", replay_mask_final_backward(widths, M, hidden, esz, tanh_in=True)
+    yield "rms_norm", replay_rms_norm(M * nb, dim, esz)
+    for shape in qk:
+        yield f"attention_gate{list(shape)}", replay_attention_gate(shape[0], shape[1], shape[2], shape[3], dim, esz)
+        for bwd in (False, True):
+            yield f"rotary_qkv{'_bwd' if bwd else ''}{list(shape)}", replay_rotary_qkv(*shape, esz, bwd)

@@ -1,0 +1,74 @@
+"""CPU: every HIP kernel of the fused train step stays inside its buffers and its LDS allocation at
+the shapes of BASELINE.json's configs (tests/bounds_model.py replays the host dispatch and the
+kernels' address arithmetic), and the replay itself detects planted addressing mistakes."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import bounds_model as bm
+
+
+@pytest.mark.parametrize("esz", [2, 4], ids=["16bit", "fp32"])
+@pytest.mark.parametrize("config", ["configs0", "configs1", "configs3", "configs4"])
+def test_fused_step_kernels_stay_in_bounds(config, esz):
+    bad = {}
+    for label, bnd in bm.all_replays(config, esz):
+        v = bnd.violations()
+        if v:
+            bad[label] = v
+    assert not bad, bad
+
+
+def test_configs4_shapes_named_in_the_review_are_covered():
+    """Band split at O = 512 over the 62 bands, M = 1896; grouped linear 512 -> 2048; mask final at
+    H = 2048 (8-wave dx blocks); qkv rotary at [124, 948, 8, 64]; the gate at D = 512."""
+    labels = [label for label, _ in bm.all_replays("configs4", 2)]
+    for want in ("band_split_fwd", "band_split_bwd", "grouped_linear_fwd", "grouped_linear_bwd",
+                 "mask_final_fwd", "mask_final_bwd", "rotary_qkv[124, 948, 8, 64]",
+                 "attention_gate[124, 948, 8, 64]"):
+        assert want in labels
+    b = bm.replay_mask_final_backward(bm.BSR_WIDTHS, 1896, 2048, 2, tanh_in=True)
+    assert b.sizes["lds"] == 3 * (32 * 256 * 2 + 8192)  # the 8-wave (HC = 256) dx kernel's ring
+    assert not b.violations()
+
+
+def test_replay_flags_a_short_buffer():
+    b = bm.replay_band_split_forward(bm.BSR_WIDTHS, 1032, 192, 2)
+    assert not b.violations()
+    b.sizes["out"] -= 2
+    assert any(v.startswith("out:") for v in b.violations())
+
+
+def test_replay_flags_a_wrong_swizzle(monkeypatch):
+    """A K-unit swizzle that names units past the four 16-byte units of a 64-byte K chunk makes the
+    mask forward's DMA read past the last row of x and W; the replay catches it (the planted
+    mistake is in the replay, on the CPU)."""
+    assert not bm.replay_mask_final_forward(bm.BSR_WIDTHS, 1032, 768, 2).violations()
+    monkeypatch.setattr(bm, "swz_k", lambda r: 4 + (r & 3))
+    v = bm.replay_mask_final_forward(bm.BSR_WIDTHS, 1032, 768, 2).violations()
+    assert any(x.startswith("x:") for x in v) and any(x.startswith("weight:") for x in v)
+
+
+def test_replay_flags_a_schedule_that_skips_units():
+    units = lambda b: 3  # noqa: E731
+    sc = bm.build_band_sched(62, 9, units)
+    bnd = bm.Bounds({})
+    bm.sched_decode(sc, 62, units, False, bnd, "ok")
+    assert not bnd.violations()
+    sc.gs[3] += 1  # XCD 2 runs one block more, XCD 3 one less: a unit runs twice
+    bnd = bm.Bounds({})
+    bm.sched_decode(sc, 62, units, False, bnd, "tampered")
+    assert any("exactly once" in v for v in bnd.violations())
+
+
+def test_replay_flags_an_unclamped_row():
+    """The row clamp of the register loaders is what keeps the last row tile in bounds: with
+    rows_valid set past the real rows the replay reports it."""
+    b = bm.Bounds({"x": 100 * 64 * 2})
+    tid = np.arange(bm.GEMM_THREADS)
+    bm.krow_loader(b, "x", 2, 64 * 64, 64, 36, 64, 64, True, 0, 2, tid)
+    assert not b.violations()
+    bm.krow_loader(b, "x", 2, 64 * 64, 64, 64, 64, 64, True, 0, 2, tid)
+    assert b.violations()
