@@ -124,8 +124,7 @@ class Workload:
             state["bs"] = e.band_split_ragged_forward_packed(w.x, w.gamma_bs, w.w_bs, w.b_bs, w.dims, write_normed=False)
 
         def bs_bwd():
-            e.band_split_ragged_backward_packed(w.g_bs, w.x, True, state["bs"][2], w.gamma_bs, w.w_bs, w.dims, True,
-                                                out=state["bs"][0].reshape(w.M, -1), bias_all=w.b_bs)
+            e.band_split_ragged_backward_packed(w.g_bs, w.x, True, state["bs"][2], w.gamma_bs, w.w_bs, w.dims, True)
 
         def qk_fwd():
             state["q"] = e.rms_norm_rotary_forward(w.q, w.gamma_q, w.cos, w.sin)

@@ -158,8 +158,9 @@ int pmsst_band_split_ragged_forward(const void* x, int64_t x_row_stride, const v
                                     const void* bias, const int64_t* dim_offsets, const int64_t* dim_inputs,
                                     int64_t band_count, int64_t rows, int64_t out_features, void* out, void* normed,
                                     float* inv_norm, int dtype, void* stream);
-/* Workspace bytes of the backward: per-row-tile dgamma partials and the per-(row, band) dots
- * (0 when rows == 0; a zero-byte workspace may be null). */
+/* Workspace bytes of the backward: per-row-tile dgamma partials, the per-(row, band, 64-wide
+ * input chunk) dot partials and the fp32 gs * gamma of every input (0 when rows == 0; a zero-byte
+ * workspace may be null). */
 size_t pmsst_band_split_ragged_backward_workspace_size(int64_t rows, int64_t total_in, int64_t band_count,
                                                        int64_t out_features);
 /* fused_band_split.cpp:316-363 band_split_ragged_backward (.cu:741-1003).  With equal widths it also
@@ -167,15 +168,15 @@ size_t pmsst_band_split_ragged_backward_workspace_size(int64_t rows, int64_t tot
  * `saved` is normed[rows, F] (saved_is_input = 0) or the forward input x[rows, F] (saved_is_input = 1,
  * normed recomputed as x * inv_norm * sqrt(I_b)).  Outputs: grad_x[rows, F], grad_gamma[F],
  * grad_weight (packed like weight), grad_bias[NB, O] or NULL.
- * `out` (the forward output [rows, NB, O]) and `bias` (the forward bias or NULL) are optional: with
- * `out` the per-row dots of the normalisation backward come from sum_o grad_out * (out - bias)
- * (= sum_i gs gamma n) and every 64-wide input chunk of every band is an independent block;
- * with out = NULL each (rows, band) block makes two passes over its band (the reference's form). */
+ * Every 64-wide input chunk of every band is an independent block that computes gs = grad_out W_b
+ * for its chunk in fp32 and its part of the per-row dot sum_i gs gamma n; a finish pass per
+ * (rows, band) adds the parts in a fixed order and writes grad_x (the reference's form makes two
+ * passes over each band instead, .cu:768-799). */
 int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, int saved_is_input,
-                                     const float* inv_norm, const void* gamma, const void* weight, const void* out,
-                                     const void* bias, const int64_t* dim_offsets, const int64_t* dim_inputs,
-                                     int64_t band_count, int64_t rows, int64_t out_features, void* grad_x,
-                                     void* grad_gamma, void* grad_weight, void* grad_bias, int dtype, void* workspace,
+                                     const float* inv_norm, const void* gamma, const void* weight,
+                                     const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
+                                     int64_t rows, int64_t out_features, void* grad_x, void* grad_gamma,
+                                     void* grad_weight, void* grad_bias, int dtype, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ grouped linear

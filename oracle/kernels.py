@@ -43,6 +43,7 @@ __all__ = [
     "grouped_linear_backward",
     "mask_estimator_final_forward",
     "mask_estimator_final_backward",
+    "mask_mlp_hidden",
     "mask_mlp_forward",
     "mask_mlp_backward",
     "attention_gate_forward",
@@ -319,13 +320,13 @@ def band_split_ragged_backward_lean(grad_out, x, inv_norm, gammas, weights, dim_
 def grouped_linear_forward(x, weight, bias, dt: str, acc=np.float64, act: str | None = None):
     """``out[m,g,o] = bias[g,o] + sum_i x[m,g,i] W[g,o,i]`` (.cu:1005-1030; bmm form tts.py:28-37).
 
-    ``act="tanh"`` applies the mask-MLP hidden activation (``inference_tanh``, fr.py:340)
-    before the single rounding to ``dt``."""
+    ``act="tanh"`` applies the mask-MLP hidden activation (``inference_tanh``, fr.py:340) to the
+    linear output rounded to ``dt`` (the reference's two steps, fr.py:338-340), then rounds again."""
     out = np.matmul(_f(x, acc).transpose(1, 0, 2), _f(weight, acc).transpose(0, 2, 1)).transpose(1, 0, 2)
     if bias is not None:
         out = out + _f(bias, acc)[None]
     if act == "tanh":
-        out = np.tanh(out)
+        out = np.tanh(round_to(out, dt))
     elif act is not None:
         raise ValueError(act)
     return round_to(out, dt)
@@ -375,11 +376,14 @@ def mask_estimator_final_forward(x, weights, bias, dim_inputs, dt: str, acc=np.f
 
 
 def mask_estimator_final_backward(grad_out, x, pre, weights, dim_inputs, dt: str, acc=np.float64,
-                                  input_act: str | None = None):
+                                  input_act: str | None = None, grad_pre_dt: str | None = None):
     """Backward of :func:`mask_estimator_final_forward` (.cu:2312-2367, .cu:2585-2704).
 
     From the saved ``pre``: ``dL = g*s``, ``dG = g*L*s*(1-s)`` with ``s = sigmoid(G)``;
     ``dbias = sum_m dpre``, ``dx_b = dpre_b W_b``, ``dW_b = dpre_b^T x_b``.
+    ``grad_pre_dt``: the grouped mode stores ``dpre`` in the tensor dtype before its GEMMs
+    (.cu:2343-2344, ``static_cast<scalar_t>``) while ``dbias`` sums the unrounded values
+    (.cu:2345-2346); ``None`` keeps ``dpre`` unrounded (the direct mode, .cu:2620-2635).
     ``input_act="tanh"``: ``x`` is a tanh output and the first result is the gradient of its
     pre-activation, ``dx * (1 - x^2)`` (chain rule through ``inference_tanh``).
     Returns ``(dx[M,NB,H], dbias[2F], [dW_b])``.
@@ -398,56 +402,50 @@ def mask_estimator_final_backward(grad_out, x, pre, weights, dim_inputs, dt: str
         gb = g[:, off[b] : off[b] + d]
         dpre = np.concatenate([gb * s, gb * left * s * (1.0 - s)], axis=1)
         dbias.append(dpre.sum(axis=0))
+        if grad_pre_dt is not None:
+            dpre = round_to(dpre, grad_pre_dt)
         dx[:, b, :] = dpre @ _f(weights[b], acc)
         dws.append(round_to(dpre.T @ x[:, b, :], dt))
     if input_act == "tanh":
-        dx = dx * (1.0 - x * x)
+        # dh in the tensor dtype (the stored product of the grouped form), then tanh's backward
+        dx = round_to(dx, dt) * (1.0 - x * x)
     elif input_act is not None:
         raise ValueError(input_act)
     return round_to(dx, dt), round_to(np.concatenate(dbias), dt), dws
 
 
-def mask_mlp_forward(x, w1, b1, weights2, bias2, dim_inputs, dt: str, acc=np.float64):
-    """Whole per-band mask MLP (depth 2): ``h = tanh(x_b W1_b^T + b1_b)`` then the final
-    Linear + GLU of :func:`mask_estimator_final_forward`.
+def mask_mlp_hidden(x, w1, b1, dt: str, acc=np.float64):
+    """Hidden layer of the mask MLP as the reference computes it: the grouped linear's output in the
+    tensor dtype (fr.py:338, .cu:1005-1030), then ``inference_tanh`` in that dtype (fr.py:340)."""
+    z = round_to(_gmm(_f(x, acc), _f(w1, acc)) + _f(b1, acc)[None], dt)
+    return round_to(np.tanh(z), dt)
 
-    Hidden layer follows grouped_linear (.cu:1005-1030) + ``inference_tanh``
-    (fr.py:340,538); ``w1[NB,Hd,dim]``, ``b1[NB,Hd]``.  ``h`` is kept unrounded
-    (it never leaves the fused kernel).  Returns ``out[M,F]``.
-    """
-    h = np.tanh(_gmm(_f(x, acc), _f(w1, acc)) + _f(b1, acc)[None])
+
+def mask_mlp_forward(x, w1, b1, weights2, bias2, dim_inputs, dt: str, acc=np.float64):
+    """Whole per-band mask MLP (depth 2): ``h = tanh(x_b W1_b^T + b1_b)`` (:func:`mask_mlp_hidden`,
+    ``w1[NB,Hd,dim]``, ``b1[NB,Hd]``), then the final Linear + GLU of
+    :func:`mask_estimator_final_forward` (fr.py:332-369).  Returns ``out[M,F]``."""
+    h = mask_mlp_hidden(x, w1, b1, dt, acc)
     out, _ = mask_estimator_final_forward(h, weights2, bias2, dim_inputs, dt, acc)
     return out
 
 
 def mask_mlp_backward(grad_out, x, w1, b1, weights2, bias2, dim_inputs, dt: str, acc=np.float64):
-    """Backward of :func:`mask_mlp_forward` with ``h`` recomputed.
-
-    Returns ``(dx[M,NB,dim], dW1[NB,Hd,dim], db1[NB,Hd], [dW2_b], dbias2[2F])``.
-    """
+    """Backward of :func:`mask_mlp_forward` with ``h`` recomputed: the final layer's backward in its
+    grouped form (``dpre`` stored in ``dt``, .cu:2343-2344) gives ``dh`` in ``dt``, the tanh backward
+    ``dz = dh (1 - h^2)`` in ``dt`` (autograd of ``inference_tanh``), then the grouped linear's backward
+    (fr.py:1042-1048).  Returns ``(dx[M,NB,dim], dW1[NB,Hd,dim], db1[NB,Hd], [dW2_b], dbias2[2F])``."""
     x = _f(x, acc)
     w1 = _f(w1, acc)
-    h = np.tanh(_gmm(x, w1) + _f(b1, acc)[None])
-    pre = []
-    off = _offsets(dim_inputs)
-    b2 = _f(bias2, acc)
-    for b, d in enumerate(dim_inputs):
-        pre.append(h[:, b, :] @ _f(weights2[b], acc).T + b2[2 * off[b] : 2 * off[b] + 2 * d])
-    pre = np.concatenate(pre, axis=1)
-    # unrounded backward through the final layer
-    dh, dbias2, dws2 = mask_estimator_final_backward(grad_out, h, pre, weights2, dim_inputs, "f64", acc)
-    dz = dh * (1.0 - h * h)
+    h = mask_mlp_hidden(x, w1, b1, dt, acc)
+    _, pre = mask_estimator_final_forward(h, weights2, bias2, dim_inputs, dt, acc)
+    dz, dbias2, dws2 = mask_estimator_final_backward(grad_out, h, pre, weights2, dim_inputs, dt, acc,
+                                                     input_act="tanh", grad_pre_dt=dt)
     dzt = dz.transpose(1, 0, 2)  # [G, M, Hd]
     dx = np.matmul(dzt, w1).transpose(1, 0, 2)
     dW1 = np.matmul(dzt.transpose(0, 2, 1), x.transpose(1, 0, 2))
     db1 = dz.sum(axis=0)
-    return (
-        round_to(dx, dt),
-        round_to(dW1, dt),
-        round_to(db1, dt),
-        [round_to(w, dt) for w in dws2],
-        round_to(dbias2, dt),
-    )
+    return round_to(dx, dt), round_to(dW1, dt), round_to(db1, dt), dws2, dbias2
 
 
 def attention_gate_forward(attn, x, weight, bias, dt: str, acc=np.float64):

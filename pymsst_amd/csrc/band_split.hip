@@ -17,11 +17,13 @@
 // stores 4 consecutive outputs of one row.  With norm off the same kernel is
 // the grouped linear of the mask-MLP hidden layer.
 //
-// Backward dx block (64 rows, band b): gs^T[i][m] = W_b^T dy^T per 64-wide i
-// chunk; pass 1 forms the per-row dot(gs*gamma, n) and the dgamma partials
-// ([m_tiles, F] workspace, reduced by col_sum_kernel), pass 2 recomputes gs and
-// writes dx.  dW block (band, 64 i x 64 o): dW^T[i][o] = sum_m n[m][i] gamma_i
-// dy[m][o], K = M.  dbias = column sums of dy.  No atomics anywhere.
+// Backward dx block (64 rows, band b, 64-wide input chunk): gs^T[i][m] = W_b^T dy^T
+// (K = O) on MFMA; the block writes t = gs * gamma (fp32), its chunk's part of the
+// per-row dot(gs * gamma, n) and the dgamma partials ([m_tiles, F], reduced by
+// col_sum_kernel).  A finish pass per (64 rows, band) adds the dot partials of the
+// band's chunks and writes dx = inv (t sqrt(I) - n dot / sqrt(I)).  dW block
+// (band, 64 i x 64 o): dW^T[i][o] = sum_m n[m][i] gamma_i dy[m][o], K = M.  dbias =
+// column sums of dy.  No atomics anywhere.
 #include "common.h"
 #include "dma_gemm.h"
 #include "gemm.h"
@@ -206,7 +208,8 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           v[r] = acc[t][j][r] * s + bv[r];
-          if (ACT == PMSST_ACT_TANH) v[r] = tanhf(v[r]);
+          // the reference rounds the linear output to the tensor dtype before tanh (fr.py:338-340)
+          if (ACT == PMSST_ACT_TANH) v[r] = tanhf(to_f32(from_f32<T>(v[r])));
         }
         store_pack<T, 4>(ot + m * kOP + ol, v);
       }
@@ -243,7 +246,8 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           v[r] = acc[t][j][r] * s + bv[r];
-          if (ACT == PMSST_ACT_TANH) v[r] = tanhf(v[r]);
+          // the reference rounds the linear output to the tensor dtype before tanh (fr.py:338-340)
+          if (ACT == PMSST_ACT_TANH) v[r] = tanhf(to_f32(from_f32<T>(v[r])));
         }
         T* dst = out + ((m0 + m) * a.NB + band) * O + o;
         if (a.ovec4) {
@@ -279,118 +283,42 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
 
 // ------------------------------------------------------------------ backward: dx + dgamma partials
 
-// Per-row dots of the band-split backward from the forward output:
-//   dot[m][b] = sum_i gs[m][i] gamma_i n[m][i] = sum_o dy[m][b][o] (out[m][b][o] - bias[b][o]),
-// since out - bias = (n * gamma) W_b^T.  One 32-lane group per (m, b) row.
-template <typename T, bool V4>
-__global__ __launch_bounds__(256) void bs_dots_kernel(const T* __restrict__ dy, const T* __restrict__ out,
-                                                      const T* __restrict__ bias, float* __restrict__ dots,
-                                                      int64_t rows, int NB, int O) {
-  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / 32;
-  const int l = threadIdx.x & 31;
-  float acc = 0.f;
-  if (row < rows) {
-    const int b = static_cast<int>(row % NB);
-    const T* pd = dy + row * O;
-    const T* po = out + row * O;
-    const T* pb = bias != nullptr ? bias + static_cast<int64_t>(b) * O : nullptr;
-    if (V4) {
-      for (int q = l * 4; q < O; q += 128) {
-        float d[4], o[4], c[4] = {0.f, 0.f, 0.f, 0.f};
-        load_pack<T, 4>(pd + q, d);
-        load_pack<T, 4>(po + q, o);
-        if (pb != nullptr) load_pack<T, 4>(pb + q, c);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc += d[j] * (o[j] - c[j]);
-      }
-    } else {
-      for (int q = l; q < O; q += 32) acc += to_f32(pd[q]) * (to_f32(po[q]) - (pb != nullptr ? to_f32(pb[q]) : 0.f));
-    }
-  }
-  acc = group_sum(acc, 32);
-  if (l == 0 && row < rows) dots[row] = acc;
-}
-
-// The same dots for 16-bit rows with O % 8 == 0 and 16-byte aligned dy / out: 8 lanes per
-// (m, b) row, U 16-byte units of dy, out and bias per lane (O = 64 U), every load issued before the
-// first product (rows past the end are clamped reads whose sums are not stored).
-template <typename T, int U>
-__global__ __launch_bounds__(256) void bs_dots16_kernel(const T* __restrict__ dy, const T* __restrict__ out,
-                                                        const T* __restrict__ bias, float* __restrict__ dots,
-                                                        int64_t rows, int NB, int O) {
-  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / 8;
-  const int l = threadIdx.x & 7;
-  const int64_t rc = row < rows ? row : rows - 1;
-  const int b = static_cast<int>(rc % NB);
-  u32x4_t vd[U], vo[U], vb[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int c = 8 * (l + 8 * u);
-    const int cc = c < O ? c : O - 8;
-    vd[u] = *reinterpret_cast<const u32x4_t*>(dy + rc * O + cc);
-    vo[u] = *reinterpret_cast<const u32x4_t*>(out + rc * O + cc);
-    vb[u] = bias != nullptr ? *reinterpret_cast<const u32x4_t*>(bias + static_cast<int64_t>(b) * O + cc)
-                            : u32x4_t{0u, 0u, 0u, 0u};
-  }
-  typedef T v8 __attribute__((ext_vector_type(8)));
-  float acc = 0.f;
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const v8 d = __builtin_bit_cast(v8, vd[u]), o = __builtin_bit_cast(v8, vo[u]), c = __builtin_bit_cast(v8, vb[u]);
-    float part = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) part += static_cast<float>(d[j]) * (static_cast<float>(o[j]) - static_cast<float>(c[j]));
-    acc += 8 * (l + 8 * u) < O ? part : 0.f;
-  }
-  acc = group_sum(acc, 8);
-  if (l == 0 && row < rows) dots[row] = acc;
-}
-
-// dx for one (64-row tile, band) block, or one (64-row tile, band, 64-wide input chunk)
-// block when SPLIT.  gs^T[i][m] = W_b^T dy^T per 64-wide input chunk (K = O), then
-//   NORM:  dx = inv (gs gamma sqrt(I) - n dot / sqrt(I)), dgamma partials sum_m gs n;
-//   !NORM: dx = gs (plain grouped linear; nsrc, inv_norm, gamma, dg_partial unused).
-// With NORM and !SPLIT the block makes two passes over the band (dots, then dx); with
-// NORM and SPLIT the per-row dots come precomputed (`dots`, from bs_dots_kernel) and
-// every block makes one pass over its chunk.
-template <typename T, bool FROM_X, bool NORM, bool SPLIT, bool V4>
+// One (64-row tile, band, 64-wide input chunk) block: gs^T[i][m] = W_b^T dy^T for the chunk
+// (K = O), then
+//   NORM:  t = gs * gamma (fp32, [M, F]), the chunk's part of dot[m] = sum_i t n (fp32, row m
+//          of a [M, pitch] array, column off_b / 64 + b + chunk) and the dgamma partials
+//          sum_m gs n ([m_tiles, F]);
+//          bs_dx_finish_kernel turns them into dx;
+//   !NORM: dx = gs (plain grouped linear; nsrc, inv_norm, gamma and the partials unused).
+// The blocks form a 1-D XCD-ordered grid: group = (band, input chunk), member = row tile,
+// so the row tiles sharing a weight chunk run on one XCD and share its L2.
+template <typename T, bool FROM_X, bool NORM, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __restrict__ dy,
                                                                  const T* __restrict__ nsrc,
                                                                  const float* __restrict__ inv_norm,
                                                                  const T* __restrict__ gamma,
                                                                  const T* __restrict__ weight, T* __restrict__ dx,
+                                                                 float* __restrict__ tbuf,
                                                                  float* __restrict__ dg_partial,
-                                                                 const float* __restrict__ dots, int max_ichunks,
-                                                                 XcdGrid xg, BandArgs a) {
+                                                                 float* __restrict__ pdot, int pitch,
+                                                                 int max_ichunks, XcdGrid xg, BandArgs a) {
   constexpr int kBI = 64;
-  constexpr int kPasses = (NORM && !SPLIT) ? 2 : 1;
   __shared__ T lds[gemm_lds_elems<T, kBI, kBM>()];
   __shared__ float sinv[kBM];
   __shared__ float sdot[4][kBM];
   using S = TileShape<kBI, kBM, 4, 1>;  // TR = 1, TC = 4
 
   const int O = a.O;
-  // SPLIT: 1-D XCD-ordered grid, group = (band, input chunk), member = row tile (the weight
-  // chunk is shared in L2); otherwise grid (row tile, band)
-  int band, ichunk;
-  int64_t mtile;
-  if (SPLIT) {
-    uint32_t grp, mt;
-    if (!xcd_block(xg, grp, mt)) return;
-    band = a.NB - 1 - static_cast<int>(grp) / max_ichunks;  // widest bands first
-    ichunk = static_cast<int>(grp) % max_ichunks;
-    mtile = mt;
-  } else {
-    band = a.NB - 1 - static_cast<int>(blockIdx.y);
-    ichunk = 0;
-    mtile = blockIdx.x;
-  }
+  uint32_t grp, mt;
+  if (!xcd_block(xg, grp, mt)) return;
+  const int band = a.NB - 1 - static_cast<int>(grp) / max_ichunks;  // widest bands first
+  const int ichunk = static_cast<int>(grp) % max_ichunks;
+  const int64_t mtile = mt;
   const int64_t m0 = mtile * kBM;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
-  const int i_begin = ichunk * kBI;
-  if (i_begin >= I) return;  // uniform over the block
-  const int i_end = SPLIT ? (i_begin + kBI < I ? i_begin + kBI : I) : I;
+  const int i0 = ichunk * kBI;
+  if (i0 >= I) return;  // uniform over the block
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rows_valid = static_cast<int>(a.M - m0 < kBM ? a.M - m0 : kBM);
   const T* wb = weight + static_cast<int64_t>(O) * off;  // [O][I]
@@ -398,108 +326,142 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
   const float root = sqrtf(static_cast<float>(I));
 
   if (NORM) {
-    if (tid < kBM) {
-      sinv[tid] = tid < rows_valid ? inv_norm[(m0 + tid) * a.NB + band] : 0.f;
-      if (SPLIT) sdot[0][tid] = tid < rows_valid ? dots[(m0 + tid) * a.NB + band] : 0.f;
-    }
+    if (tid < kBM) sinv[tid] = tid < rows_valid ? inv_norm[(m0 + tid) * a.NB + band] : 0.f;
     __syncthreads();
   }
 
-  float dotp[4] = {0.f, 0.f, 0.f, 0.f};  // per m-tile j: m = 16 j + (lane & 15)
-  for (int pass = 0; pass < kPasses; ++pass) {
-    if (NORM && !SPLIT && pass == 1) {
+  // A[i][o] = W_b[o][i0 + i] (MN-contiguous in i);  B[m][o] = dy[m0 + m][band][o]
+  MNLoader<T, kBI, V4> la{wb + i0, I, I - i0, O};
+  KRowLoader<T, kBM, V4> lb{dyb, static_cast<int64_t>(a.NB) * O, rows_valid, O};
+  f32x4_t acc[S::kTR][S::kTC];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float v = dotp[j];
-        v += __shfl_xor(v, 16, kWave);
-        v += __shfl_xor(v, 32, kWave);
-        if (lane < 16) sdot[wave][j * 16 + lane] = v;
-      }
-      __syncthreads();
-      if (tid < kBM) sdot[0][tid] = sdot[0][tid] + sdot[1][tid] + sdot[2][tid] + sdot[3][tid];
-      __syncthreads();
-    }
-    // dot partials are gathered in pass 0 of the two-pass form; dx is written in the last pass;
-    // dgamma partials in pass 0 of every NORM form
-    const bool gather_dot = NORM && !SPLIT && pass == 0;
-    const bool write_dx = pass == kPasses - 1;
-    for (int i0 = i_begin; i0 < i_end; i0 += kBI) {
-      // A[i][o] = W_b[o][i0 + i] (MN-contiguous in i);  B[m][o] = dy[m0 + m][band][o]
-      MNLoader<T, kBI, V4> la{wb + i0, I, I - i0, O};
-      KRowLoader<T, kBM, V4> lb{dyb, static_cast<int64_t>(a.NB) * O, rows_valid, O};
-      f32x4_t acc[S::kTR][S::kTC];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[0][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      gemm_mainloop<T, kBI, kBM, 4, 1, PMSST_BS_DX_DEPTH>(la, lb, O, lds, acc);
+  for (int j = 0; j < 4; ++j) acc[0][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  gemm_mainloop<T, kBI, kBM, 4, 1, PMSST_BS_DX_DEPTH>(la, lb, O, lds, acc);
 
-      // lane holds gs[m = 16 j + (lane & 15)][i = i0 + 16 wave + 4 (lane >> 4) + r]
-      const int il = i0 + wave * 16 + 4 * (lane >> 4);
-      if (!NORM) {
+  // lane holds gs[m = 16 j + (lane & 15)][i = i0 + 16 wave + 4 (lane >> 4) + r]
+  const int il = i0 + wave * 16 + 4 * (lane >> 4);
+  if (!NORM) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = j * 16 + (lane & 15);
-          if (m >= rows_valid || il >= I) continue;
-          float o[4] = {acc[0][j][0], acc[0][j][1], acc[0][j][2], acc[0][j][3]};
-          T* dp = dx + (m0 + m) * a.F + off + il;
-          if (a.vec4) {
-            store_pack<T, 4>(dp, o);
-          } else {
-            for (int r = 0; r < 4 && il + r < I; ++r) dp[r] = from_f32<T>(o[r]);
-          }
-        }
-        continue;
+    for (int j = 0; j < 4; ++j) {
+      const int m = j * 16 + (lane & 15);
+      if (m >= rows_valid || il >= I) continue;
+      float o[4] = {acc[0][j][0], acc[0][j][1], acc[0][j][2], acc[0][j][3]};
+      T* dp = dx + (m0 + m) * a.F + off + il;
+      if (a.vec4) {
+        store_pack<T, 4>(dp, o);
+      } else {
+        for (int r = 0; r < 4 && il + r < I; ++r) dp[r] = from_f32<T>(o[r]);
       }
-      float g[4];
+    }
+    return;
+  }
+  float g[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) g[r] = il + r < I ? to_f32(gamma[off + il + r]) : 0.f;
-      float dgp[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < 4; ++r) g[r] = il + r < I ? to_f32(gamma[off + il + r]) : 0.f;
+  float dgp[4] = {0.f, 0.f, 0.f, 0.f};
+  float dotp[4] = {0.f, 0.f, 0.f, 0.f};  // per m-tile j
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = j * 16 + (lane & 15);
-        if (m >= rows_valid || il >= I) continue;
-        const T* np = nsrc + (m0 + m) * a.F + off + il;
-        float n[4];
-        if (a.vec4) {
-          load_pack<T, 4>(np, n);
-        } else {
+  for (int j = 0; j < 4; ++j) {
+    const int m = j * 16 + (lane & 15);
+    if (m >= rows_valid || il >= I) continue;
+    const T* np = nsrc + (m0 + m) * a.F + off + il;
+    float n[4];
+    if (a.vec4) {
+      load_pack<T, 4>(np, n);
+    } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) n[r] = il + r < I ? to_f32(np[r]) : 0.f;
-        }
-        if (FROM_X) {
-          const float s = sinv[m] * root;
+      for (int r = 0; r < 4; ++r) n[r] = il + r < I ? to_f32(np[r]) : 0.f;
+    }
+    if (FROM_X) {
+      const float sc = sinv[m] * root;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) n[r] *= s;
-        }
-        if (pass == 0) {
+      for (int r = 0; r < 4; ++r) n[r] *= sc;
+    }
+    float t[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            if (gather_dot) dotp[j] += acc[0][j][r] * g[r] * n[r];
-            dgp[r] += acc[0][j][r] * n[r];
-          }
-        }
-        if (write_dx) {
-          const float inv = sinv[m];
-          const float dots_m = sdot[0][m] / root;
-          float o[4];
+    for (int r = 0; r < 4; ++r) {
+      t[r] = acc[0][j][r] * g[r];
+      dotp[j] += t[r] * n[r];
+      dgp[r] += acc[0][j][r] * n[r];
+    }
+    float* tp = tbuf + (m0 + m) * a.F + off + il;
+    if (a.vec4) {
+      *reinterpret_cast<float4*>(tp) = make_float4(t[0], t[1], t[2], t[3]);
+    } else {
+      for (int r = 0; r < 4 && il + r < I; ++r) tp[r] = t[r];
+    }
+  }
+  // dot partial of the chunk: the 4 lane groups of a wave, then the 4 waves (16 i each)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = inv * (acc[0][j][r] * g[r] * root - n[r] * dots_m);
-          T* dp = dx + (m0 + m) * a.F + off + il;
-          if (a.vec4) {
-            store_pack<T, 4>(dp, o);
-          } else {
-            for (int r = 0; r < 4 && il + r < I; ++r) dp[r] = from_f32<T>(o[r]);
-          }
-        }
-      }
-      if (pass == 0) {
+  for (int j = 0; j < 4; ++j) {
+    float v = dotp[j];
+    v += __shfl_xor(v, 16, kWave);
+    v += __shfl_xor(v, 32, kWave);
+    if (lane < 16) sdot[wave][j * 16 + lane] = v;
+  }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dgp[r] = group_sum(dgp[r], 16);
-        if ((lane & 15) == 0) {
-          float* dst = dg_partial + mtile * a.F + off;
+  for (int r = 0; r < 4; ++r) dgp[r] = group_sum(dgp[r], 16);
+  if ((lane & 15) == 0) {
+    float* dst = dg_partial + mtile * a.F + off;
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (il + r < I) dst[il + r] = dgp[r];
-        }
+    for (int r = 0; r < 4; ++r)
+      if (il + r < I) dst[il + r] = dgp[r];
+  }
+  __syncthreads();
+  if (tid < rows_valid)
+    pdot[(m0 + tid) * pitch + off / 64 + band + ichunk] = (sdot[0][tid] + sdot[1][tid]) + (sdot[2][tid] + sdot[3][tid]);
+}
+
+// dx of one (64-row tile, band): dot[m] = sum of the band's chunk partials (fixed order),
+// dx = inv (t sqrt(I) - n dot / sqrt(I)) with n = x inv sqrt(I) (FROM_X) or the saved normed.
+// Thread q of the block walks the tile's (row, 4-element quad) pairs row-major.
+template <typename T, bool FROM_X, bool V4>
+__global__ __launch_bounds__(256) void bs_dx_finish_kernel(const float* __restrict__ tbuf, const T* __restrict__ nsrc,
+                                                           const float* __restrict__ inv_norm,
+                                                           const float* __restrict__ pdot, T* __restrict__ dx,
+                                                           int pitch, BandArgs a) {
+  __shared__ float sinv[kBM];
+  __shared__ float sdot[kBM];
+  const int band = a.NB - 1 - static_cast<int>(blockIdx.y);
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBM;
+  const int off = static_cast<int>(a.offsets[band]);
+  const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  const int rows_valid = static_cast<int>(a.M - m0 < kBM ? a.M - m0 : kBM);
+  const int tid = threadIdx.x;
+  const float root = sqrtf(static_cast<float>(I));
+  if (tid < rows_valid) {
+    const int nch = (I + 63) / 64;
+    const float* pd = pdot + (m0 + tid) * pitch + off / 64 + band;
+    float d = 0.f;
+    for (int c = 0; c < nch; ++c) d += pd[c];
+    const float inv = inv_norm[(m0 + tid) * a.NB + band];
+    sinv[tid] = inv;
+    sdot[tid] = d / root;
+  }
+  __syncthreads();
+  const int nq = (I + 3) / 4;
+  for (int q = tid; q < rows_valid * nq; q += 256) {
+    const int r = q / nq;
+    const int k = (q - r * nq) * 4;
+    const int64_t e = (m0 + r) * a.F + off + k;
+    const float inv = sinv[r];
+    const float ns = FROM_X ? inv * root : 1.f;
+    const float c = sdot[r];
+    float n[4], t[4], o[4];
+    if (V4) {
+      const float4 tv = *reinterpret_cast<const float4*>(tbuf + e);
+      t[0] = tv.x;
+      t[1] = tv.y;
+      t[2] = tv.z;
+      t[3] = tv.w;
+      load_pack<T, 4>(nsrc + e, n);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = inv * (t[j] * root - n[j] * ns * c);
+      store_pack<T, 4>(dx + e, o);
+    } else {
+      for (int j = 0; j < 4 && k + j < I; ++j) {
+        const float nv = to_f32(nsrc[e + j]) * ns;
+        dx[e + j] = from_f32<T>(inv * (tbuf[e + j] * root - nv * c));
       }
     }
   }
@@ -941,18 +903,24 @@ size_t dg_partial_bytes(int64_t M, int F) {
   return align_up(static_cast<size_t>((M + kBM - 1) / kBM) * static_cast<size_t>(F) * sizeof(float), 256);
 }
 
-size_t dots_bytes(int64_t M, int NB) { return align_up(static_cast<size_t>(M) * NB * sizeof(float), 256); }
+// Row pitch of the dot partials: chunk c of band b sits at column off_b / 64 + b + c, which is
+// injective over (b, c < ceil(I_b / 64)) and below F / 64 + NB + 1.
+int pdot_pitch(int F, int NB) { return F / 64 + NB + 1; }
 
-// [dgamma partials | dots]
-size_t bwd_workspace(int64_t M, int F, int NB, int O) {
-  (void)O;
-  return dg_partial_bytes(M, F) + dots_bytes(M, NB);
+size_t pdot_bytes(int64_t M, int F, int NB) {
+  return align_up(static_cast<size_t>(M) * static_cast<size_t>(pdot_pitch(F, NB)) * sizeof(float), 256);
+}
+
+size_t tbuf_bytes(int64_t M, int F) { return align_up(static_cast<size_t>(M) * F * sizeof(float), 256); }
+
+// [dgamma partials | dot partials | t = gs * gamma (fp32)]
+size_t bwd_workspace(int64_t M, int F, int NB) {
+  return M == 0 ? 0 : dg_partial_bytes(M, F) + pdot_bytes(M, F, NB) + tbuf_bytes(M, F);
 }
 
 template <typename T>
 int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_norm, const void* gamma,
-               const void* weight, const void* out, const void* bias, const int64_t* offsets,
-               const int64_t* dim_inputs, const HostBands& hb,
+               const void* weight, const int64_t* offsets, const int64_t* dim_inputs, const HostBands& hb,
                int64_t M, int64_t O, void* dx, void* dgamma, void* dw, void* db, void* workspace,
                size_t workspace_bytes, hipStream_t stream) {
   const char* op = "band_split_ragged_backward";
@@ -962,7 +930,7 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
                 "%s: null pointer", op);
   PMSST_REQUIRE(gemm_stride_ok(hb.F, sizeof(T)) && gemm_stride_ok(int64_t{hb.NB} * O, sizeof(T)),
                 "%s: rows too long for 32-bit tile offsets", op);
-  const size_t need = bwd_workspace(M, hb.F, hb.NB, static_cast<int>(O));
+  const size_t need = bwd_workspace(M, hb.F, hb.NB);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     return fail(PMSST_EWORKSPACE, "%s: workspace of %zu bytes needed", op, need);
   }
@@ -974,70 +942,39 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   const T* pn = static_cast<const T*>(nsrc);
   const T* pg = static_cast<const T*>(gamma);
   const T* pw = static_cast<const T*>(weight);
-  float* partial = static_cast<float*>(workspace);
-  float* dots = reinterpret_cast<float*>(static_cast<char*>(workspace) + dg_partial_bytes(M, hb.F));
+  char* ws = static_cast<char*>(workspace);
+  float* partial = reinterpret_cast<float*>(ws);
+  float* pdot = reinterpret_cast<float*>(ws + dg_partial_bytes(M, hb.F));
+  float* tbuf = reinterpret_cast<float*>(ws + dg_partial_bytes(M, hb.F) + pdot_bytes(M, hb.F, hb.NB));
+  const int pitch = pdot_pitch(hb.F, hb.NB);
   const int m_tiles = static_cast<int>((M + kBM - 1) / kBM);
   if (M > 0) {
     const bool v4 = a.vec4 && a.ovec4;
-    const bool split = out != nullptr;  // dots from the forward output: one pass per 64-wide chunk
     const int max_ichunks = (hb.max_width + 63) / 64;
-    if (split) {
-      const bool dv4 = a.ovec4 && aligned_to(out, 4 * sizeof(T)) && aligned_to(bias, 4 * sizeof(T));
-      const int64_t rows = M * hb.NB;
-      const dim3 gd(static_cast<unsigned>((rows * 32 + 255) / 256));
-      bool d16 = false;  // 16-bit rows, O % 8 == 0, 16-byte aligned: 8 lanes per row, 16-byte loads
-      if constexpr (sizeof(T) == 2) {
-        d16 = O % 8 == 0 && aligned_to(dy, 16) && aligned_to(out, 16) && aligned_to(bias, 16) &&
-              (rows * 8 + 255) / 256 < (int64_t{1} << 31);
-        if (d16) {
-          const dim3 g16(static_cast<unsigned>((rows * 8 + 255) / 256));
-#define PMSST_DOTS16(UU)                                                                                       \
-  hipLaunchKernelGGL((bs_dots16_kernel<T, UU>), g16, dim3(256), 0, stream, pdy, static_cast<const T*>(out), \
-                     static_cast<const T*>(bias), dots, rows, hb.NB, static_cast<int>(O))
-          switch ((O + 63) / 64) {
-            case 1: PMSST_DOTS16(1); break;
-            case 2: PMSST_DOTS16(2); break;
-            case 3: PMSST_DOTS16(3); break;
-            case 4: PMSST_DOTS16(4); break;
-            case 5: PMSST_DOTS16(5); break;
-            case 6: PMSST_DOTS16(6); break;
-            case 7: PMSST_DOTS16(7); break;
-            default: PMSST_DOTS16(8); break;
-          }
-#undef PMSST_DOTS16
-        }
-      }
-      if (!d16) {
-        if (dv4)
-          hipLaunchKernelGGL((bs_dots_kernel<T, true>), gd, dim3(256), 0, stream, pdy, static_cast<const T*>(out),
-                             static_cast<const T*>(bias), dots, rows, hb.NB, static_cast<int>(O));
-        else
-          hipLaunchKernelGGL((bs_dots_kernel<T, false>), gd, dim3(256), 0, stream, pdy, static_cast<const T*>(out),
-                             static_cast<const T*>(bias), dots, rows, hb.NB, static_cast<int>(O));
-      }
-      int rc = check_launch("bs_dots_kernel");
-      if (rc != PMSST_OK) return rc;
-    }
     const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_ichunks), static_cast<uint32_t>(m_tiles)};
-    const dim3 grid = split ? dim3(xg.blocks()) : dim3(static_cast<unsigned>(m_tiles), static_cast<unsigned>(hb.NB));
-#define PMSST_BDX(FX, SPLIT, V4)                                                                               \
-  hipLaunchKernelGGL((bs_bwd_dx_kernel<T, FX, true, SPLIT, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, \
-                     inv_norm, pg, pw, static_cast<T*>(dx), partial, dots, max_ichunks, xg, a)
-    if (split) {
-      if (from_x) {
-        if (v4) PMSST_BDX(true, true, true); else PMSST_BDX(true, true, false);
-      } else {
-        if (v4) PMSST_BDX(false, true, true); else PMSST_BDX(false, true, false);
-      }
+#define PMSST_BDX(FX, V4)                                                                                          \
+  hipLaunchKernelGGL((bs_bwd_dx_kernel<T, FX, true, V4>), dim3(xg.blocks()), dim3(kGemmThreads), 0, stream, pdy, pn, \
+                     inv_norm, pg, pw, static_cast<T*>(dx), tbuf, partial, pdot, pitch, max_ichunks, xg, a)
+    if (from_x) {
+      if (v4) PMSST_BDX(true, true); else PMSST_BDX(true, false);
     } else {
-      if (from_x) {
-        if (v4) PMSST_BDX(true, false, true); else PMSST_BDX(true, false, false);
-      } else {
-        if (v4) PMSST_BDX(false, false, true); else PMSST_BDX(false, false, false);
-      }
+      if (v4) PMSST_BDX(false, true); else PMSST_BDX(false, false);
     }
 #undef PMSST_BDX
     int rc = check_launch("bs_bwd_dx_kernel");
+    if (rc != PMSST_OK) return rc;
+    const dim3 gf(static_cast<unsigned>(m_tiles), static_cast<unsigned>(hb.NB));
+    const bool fv4 = a.vec4;
+#define PMSST_FIN(FX, V4)                                                                                  \
+  hipLaunchKernelGGL((bs_dx_finish_kernel<T, FX, V4>), gf, dim3(256), 0, stream, tbuf, pn, inv_norm, pdot, \
+                     static_cast<T*>(dx), pitch, a)
+    if (from_x) {
+      if (fv4) PMSST_FIN(true, true); else PMSST_FIN(true, false);
+    } else {
+      if (fv4) PMSST_FIN(false, true); else PMSST_FIN(false, false);
+    }
+#undef PMSST_FIN
+    rc = check_launch("bs_dx_finish_kernel");
     if (rc != PMSST_OK) return rc;
   }
   bool dw_done = false;
@@ -1108,11 +1045,11 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
     const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_ichunks), static_cast<uint32_t>((M + kBM - 1) / kBM)};
     const dim3 grid(xg.blocks());
     if (a.vec4 && a.ovec4)
-      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true, true>), grid, dim3(kGemmThreads), 0, stream, pdy,
-                         px, nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, max_ichunks, xg, a);
+      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
+                         nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, nullptr, 0, max_ichunks, xg, a);
     else
-      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true, false>), grid, dim3(kGemmThreads), 0, stream, pdy,
-                         px, nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, max_ichunks, xg, a);
+      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
+                         nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, nullptr, 0, max_ichunks, xg, a);
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
@@ -1207,14 +1144,12 @@ int pmsst_grouped_linear_backward(const void* grad_out, const void* x, const voi
 size_t pmsst_band_split_ragged_backward_workspace_size(int64_t rows, int64_t total_in, int64_t band_count,
                                                        int64_t out_features) {
   if (rows < 0 || total_in <= 0 || band_count <= 0 || out_features <= 0) return 0;
-  return bwd_workspace(rows, static_cast<int>(total_in), static_cast<int>(band_count),
-                       static_cast<int>(out_features));
+  return bwd_workspace(rows, static_cast<int>(total_in), static_cast<int>(band_count));
 }
 
 int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, int saved_is_input,
-                                     const float* inv_norm, const void* gamma, const void* weight, const void* out,
-                                     const void* bias, const int64_t* dim_offsets, const int64_t* dim_inputs,
-                                     int64_t band_count,
+                                     const float* inv_norm, const void* gamma, const void* weight,
+                                     const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
                                      int64_t rows, int64_t out_features, void* grad_x, void* grad_gamma,
                                      void* grad_weight, void* grad_bias, int dtype, void* workspace,
                                      size_t workspace_bytes, void* stream) {
@@ -1223,8 +1158,7 @@ int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, in
   if (rc != PMSST_OK) return rc;
   return with_dtype(dtype, "band_split_ragged_backward", [&](auto tag) {
     using T = decltype(tag);
-    return launch_bwd<T>(grad_out, saved, saved_is_input != 0, inv_norm, gamma, weight, out, bias, dim_offsets,
-                         dim_inputs, hb,
+    return launch_bwd<T>(grad_out, saved, saved_is_input != 0, inv_norm, gamma, weight, dim_offsets, dim_inputs, hb,
                          rows, out_features, grad_x, grad_gamma, grad_weight, grad_bias, workspace, workspace_bytes,
                          static_cast<hipStream_t>(stream));
   });

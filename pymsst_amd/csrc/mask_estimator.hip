@@ -526,7 +526,9 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dx_kernel(const T* __rest
           for (int r = 0; r < 4 && h + r < H; ++r) t[r] = to_f32(x[idx + r]);
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] *= 1.0f - t[r] * t[r];
+        // dh is rounded to the tensor dtype before the tanh factor, as the reference's autograd
+        // rounds the final layer's input gradient before tanh's backward
+        for (int r = 0; r < 4; ++r) v[r] = to_f32(from_f32<T>(v[r])) * (1.0f - t[r] * t[r]);
       }
       if (a.vec4) {
         store_pack<T, 4>(dst, v);
@@ -689,7 +691,8 @@ __global__ __launch_bounds__(512) void me_bwd_dx_dma_kernel(const T* __restrict_
   // m = 64 wc + 16 j + lane % 16 (8-byte runs of 16 rows per instruction); the tile is staged as
   // [128 m][HC h] (row pitch 2 HC + 16 bytes) and written back as 16-byte pieces, 2 HC contiguous
   // bytes per row, so HBM sees whole lines.  With a tanh input the factor 1 - x^2 is applied
-  // before staging (x read at the lane's own positions), so dx is rounded once.
+  // before staging (x read at the lane's own positions) to dpre W rounded to the tensor dtype, the
+// reference's rounding point of the hidden activation's input gradient.
   __syncthreads();  // every wave is done with the ring (its last wait was vmcnt(0))
   constexpr int kOP = HC + 8;  // staged row pitch in elements
   static_assert(kDxBMd * kOP * 2 <= S * kStage, "staging tile");
@@ -706,7 +709,7 @@ __global__ __launch_bounds__(512) void me_bwd_dx_dma_kernel(const T* __restrict_
         float tx[4];
         load_pack<T, 4>(x + ((m0 + mc) * a.NB + band) * H + hc * HC + h, tx);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] *= 1.0f - tx[r] * tx[r];
+        for (int r = 0; r < 4; ++r) v[r] = to_f32(from_f32<T>(v[r])) * (1.0f - tx[r] * tx[r]);
       }
       store_pack<T, 4>(ot + m * kOP + h, v);
     }

@@ -640,13 +640,11 @@ class HipFusedExtension:
         return [out, normed, inv]
 
     def band_split_ragged_backward_packed(self, grad_out, saved, saved_is_input, inv_norm, gamma_all, weight_all,
-                                          dim_inputs, has_bias=True, out=None, bias_all=None):
+                                          dim_inputs, has_bias=True):
         """Ragged band split backward on packed parameters.
 
         ``saved`` is ``normed[M,F]`` (``saved_is_input=False``) or the forward input
-        ``x[M,F]`` (``True``; normed recomputed).  With the forward output ``out`` (and its
-        ``bias_all``) the per-row dots come from ``sum_o dy * (out - bias)`` and the kernel
-        runs one block per 64-wide input chunk.  Returns packed
+        ``x[M,F]`` (``True``; normed recomputed).  Returns packed
         ``[grad_x[M,F], grad_gamma[F], grad_weight (packed), grad_bias[NB*O] | None]``.
         """
         host, dev_offs, offs = self._bands(dim_inputs, grad_out.device)
@@ -664,8 +662,7 @@ class HipFusedExtension:
         with _DeviceGuard(dev):
             rc = self._lib.pmsst_band_split_ragged_backward(
                 _ptr(grad_out), _ptr(saved), 1 if saved_is_input else 0, _ptr(inv_norm.contiguous()),
-                _ptr(gamma_all), _ptr(weight_all), _ptr(out.contiguous() if out is not None else None),
-                _ptr(bias_all.contiguous() if (out is not None and bias_all is not None) else None), _ptr(dev_offs),
+                _ptr(gamma_all), _ptr(weight_all), _ptr(dev_offs),
                 host, nb, m, o, _ptr(dx), _ptr(dg), _ptr(dw), _ptr(db), dtype_code(grad_out.dtype), _ptr(ws),
                 ws.numel(), _stream(dev),
             )

@@ -958,9 +958,7 @@ class _FusedBandSplitRagged(torch.autograd.Function):
             out, _, inv_norm = extension.band_split_ragged_forward_packed(
                 x, gamma_all, weight_all, bias_all, dim_inputs, write_normed=False
             )
-            # the output itself is saved too (no extra memory: the next layer holds it); the
-            # backward takes the per-row dots from it instead of a second pass over each band
-            ctx.save_for_backward(x, inv_norm, gamma_all, weight_all, out, bias_all)
+            ctx.save_for_backward(x, inv_norm, gamma_all, weight_all)
             return out
         out, normed, inv_norm = extension.band_split_ragged_forward(
             x, list(gammas), list(weights), list(biases), list(dim_inputs), dim_offsets
@@ -975,10 +973,9 @@ class _FusedBandSplitRagged(torch.autograd.Function):
         grad_out = grad_out.reshape(grad_out.shape[0], nb, o).contiguous()
         dims = [int(d) for d in ctx.dim_inputs]
         if ctx.packed:
-            x, inv_norm, gamma_all, weight_all, out, bias_all = ctx.saved_tensors
+            x, inv_norm, gamma_all, weight_all = ctx.saved_tensors
             dx, dg, dw, db = ctx.extension.band_split_ragged_backward_packed(
-                grad_out, x, True, inv_norm, gamma_all, weight_all, ctx.dim_inputs, True, out=out.reshape(-1, o),
-                bias_all=bias_all,
+                grad_out, x, True, inv_norm, gamma_all, weight_all, ctx.dim_inputs, True
             )
             dgs = dg.split(dims)
             dws = [v.view(o, d) for v, d in zip(dw.split([o * d for d in dims]), dims)]

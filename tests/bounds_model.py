@@ -216,15 +216,23 @@ def sched_decode(sc: BandSched, nb: int, units, last_first: bool, bnd: Bounds, w
 # ----------------------------------------------------------------------------- gemm.h loaders
 
 
-def krow_loader(bnd, buf, esz, base_el, stride, rows_valid, k_valid, rows, v4, kbeg, nk, tid):
-    """gemm.h KRowLoader: thread t moves quads (r, k) = ((t + 256 i) / 8, 4 (t % 8)) of every chunk;
-    rows past rows_valid are clamped (interior) or masked (edge chunk)."""
+def krow_rows(tid, rows):
+    """Tile rows of each thread's quads in a KRowLoader of ``rows`` rows: [threads, quads]."""
     kq = rows * (CHUNK_K // 4) // GEMM_THREADS
-    i = np.arange(kq)
-    r = (tid[:, None] + i[None, :] * GEMM_THREADS) // (CHUNK_K // 4)
+    return (tid[:, None] + np.arange(kq)[None, :] * GEMM_THREADS) // (CHUNK_K // 4)
+
+
+def krow_loader(bnd, buf, esz, base_el, stride, rows_valid, k_valid, rows, v4, kbeg, nk, tid, row_map=None):
+    """gemm.h KRowLoader: thread t moves quads (r, k) = ((t + 256 i) / 8, 4 (t % 8)) of every chunk;
+    rows past rows_valid are clamped (interior) or masked (edge chunk).  ``row_map`` = (src, row_ok)
+    arrays replace the default map (a loader's own prepare())."""
+    r = krow_rows(tid, rows)
     lane_k = (tid % (CHUNK_K // 4)) * 4
-    src = np.minimum(r, rows_valid - 1)
-    row_ok = r < rows_valid
+    if row_map is None:
+        src = np.minimum(r, rows_valid - 1)
+        row_ok = r < rows_valid
+    else:
+        src, row_ok = row_map
     for c in steps(nk):
         k = kbeg + CHUNK_K * c + lane_k[:, None]
         edge = (c == 0 and kbeg < 0) or not v4
@@ -363,58 +371,27 @@ def replay_band_split_forward(widths, M, O, esz, *, norm=True, x_stride=None, ha
 
 
 def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=False):
-    """band_split.hip launch_bwd (saved input, forward output given: the per-row dots kernel, the split
-    dx kernel, the DMA-ring or register dW kernel, col_sum) or launch_grouped_bwd (grouped=True)."""
+    """band_split.hip launch_bwd (saved input: the split dx kernel writing t = gs * gamma and the dot
+    partials, bs_dx_finish_kernel, the DMA-ring or register dW kernel, col_sum) or launch_grouped_bwd
+    (grouped=True: the norm-free dx and dW kernels)."""
     nb, F = len(widths), int(sum(widths))
     offs = _offs(widths)
     m_tiles = cdiv(M, 64)
     dgp = cdiv(m_tiles * F * 4, 256) * 256
+    pitch = F // 64 + nb + 1
+    pdb = cdiv(M * pitch * 4, 256) * 256
+    tbb = cdiv(M * F * 4, 256) * 256
     sizes = {"dy": M * nb * O * esz, "x": M * F * esz, "inv_norm": M * nb * 4, "gamma": F * esz,
-             "weight": O * F * esz, "out": M * nb * O * esz, "bias": nb * O * esz, "dx": M * F * esz,
-             "dgamma": F * esz, "dw": O * F * esz, "db": nb * O * esz, "offsets": (nb + 1) * 8,
-             "workspace": 0 if grouped else dgp + cdiv(M * nb * 4, 256) * 256, "lds": 0}
+             "weight": O * F * esz, "dx": M * F * esz, "dgamma": F * esz, "dw": O * F * esz,
+             "db": nb * O * esz, "offsets": (nb + 1) * 8,
+             "workspace": 0 if grouped else dgp + pdb + tbb, "lds": 0, "lds_finish": 2 * 64 * 4}
     bnd = Bounds(sizes)
     vec4 = all(w % 4 == 0 for w in widths)
     ovec4 = O % 4 == 0
     tid = np.arange(GEMM_THREADS)
     lane, wave = tid & 63, tid >> 6
     norm = not grouped
-    # -- per-row dots (launch_bwd, split form)
-    if norm and M > 0:
-        rows = M * nb
-        if esz == 2 and O % 8 == 0:
-            U = min(8, cdiv(O, 64))
-            nblk = cdiv(rows * 8, 256)
-            for blk in sorted({0, nblk - 1}):
-                row = (blk * 256 + tid) // 8
-                l8 = tid & 7
-                rc = np.minimum(row, rows - 1)
-                b = rc % nb
-                for u in range(U):
-                    cc0 = 8 * (l8 + 8 * u)
-                    cc = np.where(cc0 < O, cc0, O - 8)
-                    bnd.touch("dy", (rc * O + cc) * esz, 16)
-                    bnd.touch("out", (rc * O + cc) * esz, 16)
-                    if has_bias:
-                        bnd.touch("bias", (b * O + cc) * esz, 16)
-                bnd.touch("workspace", dgp + row * 4, 4, (l8 == 0) & (row < rows))
-        else:
-            nblk = cdiv(rows * 32, 256)
-            for blk in sorted({0, nblk - 1}):
-                row = (blk * 256 + tid) // 32
-                l32 = tid & 31
-                ok = row < rows
-                b = row % nb
-                step = 4 if (ovec4 and vec4) else 1
-                for q0 in range(0, O, 128 if step == 4 else 32):
-                    q = q0 + l32 * step
-                    okq = ok & (q < O)
-                    bnd.touch("dy", (row * O + q) * esz, step * esz, okq)
-                    bnd.touch("out", (row * O + q) * esz, step * esz, okq)
-                    if has_bias:
-                        bnd.touch("bias", (b * O + q) * esz, step * esz, okq)
-                bnd.touch("workspace", dgp + row * 4, 4, (l32 == 0) & ok)
-    # -- dx (split: one block per (band, 64-wide input chunk, 64 rows))
+    # -- dx (one block per (band, 64-wide input chunk, 64 rows))
     max_ich = cdiv(max(widths), 64)
     sizes["lds"] = gemm_lds_bytes(esz, 64, 64) + 64 * 4 + 4 * 64 * 4
     if M > 0:
@@ -434,7 +411,8 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
                     r64 = np.arange(64)
                     if norm:
                         bnd.touch("inv_norm", ((m0 + r64) * nb + band) * 4, 4, r64 < rv)
-                        bnd.touch("workspace", dgp + ((m0 + r64) * nb + band) * 4, 4, r64 < rv)
+                        # dot partial of the chunk: row m, column off / 64 + band + chunk
+                        bnd.touch("workspace", dgp + ((m0 + r64) * pitch + off // 64 + band + ich) * 4, 4, r64 < rv)
                     nk = cdiv(O, CHUNK_K)
                     kbeg = O - nk * CHUNK_K
                     mn_loader(bnd, "weight", esz, O * off + i0, I, I - i0, O, 64, v4, kbeg, nk, tid)
@@ -447,20 +425,54 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
                             for r in range(4):
                                 gi = np.where(il + r < I, off + il + r, off)
                                 bnd.touch("gamma", gi * esz, esz, il + r < I)
+                        e = (m0 + m) * F + off + il
                         if vec4:
                             if norm:
-                                bnd.touch("x", ((m0 + m) * F + off + il) * esz, 4 * esz, ok)
-                            bnd.touch("dx", ((m0 + m) * F + off + il) * esz, 4 * esz, ok)
+                                bnd.touch("x", e * esz, 4 * esz, ok)
+                                bnd.touch("workspace", dgp + pdb + e * 4, 16, ok)
+                            else:
+                                bnd.touch("dx", e * esz, 4 * esz, ok)
                         else:
                             for r in range(4):
                                 okr = ok & (il + r < I)
                                 if norm:
-                                    bnd.touch("x", ((m0 + m) * F + off + il + r) * esz, esz, okr)
-                                bnd.touch("dx", ((m0 + m) * F + off + il + r) * esz, esz, okr)
+                                    bnd.touch("x", (e + r) * esz, esz, okr)
+                                    bnd.touch("workspace", dgp + pdb + (e + r) * 4, 4, okr)
+                                else:
+                                    bnd.touch("dx", (e + r) * esz, esz, okr)
                     if norm:
                         for r in range(4):
                             bnd.touch("workspace", (mtile * F + off + il + r) * 4, 4,
                                       ((lane & 15) == 0) & (il + r < I))
+        # -- finish: one block per (64 rows, band)
+        if norm:
+            for band in range(nb):
+                off, I = int(offs[band]), int(widths[band])
+                nch = cdiv(I, 64)
+                nq = cdiv(I, 4)
+                for mtile in sorted({0, m_tiles - 1}):
+                    m0 = mtile * 64
+                    rv = min(M - m0, 64)
+                    r64 = np.arange(256)
+                    okr = r64 < rv
+                    for c in range(nch):
+                        bnd.touch("workspace", dgp + ((m0 + r64) * pitch + off // 64 + band + c) * 4, 4, okr)
+                    bnd.touch("inv_norm", ((m0 + r64) * nb + band) * 4, 4, okr)
+                    bnd.touch("lds_finish", np.minimum(r64, 63) * 4, 4, okr)
+                    q = np.arange(rv * nq)
+                    r, k = q // nq, (q % nq) * 4
+                    e = (m0 + r) * F + off + k
+                    bnd.touch("lds_finish", 64 * 4 + r * 4, 4)
+                    if vec4:
+                        bnd.touch("workspace", dgp + pdb + e * 4, 16)
+                        bnd.touch("x", e * esz, 4 * esz)
+                        bnd.touch("dx", e * esz, 4 * esz)
+                    else:
+                        for j in range(4):
+                            okj = k + j < I
+                            bnd.touch("workspace", dgp + pdb + (e + j) * 4, 4, okj)
+                            bnd.touch("x", (e + j) * esz, esz, okj)
+                            bnd.touch("dx", (e + j) * esz, esz, okj)
     # -- dW
     dma = (not grouped) and esz == 2 and M >= 64 and vec4 and O % 8 == 0
     if dma:
@@ -617,7 +629,7 @@ def replay_mask_final_forward(widths, M, H, esz):
     vec4 = all(w % 4 == 0 for w in widths) and H % 4 == 0
     mtiles = cdiv(M, 128)
     if not (esz == 2 and vec4 and H % 8 == 0 and H > CHUNK_K):
-        bnd.fail("mask forward: register path not modelled")
+        _replay_me_fwd_reg(bnd, widths, offs, M, H, esz, vec4)
         return bnd
     units = lambda b: cdiv(widths[b], 64)  # noqa: E731
     sc = build_band_sched(nb, mtiles, units)
@@ -700,9 +712,11 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
              "lds_flat": (4096 + 1) * 4}
     bnd = Bounds(sizes)
     vec4 = all(w % 4 == 0 for w in widths) and H % 4 == 0
-    if not (esz == 2 and vec4 and H % 128 == 0 and M >= CHUNK_K):
-        bnd.fail("mask backward: register paths not modelled")
+    if not vec4:
+        bnd.fail("mask backward: unaligned widths not modelled")
         return bnd
+    dma_dx = esz == 2 and H % 128 == 0
+    dma_dw = esz == 2 and M >= CHUNK_K and H % 128 == 0
     # -- dpre over whole rows
     nq = F // 4
     flat_threads = cdiv(M, 8) * nq
@@ -726,6 +740,13 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
             bnd.touch("workspace", ((m0 + r) * 2 * F + 2 * off + l) * esz, 4 * esz, okw)
             bnd.touch("workspace", ((m0 + r) * 2 * F + 2 * off + l + I) * esz, 4 * esz, okw)
     bnd.touch("lds_flat", np.arange(nb + 1) * 4, 4)
+    if not dma_dx:
+        _replay_me_dx_reg(bnd, widths, offs, M, H, esz, tanh_in)
+    if not dma_dw:
+        _replay_me_dw_reg(bnd, widths, offs, M, H, esz)
+    if not (dma_dx or dma_dw):
+        bnd.touch("offsets", np.arange(nb + 1) * 8, 8)
+        return bnd
     # -- dx on the DMA ring
     HC = 256 if H % 256 == 0 else 128
     S = 3 if HC == 256 else 4
@@ -743,7 +764,7 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
     tid = np.arange(NW * 64)
     lane, wave = tid & 63, tid >> 6
     wr, wc = wave >> 1, wave & 1
-    for band, mt, hc in sorted({(b, m, s) for b, m, s in decoded if m in (0, mt_dx - 1)}):
+    for band, mt, hc in sorted({(b, m, s) for b, m, s in decoded if m in (0, mt_dx - 1) and dma_dx}):
         off, I = int(offs[band]), int(widths[band])
         K = 2 * I
         m0 = mt * 128
@@ -809,7 +830,7 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
     nk = cdiv(M, CHUNK_K)
     kbeg = M - nk * CHUNK_K
     xstride = nb * H
-    for band, _mt, sub in sorted(set(decoded2)):
+    for band, _mt, sub in sorted(set(decoded2) if dma_dw else ()):
         off, I = int(offs[band]), int(widths[band])
         K2 = 2 * I
         h0 = (sub % htl) * HT
@@ -854,6 +875,113 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
             bnd.touch("dw", ((2 * off + j0 + jj) * H + h0 + c8) * esz, 16, ok)
     bnd.touch("offsets", np.arange(nb + 1) * 8, 8)
     return bnd
+
+
+def _replay_me_fwd_reg(bnd, widths, offs, M, H, esz, vec4):
+    """mask_estimator.hip me_fwd_kernel: (band, 64 GLU outputs) groups x 128-row tiles; A = 64 left and
+    64 gate rows of W_b (LeftGateLoader row map), B = x rows; epilogue stores pre and out."""
+    nb, F = len(widths), int(sum(widths))
+    max_l = cdiv(max(widths), 64)
+    mtiles = cdiv(M, 128)
+    grp, mt, valid = xcd_decode(nb * max_l, mtiles)
+    bnd.sizes["lds"] = gemm_lds_bytes(esz, 128, 128)
+    tid = np.arange(GEMM_THREADS)
+    lane, wave = tid & 63, tid >> 6
+    nk = cdiv(H, CHUNK_K)
+    kbeg = H - nk * CHUNK_K
+    combos = sorted({(int(g), int(m)) for g, m, v in zip(grp, mt, valid) if v and int(m) in (0, mtiles - 1)})
+    for g_, mtile in combos:
+        band, l0 = g_ // max_l, (g_ % max_l) * 64
+        off, I = int(offs[band]), int(widths[band])
+        if l0 >= I:
+            continue
+        m0 = mtile * 128
+        rv = min(M - m0, 128)
+        r = krow_rows(tid, 128)
+        l = l0 + (r & 63)
+        lc = np.minimum(l, I - 1)
+        src = np.where(r < 64, lc, I + lc)
+        krow_loader(bnd, "weight", esz, 2 * off * H, H, 128, H, 128, vec4, kbeg, nk, tid, row_map=(src, l < I))
+        krow_loader(bnd, "x", esz, (m0 * nb + band) * H, nb * H, rv, H, 128, vec4, kbeg, nk, tid)
+        for i in range(4):
+            ll = l0 + i * 16 + 4 * (lane >> 4)
+            okl = ll < I
+            for rr in range(4):
+                bnd.touch("bias", (2 * off + ll + rr) * esz, esz, okl & (ll + rr < I))
+                bnd.touch("bias", (2 * off + I + ll + rr) * esz, esz, okl & (ll + rr < I))
+            for j in range(2):
+                m = wave * 32 + j * 16 + (lane & 15)
+                ok = okl & (m < rv)
+                w = 4 if vec4 else 1
+                for rr in range(4 // w):
+                    okr = ok & (ll + rr < I)
+                    bnd.touch("pre", ((m0 + m) * 2 * F + 2 * off + ll + rr) * esz, w * esz, okr)
+                    bnd.touch("pre", ((m0 + m) * 2 * F + 2 * off + I + ll + rr) * esz, w * esz, okr)
+                    bnd.touch("out", ((m0 + m) * F + off + ll + rr) * esz, w * esz, okr)
+    bnd.touch("offsets", np.arange(nb + 1) * 8, 8)
+
+
+def _replay_me_dx_reg(bnd, widths, offs, M, H, esz, tanh_in):
+    """mask_estimator.hip me_bwd_dx_kernel: (band, 128 hidden) groups x 64-row tiles, K = 2 I_b."""
+    nb, F = len(widths), int(sum(widths))
+    hch = cdiv(H, 128)
+    mtiles = cdiv(M, 64)
+    grp, mt, valid = xcd_decode(nb * hch, mtiles)
+    bnd.sizes["lds"] = max(bnd.sizes["lds"], gemm_lds_bytes(esz, 128, 64))
+    tid = np.arange(GEMM_THREADS)
+    lane, wave = tid & 63, tid >> 6
+    v4 = True
+    combos = sorted({(int(g), int(m)) for g, m, v in zip(grp, mt, valid) if v and int(m) in (0, mtiles - 1)})
+    for g_, mtile in combos:
+        band, h0 = g_ // hch, (g_ % hch) * 128
+        off, I = int(offs[band]), int(widths[band])
+        K = 2 * I
+        nk = cdiv(K, CHUNK_K)
+        kbeg = K - nk * CHUNK_K
+        m0 = mtile * 64
+        rv = min(M - m0, 64)
+        mn_loader(bnd, "weight", esz, 2 * off * H + h0, H, H - h0, K, 128, v4, kbeg, nk, tid)
+        krow_loader(bnd, "workspace", esz, m0 * 2 * F + 2 * off, 2 * F, rv, K, 64, v4, kbeg, nk, tid)
+        hr, mc = (wave >> 1) * 64, (wave & 1) * 32
+        for i in range(4):
+            h = h0 + hr + i * 16 + 4 * (lane >> 4)
+            for j in range(2):
+                m = mc + j * 16 + (lane & 15)
+                ok = (h < H) & (m < rv)
+                idx = ((m0 + m) * nb + band) * H + h
+                if tanh_in:
+                    bnd.touch("x", idx * esz, 4 * esz, ok)
+                bnd.touch("dx", idx * esz, 4 * esz, ok)
+
+
+def _replay_me_dw_reg(bnd, widths, offs, M, H, esz):
+    """mask_estimator.hip me_bwd_dw_kernel: (band, 128 hidden) groups x 64-wide j chunks, K = M; the
+    blocks of hidden tile 0 also sum dpre over the rows (dbias)."""
+    nb, F = len(widths), int(sum(widths))
+    ht = cdiv(H, 128)
+    maxj = cdiv(2 * max(widths), 64)
+    grp, jc, valid = xcd_decode(nb * ht, maxj)
+    tid = np.arange(GEMM_THREADS)
+    lane, wave = tid & 63, tid >> 6
+    nk = cdiv(M, CHUNK_K)
+    kbeg = M - nk * CHUNK_K
+    for g_, j_ in sorted({(int(g), int(j)) for g, j, v in zip(grp, jc, valid) if v}):
+        band, h0 = g_ // ht, (g_ % ht) * 128
+        j0 = j_ * 64
+        off, I = int(offs[band]), int(widths[band])
+        K2 = 2 * I
+        if j0 >= K2 or M == 0:
+            continue
+        mn_loader(bnd, "x", esz, band * H + h0, nb * H, H - h0, M, 128, True, kbeg, nk, tid)
+        mn_loader(bnd, "workspace", esz, 2 * off + j0, 2 * F, K2 - j0, M, 64, True, kbeg, nk, tid)
+        if h0 == 0:
+            bnd.touch("dbias", (2 * off + j0 + tid) * esz, esz, (tid < 64) & (tid < K2 - j0))
+        hr, jcol = (wave >> 1) * 64, (wave & 1) * 32
+        for i in range(4):
+            h = h0 + hr + i * 16 + 4 * (lane >> 4)
+            for j in range(2):
+                jj = j0 + jcol + j * 16 + (lane & 15)
+                bnd.touch("dw", (2 * off * H + jj * H + h) * esz, 4 * esz, (h < H) & (jj < K2))
 
 
 # ----------------------------------------------------------------------------- row kernels
@@ -1085,9 +1213,8 @@ def all_replays(name: str, esz: int):
     yield "band_split_bwd", replay_band_split_backward(widths, M, dim, esz)
     yield "grouped_linear_fwd", replay_band_split_forward([dim] * nb, M, hidden, esz, norm=False, act_tanh=True)
     yield "grouped_linear_bwd", replay_band_split_backward([dim] * nb, M, hidden, esz, grouped=True)
-    if esz == 2:
-        yield "mask_final_fwd", replay_mask_final_forward(widths, M, hidden, esz)
-        yield "mask_final_bwd", replay_mask_final_backward(widths, M, hidden, esz, tanh_in=True)
+    yield "mask_final_fwd", replay_mask_final_forward(widths, M, hidden, esz)
+    yield "mask_final_bwd", replay_mask_final_backward(widths, M, hidden, esz, tanh_in=True)
     yield "rms_norm", replay_rms_norm(M * nb, dim, esz)
     for shape in qk:
         yield f"attention_gate{list(shape)}", replay_attention_gate(shape[0], shape[1], shape[2], shape[3], dim, esz)

@@ -34,15 +34,17 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.pmsst_abi_version() >= 1
+    assert lib.pmsst_abi_version() == 5
     assert isinstance(_lib.last_error(), str)
 
 
 def test_workspace_queries(lib):
     assert lib.pmsst_rms_norm_backward_workspace_size(1000, 192) == 1024 * 192 * 4
+    # [dgamma partials of 17 row tiles | dot partials, pitch F / 64 + NB + 1 | fp32 gs * gamma]
     dg = -(-17 * 4100 * 4 // 256) * 256
-    dots = -(-1032 * 62 * 4 // 256) * 256
-    assert lib.pmsst_band_split_ragged_backward_workspace_size(1032, 4100, 62, 192) == dg + dots
+    dots = -(-1032 * (4100 // 64 + 62 + 1) * 4 // 256) * 256
+    t = -(-1032 * 4100 * 4 // 256) * 256
+    assert lib.pmsst_band_split_ragged_backward_workspace_size(1032, 4100, 62, 192) == dg + dots + t
     assert lib.pmsst_band_split_ragged_backward_workspace_size(0, 4100, 62, 192) == 0
     assert lib.pmsst_mask_estimator_final_backward_workspace_size(1032, 4100, 2) == -(-1032 * 8200 * 2 // 256) * 256
     assert lib.pmsst_mask_estimator_final_backward_workspace_size(0, 4100, 2) == 0

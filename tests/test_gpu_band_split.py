@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import oracle
-from tests.conftest import assert_parity, dt_name, to_np
+from tests.conftest import assert_parity, by_band, by_index, dt_name, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -45,8 +45,8 @@ def _check_ragged(ext, dim_inputs, m, o, dtype, seed, x_scale=1.0):
     npw = [to_np(v) for v in weights]
     npb = [to_np(v) for v in biases]
     r_out, r_normed, r_inv = oracle.band_split_ragged_forward(npx, npg, npw, npb, dim_inputs, dn)
-    assert_parity(out, r_out, dn, "out")
-    assert_parity(normed, r_normed, dn, "normed")
+    assert_parity(out, r_out, dn, "out", by_index(1))
+    assert_parity(normed, r_normed, dn, "normed", by_band(1, dim_inputs))
     assert_parity(inv, r_inv, "f32", "inv_norm")
     dy = torch.randn(out.shape, generator=g).to(dtype).cuda()
     res = ext.band_split_ragged_backward(dy, normed, inv, gammas, weights, list(dim_inputs), offs)
@@ -54,13 +54,13 @@ def _check_ragged(ext, dim_inputs, m, o, dtype, seed, x_scale=1.0):
     r_dx, r_dg, r_dw, r_db = oracle.band_split_ragged_backward(
         to_np(dy), to_np(normed), to_np(inv), npg, npw, dim_inputs, dn
     )
-    assert_parity(res[0], r_dx, dn, "dx")
-    assert_parity(torch.cat(res[1 : 1 + nb]), np.concatenate(r_dg), dn, "dgamma")
+    assert_parity(res[0], r_dx, dn, "dx", by_band(1, dim_inputs))
+    assert_parity(torch.cat(res[1 : 1 + nb]), np.concatenate(r_dg), dn, "dgamma", by_band(0, dim_inputs))
     for b in range(nb):
         assert res[1 + nb + b].shape == (o, dim_inputs[b])
     assert_parity(torch.cat([w.reshape(-1) for w in res[1 + nb : 1 + 2 * nb]]),
-                  np.concatenate([w.reshape(-1) for w in r_dw]), dn, "dW")
-    assert_parity(torch.stack(res[1 + 2 * nb :]), np.stack(r_db), dn, "dbias")
+                  np.concatenate([w.reshape(-1) for w in r_dw]), dn, "dW", by_band(0, [o * d for d in dim_inputs]))
+    assert_parity(torch.stack(res[1 + 2 * nb :]), np.stack(r_db), dn, "dbias", by_index(0))
     return x, gammas, weights, biases, out, inv, dy
 
 
@@ -117,24 +117,24 @@ def test_saved_input_backward(hip_ext, dtype, dims, m, o):
     assert normed is None
     r_out, _, _ = oracle.band_split_ragged_forward(to_np(x), [to_np(v) for v in gammas],
                                                    [to_np(v) for v in weights], [to_np(v) for v in biases], dims, dn)
-    assert_parity(out, r_out, dn, "out")
+    assert_parity(out, r_out, dn, "out", by_index(1))
     dy = torch.randn(out.shape, generator=g).to(dtype).cuda()
     dx, dg, dw, db = hip_ext.band_split_ragged_backward_packed(dy, x, True, inv, ga, wa, dims, True)
     r_dx, r_dg, r_dw, r_db = oracle.band_split_ragged_backward_lean(
         to_np(dy), to_np(x), to_np(inv), [to_np(v) for v in gammas], [to_np(v) for v in weights], dims, dn
     )
-    assert_parity(dx, r_dx, dn, "dx")
-    assert_parity(dg, np.concatenate(r_dg), dn, "dgamma")
-    assert_parity(dw, np.concatenate([w.reshape(-1) for w in r_dw]), dn, "dW")
-    assert_parity(db, np.concatenate(r_db), dn, "dbias")
+    assert_parity(dx, r_dx, dn, "dx", by_band(1, dims))
+    assert_parity(dg, np.concatenate(r_dg), dn, "dgamma", by_band(0, dims))
+    assert_parity(dw, np.concatenate([w.reshape(-1) for w in r_dw]), dn, "dW", by_band(0, [o * d for d in dims]))
+    assert_parity(db, np.concatenate(r_db), dn, "dbias", by_band(0, [o] * len(dims)))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("dims,m,o,has_bias", [((3, 5, 2, 7), 5, 4, True), (BSR_WIDTHS, 1032, 192, True),
                                                (BSR_WIDTHS, 130, 64, False), ((12, 520, 36), 77, 100, True)])
-def test_backward_from_output(hip_ext, dtype, dims, m, o, has_bias):
-    """Backward with the per-row dots taken from the forward output (sum_o dy * (out - bias)) and one
-    block per 64-wide input chunk, from the saved input and from normed; against the oracle."""
+def test_backward_from_input_and_normed(hip_ext, dtype, dims, m, o, has_bias):
+    """Backward from the saved input and from normed (one block per 64-wide input chunk, the row dots
+    added up in the finish pass); against the oracle."""
     dn = dt_name(dtype)
     g = torch.Generator().manual_seed(31)
     x = (0.05 * torch.randn(m, sum(dims), generator=g)).to(dtype).cuda()
@@ -148,14 +148,14 @@ def test_backward_from_output(hip_ext, dtype, dims, m, o, has_bias):
         to_np(dy), to_np(x), to_np(inv), [to_np(v) for v in gammas], [to_np(v) for v in weights], dims, dn
     )
     for saved, is_input in ((x, True), (normed, False)):
-        dx, dg, dw, db = hip_ext.band_split_ragged_backward_packed(dy, saved, is_input, inv, ga, wa, dims, has_bias,
-                                                                   out=out.reshape(m, -1), bias_all=ba)
+        dx, dg, dw, db = hip_ext.band_split_ragged_backward_packed(dy, saved, is_input, inv, ga, wa, dims, has_bias)
         tag = "x" if is_input else "normed"
-        assert_parity(dx, r_dx, dn, f"dx from {tag}")
-        assert_parity(dg, np.concatenate(r_dg), dn, f"dgamma from {tag}")
-        assert_parity(dw, np.concatenate([w.reshape(-1) for w in r_dw]), dn, f"dW from {tag}")
+        assert_parity(dx, r_dx, dn, f"dx from {tag}", by_band(1, dims))
+        assert_parity(dg, np.concatenate(r_dg), dn, f"dgamma from {tag}", by_band(0, dims))
+        assert_parity(dw, np.concatenate([w.reshape(-1) for w in r_dw]), dn, f"dW from {tag}",
+                      by_band(0, [o * d for d in dims]))
         if has_bias:
-            assert_parity(db, np.concatenate(r_db), dn, f"dbias from {tag}")
+            assert_parity(db, np.concatenate(r_db), dn, f"dbias from {tag}", by_band(0, [o] * len(dims)))
 
 
 @pytest.mark.parametrize("has_bias", [True, False])

@@ -443,3 +443,39 @@ def test_mask_apply_vs_torch_complex_autograd(zero_dc):
         assert abs(got[(bi * s + si) * c + ci, fi, ti] - want) < 1e-12
     if zero_dc:
         assert np.all(got[:, 0, :] == 0) and np.all(gm.reshape(b, s, t, f, c, 2)[:, :, :, 0] == 0)
+
+
+def test_grouped_mode_rounding_points_follow_torch_casts():
+    """``grad_pre_dt`` stores dpre in bf16 before the dx / dW products while dbias sums the unrounded
+    values (.cu:2343-2346), and the MLP hidden layer is bf16 after the linear and after tanh
+    (fr.py:338-340): checked against torch's own bf16 casts at those points; leaving the rounding out
+    of dx must show."""
+    r = _rng(15)
+    dim_inputs = (4, 8, 12)
+    m, nb, hid = 9, 3, 32
+    x = oracle.round_to(r.standard_normal((m, nb, hid)), "bf16")
+    w = [oracle.round_to(r.standard_normal((2 * d, hid)) / math.sqrt(hid), "bf16") for d in dim_inputs]
+    bias = oracle.round_to(0.1 * r.standard_normal(2 * sum(dim_inputs)), "bf16")
+    _, pre = oracle.mask_estimator_final_forward(x, w, bias, dim_inputs, "bf16")
+    g = oracle.round_to(r.standard_normal((m, sum(dim_inputs))), "bf16")
+    dx, dbias, dws = oracle.mask_estimator_final_backward(g, x, pre, w, dim_inputs, "f64", grad_pre_dt="bf16")
+    off = 0
+    for b, d in enumerate(dim_inputs):
+        p = torch.from_numpy(pre[:, 2 * off : 2 * off + 2 * d])
+        left, gate = p[:, :d], p[:, d:]
+        s = torch.sigmoid(gate)
+        gb = torch.from_numpy(g[:, off : off + d])
+        dpre = torch.cat([gb * s, gb * left * s * (1 - s)], dim=1)
+        _close(dbias[2 * off : 2 * off + 2 * d], dpre.sum(0), what=f"dbias{b}")
+        dpre16 = dpre.to(torch.bfloat16).double()
+        _close(dx[:, b], dpre16 @ torch.from_numpy(w[b]), what=f"dx{b}")
+        _close(dws[b], dpre16.t() @ torch.from_numpy(x[:, b]), what=f"dW{b}")
+        off += d
+    dx_exact, _, _ = oracle.mask_estimator_final_backward(g, x, pre, w, dim_inputs, "f64")
+    assert np.max(np.abs(dx_exact - dx)) > 1e-4
+    w1 = oracle.round_to(r.standard_normal((nb, 16, hid)) / 4, "bf16")
+    b1 = oracle.round_to(r.standard_normal((nb, 16)), "bf16")
+    h = oracle.mask_mlp_hidden(x, w1, b1, "bf16")
+    z = torch.einsum("mgi,goi->mgo", torch.from_numpy(x), torch.from_numpy(w1)) + torch.from_numpy(b1)
+    ref = torch.tanh(z.to(torch.bfloat16).double()).to(torch.bfloat16).double()
+    assert np.array_equal(h, ref.numpy())
