@@ -87,6 +87,14 @@ int pmsst_rms_norm_backward_from_input(const void* grad_out, const void* x, cons
                                        const void* gamma, void* grad_x, void* grad_gamma, int64_t rows,
                                        int64_t dim, int dtype, int gamma_dtype, void* workspace,
                                        size_t workspace_bytes, void* stream);
+/* No reference counterpart: pmsst_rms_norm_backward_from_input that allocates nothing and takes no
+ * workspace, for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Its dgamma partials live in a static 4 MiB device
+ * array per GPU, so dim <= 1024 (larger dims return PMSST_EINVAL); calls that overlap on one GPU
+ * (concurrent streams or threads) race on that array. */
+int pmsst_rms_norm_backward_from_input_noalloc(const void* grad_out, const void* x, const float* inv_norm,
+                                               const void* gamma, void* grad_x, void* grad_gamma, int64_t rows,
+                                               int64_t dim, int dtype, int gamma_dtype, void* stream);
 
 /* ------------------------------------------------------------------ rotary
  * t[batch, seq, heads, dim] (bnhd shape); cos/sin[seq, dim/2] addressed as

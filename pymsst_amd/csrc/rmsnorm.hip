@@ -11,6 +11,8 @@
 // rows it visits, the block folds them into one row of a [parts, dim] fp32
 // workspace, and col_sum_kernel adds the parts in a fixed order.  No atomics,
 // so results are bit-reproducible for a given (rows, dim).
+#include <mutex>
+
 #include "common.h"
 #include "rowgeom.h"
 
@@ -329,6 +331,41 @@ int with_dtype(int dtype, const char* op, F&& f) {
   }
 }
 
+// ------------------------------------------------------------------ allocation-free backward
+//
+// The dgamma partials of the saved-input backward live in a file-scope device array instead of a
+// caller workspace, for callers that cannot allocate.  It holds kRowBwdMaxParts partial rows of up
+// to kNoAllocMaxDim columns (4 MiB per GPU, for the life of the process).  Every call on one GPU
+// uses that GPU's array: calls that overlap on one GPU (other streams, other host threads) race.
+// Nothing needs clearing: each call writes every partial row it reads.
+constexpr int kNoAllocMaxDim = 1024;
+constexpr size_t kScratchBytes = static_cast<size_t>(kRowBwdMaxParts) * kNoAllocMaxDim * sizeof(float);
+
+__device__ __align__(256) char scratch[kScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per device.  The array's
+// host-side name is only a handle: kernels must be given this address.
+int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    return fail(PMSST_ELAUNCH, "rms_norm_backward_from_input_noalloc: no current device");
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr) {
+      return fail(PMSST_ELAUNCH, "rms_norm_backward_from_input_noalloc: hipGetSymbolAddress failed: %s",
+                  hipGetErrorString(err));
+    }
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return PMSST_OK;
+}
+
 }  // namespace
 }  // namespace pmsst
 
@@ -414,6 +451,21 @@ int pmsst_rms_norm_backward_from_input(const void* grad_out, const void* x, cons
     return launch_bwd<T, T, T, T, true>(grad_out, x, inv_norm, gamma, grad_x, grad_gamma, dtype, rows, dim,
                                         workspace, workspace_bytes, static_cast<hipStream_t>(stream));
   });
+}
+
+int pmsst_rms_norm_backward_from_input_noalloc(const void* grad_out, const void* x, const float* inv_norm,
+                                               const void* gamma, void* grad_x, void* grad_gamma, int64_t rows,
+                                               int64_t dim, int dtype, int gamma_dtype, void* stream) {
+  if (dim <= 0 || dim > kNoAllocMaxDim) {
+    return fail(PMSST_EINVAL, "rms_norm_backward_from_input_noalloc: dim=%lld outside [1, %d] (the static scratch "
+                "holds %d partial rows of %d columns)", (long long)dim, kNoAllocMaxDim, kRowBwdMaxParts,
+                kNoAllocMaxDim);
+  }
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != PMSST_OK) return rc;
+  return pmsst_rms_norm_backward_from_input(grad_out, x, inv_norm, gamma, grad_x, grad_gamma, rows, dim, dtype,
+                                            gamma_dtype, ws, kScratchBytes, stream);
 }
 
 }  // extern "C"
