@@ -1,33 +1,40 @@
 #!/usr/bin/env python3
-"""Benchmark of the fused RoFormer layer kernels on one MI355X.
+"""Benchmark of the fused RoFormer layer kernels on one MI355X (plus the
+train-step configs).
 
-One "step" is one forward + backward pass of every fused layer of the kernel
-microbench, bf16, with all inputs resident in HBM:
+One microbench "step" is one forward + backward pass of every fused layer of configs[1], with all
+inputs resident in HBM:
 
-* band split: ``x[4, 258, 4100]`` (62 BS-RoFormer bands) -> ``[4, 258, 62, 192]``,
-  saved-input backward;
+* band split: ``x[4, 258, 4100]`` (62 BS-RoFormer bands) -> ``[4, 258, 62, 192]``;
 * q/k RMSNorm over the head dim + rotary (theta 10000): two ``[248, 258, 8, 64]`` tensors;
-* mask estimator final layer: per band hidden 768 -> 2 * I_b, bias, GLU.
+* mask estimator: per band dim 192 -> hidden 768 + tanh -> 2 * I_b + GLU (both projections).
 
-``value`` is the algorithmic HBM bytes of all kernels in a step divided by the
-step time (GB/s).  Per-op average durations come from HIP events recorded on
-the launch stream inside the timed region; ``roofline`` reports the op with
-the largest share of the step.  ``cpu_baseline`` times the numpy oracle
-(``oracle/``) on a bounded sample of the same workload on the host.
+``value`` is the algorithmic HBM bytes of the step divided by the bf16 step time (GB/s); the same
+step in fp32 is reported as ``fp32_step``.  Per-op durations come from HIP events recorded on the
+launch stream inside the timed region, with the achieved TFLOP/s and MFMA utilisation of each
+grouped projection.  ``roofline`` reports the op with the largest share of the step that is a single
+kernel; its ``traffic`` is measured in the same run by two child ``rocprofv3 --pmc`` passes
+(FETCH_SIZE, WRITE_SIZE) over that op and a plain copy of known size that calibrates the counters.
 
-``train`` reports the second half of the metric: BS-RoFormer train
-samples/s with the stock modules and with the HIP kernels patched in.
+``train`` reports samples/s of full training steps with the stock modules and with the HIP kernels
+patched in, for configs[2] (the headline) and configs[0], [3] and [4] (fewer steps).
+``cpu_baseline`` times the restated stock PyTorch modules in fp32 on the host cores: the configs[1]
+step at full shapes, and the configs[0] training step.
 
-Usage: ``python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline]
-[--train-steps 20] [--train-warmup 3]``.
+Usage: ``python bench.py [--gpus 1] [--steps 30] [--warmup 10] [--no-cpu-baseline] [--no-traffic]
+[--train-steps 20] [--train-warmup 3] [--train-configs 0,2,3,4]``.
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -37,47 +44,41 @@ if str(REPO) not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
 METRIC = "fused-layer fwd+bwd HBM GB/s (% peak) + BSR train samples/s, 1 MI355X"
-# ops of the step that are a single kernel, launched n times per op call
+BSR_WIDTHS = tuple([8] * 24 + [16] * 12 + [48] * 8 + [96] * 8 + [192] * 8 + [512, 516])
+# ops of the step that are one kernel launched n times per op call: the roofline candidates
 SINGLE_KERNEL_OPS = {
     "band_split_fwd": ("bs_fwd_kernel", 1),
     "qk_norm_rotary_fwd": ("norm_rot_fwd_kernel", 2),
+    "mask_hidden_fwd": ("bs_fwd_kernel", 1),
     "mask_final_fwd": ("me_fwd_dma_kernel", 1),
 }
-# measured HBM bytes per launch, by kernel: rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (KiB per
-# dispatch x 1024).  The factors are what the same counters read for a 1 GiB bf16 copy (torch.mul) in
-# the same runs: FETCH_SIZE 524310 KiB for 1048576 KiB read, WRITE_SIZE 1048576 KiB for 1048576 written.
-TRAFFIC_PER_LAUNCH: dict = {
-    "me_fwd_dma_kernel": (57624 * 2 + 26676) * 1024,
-    "norm_rot_fwd_kernel": (32278 * 2 + 65984) * 1024,
-    "bs_fwd_kernel": (14253 * 2 + 26452) * 1024,
-}
-BSR_WIDTHS = tuple([8] * 24 + [16] * 12 + [48] * 8 + [96] * 8 + [192] * 8 + [512, 516])
+# bytes a 16-bit copy of this many elements reads (and writes): the counter calibration
+CALIB_ELEMS = 1 << 27
 
 
 def _args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
-    ap.add_argument("--train-steps", type=int, default=20, help="timed BS-RoFormer train steps per backend (0: skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the configs[1] CPU sample")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic passes")
+    ap.add_argument("--traffic-probe", default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--train-steps", type=int, default=20, help="timed configs[2] train steps per backend (0: skip)")
     ap.add_argument("--train-warmup", type=int, default=3)
+    ap.add_argument("--train-configs", default="0,2,3,4", help="train configs to time (BASELINE.json indices)")
     ap.add_argument("--train-impl", choices=("both", "fused", "stock"), default="both",
                     help="which train-step legs to run (profiling one implementation at a time)")
-    ap.add_argument("--train-workload", default="bsr_train",
-                    help="training configuration of the train leg (pymsst_amd.workloads.WORKLOADS key; "
-                         "bsr_train = configs[2])")
     return ap.parse_args(argv)
 
 
 class Workload:
-    """Seeded synthetic inputs of configs[1] (fixed seeds, so every run times the same data)."""
+    """Seeded synthetic inputs of configs[1] in one dtype (fixed seeds: every run times the same data)."""
 
     def __init__(self, torch, ext, dtype):
-        import numpy as np
-
         self.torch, self.ext, self.dtype = torch, ext, dtype
         dev = torch.device("cuda:0")
         self.dims = BSR_WIDTHS
@@ -92,7 +93,7 @@ class Workload:
         self.qk_shape = (self.B * self.NB, self.T, 8, 64)
         self.q = torch.randn(self.qk_shape, generator=g(1)).to(dev, dtype)
         self.k = torch.randn(self.qk_shape, generator=g(2)).to(dev, dtype)
-        self.h = torch.randn(self.M, self.NB, self.hidden, generator=g(3)).to(dev, dtype)
+        self.h = torch.randn(self.M, self.NB, self.dim, generator=g(3)).to(dev, dtype)
         pg = g(4)
         self.gamma_bs = (1 + 0.1 * torch.randn(self.F, generator=pg)).to(dev, dtype)
         self.w_bs = torch.cat([(torch.randn(self.dim, d, generator=pg) / d**0.5).reshape(-1) for d in self.dims])
@@ -100,10 +101,12 @@ class Workload:
         self.b_bs = (0.1 * torch.randn(self.NB * self.dim, generator=pg)).to(dev, dtype)
         self.gamma_q = (1 + 0.1 * torch.randn(64, generator=pg)).to(dev)
         self.gamma_k = (1 + 0.1 * torch.randn(64, generator=pg)).to(dev)
-        self.w_me = torch.cat(
+        self.w1 = (torch.randn(self.NB, self.hidden, self.dim, generator=pg) / self.dim**0.5).to(dev, dtype)
+        self.b1 = (0.1 * torch.randn(self.NB, self.hidden, generator=pg)).to(dev, dtype)
+        self.w2 = torch.cat(
             [(torch.randn(2 * d, self.hidden, generator=pg) / self.hidden**0.5).reshape(-1) for d in self.dims]
         ).to(dev, dtype)
-        self.b_me = (0.1 * torch.randn(2 * self.F, generator=pg)).to(dev, dtype)
+        self.b2 = (0.1 * torch.randn(2 * self.F, generator=pg)).to(dev, dtype)
         from pymsst_amd.core.transformer import RotaryEmbedding
 
         cos, sin = RotaryEmbedding(64, 10000.0).tables(self.T, dev, dtype)
@@ -113,38 +116,46 @@ class Workload:
         self.g_q = torch.randn(self.qk_shape, generator=gg).to(dev, dtype)
         self.g_k = torch.randn(self.qk_shape, generator=gg).to(dev, dtype)
         self.g_me = torch.randn(self.M, self.F, generator=gg).to(dev, dtype)
-        del np
 
     # --------------------------------------------------------------- ops (name, callable)
     def ops(self):
         e, w = self.ext, self
-        state = {}
+        st = {}
 
         def bs_fwd():
-            state["bs"] = e.band_split_ragged_forward_packed(w.x, w.gamma_bs, w.w_bs, w.b_bs, w.dims, write_normed=False)
+            st["bs"] = e.band_split_ragged_forward_packed(w.x, w.gamma_bs, w.w_bs, w.b_bs, w.dims, write_normed=False)
 
         def bs_bwd():
-            e.band_split_ragged_backward_packed(w.g_bs, w.x, True, state["bs"][2], w.gamma_bs, w.w_bs, w.dims, True)
+            e.band_split_ragged_backward_packed(w.g_bs, w.x, True, st["bs"][2], w.gamma_bs, w.w_bs, w.dims, True)
 
         def qk_fwd():
-            state["q"] = e.rms_norm_rotary_forward(w.q, w.gamma_q, w.cos, w.sin)
-            state["k"] = e.rms_norm_rotary_forward(w.k, w.gamma_k, w.cos, w.sin)
+            st["q"] = e.rms_norm_rotary_forward(w.q, w.gamma_q, w.cos, w.sin)
+            st["k"] = e.rms_norm_rotary_forward(w.k, w.gamma_k, w.cos, w.sin)
 
         def qk_bwd():
-            e.rms_norm_rotary_backward(w.g_q, w.q, state["q"][1], w.gamma_q, w.cos, w.sin)
-            e.rms_norm_rotary_backward(w.g_k, w.k, state["k"][1], w.gamma_k, w.cos, w.sin)
+            e.rms_norm_rotary_backward(w.g_q, w.q, st["q"][1], w.gamma_q, w.cos, w.sin)
+            e.rms_norm_rotary_backward(w.g_k, w.k, st["k"][1], w.gamma_k, w.cos, w.sin)
 
-        def me_fwd():
-            state["me"] = e.mask_estimator_final_forward_packed(w.h, w.w_me, w.b_me, w.dims)
+        def hid_fwd():
+            st["hid"] = e.grouped_linear_forward_act(w.h, w.w1, w.b1, activation="tanh")
 
-        def me_bwd():
-            e.mask_estimator_final_backward_packed(w.g_me, w.h, state["me"][1], w.w_me, w.dims)
+        def fin_fwd():
+            st["fin"] = e.mask_estimator_final_forward_packed(st["hid"], w.w2, w.b2, w.dims)
+
+        def fin_bwd():
+            st["dz"] = e.mask_estimator_final_backward_packed(w.g_me, st["hid"], st["fin"][1], w.w2, w.dims,
+                                                              input_activation="tanh")[0]
+
+        def hid_bwd():
+            e.grouped_linear_backward(st["dz"], w.h, w.w1, has_bias=True)
 
         return [("band_split_fwd", bs_fwd), ("band_split_bwd", bs_bwd), ("qk_norm_rotary_fwd", qk_fwd),
-                ("qk_norm_rotary_bwd", qk_bwd), ("mask_final_fwd", me_fwd), ("mask_final_bwd", me_bwd)]
+                ("qk_norm_rotary_bwd", qk_bwd), ("mask_hidden_fwd", hid_fwd), ("mask_final_fwd", fin_fwd),
+                ("mask_final_bwd", fin_bwd), ("mask_hidden_bwd", hid_bwd)]
 
     # --------------------------------------------------------------- algorithmic bytes / flops per op
     def traffic(self):
+        """``{op: (bytes, flops)}``: each op's own inputs read and outputs written, once each."""
         s = 2 if self.dtype != self.torch.float32 else 4
         M, F, NB, O, H = self.M, self.F, self.NB, self.dim, self.hidden
         R = self.qk_shape[0] * self.qk_shape[1] * self.qk_shape[2]
@@ -153,116 +164,262 @@ class Workload:
             # read x, gamma, W, bias; write out, inv
             "band_split_fwd": (M * F * s + F * s + F * O * s + NB * O * s + M * NB * O * s + 4 * M * NB,
                                2 * M * F * O),
-            # algorithmic (the op's own inputs and outputs): read dy, x, inv, gamma, W; write dx, dgamma,
-            # dW, dbias.  The kernels also read the forward output for the per-row dots; that read is
-            # this implementation's choice and is not counted.
+            # read dy, x, inv, gamma, W; write dx, dgamma, dW, dbias
             "band_split_bwd": (M * NB * O * s + 2 * M * F * s + 4 * M * NB + 2 * F * s + 2 * F * O * s + NB * O * s,
                                4 * M * F * O),
             # per tensor: read x, write out, write inv (x2 tensors)
             "qk_norm_rotary_fwd": (2 * (2 * R * D * s + 4 * R), 0),
             # per tensor: read dy, x, inv; write dx (x2)
             "qk_norm_rotary_bwd": (2 * (3 * R * D * s + 4 * R), 0),
-            # read x, W, bias; write pre, out
+            # read x, W1, b1; write h
+            "mask_hidden_fwd": (M * NB * O * s + NB * H * O * s + NB * H * s + M * NB * H * s, 2 * M * NB * O * H),
+            # read h, W2, b2; write pre, out
             "mask_final_fwd": (M * NB * H * s + 2 * F * H * s + 2 * F * s + 2 * M * F * s + M * F * s,
                                2 * M * 2 * F * H),
-            # read g, pre, x, W; write dx, dW, dbias
+            # read g, pre, h, W2; write dz, dW2, db2
             "mask_final_bwd": (M * F * s + 2 * M * F * s + 2 * M * NB * H * s + 4 * F * H * s + 2 * F * s,
                                2 * 2 * M * 2 * F * H),
+            # read dz, x, W1; write dx, dW1, db1
+            "mask_hidden_bwd": (M * NB * H * s + 2 * M * NB * O * s + 2 * NB * H * O * s + NB * H * s,
+                                2 * 2 * M * NB * O * H),
         }
 
 
-def _cpu_baseline(budget_s: float):
-    """Time the numpy oracle (float32 arithmetic) on row slices of the same workload.
+def _time_step(torch, w, steps, warmup):
+    """Whole-step time and per-op averages (HIP events on the launch stream) of one workload."""
+    ops = w.ops()
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        for _, fn in ops:
+            fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t0.record(stream)
+    for _ in range(steps):
+        for _, fn in ops:
+            fn()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = t0.elapsed_time(t1) / steps
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in ops]
+          for _ in range(steps)]
+    for i in range(steps):
+        for j, (_, fn) in enumerate(ops):
+            ev[i][j][0].record(stream)
+            fn()
+            ev[i][j][1].record(stream)
+    torch.cuda.synchronize()
+    traffic = w.traffic()
+    peak_tf = BF16_PEAK_TFLOPS if w.dtype != torch.float32 else FP32_PEAK_TFLOPS
+    per_op = {}
+    for j, (name, _) in enumerate(ops):
+        ms = sum(ev[i][j][0].elapsed_time(ev[i][j][1]) for i in range(steps)) / steps
+        nbytes, flops = traffic[name]
+        tf = flops / (ms * 1e-3) / 1e12 if flops else None
+        per_op[name] = {
+            "ms": round(ms, 5),
+            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "TFLOP/s": round(tf, 2) if tf else None,
+            "mfma_util": round(tf / peak_tf, 4) if tf else None,
+        }
+    total_bytes = sum(b for b, _ in traffic.values())
+    return ms_step, wall, per_op, total_bytes / (ms_step * 1e-3) / 1e9
 
-    Each op runs on ``rows`` rows (a bounded sample of the M=1032 / R=511,872 rows of the
-    GPU step) and its algorithmic bytes are scaled by the same fraction; the result is
-    the oracle's GB/s over one full step's bytes, extrapolated from the sample.
-    """
-    import numpy as np
 
-    import oracle
+# ------------------------------------------------------------------------------ counters
 
-    try:
-        from threadpoolctl import threadpool_info
 
-        cores = max([int(p.get("num_threads", 1)) for p in threadpool_info()] + [1])
-    except Exception:  # pragma: no cover
-        cores = os.cpu_count() or 1
-    rng = np.random.default_rng(0)
-    dims, O, H = BSR_WIDTHS, 192, 768
-    F, NB = sum(dims), len(dims)
-    m = 64  # rows per band-split / mask sample (of 1032)
-    rq = 32 * 64 * 8  # rows per q/k sample (of 511,872), one tensor [32, 64, 8, 64]
-    acc = np.float32
-    x = (rng.laplace(0, 0.05, (m, F))).astype(acc)
-    gam = [np.ones(d, acc) for d in dims]
-    ws = [rng.standard_normal((O, d)).astype(acc) for d in dims]
-    bs = [np.zeros(O, acc) for d in dims]
-    dy = rng.standard_normal((m, NB, O)).astype(acc)
-    q = rng.standard_normal((32, 64, 8, 64)).astype(acc)
-    cos, sin = oracle.rotary_tables(64, 64)
-    gq = np.ones(64, acc)
-    h = rng.standard_normal((m, NB, H)).astype(acc)
-    w2 = [rng.standard_normal((2 * d, H)).astype(acc) for d in dims]
-    b2 = np.zeros(2 * F, acc)
-    g2 = rng.standard_normal((m, F)).astype(acc)
-    s = 4
-    sample_bytes = (
-        (m * F + F + F * O + NB * O + m * NB * O) * s + 4 * m * NB  # band split fwd
-        + (m * NB * O + 2 * m * F + 2 * F + 2 * F * O + NB * O) * s + 4 * m * NB  # band split bwd
-        + (2 * rq * 64 * s + 4 * rq) + (3 * rq * 64 * s + 4 * rq)  # one q/k tensor fwd + bwd
-        + (m * NB * H + 2 * F * H + 2 * F + 3 * m * F) * s  # mask fwd
-        + (3 * m * F + 2 * m * NB * H + 4 * F * H + 2 * F) * s  # mask bwd
-    )
+def _traffic_probe(op: str) -> int:
+    """Child of the traffic passes: runs ``op`` (with the forward ops it depends on) a few times, then the
+    calibration copy; rocprofv3 records the counters of both."""
+    import torch
 
-    def one():
-        o, n, inv = oracle.band_split_ragged_forward(x, gam, ws, bs, dims, "f32", acc)
-        oracle.band_split_ragged_backward_lean(dy, x, inv, gam, ws, dims, "f32", acc)
-        oq, iq = oracle.rms_norm_rotary_forward(q, gq, cos, sin, "f32", acc)
-        oracle.rms_norm_rotary_backward(q, q, iq, gq, cos, sin, "f32", "f32", acc)
-        out, pre = oracle.mask_estimator_final_forward(h, w2, b2, dims, "f32", acc)
-        oracle.mask_estimator_final_backward(g2, h, pre, w2, dims, "f32", acc)
+    from pymsst_amd.fused_extension import load_fused_band_split_extension
 
-    one()
-    reps, t0 = 0, time.perf_counter()
+    w = Workload(torch, load_fused_band_split_extension(), torch.bfloat16)
+    ops = dict(w.ops())
+    deps = {"mask_final_fwd": ["mask_hidden_fwd"]}
+    for _ in range(3):
+        for d in deps.get(op, []):
+            ops[d]()
+        ops[op]()
+    src = torch.empty(CALIB_ELEMS, dtype=torch.bfloat16, device="cuda").uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print("probe done", flush=True)
+    return 0
+
+
+def _counter_means(path: Path, kernel: str) -> tuple[float | None, float | None]:
+    """Mean counter value per dispatch of ``kernel`` and of the calibration copy in a counter CSV."""
+    k, c = [], []
+    with path.open(newline="") as fh:
+        for row in csv.DictReader(fh):
+            name = row.get("Kernel_Name", "")
+            val = float(row.get("Counter_Value", "nan"))
+            if kernel in name:
+                k.append(val)
+            elif "MulFunctor" in name:  # the probe's only multiply is the calibration copy
+                c.append(val)
+    return (sum(k) / len(k) if k else None), (sum(c) / len(c) if c else None)
+
+
+def _measure_traffic(op: str, kernel: str, nlaunch: int) -> dict:
+    """HBM bytes per launch of ``kernel`` from FETCH_SIZE and WRITE_SIZE passes, each scaled by what the same
+    counter reads for a copy of 2^27 bf16 elements (256 MiB read, 256 MiB written)."""
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return {"traffic": None, "reason": "rocprofv3 not found"}
+    out: dict = {}
+    calib_bytes = CALIB_ELEMS * 2
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        with tempfile.TemporaryDirectory() as tmp:
+            cmd = [prof, "--pmc", counter, "-f", "csv", "-d", tmp, "-o", "run", "--", sys.executable, "-u",
+                   str(Path(__file__).resolve()), "--traffic-probe", op]
+            try:
+                proc = subprocess.run(cmd, capture_output=True, text=True, timeout=240, cwd=str(REPO),
+                                      env={**os.environ, "TMPDIR": tmp})
+            except subprocess.TimeoutExpired:
+                return {"traffic": None, "reason": f"{counter} pass timed out"}
+            files = list(Path(tmp).rglob("*counter_collection.csv"))
+            if proc.returncode != 0 and not files:
+                return {"traffic": None, "reason": f"{counter} pass failed: {proc.stderr[-300:]}"}
+            if not files:
+                return {"traffic": None, "reason": f"{counter} pass wrote no counter file"}
+            kv, cv = _counter_means(files[0], kernel)
+            if kv is None or not cv:
+                return {"traffic": None, "reason": f"{counter}: kernel or calibration copy not found"}
+            scale = calib_bytes / (cv * 1024)
+            out[counter] = {"KiB_per_dispatch": round(kv, 1), "calib_KiB": round(cv, 1), "scale": round(scale, 4),
+                            "bytes": kv * 1024 * scale}
+    traffic = (out["FETCH_SIZE"]["bytes"] + out["WRITE_SIZE"]["bytes"])
+    return {"traffic": int(traffic), "counters": out,
+            "method": f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over {op} ({nlaunch} launch(es) per op call, "
+                      "mean per dispatch), each scaled by the same counter's reading for a 256 MiB bf16 copy"}
+
+
+# ------------------------------------------------------------------------------ CPU baseline
+
+
+def _cpu_baseline(budget_s: float) -> dict:
+    """The restated stock PyTorch modules (``pymsst_amd.core``) in fp32 on the host: whole configs[1] steps
+    at full shapes (band split, q/k RMSNorm + rotary, mask estimator MLP; forward + backward) for about
+    ``budget_s`` seconds, scaled to GB/s with the GPU step's algorithmic bytes; and configs[0] train steps
+    (BS-RoFormer tiny, fp32) as samples/s."""
+    import statistics
+
+    import torch
+
+    from pymsst_amd.core.bands import BandSplit, MaskEstimator
+    from pymsst_amd.core.transformer import RMSNorm, RotaryEmbedding, apply_rotary_emb_fast
+    from pymsst_amd.workloads import WORKLOADS, workload_batch
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(0)
+    B, T, NB, O, H = 4, 258, len(BSR_WIDTHS), 192, 768
+    F = sum(BSR_WIDTHS)
+    torch.manual_seed(4)
+    bs = BandSplit(O, BSR_WIDTHS)
+    me = MaskEstimator(O, BSR_WIDTHS, depth=2, mlp_expansion_factor=4)
+    nq, nk = RMSNorm(64), RMSNorm(64)
+    x = torch.distributions.Laplace(0.0, 0.05).sample((B, T, F)).requires_grad_()
+    h = torch.randn(B, T, NB, O, generator=g).requires_grad_()
+    q = torch.randn(B * NB, T, 8, 64, generator=g).requires_grad_()
+    k = torch.randn(B * NB, T, 8, 64, generator=g).requires_grad_()
+    cos, sin = RotaryEmbedding(64, 10000.0).tables(T, torch.device("cpu"), torch.float32)
+    grads = {}
+
+    def step():
+        for name, fn in (("bs", lambda: bs(x)), ("me", lambda: me(h)), ("q", lambda: apply_rotary_emb_fast(cos, sin, nq(q))),
+                         ("k", lambda: apply_rotary_emb_fast(cos, sin, nk(k)))):
+            y = fn()
+            if name not in grads:
+                grads[name] = torch.randn(y.shape, generator=g)
+            y.backward(grads[name])
+
+    step()
+    times = []
+    t_all = time.perf_counter()
     while True:
-        one()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all >= budget_s:
             break
-    gbs = sample_bytes * reps / el / 1e9
+    # the GPU step's algorithmic bytes at fp32 (s = 4)
+    M, R, D, s = B * T, B * NB * T * 8, 64, 4
+    step_bytes = (
+        (M * F + F + F * O + NB * O + M * NB * O) * s + 4 * M * NB
+        + (M * NB * O + 2 * M * F + 2 * F + 2 * F * O + NB * O) * s + 4 * M * NB
+        + 2 * (2 * R * D * s + 4 * R) + 2 * (3 * R * D * s + 4 * R)
+        + (M * NB * O + NB * H * O + NB * H + M * NB * H) * s
+        + (M * NB * H + 2 * F * H + 2 * F + 3 * M * F) * s
+        + (3 * M * F + 2 * M * NB * H + 4 * F * H + 2 * F) * s
+        + (M * NB * H + 2 * M * NB * O + 2 * NB * H * O + NB * H) * s
+    )
+    med = statistics.median(times)
+    # configs[0]: whole BS-RoFormer tiny training steps on the CPU
+    wl = WORKLOADS["bsr_tiny"]
+    model = wl.build_model(None, seed=4)
+    model.train()
+    opt = torch.optim.AdamW(model.parameters(), lr=wl.lr)
+    target, mixture = workload_batch(wl, seed=0)
+    ctimes = []
+    for i in range(4):
+        t0 = time.perf_counter()
+        loss = model(mixture, target)
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        if i >= 1:
+            ctimes.append(time.perf_counter() - t0)
+    c0 = statistics.median(ctimes)
     return {
-        "value": round(gbs, 3),
+        "value": round(step_bytes / med / 1e9, 3),
         "unit": "GB/s",
-        "cores": int(cores),
+        "cores": threads,
         "kind": "port",
-        "sample": f"numpy oracle (fp32) on {m} of 1032 rows for band split and mask final, "
-                  f"{rq} of 511872 q/k rows (one tensor); {reps} reps in {el:.1f}s",
+        "sample": f"restated stock PyTorch modules (pymsst_amd.core), fp32, {len(times)} whole configs[1] steps at "
+                  f"full shapes (band split, q/k RMSNorm+rotary, mask-estimator MLP; fwd+bwd), median "
+                  f"{med:.3f} s per step; os.cpu_count()={os.cpu_count()}, torch.get_num_threads()={threads}",
+        "ms_per_step": round(med * 1e3, 1),
+        "configs0_train": {"samples_per_s": round(wl.batch / c0, 3), "ms_median": round(c0 * 1e3, 1), "steps": 3,
+                           "workload": "configs[0] BS-RoFormer tiny, fp32, batch 2 x 32768 stereo, spectrogram L1, "
+                                       "AdamW"},
     }
 
 
-_TRAIN_DESCRIPTIONS = {
-    "bsr_train": "configs[2] BS-RoFormer dim 192, depth 6, 8x64 heads, 4 stems, batch 4 x 131584 stereo "
-                 "(258 frames), bf16 autocast, multi-res STFT L1, AdamW 5e-4",
-    "bsr_large": "configs[4] BS-RoFormer dim 512, depth 12, 8x64 heads, 1 stem, batch 2 x 485100 stereo "
-                 "(948 frames), activation checkpointing per axial block, bf16 autocast, L1, AdamW 5e-4",
-    "mbr_train": "configs[3] Mel-band RoFormer dim 192, depth 8, 8x64 heads, 4 stems, 60 mel bands, batch 4 x "
-                 "352800 stereo (690 frames), bf16 autocast, L1, AdamW 5e-4",
+# ------------------------------------------------------------------------------ train leg
+
+
+_TRAIN = {
+    0: ("bsr_tiny", "configs[0] BS-RoFormer tiny dim 64, depth 1, 4x32 heads, 1 stem, batch 2 x 32768 stereo, fp32, "
+                    "spectrogram L1, AdamW"),
+    2: ("bsr_train", "configs[2] BS-RoFormer dim 192, depth 6, 8x64 heads, 4 stems, batch 4 x 131584 stereo "
+                     "(258 frames), bf16 autocast, multi-res STFT L1, AdamW 5e-4"),
+    3: ("mbr_train", "configs[3] Mel-band RoFormer dim 192, depth 8, 8x64 heads, 4 stems, 60 mel bands, batch 4 x "
+                     "352800 stereo (690 frames), bf16 autocast, L1, AdamW 5e-4"),
+    4: ("bsr_large", "configs[4] BS-RoFormer dim 512, depth 12, 8x64 heads, 1 stem, batch 2 x 485100 stereo "
+                     "(948 frames), activation checkpointing per axial block, bf16 autocast, L1, AdamW 5e-4"),
 }
 
 
-def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused"), workload: str = "bsr_train") -> dict:
-    """Default configs[2]: BS-RoFormer dim 192, depth 6, 4 stems, batch 4 x 131584 stereo samples,
-    bf16 autocast, multi-resolution STFT loss, AdamW 5e-4.  One step = forward, backward and
-    optimizer step; train samples/s = batch / median step time, for the stock modules and for
-    the model patched onto the HIP kernels (same seed, same batch)."""
+def _train_leg(torch, cfg: int, steps: int, warmup: int, impls=("stock", "fused")) -> dict:
+    """Samples/s of full training steps (forward, backward, AdamW step) = batch / median step time, for the
+    stock modules and for the model patched onto the HIP kernels (same seed, same batch)."""
     import statistics
 
     from pymsst_amd import fused_roformer as fr
     from pymsst_amd.workloads import WORKLOADS, workload_batch
 
-    wl = WORKLOADS[workload]
+    key, desc = _TRAIN[cfg]
+    wl = WORKLOADS[key]
     dev = torch.device("cuda:0")
     target, mixture = workload_batch(wl, seed=0, device=dev)
     out = {}
@@ -270,10 +427,9 @@ def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused"), workloa
         fr.restore_stock_implementations()
         model = wl.build_model(dev, seed=4)
         model.train()
-        status = None
         if impl == "fused":
-            for key, value in fr.RUNTIME_PRESETS["hip_full"].items():
-                os.environ[key] = value
+            for k, v in fr.RUNTIME_PRESETS["hip_full"].items():
+                os.environ[k] = v
             status = fr.apply_roformer_fused_training_backend(model, "hip", rms_norm_mode="fast")
             if status.active == "off":
                 raise RuntimeError(f"fused backend inactive: {status.reason}")
@@ -282,7 +438,7 @@ def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused"), workloa
         opt = torch.optim.AdamW(model.parameters(), lr=wl.lr)
         times, losses = [], []
         for i in range(warmup + steps):
-            print(f"[train] {workload} {impl} step {i}", file=sys.stderr, flush=True)
+            print(f"[train] configs[{cfg}] {impl} step {i}", file=sys.stderr, flush=True)
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             with torch.autocast("cuda", dtype=wl.amp_dtype or torch.float32, enabled=wl.amp_dtype is not None):
@@ -300,12 +456,7 @@ def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused"), workloa
         fr.restore_stock_implementations(model)
         del model, opt
         torch.cuda.empty_cache()
-    res = {
-        "workload": _TRAIN_DESCRIPTIONS.get(workload, workload),
-        "steps": steps,
-        "warmup": warmup,
-        "detail": out,
-    }
+    res = {"workload": desc, "steps": steps, "warmup": warmup, "detail": out}
     for impl in impls:
         res[f"{impl}_samples_per_s"] = out[impl]["samples_per_s"]
     if "fused" in out and "stock" in out:
@@ -313,8 +464,13 @@ def _train_leg(torch, steps: int, warmup: int, impls=("stock", "fused"), workloa
     return res
 
 
+# ------------------------------------------------------------------------------ main
+
+
 def main(argv=None) -> int:
     args = _args(argv)
+    if args.traffic_probe:
+        return _traffic_probe(args.traffic_probe)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (multi-GPU runs are out of scope)"}))
         return 2
@@ -323,78 +479,42 @@ def main(argv=None) -> int:
     from pymsst_amd.fused_extension import load_fused_band_split_extension
 
     ext = load_fused_band_split_extension()
-    dtype = torch.bfloat16
-    w = Workload(torch, ext, dtype)
-    ops = w.ops()
+    w = Workload(torch, ext, torch.bfloat16)
+    ms_per_step, wall, per_op, value = _time_step(torch, w, args.steps, args.warmup)
     traffic = w.traffic()
-    stream = torch.cuda.current_stream()
+    del w
+    w32 = Workload(torch, ext, torch.float32)
+    ms32, _, per_op32, value32 = _time_step(torch, w32, max(args.steps // 3, 3), 3)
+    del w32
+    torch.cuda.empty_cache()
 
-    def step():
-        for _, fn in ops:
-            fn()
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    # whole-step timing
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    t_start.record(stream)
-    for _ in range(args.steps):
-        step()
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    ms_per_step = t_start.elapsed_time(t_end) / args.steps
-
-    # per-op timing with events bracketing each op on the launch stream
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in ops]
-          for _ in range(args.steps)]
-    for i in range(args.steps):
-        for j, (_, fn) in enumerate(ops):
-            ev[i][j][0].record(stream)
-            fn()
-            ev[i][j][1].record(stream)
-    torch.cuda.synchronize()
-    per_op = {}
-    for j, (name, _) in enumerate(ops):
-        ms = sum(ev[i][j][0].elapsed_time(ev[i][j][1]) for i in range(args.steps)) / args.steps
-        nbytes, flops = traffic[name]
-        per_op[name] = {
-            "ms": round(ms, 5),
-            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2) if flops else None,
-        }
-    total_bytes = sum(b for b, _ in traffic.values())
-    value = total_bytes / (ms_per_step * 1e-3) / 1e9
-    # roofline of the dominant single kernel: ops that are one kernel launched `n` times
+    # roofline of the dominant single kernel
     single = {name: per_op[name]["ms"] / n for name, (_, n) in SINGLE_KERNEL_OPS.items()}
     dom = max(single, key=single.get)
     kname, nlaunch = SINGLE_KERNEL_OPS[dom]
     launch_ms = single[dom]
     launch_bytes = traffic[dom][0] / nlaunch
-    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
+    launch_flops = traffic[dom][1] / nlaunch
+    ai = launch_flops / launch_bytes
+    if ai > BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+        achieved, peak, unit, bound = launch_flops / (launch_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma"
+    else:
+        achieved, peak, unit, bound = launch_bytes / (launch_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", "hbm"
+    meas = {"traffic": None, "reason": "skipped (--no-traffic)"} if args.no_traffic else \
+        _measure_traffic(dom, kname, nlaunch)
     roofline = {
-        "kernel": kname,
-        "op": dom,
-        "bound": "hbm",
-        "achieved": round(achieved, 1),
-        "peak": HBM_PEAK_GBS,
-        "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": TRAFFIC_PER_LAUNCH.get(kname),
-        "bytes_per_launch": int(launch_bytes),
-        "avg_ms": round(launch_ms, 5),
+        "kernel": kname, "op": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+        "frac": round(achieved / peak, 4), "traffic": meas.get("traffic"), "bytes_per_launch": int(launch_bytes),
+        "flops_per_launch": int(launch_flops), "avg_ms": round(launch_ms, 5),
+        "traffic_detail": {k: v for k, v in meas.items() if k != "traffic"},
     }
+
     # achievable streaming rate on this GPU: a plain elementwise copy of 1 GiB (read + write)
     src = torch.empty(1 << 29, dtype=torch.bfloat16, device="cuda").uniform_()
     dst = torch.empty_like(src)
     for _ in range(3):
         torch.mul(src, 1.0, out=dst)
+    stream = torch.cuda.current_stream()
     c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     c0.record(stream)
     for _ in range(10):
@@ -403,9 +523,19 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     copy_gbs = 2 * src.numel() * src.element_size() * 10 / (c0.elapsed_time(c1) * 1e-3) / 1e9
     del src, dst
+
     impls = ("stock", "fused") if args.train_impl == "both" else (args.train_impl,)
-    train = (_train_leg(torch, args.train_steps, args.train_warmup, impls, args.train_workload)
-             if args.train_steps > 0 else None)
+    train = None
+    if args.train_steps > 0:
+        cfgs = [int(c) for c in args.train_configs.split(",") if c.strip()]
+        head = 2 if 2 in cfgs else cfgs[0]
+        train = _train_leg(torch, head, args.train_steps, args.train_warmup, impls)
+        others = {}
+        for cfg in cfgs:
+            if cfg != head:
+                others[f"configs[{cfg}]"] = _train_leg(torch, cfg, max(args.train_steps // 3, 4), 2, impls)
+        if others:
+            train["other_configs"] = others
     cpu = None if args.no_cpu_baseline else _cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC,
@@ -421,13 +551,14 @@ def main(argv=None) -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "configs[1] kernel microbench: band split [4,258,4100]->192 (62 bands), "
-                        "q/k RMSNorm+rotary [248,258,8,64]x2, mask-estimator final 768->2*I_b+GLU; fwd+bwd",
+            "workload": "configs[1] kernel microbench, fwd+bwd: band split [4,258,4100]->192 (62 bands), q/k "
+                        "RMSNorm+rotary [248,258,8,64]x2, mask estimator per band 192 -> 768 + tanh -> 2*I_b + GLU",
             "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
             "hbm_copy_GBps_measured": round(copy_gbs, 1),
             "wall_s_timed": round(wall, 3),
         },
         "per_op": per_op,
+        "fp32_step": {"ms_per_step": round(ms32, 4), "GB/s": round(value32, 2), "per_op": per_op32},
         "train": train,
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -37,6 +37,7 @@ import torch
 import torch.nn.functional as F
 
 from .fused_extension import FusedKernelUnavailable, load_fused_band_split_extension
+from .packed_params import band_split_packs, mask_layer_packs
 
 CORE_GROUPED_TRAIN_ENV = "PYMSS_CORE_EXPERIMENTAL_TRAIN_GROUPED_BANDS"
 EXPERIMENTAL_GROUPED_LINEAR_ENV = "PYMSST_EXPERIMENTAL_FUSED_GROUPED_LINEAR"
@@ -254,7 +255,7 @@ def apply_roformer_fused_training_backend(
     gate_mode = _attention_gates_mode()
     gates = _patch_core_attention_gates(ext, gate_mode) if gate_mode else False
     grouped_linear = _patch_core_grouped_linear(ext) if _flag(EXPERIMENTAL_GROUPED_LINEAR_ENV) else False
-    layout = _patch_core_layout_reduce_copy() if _flag(EXPERIMENTAL_LAYOUT_REDUCE_COPY_ENV) else False
+    layout = _patch_core_packed_params() if _flag(EXPERIMENTAL_LAYOUT_REDUCE_COPY_ENV) else False
     pack_autograd = layout and _flag(EXPERIMENTAL_TRAIN_PARAM_PACK_AUTOGRAD_ENV)
     final_autograd = layout and _flag(EXPERIMENTAL_MASK_FINAL_AUTOGRAD_ENV)
     final_mode = _mask_estimator_final_mode(ext)
@@ -548,194 +549,117 @@ def _patch_core_grouped_linear(ext: Any) -> bool:
     return True
 
 
-# ---------------------------------------------------------------------- layout-reduce-copy helpers
+# ---------------------------------------------------------------------- packed parameters
 
 
-def _contiguous_index_range(indices: tuple[int, ...]) -> tuple[int, int] | None:
-    """``(start, end)`` if ``indices`` is ``start, start+1, ..., end-1`` (fr.py:661-666)."""
-    if not indices:
+def _run_of(indices) -> tuple[int, int] | None:
+    """``(start, end)`` when ``indices`` are consecutive band numbers."""
+    idx = tuple(int(i) for i in indices)
+    if idx and idx == tuple(range(idx[0], idx[0] + len(idx))):
+        return idx[0], idx[0] + len(idx)
+    return None
+
+
+def _packed_band_group_params(self, start, end, device, dtype):
+    """``BandSplit._get_group_params`` served from the module's flat parameter storages: the stacked
+    ``(gamma[G, I], weight[G, O, I], bias[G, O] | None)`` of bands ``[start, end)`` are views (cast once
+    per optimizer step under autocast), not per-step stacks."""
+    gamma_p, weight_p, bias_p = band_split_packs(self)
+    if gamma_p.storage.device != torch.device(device) or (bias_p is None and self.to_features[start][1].bias is not None):
+        return self._pymsst_stock_get_group_params(start, end, device, dtype)
+    return (gamma_p.group(start, end, dtype), weight_p.group(start, end, dtype),
+            bias_p.group(start, end, dtype) if bias_p is not None else None)
+
+
+def _packed_layer_group_params(self, layer_index, signature, indices, device, dtype):
+    """``MaskEstimator._get_layer_group_params`` from the flat storages when the bands are a consecutive
+    run (views, no stack); other groups keep the stock stack."""
+    run = _run_of(indices)
+    if run is not None:
+        weight_p, bias_p = mask_layer_packs(self, layer_index)
+        lin = self._band_groupable_layers()[run[0]][layer_index][1]
+        if weight_p.storage.device == torch.device(device) and (bias_p is not None or lin.bias is None):
+            return (weight_p.group(run[0], run[1], dtype),
+                    bias_p.group(run[0], run[1], dtype) if bias_p is not None else None)
+    return self._pymsst_stock_get_layer_group_params(layer_index, signature, indices, device, dtype)
+
+
+def _bands_of(module, h, indices):
+    """``h[..., indices, :]``: a narrow for a run of bands, one index_select otherwise."""
+    run = _run_of(indices)
+    if run is not None:
+        return h.narrow(-2, run[0], run[1] - run[0])
+    return h.index_select(-2, module._indices_tensor(tuple(indices), h.device))
+
+
+def _grouped_mlp_forward(self, x):
+    """The mask MLP with one grouped Linear per group of bands sharing a layer signature
+    (fr.py:332-369 runs the same grouping): hidden layers concatenate the groups' outputs and, when the
+    groups are not runs in band order, restore band order with one index_select; the last layer's
+    per-band GLU outputs are concatenated in band order."""
+    bands, _, _ = _core()
+    plan = self._layer_grouping_plan()
+    if plan is None:
         return None
-    start = int(indices[0])
-    end = int(indices[-1]) + 1
-    return (start, end) if tuple(indices) == tuple(range(start, end)) else None
+    h = x
+    for li, (kind, groups) in enumerate(plan):
+        if kind == "tanh":
+            h = bands.inference_tanh(h)
+            continue
+        last = li == len(plan) - 1
+        if not last and len({sig[1] for sig, _ in groups}) != 1:
+            return None
+        ys, order = [], []
+        for sig, idx in groups:
+            w, b = self._get_layer_group_params(li, sig, idx, x.device, x.dtype)
+            part = _bands_of(self, h, idx)
+            if last and _flag(EXPERIMENTAL_MASK_FINAL_AUTOGRAD_ENV):
+                ys.append(_MaskFinalGroupedLinearGLU.apply(part, w, b))
+            elif last:
+                ys.append(F.glu(bands.grouped_linear(part, w, b), dim=-1))
+            else:
+                ys.append(bands.grouped_linear(part, w, b))
+            order.extend(int(i) for i in idx)
+        in_order = order == list(range(len(order)))
+        if last:
+            if in_order:
+                return torch.cat([y.flatten(-2) for y in ys], dim=-1)
+            per_band = [None] * len(order)
+            for y, band in zip((t for y in ys for t in y.unbind(-2)), order):
+                per_band[band] = y
+            return torch.cat(per_band, dim=-1)
+        h = torch.cat(ys, dim=-2)
+        if not in_order:
+            inverse = [0] * len(order)
+            for pos, band in enumerate(order):
+                inverse[band] = pos
+            h = h.index_select(-2, self._indices_tensor(tuple(inverse), h.device))
+    return None
 
 
-def _select_band_group(x, indices, device, index_tensor_fn):
-    """Slice for contiguous bands, ``index_select`` otherwise (fr.py:669-674)."""
-    run = _contiguous_index_range(indices)
-    if run is not None:
-        return x[..., run[0] : run[1], :]
-    return x.index_select(-2, index_tensor_fn(indices, device))
-
-
-def _copy_band_group(destination, indices, source, device, index_tensor_fn) -> None:
-    """Slice assignment for contiguous bands, ``index_copy_`` otherwise (fr.py:677-690)."""
-    run = _contiguous_index_range(indices)
-    if run is not None:
-        destination[..., run[0] : run[1], :] = source
-        return
-    destination.index_copy_(-2, index_tensor_fn(indices, device), source)
-
-
-class _StackConvertedTensors(torch.autograd.Function):
-    """``stack([t.to(device, dtype)])`` whose backward returns each slice in its source dtype (fr.py:1136-1151)."""
-
-    @staticmethod
-    def forward(ctx, device, dtype, *tensors):
-        ctx.meta = tuple((t.device, t.dtype) for t in tensors)
-        return torch.stack([t.to(device=device, dtype=dtype) for t in tensors], dim=0)
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        grads = []
-        for i, (dev, dt) in enumerate(ctx.meta):
-            g = grad_out[i]
-            grads.append(g if (g.device == dev and g.dtype == dt) else g.to(device=dev, dtype=dt))
-        return (None, None, *grads)
-
-
-def _stack_converted_tensors(tensors, device, dtype):
-    """fr.py:702-707."""
-    tensors = list(tensors)
-    if len(tensors) == 1:
-        return tensors[0].to(device=device, dtype=dtype).unsqueeze(0)
-    if _flag(EXPERIMENTAL_TRAIN_PARAM_PACK_AUTOGRAD_ENV) and any(t.requires_grad for t in tensors):
-        return _StackConvertedTensors.apply(device, dtype, *tensors)
-    return torch.stack([t.to(device=device, dtype=dtype) for t in tensors], dim=0)
-
-
-def _refs_cache(module):
-    cache = getattr(module, "_pymsst_train_param_refs_cache", None)
-    if cache is None:
-        cache = {}
-        module._pymsst_train_param_refs_cache = cache
-    return cache
-
-
-def _band_split_group_param_refs(module, start: int, end: int):
-    """Cached ``(gammas, weights, biases|None)`` parameter tuples of bands ``[start, end)`` (fr.py:605-620)."""
-    cache = _refs_cache(module)
-    key = ("band_split", start, end)
-    hit = cache.get(key)
-    if hit is None:
-        nets = [module.to_features[i] for i in range(start, end)]
-        gammas = tuple(n[0].gamma for n in nets)
-        weights = tuple(n[1].weight for n in nets)
-        biases = tuple(n[1].bias for n in nets) if nets[0][1].bias is not None else None
-        hit = cache[key] = (gammas, weights, biases)
-    return hit
-
-
-def _mask_layer_param_refs(module, layer_index: int, indices: tuple[int, ...]):
-    """Cached ``(weights, biases|None)`` of one MLP layer for the given bands (fr.py:623-638)."""
-    cache = _refs_cache(module)
-    key = ("mask_layer", layer_index, tuple(indices))
-    hit = cache.get(key)
-    if hit is None:
-        layers = module._band_groupable_layers()
-        lins = [layers[i][layer_index][1] for i in indices]
-        hit = cache[key] = (tuple(l.weight for l in lins), tuple(l.bias for l in lins) if lins[0].bias is not None else None)
-    return hit
-
-
-def _packed_mask_layer_param_refs(module, estimators, layer_index: int, indices: tuple[int, ...]):
-    """As :func:`_mask_layer_param_refs` across several estimators (fr.py:641-658)."""
-    cache = _refs_cache(module)
-    key = ("packed_mask_layer", tuple(id(e) for e in estimators), layer_index, tuple(indices))
-    hit = cache.get(key)
-    if hit is None:
-        lins = [e._band_groupable_layers()[b][layer_index][1] for e in estimators for b in indices]
-        hit = cache[key] = (tuple(l.weight for l in lins), tuple(l.bias for l in lins) if lins[0].bias is not None else None)
-    return hit
-
-
-def _patch_core_layout_reduce_copy() -> bool:
-    """Mask-MLP grouping with slice/``index_copy`` layout and cached parameter packing (fr.py:321-500)."""
+def _patch_core_packed_params() -> bool:
+    """``PYMSST_EXPERIMENTAL_LAYOUT_REDUCE_COPY`` (fr.py:321-500): the band modules' grouped parameters
+    come from flat per-kind storages (``pymsst_amd.packed_params``) as views instead of per-step stacks,
+    and the mask MLP runs :func:`_grouped_mlp_forward`."""
     try:
         bands, _, _ = _core()
     except Exception:
         return False
-    ME = bands.MaskEstimator
-    if not getattr(ME._forward_layer_grouped_mlp, "_pymsst_layout_reduce_copy", False):
-        original = ME._forward_layer_grouped_mlp
-
-        def forward_layer_grouped_mlp_layout_reduce_copy(self, x):
-            plan = self._layer_grouping_plan()
-            if plan is None:
-                return None
-            h = x
-            for li, (kind, groups) in enumerate(plan):
-                if kind == "tanh":
-                    h = bands.inference_tanh(h)
-                    continue
-                if len({sig[1] for sig, _ in groups}) != 1:
-                    if li != len(plan) - 1:
-                        return None
-                    outs = [None] * len(self.to_freqs)
-                    for sig, idx in groups:
-                        w, b = self._get_layer_group_params(li, sig, idx, x.device, x.dtype)
-                        sel = _select_band_group(h, idx, x.device, self._indices_tensor)
-                        if _flag(EXPERIMENTAL_MASK_FINAL_AUTOGRAD_ENV):
-                            y = _MaskFinalGroupedLinearGLU.apply(sel, w, b)
-                        else:
-                            y = F.glu(bands.grouped_linear(sel, w, b), dim=-1)
-                        for pos, band_out in zip(idx, y.unbind(dim=-2)):
-                            outs[pos] = band_out
-                    return torch.cat(outs, dim=-1)
-                nxt = None
-                for sig, idx in groups:
-                    w, b = self._get_layer_group_params(li, sig, idx, x.device, x.dtype)
-                    y = bands.grouped_linear(_select_band_group(h, idx, x.device, self._indices_tensor), w, b)
-                    if nxt is None:
-                        nxt = y.new_empty(*h.shape[:-1], y.shape[-1])
-                    _copy_band_group(nxt, idx, y, x.device, self._indices_tensor)
-                h = nxt
-            return F.glu(h, dim=-1).flatten(start_dim=-2)
-
-        forward_layer_grouped_mlp_layout_reduce_copy._pymsst_layout_reduce_copy = True
-        forward_layer_grouped_mlp_layout_reduce_copy._pymsst_original_forward_layer_grouped_mlp = original
-        ME._forward_layer_grouped_mlp = forward_layer_grouped_mlp_layout_reduce_copy
-
-    if not getattr(bands.BandSplit._get_group_params, "_pymsst_layout_reduce_copy", False):
-        orig_bs = bands.BandSplit._get_group_params
-
-        def band_split_get_group_params(self, start, end, device, dtype):
-            key = (start, end, device.type, device.index, dtype)
-            if not self.training and key in self._group_cache:
-                return self._group_cache[key]
-            gammas, weights, biases = _band_split_group_param_refs(self, start, end)
-            out = (
-                _stack_converted_tensors(gammas, device, dtype),
-                _stack_converted_tensors(weights, device, dtype),
-                _stack_converted_tensors(biases, device, dtype) if biases is not None else None,
-            )
-            if not self.training:
-                self._group_cache[key] = out
-            return out
-
-        band_split_get_group_params._pymsst_layout_reduce_copy = True
-        band_split_get_group_params._pymsst_original_get_group_params = orig_bs
-        bands.BandSplit._get_group_params = band_split_get_group_params
-
-    if not getattr(ME._get_layer_group_params, "_pymsst_layout_reduce_copy", False):
-        orig_layer = ME._get_layer_group_params
-
-        def get_layer_group_params(self, layer_index, signature, indices, device, dtype):
-            key = (layer_index, signature, tuple(indices), device.type, device.index, dtype)
-            if not self.training and key in self._layer_group_cache:
-                return self._layer_group_cache[key]
-            weights, biases = _mask_layer_param_refs(self, layer_index, tuple(indices))
-            out = (
-                _stack_converted_tensors(weights, device, dtype),
-                _stack_converted_tensors(biases, device, dtype) if biases is not None else None,
-            )
-            if not self.training:
-                self._layer_group_cache[key] = out
-            return out
-
-        get_layer_group_params._pymsst_layout_reduce_copy = True
-        get_layer_group_params._pymsst_original_get_layer_group_params = orig_layer
-        ME._get_layer_group_params = get_layer_group_params
+    BS, ME = bands.BandSplit, bands.MaskEstimator
+    if not getattr(BS._get_group_params, "_pymsst_packed", False):
+        BS._pymsst_stock_get_group_params = BS._get_group_params
+        _packed_band_group_params._pymsst_packed = True
+        _packed_band_group_params._pymsst_original_get_group_params = BS._get_group_params
+        BS._get_group_params = _packed_band_group_params
+    if not getattr(ME._get_layer_group_params, "_pymsst_packed", False):
+        ME._pymsst_stock_get_layer_group_params = ME._get_layer_group_params
+        _packed_layer_group_params._pymsst_packed = True
+        _packed_layer_group_params._pymsst_original_get_layer_group_params = ME._get_layer_group_params
+        ME._get_layer_group_params = _packed_layer_group_params
+    if not getattr(ME._forward_layer_grouped_mlp, "_pymsst_packed", False):
+        _grouped_mlp_forward._pymsst_packed = True
+        _grouped_mlp_forward._pymsst_original_forward_layer_grouped_mlp = ME._forward_layer_grouped_mlp
+        ME._forward_layer_grouped_mlp = _grouped_mlp_forward
     return True
 
 
@@ -771,6 +695,8 @@ def _patch_core_mask_estimator_final(ext: Any, mode: str) -> bool:
             fused = _fused_mask_mlp(self, x, plan, ext)
             if fused is not None:
                 return fused
+        # hidden layers: one grouped Linear per group of bands (all groups must share the output
+        # width), outputs back in band order
         h = x
         for li, (kind, groups) in enumerate(plan[:-1]):
             if kind == "tanh":
@@ -778,31 +704,38 @@ def _patch_core_mask_estimator_final(ext: Any, mode: str) -> bool:
                 continue
             if len({sig[1] for sig, _ in groups}) != 1:
                 return original(self, x)
-            nxt = None
+            ys, order = [], []
             for sig, idx in groups:
                 w, b = self._get_layer_group_params(li, sig, idx, x.device, x.dtype)
-                y = bands.grouped_linear(_select_band_group(h, idx, x.device, self._indices_tensor), w, b)
-                if nxt is None:
-                    nxt = y.new_empty(*h.shape[:-1], y.shape[-1])
-                _copy_band_group(nxt, idx, y, x.device, self._indices_tensor)
-            h = nxt
+                ys.append(bands.grouped_linear(_bands_of(self, h, idx), w, b))
+                order.extend(int(i) for i in idx)
+            h = torch.cat(ys, dim=-2)
+            if order != list(range(len(order))):
+                inverse = [0] * len(order)
+                for pos, band in enumerate(order):
+                    inverse[band] = pos
+                h = h.index_select(-2, self._indices_tensor(tuple(inverse), h.device))
         last = len(plan) - 1
-        weights, biases = [], []
         for b_idx, layers in enumerate(self._band_groupable_layers()):
             kind, lin = layers[last]
             if kind != "linear" or lin.bias is None:
                 return original(self, x)
             if lin.in_features != h.shape[-1] or lin.out_features != self.dim_inputs[b_idx] * 2:
                 return original(self, x)
-            weights.append(lin.weight if lin.weight.dtype == h.dtype else lin.weight.to(h.dtype))
-            biases.append(lin.bias if lin.bias.dtype == h.dtype else lin.bias.to(h.dtype))
+        weight_p, bias_p = mask_layer_packs(self, last)
+        if weight_p.storage.device != h.device:
+            return original(self, x)
         lead = h.shape[:-2]
         h3 = h.reshape(-1, len(self.to_freqs), h.shape[-1])
-        bias_flat = torch.cat(biases, dim=0)
-        out = _FusedMaskEstimatorFinal.apply(
-            h3, bias_flat, _dim_offsets_tensor(self, x.device), ext, tuple(int(d) for d in self.dim_inputs), mode,
-            *weights,
-        )
+        if _packed_mask_final_ops(ext):
+            out = _FusedMaskEstimatorFinalPacked.apply(
+                h3, weight_p.flat(h.dtype), bias_p.flat(h.dtype), ext, tuple(int(d) for d in self.dim_inputs))
+        else:
+            weights = [v.view(s) for v, s in zip(weight_p.flat(h.dtype).split(weight_p.sizes), weight_p.shapes)]
+            out = _FusedMaskEstimatorFinal.apply(
+                h3, bias_p.flat(h.dtype), _dim_offsets_tensor(self, x.device), ext,
+                tuple(int(d) for d in self.dim_inputs), mode, *weights,
+            )
         return out.reshape(*lead, self._dim_total)
 
     forward_layer_grouped_mlp_mask_final_fused._pymsst_mask_estimator_final_fused = True
@@ -811,10 +744,15 @@ def _patch_core_mask_estimator_final(ext: Any, mode: str) -> bool:
     return True
 
 
+def _packed_mask_final_ops(ext) -> bool:
+    return hasattr(ext, "mask_estimator_final_forward_packed") and hasattr(ext, "mask_estimator_final_backward_packed")
+
+
 def _fused_mask_mlp(module, x, plan, ext):
     """Whole depth-2 mask MLP (Linear -> tanh -> Linear -> GLU) on the kernels, or ``None`` when the
-    module does not have that shape.  Under autocast the compute dtype is the autocast dtype,
-    as for the stock grouped GEMMs."""
+    module does not have that shape.  The parameters come from the module's flat storages (the
+    first layer's ``[NB, H, dim]`` stack is a view); under autocast they and x are in the autocast
+    dtype, as for the stock grouped GEMMs."""
     nb = len(module.to_freqs)
     if len(plan) != 3 or plan[0][0] != "linear" or plan[1][0] != "tanh" or plan[2][0] != "linear":
         return None
@@ -830,14 +768,18 @@ def _fused_mask_mlp(module, x, plan, ext):
         return None
     if any(l.out_features != 2 * d or l.in_features != first[0].out_features for l, d in zip(last, module.dim_inputs)):
         return None
+    w1_p, b1_p = mask_layer_packs(module, 0)
+    w2_p, b2_p = mask_layer_packs(module, 2)
+    if w1_p.storage.device != x.device:
+        return None
     dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else x.dtype
+    hidden = first[0].out_features
     lead = x.shape[:-2]
     x3 = x.reshape(-1, nb, x.shape[-1]).to(dt)
-    w1 = torch.stack([l.weight for l in first]).to(dt)
-    b1 = torch.stack([l.bias for l in first]).to(dt)
-    w2 = torch.cat([l.weight.reshape(-1) for l in last]).to(dt)
-    b2 = torch.cat([l.bias for l in last]).to(dt)
-    out = _FusedMaskMLP.apply(x3, w1, b1, w2, b2, ext, tuple(int(d) for d in module.dim_inputs))
+    w1 = w1_p.group(0, nb, dt)
+    b1 = b1_p.group(0, nb, dt)
+    out = _FusedMaskMLP.apply(x3, w1.view(nb, hidden, -1), b1.view(nb, hidden), w2_p.flat(dt), b2_p.flat(dt), ext,
+                              tuple(int(d) for d in module.dim_inputs))
     return out.reshape(*lead, module._dim_total)
 
 
@@ -856,6 +798,10 @@ def _dim_offsets_tensor(module, device) -> torch.Tensor:
 # ---------------------------------------------------------------------- band split forward
 
 
+def _packed_band_split_ops(ext) -> bool:
+    return hasattr(ext, "band_split_ragged_forward_packed") and hasattr(ext, "band_split_ragged_backward_packed")
+
+
 def _forward_grouped_band_split_cuda_ext(self, x: torch.Tensor) -> torch.Tensor:
     """Patched ``BandSplit._forward_grouped`` (fr.py:827-873)."""
     if not self.training or x.device.type != "cuda" or x.dtype not in _FLOAT_TYPES:
@@ -872,16 +818,21 @@ def _forward_grouped_band_split_cuda_ext(self, x: torch.Tensor) -> torch.Tensor:
     if torch.is_autocast_enabled("cuda"):
         x = x.to(torch.get_autocast_dtype("cuda"))
     if ragged:
-        gammas = [net[0].gamma for net in self.to_features]
-        weights = [net[1].weight for net in self.to_features]
-        biases = [net[1].bias for net in self.to_features]
-        if any(t.dtype != x.dtype for t in (gammas[0], weights[0], biases[0])):
-            gammas, weights, biases = _cast_band_params(gammas, weights, biases, x.dtype)
+        dims = tuple(int(d) for d in self.dim_inputs)
+        if _packed_band_split_ops(ext):
+            gamma_p, weight_p, bias_p = band_split_packs(self)
+            if gamma_p.storage.device == x.device:
+                out = _FusedBandSplitPacked.apply(x.reshape(-1, x.shape[-1]), gamma_p.flat(x.dtype),
+                                                  weight_p.flat(x.dtype), bias_p.flat(x.dtype), ext, dims)
+                return out.reshape(*lead, len(dims), -1)
+        gammas = [net[0].gamma.to(x.dtype) for net in self.to_features]
+        weights = [net[1].weight.to(x.dtype) for net in self.to_features]
+        biases = [net[1].bias.to(x.dtype) for net in self.to_features]
         out = _FusedBandSplitRagged.apply(
-            x.reshape(-1, x.shape[-1]), _dim_offsets_tensor(self, x.device), ext,
-            tuple(int(d) for d in self.dim_inputs), bwd_mode, *gammas, *weights, *biases,
+            x.reshape(-1, x.shape[-1]), _dim_offsets_tensor(self, x.device), ext, dims, bwd_mode,
+            *gammas, *weights, *biases,
         )
-        return out.reshape(*lead, len(self.dim_inputs), -1)
+        return out.reshape(*lead, len(dims), -1)
     outs = []
     for start, end, width in self._dim_groups:
         part = x[..., self._dim_offsets[start] : self._dim_offsets[end]].reshape(-1, end - start, width)
@@ -889,16 +840,6 @@ def _forward_grouped_band_split_cuda_ext(self, x: torch.Tensor) -> torch.Tensor:
         y = _FusedBandSplitGroup.apply(part, gamma, weight, bias, ext, bwd_mode)
         outs.append(y.reshape(*lead, end - start, -1))
     return torch.cat(outs, dim=-2)
-
-
-def _cast_band_params(gammas, weights, biases, dtype):
-    """Per-band parameters in ``dtype`` with one cast per parameter kind: concatenate, cast, split
-    (three kernels instead of one cast per band; gradients flow back through the views)."""
-    out = []
-    for group in (gammas, weights, biases):
-        flat = torch.cat([t.reshape(-1) for t in group]).to(dtype)
-        out.append([v.view(t.shape) for v, t in zip(flat.split([t.numel() for t in group]), group)])
-    return out
 
 
 # ---------------------------------------------------------------------- autograd Functions
@@ -1007,6 +948,51 @@ class _FusedBandSplitRagged(torch.autograd.Function):
             dbs.append(gb[0])
             start += d
         return (dx, None, None, None, None, *dgs, *dws, *dbs)
+
+
+class _FusedBandSplitPacked(torch.autograd.Function):
+    """All bands in one launch on the flat parameter buffers (this build's form of fr.py:929-1026):
+    ``gamma_all[F]``, ``weight_all`` (the ``[O, I_b]`` weights back to back), ``bias_all[NB*O]``.  Saves
+    x (not a normalised copy) and inv_norm; the backward returns the flat gradients, which the
+    parameter view's backward splits per band."""
+
+    @staticmethod
+    def forward(ctx, x, gamma_all, weight_all, bias_all, extension, dim_inputs):
+        x = x.contiguous()
+        out, _, inv_norm = extension.band_split_ragged_forward_packed(x, gamma_all, weight_all, bias_all, dim_inputs,
+                                                                     write_normed=False)
+        ctx.extension, ctx.dim_inputs = extension, dim_inputs
+        ctx.save_for_backward(x, inv_norm, gamma_all, weight_all)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, inv_norm, gamma_all, weight_all = ctx.saved_tensors
+        nb = len(ctx.dim_inputs)
+        grad_out = grad_out.reshape(x.shape[0], nb, -1).contiguous()
+        dx, dg, dw, db = ctx.extension.band_split_ragged_backward_packed(
+            grad_out, x, True, inv_norm, gamma_all, weight_all, ctx.dim_inputs, True)
+        return dx, dg, dw, db, None, None
+
+
+class _FusedMaskEstimatorFinalPacked(torch.autograd.Function):
+    """Final per-band Linear + GLU for all bands on the flat weight / bias buffers (this build's form of
+    fr.py:1087-1133); both reference modes compute these values."""
+
+    @staticmethod
+    def forward(ctx, x, weight_all, bias_all, extension, dim_inputs):
+        x = x.contiguous()
+        out, pre = extension.mask_estimator_final_forward_packed(x, weight_all, bias_all, dim_inputs)
+        ctx.extension, ctx.dim_inputs = extension, dim_inputs
+        ctx.save_for_backward(x, pre, weight_all)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, pre, weight_all = ctx.saved_tensors
+        grad_out = grad_out.reshape(x.shape[0], -1).to(x.dtype).contiguous()
+        dx, db, dw = ctx.extension.mask_estimator_final_backward_packed(grad_out, x, pre, weight_all, ctx.dim_inputs)
+        return dx, dw, db, None, None
 
 
 class _FusedGroupedLinear(torch.autograd.Function):

@@ -149,37 +149,13 @@ def test_restore_stock_implementations_unwinds_everything(monkeypatch):
     assert not getattr(model.band_split, "_pymsst_fused_band_split", False)
 
 
-def test_layout_helpers_slice_contiguous_band_indices():
+def test_band_selection_narrows_runs_and_gathers_the_rest():
     x = torch.arange(2 * 4 * 3, dtype=torch.float32).reshape(2, 4, 3)
-    calls = []
-
-    def index_tensor(indices, device):
-        calls.append(indices)
-        return torch.as_tensor(indices, device=device)
-
-    assert fr._contiguous_index_range((1, 2)) == (1, 3)
-    sel = fr._select_band_group(x, (1, 2), x.device, index_tensor)
-    assert not calls and torch.equal(sel, x[..., 1:3, :])
-    dst = torch.zeros_like(x)
-    fr._copy_band_group(dst, (1, 2), sel, x.device, index_tensor)
-    assert not calls and torch.equal(dst[..., 1:3, :], sel)
-
-
-def test_layout_helpers_keep_index_select_for_noncontiguous_indices():
-    x = torch.arange(2 * 4 * 3, dtype=torch.float32).reshape(2, 4, 3)
-    calls = []
-
-    def index_tensor(indices, device):
-        calls.append(indices)
-        return torch.as_tensor(indices, device=device)
-
-    assert fr._contiguous_index_range((0, 2)) is None
-    assert fr._contiguous_index_range(()) is None
-    sel = fr._select_band_group(x, (0, 2), x.device, index_tensor)
-    assert len(calls) == 1 and torch.equal(sel, x.index_select(-2, torch.tensor((0, 2))))
-    dst = torch.zeros_like(x)
-    fr._copy_band_group(dst, (0, 2), sel, x.device, index_tensor)
-    assert torch.equal(dst[..., 0, :], x[..., 0, :]) and torch.equal(dst[..., 2, :], x[..., 2, :])
+    est = _small_model().mask_estimators[0]
+    assert fr._run_of((1, 2)) == (1, 3) and fr._run_of((0, 2)) is None and fr._run_of(()) is None
+    run = fr._bands_of(est, x, (1, 2))
+    assert run._base is not None and torch.equal(run, x[..., 1:3, :])  # a view, no gather
+    assert torch.equal(fr._bands_of(est, x, (0, 2)), x.index_select(-2, torch.tensor((0, 2))))
 
 
 @pytest.mark.parametrize("mask_depth", [2, 3])
@@ -196,18 +172,67 @@ def test_layout_reduce_copy_matches_original_mask_mlp(monkeypatch, mask_depth):
     assert torch.equal(candidate, reference)
 
 
-def test_train_param_pack_autograd_matches_stack_to(monkeypatch):
-    tensors = [torch.randn(2, 3, requires_grad=True) for _ in range(3)]
-    ref_tensors = [t.detach().clone().requires_grad_() for t in tensors]
+def test_flat_params_views_match_stack_and_cast():
+    """A packed run of parameters, cast to fp16, equals ``stack([p.to(fp16)])`` and its backward gives each
+    parameter its slice of the gradient in the parameter's dtype; the parameters keep their identity and
+    become views of one storage."""
+    from pymsst_amd.packed_params import FlatParams
+
+    params = [torch.nn.Parameter(torch.randn(2, 3)) for _ in range(4)]
+    refs = [p.detach().clone().requires_grad_() for p in params]
+    ids = [id(p) for p in params]
+    pk = FlatParams(params)
+    assert [id(p) for p in params] == ids and pk.intact()
+    assert all(p.data_ptr() == pk.storage.data_ptr() + 6 * 4 * i for i, p in enumerate(params))
     grad = torch.randn(3, 2, 3, dtype=torch.float16)
-    monkeypatch.setenv(fr.EXPERIMENTAL_TRAIN_PARAM_PACK_AUTOGRAD_ENV, "1")
-    packed = fr._stack_converted_tensors(tensors, torch.device("cpu"), torch.float16)
-    reference = torch.stack([t.to(dtype=torch.float16) for t in ref_tensors], dim=0)
-    packed.backward(grad)
-    reference.backward(grad)
-    assert torch.equal(packed, reference)
-    for t, r in zip(tensors, ref_tensors):
-        assert torch.equal(t.grad, r.grad)
+    got = pk.group(1, 4, torch.float16)
+    want = torch.stack([r.to(torch.float16) for r in refs[1:]], dim=0)
+    assert torch.equal(got, want)
+    got.backward(grad)
+    want.backward(grad)
+    assert params[0].grad is None
+    for p, r in zip(params[1:], refs[1:]):
+        assert p.grad.dtype == torch.float32 and torch.equal(p.grad, r.grad)
+    flat = pk.flat()
+    assert torch.equal(flat, torch.cat([r.detach().reshape(-1) for r in refs]))
+
+
+def test_flat_params_cast_follows_optimizer_updates_and_device_moves():
+    from pymsst_amd.packed_params import FlatParams, pack
+
+    mod = torch.nn.Module()
+    params = [torch.nn.Parameter(torch.randn(5)) for _ in range(3)]
+    pk = pack(mod, "k", params)
+    assert pack(mod, "k", params) is pk
+    c1 = pk.flat(torch.bfloat16).detach().clone()
+    opt = torch.optim.SGD(params, lr=1.0)
+    for p in params:
+        p.grad = torch.ones_like(p)
+    opt.step()
+    c2 = pk.flat(torch.bfloat16)
+    assert not torch.equal(c2, c1)  # the cached cast was refreshed
+    assert torch.equal(c2, torch.cat([p.detach() for p in params]).bfloat16())
+    params[1].data = params[1].data.clone()  # no longer a view of the storage (what .to() does)
+    assert not pk.intact()
+    pk2 = pack(mod, "k", params)
+    assert pk2 is not pk and pk2.intact() and isinstance(pk2, FlatParams)
+
+
+def test_packed_band_split_keeps_state_dict_and_is_zero_copy(monkeypatch):
+    monkeypatch.setenv(fr.EXPERIMENTAL_LAYOUT_REDUCE_COPY_ENV, "1")
+    model = _small_model()
+    keys = list(model.state_dict())
+    ref = {k: v.clone() for k, v in model.state_dict().items()}
+    bs = model.band_split
+    stock = bands.BandSplit._get_group_params(bs, 0, 2, torch.device("cpu"), torch.float32)
+    fr.apply_roformer_fused_training_backend(model, "cuda_ext", extension=object())
+    got = bs._get_group_params(0, 2, torch.device("cpu"), torch.float32)
+    assert all(torch.equal(a, b) for a, b in zip(got, stock))
+    gamma_pack = bs.__dict__["_pymsst_packs"]["band_split.gamma"]
+    assert got[0].data_ptr() == gamma_pack.storage.data_ptr()  # a view of the storage, not a stack
+    assert list(model.state_dict()) == keys
+    assert all(torch.equal(v, ref[k]) for k, v in model.state_dict().items())
+    fr.restore_stock_implementations(model)
 
 
 def _reference_grouped_linear(x, weight, bias):
@@ -236,18 +261,20 @@ def test_mask_final_grouped_linear_glu_matches_reference():
         assert torch.allclose(a.grad, b.grad, atol=1e-6, rtol=1e-6)
 
 
-def test_layout_param_reference_caches_are_stable():
-    model = _small_model()
-    estimator = model.mask_estimators[0]
-    fr.apply_roformer_fused_training_backend(model, "cuda_ext", extension=object())
-    b1 = fr._band_split_group_param_refs(model.band_split, 0, 2)
-    b2 = fr._band_split_group_param_refs(model.band_split, 0, 2)
-    m1 = fr._mask_layer_param_refs(estimator, 0, (0, 1))
-    m2 = fr._mask_layer_param_refs(estimator, 0, (0, 1))
-    p1 = fr._packed_mask_layer_param_refs(estimator, (estimator,), 0, (0, 1))
-    p2 = fr._packed_mask_layer_param_refs(estimator, (estimator,), 0, (0, 1))
-    assert b1 is b2 and m1 is m2 and p1 is p2
-    assert len(b1[0]) == 2 and len(m1[0]) == 2 and len(p1[0]) == 2
+def test_grouped_mlp_forward_restores_band_order_for_interleaved_groups(monkeypatch):
+    """Widths whose equal-signature bands are not runs (8, 16, 8, 16): the final layer's groups are
+    gathered with index_select and the outputs come back in band order, equal to the per-band MLPs."""
+    monkeypatch.setenv(fr.EXPERIMENTAL_LAYOUT_REDUCE_COPY_ENV, "1")
+    torch.manual_seed(5)
+    est = bands.MaskEstimator(16, (8, 16, 8, 16), depth=2, mlp_expansion_factor=2)
+    x = torch.randn(3, 4, 16)
+    per_band = torch.cat([mlp(xb) for xb, mlp in zip(x.unbind(dim=-2), est.to_freqs)], dim=-1)
+    fr._patch_core_packed_params()
+    try:
+        got = est._forward_layer_grouped_mlp(x)
+    finally:
+        fr.restore_stock_implementations()
+    assert torch.allclose(got, per_band, atol=1e-6, rtol=1e-6)
 
 
 def test_cpu_inputs_take_the_stock_path_after_patching(monkeypatch):
