@@ -20,7 +20,7 @@
 // Backward dx block (64 rows, band b, 64-wide input chunk): gs^T[i][m] = W_b^T dy^T
 // (K = O) on MFMA; the block writes t = gs * gamma (fp32), its chunk's part of the
 // per-row dot(gs * gamma, n) and the dgamma partials ([m_tiles, F], reduced by
-// col_sum_kernel).  A finish pass per (64 rows, band) adds the dot partials of the
+// col_sum_kernel).  A finish pass over the same blocks adds the dot partials of the
 // band's chunks and writes dx = inv (t sqrt(I) - n dot / sqrt(I)).  dW block
 // (band, 64 i x 64 o): dW^T[i][o] = sum_m n[m][i] gamma_i dy[m][o], K = M.  dbias =
 // column sums of dy.  No atomics anywhere.
@@ -412,57 +412,76 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
     pdot[(m0 + tid) * pitch + off / 64 + band + ichunk] = (sdot[0][tid] + sdot[1][tid]) + (sdot[2][tid] + sdot[3][tid]);
 }
 
-// dx of one (64-row tile, band): dot[m] = sum of the band's chunk partials (fixed order),
-// dx = inv (t sqrt(I) - n dot / sqrt(I)) with n = x inv sqrt(I) (FROM_X) or the saved normed.
-// Thread q of the block walks the tile's (row, 4-element quad) pairs row-major.
+// dx of one (64-row tile, band, 64-wide input chunk), the blocks of the dx kernel's grid:
+// dot[m] = the band's chunk partials added in a fixed order (4 threads per row, then a fixed
+// butterfly), dx = inv (t sqrt(I) - n dot / sqrt(I)) with n = x inv sqrt(I) (FROM_X) or the saved
+// normed.  Thread t covers the 4-element quad t % 16 of the chunk on rows t / 16 + 16 j, j < 4:
+// every load of the thread is issued before the first store.
 template <typename T, bool FROM_X, bool V4>
 __global__ __launch_bounds__(256) void bs_dx_finish_kernel(const float* __restrict__ tbuf, const T* __restrict__ nsrc,
                                                            const float* __restrict__ inv_norm,
                                                            const float* __restrict__ pdot, T* __restrict__ dx,
-                                                           int pitch, BandArgs a) {
+                                                           int pitch, int max_ichunks, XcdGrid xg, BandArgs a) {
   __shared__ float sinv[kBM];
   __shared__ float sdot[kBM];
-  const int band = a.NB - 1 - static_cast<int>(blockIdx.y);
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBM;
+  uint32_t grp, mt;
+  if (!xcd_block(xg, grp, mt)) return;
+  const int band = a.NB - 1 - static_cast<int>(grp) / max_ichunks;
+  const int i0 = static_cast<int>(grp) % max_ichunks * 64;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  if (i0 >= I) return;  // uniform over the block
+  const int64_t m0 = static_cast<int64_t>(mt) * kBM;
   const int rows_valid = static_cast<int>(a.M - m0 < kBM ? a.M - m0 : kBM);
   const int tid = threadIdx.x;
   const float root = sqrtf(static_cast<float>(I));
-  if (tid < rows_valid) {
+  {
+    const int r = tid >> 2, part = tid & 3;
     const int nch = (I + 63) / 64;
-    const float* pd = pdot + (m0 + tid) * pitch + off / 64 + band;
     float d = 0.f;
-    for (int c = 0; c < nch; ++c) d += pd[c];
-    const float inv = inv_norm[(m0 + tid) * a.NB + band];
-    sinv[tid] = inv;
-    sdot[tid] = d / root;
+    if (r < rows_valid) {
+      const float* pd = pdot + (m0 + r) * pitch + off / 64 + band;
+      for (int c = part; c < nch; c += 4) d += pd[c];
+    }
+    d += __shfl_xor(d, 1, kWave);
+    d += __shfl_xor(d, 2, kWave);
+    if (part == 0 && r < rows_valid) {
+      sinv[r] = inv_norm[(m0 + r) * a.NB + band];
+      sdot[r] = d / root;
+    }
   }
   __syncthreads();
-  const int nq = (I + 3) / 4;
-  for (int q = tid; q < rows_valid * nq; q += 256) {
-    const int r = q / nq;
-    const int k = (q - r * nq) * 4;
-    const int64_t e = (m0 + r) * a.F + off + k;
-    const float inv = sinv[r];
-    const float ns = FROM_X ? inv * root : 1.f;
-    const float c = sdot[r];
-    float n[4], t[4], o[4];
-    if (V4) {
-      const float4 tv = *reinterpret_cast<const float4*>(tbuf + e);
-      t[0] = tv.x;
-      t[1] = tv.y;
-      t[2] = tv.z;
-      t[3] = tv.w;
-      load_pack<T, 4>(nsrc + e, n);
+  const int k = i0 + 4 * (tid & 15);
+  if (k >= I) return;
+  constexpr int kJ = kBM / 16;
+  if (V4) {
+    float4 t[kJ];
+    float n[kJ][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = inv * (t[j] * root - n[j] * ns * c);
-      store_pack<T, 4>(dx + e, o);
-    } else {
-      for (int j = 0; j < 4 && k + j < I; ++j) {
-        const float nv = to_f32(nsrc[e + j]) * ns;
-        dx[e + j] = from_f32<T>(inv * (tbuf[e + j] * root - nv * c));
-      }
+    for (int j = 0; j < kJ; ++j) {
+      const int r = (tid >> 4) + 16 * j;
+      const int rc = r < rows_valid ? r : rows_valid - 1;  // clamped loads, no branch before the math
+      const int64_t e = (m0 + rc) * a.F + off + k;
+      t[j] = *reinterpret_cast<const float4*>(tbuf + e);
+      load_pack<T, 4>(nsrc + e, n[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const int r = (tid >> 4) + 16 * j;
+      if (r >= rows_valid) continue;
+      const float inv = sinv[r], c = sdot[r] * (FROM_X ? inv * root : 1.f);
+      const float o[4] = {inv * (t[j].x * root - n[j][0] * c), inv * (t[j].y * root - n[j][1] * c),
+                          inv * (t[j].z * root - n[j][2] * c), inv * (t[j].w * root - n[j][3] * c)};
+      store_pack<T, 4>(dx + (m0 + r) * a.F + off + k, o);
+    }
+  } else {
+    for (int j = 0; j < kJ; ++j) {
+      const int r = (tid >> 4) + 16 * j;
+      if (r >= rows_valid) continue;
+      const float inv = sinv[r], c = sdot[r] * (FROM_X ? inv * root : 1.f);
+      const int64_t e = (m0 + r) * a.F + off + k;
+      for (int q = 0; q < 4 && k + q < I; ++q)
+        dx[e + q] = from_f32<T>(inv * (tbuf[e + q] * root - to_f32(nsrc[e + q]) * c));
     }
   }
 }
@@ -963,11 +982,10 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
 #undef PMSST_BDX
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
-    const dim3 gf(static_cast<unsigned>(m_tiles), static_cast<unsigned>(hb.NB));
     const bool fv4 = a.vec4;
-#define PMSST_FIN(FX, V4)                                                                                  \
-  hipLaunchKernelGGL((bs_dx_finish_kernel<T, FX, V4>), gf, dim3(256), 0, stream, tbuf, pn, inv_norm, pdot, \
-                     static_cast<T*>(dx), pitch, a)
+#define PMSST_FIN(FX, V4)                                                                                        \
+  hipLaunchKernelGGL((bs_dx_finish_kernel<T, FX, V4>), dim3(xg.blocks()), dim3(256), 0, stream, tbuf, pn, inv_norm, \
+                     pdot, static_cast<T*>(dx), pitch, max_ichunks, xg, a)
     if (from_x) {
       if (fv4) PMSST_FIN(true, true); else PMSST_FIN(true, false);
     } else {

@@ -444,35 +444,47 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
                         for r in range(4):
                             bnd.touch("workspace", (mtile * F + off + il + r) * 4, 4,
                                       ((lane & 15) == 0) & (il + r < I))
-        # -- finish: one block per (64 rows, band)
+        # -- finish: the dx kernel's blocks (band, 64-wide chunk, 64 rows)
         if norm:
             for band in range(nb):
                 off, I = int(offs[band]), int(widths[band])
                 nch = cdiv(I, 64)
-                nq = cdiv(I, 4)
-                for mtile in sorted({0, m_tiles - 1}):
-                    m0 = mtile * 64
-                    rv = min(M - m0, 64)
-                    r64 = np.arange(256)
-                    okr = r64 < rv
-                    for c in range(nch):
-                        bnd.touch("workspace", dgp + ((m0 + r64) * pitch + off // 64 + band + c) * 4, 4, okr)
-                    bnd.touch("inv_norm", ((m0 + r64) * nb + band) * 4, 4, okr)
-                    bnd.touch("lds_finish", np.minimum(r64, 63) * 4, 4, okr)
-                    q = np.arange(rv * nq)
-                    r, k = q // nq, (q % nq) * 4
-                    e = (m0 + r) * F + off + k
-                    bnd.touch("lds_finish", 64 * 4 + r * 4, 4)
-                    if vec4:
-                        bnd.touch("workspace", dgp + pdb + e * 4, 16)
-                        bnd.touch("x", e * esz, 4 * esz)
-                        bnd.touch("dx", e * esz, 4 * esz)
-                    else:
+                for ich in range(max_ich):
+                    i0 = ich * 64
+                    if i0 >= I:
+                        continue
+                    for mtile in sorted({0, m_tiles - 1}):
+                        m0 = mtile * 64
+                        rv = min(M - m0, 64)
+                        r, part = tid >> 2, tid & 3
+                        for c0 in range(4):
+                            for c in range(c0, nch, 4):
+                                ok = (r < rv) & (part == c0)
+                                bnd.touch("workspace", dgp + ((m0 + r) * pitch + off // 64 + band + c) * 4, 4, ok)
+                        okw = (part == 0) & (r < rv)
+                        bnd.touch("inv_norm", ((m0 + r) * nb + band) * 4, 4, okw)
+                        bnd.touch("lds_finish", r * 4, 4, okw)
+                        bnd.touch("lds_finish", 64 * 4 + r * 4, 4, okw)
+                        k = i0 + 4 * (tid & 15)
+                        live = k < I
                         for j in range(4):
-                            okj = k + j < I
-                            bnd.touch("workspace", dgp + pdb + (e + j) * 4, 4, okj)
-                            bnd.touch("x", (e + j) * esz, esz, okj)
-                            bnd.touch("dx", (e + j) * esz, esz, okj)
+                            rr = (tid >> 4) + 16 * j
+                            rc = np.where(rr < rv, rr, rv - 1)
+                            okr = live & (rr < rv)
+                            bnd.touch("lds_finish", np.minimum(rr, 63) * 4, 4, okr)
+                            bnd.touch("lds_finish", 64 * 4 + np.minimum(rr, 63) * 4, 4, okr)
+                            if vec4:
+                                e = (m0 + rc) * F + off + k
+                                bnd.touch("workspace", dgp + pdb + e * 4, 16, live)
+                                bnd.touch("x", e * esz, 4 * esz, live)
+                                bnd.touch("dx", ((m0 + rr) * F + off + k) * esz, 4 * esz, okr)
+                            else:
+                                e = (m0 + rr) * F + off + k
+                                for q in range(4):
+                                    okq = okr & (k + q < I)
+                                    bnd.touch("workspace", dgp + pdb + (e + q) * 4, 4, okq)
+                                    bnd.touch("x", (e + q) * esz, esz, okq)
+                                    bnd.touch("dx", (e + q) * esz, esz, okq)
     # -- dW
     dma = (not grouped) and esz == 2 and M >= 64 and vec4 and O % 8 == 0
     if dma:
