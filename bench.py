@@ -53,6 +53,7 @@ SINGLE_KERNEL_OPS = {
     "qk_norm_rotary_fwd": ("norm_rot_fwd_kernel", 2),
     "mask_hidden_fwd": ("bs_fwd_kernel", 1),
     "mask_final_fwd": ("me_fwd_dma_kernel", 1),
+    "mask_mlp_fwd": ("mlp_fwd_kernel", 1),
 }
 # bytes a 16-bit copy of this many elements reads (and writes): the counter calibration
 CALIB_ELEMS = 1 << 27
@@ -142,6 +143,10 @@ class Workload:
         def fin_fwd():
             st["fin"] = e.mask_estimator_final_forward_packed(st["hid"], w.w2, w.b2, w.dims)
 
+        def mlp_fwd():  # one pass; the hidden layer is written for the backward, as in training
+            out, pre, st["hid"] = e.mask_mlp_forward(w.h, w.w1, w.b1, w.w2, w.b2, w.dims, save_hidden=True)
+            st["fin"] = (out, pre)
+
         def fin_bwd():
             st["dz"] = e.mask_estimator_final_backward_packed(w.g_me, st["hid"], st["fin"][1], w.w2, w.dims,
                                                               input_activation="tanh")[0]
@@ -149,9 +154,12 @@ class Workload:
         def hid_bwd():
             e.grouped_linear_backward(st["dz"], w.h, w.w1, has_bias=True)
 
+        one_pass = (hasattr(e, "mask_mlp_forward") and w.dtype != w.torch.float32
+                    and e.mask_mlp_supported(w.dim, w.hidden, w.dims, w.dtype))
+        mask_fwd = ([("mask_mlp_fwd", mlp_fwd)] if one_pass
+                    else [("mask_hidden_fwd", hid_fwd), ("mask_final_fwd", fin_fwd)])
         return [("band_split_fwd", bs_fwd), ("band_split_bwd", bs_bwd), ("qk_norm_rotary_fwd", qk_fwd),
-                ("qk_norm_rotary_bwd", qk_bwd), ("mask_hidden_fwd", hid_fwd), ("mask_final_fwd", fin_fwd),
-                ("mask_final_bwd", fin_bwd), ("mask_hidden_bwd", hid_bwd)]
+                ("qk_norm_rotary_bwd", qk_bwd), *mask_fwd, ("mask_final_bwd", fin_bwd), ("mask_hidden_bwd", hid_bwd)]
 
     # --------------------------------------------------------------- algorithmic bytes / flops per op
     def traffic(self):
@@ -176,6 +184,9 @@ class Workload:
             # read h, W2, b2; write pre, out
             "mask_final_fwd": (M * NB * H * s + 2 * F * H * s + 2 * F * s + 2 * M * F * s + M * F * s,
                                2 * M * 2 * F * H),
+            # read x, W1, b1, W2, b2; write pre, out and (for the backward) h
+            "mask_mlp_fwd": (M * NB * O * s + NB * H * O * s + NB * H * s + 2 * F * H * s + 2 * F * s
+                             + 2 * M * F * s + M * F * s + M * NB * H * s, 2 * M * NB * O * H + 2 * M * 2 * F * H),
             # read g, pre, h, W2; write dz, dW2, db2
             "mask_final_bwd": (M * F * s + 2 * M * F * s + 2 * M * NB * H * s + 4 * F * H * s + 2 * F * s,
                                2 * 2 * M * 2 * F * H),
@@ -489,7 +500,7 @@ def main(argv=None) -> int:
     torch.cuda.empty_cache()
 
     # roofline of the dominant single kernel
-    single = {name: per_op[name]["ms"] / n for name, (_, n) in SINGLE_KERNEL_OPS.items()}
+    single = {name: per_op[name]["ms"] / n for name, (_, n) in SINGLE_KERNEL_OPS.items() if name in per_op}
     dom = max(single, key=single.get)
     kname, nlaunch = SINGLE_KERNEL_OPS[dom]
     launch_ms = single[dom]

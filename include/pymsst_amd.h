@@ -239,6 +239,28 @@ int pmsst_mask_estimator_final_backward(const void* grad_out, const void* x, con
                                         void* grad_weight, int input_activation, int dtype, void* workspace,
                                         size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------ whole mask MLP (depth 2)
+ * out = GLU(tanh(x_b W1_b^T + b1_b) W2_b^T + b2_b) for every band in one pass: x[rows, NB, dim],
+ * w1[NB, hidden, dim], b1[NB, hidden], w2 / b2 packed as for pmsst_mask_estimator_final_forward;
+ * writes pre[rows, 2F] and out[rows, F], and hidden_out[rows, NB, hidden] = tanh(...) only when
+ * hidden_out is not NULL.  The pre-activation and the tanh are rounded to the storage dtype as
+ * the reference's grouped Linear and inference_tanh do.  16-bit dtypes only.
+ */
+
+/* 1 when pmsst_mask_mlp_forward takes this shape: a 16-bit dtype, dim in {64, 128, 192, 256,
+ * 384, 512}, hidden a multiple of 32 in [64, 2048], every I_b a positive multiple of 4. */
+int pmsst_mask_mlp_supported(int64_t dim, int64_t hidden, const int64_t* dim_inputs, int64_t band_count, int dtype);
+/* Host copy of the table the forward reads tanh from: entries = 32768, out[b] = the correctly rounded
+ * tanh of the non-negative 16-bit pattern b of the dtype (bf16 or fp16).  No reference
+ * counterpart; it lets tests check the table on the CPU. */
+int pmsst_mask_mlp_tanh_table(int dtype, uint16_t* out, int64_t entries);
+/* Replaces the hidden-layer loop of fr.py:332-369 (grouped Linear .cu:1005-1030 + inference_tanh)
+ * followed by mask_estimator_final_forward (.cpp:589-622, .cu:2283-2310) for the depth-2 MLP. */
+int pmsst_mask_mlp_forward(const void* x, const void* w1, const void* b1, const void* w2, const void* b2,
+                           const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count, int64_t rows,
+                           int64_t dim, int64_t hidden, void* pre, void* out, void* hidden_out, int dtype,
+                           void* stream);
+
 /* ------------------------------------------------------------------ attention output gate
  * gate[m, h] = sigmoid(x[m] . W[h] + b[h]) stored in the tensor dtype; out[m, h*Dh + d] =
  * attn[m, h, d] * gate[m, h].  Rows m = b * seq + n.  attn is [batch, seq, heads, dim_head]

@@ -41,6 +41,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source flags on top of HIPCC_FLAGS.
+EXTRA_FLAGS: dict[str, list[str]] = {}
+
+
+def extra_flags(name: str) -> list[str]:
+    return list(EXTRA_FLAGS.get(name, []))
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and Path(cand).exists():
@@ -50,7 +58,7 @@ def hipcc() -> str:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra_flags(src.name), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -946,6 +946,45 @@ class HipFusedExtension:
         check(rc, "pmsst_mask_estimator_final_backward")
         return [dx, db, dw]
 
+    # ------------------------------------------------------------------ whole mask MLP
+
+    def mask_mlp_supported(self, dim, hidden, dim_inputs, dtype) -> bool:
+        """Whether :meth:`mask_mlp_forward` takes this shape and dtype."""
+        dims = tuple(int(d) for d in dim_inputs)
+        host = (ctypes.c_int64 * len(dims))(*dims)
+        code = dtype_code(dtype) if dtype in (torch.float32, torch.float16, torch.bfloat16) else -1
+        return bool(self._lib.pmsst_mask_mlp_supported(int(dim), int(hidden), host, len(dims), code))
+
+    def mask_mlp_forward(self, x, w1, b1, w2_all, b2, dim_inputs, save_hidden=False):
+        """Depth-2 mask MLP in one pass: ``x[M,NB,D]``, ``w1[NB,H,D]``, ``b1[NB,H]``, packed ``w2`` and
+        ``b2[2F]``.  Returns ``[out[M,F], pre[M,2F], hidden[M,NB,H] | None]`` (``hidden`` only with
+        ``save_hidden``)."""
+        _req(x.is_cuda and x.dim() == 3, "x must be a CUDA tensor of shape [M, NB, D]")
+        host, dev_offs, offs = self._bands(dim_inputs, x.device)
+        nb, total = len(offs) - 1, offs[-1]
+        _req(x.size(1) == nb, "x band count must match dim_inputs")
+        x = x.contiguous()
+        w1 = w1.contiguous()
+        b1 = b1.contiguous()
+        m, d = x.size(0), x.size(2)
+        hd = w1.size(1)
+        _req(tuple(w1.shape) == (nb, hd, d), "w1 must have shape [NB, H, D]")
+        _req(b1.numel() == nb * hd, "b1 must have NB * H elements")
+        _req(w2_all.numel() == 2 * total * hd, "w2 must hold the packed [2 I_b, H] weights")
+        _req(b2.numel() == 2 * total, "b2 must have 2F elements")
+        for t in (w1, b1, w2_all, b2):
+            _req(t.dtype == x.dtype and t.device == x.device, "parameters must match x in dtype and device")
+        pre = torch.empty((m, 2 * total), dtype=x.dtype, device=x.device)
+        out = torch.empty((m, total), dtype=x.dtype, device=x.device)
+        hid = torch.empty((m, nb, hd), dtype=x.dtype, device=x.device) if save_hidden else None
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_mask_mlp_forward(
+                _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2_all), _ptr(b2), _ptr(dev_offs), host, nb, m, d, hd, _ptr(pre),
+                _ptr(out), _ptr(hid), dtype_code(x.dtype), _stream(x.device),
+            )
+        check(rc, "pmsst_mask_mlp_forward")
+        return [out, pre, hid]
+
     def mask_estimator_final_forward(self, x, weights, bias, dim_inputs, dim_offsets):
         """``.cpp:589-622`` / ``.cpp:660-693`` (direct): ``x[M,NB,H]``, per-band ``weight[2*I_b, H]``,
         ``bias[2F]`` -> ``[out[M,F], pre[M,2F], x_contiguous]``."""

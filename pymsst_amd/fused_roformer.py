@@ -1097,16 +1097,29 @@ class _FusedMaskEstimatorFinal(torch.autograd.Function):
         return (res[0].reshape(ctx.input_shape), res[1], None, None, None, None, *res[2:])
 
 
+def _one_pass_mask_mlp(ext, x, w1, dim_inputs) -> bool:
+    """The depth-2 MLP forward runs as one kernel (16-bit, supported dim / hidden / widths)."""
+    return (hasattr(ext, "mask_mlp_forward") and x.dtype in (torch.float16, torch.bfloat16)
+            and ext.mask_mlp_supported(x.shape[-1], w1.shape[1], dim_inputs, x.dtype))
+
+
 class _FusedMaskMLP(torch.autograd.Function):
-    """Depth-2 mask MLP for all bands: hidden = tanh(x W1_b^T + b1_b) (tanh in the GEMM epilogue),
-    then the final per-band Linear + GLU.  The backward fuses tanh' = 1 - h^2 into the final
-    layer's dx epilogue and runs the hidden layer's backward on the grouped-linear kernels.
-    Saves x, h and pre (the tensors the stock autograd graph keeps)."""
+    """Depth-2 mask MLP for all bands: hidden = tanh(x W1_b^T + b1_b), then the final per-band Linear +
+    GLU, as one kernel in 16-bit (``mask_mlp_forward``; the hidden layer stays on chip unless the
+    backward needs it) or as the grouped linear with a tanh epilogue followed by the final layer.
+    The backward fuses tanh' = 1 - h^2 into the final layer's dx epilogue and runs the hidden
+    layer's backward on the grouped-linear kernels.  Saves x, h and pre (the tensors the stock
+    autograd graph keeps)."""
 
     @staticmethod
     def forward(ctx, x, w1, b1, w2, b2, extension, dim_inputs):
-        h = extension.grouped_linear_forward_act(x, w1, b1, activation="tanh")
-        out, pre = extension.mask_estimator_final_forward_packed(h, w2, b2, dim_inputs)
+        if _one_pass_mask_mlp(extension, x, w1, dim_inputs):
+            # one kernel; the hidden layer goes to HBM only when the backward needs it
+            out, pre, h = extension.mask_mlp_forward(x, w1, b1, w2, b2, dim_inputs,
+                                                     save_hidden=any(ctx.needs_input_grad[:5]))
+        else:
+            h = extension.grouped_linear_forward_act(x, w1, b1, activation="tanh")
+            out, pre = extension.mask_estimator_final_forward_packed(h, w2, b2, dim_inputs)
         ctx.save_for_backward(x, w1, h, pre, w2)
         ctx.extension = extension
         ctx.dim_inputs = dim_inputs

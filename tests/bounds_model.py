@@ -889,6 +889,119 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
     return bnd
 
 
+MLP_TILES = {64: (2, 4), 128: (4, 4), 192: (6, 4), 256: (8, 4), 384: (12, 2), 512: (16, 2)}
+
+
+def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True):
+    """mask_mlp.hip mlp_fwd_kernel (whole depth-2 mask MLP, 16-bit) on its band schedule: the b1 fill,
+    the x fragments, the W1 / W2 DMA ring, the LDS fragment reads, the hidden stores and the GLU
+    epilogue."""
+    nb, F = len(widths), int(sum(widths))
+    offs = _offs(widths)
+    DK, NT = MLP_TILES[D]
+    S, J = (2 if DK >= 12 else 3), 64
+    kStage = DK * 2048 + 2 * J * 64
+    sizes = {"x": M * nb * D * esz, "w1": nb * H * D * esz, "b1": nb * H * esz, "w2": 2 * F * H * esz,
+             "b2": 2 * F * esz, "pre": M * 2 * F * esz, "out": M * F * esz, "hid": M * nb * H * esz,
+             "offsets": (nb + 1) * 8, "lds": S * kStage, "sb1": 2048 * 4, "tanh": 2 * 32768 * 2,
+             "stab": 32768 * 2}
+    bnd = Bounds(sizes)
+    if S * kStage + 32768 * 2 + 2048 * 4 > 160 * 1024:
+        bnd.fail("mlp_fwd: more than 160 KB of LDS")
+    if H > 2048 or H % 32 or any(w % 4 for w in widths):
+        bnd.fail("mask_mlp: shape outside the host check")
+        return bnd
+    wave_rows = 16 * NT
+    mtiles = cdiv(M, 4 * wave_rows)
+    units = lambda b: cdiv(widths[b], J)  # noqa: E731
+    sc = build_band_sched(nb, mtiles, units)
+    decoded = sched_decode(sc, nb, units, True, bnd, "mlp_fwd")
+    tid = np.arange(256)
+    lane = tid & 63
+    g, rr = lane >> 4, lane & 15
+    u = (lane & 3) ^ swz_k(lane >> 2)
+    nc = H // 32
+    kmax_pw = (2 * DK + 8 + 3) // 4
+    for band, mt, pss in sorted({(b, m, p) for b, m, p in decoded if m in (0, mtiles - 1)}):
+        off, I = int(offs[band]), int(widths[band])
+        j0 = pss * J
+        for i0 in range(0, H, 256):
+            i = i0 + tid
+            bnd.touch("b1", (band * H + i) * esz, esz, i < H)
+            bnd.touch("sb1", i * 4, 4, i < H)
+        for k in range(64):  # tanh table: 64 DMAs of 1 KB (wave k % 4), bf16 table first
+            bnd.touch("tanh", k * 1024 + lane * 16, 16)
+            bnd.touch("stab", k * 1024 + lane * 16, 16)
+        bnd.touch("stab", np.array([0, 0x7FFF]) * 2, 2)  # table reads: index = pattern & 0x7fff
+        nv2 = min(4, cdiv(I - j0, 16))
+        ntot = 2 * DK + 2 * nv2
+        for wave in range(4):
+            npw = (ntot - wave + 3) // 4
+            if npw > kmax_pw:
+                bnd.fail("mlp_fwd: more DMA instructions than the plan holds")
+            for q in range(npw):
+                k = wave + 4 * q
+                if k < 2 * DK:
+                    r = 16 * (k & 1) + (lane >> 2)
+                    gsrc = (r * D + 32 * (k >> 1) + 8 * u) * 2
+                    ldst = (k >> 1) * 2048 + (k & 1) * 1024
+                    base, stride, buf = band * H * D * esz, 64 * D, "w1"
+                else:
+                    k2 = k - 2 * DK
+                    half, grp = k2 // nv2, k2 % nv2
+                    jr = j0 + 16 * grp + (lane >> 2)
+                    jc = np.minimum(jr, I - 1)
+                    prow = I + jc if half else jc
+                    gsrc = (prow * H + 8 * u) * 2
+                    ldst = DK * 2048 + (4 * half + grp) * 1024
+                    base, stride, buf = 2 * off * H * esz, 64, "w2"
+                    if ldst + 1024 > kStage:
+                        bnd.fail("mlp_fwd: W2 group outside the stage")
+                if np.any(gsrc + (nc - 1) * stride >= 1 << 32):
+                    bnd.fail("mlp_fwd: 32-bit DMA offset overflows")
+                for c in steps(nc):
+                    bnd.touch(buf, base + gsrc + c * stride, 16)
+                for stage in range(S):
+                    bnd.touch("lds", stage * kStage + ldst + lane * 16, 16)
+            wrow0 = mt * 4 * wave_rows + wave * wave_rows
+            left = M - wrow0
+            nvt = 0 if left <= 0 else (NT if left >= wave_rows else cdiv(left, 16))
+            for n in range(NT):
+                m = np.minimum(wrow0 + 16 * n + rr, M - 1)
+                for s_ in range(DK):
+                    bnd.touch("x", ((m * nb + band) * D + 8 * g + 32 * s_) * esz, 16)
+            if nvt == 0:
+                continue
+            for stage in range(S):
+                sb = stage * kStage
+                for t in range(2):
+                    r = 8 * (rr >> 2) + 4 * t + (rr & 3)
+                    a1 = r * 64 + 16 * (g ^ swz_k(r & 15))
+                    for s_ in range(DK):
+                        bnd.touch("lds", sb + a1 + 2048 * s_, 16)
+                a2 = DK * 2048 + rr * 64 + 16 * (g ^ swz_k(rr))
+                for t in range(8):  # all 8 GEMM2 row tiles are read
+                    bnd.touch("lds", sb + a2 + 1024 * t, 16)
+            for c in steps(nc):
+                bnd.touch("sb1", (32 * c + 8 * g) * 4, 32)
+                if write_h:
+                    for n in range(NT):
+                        m = wrow0 + 16 * n + rr
+                        bnd.touch("hid", ((m * nb + band) * H + 32 * c + 8 * g) * esz, 16, (n < nvt) & (m < M))
+            for t in range(4):
+                j = j0 + 16 * t + 4 * g
+                okj = (t < nv2) & (j < I)
+                bnd.touch("b2", (2 * off + j) * esz, 4 * esz, okj)
+                bnd.touch("b2", (2 * off + I + j) * esz, 4 * esz, okj)
+                for n in range(NT):
+                    m = wrow0 + 16 * n + rr
+                    ok = okj & (n < nvt) & (m < M)
+                    bnd.touch("pre", (m * 2 * F + 2 * off + j) * esz, 4 * esz, ok)
+                    bnd.touch("pre", (m * 2 * F + 2 * off + I + j) * esz, 4 * esz, ok)
+                    bnd.touch("out", (m * F + off + j) * esz, 4 * esz, ok)
+    return bnd
+
+
 def _replay_me_fwd_reg(bnd, widths, offs, M, H, esz, vec4):
     """mask_estimator.hip me_fwd_kernel: (band, 64 GLU outputs) groups x 128-row tiles; A = 64 left and
     64 gate rows of W_b (LeftGateLoader row map), B = x rows; epilogue stores pre and out."""
@@ -1227,6 +1340,8 @@ def all_replays(name: str, esz: int):
     yield "grouped_linear_bwd", replay_band_split_backward([dim] * nb, M, hidden, esz, grouped=True)
     yield "mask_final_fwd", replay_mask_final_forward(widths, M, hidden, esz)
     yield "mask_final_bwd", replay_mask_final_backward(widths, M, hidden, esz, tanh_in=True)
+    if esz == 2:
+        yield "mask_mlp_fwd", replay_mask_mlp_forward(widths, M, dim, hidden, esz)
     yield "rms_norm", replay_rms_norm(M * nb, dim, esz)
     for shape in qk:
         yield f"attention_gate{list(shape)}", replay_attention_gate(shape[0], shape[1], shape[2], shape[3], dim, esz)
