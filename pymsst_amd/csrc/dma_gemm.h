@@ -232,6 +232,35 @@ inline bool build_band_sched(int NB, int64_t m_tiles, UnitsOf units, CostOf cost
   return true;
 }
 
+// Equal-cost blocks split evenly: XCD x takes canonical blocks [x total / 8, (x + 1) total / 8), so a
+// (band, row tile) unit may straddle two XCDs.  For kernels whose blocks all cost about the same,
+// where whole-unit ranges would leave some XCDs with a round of blocks more than others.
+template <class UnitsOf>
+inline bool build_even_sched(int NB, int64_t m_tiles, UnitsOf units, BandSched* sc, uint32_t* per_xcd) {
+  sc->m_tiles = 0;
+  if (NB > kSchedMaxBands || m_tiles <= 0) return false;
+  int64_t total = 0;
+  sc->cumb[0] = 0;
+  for (int b = 0; b < NB; ++b) {
+    total += units(b) * m_tiles;
+    if (total >= (int64_t{1} << 31)) return false;
+    sc->cumb[b + 1] = static_cast<uint32_t>(total);
+  }
+  uint32_t mx = 0;
+  int b = 0;
+  for (uint32_t x = 0; x <= kXcds; ++x) {
+    sc->gs[x] = static_cast<uint32_t>(total * x / kXcds);
+    if (x < kXcds) {
+      while (b < NB - 1 && sc->cumb[b + 1] <= sc->gs[x]) ++b;
+      sc->bstart[x] = static_cast<uint32_t>(b);
+    }
+    if (x > 0) mx = sc->gs[x] - sc->gs[x - 1] > mx ? sc->gs[x] - sc->gs[x - 1] : mx;
+  }
+  sc->m_tiles = static_cast<uint32_t>(m_tiles);
+  *per_xcd = mx;
+  return true;
+}
+
 // Equal-cost blocks.
 template <class UnitsOf>
 inline bool build_band_sched(int NB, int64_t m_tiles, UnitsOf units, BandSched* sc, uint32_t* per_xcd) {

@@ -450,14 +450,10 @@ int launch_dk(const void* x, const void* w1, const void* b1, const void* w2, con
   BandSched sc;
   uint32_t per_xcd = 0;
   const int64_t rows_per_block = 64 * NT;
-  if (!build_band_sched(
-          a.NB, (a.M + rows_per_block - 1) / rows_per_block,
-          [&](int b) { return (dim_inputs[b] + kMlpJ - 1) / kMlpJ; },
-          [&](int b) {  // MFMAs per chunk and wave: GEMM1 2 DK NT, GEMM2 2 nv2 NT
-            const int64_t nv2 = dim_inputs[b] >= kMlpJ ? 4 : (dim_inputs[b] + 15) / 16;
-            return (2 * DK + 2 * nv2) * NT;
-          },
-          &sc, &per_xcd))
+  // every block runs all H / 32 chunks with the same MFMA count: an even split of the blocks over the
+  // XCDs (units of one band stay contiguous, so its weight chunks are shared in one L2 but at the seams)
+  if (!build_even_sched(a.NB, (a.M + rows_per_block - 1) / rows_per_block,
+                        [&](int b) { return (dim_inputs[b] + kMlpJ - 1) / kMlpJ; }, &sc, &per_xcd))
     return fail(PMSST_EINVAL, "mask_mlp_forward: too many bands or rows for the block schedule");
   const dim3 grid(per_xcd * kXcds);
   const T* xp = static_cast<const T*>(x);

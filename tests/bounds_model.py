@@ -179,6 +179,25 @@ def build_band_sched(nb: int, m_tiles: int, units, cost=lambda b: 1):
     return BandSched(gs, cumb, bstart, m_tiles, per_xcd)
 
 
+def build_even_sched(nb: int, m_tiles: int, units):
+    """dma_gemm.h build_even_sched: canonical blocks split evenly over the XCDs."""
+    if nb > 256 or m_tiles <= 0:
+        return None
+    cumb = [0]
+    for b in range(nb):
+        cumb.append(cumb[-1] + int(units(b)) * m_tiles)
+    total = cumb[-1]
+    gs = [total * x // XCDS for x in range(XCDS + 1)]
+    bstart = []
+    b = 0
+    for x in range(XCDS):
+        while b < nb - 1 and cumb[b + 1] <= gs[x]:
+            b += 1
+        bstart.append(b)
+    per_xcd = max(gs[x + 1] - gs[x] for x in range(XCDS))
+    return BandSched(gs, cumb, bstart, m_tiles, per_xcd)
+
+
 def sched_decode(sc: BandSched, nb: int, units, last_first: bool, bnd: Bounds, what: str):
     """dma_gemm.h sched_block over every block of the grid; checks that the units are covered once
     and that the forward band search starting at bstart finds each block's band."""
@@ -914,7 +933,7 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True):
     wave_rows = 16 * NT
     mtiles = cdiv(M, 4 * wave_rows)
     units = lambda b: cdiv(widths[b], J)  # noqa: E731
-    sc = build_band_sched(nb, mtiles, units)
+    sc = build_even_sched(nb, mtiles, units)
     decoded = sched_decode(sc, nb, units, True, bnd, "mlp_fwd")
     tid = np.arange(256)
     lane = tid & 63
