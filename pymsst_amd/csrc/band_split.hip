@@ -27,6 +27,7 @@
 #include "common.h"
 #include "dma_gemm.h"
 #include "gemm.h"
+#include "grouped_dx.h"
 #include "rowgeom.h"
 
 #include <vector>
@@ -1058,7 +1059,12 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
   const T* pdy = static_cast<const T*>(dy);
   const T* px = static_cast<const T*>(x);
   const T* pw = static_cast<const T*>(weight);
-  if (M > 0) {
+  if (M > 0 && grouped_dx_supported(hb.NB, hb.max_width, O, M, sizeof(T), dy, weight, dx)) {
+    if constexpr (sizeof(T) == 2) {
+      const int rc = launch_grouped_dx<T>(dy, weight, dx, hb.NB, hb.max_width, O, M, stream);
+      if (rc != PMSST_OK) return rc;
+    }
+  } else if (M > 0) {
     const int max_ichunks = (hb.max_width + 63) / 64;
     const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_ichunks), static_cast<uint32_t>((M + kBM - 1) / kBM)};
     const dim3 grid(xg.blocks());
@@ -1071,7 +1077,12 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }
-  {
+  if (uniform_dw_supported(hb.NB, hb.max_width, O, M, sizeof(T), dy, x, dw)) {
+    if constexpr (sizeof(T) == 2) {
+      const int rc = launch_uniform_dw<T>(dy, x, dw, db, hb.NB, hb.max_width, O, M, stream);
+      if (rc != PMSST_OK) return rc;
+    }
+  } else {
     const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
     const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_itiles), static_cast<uint32_t>((O + kDwBO - 1) / kDwBO)};
     const dim3 grid(xg.blocks());

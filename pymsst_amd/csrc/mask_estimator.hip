@@ -28,6 +28,7 @@
 #include "dma_gemm.h"
 #include "gemm.h"
 #include "rowgeom.h"
+#include "grouped_dx.h"
 
 namespace pmsst {
 namespace {
@@ -39,6 +40,7 @@ struct MaskArgs {
   int H;
   int F;
   bool vec4;  // every I_b and H a multiple of 4 and all tensors 4-element aligned
+  int uniform_I = 0;  // > 0: every band has I_b = uniform_I (offsets unused; the dW kernel only)
 };
 
 __device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + __expf(-z)); }
@@ -816,7 +818,7 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
                                                            MaskArgs a) {
   constexpr int S = HT == 128 ? PMSST_ME_DW_STAGES : PMSST_ME_DW256_STAGES;
   static_assert(S >= 3 && S <= 8, "stages");
-  static_assert(HT == 128 || HT == 256, "hidden columns per block");
+  static_assert(HT == 64 || HT == 128 || HT == 256, "hidden columns per block");
   constexpr int NW = HT / 32;              // waves: (HT / 64) x 2
   constexpr int kU = HT / 8;               // 16-byte units per x K-row
   constexpr int kXTile = kChunkK * HT * 2;  // x tile bytes; the dpre tile (32 K-rows x 128 j) follows
@@ -830,8 +832,8 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
   const int htiles = H / HT;
   const int h0 = static_cast<int>(sub % htiles) * HT;
   const int j0 = static_cast<int>(sub / htiles) * kDwT;
-  const int off = static_cast<int>(a.offsets[band]);
-  const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  const int off = a.uniform_I > 0 ? band * a.uniform_I : static_cast<int>(a.offsets[band]);
+  const int I = a.uniform_I > 0 ? a.uniform_I : static_cast<int>(a.offsets[band + 1]) - off;
   const int K2 = 2 * I;
   const int M = static_cast<int>(a.M);
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
@@ -895,7 +897,7 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // dbias = ones^T dpre: the two waves of the first hidden tile's first 64 columns also multiply
   // their dpre fragments by an all-ones A fragment (every row of the product is the column sum)
-  const bool do_bias = h0 == 0 && wr == 0;
+  const bool do_bias = h0 == 0 && wr == 0 && dbias != nullptr;
   const uint32_t one2 = std::is_same<T, bf16>::value ? 0x3F803F80u : 0x3C003C00u;
   const u32x4_t ones{one2, one2, one2, one2};
   f32x4_t accb[4];
@@ -1184,6 +1186,26 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
   return PMSST_OK;
 }
 
+template <typename T>
+int launch_uniform_dw_impl(const void* dy, const void* x, void* dw, void* db, int64_t groups, int64_t in_features,
+                           int64_t out_features, int64_t rows, hipStream_t stream) {
+  // dW_g[o][i] = sum_m dy[m][g][o] x[m][g][i] on me_bwd_dw_dma_kernel: dy plays dpre (bands of
+  // uniform width 2 I_b = out_features), x plays the hidden activations (H = in_features)
+  const int I = static_cast<int>(out_features / 2);
+  MaskArgs a{nullptr, rows, static_cast<int>(groups), static_cast<int>(in_features), static_cast<int>(groups) * I,
+             true, I};
+  BandSched wsc;
+  uint32_t per_xcd = 0;
+  const int64_t htl = in_features / 64;
+  if (!build_band_sched(static_cast<int>(groups), 1,
+                        [&](int) { return htl * ((out_features + kDwT - 1) / kDwT); }, &wsc, &per_xcd))
+    return fail(PMSST_EINVAL, "grouped_linear_backward: too many groups for the dW schedule");
+  hipLaunchKernelGGL((me_bwd_dw_dma_kernel<T, 64>), dim3(per_xcd * kXcds), dim3(128), 0, stream,
+                     static_cast<const T*>(dy), static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(db),
+                     wsc, a);
+  return check_launch("me_bwd_dw_dma_kernel");
+}
+
 template <typename F>
 int with_dtype(int dtype, const char* op, F&& f) {
   switch (dtype) {
@@ -1195,6 +1217,25 @@ int with_dtype(int dtype, const char* op, F&& f) {
 }
 
 }  // namespace
+
+bool uniform_dw_supported(int64_t groups, int64_t in_features, int64_t out_features, int64_t rows, size_t elem,
+                          const void* dy, const void* x, const void* dw) {
+  return elem == 2 && rows >= kChunkK && in_features % 64 == 0 && in_features > 0 && out_features % 8 == 0 &&
+         out_features >= 8 && groups > 0 && groups <= kSchedMaxBands && al(dy, 16) && al(x, 16) && al(dw, 16) &&
+         (static_cast<int64_t>(kChunkK) * groups * in_features + in_features) * 2 < (int64_t{1} << 31) &&
+         (static_cast<int64_t>(kChunkK) * groups * out_features + groups * out_features) * 2 < (int64_t{1} << 31);
+}
+
+template <typename T>
+int launch_uniform_dw(const void* dy, const void* x, void* dw, void* db, int64_t groups, int64_t in_features,
+                      int64_t out_features, int64_t rows, hipStream_t stream) {
+  return launch_uniform_dw_impl<T>(dy, x, dw, db, groups, in_features, out_features, rows, stream);
+}
+template int launch_uniform_dw<bf16>(const void*, const void*, void*, void*, int64_t, int64_t, int64_t, int64_t,
+                                     hipStream_t);
+template int launch_uniform_dw<f16>(const void*, const void*, void*, void*, int64_t, int64_t, int64_t, int64_t,
+                                    hipStream_t);
+
 }  // namespace pmsst
 
 using namespace pmsst;

@@ -410,10 +410,17 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
     tid = np.arange(GEMM_THREADS)
     lane, wave = tid & 63, tid >> 6
     norm = not grouped
+    # -- dx of the grouped linear on grouped_dx.hip (16-bit, uniform supported widths)
+    if grouped and esz == 2 and M > 0 and len(set(widths)) == 1 and widths[0] in GDX_TILES and O % 32 == 0 \
+            and O >= 64:
+        _replay_glin_dx(bnd, nb, widths[0], O, M)
+        M_dx = 0  # the register-path dx kernel below does not run
+    else:
+        M_dx = M
     # -- dx (one block per (band, 64-wide input chunk, 64 rows))
     max_ich = cdiv(max(widths), 64)
     sizes["lds"] = gemm_lds_bytes(esz, 64, 64) + 64 * 4 + 4 * 64 * 4
-    if M > 0:
+    if M_dx > 0:
         grp, mt, valid = xcd_decode(nb * max_ich, m_tiles)
         if np.any(mt[valid] >= m_tiles):
             bnd.fail("dx: member out of range")
@@ -506,14 +513,84 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
                                     bnd.touch("dx", (e + q) * esz, esz, okq)
     # -- dW
     dma = (not grouped) and esz == 2 and M >= 64 and vec4 and O % 8 == 0
+    uniform_dw = grouped and esz == 2 and M >= CHUNK_K and len(set(widths)) == 1 and widths[0] % 64 == 0 \
+        and O % 8 == 0
     if dma:
         _replay_bs_dw_dma(bnd, widths, offs, M, O, esz, has_bias)
+    elif uniform_dw:  # the mask-estimator DMA dW kernel with HT = 64 on bands of width 2 I_b = O
+        _replay_me_dw_dma(bnd, [O // 2] * nb, _offs([O // 2] * nb), M, widths[0], esz, 64, "dy", "x", "dw",
+                          "db" if has_bias else None, "lds_dw")
     else:
         _replay_bs_dw_reg(bnd, widths, offs, M, O, esz, has_bias, norm, vec4 and ovec4)
     if norm:
         # col_sum_kernel over the m_tiles x F partials -> dgamma
         _replay_col_sum(bnd, "workspace", m_tiles, F, "dgamma", esz)
     return bnd
+
+
+GDX_TILES = {64: (4, 4), 128: (8, 4), 192: (12, 2), 256: (16, 2)}
+
+
+def _replay_glin_dx(bnd, G, I, O, M):
+    """grouped_dx.hip glin_dx_kernel: the DMA ring of weight slabs and dy tiles, the transposed weight
+    fragments, the dy B fragments and the dx stores, on the even block schedule."""
+    DT, NT = GDX_TILES[I]
+    S, kUnits, kSlab = 4, I // 8, 32 * 2 * I
+    kInstr = kSlab // 1024
+    wave_rows = 16 * NT
+    kStage = kSlab + 4 * wave_rows * 64
+    bnd.sizes["lds_gdx"] = S * kStage
+    if S * kStage > 160 * 1024:
+        bnd.fail("glin_dx: more than 160 KB of LDS")
+    mtiles = cdiv(M, 4 * wave_rows)
+    units = lambda b: 1  # noqa: E731
+    sc = build_even_sched(G, mtiles, units)
+    decoded = sched_decode(sc, G, units, True, bnd, "glin_dx")
+    lane = np.arange(64)
+    gq, rr = lane >> 4, lane & 15
+    nc = O // 32
+    for g, mt, _ in sorted({(b, m, s_) for b, m, s_ in decoded if m in (0, mtiles - 1)}):
+        for wave in range(4):
+            npw = (kInstr - wave + 3) // 4
+            for q in range(npw):
+                t = wave + 4 * q
+                P = 64 * t + lane
+                kr, pu = P // kUnits, P % kUnits
+                u = pu ^ swz_mn(kr)
+                if np.any(u >= kUnits):
+                    bnd.fail("glin_dx: swizzled unit leaves its row")
+                for c in steps(nc):
+                    bnd.touch("weight", g * O * I * 2 + ((32 * c + kr) * I + 8 * u) * 2, 16)
+                for stage in range(S):
+                    bnd.touch("lds_gdx", stage * kStage + t * 1024 + lane * 16, 16)
+            wrow0 = mt * 4 * wave_rows + wave * wave_rows
+            left = M - wrow0
+            nvt = 0 if left <= 0 else (NT if left >= wave_rows else cdiv(left, 16))
+            u = (lane & 3) ^ swz_k(lane >> 2)
+            for n in range(nvt):
+                m = np.minimum(wrow0 + 16 * n + (lane >> 2), M - 1)
+                for c in steps(nc):
+                    bnd.touch("dy", ((m * G + g) * O + 8 * u + 32 * c) * 2, 16)
+                for stage in range(S):
+                    bnd.touch("lds_gdx", stage * kStage + kSlab + (wave * NT + n) * 1024 + lane * 16, 16)
+            if nvt == 0:
+                continue
+            jq = lane & 15
+            kr0 = 8 * gq + (jq >> 2)
+            for stage in range(S):
+                base = stage * kStage
+                for d in range(DT):
+                    col = 16 * d + 4 * (jq & 3)
+                    off = kr0 * 2 * I + 16 * ((col >> 3) ^ swz_mn(kr0)) + 2 * (col & 7)
+                    bnd.touch("lds_gdx", base + off, 8)
+                    bnd.touch("lds_gdx", base + off + 4 * 2 * I, 8)
+                for n in range(NT):
+                    bnd.touch("lds_gdx", base + kSlab + wave * NT * 1024 + rr * 64 + 16 * (gq ^ swz_k(rr)) + n * 1024, 16)
+            for n in range(NT):
+                m = wrow0 + 16 * n + rr
+                ok = (n < nvt) & (m < M)
+                for d in range(DT):
+                    bnd.touch("dx", ((m * G + g) * I + 4 * gq + 16 * d) * 2, 8, ok)
 
 
 def _replay_col_sum(bnd, pbuf, parts, dim, obuf, osz, poff=0):
@@ -732,6 +809,75 @@ def replay_mask_final_forward(widths, M, H, esz):
     return bnd
 
 
+def _replay_me_dw_dma(bnd, widths, offs, M, H, esz, HT, dpre_buf, x_buf, dw_buf, db_buf, lds_buf):
+    """mask_estimator.hip me_bwd_dw_dma_kernel<T, HT> (HT hidden columns x 128 j per block, HT / 32
+    waves) on its band schedule, over a dpre-like buffer of row pitch 2 F."""
+    nb, F = len(widths), int(sum(widths))
+    kDwT, S2 = 128, 3
+    NW2 = HT // 32
+    kU2 = HT // 8
+    kXTile = CHUNK_K * HT * 2
+    kStage2 = kXTile + 8192
+    kDI2 = 8 // NW2
+    bnd.sizes[lds_buf] = max(bnd.sizes.get(lds_buf, 0), S2 * kStage2)
+    htl = H // HT
+    units2 = lambda b: htl * cdiv(2 * widths[b], kDwT)  # noqa: E731
+    sc2 = build_band_sched(nb, 1, units2)
+    decoded2 = sched_decode(sc2, nb, units2, False, bnd, "me_bwd_dw_dma")
+    tid = np.arange(NW2 * 64)
+    lane, wave = tid & 63, tid >> 6
+    wr, wc = wave >> 1, wave & 1
+    nk = cdiv(M, CHUNK_K)
+    kbeg = M - nk * CHUNK_K
+    xstride = nb * H
+    for band, _mt, sub in sorted(set(decoded2)):
+        off, I = int(offs[band]), int(widths[band])
+        K2 = 2 * I
+        h0 = (sub % htl) * HT
+        j0 = (sub // htl) * kDwT
+        for c in steps(nk):
+            st = (c % S2) * kStage2
+            for t in range(2):
+                kr = (64 // kU2) * (wave + NW2 * t) + lane // kU2
+                uu = (lane % kU2) ^ swz_mn(kr)
+                row = kbeg + c * CHUNK_K + kr
+                row = np.where((c == 0) & (row < 0), 0, row)
+                bnd.touch(x_buf, (row * xstride + band * H + h0 + 8 * uu) * esz, 16)
+                bnd.touch(lds_buf, st + (wave + NW2 * t) * 1024 + 16 * lane, 16)
+            for t in range(kDI2):
+                kr = 4 * (wave + NW2 * t) + (lane >> 4)
+                uu = (lane & 15) ^ swz_mn(kr)
+                jc = np.minimum(j0 + 8 * uu, K2 - 8)
+                row = kbeg + c * CHUNK_K + kr
+                row = np.where((c == 0) & (row < 0), 0, row)
+                bnd.touch(dpre_buf, (row * 2 * F + 2 * off + jc) * esz, 16)
+                bnd.touch(lds_buf, st + kXTile + (wave + NW2 * t) * 1024 + 16 * lane, 16)
+            for i in range(4):
+                fa = frag_mn_addr(0, 64 * wr + 16 * i, 2 * HT, lane) + st
+                fb = frag_mn_addr(kXTile, 64 * wc + 16 * i, 2 * kDwT, lane) + st
+                for a_, p in ((fa, 2 * HT), (fb, 2 * kDwT)):
+                    bnd.touch(lds_buf, a_, 8)
+                    bnd.touch(lds_buf, a_ + 4 * p, 8)
+        jv = min(K2 - j0, kDwT)
+        if db_buf is not None:
+            for j in range(4):
+                jj = 64 * wc + 16 * j + lane
+                bnd.touch(db_buf, (2 * off + j0 + jj) * esz, esz, (h0 == 0) & (wr == 0) & (lane < 16) & (jj < jv))
+        kop = HT + 8
+        if kDwT * kop * 2 > S2 * kStage2:
+            bnd.fail("me_bwd_dw_dma: staging tile larger than the ring")
+        for j in range(4):
+            jj = 64 * wc + 16 * j + (lane & 15)
+            for i in range(4):
+                bnd.touch(lds_buf, (jj * kop + 64 * wr + 16 * i + 4 * (lane >> 4)) * esz, 4 * esz)
+        c8 = (tid % kU2) * 8
+        for p in range(kDwT // 16):
+            jj = tid // kU2 + 16 * p
+            ok = jj < jv
+            bnd.touch(lds_buf, (jj * kop + c8) * esz, 16, ok)
+            bnd.touch(dw_buf, ((2 * off + j0 + jj) * H + h0 + c8) * esz, 16, ok)
+
+
 def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
     """mask_estimator.hip launch_me_bwd: me_dpre_flat_kernel, me_bwd_dx_dma_kernel (HC = 256 when
     H % 256 == 0, else 128), me_bwd_dw_dma_kernel (HT = 128)."""
@@ -843,67 +989,8 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
             bnd.touch("lds", (row * kop + c8) * esz, 16, ok)
             bnd.touch("dx", (((m0 + row) * nb + band) * H + hc * HC + c8) * esz, 16, ok)
     # -- dW on the DMA ring
-    HT, kDwT = 128, 128
-    S2 = 3
-    NW2 = HT // 32
-    kU2 = HT // 8
-    kXTile = CHUNK_K * HT * 2
-    kStage2 = kXTile + 8192
-    kDI2 = 8 // NW2
-    bnd.sizes["lds"] = max(bnd.sizes["lds"], S2 * kStage2)
-    htl = H // HT
-    units2 = lambda b: htl * cdiv(2 * widths[b], kDwT)  # noqa: E731
-    sc2 = build_band_sched(nb, 1, units2)
-    decoded2 = sched_decode(sc2, nb, units2, False, bnd, "me_bwd_dw_dma")
-    tid = np.arange(NW2 * 64)
-    lane, wave = tid & 63, tid >> 6
-    wr, wc = wave >> 1, wave & 1
-    nk = cdiv(M, CHUNK_K)
-    kbeg = M - nk * CHUNK_K
-    xstride = nb * H
-    for band, _mt, sub in sorted(set(decoded2) if dma_dw else ()):
-        off, I = int(offs[band]), int(widths[band])
-        K2 = 2 * I
-        h0 = (sub % htl) * HT
-        j0 = (sub // htl) * kDwT
-        for c in steps(nk):
-            st = (c % S2) * kStage2
-            for t in range(2):
-                kr = (64 // kU2) * (wave + NW2 * t) + lane // kU2
-                uu = (lane % kU2) ^ swz_mn(kr)
-                row = kbeg + c * CHUNK_K + kr
-                row = np.where((c == 0) & (row < 0), 0, row)
-                bnd.touch("x", (row * xstride + band * H + h0 + 8 * uu) * esz, 16)
-                bnd.touch("lds", st + (wave + NW2 * t) * 1024 + 16 * lane, 16)
-            for t in range(kDI2):
-                kr = 4 * (wave + NW2 * t) + (lane >> 4)
-                uu = (lane & 15) ^ swz_mn(kr)
-                jc = np.minimum(j0 + 8 * uu, K2 - 8)
-                row = kbeg + c * CHUNK_K + kr
-                row = np.where((c == 0) & (row < 0), 0, row)
-                bnd.touch("workspace", (row * 2 * F + 2 * off + jc) * esz, 16)
-                bnd.touch("lds", st + kXTile + (wave + NW2 * t) * 1024 + 16 * lane, 16)
-            for i in range(4):
-                fa = frag_mn_addr(0, 64 * wr + 16 * i, 2 * HT, lane) + st
-                fb = frag_mn_addr(kXTile, 64 * wc + 16 * i, 2 * kDwT, lane) + st
-                for a, p in ((fa, 2 * HT), (fb, 2 * kDwT)):
-                    bnd.touch("lds", a, 8)
-                    bnd.touch("lds", a + 4 * p, 8)
-        jv = min(K2 - j0, kDwT)
-        for j in range(4):
-            jj = 64 * wc + 16 * j + lane
-            bnd.touch("dbias", (2 * off + j0 + jj) * esz, esz, (h0 == 0) & (wr == 0) & (lane < 16) & (jj < jv))
-        kop = HT + 8
-        for j in range(4):
-            jj = 64 * wc + 16 * j + (lane & 15)
-            for i in range(4):
-                bnd.touch("lds", (jj * kop + 64 * wr + 16 * i + 4 * (lane >> 4)) * esz, 4 * esz)
-        c8 = (tid % kU2) * 8
-        for p in range(kDwT // 16):
-            jj = tid // kU2 + 16 * p
-            ok = jj < jv
-            bnd.touch("lds", (jj * kop + c8) * esz, 16, ok)
-            bnd.touch("dw", ((2 * off + j0 + jj) * H + h0 + c8) * esz, 16, ok)
+    if dma_dw:
+        _replay_me_dw_dma(bnd, widths, offs, M, H, esz, 128, "workspace", "x", "dw", "dbias", "lds")
     bnd.touch("offsets", np.arange(nb + 1) * 8, 8)
     return bnd
 

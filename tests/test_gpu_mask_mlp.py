@@ -81,3 +81,26 @@ def test_mask_mlp_forward_matches_two_kernel_path(hip_ext):
     diff = (hid.float() - h2.float()).abs()
     assert (diff <= h2.float().abs() * 2.0**-6 + 1e-6).all()
     assert (diff > 0).float().mean().item() < 1e-3
+
+
+@pytest.mark.parametrize("m,groups,i,o,dtype", [
+    (1032, 62, 192, 768, torch.bfloat16),
+    (77, 5, 128, 96, torch.float16),
+    (300, 7, 256, 64, torch.bfloat16),
+    (1, 3, 192, 768, torch.bfloat16),
+    (257, 9, 64, 256, torch.float16),
+])
+def test_grouped_dx_register_kernel_vs_oracle(hip_ext, m, groups, i, o, dtype):
+    """The grouped linear's input gradient on glin_dx_kernel (16-bit, in_features 64-256): full and
+    partial row tiles, a single row, and the mask MLP's configs[1] hidden layer."""
+    dn = dt_name(dtype)
+    print(f"grouped dx m={m} groups={groups} i={i} o={o} {dn}", flush=True)
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(m, groups, i, generator=g).to(dtype).cuda()
+    w = (torch.randn(groups, o, i, generator=g) / o**0.5).to(dtype).cuda()
+    dy = torch.randn(m, groups, o, generator=g).to(dtype).cuda()
+    dx, dw, db = hip_ext.grouped_linear_backward(dy, x, w, True)
+    rdx, rdw, rdb = oracle.grouped_linear_backward(to_np(dy), to_np(x), to_np(w), True, dn)
+    assert_parity(dx, rdx, dn, "dx", by_index(1))
+    assert_parity(dw, rdw, dn, "dW", by_index(0))
+    assert_parity(db, rdb, dn, "db", by_index(0))
