@@ -1,5 +1,6 @@
-// Grouped linear backward on the register-accumulating input-gradient kernel (grouped_dx.hip) and
-// on the DMA-ring weight-gradient kernel of the mask-estimator backward (mask_estimator.hip).
+// Band GEMMs of the backward on register-accumulating DMA-ring kernels: the grouped linear input
+// gradient (grouped_dx.hip), its weight gradient on the mask-estimator DMA dW kernel
+// (mask_estimator.hip), and the mask-estimator final layer input gradient (mask_dz.hip).
 #pragma once
 
 #include "common.h"
@@ -25,5 +26,15 @@ bool uniform_dw_supported(int64_t groups, int64_t in_features, int64_t out_featu
 template <typename T>
 int launch_uniform_dw(const void* dy, const void* x, void* dw, void* db, int64_t groups, int64_t in_features,
                       int64_t out_features, int64_t rows, hipStream_t stream);
+
+// Whether launch_mask_dz takes this shape (16-bit, H a multiple of 128 or 192, aligned pointers).
+bool mask_dz_supported(int64_t H, int64_t rows, size_t elem, const void* dpre, const void* w, const void* x,
+                       const void* dx, int64_t total);
+
+// Mask-estimator final layer input gradient dx[m, b, :] = dpre[m, band b] W_b ([2 I_b, H] packed), with
+// dz = round(dx) (1 - x^2) when tanh_in (mask_dz.hip).
+template <typename T>
+int launch_mask_dz(const void* dpre, const void* w, const void* x, void* dx, const int64_t* offsets,
+                   const int64_t* dim_inputs, int NB, int64_t M, int64_t H, int F, bool tanh_in, hipStream_t stream);
 
 }  // namespace pmsst

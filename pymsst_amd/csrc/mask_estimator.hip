@@ -1099,11 +1099,20 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
                        static_cast<const T*>(pre), dpre, a);
     int rc = check_launch("me_dpre_kernel");
     if (rc != PMSST_OK) return rc;
+    bool dx_done = false;
+    if constexpr (sizeof(T) == 2) {
+      if (mask_dz_supported(H, M, sizeof(T), dpre, weight, x, dx, hm.F)) {
+        rc = launch_mask_dz<T>(dpre, weight, x, dx, offsets, dim_inputs, hm.NB, M, H, hm.F,
+                               input_act == PMSST_ACT_TANH, stream);
+        if (rc != PMSST_OK) return rc;
+        dx_done = true;
+      }
+    }
     BandSched dsc;
     uint32_t dx_per_xcd = 0;
     const int dx_hc = PMSST_ME_DX_HC == 256 && H % 256 == 0 ? 256 : 128;
     const int nhc = static_cast<int>(H / dx_hc);
-    const bool dx_dma = sizeof(T) == 2 && PMSST_ME_DX_DMA && a.vec4 && H % dx_hc == 0 && al(weight, 16) &&
+    const bool dx_dma = !dx_done && sizeof(T) == 2 && PMSST_ME_DX_DMA && a.vec4 && H % dx_hc == 0 && al(weight, 16) &&
                         al(dx, 16) &&
                         (static_cast<int64_t>(kChunkK) * H + H) * 2 < (int64_t{1} << 31) &&
                         (kDxBMd * 2 * static_cast<int64_t>(hm.F) + 64) * 2 < (int64_t{1} << 31) &&
@@ -1133,7 +1142,7 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
         if (rc != PMSST_OK) return rc;
       }
     }
-    if (!dx_dma) {
+    if (!dx_dma && !dx_done) {
       const int hchunks = static_cast<int>((H + kDxBH - 1) / kDxBH);
       const XcdGrid xg2{static_cast<uint32_t>(hm.NB * hchunks), static_cast<uint32_t>((M + kDxBM - 1) / kDxBM)};
       const dim3 g2(xg2.blocks());

@@ -878,6 +878,91 @@ def _replay_me_dw_dma(bnd, widths, offs, M, H, esz, HT, dpre_buf, x_buf, dw_buf,
             bnd.touch(dw_buf, ((2 * off + j0 + jj) * H + h0 + c8) * esz, 16, ok)
 
 
+def _replay_me_dz(bnd, widths, offs, M, H, esz, tanh_in):
+    """mask_dz.hip me_dz_kernel: the ring of weight slabs (rows clamped to the band) and dpre tiles
+    (columns clamped to the band), the transposed weight fragments, the dpre B fragments, the x
+    prefetch (tanh input) and the dz stores, on the cost-balanced band schedule."""
+    nb, F = len(widths), int(sum(widths))
+    DT, NT = (12, 2) if H % 192 == 0 else (8, 2)
+    S, HT = 4, 16 * DT
+    kUnits, kSlab = HT // 8, 32 * 2 * HT
+    kInstr = kSlab // 1024
+    wave_rows = 16 * NT
+    kStage = kSlab + 4 * wave_rows * 64
+    bnd.sizes["lds_dz"] = S * kStage
+    if S * kStage > 160 * 1024:
+        bnd.fail("me_dz: more than 160 KB of LDS")
+    mtiles = cdiv(M, 4 * wave_rows)
+    units = lambda b: H // HT  # noqa: E731
+    sc = build_band_sched(nb, mtiles, units, lambda b: cdiv(2 * widths[b], 32) + 2)
+    decoded = sched_decode(sc, nb, units, True, bnd, "me_dz")
+    lane = np.arange(64)
+    gq, rr = lane >> 4, lane & 15
+    for band, mt, sub in sorted({(b, m, s_) for b, m, s_ in decoded if m in (0, mtiles - 1)}):
+        off, I = int(offs[band]), int(widths[band])
+        K = 2 * I
+        nc = cdiv(K, 32)
+        h0 = sub * HT
+        for wave in range(4):
+            wrow0 = mt * 4 * wave_rows + wave * wave_rows
+            left = M - wrow0
+            nvt = 0 if left <= 0 else (NT if left >= wave_rows else cdiv(left, 16))
+            npw = (kInstr - wave + 3) // 4
+            for q in range(npw):
+                t = wave + 4 * q
+                P = 64 * t + lane
+                kr, pu = P // kUnits, P % kUnits
+                col = h0 + 8 * (pu ^ swz_mn(kr))
+                if np.any(pu ^ swz_mn(kr) >= kUnits):
+                    bnd.fail("me_dz: swizzled unit leaves its row")
+                for c in steps(nc):
+                    j = np.minimum(32 * c + kr, K - 1)
+                    bnd.touch("weight", ((2 * off + j) * H + col) * esz, 16)
+                for stage in range(S):
+                    bnd.touch("lds_dz", stage * kStage + t * 1024 + lane * 16, 16)
+            du = (lane & 3) ^ swz_k(lane >> 2)
+            for n in range(nvt):
+                m = np.minimum(wrow0 + 16 * n + (lane >> 2), M - 1)
+                for c in steps(nc):
+                    col = np.minimum(32 * c + 8 * du, K - 8)
+                    bnd.touch("workspace", (m * 2 * F + 2 * off + col) * esz, 16)
+                for stage in range(S):
+                    bnd.touch("lds_dz", stage * kStage + kSlab + (wave * NT + n) * 1024 + lane * 16, 16)
+            if nvt == 0:
+                continue
+            jq = lane & 15
+            kr0 = 8 * gq + (jq >> 2)
+            for stage in range(S):
+                base = stage * kStage
+                for d in range(DT):
+                    col = 16 * d + 4 * (jq & 3)
+                    o = kr0 * 2 * HT + 16 * ((col >> 3) ^ swz_mn(kr0)) + 2 * (col & 7)
+                    bnd.touch("lds_dz", base + o, 8)
+                    bnd.touch("lds_dz", base + o + 4 * 2 * HT, 8)
+                for n in range(NT):
+                    bnd.touch("lds_dz", base + kSlab + wave * NT * 1024 + rr * 64 + 16 * (gq ^ swz_k(rr)) + n * 1024, 16)
+            kop = HT + 8
+            for n in range(NT):  # staging writes of the epilogue
+                r = wave * wave_rows + 16 * n + rr
+                for d in range(DT):
+                    bnd.touch("lds_dz", (r * kop + 16 * d + 4 * gq) * esz, 4 * esz)
+        # epilogue: 16-byte units along whole rows (x read with clamped rows, dx written for m < M)
+        kop = HT + 8
+        if 4 * wave_rows * kop * esz > S * kStage:
+            bnd.fail("me_dz: staging tile larger than the ring")
+        tid = np.arange(256)
+        m0 = mt * 4 * wave_rows
+        for k in range(4 * wave_rows * kUnits // 256):
+            q = tid + 256 * k
+            r, u = q // kUnits, q % kUnits
+            if tanh_in:
+                m = np.minimum(m0 + r, M - 1)
+                bnd.touch("x", ((m * nb + band) * H + h0 + 8 * u) * esz, 16)
+            ok = m0 + r < M
+            bnd.touch("lds_dz", (r * kop + 8 * u) * esz, 16, ok)
+            bnd.touch("dx", (((m0 + r) * nb + band) * H + h0 + 8 * u) * esz, 16, ok)
+
+
 def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
     """mask_estimator.hip launch_me_bwd: me_dpre_flat_kernel, me_bwd_dx_dma_kernel (HC = 256 when
     H % 256 == 0, else 128), me_bwd_dw_dma_kernel (HT = 128)."""
@@ -892,7 +977,8 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
     if not vec4:
         bnd.fail("mask backward: unaligned widths not modelled")
         return bnd
-    dma_dx = esz == 2 and H % 128 == 0
+    dz_ring = esz == 2 and (H % 192 == 0 or H % 128 == 0)  # mask_dz.hip me_dz_kernel
+    dma_dx = esz == 2 and H % 128 == 0 and not dz_ring
     dma_dw = esz == 2 and M >= CHUNK_K and H % 128 == 0
     # -- dpre over whole rows
     nq = F // 4
@@ -917,7 +1003,9 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
             bnd.touch("workspace", ((m0 + r) * 2 * F + 2 * off + l) * esz, 4 * esz, okw)
             bnd.touch("workspace", ((m0 + r) * 2 * F + 2 * off + l + I) * esz, 4 * esz, okw)
     bnd.touch("lds_flat", np.arange(nb + 1) * 4, 4)
-    if not dma_dx:
+    if dz_ring:
+        _replay_me_dz(bnd, widths, offs, M, H, esz, tanh_in)
+    elif not dma_dx:
         _replay_me_dx_reg(bnd, widths, offs, M, H, esz, tanh_in)
     if not dma_dw:
         _replay_me_dw_reg(bnd, widths, offs, M, H, esz)
