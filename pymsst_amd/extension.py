@@ -286,10 +286,13 @@ class HipFusedExtension:
         self._rot_check(grad_out, cos, sin, "grad_out")
         return self._rotary("pmsst_rotary_backward", grad_out, cos, sin)
 
-    def rotary_qkv_forward(self, qkv, heads, cos, sin):
+    def rotary_qkv_forward(self, qkv, heads, cos, sin, out_layout="bhnd"):
         """Build addition: split a fused ``qkv[B, N, 3*H*D]`` projection and rotate q and k in one
-        launch.  Returns ``(q, k, v)``, each the ``[B,N,H,D]``-shaped transpose of a dense
-        ``[B,H,N,D]`` buffer (the layout attention reads); v is copied unrotated."""
+        launch.  Returns ``(q, k, v)``, ``[B,N,H,D]``-shaped; v is copied unrotated.  With
+        ``out_layout="bhnd"`` each is the transpose of a dense ``[B,H,N,D]`` buffer (what a
+        ``.contiguous()`` of the ``[B,H,N,D]`` view would produce); with ``"bnhd"`` each is dense
+        ``[B,N,H,D]``, the layout the flash-attention kernels read and write without copies."""
+        _req(out_layout in ("bhnd", "bnhd"), f"unsupported out_layout {out_layout!r}")
         _req(qkv.is_cuda and qkv.dim() == 3, "qkv must be a CUDA tensor of shape [B, N, 3*H*D]")
         _req(qkv.size(2) % (3 * heads) == 0, "qkv last dimension must be 3 * heads * dim_head")
         if qkv.stride(2) != 1:
@@ -299,7 +302,10 @@ class HipFusedExtension:
         q, k, v = qkv.view(b, n, 3, heads, d).unbind(2)
         self._rot_check(q, cos, sin, "q")
         cos, sin, s_seq, s_pair = self._tables(cos, sin)
-        outs = [torch.empty((b, heads, n, d), dtype=qkv.dtype, device=qkv.device).transpose(1, 2) for _ in range(3)]
+        if out_layout == "bhnd":
+            outs = [torch.empty((b, heads, n, d), dtype=qkv.dtype, device=qkv.device).transpose(1, 2) for _ in range(3)]
+        else:
+            outs = [torch.empty((b, n, heads, d), dtype=qkv.dtype, device=qkv.device) for _ in range(3)]
         ist = (ctypes.c_int64 * 9)(*[st for t in (q, k, v) for st in (t.stride(0), t.stride(1), t.stride(2))])
         ost = (ctypes.c_int64 * 9)(*[st for t in outs for st in (t.stride(0), t.stride(1), t.stride(2))])
         with _DeviceGuard(qkv.device):
@@ -485,8 +491,8 @@ class HipFusedExtension:
 
     def attention_gate_backward_bnhd(self, grad_out, attn, x, weight, gate, out_layout="bhnd"):
         """Build addition: backward of :meth:`attention_gate_forward_bnhd`; ``grad_attn`` comes back
-        ``[B,N,H,Dh]``-shaped, by default as the transpose of a dense ``[B,H,N,Dh]`` buffer (the layout
-        SDPA's backward reads)."""
+        ``[B,N,H,Dh]``-shaped, as the transpose of a dense ``[B,H,N,Dh]`` buffer (``out_layout="bhnd"``)
+        or dense (``"bnhd"``, the layout the flash-attention backward reads without a copy)."""
         _req(grad_out.is_cuda and grad_out.dim() == 2, "grad_out must have shape [B*N, H*DH]")
         _req(grad_out.size(0) == attn.size(0) * attn.size(1) and grad_out.size(1) == attn.size(2) * attn.size(3),
              "grad_out must match attn")

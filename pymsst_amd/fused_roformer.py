@@ -428,16 +428,26 @@ def _patch_core_attention_gates(ext: Any, mode: str) -> bool:
             return original(self, x)
         x = self.norm(x)
         qkv = self.to_qkv(x)
+        flash_layout = False
         if self.rotary_embed is not None and _fused_qkv_split_ok(ext, qkv):
-            # rotary patch active too: split + rotate (+ gradient stacking) in one op each way
+            # rotary patch active too: split + rotate (+ gradient stacking) in one op each way.  In
+            # 16-bit, q/k/v are written dense [B, N, H, D]: SDPA's flash kernels read that layout in
+            # place and then write their output, and read its gradient, in it as well, so neither
+            # direction copies q, k, v, the output or its gradient
+            flash_layout = qkv.dtype in (torch.float16, torch.bfloat16)
             cos, sin = self.rotary_embed.tables(qkv.shape[1], qkv.device, qkv.dtype)
-            q, k, v = _FusedQKVRotary.apply(qkv, cos[..., ::2], sin[..., ::2], self.heads, ext)
+            q, k, v = _FusedQKVRotary.apply(qkv, cos[..., ::2], sin[..., ::2], self.heads, ext,
+                                            "bnhd" if flash_layout else "bhnd")
         else:
             q, k, v = transformer.qkv_to_bnhd(qkv, self.heads)
             if self.rotary_embed is not None:
                 q, k = transformer.rotate_qk_fast_bnhd(self.rotary_embed, q, k)
         q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
-        out = self._attention(q, k, v).transpose(1, 2)
+        if flash_layout:
+            # the stock _attention's .contiguous() would copy these [B, H, N, D] views back
+            out = transformer._sdpa(q, k, v, self.dropout if self.training else 0.0).transpose(1, 2)
+        else:
+            out = self._attention(q, k, v).transpose(1, 2)
         gate_dtype = out.dtype
         gated = _FusedAttentionGate.apply(
             out,
@@ -1156,8 +1166,8 @@ class _FusedQKVRotary(torch.autograd.Function):
     the qkv gradient directly, replacing the two inverse rotations and the stack of the split."""
 
     @staticmethod
-    def forward(ctx, qkv, cos, sin, heads, extension):
-        q, k, v = extension.rotary_qkv_forward(qkv, heads, cos, sin)
+    def forward(ctx, qkv, cos, sin, heads, extension, out_layout="bhnd"):
+        q, k, v = extension.rotary_qkv_forward(qkv, heads, cos, sin, out_layout=out_layout)
         ctx.save_for_backward(cos, sin)
         ctx.extension = extension
         return q, k, v
@@ -1167,7 +1177,7 @@ class _FusedQKVRotary(torch.autograd.Function):
         cos, sin = ctx.saved_tensors
         ref = next(g for g in (grad_q, grad_k, grad_v) if g is not None)
         grads = [torch.zeros_like(ref) if g is None else g for g in (grad_q, grad_k, grad_v)]
-        return ctx.extension.rotary_qkv_backward(*grads, cos, sin), None, None, None, None
+        return ctx.extension.rotary_qkv_backward(*grads, cos, sin), None, None, None, None, None
 
 
 class _FusedBandGather(torch.autograd.Function):
@@ -1226,8 +1236,9 @@ class _FusedMaskApply(torch.autograd.Function):
 
 class _FusedAttentionGate(torch.autograd.Function):
     """fr.py:1228-1262.  With an extension that reads ``[B,N,H,Dh]`` views in place
-    (``attention_gate_forward_bnhd``), the transposed SDPA output is not copied and the attn
-    gradient comes back in the ``[B,H,N,Dh]`` layout SDPA's backward reads."""
+    (``attention_gate_forward_bnhd``), the transposed SDPA output is not copied, and the attn
+    gradient comes back in the layout SDPA's backward reads without a copy: dense ``[B,N,H,Dh]`` for
+    16-bit tensors (the flash kernels' layout), dense ``[B,H,N,Dh]`` otherwise."""
 
     @staticmethod
     def forward(ctx, attn, x, weight, bias, extension):
@@ -1253,8 +1264,9 @@ class _FusedAttentionGate(torch.autograd.Function):
         rows = gate.shape[0]
         grad_out_2d = grad_out.reshape(rows, -1)
         if ctx.bnhd:
+            layout = "bnhd" if gate.dtype in (torch.float16, torch.bfloat16) else "bhnd"
             grad_attn, grad_x, grad_weight, grad_bias = ctx.extension.attention_gate_backward_bnhd(
-                grad_out_2d, saved_attn, saved_x, weight, gate
+                grad_out_2d, saved_attn, saved_x, weight, gate, out_layout=layout
             )
         else:
             grad_attn, grad_x, grad_weight, grad_bias = ctx.extension.attention_gate_backward(

@@ -92,6 +92,56 @@ def test_bnhd_views_in_place(hip_ext, dtype):
     assert_parity(gx, r[1], dn, "grad_x")
     assert_parity(gw, r[2], dn, "grad_weight")
     assert_parity(gb, r[3], dn, "grad_bias")
+    # dense [B,N,H,Dh] gradient (the flash-attention layout): same values, other storage order
+    ga2, gx2, gw2, gb2 = hip_ext.attention_gate_backward_bnhd(gout, sa, sx, w, gate, out_layout="bnhd")
+    assert ga2.shape == attn.shape and ga2.is_contiguous()
+    assert torch.equal(ga2, ga) and torch.equal(gx2, gx) and torch.equal(gw2, gw) and torch.equal(gb2, gb)
+
+
+def test_flash_layout_attention_copies_nothing(hip_ext):
+    """16-bit attention block on the fused path: q/k/v from the qkv rotary in dense [B,N,H,D], SDPA on
+    their [B,H,N,D] views, the gate on its output; no aten::clone runs in forward or backward."""
+    from torch.profiler import ProfilerActivity, profile
+
+    from pymsst_amd.core import transformer
+    from pymsst_amd.fused_roformer import _FusedAttentionGate, _FusedQKVRotary
+
+    g = torch.Generator().manual_seed(35)
+    bsz, n, h, dh, d = 8, 62, 8, 64, 192
+    qkv = torch.randn(bsz, n, 3 * h * dh, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+    pos = torch.arange(n, dtype=torch.float32)[:, None] / (10000 ** (torch.arange(0, dh, 2) / dh))[None]
+    cos = pos.cos().repeat_interleave(2, -1).view(1, n, 1, dh).to(torch.bfloat16).cuda()
+    sin = pos.sin().repeat_interleave(2, -1).view(1, n, 1, dh).to(torch.bfloat16).cuda()
+    x = torch.randn(bsz, n, d, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+    w = (torch.randn(h, d, generator=g) / d**0.5).to(torch.bfloat16).cuda().requires_grad_()
+    b = torch.randn(h, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+
+    def block(layout):
+        q, k, v = _FusedQKVRotary.apply(qkv, cos[..., ::2], sin[..., ::2], h, hip_ext, layout)
+        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        if layout == "bnhd":
+            out = transformer._sdpa(q, k, v, 0.0).transpose(1, 2)
+        else:
+            out = transformer._sdpa(q.contiguous(), k.contiguous(), v.contiguous(), 0.0).transpose(1, 2)
+        gated = _FusedAttentionGate.apply(out, x, w, b, hip_ext)
+        (gated.float() * torch.linspace(-1, 1, gated.shape[-1], device="cuda")).sum().backward()
+        grads = [t.grad for t in (qkv, x, w, b)]
+        for t in (qkv, x, w, b):
+            t.grad = None
+        return gated.detach(), grads
+
+    ref_out, ref_grads = block("bhnd")
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CPU]) as prof:
+        out, grads = block("bnhd")
+        torch.cuda.synchronize()
+    clones = [e for e in prof.events() if e.name == "aten::clone"]
+    assert not clones, [e.name for e in clones]
+    # the layouts change the storage order only: same values, to bf16 rounding of the attention
+    assert torch.allclose(out.float(), ref_out.float(), rtol=2e-2, atol=2e-2)
+    for got, want in zip(grads, ref_grads):
+        err = (got.float() - want.float()).norm() / want.float().norm()
+        assert err < 2e-2, err
 
 
 def test_no_rows(hip_ext):

@@ -208,8 +208,8 @@ def test_rotary_strided_qkv_view_and_bhnd_output(hip_ext, dtype, shape):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("shape", [(2, 7, 3, 16), (248, 258, 8, 64), (1032, 62, 8, 64), (3, 5, 2, 6)])
 def test_rotary_qkv_split_forward_backward(hip_ext, dtype, shape):
-    """One launch splits a fused qkv projection into rotated q, rotated k and v (dense [B,H,N,D]
-    storage); the backward writes the qkv gradient (q, k rotated back, v copied) in one launch."""
+    """One launch splits a fused qkv projection into rotated q, rotated k and v (dense [B,H,N,D] or
+    dense [B,N,H,D] storage); the backward writes the qkv gradient (q, k rotated back, v copied) in one launch."""
     dn = dt_name(dtype)
     b, n, h, d = shape
     qkv = _rand((b, n, 3 * h * d), dtype, 45)
@@ -223,6 +223,9 @@ def test_rotary_qkv_split_forward_backward(hip_ext, dtype, shape):
             assert_parity(out, oracle.rotary_forward(to_np(src), cn, sn, dn), dn, f"qkv fwd {name}")
         else:
             assert torch.equal(out, src)
+    # dense [B,N,H,D] outputs: the same values
+    for out, dense in zip((q, k, v), hip_ext.rotary_qkv_forward(qkv, h, cos, sin, out_layout="bnhd")):
+        assert dense.shape == (b, n, h, d) and dense.is_contiguous() and torch.equal(dense, out)
     gq, gk, gv = (_rand((b, h, n, d), dtype, 46 + i).transpose(1, 2) for i in range(3))
     dqkv = hip_ext.rotary_qkv_backward(gq, gk, gv, cos, sin)
     assert dqkv.shape == qkv.shape and dqkv.is_contiguous()

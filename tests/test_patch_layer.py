@@ -327,7 +327,7 @@ class _OracleGateExt:
         out, gate, _, _ = self.attention_gate_forward(attn.reshape(-1, *attn.shape[2:]), x, weight, bias)
         return [out, gate, attn, x]
 
-    def _bwd4(self, grad_out, attn, x, weight, gate):
+    def _bwd4(self, grad_out, attn, x, weight, gate, out_layout="bhnd"):
         ga, gx, gw, gb = self.attention_gate_backward(grad_out, attn.reshape(-1, *attn.shape[2:]), x, weight, gate)
         return [ga.reshape(attn.shape), gx, gw, gb]
 
