@@ -9,7 +9,8 @@
 //   w2  sum_b 2 I_b H   (band b's [2 I_b, H] at 2 off_b H)      b2 [2F] (band b at 2 off_b)
 //   pre [M, 2F]         out [M, F]          hidden (optional) [M, NB, H]
 //
-// Block = (band b, pass p, row tile): 4 waves x 16 NT rows, GLU outputs j in [64 p, 64 p + 64).
+// Block = (band b, pass p, row tile): WV waves x 16 NT rows (4 x 64 or, at dim 192, 8 x 32), GLU
+// outputs j in [64 p, 64 p + 64).
 // Each wave keeps its rows of x_b in registers as MFMA B fragments (NT tiles x D / 32 K steps)
 // and walks the hidden axis in chunks of 32:
 //   GEMM1  h^T[32 x 16 NT] = W1_b[chunk] x_b^T     (A = W1 rows from LDS, B = x registers)
@@ -18,7 +19,7 @@
 //          slice of a GEMM2 B fragment: the hidden tile never leaves the registers
 //   GEMM2  pre^T[128 x 16 NT] += W2_b[64 left + 64 gate rows, chunk] h^T
 // The W1 chunk (32 x D) and the W2 chunk (128 x 32) of the block's band move from HBM/L2 into a
-// ring of LDS stages by global -> LDS DMA, shared by the 4 waves.  Epilogue: bias, GLU, stores.
+// ring of LDS stages by global -> LDS DMA, shared by the waves.  Epilogue: bias, GLU, stores.
 // Bands wider than 64 take several passes, each recomputing GEMM1 (the price of keeping every
 // accumulator in registers).
 //
@@ -33,6 +34,7 @@
 
 #include "common.h"
 #include "dma_gemm.h"
+
 
 namespace pmsst {
 namespace {
@@ -111,8 +113,8 @@ __device__ __forceinline__ u32x4_t lds_frag(const char* lds, uint32_t off) {
   return *reinterpret_cast<const u32x4_t*>(lds + off);
 }
 
-template <typename T, int DK, int NT, bool WRITE_H>
-__global__ __launch_bounds__(256) void mlp_fwd_kernel(const T* __restrict__ x, const T* __restrict__ w1,
+template <typename T, int DK, int NT, int WV, bool WRITE_H>
+__global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ x, const T* __restrict__ w1,
                                                       const T* __restrict__ b1, const T* __restrict__ w2,
                                                       const T* __restrict__ b2, T* __restrict__ pre,
                                                       T* __restrict__ out, T* __restrict__ hid, MlpArgs a,
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const T* __restrict__ x, c
   constexpr int kStage = mlp_stage_bytes<DK>();
   constexpr int D = 32 * DK;
   constexpr int kWaveRows = 16 * NT;
-  constexpr int kMaxPW = (2 * DK + 8 + 3) / 4;  // DMA instructions per wave and chunk, at most
+  constexpr int kMaxPW = (2 * DK + 8 + WV - 1) / WV;  // DMA instructions per wave and chunk, at most
   __shared__ __attribute__((aligned(1024))) char lds[S * kStage];
   __shared__ __attribute__((aligned(1024))) uint16_t stab[kTanhEntries];
   __shared__ float sb1[kMlpMaxH];
@@ -136,11 +138,11 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const T* __restrict__ x, c
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 4, rr = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t wrow0 = static_cast<int64_t>(mt) * (4 * kWaveRows) + wave * kWaveRows;
+  const int64_t wrow0 = static_cast<int64_t>(mt) * (WV * kWaveRows) + wave * kWaveRows;
   const int64_t rows_left = a.M - wrow0;
   const int nvt = rows_left <= 0 ? 0 : (rows_left >= kWaveRows ? NT : static_cast<int>((rows_left + 15) / 16));
 
-  for (int i = tid; i < H; i += 256) sb1[i] = to_f32(b1[static_cast<int64_t>(band) * H + i]);
+  for (int i = tid; i < H; i += 64 * WV) sb1[i] = to_f32(b1[static_cast<int64_t>(band) * H + i]);
   __syncthreads();
 
   // ---- DMA plan.  Instruction k of a chunk: k < 2 DK moves rows 16 (k % 2) .. + 15 of W1 K slice
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const T* __restrict__ x, c
   // the band are not moved (their products are never stored).  Wave w issues k = w, w + 4, ...
   const int nv2 = (I - j0 + 15) / 16 < 4 ? (I - j0 + 15) / 16 : 4;
   const int ntot = 2 * DK + 2 * nv2;
-  const int npw = (ntot - wave + 3) / 4;
+  const int npw = (ntot - wave + WV - 1) / WV;
   const int u = (lane & 3) ^ swz_k(lane >> 2);  // logical 16-byte unit this lane moves
   const char* w1b = reinterpret_cast<const char*>(w1 + static_cast<int64_t>(band) * H * D);
   const char* w2b = reinterpret_cast<const char*>(w2 + static_cast<int64_t>(2) * off * H);
@@ -157,7 +159,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const T* __restrict__ x, c
   uint32_t ldst[kMaxPW];
 #pragma unroll
   for (int q = 0; q < kMaxPW; ++q) {
-    const int k = wave + 4 * q;
+    const int k = wave + WV * q;
     if (k < 2 * DK) {
       const int r = 16 * (k & 1) + (lane >> 2);
       gsrc[q] = static_cast<uint32_t>((r * D + 32 * (k >> 1) + 8 * u) * 2);
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const T* __restrict__ x, c
 #pragma unroll
     for (int q = 0; q < kMaxPW; ++q) {
       if (q < npw) {
-        const int k = wave + 4 * q;
+        const int k = wave + WV * q;
         const char* src = k < 2 * DK ? w1b + gsrc[q] + static_cast<uint32_t>(c) * (64u * D)
                                      : w2b + gsrc[q] + static_cast<uint32_t>(c) * 64u;
         dma_lds16(src, lds + stage * kStage + ldst[q]);
@@ -196,11 +198,11 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const T* __restrict__ x, c
     for (int s = 0; s < DK; ++s) xf[n][s] = *reinterpret_cast<const u32x4_t*>(xr + 32 * s);
   }
 
-  // the tanh table: 64 DMAs of 1 KB, wave w moves pieces w, w + 4, ...; issued before
+  // the tanh table: 64 DMAs of 1 KB, wave w moves pieces w, w + WV, ...; issued before
   // the ring's first chunks, so the first ring wait covers them (loads complete in order)
 #pragma unroll
-  for (int q = 0; q < kTanhBytes / 1024 / 4; ++q) {
-    const int k = wave + 4 * q;
+  for (int q = 0; q < kTanhBytes / 1024 / WV; ++q) {
+    const int k = wave + WV * q;
     dma_lds16(reinterpret_cast<const char*>(a.tanh) + k * 1024 + lane * 16, reinterpret_cast<char*>(stab) + k * 1024);
   }
 #pragma unroll
@@ -256,7 +258,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_kernel(const T* __restrict__ x, c
     }
   };
   // GEMM2 A fragments of chunk c (all 8 row tiles; tiles past the band hold stale LDS data and feed
-  // accumulators that are never stored)
+  // accumulators that are never stored: skipping them per block costs registers (spills) instead)
   auto read_fb = [&](int c, u32x4_t (&fb)[8]) {
     const char* sb = lds + (c % S) * kStage;
 #pragma unroll
@@ -444,12 +446,12 @@ int tanh_tables(hipStream_t stream, const uint16_t** out) {
   return PMSST_OK;
 }
 
-template <typename T, int DK, int NT>
+template <typename T, int DK, int NT, int WV = 4>
 int launch_dk(const void* x, const void* w1, const void* b1, const void* w2, const void* b2, void* pre, void* out,
               void* hid, const MlpArgs& a, const int64_t* dim_inputs, hipStream_t stream) {
   BandSched sc;
   uint32_t per_xcd = 0;
-  const int64_t rows_per_block = 64 * NT;
+  const int64_t rows_per_block = 16 * NT * WV;
   // every block runs all H / 32 chunks with the same MFMA count: an even split of the blocks over the
   // XCDs (units of one band stay contiguous, so its weight chunks are shared in one L2 but at the seams)
   if (!build_even_sched(a.NB, (a.M + rows_per_block - 1) / rows_per_block,
@@ -462,10 +464,10 @@ int launch_dk(const void* x, const void* w1, const void* b1, const void* w2, con
   const T* w2p = static_cast<const T*>(w2);
   const T* b2p = static_cast<const T*>(b2);
   if (hid != nullptr)
-    hipLaunchKernelGGL((mlp_fwd_kernel<T, DK, NT, true>), grid, dim3(256), 0, stream, xp, w1p, b1p, w2p, b2p,
+    hipLaunchKernelGGL((mlp_fwd_kernel<T, DK, NT, WV, true>), grid, dim3(64 * WV), 0, stream, xp, w1p, b1p, w2p, b2p,
                        static_cast<T*>(pre), static_cast<T*>(out), static_cast<T*>(hid), a, sc);
   else
-    hipLaunchKernelGGL((mlp_fwd_kernel<T, DK, NT, false>), grid, dim3(256), 0, stream, xp, w1p, b1p, w2p, b2p,
+    hipLaunchKernelGGL((mlp_fwd_kernel<T, DK, NT, WV, false>), grid, dim3(64 * WV), 0, stream, xp, w1p, b1p, w2p, b2p,
                        static_cast<T*>(pre), static_cast<T*>(out), static_cast<T*>(hid), a, sc);
   return check_launch("mlp_fwd_kernel");
 }
@@ -476,7 +478,9 @@ int launch_mlp_fwd(const void* x, const void* w1, const void* b1, const void* w2
   switch (D) {
     case 64: return launch_dk<T, 2, 4>(x, w1, b1, w2, b2, pre, out, hid, a, dim_inputs, stream);
     case 128: return launch_dk<T, 4, 4>(x, w1, b1, w2, b2, pre, out, hid, a, dim_inputs, stream);
-    case 192: return launch_dk<T, 6, 4>(x, w1, b1, w2, b2, pre, out, hid, a, dim_inputs, stream);
+    // 8 waves of 32 rows: 254 VGPRs, two waves per SIMD (one block per CU, for its LDS), so one wave's
+    // table lookups overlap the other's MFMAs (4 waves of 64 rows: 111 -> 97 us at configs[1])
+    case 192: return launch_dk<T, 6, 2, 8>(x, w1, b1, w2, b2, pre, out, hid, a, dim_inputs, stream);
     case 256: return launch_dk<T, 8, 4>(x, w1, b1, w2, b2, pre, out, hid, a, dim_inputs, stream);
     case 384: return launch_dk<T, 12, 2>(x, w1, b1, w2, b2, pre, out, hid, a, dim_inputs, stream);
     case 512: return launch_dk<T, 16, 2>(x, w1, b1, w2, b2, pre, out, hid, a, dim_inputs, stream);

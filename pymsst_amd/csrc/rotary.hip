@@ -406,18 +406,21 @@ __global__ __launch_bounds__(kRowBwdThreads) void norm_rot_bwd_kernel(
     for (int i = 0; i < VEC; ++i) acc[v][i] = 0.f;
   }
   const float inv_scale = 1.0f / scale;
+  // rows per lane slot in flight: one for rows of 3 or 4 packs per lane (two would need more than
+  // the 256 registers of a wave and spill)
+  constexpr int RPS = NV >= 3 ? 1 : kRowsPerSlot;
 
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block * kRowsPerSlot; base < rows;
-       base += static_cast<int64_t>(gridDim.x) * rows_per_block * kRowsPerSlot) {
-    // loads of all kRowsPerSlot rows first, held raw until every load of the trip has issued.
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block * RPS; base < rows;
+       base += static_cast<int64_t>(gridDim.x) * rows_per_block * RPS) {
+    // loads of all RPS rows first, held raw until every load of the trip has issued.
     // Rows past the end load the last row (no branch around the loads) and recompute it: their
     // dx stores write the bits the last row's own stores write, and only the dgamma
     // accumulation excludes them.
-    u32x4_t dr[kRowsPerSlot][NV], xr[kRowsPerSlot][NV];
-    TabPiece<T, VEC / 2, TS> ct[kRowsPerSlot][NV], st[kRowsPerSlot][NV];
-    float inv[kRowsPerSlot];
+    u32x4_t dr[RPS][NV], xr[RPS][NV];
+    TabPiece<T, VEC / 2, TS> ct[RPS][NV], st[RPS][NV];
+    float inv[RPS];
 #pragma unroll
-    for (int u = 0; u < kRowsPerSlot; ++u) {
+    for (int u = 0; u < RPS; ++u) {
       const int64_t row = base + u * rows_per_block + wave * rows_per_wave + slot;
       const int64_t rl = row < rows ? row : rows - 1;
       inv[u] = inv_norm[rl];
@@ -433,7 +436,7 @@ __global__ __launch_bounds__(kRowBwdThreads) void norm_rot_bwd_kernel(
     }
     __builtin_amdgcn_sched_barrier(0);  // all loads of the trip issue before the first wait
 #pragma unroll
-    for (int u = 0; u < kRowsPerSlot; ++u) {
+    for (int u = 0; u < RPS; ++u) {
       const int64_t row = base + u * rows_per_block + wave * rows_per_wave + slot;
       const bool valid = row < rows;
       const int64_t rl = valid ? row : rows - 1;

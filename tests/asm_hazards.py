@@ -111,3 +111,22 @@ def check_source(src: Path) -> dict[str, list[str]]:
         if bad:
             result[name] = bad
     return result
+
+
+_SCRATCH = re.compile(r"^\s*\.(?:amdhsa_)?private_segment_fixed_size:?\s+(\d+)", re.M)
+
+
+def scratch_bytes(asm: str) -> dict[str, int]:
+    """Per-lane scratch (register spill) bytes of every kernel of an assembly listing."""
+    out = {}
+    for m in re.finditer(r"^\s*\.amdhsa_kernel\s+(\S+)(.*?)\.end_amdhsa_kernel", asm, re.M | re.S):
+        s = _SCRATCH.search(m.group(2))
+        out[m.group(1)] = int(s.group(1)) if s else 0
+    return out
+
+
+def spills_of_source(src: Path) -> dict[str, int]:
+    """Kernels of one HIP source that use scratch memory (spilled registers), with the bytes per lane."""
+    with tempfile.TemporaryDirectory() as tmp:
+        asm = device_asm(src, Path(tmp)).read_text()
+    return {k: v for k, v in scratch_bytes(asm).items() if v}

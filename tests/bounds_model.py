@@ -1083,16 +1083,18 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
     return bnd
 
 
-MLP_TILES = {64: (2, 4), 128: (4, 4), 192: (6, 4), 256: (8, 4), 384: (12, 2), 512: (16, 2)}
+MLP_TILES = {64: (2, 4, 4), 128: (4, 4, 4), 192: (6, 2, 8), 256: (8, 4, 4), 384: (12, 2, 4), 512: (16, 2, 4)}
 
 
-def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True):
+def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None):
     """mask_mlp.hip mlp_fwd_kernel (whole depth-2 mask MLP, 16-bit) on its band schedule: the b1 fill,
     the x fragments, the W1 / W2 DMA ring, the LDS fragment reads, the hidden stores and the GLU
     epilogue."""
     nb, F = len(widths), int(sum(widths))
     offs = _offs(widths)
-    DK, NT = MLP_TILES[D]
+    DK, NT, WV = MLP_TILES[D]
+    if wv is not None:  # same rows per block
+        NT, WV = NT * WV // wv, wv
     S, J = (2 if DK >= 12 else 3), 64
     kStage = DK * 2048 + 2 * J * 64
     sizes = {"x": M * nb * D * esz, "w1": nb * H * D * esz, "b1": nb * H * esz, "w2": 2 * F * H * esz,
@@ -1106,35 +1108,35 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True):
         bnd.fail("mask_mlp: shape outside the host check")
         return bnd
     wave_rows = 16 * NT
-    mtiles = cdiv(M, 4 * wave_rows)
+    mtiles = cdiv(M, WV * wave_rows)
     units = lambda b: cdiv(widths[b], J)  # noqa: E731
     sc = build_even_sched(nb, mtiles, units)
     decoded = sched_decode(sc, nb, units, True, bnd, "mlp_fwd")
-    tid = np.arange(256)
+    tid = np.arange(64 * WV)
     lane = tid & 63
     g, rr = lane >> 4, lane & 15
     u = (lane & 3) ^ swz_k(lane >> 2)
     nc = H // 32
-    kmax_pw = (2 * DK + 8 + 3) // 4
+    kmax_pw = (2 * DK + 8 + WV - 1) // WV
     for band, mt, pss in sorted({(b, m, p) for b, m, p in decoded if m in (0, mtiles - 1)}):
         off, I = int(offs[band]), int(widths[band])
         j0 = pss * J
-        for i0 in range(0, H, 256):
+        for i0 in range(0, H, 64 * WV):
             i = i0 + tid
             bnd.touch("b1", (band * H + i) * esz, esz, i < H)
             bnd.touch("sb1", i * 4, 4, i < H)
-        for k in range(64):  # tanh table: 64 DMAs of 1 KB (wave k % 4), bf16 table first
+        for k in range(64):  # tanh table: 64 DMAs of 1 KB (wave k % WV), bf16 table first
             bnd.touch("tanh", k * 1024 + lane * 16, 16)
             bnd.touch("stab", k * 1024 + lane * 16, 16)
         bnd.touch("stab", np.array([0, 0x7FFF]) * 2, 2)  # table reads: index = pattern & 0x7fff
         nv2 = min(4, cdiv(I - j0, 16))
         ntot = 2 * DK + 2 * nv2
-        for wave in range(4):
-            npw = (ntot - wave + 3) // 4
+        for wave in range(WV):
+            npw = (ntot - wave + WV - 1) // WV
             if npw > kmax_pw:
                 bnd.fail("mlp_fwd: more DMA instructions than the plan holds")
             for q in range(npw):
-                k = wave + 4 * q
+                k = wave + WV * q
                 if k < 2 * DK:
                     r = 16 * (k & 1) + (lane >> 2)
                     gsrc = (r * D + 32 * (k >> 1) + 8 * u) * 2
@@ -1157,7 +1159,7 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True):
                     bnd.touch(buf, base + gsrc + c * stride, 16)
                 for stage in range(S):
                     bnd.touch("lds", stage * kStage + ldst + lane * 16, 16)
-            wrow0 = mt * 4 * wave_rows + wave * wave_rows
+            wrow0 = mt * WV * wave_rows + wave * wave_rows
             left = M - wrow0
             nvt = 0 if left <= 0 else (NT if left >= wave_rows else cdiv(left, 16))
             for n in range(NT):

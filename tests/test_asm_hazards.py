@@ -1,7 +1,10 @@
-"""No inline-asm LDS read of any kernel has its registers touched before its explicit wait.
+"""No inline-asm LDS read of any kernel has its registers touched before its explicit wait, and no
+kernel spills registers to scratch memory.
 
 Compiles every ``pymsst_amd/csrc/*.hip`` to gfx950 assembly with the build's flags and scans each
-kernel (``tests/asm_hazards.py``).  Also checks that the scan finds a planted hazard.
+kernel (``tests/asm_hazards.py``).  Also checks that the scan finds a planted hazard.  A spill turns
+a register-resident kernel into one that streams its accumulators through memory (a conditional
+GEMM tile once made the mask-MLP forward spill 420 bytes per lane and run six times slower).
 """
 
 from __future__ import annotations
@@ -23,6 +26,22 @@ def test_no_inline_lds_read_hazards():
         results = dict(zip(sources, pool.map(ah.check_source, sources)))
     bad = {src.name: {k: v[:3] for k, v in r.items()} for src, r in results.items() if r}
     assert not bad, bad
+
+
+def test_no_kernel_spills_registers():
+    sources = sorted(ah.CSRC.glob("*.hip"))
+    with cf.ThreadPoolExecutor(max_workers=8) as pool:
+        results = dict(zip(sources, pool.map(ah.spills_of_source, sources)))
+    bad = {src.name: r for src, r in results.items() if r}
+    assert not bad, bad
+
+
+def test_scratch_parser_reads_the_kernel_descriptor():
+    asm = "\n".join([
+        "\t.amdhsa_kernel _Z1av", "\t\t.amdhsa_private_segment_fixed_size 0", "\t.end_amdhsa_kernel",
+        "\t.amdhsa_kernel _Z1bv", "\t\t.amdhsa_private_segment_fixed_size 420", "\t.end_amdhsa_kernel",
+    ])
+    assert ah.scratch_bytes(asm) == {"_Z1av": 0, "_Z1bv": 420}
 
 
 def test_scan_finds_a_planted_copy():
