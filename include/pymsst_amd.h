@@ -260,6 +260,18 @@ int pmsst_mask_mlp_forward(const void* x, const void* w1, const void* b1, const 
                            const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count, int64_t rows,
                            int64_t dim, int64_t hidden, void* pre, void* out, void* hidden_out, int dtype,
                            void* stream);
+/* The same MLP for stem `stem` of `stems` with the mask application in its epilogue (the fusion that
+ * cuda_graph.py:140-158's layout and the stock `spec * mask` product leave to two passes): instead
+ * of out, writes est[b, stem, c, f, t] = spec[b, f*channels + c, t] * (out[m, 2r], out[m, 2r+1]) for
+ * rows m = b*frames + t and complex rows r = f*channels + c, with the mask rounded to the storage
+ * dtype first (est is 0 at f = 0 when zero_dc).  spec: complex64 [rows/frames, bins*channels, frames];
+ * est: complex64 [rows/frames * stems * channels, bins, frames] (the iSTFT input), bins = sum of the
+ * widths / (2 * channels).  pre and hidden_out as for pmsst_mask_mlp_forward. */
+int pmsst_mask_mlp_forward_apply(const void* x, const void* w1, const void* b1, const void* w2, const void* b2,
+                                 const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
+                                 int64_t rows, int64_t dim, int64_t hidden, void* pre, void* hidden_out,
+                                 const void* spec, void* est, int64_t frames, int64_t channels, int64_t stems,
+                                 int64_t stem, int zero_dc, int dtype, void* stream);
 
 /* ------------------------------------------------------------------ attention output gate
  * gate[m, h] = sigmoid(x[m] . W[h] + b[h]) stored in the tensor dtype; out[m, h*Dh + d] =
@@ -322,7 +334,8 @@ int pmsst_mask_apply_forward(const void* spec, const void* mask, int64_t mask_ba
                              int64_t batch, int64_t stems, int64_t channels, int64_t freqs, int64_t frames,
                              int zero_dc, void* est, int mask_dtype, void* stream);
 /* grad_mask (mask_dtype, contiguous [batch, stems, frames, 2*freqs*channels]) = grad_est * conj(spec);
- * grad_spec (complex64 like spec, NULL to skip) = sum over stems of grad_est * conj(mask). */
+ * grad_spec (complex64 like spec, NULL to skip) = sum over stems of grad_est * conj(mask).  mask is read
+ * only for grad_spec: with grad_spec NULL any buffer of its layout may be passed (e.g. grad_mask). */
 int pmsst_mask_apply_backward(const void* grad_est, const void* spec, const void* mask, int64_t mask_batch_stride,
                               int64_t mask_stem_stride, int64_t batch, int64_t stems, int64_t channels, int64_t freqs,
                               int64_t frames, int zero_dc, void* grad_mask, void* grad_spec, int mask_dtype,

@@ -161,6 +161,11 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
     def _masks(self, spec: torch.Tensor) -> torch.Tensor:
         """Complex ``spec[B, F*C, T]`` -> the stems' masks ``[B, stems, T, features]`` (band features,
         band split, axial blocks, final norm, mask estimators)."""
+        return self._estimate_masks(self._mask_features(spec))
+
+    def _mask_features(self, spec: torch.Tensor) -> torch.Tensor:
+        """Complex ``spec[B, F*C, T]`` -> the mask estimators' input ``[B, T, NB, dim]`` (band features,
+        band split, axial blocks, final norm)."""
         x = self._band_features(spec)  # [B, T, features]
         x = self.band_split(x)  # [B, T, NB, dim]
         for time_tf, freq_tf in self.layers:
@@ -168,7 +173,7 @@ class BSRoformer(RoformerRuntimeMixin, nn.Module):
                 x = checkpoint(self._axial, x, time_tf, freq_tf, use_reentrant=False)
             else:
                 x = self._axial(x, time_tf, freq_tf)
-        return self._estimate_masks(self.final_norm(x))
+        return self.final_norm(x)
 
     def _mask_core(self, spec: torch.Tensor, channels: int) -> torch.Tensor:
         """The part between STFT and iSTFT (pymsst's "mask core"): complex ``spec[B, F*C, T]`` -> masked

@@ -48,11 +48,23 @@ constexpr int kTanhBytes = kTanhEntries * 2;
 // tanh tables: [bf16 patterns | fp16 patterns], filled once per device from the host
 __device__ __align__(256) uint16_t g_tanh_tables[2 * kTanhEntries];
 
+// Mask application in the epilogue (stem s of S): est[b, s, c, f, t] = spec[b, f C + c, t] x the
+// complex mask (out[m, 2 r], out[m, 2 r + 1]) of row m = b T + t, complex row r = f C + c, in the
+// iSTFT layout [B * S * C, Fbins, T] (complex64); bin 0 zero when zero_dc.  The mask values are
+// rounded to the storage dtype first, as the stored mask the stock product multiplies is.
+struct MlpApply {
+  const float2* spec;  // complex64 [B, Fbins * C, T]
+  float2* est;         // complex64 [B * S * C, Fbins, T]
+  FastDiv frames;      // T
+  int C, Fbins, S, s, zero_dc;
+};
+
 struct MlpArgs {
   const int64_t* offsets;  // device [NB + 1] prefix sums of I_b
   const uint16_t* tanh;    // this dtype's table in device memory
   int64_t M;
   int NB, H, F;
+  MlpApply ap;             // used by the APPLY kernels only
 };
 
 template <int DK>
@@ -113,7 +125,7 @@ __device__ __forceinline__ u32x4_t lds_frag(const char* lds, uint32_t off) {
   return *reinterpret_cast<const u32x4_t*>(lds + off);
 }
 
-template <typename T, int DK, int NT, int WV, bool WRITE_H>
+template <typename T, int DK, int NT, int WV, bool WRITE_H, bool APPLY>
 __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ x, const T* __restrict__ w1,
                                                       const T* __restrict__ b1, const T* __restrict__ w2,
                                                       const T* __restrict__ b2, T* __restrict__ pre,
@@ -369,7 +381,32 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
       T* pl = pre + m * pitch2 + 2 * off + j;
       store_pack<T, 4>(pl, vl);
       store_pack<T, 4>(pl + I, vg);
-      store_pack<T, 4>(out + m * a.F + off + j, vo);
+      if constexpr (APPLY) {
+        // the lane's 4 outputs are the (re, im) pairs of complex rows r0 and r0 + 1 (off + j is a
+        // multiple of 4); lanes rr = 0..15 hold consecutive rows m, i.e. consecutive frames
+        const MlpApply& ap = a.ap;
+        const uint32_t um = static_cast<uint32_t>(m);
+        const uint32_t bb = ap.frames.div(um), tt = um - bb * ap.frames.d;
+        const int r0 = (off + j) >> 1;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int r = r0 + q;
+          const int f = r / ap.C, c = r - f * ap.C;
+          // the mask rounded as the stored mask is: the fp32 product, then the 16-bit conversion (the
+          // empty asm keeps the product in a register, or the compiler fuses product and fp16
+          // conversion into a v_fma_mixlo_f16 that rounds once and can land one fp16 ulp away)
+          float pr = vo[2 * q], pi = vo[2 * q + 1];
+          asm volatile("" : "+v"(pr), "+v"(pi));
+          const float mr = to_f32(from_f32<T>(pr)), mi = to_f32(from_f32<T>(pi));
+          const float2 sv = ap.spec[(static_cast<int64_t>(bb) * ap.Fbins * ap.C + r) * ap.frames.d + tt];
+          float2 e = make_float2(sv.x * mr - sv.y * mi, sv.x * mi + sv.y * mr);
+          if (ap.zero_dc && f == 0) e = make_float2(0.f, 0.f);
+          ap.est[((static_cast<int64_t>(bb) * ap.S + ap.s) * ap.C + c) * static_cast<int64_t>(ap.Fbins) * ap.frames.d +
+                 static_cast<int64_t>(f) * ap.frames.d + tt] = e;
+        }
+      } else {
+        store_pack<T, 4>(out + m * a.F + off + j, vo);
+      }
     }
   }
 }
@@ -463,12 +500,17 @@ int launch_dk(const void* x, const void* w1, const void* b1, const void* w2, con
   const T* b1p = static_cast<const T*>(b1);
   const T* w2p = static_cast<const T*>(w2);
   const T* b2p = static_cast<const T*>(b2);
-  if (hid != nullptr)
-    hipLaunchKernelGGL((mlp_fwd_kernel<T, DK, NT, WV, true>), grid, dim3(64 * WV), 0, stream, xp, w1p, b1p, w2p, b2p,
-                       static_cast<T*>(pre), static_cast<T*>(out), static_cast<T*>(hid), a, sc);
-  else
-    hipLaunchKernelGGL((mlp_fwd_kernel<T, DK, NT, WV, false>), grid, dim3(64 * WV), 0, stream, xp, w1p, b1p, w2p, b2p,
-                       static_cast<T*>(pre), static_cast<T*>(out), static_cast<T*>(hid), a, sc);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * WV), 0, stream, xp, w1p, b1p, w2p, b2p, static_cast<T*>(pre),
+                       static_cast<T*>(out), static_cast<T*>(hid), a, sc);
+  };
+  if (a.ap.est != nullptr) {
+    if (hid != nullptr) go(mlp_fwd_kernel<T, DK, NT, WV, true, true>);
+    else go(mlp_fwd_kernel<T, DK, NT, WV, false, true>);
+  } else {
+    if (hid != nullptr) go(mlp_fwd_kernel<T, DK, NT, WV, true, false>);
+    else go(mlp_fwd_kernel<T, DK, NT, WV, false, false>);
+  }
   return check_launch("mlp_fwd_kernel");
 }
 
@@ -494,6 +536,38 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 }  // namespace pmsst
 
 using namespace pmsst;
+
+namespace pmsst {
+
+int mask_mlp_forward_impl(const char* op, const void* x, const void* w1, const void* b1, const void* w2,
+                          const void* b2, const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
+                          int64_t rows, int64_t dim, int64_t hidden, void* pre, void* out, void* hidden_out,
+                          const MlpApply& ap, int dtype, void* stream) {
+  PMSST_REQUIRE(pmsst_mask_mlp_supported(dim, hidden, dim_inputs, band_count, dtype) == 1,
+                "%s: unsupported shape or dtype (dim %lld, hidden %lld, dtype %d)", op, (long long)dim,
+                (long long)hidden, dtype);
+  PMSST_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), "%s: bad row count", op);
+  PMSST_REQUIRE(dim_offsets != nullptr, "%s: dim_offsets is null", op);
+  if (rows == 0) return PMSST_OK;
+  PMSST_REQUIRE(x && w1 && b1 && w2 && b2 && pre, "%s: null tensor", op);
+  PMSST_REQUIRE(aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(hidden_out),
+                "%s: x, w1, w2 and hidden must be 16-byte aligned", op);
+  PMSST_REQUIRE(reinterpret_cast<uintptr_t>(b2) % 8 == 0 && reinterpret_cast<uintptr_t>(pre) % 8 == 0 &&
+                    reinterpret_cast<uintptr_t>(out) % 8 == 0,
+                "%s: b2, pre and out must be 8-byte aligned", op);
+  int64_t total = 0;
+  for (int64_t b = 0; b < band_count; ++b) total += dim_inputs[b];
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* tabs = nullptr;
+  const int rc = tanh_tables(s, &tabs);
+  if (rc != PMSST_OK) return rc;
+  MlpArgs a{dim_offsets, tabs + (dtype == PMSST_BF16 ? 0 : kTanhEntries), rows, static_cast<int>(band_count),
+            static_cast<int>(hidden), static_cast<int>(total), ap};
+  if (dtype == PMSST_BF16) return launch_mlp_fwd<bf16>(x, w1, b1, w2, b2, pre, out, hidden_out, a, dim, dim_inputs, s);
+  return launch_mlp_fwd<f16>(x, w1, b1, w2, b2, pre, out, hidden_out, a, dim, dim_inputs, s);
+}
+
+}  // namespace pmsst
 
 extern "C" {
 
@@ -525,29 +599,35 @@ int pmsst_mask_mlp_forward(const void* x, const void* w1, const void* b1, const 
                            const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count, int64_t rows,
                            int64_t dim, int64_t hidden, void* pre, void* out, void* hidden_out, int dtype,
                            void* stream) {
-  const char* op = "mask_mlp_forward";
-  PMSST_REQUIRE(pmsst_mask_mlp_supported(dim, hidden, dim_inputs, band_count, dtype) == 1,
-                "%s: unsupported shape or dtype (dim %lld, hidden %lld, dtype %d)", op, (long long)dim,
-                (long long)hidden, dtype);
-  PMSST_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), "%s: bad row count", op);
-  PMSST_REQUIRE(dim_offsets != nullptr, "%s: dim_offsets is null", op);
-  if (rows == 0) return PMSST_OK;
-  PMSST_REQUIRE(x && w1 && b1 && w2 && b2 && pre && out, "%s: null tensor", op);
-  PMSST_REQUIRE(aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(hidden_out),
-                "%s: x, w1, w2 and hidden must be 16-byte aligned", op);
-  PMSST_REQUIRE(reinterpret_cast<uintptr_t>(b2) % 8 == 0 && reinterpret_cast<uintptr_t>(pre) % 8 == 0 &&
-                    reinterpret_cast<uintptr_t>(out) % 8 == 0,
-                "%s: b2, pre and out must be 8-byte aligned", op);
+  PMSST_REQUIRE(out != nullptr || rows == 0, "mask_mlp_forward: null tensor");
+  return pmsst::mask_mlp_forward_impl("mask_mlp_forward", x, w1, b1, w2, b2, dim_offsets, dim_inputs, band_count, rows,
+                                      dim, hidden, pre, out, hidden_out, pmsst::MlpApply{}, dtype, stream);
+}
+
+int pmsst_mask_mlp_forward_apply(const void* x, const void* w1, const void* b1, const void* w2, const void* b2,
+                                 const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
+                                 int64_t rows, int64_t dim, int64_t hidden, void* pre, void* hidden_out,
+                                 const void* spec, void* est, int64_t frames, int64_t channels, int64_t stems,
+                                 int64_t stem, int zero_dc, int dtype, void* stream) {
+  const char* op = "mask_mlp_forward_apply";
+  PMSST_REQUIRE(frames > 0 && frames < (int64_t{1} << 31) && rows % frames == 0, "%s: rows must be batch * frames",
+                op);
+  PMSST_REQUIRE(channels > 0 && channels < 64 && stems > 0 && stem >= 0 && stem < stems && stems < (1 << 16),
+                "%s: bad channels / stems / stem", op);
+  PMSST_REQUIRE(dim_inputs != nullptr && band_count > 0, "%s: no bands", op);
   int64_t total = 0;
   for (int64_t b = 0; b < band_count; ++b) total += dim_inputs[b];
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  const uint16_t* tabs = nullptr;
-  const int rc = tanh_tables(s, &tabs);
-  if (rc != PMSST_OK) return rc;
-  MlpArgs a{dim_offsets, tabs + (dtype == PMSST_BF16 ? 0 : kTanhEntries), rows, static_cast<int>(band_count),
-            static_cast<int>(hidden), static_cast<int>(total)};
-  if (dtype == PMSST_BF16) return launch_mlp_fwd<bf16>(x, w1, b1, w2, b2, pre, out, hidden_out, a, dim, dim_inputs, s);
-  return launch_mlp_fwd<f16>(x, w1, b1, w2, b2, pre, out, hidden_out, a, dim, dim_inputs, s);
+  PMSST_REQUIRE(total % (2 * channels) == 0, "%s: features must be 2 * channels * bins", op);
+  const int64_t fbins = total / (2 * channels);
+  PMSST_REQUIRE(rows == 0 || (spec && est), "%s: null spectrum or estimate", op);
+  PMSST_REQUIRE(reinterpret_cast<uintptr_t>(spec) % 8 == 0 && reinterpret_cast<uintptr_t>(est) % 8 == 0,
+                "%s: spectrum and estimate must be 8-byte aligned", op);
+  PMSST_REQUIRE((rows / frames) * stems * channels * fbins * frames < (int64_t{1} << 40), "%s: estimate too large", op);
+  const pmsst::MlpApply ap{static_cast<const float2*>(spec), static_cast<float2*>(est),
+                           pmsst::FastDiv(static_cast<uint32_t>(frames)), static_cast<int>(channels),
+                           static_cast<int>(fbins), static_cast<int>(stems), static_cast<int>(stem), zero_dc != 0};
+  return pmsst::mask_mlp_forward_impl(op, x, w1, b1, w2, b2, dim_offsets, dim_inputs, band_count, rows, dim, hidden,
+                                      pre, nullptr, hidden_out, ap, dtype, stream);
 }
 
 }  // extern "C"

@@ -991,6 +991,67 @@ class HipFusedExtension:
         check(rc, "pmsst_mask_mlp_forward")
         return [out, pre, hid]
 
+    def mask_mlp_forward_apply(self, x, w1, b1, w2_all, b2, dim_inputs, spec, est, stem: int, channels: int,
+                               zero_dc: bool = False, save_hidden: bool = False):
+        """:meth:`mask_mlp_forward` with the mask application in its epilogue: writes stem ``stem`` of
+        ``est`` (complex64 ``[B*S*C, F, T]``, the iSTFT input) = complex ``spec[B, F*C, T]`` times this
+        stem's mask, instead of returning the mask.  Rows of ``x`` are ``(batch, frame)``.  Returns
+        ``[pre[M,2F], hidden[M,NB,H] | None]``."""
+        _req(x.is_cuda and x.dim() == 3, "x must be a CUDA tensor of shape [M, NB, D]")
+        _req(spec.is_cuda and spec.dtype == torch.complex64 and spec.dim() == 3 and spec.is_contiguous(),
+             "spec must be a contiguous CUDA complex64 [B, F*C, T]")
+        _req(est.is_cuda and est.dtype == torch.complex64 and est.dim() == 3 and est.is_contiguous(),
+             "est must be a contiguous CUDA complex64 [B*S*C, F, T]")
+        host, dev_offs, offs = self._bands(dim_inputs, x.device)
+        nb, total = len(offs) - 1, offs[-1]
+        b, fc, t = spec.shape
+        _req(channels > 0 and fc % channels == 0 and 2 * fc == total, "spec rows must be the features / 2")
+        _req(x.size(0) == b * t and x.size(1) == nb, "x must have B * T rows and one slice per band")
+        _req(est.size(0) % (b * channels) == 0 and tuple(est.shape[1:]) == (fc // channels, t),
+             "est must have shape [B * S * C, F, T]")
+        stems = est.size(0) // (b * channels)
+        _req(0 <= stem < stems, "stem out of range")
+        x = x.contiguous()
+        w1 = w1.contiguous()
+        b1 = b1.contiguous()
+        m, d = x.size(0), x.size(2)
+        hd = w1.size(1)
+        _req(tuple(w1.shape) == (nb, hd, d), "w1 must have shape [NB, H, D]")
+        _req(b1.numel() == nb * hd, "b1 must have NB * H elements")
+        _req(w2_all.numel() == 2 * total * hd, "w2 must hold the packed [2 I_b, H] weights")
+        _req(b2.numel() == 2 * total, "b2 must have 2F elements")
+        for tt in (w1, b1, w2_all, b2):
+            _req(tt.dtype == x.dtype and tt.device == x.device, "parameters must match x in dtype and device")
+        pre = torch.empty((m, 2 * total), dtype=x.dtype, device=x.device)
+        hid = torch.empty((m, nb, hd), dtype=x.dtype, device=x.device) if save_hidden else None
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_mask_mlp_forward_apply(
+                _ptr(x), _ptr(w1), _ptr(b1), _ptr(w2_all), _ptr(b2), _ptr(dev_offs), host, nb, m, d, hd, _ptr(pre),
+                _ptr(hid), _ptr(spec), _ptr(est), t, channels, stems, stem, int(bool(zero_dc)), dtype_code(x.dtype),
+                _stream(x.device),
+            )
+        check(rc, "pmsst_mask_mlp_forward_apply")
+        return [pre, hid]
+
+    def mask_apply_grad_mask(self, grad_est, spec, stems: int, channels: int, dtype, zero_dc: bool = False):
+        """``grad_est * conj(spec)`` as the per-stem mask gradients ``[B, S, T, F*C*2]`` in ``dtype`` (the
+        mask-gradient half of :meth:`mask_apply_backward`, for masks that were never stored)."""
+        b, fc, t = spec.shape
+        f = fc // channels
+        _req(grad_est.is_cuda and grad_est.dtype == torch.complex64 and tuple(grad_est.shape) == (b * stems * channels, f, t),
+             "grad_est must be CUDA complex64 [B*S*C, F, T]")
+        grad_est = grad_est.contiguous()
+        spec = spec.contiguous()
+        grad_mask = torch.empty((b, stems, t, 2 * fc), dtype=dtype, device=spec.device)
+        with _DeviceGuard(spec.device):
+            # the mask argument is read only for the spectrum gradient, which is not asked for here
+            rc = self._lib.pmsst_mask_apply_backward(
+                _ptr(grad_est), _ptr(spec), _ptr(grad_mask), grad_mask.stride(0), grad_mask.stride(1), b, stems, channels,
+                f, t, int(bool(zero_dc)), _ptr(grad_mask), None, dtype_code(dtype), _stream(spec.device),
+            )
+        check(rc, "pmsst_mask_apply_backward")
+        return grad_mask
+
     def mask_estimator_final_forward(self, x, weights, bias, dim_inputs, dim_offsets):
         """``.cpp:589-622`` / ``.cpp:660-693`` (direct): ``x[M,NB,H]``, per-band ``weight[2*I_b, H]``,
         ``bias[2F]`` -> ``[out[M,F], pre[M,2F], x_contiguous]``."""

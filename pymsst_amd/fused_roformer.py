@@ -532,6 +532,36 @@ def _patch_mask_apply(ext: Any) -> bool:
     masked_spectrum_cuda_ext._pymsst_fused_mask_apply = True
     masked_spectrum_cuda_ext._pymsst_original_masked_spectrum = original
     cls._masked_spectrum = masked_spectrum_cuda_ext
+
+    # With the one-pass mask MLP active too, the mask product moves into that kernel's epilogue: the
+    # stock path writes every stem's mask, then multiplies the spectrum by it and permutes the product
+    # for the iSTFT; here the masks are never written.
+    original_core = cls._mask_core
+    stock_masks = cls._masks
+
+    def mask_core_cuda_ext(self, spec, channels):
+        bands, _, _ = _core()
+        if (not self.training or type(self)._spectral_mask is not stock_spectral_mask
+                or type(self)._masks is not stock_masks or not spec.is_cuda or spec.dtype != torch.complex64
+                or spec.requires_grad or not hasattr(ext, "mask_mlp_forward_apply") or not _mask_mlp_enabled(ext)
+                or not getattr(bands.MaskEstimator._forward_layer_grouped_mlp, "_pymsst_mask_estimator_final_fused",
+                               False)):
+            return original_core(self, spec, channels)
+        x = self._mask_features(spec)
+        params, dims = [], None
+        for est in self._active_mask_estimators():
+            plan = est._layer_grouping_plan()
+            ops = _mask_mlp_operands(est, x, plan) if plan and x.device.type == "cuda" else None
+            if ops is None or not _one_pass_mask_mlp(ext, ops[0], ops[1], ops[5]) or (dims is not None
+                                                                                      and ops[5] != dims):
+                return self._masked_spectrum(spec, self._estimate_masks(x), channels)
+            x3, dims = ops[0], ops[5]
+            params += list(ops[1:5])
+        return _FusedMaskMLPApply.apply(spec, x3, channels, bool(getattr(self, "zero_dc", False)), dims, ext, *params)
+
+    mask_core_cuda_ext._pymsst_fused_mask_apply = True
+    mask_core_cuda_ext._pymsst_original_mask_core = original_core
+    cls._mask_core = mask_core_cuda_ext
     return True
 
 
@@ -763,6 +793,17 @@ def _fused_mask_mlp(module, x, plan, ext):
     module does not have that shape.  The parameters come from the module's flat storages (the
     first layer's ``[NB, H, dim]`` stack is a view); under autocast they and x are in the autocast
     dtype, as for the stock grouped GEMMs."""
+    ops = _mask_mlp_operands(module, x, plan)
+    if ops is None:
+        return None
+    x3, w1, b1, w2, b2, dims, lead = ops
+    out = _FusedMaskMLP.apply(x3, w1, b1, w2, b2, ext, dims)
+    return out.reshape(*lead, module._dim_total)
+
+
+def _mask_mlp_operands(module, x, plan):
+    """``(x3[M, NB, dim], w1[NB, H, dim], b1[NB, H], w2 (packed), b2[2F], dim_inputs, lead shape)`` of a
+    depth-2 mask MLP in the compute dtype, or ``None`` when the module does not have that shape."""
     nb = len(module.to_freqs)
     if len(plan) != 3 or plan[0][0] != "linear" or plan[1][0] != "tanh" or plan[2][0] != "linear":
         return None
@@ -788,9 +829,8 @@ def _fused_mask_mlp(module, x, plan, ext):
     x3 = x.reshape(-1, nb, x.shape[-1]).to(dt)
     w1 = w1_p.group(0, nb, dt)
     b1 = b1_p.group(0, nb, dt)
-    out = _FusedMaskMLP.apply(x3, w1.view(nb, hidden, -1), b1.view(nb, hidden), w2_p.flat(dt), b2_p.flat(dt), ext,
-                              tuple(int(d) for d in module.dim_inputs))
-    return out.reshape(*lead, module._dim_total)
+    return (x3, w1.view(nb, hidden, -1), b1.view(nb, hidden), w2_p.flat(dt), b2_p.flat(dt),
+            tuple(int(d) for d in module.dim_inputs), lead)
 
 
 def _dim_offsets_tensor(module, device) -> torch.Tensor:
@@ -1146,6 +1186,48 @@ class _FusedMaskMLP(torch.autograd.Function):
         return dx, dw1, db1, dw2, db2, None, None
 
 
+class _FusedMaskMLPApply(torch.autograd.Function):
+    """The stems' depth-2 mask MLPs with the mask application in their epilogue: each stem's one-pass
+    MLP kernel writes its slice of the masked spectrum in the iSTFT layout ``[B*S*C, F, T]``
+    (``mask_mlp_forward_apply``) instead of a mask; the masks are never stored.  Backward: the mask
+    gradients ``grad_est * conj(spec)`` of all stems in one pass (``mask_apply_grad_mask``), then each
+    stem's MLP backward as in :class:`_FusedMaskMLP`.  ``spec`` must not need a gradient."""
+
+    @staticmethod
+    def forward(ctx, spec, x3, channels, zero_dc, dims, extension, *params):
+        stems = len(params) // 4
+        b, fc, t = spec.shape
+        spec = spec.contiguous()
+        est = torch.empty((b * stems * channels, fc // channels, t), dtype=torch.complex64, device=spec.device)
+        saved = []
+        for s in range(stems):
+            w1, b1, w2, b2 = params[4 * s: 4 * s + 4]
+            pre, h = extension.mask_mlp_forward_apply(x3, w1, b1, w2, b2, dims, spec, est, s, channels, zero_dc,
+                                                      save_hidden=True)
+            saved += [w1, h, pre, w2]
+        ctx.save_for_backward(spec, x3, *saved)
+        ctx.meta = (channels, zero_dc, dims, stems)
+        ctx.extension = extension
+        return est
+
+    @staticmethod
+    def backward(ctx, grad_est):
+        spec, x3, *saved = ctx.saved_tensors
+        channels, zero_dc, dims, stems = ctx.meta
+        ext = ctx.extension
+        dmask = ext.mask_apply_grad_mask(grad_est, spec, stems, channels, x3.dtype, zero_dc)  # [B, S, T, 2FC]
+        m = x3.shape[0]
+        dx, grads = None, []
+        for s in range(stems):
+            w1, h, pre, w2 = saved[4 * s: 4 * s + 4]
+            go = dmask[:, s].reshape(m, -1).contiguous()
+            dz, db2, dw2 = ext.mask_estimator_final_backward_packed(go, h, pre, w2, dims, input_activation="tanh")
+            dxs, dw1, db1 = ext.grouped_linear_backward(dz, x3, w1, has_bias=True)
+            dx = dxs if dx is None else dx + dxs
+            grads += [dw1, db1, dw2, db2]
+        return (None, dx, None, None, None, None, *grads)
+
+
 def _fused_qkv_split_ok(ext: Any, qkv: torch.Tensor) -> bool:
     """The fused q/k/v split + rotary runs where the stock path would call the patched rotary."""
     _, transformer, _ = _core()
@@ -1389,6 +1471,7 @@ _CORE_PATCH_POINTS = (
     ("mel_band_roformer", "MelBandRoformer", "_band_features", "_pymsst_original_band_features"),
     ("mel_band_roformer", "MelBandRoformer", "_spectral_mask", "_pymsst_original_spectral_mask"),
     ("bs_roformer", "BSRoformer", "_masked_spectrum", "_pymsst_original_masked_spectrum"),
+    ("bs_roformer", "BSRoformer", "_mask_core", "_pymsst_original_mask_core"),
 )
 
 

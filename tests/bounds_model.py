@@ -1086,7 +1086,7 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
 MLP_TILES = {64: (2, 4, 4), 128: (4, 4, 4), 192: (6, 2, 8), 256: (8, 4, 4), 384: (12, 2, 4), 512: (16, 2, 4)}
 
 
-def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None):
+def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, apply=None):
     """mask_mlp.hip mlp_fwd_kernel (whole depth-2 mask MLP, 16-bit) on its band schedule: the b1 fill,
     the x fragments, the W1 / W2 DMA ring, the LDS fragment reads, the hidden stores and the GLU
     epilogue."""
@@ -1101,6 +1101,12 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None):
              "b2": 2 * F * esz, "pre": M * 2 * F * esz, "out": M * F * esz, "hid": M * nb * H * esz,
              "offsets": (nb + 1) * 8, "lds": S * kStage, "sb1": 2048 * 4, "tanh": 2 * 32768 * 2,
              "stab": 32768 * 2}
+    if apply is not None:
+        if M % apply["frames"] or F % (2 * apply["channels"]):
+            raise ValueError("apply: rows must be batch * frames and features 2 * channels * bins")
+        bsz = M // apply["frames"]
+        sizes["spec"] = bsz * (F // 2) * apply["frames"] * 8
+        sizes["est"] = bsz * apply["stems"] * (F // 2) * apply["frames"] * 8
     bnd = Bounds(sizes)
     if S * kStage + 32768 * 2 + 2048 * 4 > 160 * 1024:
         bnd.fail("mlp_fwd: more than 160 KB of LDS")
@@ -1194,7 +1200,19 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None):
                     ok = okj & (n < nvt) & (m < M)
                     bnd.touch("pre", (m * 2 * F + 2 * off + j) * esz, 4 * esz, ok)
                     bnd.touch("pre", (m * 2 * F + 2 * off + I + j) * esz, 4 * esz, ok)
-                    bnd.touch("out", (m * F + off + j) * esz, 4 * esz, ok)
+                    if apply is None:
+                        bnd.touch("out", (m * F + off + j) * esz, 4 * esz, ok)
+                        continue
+                    # mask application (mask_mlp_forward_apply): complex rows r0, r0 + 1 of row m
+                    fr, ch, ns, st = apply["frames"], apply["channels"], apply["stems"], apply["stem"]
+                    fbins = F // (2 * ch)
+                    mm = np.minimum(m, M - 1)
+                    bb, tt = mm // fr, mm % fr
+                    for q in range(2):
+                        r = (off + j) // 2 + q
+                        f, c = r // ch, r % ch
+                        bnd.touch("spec", ((bb * fbins * ch + r) * fr + tt) * 8, 8, ok)
+                        bnd.touch("est", ((((bb * ns + st) * ch + c) * fbins + f) * fr + tt) * 8, 8, ok)
     return bnd
 
 
@@ -1538,6 +1556,11 @@ def all_replays(name: str, esz: int):
     yield "mask_final_bwd", replay_mask_final_backward(widths, M, hidden, esz, tanh_in=True)
     if esz == 2:
         yield "mask_mlp_fwd", replay_mask_mlp_forward(widths, M, dim, hidden, esz)
+        if name in ("configs1", "configs4"):  # BS-RoFormer: stereo, bins x 2 channels x (re, im)
+            frames = {"configs1": 258, "configs4": 948}[name]
+            stems = {"configs1": 4, "configs4": 1}[name]
+            yield "mask_mlp_fwd_apply", replay_mask_mlp_forward(
+                widths, M, dim, hidden, esz, apply={"frames": frames, "channels": 2, "stems": stems, "stem": stems - 1})
     yield "rms_norm", replay_rms_norm(M * nb, dim, esz)
     for shape in qk:
         yield f"attention_gate{list(shape)}", replay_attention_gate(shape[0], shape[1], shape[2], shape[3], dim, esz)

@@ -104,3 +104,133 @@ def test_grouped_dx_register_kernel_vs_oracle(hip_ext, m, groups, i, o, dtype):
     assert_parity(dx, rdx, dn, "dx", by_index(1))
     assert_parity(dw, rdw, dn, "dW", by_index(0))
     assert_parity(db, rdb, dn, "db", by_index(0))
+
+
+APPLY_CASES = [
+    # dims, batch, frames, dim, hidden, dtype, stems, stem, channels, zero_dc
+    pytest.param(BSR_WIDTHS, 4, 258, 192, 768, torch.bfloat16, 4, 2, 2, False, id="configs1-bf16-stem2"),
+    pytest.param(BSR_WIDTHS, 4, 258, 192, 768, torch.float16, 4, 0, 2, True, id="configs1-fp16-stem0-zdc"),
+    pytest.param(BSR_WIDTHS, 2, 65, 64, 256, torch.bfloat16, 1, 0, 2, True, id="configs0-bf16-zdc"),
+    pytest.param(BSR_WIDTHS, 1, 300, 512, 2048, torch.bfloat16, 1, 0, 2, False, id="configs4-dims-bf16"),
+    pytest.param((4, 8, 12, 400, 64, 128, 4), 7, 11, 128, 96, torch.float16, 3, 1, 2, False, id="ragged-fp16"),
+    pytest.param((4, 8, 12, 400, 64, 128, 4), 7, 11, 128, 96, torch.bfloat16, 2, 1, 1, True, id="ragged-mono-zdc"),
+]
+
+
+def _complex_product_bound(spec, mask_ri):
+    """One-ulp-scale bound for re/im of ``spec * m`` computed in fp32 with or without fused
+    multiply-adds: 2^-22 (|re s||re m| + |im s||im m|) per component, componentwise."""
+    sr, si = spec.real.abs(), spec.imag.abs()
+    mr, mi = mask_ri[..., 0].abs(), mask_ri[..., 1].abs()
+    return torch.stack([sr * mr + si * mi, sr * mi + si * mr], dim=-1) * 2.0**-22
+
+
+@pytest.mark.parametrize("dims,b,t,dim,hidden,dtype,stems,stem,channels,zero_dc", APPLY_CASES)
+def test_mask_mlp_forward_apply_matches_mlp_then_apply(hip_ext, dims, b, t, dim, hidden, dtype, stems, stem,
+                                                       channels, zero_dc):
+    """The mask MLP with the mask product in its epilogue (``pmsst_mask_mlp_forward_apply``) writes
+    stem ``stem`` of the iSTFT-layout estimate equal to ``mask_mlp_forward`` followed by
+    ``mask_apply_forward`` (each pinned to the oracle above and in test_gpu_mask_apply.py), within
+    one fp32 rounding of the complex product; pre and hidden are bit-identical to
+    ``mask_mlp_forward``'s, and the other stems' slices of the estimate are not written."""
+    dn = dt_name(dtype)
+    m, total = b * t, sum(dims)
+    fc = total // 2
+    f = fc // channels
+    print(f"mask_mlp_forward_apply bands={len(dims)} b={b} t={t} dim={dim} hidden={hidden} {dn} stems={stems} "
+          f"stem={stem} channels={channels} zero_dc={zero_dc}", flush=True)
+    x, w1, b1, w2, w2s, b2 = _inputs(dims, m, dim, hidden, dtype, seed=17 + stem)
+    g = torch.Generator().manual_seed(23)
+    spec = torch.complex(torch.randn(b, fc, t, generator=g), torch.randn(b, fc, t, generator=g)).cuda()
+    sentinel = complex(7.0, -3.0)
+    est = torch.full((b * stems * channels, f, t), sentinel, dtype=torch.complex64, device="cuda")
+    pre, hid = hip_ext.mask_mlp_forward_apply(x, w1, b1, w2, b2, dims, spec, est, stem, channels, zero_dc,
+                                              save_hidden=True)
+    out_r, pre_r, hid_r = hip_ext.mask_mlp_forward(x, w1, b1, w2, b2, dims, save_hidden=True)
+    torch.cuda.synchronize()
+    assert torch.equal(pre, pre_r) and torch.equal(hid, hid_r)
+    mask = torch.zeros(b, stems, t, total, dtype=dtype, device="cuda")
+    mask[:, stem] = out_r.view(b, t, total)
+    want = hip_ext.mask_apply_forward(spec, mask, channels, zero_dc).view(b, stems, channels, f, t)
+    got = est.view(b, stems, channels, f, t)
+    others = [s for s in range(stems) if s != stem]
+    assert (got[:, others] == sentinel).all(), "stems other than `stem` were written"
+    got_s, want_s = torch.view_as_real(got[:, stem]), torch.view_as_real(want[:, stem])
+    # mask[b, t, (f*C + c)*2 + {0,1}] -> [b, c, f, t, 2], the estimate's layout
+    m_ri = mask[:, stem].float().view(b, t, f, channels, 2).permute(0, 3, 2, 1, 4)
+    s_l = spec.view(b, f, channels, t).permute(0, 2, 1, 3)
+    bound = _complex_product_bound(s_l, m_ri)
+    diff = (got_s - want_s).abs()
+    assert torch.isfinite(got_s).all()
+    assert (diff <= bound).all(), f"max excess {(diff - bound).max().item():.3e}"
+    if zero_dc:
+        assert (got_s[:, :, 0] == 0).all()
+    # the estimate against the oracle's product of the spectrum and the kernel's rounded mask
+    ref = oracle.mask_apply_forward(spec.cpu().numpy(), mask.float().cpu().numpy(), channels, zero_dc)
+    ref = ref.reshape(b, stems, channels, f, t)[:, stem]
+    ref_ri = np.stack([ref.real, ref.imag], axis=-1)
+    assert_parity(got_s, ref_ri, "f32", "est")
+    # without the hidden output: same estimate and pre-activation
+    est2 = torch.full_like(est, sentinel)
+    pre2, none = hip_ext.mask_mlp_forward_apply(x, w1, b1, w2, b2, dims, spec, est2, stem, channels, zero_dc)
+    assert none is None and torch.equal(pre2, pre) and torch.equal(est2, est)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("zero_dc", [False, True])
+def test_mask_apply_grad_mask_matches_backward(hip_ext, dtype, zero_dc):
+    """``mask_apply_grad_mask`` (no mask argument) returns ``mask_apply_backward``'s mask gradient."""
+    b, s, c, f, t = 2, 4, 2, 1025, 67
+    g = torch.Generator().manual_seed(3)
+    spec = torch.complex(torch.randn(b, f * c, t, generator=g), torch.randn(b, f * c, t, generator=g)).cuda()
+    mask = torch.randn(b, s, t, 2 * f * c, generator=g).to(dtype).cuda()
+    grad_est = torch.complex(torch.randn(b * s * c, f, t, generator=g), torch.randn(b * s * c, f, t, generator=g)).cuda()
+    want, _ = hip_ext.mask_apply_backward(grad_est, spec, mask, c, zero_dc, need_spec_grad=False)
+    got = hip_ext.mask_apply_grad_mask(grad_est, spec, s, c, dtype, zero_dc)
+    assert got.dtype == dtype and got.shape == want.shape
+    assert torch.equal(got, want)
+    gm, _ = oracle.mask_apply_backward(grad_est.cpu().numpy(), spec.cpu().numpy(), mask.float().cpu().numpy(), c, zero_dc)
+    assert_parity(got, gm, dt_name(dtype), "grad_mask")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_mask_mlp_apply_autograd_matches_two_functions(hip_ext, dtype):
+    """``_FusedMaskMLPApply`` (masks never stored) against the stems' ``_FusedMaskMLP`` outputs stacked
+    and multiplied in by ``_FusedMaskApply``: the estimate within one fp32 rounding of the product,
+    the input and parameter gradients to the 16-bit bar (both run the same backward kernels)."""
+    from pymsst_amd import fused_roformer as fr
+
+    dims, b, t, dim, hidden, stems, channels = BSR_WIDTHS, 2, 129, 192, 768, 2, 2
+    total = sum(dims)
+    fc = total // 2
+    g = torch.Generator().manual_seed(9)
+    spec = torch.complex(torch.randn(b, fc, t, generator=g), torch.randn(b, fc, t, generator=g)).cuda()
+    x0 = torch.randn(b * t, len(dims), dim, generator=g).to(dtype).cuda()
+    params = []
+    for s in range(stems):
+        _, w1, b1, w2, _, b2 = _inputs(dims, 1, dim, hidden, dtype, seed=100 + s)
+        params += [p.clone().requires_grad_(True) for p in (w1, b1, w2, b2)]
+    weight = torch.randn(b * stems * channels, fc // channels, t, 2, generator=g).cuda()
+
+    def run(fused):
+        x = x0.clone().requires_grad_(True)
+        ps = [p.detach().clone().requires_grad_(True) for p in params]
+        if fused:
+            est = fr._FusedMaskMLPApply.apply(spec, x, channels, True, dims, hip_ext, *ps)
+        else:
+            outs = [fr._FusedMaskMLP.apply(x, *ps[4 * s: 4 * s + 4], hip_ext, dims) for s in range(stems)]
+            mask = torch.stack([o.view(b, t, total) for o in outs], dim=1)
+            est = fr._FusedMaskApply.apply(spec, mask, channels, True, hip_ext)
+        (torch.view_as_real(est) * weight).sum().backward()
+        torch.cuda.synchronize()
+        return est.detach(), x.grad, [p.grad for p in ps]
+
+    est_f, dx_f, gp_f = run(True)
+    est_r, dx_r, gp_r = run(False)
+    assert (torch.view_as_real(est_f) - torch.view_as_real(est_r)).abs().max().item() <= \
+        2.0**-20 * torch.view_as_real(est_r).abs().max().item()
+    dn = dt_name(dtype)
+    assert_parity(dx_f, to_np(dx_r), dn, "dx", by_index(1))
+    names = ("w1", "b1", "w2", "b2")
+    for i, (gf, gr) in enumerate(zip(gp_f, gp_r)):
+        assert_parity(gf, to_np(gr), dn, f"stem {i // 4} {names[i % 4]}")

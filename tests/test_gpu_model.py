@@ -35,6 +35,20 @@ def hip_env(monkeypatch, hip_ext):
     fr.restore_stock_implementations()
 
 
+def _count_fused_mask_core(monkeypatch) -> list:
+    """Counts the calls of the mask MLP that multiplies the masks into the spectrum in its epilogue
+    (the patched ``_mask_core``'s fused path)."""
+    calls = []
+    original = fr._FusedMaskMLPApply.apply
+
+    def counted(*args):
+        calls.append(1)
+        return original(*args)
+
+    monkeypatch.setattr(fr._FusedMaskMLPApply, "apply", counted)
+    return calls
+
+
 def _loss_and_grads(workload, fused, target, mixture, amp_dtype, ext=None):
     model = workload.build_model("cuda", seed=4)
     model.train()
@@ -91,7 +105,7 @@ _LARGE_WL = TrainWorkload(
 )
 
 
-def test_fused_model_bf16_autocast_within_tolerance(hip_env):
+def test_fused_model_bf16_autocast_within_tolerance(hip_env, monkeypatch):
     """bf16 autocast at configs[2] (depth 6, batch 4): the fused model's loss and gradients within 2e-2
     relative (L2) of the stock modules evaluated at fp32, the precise value of the same function (a
     bf16-vs-bf16 difference would mostly measure the stock path's own rounding).  A gradient may exceed
@@ -100,8 +114,10 @@ def test_fused_model_bf16_autocast_within_tolerance(hip_env):
     target, mixture = workload_batch(_BF16_WL, seed=0, device="cuda")
     l32, g32, _ = _loss_and_grads(_BF16_WL, False, target, mixture, None)
     ls, gs, _ = _loss_and_grads(_BF16_WL, False, target, mixture, torch.bfloat16)
+    calls = _count_fused_mask_core(monkeypatch)
     lf, gf, status = _loss_and_grads(_BF16_WL, True, target, mixture, torch.bfloat16, hip_env)
     assert status.active == "cuda_ext"
+    assert calls, "the mask estimators did not run with the mask product in their epilogue"
     assert abs(lf - l32) <= 2e-2 * abs(l32), (lf, l32)
     rel = lambda a, b: ((a - b).norm() / b.norm().clamp_min(1e-30)).item()  # noqa: E731
     worst_f, worst_s, bad = 0.0, 0.0, []
@@ -116,13 +132,16 @@ def test_fused_model_bf16_autocast_within_tolerance(hip_env):
 
 
 @pytest.mark.parametrize("amp", [None, torch.bfloat16], ids=["fp32", "bf16"])
-def test_fused_model_dim512_checkpointed(hip_env, amp):
+def test_fused_model_dim512_checkpointed(hip_env, amp, monkeypatch):
     """configs[4]'s model shape (dim 512, mask hidden 2048, 1 stem, activation checkpointing) at depth 2:
     fused vs stock, fp32 to the fp32 bars, bf16 against the stock model at fp32 as above."""
     target, mixture = workload_batch(_LARGE_WL, seed=0, device="cuda")
     l32, g32, _ = _loss_and_grads(_LARGE_WL, False, target, mixture, None)
+    calls = _count_fused_mask_core(monkeypatch)
     lf, gf, status = _loss_and_grads(_LARGE_WL, True, target, mixture, amp, hip_env)
     assert status.active == "cuda_ext" and status.patched_mask_mlp
+    # the one-pass MLP (and with it the fused mask product) is 16-bit only
+    assert bool(calls) == (amp is not None)
     assert set(gf) == set(g32)
     rel = lambda a, b: ((a - b).norm() / b.norm().clamp_min(1e-30)).item()  # noqa: E731
     if amp is None:
