@@ -34,6 +34,7 @@
 
 #include "common.h"
 #include "dma_gemm.h"
+#include "ring.h"
 
 
 namespace pmsst {
@@ -83,25 +84,6 @@ constexpr int mlp_stages() {
 // 8 (l / 16) + 4 + i: together the 8 consecutive K values of its GEMM2 B fragment.
 __device__ __forceinline__ int mlp_hid_row(int t, int r) { return 8 * (r >> 2) + 4 * t + (r & 3); }
 
-// s_waitcnt vmcnt(n) for a wave-uniform n <= 12.
-__device__ __forceinline__ void vm_wait_upto(int n) {
-  switch (n) {
-    case 0: vm_wait<0>(); break;
-    case 1: vm_wait<1>(); break;
-    case 2: vm_wait<2>(); break;
-    case 3: vm_wait<3>(); break;
-    case 4: vm_wait<4>(); break;
-    case 5: vm_wait<5>(); break;
-    case 6: vm_wait<6>(); break;
-    case 7: vm_wait<7>(); break;
-    case 8: vm_wait<8>(); break;
-    case 9: vm_wait<9>(); break;
-    case 10: vm_wait<10>(); break;
-    case 11: vm_wait<11>(); break;
-    default: vm_wait<12>(); break;
-  }
-}
-
 __device__ __forceinline__ float mlp_sigmoid(float z) { return 1.0f / (1.0f + __expf(-z)); }
 
 // z pair (lo, hi) rounded to the storage dtype (round to nearest even), as packed 16-bit patterns
@@ -136,6 +118,13 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
   constexpr int D = 32 * DK;
   constexpr int kWaveRows = 16 * NT;
   constexpr int kMaxPW = (2 * DK + 8 + WV - 1) / WV;  // DMA instructions per wave and chunk, at most
+  // kLean: DMAs through dma16_m0 (the compiler does not track them, so its waits for its own LDS
+  // reads stay exact; a tracked LDS DMA makes it drain every LDS read before each use) and every
+  // wave issues kMaxPW of them per chunk (padded), so the ring waits on a compile-time count.  Dim
+  // 256 (4 waves of 64 rows) has no registers left for either and keeps the builtin DMA and its own
+  // count.
+  constexpr bool kLean = DK != 8;
+  static_assert(WV <= 2 * DK, "a wave's padding DMA repeats its first piece, which must be a W1 piece");
   __shared__ __attribute__((aligned(1024))) char lds[S * kStage];
   __shared__ __attribute__((aligned(1024))) uint16_t stab[kTanhEntries];
   __shared__ float sb1[kMlpMaxH];
@@ -160,19 +149,26 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
   // ---- DMA plan.  Instruction k of a chunk: k < 2 DK moves rows 16 (k % 2) .. + 15 of W1 K slice
   // k / 2 (1 KB); the next 2 nv2 move 16-row groups of the W2 chunk (left rows j0 + 16 q + r, then
   // gate rows I + j0 + 16 q + r; rows past the band clamped to its last row).  Groups wholly past
-  // the band are not moved (their products are never stored).  Wave w issues k = w, w + 4, ...
+  // the band are not moved (their products are never stored).  Wave w issues k = w, w + WV, ...
+  // and, with kLean, pads its share to kMaxPW with piece k = w again (same source, same LDS bytes).
   const int nv2 = (I - j0 + 15) / 16 < 4 ? (I - j0 + 15) / 16 : 4;
   const int ntot = 2 * DK + 2 * nv2;
-  const int npw = (ntot - wave + WV - 1) / WV;
+  const int npw = kLean ? kMaxPW : (ntot - wave + WV - 1) / WV;
   const int u = (lane & 3) ^ swz_k(lane >> 2);  // logical 16-byte unit this lane moves
   const char* w1b = reinterpret_cast<const char*>(w1 + static_cast<int64_t>(band) * H * D);
   const char* w2b = reinterpret_cast<const char*>(w2 + static_cast<int64_t>(2) * off * H);
   uint32_t gsrc[kMaxPW];
   uint32_t ldst[kMaxPW];
+  bool w1k[kMaxPW];
 #pragma unroll
   for (int q = 0; q < kMaxPW; ++q) {
     const int k = wave + WV * q;
-    if (k < 2 * DK) {
+    w1k[q] = k < 2 * DK || k >= ntot;
+    if (kLean && k >= ntot) {  // padding: piece k = wave (wave < WV <= 2 DK, a W1 piece)
+      const int r = 16 * (wave & 1) + (lane >> 2);
+      gsrc[q] = static_cast<uint32_t>((r * D + 32 * (wave >> 1) + 8 * u) * 2);
+      ldst[q] = static_cast<uint32_t>((wave >> 1) * 2048 + (wave & 1) * 1024);
+    } else if (k < 2 * DK) {
       const int r = 16 * (k & 1) + (lane >> 2);
       gsrc[q] = static_cast<uint32_t>((r * D + 32 * (k >> 1) + 8 * u) * 2);
       ldst[q] = static_cast<uint32_t>((k >> 1) * 2048 + (k & 1) * 1024);
@@ -187,14 +183,17 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
     }
   }
   const int nc = H / 32;
+  const uint32_t lds0 = lds_addr(lds);
   auto dma = [&](int c, int stage) {
 #pragma unroll
     for (int q = 0; q < kMaxPW; ++q) {
-      if (q < npw) {
-        const int k = wave + WV * q;
-        const char* src = k < 2 * DK ? w1b + gsrc[q] + static_cast<uint32_t>(c) * (64u * D)
-                                     : w2b + gsrc[q] + static_cast<uint32_t>(c) * 64u;
-        dma_lds16(src, lds + stage * kStage + ldst[q]);
+      if (kLean || q < npw) {
+        const char* src = w1k[q] ? w1b + gsrc[q] + static_cast<uint32_t>(c) * (64u * D)
+                                 : w2b + gsrc[q] + static_cast<uint32_t>(c) * 64u;
+        if constexpr (kLean)
+          dma16_m0(src, __builtin_amdgcn_readfirstlane(lds0 + static_cast<uint32_t>(stage * kStage) + ldst[q]));
+        else
+          dma_lds16(src, lds + stage * kStage + ldst[q]);
       }
     }
   };
@@ -215,7 +214,11 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
 #pragma unroll
   for (int q = 0; q < kTanhBytes / 1024 / WV; ++q) {
     const int k = wave + WV * q;
-    dma_lds16(reinterpret_cast<const char*>(a.tanh) + k * 1024 + lane * 16, reinterpret_cast<char*>(stab) + k * 1024);
+    if constexpr (kLean)
+      dma16_m0(reinterpret_cast<const char*>(a.tanh) + k * 1024 + lane * 16,
+               __builtin_amdgcn_readfirstlane(lds_addr(stab) + static_cast<uint32_t>(k) * 1024u));
+    else
+      dma_lds16(reinterpret_cast<const char*>(a.tanh) + k * 1024 + lane * 16, reinterpret_cast<char*>(stab) + k * 1024);
   }
 #pragma unroll
   for (int c = 0; c < S - 1; ++c) dma(c < nc ? c : nc - 1, c);
@@ -242,7 +245,8 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
   // may still be in flight; loads complete in order) and its LDS reads are done, then every wave's
   // are (barrier), so the stage chunk c - 1 used is free for chunk c + S - 1
   auto ring_step = [&](int c) {
-    vm_wait_upto((S - 2) * npw);
+    if constexpr (kLean) vm_wait<(S - 2) * kMaxPW>();
+    else ring_vm_wait<(S - 2) * kMaxPW>((S - 2) * npw);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");

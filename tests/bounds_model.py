@@ -1137,12 +1137,17 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
         bnd.touch("stab", np.array([0, 0x7FFF]) * 2, 2)  # table reads: index = pattern & 0x7fff
         nv2 = min(4, cdiv(I - j0, 16))
         ntot = 2 * DK + 2 * nv2
+        if WV > 2 * DK:
+            bnd.fail("mlp_fwd: a wave's padding DMA would not repeat a W1 piece")
         for wave in range(WV):
             npw = (ntot - wave + WV - 1) // WV
             if npw > kmax_pw:
                 bnd.fail("mlp_fwd: more DMA instructions than the plan holds")
-            for q in range(npw):
-                k = wave + WV * q
+            # with padding (all but dim 256) every wave issues kmax_pw DMAs, those past its share
+            # repeating piece k = wave
+            pad = DK != 8  # kLean
+            for q in range(kmax_pw if pad else npw):
+                k = wave + WV * q if q < npw else wave
                 if k < 2 * DK:
                     r = 16 * (k & 1) + (lane >> 2)
                     gsrc = (r * D + 32 * (k >> 1) + 8 * u) * 2
