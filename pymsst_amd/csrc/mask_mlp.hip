@@ -21,7 +21,8 @@
 // The W1 chunk (32 x D) and the W2 chunk (128 x 32) of the block's band move from HBM/L2 into a
 // ring of LDS stages by global -> LDS DMA, shared by the waves.  Epilogue: bias, GLU, stores.
 // Bands wider than 64 take several passes, each recomputing GEMM1 (the price of keeping every
-// accumulator in registers).
+// accumulator in registers).  A pass whose band part has 1 or 2 groups of 16 GLU outputs per half
+// runs an instance of the block with 2 or 4 GEMM2 tiles instead of 8.
 //
 // tanh: z is rounded to the storage dtype before the tanh (the reference's grouped Linear output),
 // so tanh is a function of 16 bits.  A 64 KB table of the correctly rounded tanh of every
@@ -94,30 +95,25 @@ __device__ __forceinline__ uint32_t round_pair(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, t2));
 }
 
-// tanh of a packed pair from the LDS table (index = the pattern without its sign; tanh is odd)
-__device__ __forceinline__ uint32_t tanh_pair(uint32_t zp, const uint16_t* tab) {
-  const uint32_t lo = tab[zp & 0x7fffu];
-  const uint32_t hi = tab[(zp >> 16) & 0x7fffu];
-  return (lo | (hi << 16)) | (zp & 0x80008000u);
-}
-
 // LDS fragment read the compiler schedules and waits for itself (no inline asm: a value of an asm
 // read is not known to be in flight, so the compiler may copy its register before the explicit wait).
 __device__ __forceinline__ u32x4_t lds_frag(const char* lds, uint32_t off) {
   return *reinterpret_cast<const u32x4_t*>(lds + off);
 }
 
-template <typename T, int DK, int NT, int WV, bool WRITE_H, bool APPLY>
-__global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ x, const T* __restrict__ w1,
-                                                      const T* __restrict__ b1, const T* __restrict__ w2,
-                                                      const T* __restrict__ b2, T* __restrict__ pre,
-                                                      T* __restrict__ out, T* __restrict__ hid, MlpArgs a,
-                                                      BandSched sc) {
+// One block of the kernel below, for a pass whose band has NV (1, 2 or 4) 16-row groups of GLU
+// outputs in each half: GEMM2 runs 2 NV tiles (left 0 .. NV - 1, gate NV .. 2 NV - 1 of acc2).
+template <typename T, int DK, int NT, int WV, bool WRITE_H, bool APPLY, int NV>
+__device__ __forceinline__ void mlp_fwd_block(const T* __restrict__ x, const T* __restrict__ w1,
+                                              const T* __restrict__ b1, const T* __restrict__ w2,
+                                              const T* __restrict__ b2, T* __restrict__ pre, T* __restrict__ out,
+                                              T* __restrict__ hid, const MlpArgs& a, char* lds, uint16_t* stab,
+                                              float* sb1, int band, uint32_t mt, uint32_t pass, int off, int I) {
   constexpr int S = mlp_stages<DK>();
   constexpr int kStage = mlp_stage_bytes<DK>();
   constexpr int D = 32 * DK;
   constexpr int kWaveRows = 16 * NT;
-  constexpr int kMaxPW = (2 * DK + 8 + WV - 1) / WV;  // DMA instructions per wave and chunk, at most
+  constexpr int kMaxPW = (2 * DK + 2 * NV + WV - 1) / WV;  // DMA instructions per wave and chunk, at most
   // kLean: DMAs through dma16_m0 (the compiler does not track them, so its waits for its own LDS
   // reads stay exact; a tracked LDS DMA makes it drain every LDS read before each use) and every
   // wave issues kMaxPW of them per chunk (padded), so the ring waits on a compile-time count.  Dim
@@ -125,15 +121,6 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
   // count.
   constexpr bool kLean = DK != 8;
   static_assert(WV <= 2 * DK, "a wave's padding DMA repeats its first piece, which must be a W1 piece");
-  __shared__ __attribute__((aligned(1024))) char lds[S * kStage];
-  __shared__ __attribute__((aligned(1024))) uint16_t stab[kTanhEntries];
-  __shared__ float sb1[kMlpMaxH];
-
-  int band;
-  uint32_t mt, pass, npass;
-  if (!sched_block<true>(sc, band, mt, pass, npass)) return;
-  const int off = static_cast<int>(a.offsets[band]);
-  const int I = static_cast<int>(a.offsets[band + 1]) - off;
   const int j0 = static_cast<int>(pass) * kMlpJ;
   const int H = a.H;
   const int tid = threadIdx.x;
@@ -151,7 +138,7 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
   // gate rows I + j0 + 16 q + r; rows past the band clamped to its last row).  Groups wholly past
   // the band are not moved (their products are never stored).  Wave w issues k = w, w + WV, ...
   // and, with kLean, pads its share to kMaxPW with piece k = w again (same source, same LDS bytes).
-  const int nv2 = (I - j0 + 15) / 16 < 4 ? (I - j0 + 15) / 16 : 4;
+  const int nv2 = (I - j0 + 15) / 16 < NV ? (I - j0 + 15) / 16 : NV;
   const int ntot = 2 * DK + 2 * nv2;
   const int npw = kLean ? kMaxPW : (ntot - wave + WV - 1) / WV;
   const int u = (lane & 3) ^ swz_k(lane >> 2);  // logical 16-byte unit this lane moves
@@ -223,9 +210,9 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
 #pragma unroll
   for (int c = 0; c < S - 1; ++c) dma(c < nc ? c : nc - 1, c);
 
-  f32x4_t acc2[8][NT];
+  f32x4_t acc2[2 * NV][NT];
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
+  for (int t = 0; t < 2 * NV; ++t)
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc2[t][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
@@ -237,8 +224,10 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
     a1off[t] = static_cast<uint32_t>(r * 64 + 16 * (g ^ swz_k(r & 15)));
   }
   const uint32_t a2off = static_cast<uint32_t>(DK * 2048 + rr * 64 + 16 * (g ^ swz_k(rr)));
-  // GEMM2 row tiles t (left 0..3, gate 4..7) with rows inside the band
-  const int nt2 = nv2;  // left tiles 0 .. nv2 - 1 and gate tiles 4 .. 4 + nv2 - 1
+  // GEMM2 row tiles: left 0 .. NV - 1 and gate NV .. 2 NV - 1 (acc2 index), the stage's W2 groups
+  // t and 4 + t; tiles t >= nv2 (NV = 4 with 3 groups) hold stale LDS data and feed accumulators
+  // that are never stored
+  const int nt2 = nv2;
 
   // ---- per-chunk pieces
   // ring step of chunk c: this wave's DMAs of chunk c have landed (only chunks c + 1 .. c + S - 2
@@ -273,12 +262,12 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
       }
     }
   };
-  // GEMM2 A fragments of chunk c (all 8 row tiles; tiles past the band hold stale LDS data and feed
-  // accumulators that are never stored: skipping them per block costs registers (spills) instead)
-  auto read_fb = [&](int c, u32x4_t (&fb)[8]) {
+  // GEMM2 A fragments of chunk c (the 2 NV tiles; skipping tiles per block at run time costs
+  // registers (spills), hence the NV instances)
+  auto read_fb = [&](int c, u32x4_t (&fb)[2 * NV]) {
     const char* sb = lds + (c % S) * kStage;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) fb[t] = lds_frag(sb, a2off + 1024u * t);
+    for (int t = 0; t < 2 * NV; ++t) fb[t] = lds_frag(sb, a2off + 1024u * (t < NV ? t : 4 + t - NV));
   };
   // z pairs in the stored dtype (word k of tile n: hidden 8 g + 2 k, + 1) and their table reads
   auto tanh_issue = [&](const f32x4_t (&acc)[2][NT], uint32_t (&zp)[NT][4], uint32_t (&th)[NT][8]) {
@@ -312,9 +301,9 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
       }
     }
   };
-  auto gemm2 = [&](const u32x4_t (&fb)[8], const u32x4_t (&hb)[NT]) {
+  auto gemm2 = [&](const u32x4_t (&fb)[2 * NV], const u32x4_t (&hb)[NT]) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
+    for (int t = 0; t < 2 * NV; ++t)
 #pragma unroll
       for (int n = 0; n < NT; ++n) acc2[t][n] = mfma_raw<T>(fb[t], hb[n], acc2[t][n]);
   };
@@ -322,7 +311,7 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
   // ---- software pipeline over the chunks: iteration c runs GEMM1(c) while the table reads of chunk
   // c - 1 are in flight, then GEMM2(c - 1) with the fragments read in iteration c - 1
   f32x4_t accA[2][NT], accB[2][NT];
-  u32x4_t fbp[8], hbp[NT];
+  u32x4_t fbp[2 * NV], hbp[NT];
   uint32_t zp[NT][4], th[NT][8];
   ring_step(0);
   if (nvt > 0) {
@@ -361,11 +350,11 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
   if (nvt == 0) return;
 
   // ---- epilogue: lane holds pre columns j0 + 16 t + 4 g + i (left, tile t) and the same + I
-  // (gate, tile t + 4) of rows wrow0 + 16 n + rr.  I is a multiple of 4 (host check): the 4
+  // (gate, tile NV + t) of rows wrow0 + 16 n + rr.  I is a multiple of 4 (host check): the 4
   // outputs of a lane are all inside the band or all outside.
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < NV; ++t) {
     const int j = j0 + 16 * t + 4 * g;
     if (t >= nt2 || j >= I) continue;
     float bl[4], bg[4];
@@ -379,8 +368,12 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         vl[i] = acc2[t][n][i] + bl[i];
-        vg[i] = acc2[t + 4][n][i] + bg[i];
+        vg[i] = acc2[NV + t][n][i] + bg[i];
         vo[i] = vl[i] * mlp_sigmoid(vg[i]);
+        // the GLU output rounded to fp32 before its 16-bit conversion, as torch and the reference
+        // round it: the empty asm keeps the product in a register, or the compiler may fuse product
+        // and fp16 conversion into a v_fma_mixlo_f16 that rounds once (one fp16 ulp away at times)
+        asm volatile("" : "+v"(vo[i]));
       }
       T* pl = pre + m * pitch2 + 2 * off + j;
       store_pack<T, 4>(pl, vl);
@@ -396,12 +389,8 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
         for (int q = 0; q < 2; ++q) {
           const int r = r0 + q;
           const int f = r / ap.C, c = r - f * ap.C;
-          // the mask rounded as the stored mask is: the fp32 product, then the 16-bit conversion (the
-          // empty asm keeps the product in a register, or the compiler fuses product and fp16
-          // conversion into a v_fma_mixlo_f16 that rounds once and can land one fp16 ulp away)
-          float pr = vo[2 * q], pi = vo[2 * q + 1];
-          asm volatile("" : "+v"(pr), "+v"(pi));
-          const float mr = to_f32(from_f32<T>(pr)), mi = to_f32(from_f32<T>(pi));
+          // the mask rounded to the storage dtype, as the stored mask is
+          const float mr = to_f32(from_f32<T>(vo[2 * q])), mi = to_f32(from_f32<T>(vo[2 * q + 1]));
           const float2 sv = ap.spec[(static_cast<int64_t>(bb) * ap.Fbins * ap.C + r) * ap.frames.d + tt];
           float2 e = make_float2(sv.x * mr - sv.y * mi, sv.x * mi + sv.y * mr);
           if (ap.zero_dc && f == 0) e = make_float2(0.f, 0.f);
@@ -413,6 +402,34 @@ __global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ 
       }
     }
   }
+}
+
+template <typename T, int DK, int NT, int WV, bool WRITE_H, bool APPLY>
+__global__ __launch_bounds__(64 * WV) void mlp_fwd_kernel(const T* __restrict__ x, const T* __restrict__ w1,
+                                                      const T* __restrict__ b1, const T* __restrict__ w2,
+                                                      const T* __restrict__ b2, T* __restrict__ pre,
+                                                      T* __restrict__ out, T* __restrict__ hid, MlpArgs a,
+                                                      BandSched sc) {
+  __shared__ __attribute__((aligned(1024))) char lds[mlp_stages<DK>() * mlp_stage_bytes<DK>()];
+  __shared__ __attribute__((aligned(1024))) uint16_t stab[kTanhEntries];
+  __shared__ float sb1[kMlpMaxH];
+
+  int band;
+  uint32_t mt, pass, npass;
+  if (!sched_block<true>(sc, band, mt, pass, npass)) return;
+  const int off = static_cast<int>(a.offsets[band]);
+  const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  const int groups = (I - static_cast<int>(pass) * kMlpJ + 15) / 16;  // 16-row groups of this pass, 1 .. 4+
+  // the widest instance first: in this order none of the three spills registers
+  if (groups >= 3)
+    mlp_fwd_block<T, DK, NT, WV, WRITE_H, APPLY, 4>(x, w1, b1, w2, b2, pre, out, hid, a, lds, stab, sb1, band, mt,
+                                                    pass, off, I);
+  else if (groups == 2)
+    mlp_fwd_block<T, DK, NT, WV, WRITE_H, APPLY, 2>(x, w1, b1, w2, b2, pre, out, hid, a, lds, stab, sb1, band, mt,
+                                                    pass, off, I);
+  else
+    mlp_fwd_block<T, DK, NT, WV, WRITE_H, APPLY, 1>(x, w1, b1, w2, b2, pre, out, hid, a, lds, stab, sb1, band, mt,
+                                                    pass, off, I);
 }
 
 // ------------------------------------------------------------------ host side
@@ -493,8 +510,9 @@ int launch_dk(const void* x, const void* w1, const void* b1, const void* w2, con
   BandSched sc;
   uint32_t per_xcd = 0;
   const int64_t rows_per_block = 16 * NT * WV;
-  // every block runs all H / 32 chunks with the same MFMA count: an even split of the blocks over the
-  // XCDs (units of one band stay contiguous, so its weight chunks are shared in one L2 but at the seams)
+  // an even split of the blocks over the XCDs (units of one band stay contiguous, so its weight chunks
+  // are shared in one L2 but at the seams).  Narrow passes (NV 1 or 2) run fewer GEMM2 tiles, but
+  // measured they take nearly the time of full ones (a split weighted by MFMA count was slower).
   if (!build_even_sched(a.NB, (a.M + rows_per_block - 1) / rows_per_block,
                         [&](int b) { return (dim_inputs[b] + kMlpJ - 1) / kMlpJ; }, &sc, &per_xcd))
     return fail(PMSST_EINVAL, "mask_mlp_forward: too many bands or rows for the block schedule");

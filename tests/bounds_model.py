@@ -1116,6 +1116,11 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
     wave_rows = 16 * NT
     mtiles = cdiv(M, WV * wave_rows)
     units = lambda b: cdiv(widths[b], J)  # noqa: E731
+
+    def nv_of(b, p):  # the kernel's instance: 1, 2 or 4 16-row output groups per half
+        groups = cdiv(widths[b] - J * p, 16)
+        return 4 if groups >= 3 else groups
+
     sc = build_even_sched(nb, mtiles, units)
     decoded = sched_decode(sc, nb, units, True, bnd, "mlp_fwd")
     tid = np.arange(64 * WV)
@@ -1123,10 +1128,11 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
     g, rr = lane >> 4, lane & 15
     u = (lane & 3) ^ swz_k(lane >> 2)
     nc = H // 32
-    kmax_pw = (2 * DK + 8 + WV - 1) // WV
     for band, mt, pss in sorted({(b, m, p) for b, m, p in decoded if m in (0, mtiles - 1)}):
         off, I = int(offs[band]), int(widths[band])
         j0 = pss * J
+        NV = nv_of(band, pss)
+        kmax_pw = (2 * DK + 2 * NV + WV - 1) // WV
         for i0 in range(0, H, 64 * WV):
             i = i0 + tid
             bnd.touch("b1", (band * H + i) * esz, esz, i < H)
@@ -1135,7 +1141,7 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
             bnd.touch("tanh", k * 1024 + lane * 16, 16)
             bnd.touch("stab", k * 1024 + lane * 16, 16)
         bnd.touch("stab", np.array([0, 0x7FFF]) * 2, 2)  # table reads: index = pattern & 0x7fff
-        nv2 = min(4, cdiv(I - j0, 16))
+        nv2 = min(NV, cdiv(I - j0, 16))
         ntot = 2 * DK + 2 * nv2
         if WV > 2 * DK:
             bnd.fail("mlp_fwd: a wave's padding DMA would not repeat a W1 piece")
@@ -1187,15 +1193,15 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
                     for s_ in range(DK):
                         bnd.touch("lds", sb + a1 + 2048 * s_, 16)
                 a2 = DK * 2048 + rr * 64 + 16 * (g ^ swz_k(rr))
-                for t in range(8):  # all 8 GEMM2 row tiles are read
-                    bnd.touch("lds", sb + a2 + 1024 * t, 16)
+                for t in range(2 * NV):  # the instance's 2 NV GEMM2 row tiles (W2 groups t, 4 + t)
+                    bnd.touch("lds", sb + a2 + 1024 * (t if t < NV else 4 + t - NV), 16)
             for c in steps(nc):
                 bnd.touch("sb1", (32 * c + 8 * g) * 4, 32)
                 if write_h:
                     for n in range(NT):
                         m = wrow0 + 16 * n + rr
                         bnd.touch("hid", ((m * nb + band) * H + 32 * c + 8 * g) * esz, 16, (n < nvt) & (m < M))
-            for t in range(4):
+            for t in range(NV):
                 j = j0 + 16 * t + 4 * g
                 okj = (t < nv2) & (j < I)
                 bnd.touch("b2", (2 * off + j) * esz, 4 * esz, okj)
