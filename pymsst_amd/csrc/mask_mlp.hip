@@ -351,24 +351,59 @@ __device__ __forceinline__ void mlp_fwd_block(const T* __restrict__ x, const T* 
 
   // ---- epilogue: lane holds pre columns j0 + 16 t + 4 g + i (left, tile t) and the same + I
   // (gate, tile NV + t) of rows wrow0 + 16 n + rr.  I is a multiple of 4 (host check): the 4
-  // outputs of a lane are all inside the band or all outside.
+  // outputs of a lane are all inside the band or all outside.  Every load of the epilogue (b2, and
+  // the spectrum with APPLY) is issued first, from addresses clamped into the band and the rows, so
+  // the block waits for one memory latency instead of one per tile.
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
+  // the lane's row and column indices pass an empty asm here, so the compiler cannot compute the
+  // epilogue's addresses before the main loop (where they would take registers from it)
+  int ge = g, rre = rr;
+  asm volatile("" : "+v"(ge), "+v"(rre));
+  float bl[NV][4], bg[NV][4];
 #pragma unroll
   for (int t = 0; t < NV; ++t) {
-    const int j = j0 + 16 * t + 4 * g;
-    if (t >= nt2 || j >= I) continue;
-    float bl[4], bg[4];
-    load_pack<T, 4>(b2 + 2 * off + j, bl);
-    load_pack<T, 4>(b2 + 2 * off + I + j, bg);
+    const int jt = j0 + 16 * t + 4 * ge;
+    const int jc = t < nt2 && jt < I ? jt : I - 4;
+    load_pack<T, 4>(b2 + 2 * off + jc, bl[t]);
+    load_pack<T, 4>(b2 + 2 * off + I + jc, bg[t]);
+  }
+  // APPLY: the lane's 4 outputs of tile t are the (re, im) pairs of complex rows r0 and r0 + 1
+  // (off + j is a multiple of 4); lanes rr = 0..15 hold consecutive rows m, i.e. consecutive frames
+  [[maybe_unused]] float2 spv[NV][NT][2];
+  [[maybe_unused]] uint32_t bbn[NT], ttn[NT];
+  if constexpr (APPLY) {
+    const MlpApply& ap = a.ap;
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
-      const int64_t m = wrow0 + 16 * n + rr;
+      const int64_t m = wrow0 + 16 * n + rre;
+      const uint32_t um = static_cast<uint32_t>(m < a.M ? m : a.M - 1);
+      bbn[n] = ap.frames.div(um);
+      ttn[n] = um - bbn[n] * ap.frames.d;
+    }
+#pragma unroll
+    for (int t = 0; t < NV; ++t) {
+      const int jt = j0 + 16 * t + 4 * ge;
+      const int r0 = (off + (t < nt2 && jt < I ? jt : I - 4)) >> 1;
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          spv[t][n][q] = ap.spec[(static_cast<int64_t>(bbn[n]) * ap.Fbins * ap.C + r0 + q) * ap.frames.d + ttn[n]];
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NV; ++t) {
+    const int j = j0 + 16 * t + 4 * ge;
+    if (t >= nt2 || j >= I) continue;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int64_t m = wrow0 + 16 * n + rre;
       if (n >= nvt || m >= a.M) continue;
       float vl[4], vg[4], vo[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        vl[i] = acc2[t][n][i] + bl[i];
-        vg[i] = acc2[NV + t][n][i] + bg[i];
+        vl[i] = acc2[t][n][i] + bl[t][i];
+        vg[i] = acc2[NV + t][n][i] + bg[t][i];
         vo[i] = vl[i] * mlp_sigmoid(vg[i]);
         // the GLU output rounded to fp32 before its 16-bit conversion, as torch and the reference
         // round it: the empty asm keeps the product in a register, or the compiler may fuse product
@@ -379,11 +414,7 @@ __device__ __forceinline__ void mlp_fwd_block(const T* __restrict__ x, const T* 
       store_pack<T, 4>(pl, vl);
       store_pack<T, 4>(pl + I, vg);
       if constexpr (APPLY) {
-        // the lane's 4 outputs are the (re, im) pairs of complex rows r0 and r0 + 1 (off + j is a
-        // multiple of 4); lanes rr = 0..15 hold consecutive rows m, i.e. consecutive frames
         const MlpApply& ap = a.ap;
-        const uint32_t um = static_cast<uint32_t>(m);
-        const uint32_t bb = ap.frames.div(um), tt = um - bb * ap.frames.d;
         const int r0 = (off + j) >> 1;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
@@ -391,11 +422,12 @@ __device__ __forceinline__ void mlp_fwd_block(const T* __restrict__ x, const T* 
           const int f = r / ap.C, c = r - f * ap.C;
           // the mask rounded to the storage dtype, as the stored mask is
           const float mr = to_f32(from_f32<T>(vo[2 * q])), mi = to_f32(from_f32<T>(vo[2 * q + 1]));
-          const float2 sv = ap.spec[(static_cast<int64_t>(bb) * ap.Fbins * ap.C + r) * ap.frames.d + tt];
+          const float2 sv = spv[t][n][q];
           float2 e = make_float2(sv.x * mr - sv.y * mi, sv.x * mi + sv.y * mr);
           if (ap.zero_dc && f == 0) e = make_float2(0.f, 0.f);
-          ap.est[((static_cast<int64_t>(bb) * ap.S + ap.s) * ap.C + c) * static_cast<int64_t>(ap.Fbins) * ap.frames.d +
-                 static_cast<int64_t>(f) * ap.frames.d + tt] = e;
+          ap.est[((static_cast<int64_t>(bbn[n]) * ap.S + ap.s) * ap.C + c) * static_cast<int64_t>(ap.Fbins) *
+                     ap.frames.d +
+                 static_cast<int64_t>(f) * ap.frames.d + ttn[n]] = e;
         }
       } else {
         store_pack<T, 4>(out + m * a.F + off + j, vo);

@@ -1201,11 +1201,24 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
                     for n in range(NT):
                         m = wrow0 + 16 * n + rr
                         bnd.touch("hid", ((m * nb + band) * H + 32 * c + 8 * g) * esz, 16, (n < nvt) & (m < M))
+            # epilogue loads first, from addresses clamped into the band (and rows, for the spectrum)
+            for t in range(NV):
+                jt = j0 + 16 * t + 4 * g
+                jc = np.where((t < nv2) & (jt < I), jt, I - 4)
+                bnd.touch("b2", (2 * off + jc) * esz, 4 * esz)
+                bnd.touch("b2", (2 * off + I + jc) * esz, 4 * esz)
+                if apply is not None:
+                    fr, ch = apply["frames"], apply["channels"]
+                    fbins = F // (2 * ch)
+                    for n in range(NT):
+                        mm = np.minimum(wrow0 + 16 * n + rr, M - 1)
+                        bb, tt = mm // fr, mm % fr
+                        for q in range(2):
+                            r = (off + jc) // 2 + q
+                            bnd.touch("spec", ((bb * fbins * ch + r) * fr + tt) * 8, 8)
             for t in range(NV):
                 j = j0 + 16 * t + 4 * g
                 okj = (t < nv2) & (j < I)
-                bnd.touch("b2", (2 * off + j) * esz, 4 * esz, okj)
-                bnd.touch("b2", (2 * off + I + j) * esz, 4 * esz, okj)
                 for n in range(NT):
                     m = wrow0 + 16 * n + rr
                     ok = okj & (n < nvt) & (m < M)
@@ -1222,7 +1235,6 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
                     for q in range(2):
                         r = (off + j) // 2 + q
                         f, c = r // ch, r % ch
-                        bnd.touch("spec", ((bb * fbins * ch + r) * fr + tt) * 8, 8, ok)
                         bnd.touch("est", ((((bb * ns + st) * ch + c) * fbins + f) * fr + tt) * 8, 8, ok)
     return bnd
 
