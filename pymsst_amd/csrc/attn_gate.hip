@@ -21,9 +21,14 @@
 // kernel mirrors it, hands the per-head gpre to every lane with readlane for grad_x, and keeps
 // each lane's [D/64][H] slice of grad_W in registers; blocks fold their waves in order and the
 // deterministic column sum over blocks finishes grad_W / grad_b.  Each wave takes two tokens per
-// loop trip with every load of both issued first.
+// loop trip, software-pipelined: the next trip's loads (raw 16-byte packs) are issued before this
+// trip's stores, so waiting for them never waits for the stores (vmcnt counts loads and stores in
+// issue order).  The grids hold as many blocks as fit on the device at once, so a block's staging of
+// W is spread over as many tokens as possible.
 //
 // Any other shape runs the generic kernels (one wave per token, one head at a time).
+#include <algorithm>
+
 #include "common.h"
 #include "rowgeom.h"
 
@@ -100,7 +105,7 @@ __device__ __forceinline__ float head_sums(float (&p)[1 << LOGH], int lane) {
 // ------------------------------------------------------------------ fast forward
 
 // Rows per wave per loop trip: the loads of both rows (attention packs and x slices) are
-// issued before any arithmetic, so no global-memory latency sits inside the dot loop.
+// issued a trip ahead, so no global-memory latency sits inside the dot loop.
 constexpr int kGateRows = 2;
 
 template <typename T, int E, int LOGH, int JX>
@@ -119,26 +124,35 @@ __global__ __launch_bounds__(kGateThreads) void gate_fwd_kernel(const T* __restr
   const int head = lane / LPH;
   const int sub = lane - head * LPH;
   const float bh = to_f32(bias[head]);
-  for (int64_t m0 = (static_cast<int64_t>(blockIdx.x) * kGateWaves + wave) * R; m0 < rows;
-       m0 += static_cast<int64_t>(gridDim.x) * kGateWaves * R) {
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kGateWaves * R;
+  int64_t m0 = (static_cast<int64_t>(blockIdx.x) * kGateWaves + wave) * R;
+  // rows past the end load the last row (their results are not stored)
+  Pack<T, E> ap[R];
+  T xr[R][JX];
+  auto load = [&](int64_t mb) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t m = mb + r < rows ? mb + r : rows - 1;
+      ap[r] = *reinterpret_cast<const Pack<T, E>*>(token_base(attn, ar, static_cast<uint32_t>(m)) + head * ar.sh +
+                                                   sub * E);
+#pragma unroll
+      for (int j = 0; j < JX; ++j) {
+        const int i = lane + j * kWave;
+        xr[r][j] = x[m * dim + (i < dim ? i : 0)];
+      }
+    }
+  };
+  if (m0 < rows) load(m0);
+  for (; m0 < rows; m0 += step) {
     float a[R][E], xv[R][JX];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t m = m0 + r;
-      if (m < rows) {
-        load_pack<T, E>(token_base(attn, ar, static_cast<uint32_t>(m)) + head * ar.sh + sub * E, a[r]);
 #pragma unroll
-        for (int j = 0; j < JX; ++j) {
-          const int i = lane + j * kWave;
-          xv[r][j] = i < dim ? to_f32(x[m * dim + i]) : 0.f;
-        }
-      } else {
+      for (int e = 0; e < E; ++e) a[r][e] = to_f32(ap[r].v[e]);
 #pragma unroll
-        for (int e = 0; e < E; ++e) a[r][e] = 0.f;
-#pragma unroll
-        for (int j = 0; j < JX; ++j) xv[r][j] = 0.f;
-      }
+      for (int j = 0; j < JX; ++j) xv[r][j] = lane + j * kWave < dim ? to_f32(xr[r][j]) : 0.f;
     }
+    if (m0 + step < rows) load(m0 + step);
     float p[R][H];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -203,23 +217,41 @@ __global__ __launch_bounds__(kGateThreads) void gate_bwd_kernel(
 #pragma unroll
     for (int h = 0; h < H; ++h) acc[j][h] = 0.f;
 
-  for (int64_t m0 = (static_cast<int64_t>(blockIdx.x) * kGateWaves + wave) * R; m0 < rows;
-       m0 += static_cast<int64_t>(gridDim.x) * kGateWaves * R) {
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kGateWaves * R;
+  int64_t m0 = (static_cast<int64_t>(blockIdx.x) * kGateWaves + wave) * R;
+  // rows past the end load the last row (their results are not stored)
+  Pack<T, E> gp[R], ap[R];
+  T gtr[R], xr[R][JX];
+  auto load = [&](int64_t mb) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t m = mb + r < rows ? mb + r : rows - 1;
+      gp[r] = *reinterpret_cast<const Pack<T, E>*>(grad_out + m * (H * LPH * E) + lane * E);
+      ap[r] = *reinterpret_cast<const Pack<T, E>*>(token_base(attn, ar, static_cast<uint32_t>(m)) + head * ar.sh +
+                                                   sub * E);
+      gtr[r] = gate[m * H + head];
+#pragma unroll
+      for (int j = 0; j < JX; ++j) {
+        const int i = lane + j * kWave;
+        xr[r][j] = x[m * dim + (i < dim ? i : 0)];
+      }
+    }
+  };
+  if (m0 < rows) load(m0);
+  for (; m0 < rows; m0 += step) {
     float g[R][E], a[R][E], gf[R], xv[R][JX];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t m = m0 + r;
-      if (m < rows) {
-        load_pack<T, E>(grad_out + m * (H * LPH * E) + lane * E, g[r]);
-        load_pack<T, E>(token_base(attn, ar, static_cast<uint32_t>(m)) + head * ar.sh + sub * E, a[r]);
-        gf[r] = to_f32(gate[m * H + head]);
 #pragma unroll
-        for (int j = 0; j < JX; ++j) {
-          const int i = lane + j * kWave;
-          xv[r][j] = i < dim ? to_f32(x[m * dim + i]) : 0.f;
-        }
+      for (int e = 0; e < E; ++e) {
+        g[r][e] = to_f32(gp[r].v[e]);
+        a[r][e] = to_f32(ap[r].v[e]);
       }
+      gf[r] = to_f32(gtr[r]);
+#pragma unroll
+      for (int j = 0; j < JX; ++j) xv[r][j] = lane + j * kWave < dim ? to_f32(xr[r][j]) : 0.f;
     }
+    if (m0 + step < rows) load(m0 + step);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t m = m0 + r;
@@ -427,6 +459,15 @@ inline int gate_blocks(int64_t rows, int rows_per_wave, int max_blocks) {
   return static_cast<int>(b < max_blocks ? b : max_blocks);
 }
 
+// Blocks of a kGateThreads-thread kernel with `shmem` bytes of dynamic LDS that fit on the device at
+// once (at least one per CU).
+inline int gate_resident_blocks(const void* kernel, size_t shmem) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGateThreads, shmem) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  return per_cu * num_cus();
+}
+
 // Blocks of the fused backward = rows of its grad_W / grad_b partials.
 constexpr int kGateBwdMaxBlocks = 1024;
 
@@ -501,8 +542,11 @@ int launch_gate_fwd(const void* attn, const int64_t* attn_strides, const void* x
   const int jx = gate_jx(s.dim);
   const size_t shmem = static_cast<size_t>(s.heads * s.dim) * sizeof(float);
 #define PMSST_GF(E, LOGH, JX)                                                                                  \
-  hipLaunchKernelGGL((gate_fwd_kernel<T, E, LOGH, JX>), dim3(blocks), dim3(kGateThreads), shmem, stream, pa, ar, \
-                     px, pw, pb, po, pg, rows, dim)
+  hipLaunchKernelGGL((gate_fwd_kernel<T, E, LOGH, JX>),                                                          \
+                     dim3(std::min(blocks, gate_resident_blocks(reinterpret_cast<const void*>(                    \
+                                                                   &gate_fwd_kernel<T, E, LOGH, JX>),             \
+                                                               shmem))),                                          \
+                     dim3(kGateThreads), shmem, stream, pa, ar, px, pw, pb, po, pg, rows, dim)
 #define PMSST_GF_J(E, LOGH)                  \
   do {                                       \
     if (jx == 1) PMSST_GF(E, LOGH, 1);       \
@@ -593,9 +637,14 @@ int launch_gate_bwd(const void* grad_out, const void* attn, const int64_t* attn_
       nparts = gate_blocks(rows, kGateRows, kGateBwdMaxBlocks);
       const int jx = gate_jx(s.dim);
       const size_t shmem = static_cast<size_t>(2 * s.heads * s.dim + s.heads) * sizeof(float);
+      // (as many blocks as fit on the device at once; nparts is also the partial rows' count)
 #define PMSST_GB(E, LOGH, JX)                                                                                   \
-  hipLaunchKernelGGL((gate_bwd_kernel<T, E, LOGH, JX>), dim3(nparts), dim3(kGateThreads), shmem, stream, pgo, pa, \
-                     ar, px, pw_, pg, pga, gr, pgx, pw, pbias, rows, dim)
+  do {                                                                                                          \
+    nparts = std::min(nparts, gate_resident_blocks(reinterpret_cast<const void*>(&gate_bwd_kernel<T, E, LOGH, JX>), \
+                                                   shmem));                                                     \
+    hipLaunchKernelGGL((gate_bwd_kernel<T, E, LOGH, JX>), dim3(nparts), dim3(kGateThreads), shmem, stream, pgo,  \
+                       pa, ar, px, pw_, pg, pga, gr, pgx, pw, pbias, rows, dim);                                \
+  } while (0)
 #define PMSST_GB_J(E, LOGH)                  \
   do {                                       \
     if (jx == 1) PMSST_GB(E, LOGH, 1);       \

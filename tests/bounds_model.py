@@ -1498,22 +1498,26 @@ def replay_attention_gate(B: int, N: int, H: int, Dh: int, dim: int, esz: int):
     k = np.arange(H * dim)
     bnd.touch("weight", k * esz, esz)
     bnd.touch("lds", ((k % dim) * H + k // dim) * 4, 4)
-    for kind, maxb in (("fwd", 4096), ("bwd", 1024)):
+    # the grids: up to 4096 / 1024 blocks, fewer where fewer fit on the device at once (any count works:
+    # the loops stride over the grid); both ends are replayed
+    for kind, maxb in (("fwd", 4096), ("fwd", 1792), ("bwd", 1024), ("bwd", 768)):
         nblk = min(cdiv(rows, 4 * 2), maxb)
         for blk in sorted({0, nblk - 1}):
-            # a wave's rows: m0 = (block * 4 + wave) * 2 + trip * (grid * 8) while m0 < rows
+            # a wave's rows: m0 = (block * 4 + wave) * 2 + trip * (grid * 8) while m0 < rows; the
+            # loads of a live trip read rows clamped to the last one, the stores only rows < rows
             first = (blk * 4 + wave) * 2
             trips = np.where(first < rows, (rows - 1 - first) // (nblk * 8), -1)
             for m0, live in ((first, first < rows), (first + np.maximum(trips, 0) * nblk * 8, trips >= 0)):
                 for r in range(2):
                     m = m0 + r
                     ok = live & (m < rows)
-                    bb, nn = m // N, m % N
-                    tok = bb * sb + nn * sn + head * sh + sub * E
-                    bnd.touch("attn", tok * esz, E * esz, ok)
+                    mc = np.minimum(m, rows - 1)
+                    bb, nn = mc // N, mc % N
+                    tokc = bb * sb + nn * sn + head * sh + sub * E
+                    bnd.touch("attn", tokc * esz, E * esz, live)
                     for j in range(jx):
                         i = lane + j * WAVE
-                        bnd.touch("x", (m * dim + i) * esz, esz, ok & (i < dim))
+                        bnd.touch("x", (mc * dim + np.where(i < dim, i, 0)) * esz, esz, live)
                         if kind == "bwd":
                             bnd.touch("grad_x", (m * dim + i) * esz, esz, ok & (i < dim))
                             bnd.touch("lds", (i * H + head) * 4, 4, ok & (i < dim))
@@ -1521,9 +1525,9 @@ def replay_attention_gate(B: int, N: int, H: int, Dh: int, dim: int, esz: int):
                         bnd.touch("gate", (m * H + head) * esz, esz, ok & (sub == 0))
                         bnd.touch("out", (m * HD + lane * E) * esz, E * esz, ok)
                     else:
-                        bnd.touch("grad_out", (m * HD + lane * E) * esz, E * esz, ok)
-                        bnd.touch("gate", (m * H + head) * esz, esz, ok)
-                        bnd.touch("grad_attn", tok * esz, E * esz, ok)
+                        bnd.touch("grad_out", (mc * HD + lane * E) * esz, E * esz, live)
+                        bnd.touch("gate", (mc * H + head) * esz, esz, live)
+                        bnd.touch("grad_attn", tokc * esz, E * esz, ok)
         if kind == "bwd":
             for j in range(jx):
                 i = lane + j * WAVE
