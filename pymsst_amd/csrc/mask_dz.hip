@@ -220,7 +220,11 @@ int launch(const void* dpre, const void* w, const void* x, void* dz, const DzArg
   const int64_t rows = 64 * NT;
   if (!build_band_sched(
           a.NB, (a.M + rows - 1) / rows, [&](int) { return static_cast<int64_t>(a.H / HT); },
-          [&](int b) { return (2 * dim_inputs[b] + 31) / 32 + 2; },  // K chunks (+2 for the epilogue)
+          // cost of a block: its K chunks plus 5 for the prologue and the epilogue (its x read and dz
+          // write); measured at configs[1], a 1-chunk block takes ~5.8 us against ~1.2 us per chunk of
+          // a 33-chunk one.  With +2 the XCDs holding the 8- and 16-wide bands ran 9 rounds of them and
+          // finished last (73 -> 59 us)
+          [&](int b) { return (2 * dim_inputs[b] + 31) / 32 + 5; },
           &sc, &per_xcd))
     return fail(PMSST_EINVAL, "mask_estimator_final_backward: too many bands or rows for the dz schedule");
   const dim3 grid(per_xcd * kXcds);

@@ -894,7 +894,7 @@ def _replay_me_dz(bnd, widths, offs, M, H, esz, tanh_in):
         bnd.fail("me_dz: more than 160 KB of LDS")
     mtiles = cdiv(M, 4 * wave_rows)
     units = lambda b: H // HT  # noqa: E731
-    sc = build_band_sched(nb, mtiles, units, lambda b: cdiv(2 * widths[b], 32) + 2)
+    sc = build_band_sched(nb, mtiles, units, lambda b: cdiv(2 * widths[b], 32) + 5)
     decoded = sched_decode(sc, nb, units, True, bnd, "me_dz")
     lane = np.arange(64)
     gq, rr = lane >> 4, lane & 15
