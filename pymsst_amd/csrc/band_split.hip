@@ -293,6 +293,25 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
 //   !NORM: dx = gs (plain grouped linear; nsrc, inv_norm, gamma and the partials unused).
 // The blocks form a 1-D XCD-ordered grid: group = (band, input chunk), member = row tile,
 // so the row tiles sharing a weight chunk run on one XCD and share its L2.
+// Block -> (band, row tile, 64-wide input chunk) of the dx and finish grids: with a schedule
+// (sc.m_tiles != 0) only the chunks that exist get a block, XCD x running a contiguous range
+// (a row tile's chunks and a band's row tiles share its L2); without one (more bands than the
+// schedule holds) the XcdGrid of NB * max_ichunks groups, whose blocks past a band's width exit.
+__device__ __forceinline__ bool bs_dx_block(const BandSched& sc, const XcdGrid& xg, int max_ichunks, int nb,
+                                            int& band, int& ichunk, uint32_t& mt) {
+  if (sc.m_tiles != 0) {
+    uint32_t sub, per_unit;
+    if (!sched_block<true>(sc, band, mt, sub, per_unit)) return false;
+    ichunk = static_cast<int>(sub);
+    return true;
+  }
+  uint32_t grp;
+  if (!xcd_block(xg, grp, mt)) return false;
+  band = nb - 1 - static_cast<int>(grp) / max_ichunks;  // widest bands first
+  ichunk = static_cast<int>(grp) % max_ichunks;
+  return true;
+}
+
 template <typename T, bool FROM_X, bool NORM, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __restrict__ dy,
                                                                  const T* __restrict__ nsrc,
@@ -302,7 +321,8 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
                                                                  float* __restrict__ tbuf,
                                                                  float* __restrict__ dg_partial,
                                                                  float* __restrict__ pdot, int pitch,
-                                                                 int max_ichunks, XcdGrid xg, BandArgs a) {
+                                                                 int max_ichunks, XcdGrid xg, BandSched sc,
+                                                                 BandArgs a) {
   constexpr int kBI = 64;
   __shared__ T lds[gemm_lds_elems<T, kBI, kBM>()];
   __shared__ float sinv[kBM];
@@ -310,10 +330,9 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
   using S = TileShape<kBI, kBM, 4, 1>;  // TR = 1, TC = 4
 
   const int O = a.O;
-  uint32_t grp, mt;
-  if (!xcd_block(xg, grp, mt)) return;
-  const int band = a.NB - 1 - static_cast<int>(grp) / max_ichunks;  // widest bands first
-  const int ichunk = static_cast<int>(grp) % max_ichunks;
+  int band, ichunk;
+  uint32_t mt;
+  if (!bs_dx_block(sc, xg, max_ichunks, a.NB, band, ichunk, mt)) return;
   const int64_t mtile = mt;
   const int64_t m0 = mtile * kBM;
   const int off = static_cast<int>(a.offsets[band]);
@@ -422,13 +441,14 @@ template <typename T, bool FROM_X, bool V4>
 __global__ __launch_bounds__(256) void bs_dx_finish_kernel(const float* __restrict__ tbuf, const T* __restrict__ nsrc,
                                                            const float* __restrict__ inv_norm,
                                                            const float* __restrict__ pdot, T* __restrict__ dx,
-                                                           int pitch, int max_ichunks, XcdGrid xg, BandArgs a) {
+                                                           int pitch, int max_ichunks, XcdGrid xg, BandSched sc,
+                                                           BandArgs a) {
   __shared__ float sinv[kBM];
   __shared__ float sdot[kBM];
-  uint32_t grp, mt;
-  if (!xcd_block(xg, grp, mt)) return;
-  const int band = a.NB - 1 - static_cast<int>(grp) / max_ichunks;
-  const int i0 = static_cast<int>(grp) % max_ichunks * 64;
+  int band, ichunk;
+  uint32_t mt;
+  if (!bs_dx_block(sc, xg, max_ichunks, a.NB, band, ichunk, mt)) return;
+  const int i0 = ichunk * 64;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
   if (i0 >= I) return;  // uniform over the block
@@ -972,9 +992,14 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
     const bool v4 = a.vec4 && a.ovec4;
     const int max_ichunks = (hb.max_width + 63) / 64;
     const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_ichunks), static_cast<uint32_t>(m_tiles)};
+    BandSched sc;  // one block per existing (band, row tile, chunk); sc.m_tiles = 0 without
+    uint32_t per_xcd = 0;
+    const dim3 grid(build_even_sched(hb.NB, m_tiles, [&](int b) { return (dim_inputs[b] + 63) / 64; }, &sc, &per_xcd)
+                        ? per_xcd * kXcds
+                        : xg.blocks());
 #define PMSST_BDX(FX, V4)                                                                                          \
-  hipLaunchKernelGGL((bs_bwd_dx_kernel<T, FX, true, V4>), dim3(xg.blocks()), dim3(kGemmThreads), 0, stream, pdy, pn, \
-                     inv_norm, pg, pw, static_cast<T*>(dx), tbuf, partial, pdot, pitch, max_ichunks, xg, a)
+  hipLaunchKernelGGL((bs_bwd_dx_kernel<T, FX, true, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, pg, \
+                     pw, static_cast<T*>(dx), tbuf, partial, pdot, pitch, max_ichunks, xg, sc, a)
     if (from_x) {
       if (v4) PMSST_BDX(true, true); else PMSST_BDX(true, false);
     } else {
@@ -985,8 +1010,8 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
     if (rc != PMSST_OK) return rc;
     const bool fv4 = a.vec4;
 #define PMSST_FIN(FX, V4)                                                                                        \
-  hipLaunchKernelGGL((bs_dx_finish_kernel<T, FX, V4>), dim3(xg.blocks()), dim3(256), 0, stream, tbuf, pn, inv_norm, \
-                     pdot, static_cast<T*>(dx), pitch, max_ichunks, xg, a)
+  hipLaunchKernelGGL((bs_dx_finish_kernel<T, FX, V4>), grid, dim3(256), 0, stream, tbuf, pn, inv_norm, pdot, \
+                     static_cast<T*>(dx), pitch, max_ichunks, xg, sc, a)
     if (from_x) {
       if (fv4) PMSST_FIN(true, true); else PMSST_FIN(true, false);
     } else {
@@ -1068,12 +1093,15 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
     const int max_ichunks = (hb.max_width + 63) / 64;
     const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_ichunks), static_cast<uint32_t>((M + kBM - 1) / kBM)};
     const dim3 grid(xg.blocks());
+    const BandSched nosc{};  // groups of one width: every XcdGrid block has a chunk
     if (a.vec4 && a.ovec4)
       hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
-                         nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, nullptr, 0, max_ichunks, xg, a);
+                         nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, nullptr, 0, max_ichunks, xg, nosc,
+                         a);
     else
       hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
-                         nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, nullptr, 0, max_ichunks, xg, a);
+                         nullptr, nullptr, pw, static_cast<T*>(dx), nullptr, nullptr, nullptr, 0, max_ichunks, xg, nosc,
+                         a);
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
   }

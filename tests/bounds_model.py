@@ -421,9 +421,15 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
     max_ich = cdiv(max(widths), 64)
     sizes["lds"] = gemm_lds_bytes(esz, 64, 64) + 64 * 4 + 4 * 64 * 4
     if M_dx > 0:
-        grp, mt, valid = xcd_decode(nb * max_ich, m_tiles)
-        if np.any(mt[valid] >= m_tiles):
-            bnd.fail("dx: member out of range")
+        # norm: the even schedule over the existing (band, row tile, chunk) blocks (the XcdGrid of
+        # NB * max_ichunks groups past 256 bands); grouped: the XcdGrid (all groups one width)
+        sc = build_even_sched(nb, m_tiles, lambda b: cdiv(widths[b], 64)) if norm else None
+        if sc is not None:
+            sched_decode(sc, nb, lambda b: cdiv(widths[b], 64), True, bnd, "bs_bwd_dx")
+        else:
+            grp, mt, valid = xcd_decode(nb * max_ich, m_tiles)
+            if np.any(mt[valid] >= m_tiles):
+                bnd.fail("dx: member out of range")
         v4 = vec4 and ovec4
         for band in range(nb):
             off, I = int(offs[band]), int(widths[band])
