@@ -519,15 +519,26 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
                                                                  const float* __restrict__ inv_norm,
                                                                  const T* __restrict__ gamma, T* __restrict__ dw,
                                                                  T* __restrict__ db, int max_itiles, XcdGrid xg,
-                                                                 BandArgs a) {
+                                                                 BandSched sc, BandArgs a) {
   __shared__ T lds[gemm_lds_elems<T, kDwBI, kDwBO>()];
   using S = TileShape<kDwBI, kDwBO, 2, 2>;
   const int O = a.O;
-  uint32_t grp, ot;  // group = (band, input tile), member = output tile: the input slab shared in L2
-  if (!xcd_block(xg, grp, ot)) return;
-  const int o0 = static_cast<int>(ot) * kDwBO;
-  const int band = static_cast<int>(grp) / max_itiles;
-  const int i0 = (static_cast<int>(grp) % max_itiles) * kDwBI;
+  int band, i0, o0;
+  if (sc.m_tiles != 0) {
+    // one block per existing (band, input tile, output tile), evenly split over the XCDs; the
+    // output tiles of one input slab are neighbours
+    const uint32_t otiles = (O + kDwBO - 1) / kDwBO;
+    uint32_t mt, sub, per_unit;
+    if (!sched_block(sc, band, mt, sub, per_unit)) return;
+    i0 = static_cast<int>(sub / otiles) * kDwBI;
+    o0 = static_cast<int>(sub % otiles) * kDwBO;
+  } else {
+    uint32_t grp, ot;  // group = (band, input tile), member = output tile: the input slab shared in L2
+    if (!xcd_block(xg, grp, ot)) return;
+    o0 = static_cast<int>(ot) * kDwBO;
+    band = static_cast<int>(grp) / max_itiles;
+    i0 = (static_cast<int>(grp) % max_itiles) * kDwBI;
+  }
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
   if (i0 >= I) return;
@@ -852,6 +863,7 @@ struct HostBands {
   int F;
   int max_width;
   bool vec4;
+  const int64_t* widths;  // host [NB], the caller's array (valid for the call)
 };
 
 int check_bands(const char* op, const int64_t* dim_inputs, int64_t band_count, HostBands* hb) {
@@ -870,7 +882,18 @@ int check_bands(const char* op, const int64_t* dim_inputs, int64_t band_count, H
   hb->F = static_cast<int>(total);
   hb->max_width = static_cast<int>(maxw);
   hb->vec4 = vec4;
+  hb->widths = dim_inputs;
   return PMSST_OK;
+}
+
+// Grid of bs_bwd_dw_kernel: one block per existing (band, 64-wide input tile, 64-wide output tile)
+// on an even XCD schedule; past the schedule's band count sc->m_tiles = 0 and the XcdGrid.
+uint32_t dw_grid(const HostBands& hb, int64_t O, const XcdGrid& xg, BandSched* sc) {
+  const int64_t otiles = (O + kDwBO - 1) / kDwBO;
+  uint32_t per_xcd = 0;
+  if (build_even_sched(hb.NB, 1, [&](int b) { return (hb.widths[b] + kDwBI - 1) / kDwBI * otiles; }, sc, &per_xcd))
+    return per_xcd * kXcds;
+  return xg.blocks();
 }
 
 // 64-wide output tiles per forward block (capacity 64 * TO >= min(O, 256)).
@@ -1046,13 +1069,14 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
     }
   }
   if (!dw_done) {
+    BandSched wsc;
     const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
     const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_itiles), static_cast<uint32_t>((O + kDwBO - 1) / kDwBO)};
-    const dim3 grid(xg.blocks());
+    const dim3 grid(dw_grid(hb, O, xg, &wsc));
     const bool v4 = a.vec4 && a.ovec4;
 #define PMSST_BDW(FX, V4)                                                                                   \
   hipLaunchKernelGGL((bs_bwd_dw_kernel<T, FX, true, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, \
-                     pg, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, a)
+                     pg, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, wsc, a)
     if (from_x) {
       if (v4) PMSST_BDW(true, true); else PMSST_BDW(true, false);
     } else {
@@ -1113,13 +1137,14 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
   } else {
     const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
     const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_itiles), static_cast<uint32_t>((O + kDwBO - 1) / kDwBO)};
-    const dim3 grid(xg.blocks());
+    BandSched wsc;
+    const dim3 grid(dw_grid(hb, O, xg, &wsc));
     if (a.vec4 && a.ovec4)
       hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
-                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, a);
+                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, wsc, a);
     else
       hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, px,
-                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, a);
+                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, wsc, a);
     int rc = check_launch("bs_bwd_dw_kernel");
     if (rc != PMSST_OK) return rc;
   }

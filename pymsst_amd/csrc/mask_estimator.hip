@@ -84,13 +84,22 @@ template <typename T, bool V4>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(PMSST_ME_FWD_WAVES))) void me_fwd_kernel(const T* __restrict__ x, const T* __restrict__ weight,
                                                               const T* __restrict__ bias, T* __restrict__ pre,
                                                               T* __restrict__ out, int max_lchunks, XcdGrid xg,
-                                                              MaskArgs a) {
+                                                              MaskArgs a, BandSched sc) {
   __shared__ T lds[gemm_lds_elems<T, 128, kFwdBM>()];
   using S = TileShape<128, kFwdBM, 1, 4>;  // TR = 8 (4 left + 4 gate), TC = 2
-  uint32_t grp, mt;  // group = (band, 64-output chunk), member = row tile: weight chunk shared in L2
-  if (!xcd_block(xg, grp, mt)) return;
-  const int band = static_cast<int>(grp) / max_lchunks;
-  const int l0 = (static_cast<int>(grp) % max_lchunks) * 64;
+  int band, l0;
+  uint32_t mt;
+  if (sc.m_tiles != 0) {
+    // one block per existing (band, row tile, 64-output chunk), evenly split over the XCDs
+    uint32_t chunk, nch;
+    if (!sched_block(sc, band, mt, chunk, nch)) return;
+    l0 = static_cast<int>(chunk) * 64;
+  } else {
+    uint32_t grp;  // group = (band, 64-output chunk), member = row tile: weight chunk shared in L2
+    if (!xcd_block(xg, grp, mt)) return;
+    band = static_cast<int>(grp) / max_lchunks;
+    l0 = (static_cast<int>(grp) % max_lchunks) * 64;
+  }
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
   if (l0 >= I) return;
@@ -733,16 +742,29 @@ constexpr int kDwBJ = 64;
 template <typename T, bool V4>
 __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __restrict__ dpre, const T* __restrict__ x,
                                                                  T* __restrict__ dw, T* __restrict__ dbias,
-                                                                 int htiles, XcdGrid xg, MaskArgs a) {
+                                                                 int htiles, XcdGrid xg, MaskArgs a, BandSched sc) {
   __shared__ T lds[gemm_lds_elems<T, kDwBH, kDwBJ>()];
   using S = TileShape<kDwBH, kDwBJ, 2, 2>;
-  uint32_t grp, jchunk;  // group = (band, hidden tile), member = j chunk: the x slab shared in L2
-  if (!xcd_block(xg, grp, jchunk)) return;
-  const int band = static_cast<int>(grp) / htiles;
-  const int h0 = (static_cast<int>(grp) % htiles) * kDwBH;
-  const int j0 = static_cast<int>(jchunk) * kDwBJ;
-  const int off = static_cast<int>(a.offsets[band]);
-  const int I = static_cast<int>(a.offsets[band + 1]) - off;
+  int band, h0, j0, off, I;
+  if (sc.m_tiles != 0) {
+    // one block per existing (band, hidden tile, j chunk), evenly split over the XCDs; a band's
+    // blocks run hidden tile by hidden tile, so the blocks of one x slab are neighbours
+    uint32_t mt, sub, per_unit;
+    if (!sched_block(sc, band, mt, sub, per_unit)) return;
+    off = static_cast<int>(a.offsets[band]);
+    I = static_cast<int>(a.offsets[band + 1]) - off;
+    const uint32_t nj = (2 * I + kDwBJ - 1) / kDwBJ;
+    h0 = static_cast<int>(sub / nj) * kDwBH;
+    j0 = static_cast<int>(sub % nj) * kDwBJ;
+  } else {
+    uint32_t grp, jchunk;  // group = (band, hidden tile), member = j chunk: the x slab shared in L2
+    if (!xcd_block(xg, grp, jchunk)) return;
+    band = static_cast<int>(grp) / htiles;
+    h0 = (static_cast<int>(grp) % htiles) * kDwBH;
+    j0 = static_cast<int>(jchunk) * kDwBJ;
+    off = static_cast<int>(a.offsets[band]);
+    I = static_cast<int>(a.offsets[band + 1]) - off;
+  }
   const int K2 = 2 * I;
   if (j0 >= K2) return;
   const int H = a.H;
@@ -1054,14 +1076,20 @@ int launch_me_fwd(const void* x, const void* weight, const void* bias, const int
       return check_launch("me_fwd_dma_kernel");
     }
   }
+  BandSched sc;  // sc.m_tiles = 0 (the XcdGrid, whose blocks past a band's width exit) past 256 bands
+  uint32_t per_xcd = 0;
+  const dim3 g(build_even_sched(hm.NB, (M + kFwdBM - 1) / kFwdBM, [&](int b) { return (dim_inputs[b] + 63) / 64; },
+                                &sc, &per_xcd)
+                   ? per_xcd * kXcds
+                   : grid.x);
   if (a.vec4)
-    hipLaunchKernelGGL((me_fwd_kernel<T, true>), grid, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
+    hipLaunchKernelGGL((me_fwd_kernel<T, true>), g, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
                        static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
-                       static_cast<T*>(out), max_lchunks, xg, a);
+                       static_cast<T*>(out), max_lchunks, xg, a, sc);
   else
-    hipLaunchKernelGGL((me_fwd_kernel<T, false>), grid, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
+    hipLaunchKernelGGL((me_fwd_kernel<T, false>), g, dim3(kGemmThreads), 0, stream, static_cast<const T*>(x),
                        static_cast<const T*>(weight), static_cast<const T*>(bias), static_cast<T*>(pre),
-                       static_cast<T*>(out), max_lchunks, xg, a);
+                       static_cast<T*>(out), max_lchunks, xg, a, sc);
   return check_launch("me_fwd_kernel");
 }
 
@@ -1182,13 +1210,19 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
   const int max_jchunks = (2 * hm.max_width + kDwBJ - 1) / kDwBJ;
   const int htiles = static_cast<int>((H + kDwBH - 1) / kDwBH);
   const XcdGrid xg3{static_cast<uint32_t>(hm.NB * htiles), static_cast<uint32_t>(max_jchunks)};
-  const dim3 g3(xg3.blocks());
+  BandSched wsc3;  // wsc3.m_tiles = 0 (the XcdGrid, whose blocks past a band's width exit) past 256 bands
+  uint32_t w3_per_xcd = 0;
+  const dim3 g3(build_even_sched(
+                    hm.NB, 1, [&](int b) { return htiles * ((2 * dim_inputs[b] + kDwBJ - 1) / kDwBJ); }, &wsc3,
+                    &w3_per_xcd)
+                    ? w3_per_xcd * kXcds
+                    : xg3.blocks());
   if (a.vec4)
     hipLaunchKernelGGL((me_bwd_dw_kernel<T, true>), g3, dim3(kGemmThreads), 0, stream, dpre, static_cast<const T*>(x),
-                       static_cast<T*>(dw), static_cast<T*>(dbias), htiles, xg3, a);
+                       static_cast<T*>(dw), static_cast<T*>(dbias), htiles, xg3, a, wsc3);
   else
     hipLaunchKernelGGL((me_bwd_dw_kernel<T, false>), g3, dim3(kGemmThreads), 0, stream, dpre,
-                       static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(dbias), htiles, xg3, a);
+                       static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(dbias), htiles, xg3, a, wsc3);
   int rc = check_launch("me_bwd_dw_kernel");
   if (rc != PMSST_OK) return rc;
   // dbias was summed by the dW kernel (which also runs for M == 0 and then writes zeros)

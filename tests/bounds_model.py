@@ -697,13 +697,23 @@ def _replay_bs_dw_reg(bnd, widths, offs, M, O, esz, has_bias, norm, v4):
     """band_split.hip bs_bwd_dw_kernel (register-staged main loop; also the grouped linear's dW)."""
     nb, F = len(widths), int(sum(widths))
     max_it = cdiv(max(widths), 64)
-    grp, ot, valid = xcd_decode(nb * max_it, cdiv(O, 64))
+    # the even schedule over the existing (band, input tile, output tile) blocks (sub = input tile x
+    # output tiles + output tile); the XcdGrid past 256 bands
+    otiles = cdiv(O, 64)
+    units = lambda b: cdiv(widths[b], 64) * otiles
+    sc = build_even_sched(nb, 1, units)
+    if sc is not None:
+        dec = sched_decode(sc, nb, units, False, bnd, "bs_bwd_dw")
+        blocks = [(b * max_it + sub // otiles, sub % otiles) for b, _, sub in dec]
+    else:
+        grp, ot, valid = xcd_decode(nb * max_it, otiles)
+        blocks = list(zip(grp[valid], ot[valid]))
     tid = np.arange(GEMM_THREADS)
     lane, wave = tid & 63, tid >> 6
     nk = cdiv(M, CHUNK_K)
     kbeg = M - nk * CHUNK_K
     bnd.sizes["lds"] = max(bnd.sizes["lds"], gemm_lds_bytes(esz, 64, 64))
-    for g_, o_ in zip(grp[valid], ot[valid]):
+    for g_, o_ in blocks:
         band, i0 = int(g_) // max_it, (int(g_) % max_it) * 64
         o0 = int(o_) * 64
         off, I = int(offs[band]), int(widths[band])
@@ -1251,13 +1261,20 @@ def _replay_me_fwd_reg(bnd, widths, offs, M, H, esz, vec4):
     nb, F = len(widths), int(sum(widths))
     max_l = cdiv(max(widths), 64)
     mtiles = cdiv(M, 128)
-    grp, mt, valid = xcd_decode(nb * max_l, mtiles)
     bnd.sizes["lds"] = gemm_lds_bytes(esz, 128, 128)
     tid = np.arange(GEMM_THREADS)
     lane, wave = tid & 63, tid >> 6
     nk = cdiv(H, CHUNK_K)
     kbeg = H - nk * CHUNK_K
-    combos = sorted({(int(g), int(m)) for g, m, v in zip(grp, mt, valid) if v and int(m) in (0, mtiles - 1)})
+    # the even schedule over the existing (band, row tile, chunk) blocks; the XcdGrid past 256 bands
+    units = lambda b: cdiv(widths[b], 64)
+    sc = build_even_sched(nb, mtiles, units)
+    if sc is not None:
+        dec = sched_decode(sc, nb, units, False, bnd, "me_fwd")
+        combos = sorted({(b * max_l + sub, mt) for b, mt, sub in dec if mt in (0, mtiles - 1)})
+    else:
+        grp, mt, valid = xcd_decode(nb * max_l, mtiles)
+        combos = sorted({(int(g), int(m)) for g, m, v in zip(grp, mt, valid) if v and int(m) in (0, mtiles - 1)})
     for g_, mtile in combos:
         band, l0 = g_ // max_l, (g_ % max_l) * 64
         off, I = int(offs[band]), int(widths[band])
@@ -1328,12 +1345,22 @@ def _replay_me_dw_reg(bnd, widths, offs, M, H, esz):
     nb, F = len(widths), int(sum(widths))
     ht = cdiv(H, 128)
     maxj = cdiv(2 * max(widths), 64)
-    grp, jc, valid = xcd_decode(nb * ht, maxj)
     tid = np.arange(GEMM_THREADS)
     lane, wave = tid & 63, tid >> 6
     nk = cdiv(M, CHUNK_K)
     kbeg = M - nk * CHUNK_K
-    for g_, j_ in sorted({(int(g), int(j)) for g, j, v in zip(grp, jc, valid) if v}):
+    # the even schedule over the existing (band, hidden tile, j chunk) blocks (sub = hidden tile x
+    # the band's j chunks + j chunk); the XcdGrid past 256 bands
+    nj = lambda b: cdiv(2 * widths[b], 64)
+    units = lambda b: ht * nj(b)
+    sc = build_even_sched(nb, 1, units)
+    if sc is not None:
+        dec = sched_decode(sc, nb, units, False, bnd, "me_bwd_dw")
+        pairs = sorted({(b * ht + sub // nj(b), sub % nj(b)) for b, _, sub in dec})
+    else:
+        grp, jc, valid = xcd_decode(nb * ht, maxj)
+        pairs = sorted({(int(g), int(j)) for g, j, v in zip(grp, jc, valid) if v})
+    for g_, j_ in pairs:
         band, h0 = g_ // ht, (g_ % ht) * 128
         j0 = j_ * 64
         off, I = int(offs[band]), int(widths[band])
