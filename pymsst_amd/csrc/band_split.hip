@@ -639,7 +639,8 @@ __device__ __forceinline__ void vm_wait_steps(int nd) {  // at most N nd DMAs ou
 template <typename T, bool FROM_X>
 __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_dma_kernel(
     const T* __restrict__ dy, const T* __restrict__ nsrc, const float* __restrict__ inv_norm,
-    const T* __restrict__ gamma, T* __restrict__ dw, T* __restrict__ db, BandSched sc, BandArgs a, int otiles) {
+    const T* __restrict__ gamma, T* __restrict__ dw, T* __restrict__ db, BandSched sc, BandArgs a, int otiles,
+    const float* __restrict__ dg_partial, int dg_parts, T* __restrict__ dgamma, uint32_t main_blocks) {
   constexpr int S = PMSST_BS_DWD_STAGES;
   constexpr int KS = PMSST_BS_DWD_KS;
   constexpr int KR = KS * kChunkK;             // rows per step
@@ -653,6 +654,14 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_dma_kernel(
   static_assert(S >= 3 && (S - 2) <= 6 && (S - 2) * (kXI + kDI) <= 63, "stages (wait table)");
   __shared__ __attribute__((aligned(1024))) char lds[S * kStage];
   __shared__ float sinv[FROM_X ? kBdWinRows : 1];
+  static_assert(S * kStage >= kColSumLds, "column-sum tile LDS");
+  if (blockIdx.x >= main_blocks) {
+    // tail blocks: dgamma = column sums of the dx kernel's partials (complete two launches back),
+    // in col_sum_kernel's order, instead of a launch of their own
+    col_sum_tile<T, kGemmThreads>(dg_partial, dg_parts, a.F, dgamma, static_cast<int>(blockIdx.x - main_blocks),
+                    reinterpret_cast<float*>(lds));
+    return;
+  }
   int band;
   uint32_t mt, sub, per_unit;
   if (!sched_block(sc, band, mt, sub, per_unit)) return;
@@ -1056,13 +1065,18 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
         (static_cast<int64_t>(KR) * hb.NB * O + O) * 2 < (int64_t{1} << 31) &&
         build_band_sched(hb.NB, 1, [&](int b) { return (dim_inputs[b] + kBdT - 1) / kBdT * otiles; }, &sc,
                          &per_xcd)) {
-      const dim3 grid(per_xcd * kXcds);
+      // + one tail block per 16 columns of dgamma (the partials' column sums)
+      const uint32_t main_blocks = per_xcd * kXcds;
+      const dim3 grid(main_blocks + static_cast<uint32_t>((hb.F + kColSumCols - 1) / kColSumCols));
+      T* pdg = static_cast<T*>(dgamma);
       if (from_x)
         hipLaunchKernelGGL((bs_bwd_dw_dma_kernel<T, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
-                           pg, static_cast<T*>(dw), static_cast<T*>(db), sc, a, otiles);
+                           pg, static_cast<T*>(dw), static_cast<T*>(db), sc, a, otiles, partial, m_tiles, pdg,
+                           main_blocks);
       else
         hipLaunchKernelGGL((bs_bwd_dw_dma_kernel<T, false>), grid, dim3(kGemmThreads), 0, stream, pdy, pn,
-                           inv_norm, pg, static_cast<T*>(dw), static_cast<T*>(db), sc, a, otiles);
+                           inv_norm, pg, static_cast<T*>(dw), static_cast<T*>(db), sc, a, otiles, partial, m_tiles,
+                           pdg, main_blocks);
       const int rc = check_launch("bs_bwd_dw_dma_kernel");
       if (rc != PMSST_OK) return rc;
       dw_done = true;
@@ -1086,7 +1100,9 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
     int rc = check_launch("bs_bwd_dw_kernel");
     if (rc != PMSST_OK) return rc;
   }
-  // dbias was summed by the dW kernel (the fallback one also runs for M == 0 and then writes zeros)
+  // dbias was summed by the dW kernel (the fallback one also runs for M == 0 and then writes zeros);
+  // the DMA dW kernel's tail blocks summed dgamma
+  if (dw_done) return PMSST_OK;
   return launch_col_sum(partial, m_tiles, hb.F, dgamma, dtype_code<T>(), stream);
 }
 

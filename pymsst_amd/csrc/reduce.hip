@@ -5,43 +5,19 @@
 namespace pmsst {
 namespace {
 
-constexpr int kColsPerBlock = 16;
-constexpr int kGroups = 64;  // 16 x 64 = 1024 threads
-
+// One 16-column tile per block of 1024 threads (col_sum_tile): one row group per thread.
 template <typename TO>
-__global__ __launch_bounds__(kColsPerBlock* kGroups) void col_sum_kernel(const float* __restrict__ partial,
-                                                                         int parts, int dim, TO* __restrict__ out) {
-  __shared__ float red[kGroups][kColsPerBlock + 1];
-  const int cl = threadIdx.x % kColsPerBlock;
-  const int grp = threadIdx.x / kColsPerBlock;
-  const int c = blockIdx.x * kColsPerBlock + cl;
-  // 8 independent loads in flight per trip (a serial chain of round trips otherwise sets the time)
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (c < dim) {
-    int p = grp;
-    for (; p + 7 * kGroups < parts; p += 8 * kGroups) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = partial[static_cast<int64_t>(p + u * kGroups) * dim + c];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) acc[u] += v[u];
-    }
-    for (; p < parts; p += kGroups) acc[0] += partial[static_cast<int64_t>(p) * dim + c];
-  }
-  red[grp][cl] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
-  __syncthreads();
-  for (int stride = kGroups / 2; stride > 0; stride >>= 1) {
-    if (grp < stride) red[grp][cl] += red[grp + stride][cl];
-    __syncthreads();
-  }
-  if (grp == 0 && c < dim) out[c] = from_f32<TO>(red[0][cl]);
+__global__ __launch_bounds__(1024) void col_sum_kernel(const float* __restrict__ partial, int parts, int dim,
+                                                       TO* __restrict__ out) {
+  __shared__ float red[kColSumLds / 4];
+  col_sum_tile<TO, 1024>(partial, parts, dim, out, blockIdx.x, red);
 }
 
 }  // namespace
 
 int launch_col_sum(const float* partial, int parts, int dim, void* out, int out_dtype, hipStream_t stream) {
-  const int blocks = (dim + kColsPerBlock - 1) / kColsPerBlock;
-  const dim3 grid(blocks), block(kColsPerBlock * kGroups);
+  const int blocks = (dim + kColSumCols - 1) / kColSumCols;
+  const dim3 grid(blocks), block(1024);
   switch (out_dtype) {
     case PMSST_F32:
       hipLaunchKernelGGL(col_sum_kernel<float>, grid, block, 0, stream, partial, parts, dim,

@@ -59,4 +59,47 @@ inline size_t row_bwd_workspace(int64_t dim) {
 // parts == 0 writes zeros.
 int launch_col_sum(const float* partial, int parts, int dim, void* out, int out_dtype, hipStream_t stream);
 
+constexpr int kColSumCols = 16;     // columns per 256-thread tile
+constexpr int kColSumGroups = 64;   // row groups per column
+constexpr int kColSumLds = kColSumGroups * (kColSumCols + 1) * 4;  // bytes of LDS a tile uses
+
+// Columns [16 blk, 16 blk + 16) of out[c] = sum_p partial[p * dim + c] by one block of NT threads
+// (256 or 1024: col_sum_kernel, and tail blocks of kernels that run after the partials are
+// complete).  Row group g < 64 sums rows g, g + 64, ... with 8 loads in flight per trip; thread t
+// works groups t / 16 + (NT / 16) v of column t % 16; the groups are then added in a fixed tree.
+// The order of every addition depends on parts and dim only, not on NT.  `red` is kColSumLds
+// bytes of LDS.
+template <typename TO, int NT>
+__device__ __forceinline__ void col_sum_tile(const float* __restrict__ partial, int parts, int dim,
+                                             TO* __restrict__ out, int blk, float* red) {
+  constexpr int G = kColSumGroups, P = kColSumCols + 1, TG = NT / kColSumCols;
+  static_assert(NT == 256 || NT == 1024, "threads");
+  const int cl = threadIdx.x % kColSumCols;
+  const int tg = threadIdx.x / kColSumCols;
+  const int c = blk * kColSumCols + cl;
+#pragma unroll
+  for (int v = 0; v < G / TG; ++v) {
+    const int grp = tg + TG * v;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (c < dim) {
+      int p = grp;
+      for (; p + 7 * G < parts; p += 8 * G) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = partial[static_cast<int64_t>(p + u * G) * dim + c];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u] += x[u];
+      }
+      for (; p < parts; p += G) acc[0] += partial[static_cast<int64_t>(p) * dim + c];
+    }
+    red[grp * P + cl] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  }
+  __syncthreads();
+  for (int stride = G / 2; stride > 0; stride >>= 1) {
+    for (int grp = tg; grp < stride; grp += TG) red[grp * P + cl] += red[(grp + stride) * P + cl];
+    __syncthreads();
+  }
+  if (tg == 0 && c < dim) out[c] = from_f32<TO>(red[cl]);
+}
+
 }  // namespace pmsst

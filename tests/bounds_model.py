@@ -600,17 +600,26 @@ def _replay_glin_dx(bnd, G, I, O, M):
 
 
 def _replay_col_sum(bnd, pbuf, parts, dim, obuf, osz, poff=0):
-    """reduce.hip col_sum_kernel: 16 columns x 64 groups per block."""
-    tid = np.arange(1024)
-    cl, grp = tid % 16, tid // 16
+    """rowgeom.h col_sum_tile (col_sum_kernel with 1024 threads, one row group each; the band-split DMA
+    dW kernel's tail blocks with 256 threads, 4 groups each: the same rows): 64 row groups per 16
+    columns, group g reading rows g, g + 64, ... (trips of 8 loads, then single loads); first and
+    last tile."""
+    tid = np.arange(256)
+    cl, tg = tid % 16, tid // 16
     for blk in sorted({0, cdiv(dim, 16) - 1}):
         c = blk * 16 + cl
         ok = c < dim
-        for p0 in sorted({0, max(parts - 1, 0)}):
-            p = np.full_like(c, p0)
-            bnd.touch(pbuf, poff + (p * dim + c) * 4, 4, ok & (p < parts))
-        bnd.touch(obuf, c * osz, osz, ok & (grp == 0))
-    _ = grp
+        for v in range(4):
+            p = tg + 16 * v
+            while np.any(p + 7 * 64 < parts):
+                live = p + 7 * 64 < parts
+                for u in range(8):
+                    bnd.touch(pbuf, poff + ((p + 64 * u) * dim + c) * 4, 4, ok & live)
+                p = np.where(live, p + 8 * 64, p)
+            while np.any(p < parts):
+                bnd.touch(pbuf, poff + (p * dim + c) * 4, 4, ok & (p < parts))
+                p = p + 64
+        bnd.touch(obuf, c * osz, osz, ok & (tg == 0))
 
 
 def _replay_bs_dw_dma(bnd, widths, offs, M, O, esz, has_bias):
