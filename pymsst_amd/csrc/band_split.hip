@@ -298,10 +298,10 @@ __global__ __launch_bounds__(kGemmThreads) void bs_fwd_kernel(const T* __restric
 // (a row tile's chunks and a band's row tiles share its L2); without one (more bands than the
 // schedule holds) the XcdGrid of NB * max_ichunks groups, whose blocks past a band's width exit.
 __device__ __forceinline__ bool bs_dx_block(const BandSched& sc, const XcdGrid& xg, int max_ichunks, int nb,
-                                            int& band, int& ichunk, uint32_t& mt) {
+                                            uint32_t blk, int& band, int& ichunk, uint32_t& mt) {
   if (sc.m_tiles != 0) {
     uint32_t sub, per_unit;
-    if (!sched_block<true>(sc, band, mt, sub, per_unit)) return false;
+    if (!sched_block_at<true>(sc, blk, band, mt, sub, per_unit)) return false;
     ichunk = static_cast<int>(sub);
     return true;
   }
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
   const int O = a.O;
   int band, ichunk;
   uint32_t mt;
-  if (!bs_dx_block(sc, xg, max_ichunks, a.NB, band, ichunk, mt)) return;
+  if (!bs_dx_block(sc, xg, max_ichunks, a.NB, blockIdx.x, band, ichunk, mt)) return;
   const int64_t mtile = mt;
   const int64_t m0 = mtile * kBM;
   const int off = static_cast<int>(a.offsets[band]);
@@ -437,17 +437,17 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
 // butterfly), dx = inv (t sqrt(I) - n dot / sqrt(I)) with n = x inv sqrt(I) (FROM_X) or the saved
 // normed.  Thread t covers the 4-element quad t % 16 of the chunk on rows t / 16 + 16 j, j < 4:
 // every load of the thread is issued before the first store.
+// The finish of block `blk` of the grid (256 threads; sinv and sdot are kBM floats of LDS each):
+// bs_dx_finish_kernel, or tail blocks of the DMA dW kernel, which runs after the dx kernel.
 template <typename T, bool FROM_X, bool V4>
-__global__ __launch_bounds__(256) void bs_dx_finish_kernel(const float* __restrict__ tbuf, const T* __restrict__ nsrc,
-                                                           const float* __restrict__ inv_norm,
-                                                           const float* __restrict__ pdot, T* __restrict__ dx,
-                                                           int pitch, int max_ichunks, XcdGrid xg, BandSched sc,
-                                                           BandArgs a) {
-  __shared__ float sinv[kBM];
-  __shared__ float sdot[kBM];
+__device__ __forceinline__ void bs_dx_finish_body(const float* __restrict__ tbuf, const T* __restrict__ nsrc,
+                                                  const float* __restrict__ inv_norm, const float* __restrict__ pdot,
+                                                  T* __restrict__ dx, int pitch, int max_ichunks, const XcdGrid& xg,
+                                                  const BandSched& sc, const BandArgs& a, uint32_t blk, float* sinv,
+                                                  float* sdot) {
   int band, ichunk;
   uint32_t mt;
-  if (!bs_dx_block(sc, xg, max_ichunks, a.NB, band, ichunk, mt)) return;
+  if (!bs_dx_block(sc, xg, max_ichunks, a.NB, blk, band, ichunk, mt)) return;
   const int i0 = ichunk * 64;
   const int off = static_cast<int>(a.offsets[band]);
   const int I = static_cast<int>(a.offsets[band + 1]) - off;
@@ -505,6 +505,18 @@ __global__ __launch_bounds__(256) void bs_dx_finish_kernel(const float* __restri
         dx[e + q] = from_f32<T>(inv * (tbuf[e + q] * root - to_f32(nsrc[e + q]) * c));
     }
   }
+}
+
+template <typename T, bool FROM_X, bool V4>
+__global__ __launch_bounds__(256) void bs_dx_finish_kernel(const float* __restrict__ tbuf, const T* __restrict__ nsrc,
+                                                           const float* __restrict__ inv_norm,
+                                                           const float* __restrict__ pdot, T* __restrict__ dx,
+                                                           int pitch, int max_ichunks, XcdGrid xg, BandSched sc,
+                                                           BandArgs a) {
+  __shared__ float sinv[kBM];
+  __shared__ float sdot[kBM];
+  bs_dx_finish_body<T, FROM_X, V4>(tbuf, nsrc, inv_norm, pdot, dx, pitch, max_ichunks, xg, sc, a, blockIdx.x, sinv,
+                                   sdot);
 }
 
 // ------------------------------------------------------------------ backward: dW
@@ -640,7 +652,9 @@ template <typename T, bool FROM_X>
 __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_dma_kernel(
     const T* __restrict__ dy, const T* __restrict__ nsrc, const float* __restrict__ inv_norm,
     const T* __restrict__ gamma, T* __restrict__ dw, T* __restrict__ db, BandSched sc, BandArgs a, int otiles,
-    const float* __restrict__ dg_partial, int dg_parts, T* __restrict__ dgamma, uint32_t main_blocks) {
+    const float* __restrict__ dg_partial, int dg_parts, T* __restrict__ dgamma, uint32_t main_blocks,
+    const float* __restrict__ tbuf, const float* __restrict__ pdot, T* __restrict__ dx, int pitch, BandSched fsc,
+    uint32_t fin_blocks) {
   constexpr int S = PMSST_BS_DWD_STAGES;
   constexpr int KS = PMSST_BS_DWD_KS;
   constexpr int KR = KS * kChunkK;             // rows per step
@@ -655,11 +669,21 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_dma_kernel(
   __shared__ __attribute__((aligned(1024))) char lds[S * kStage];
   __shared__ float sinv[FROM_X ? kBdWinRows : 1];
   static_assert(S * kStage >= kColSumLds, "column-sum tile LDS");
+  // Tail blocks, after the scheduled ones, for work that needs only the dx kernel's results: first
+  // fin_blocks blocks of the dx finish (on the dx kernel's schedule fsc; main_blocks is a multiple
+  // of kXcds, so each keeps its XCD), then dgamma = the column sums of the dx kernel's partials in
+  // col_sum_kernel's order.  Neither gets a launch of its own.
+  if (blockIdx.x >= main_blocks + fin_blocks) {
+    col_sum_tile<T, kGemmThreads>(dg_partial, dg_parts, a.F, dgamma,
+                                  static_cast<int>(blockIdx.x - main_blocks - fin_blocks),
+                                  reinterpret_cast<float*>(lds));
+    return;
+  }
   if (blockIdx.x >= main_blocks) {
-    // tail blocks: dgamma = column sums of the dx kernel's partials (complete two launches back),
-    // in col_sum_kernel's order, instead of a launch of their own
-    col_sum_tile<T, kGemmThreads>(dg_partial, dg_parts, a.F, dgamma, static_cast<int>(blockIdx.x - main_blocks),
-                    reinterpret_cast<float*>(lds));
+    const XcdGrid nogrid{0, 1};  // unused: fsc is a schedule
+    float* fl = reinterpret_cast<float*>(lds);
+    bs_dx_finish_body<T, FROM_X, true>(tbuf, nsrc, inv_norm, pdot, dx, pitch, 1, nogrid, fsc, a,
+                                       blockIdx.x - main_blocks, fl, fl + kBM);
     return;
   }
   int band;
@@ -1020,15 +1044,27 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
   float* tbuf = reinterpret_cast<float*>(ws + dg_partial_bytes(M, hb.F) + pdot_bytes(M, hb.F, hb.NB));
   const int pitch = pdot_pitch(hb.F, hb.NB);
   const int m_tiles = static_cast<int>((M + kBM - 1) / kBM);
+  // DMA-ring dW: 16-bit, 4-aligned widths and pointers, O % 8 == 0 with 16-byte aligned dy rows
+  constexpr int KR = PMSST_BS_DWD_KS * kChunkK;
+  const int otiles = static_cast<int>((O + kBdT - 1) / kBdT);
+  BandSched wsc;
+  uint32_t w_per_xcd = 0;
+  const bool dma_dw = sizeof(T) == 2 && PMSST_BS_DW_DMA && M >= KR && a.vec4 && O % 8 == 0 && aligned_to(dy, 16) &&
+                      (static_cast<int64_t>(KR) * hb.F + hb.F) * 2 < (int64_t{1} << 31) &&
+                      (static_cast<int64_t>(KR) * hb.NB * O + O) * 2 < (int64_t{1} << 31) &&
+                      build_band_sched(hb.NB, 1, [&](int b) { return (dim_inputs[b] + kBdT - 1) / kBdT * otiles; },
+                                       &wsc, &w_per_xcd);
+  BandSched sc;  // dx and finish: one block per existing (band, row tile, chunk); sc.m_tiles = 0 without
+  uint32_t per_xcd = 0;
+  const bool dx_sched =
+      M > 0 && build_even_sched(hb.NB, m_tiles, [&](int b) { return (dim_inputs[b] + 63) / 64; }, &sc, &per_xcd);
+  // the finish runs in the DMA dW kernel's tail blocks when both have their schedules
+  const bool fold_finish = dma_dw && dx_sched;
   if (M > 0) {
     const bool v4 = a.vec4 && a.ovec4;
     const int max_ichunks = (hb.max_width + 63) / 64;
     const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_ichunks), static_cast<uint32_t>(m_tiles)};
-    BandSched sc;  // one block per existing (band, row tile, chunk); sc.m_tiles = 0 without
-    uint32_t per_xcd = 0;
-    const dim3 grid(build_even_sched(hb.NB, m_tiles, [&](int b) { return (dim_inputs[b] + 63) / 64; }, &sc, &per_xcd)
-                        ? per_xcd * kXcds
-                        : xg.blocks());
+    const dim3 grid(dx_sched ? per_xcd * kXcds : xg.blocks());
 #define PMSST_BDX(FX, V4)                                                                                          \
   hipLaunchKernelGGL((bs_bwd_dx_kernel<T, FX, true, V4>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm, pg, \
                      pw, static_cast<T*>(dx), tbuf, partial, pdot, pitch, max_ichunks, xg, sc, a)
@@ -1040,43 +1076,39 @@ int launch_bwd(const void* dy, const void* nsrc, bool from_x, const float* inv_n
 #undef PMSST_BDX
     int rc = check_launch("bs_bwd_dx_kernel");
     if (rc != PMSST_OK) return rc;
-    const bool fv4 = a.vec4;
+    if (!fold_finish) {  // else the DMA dW kernel's tail blocks finish dx
+      const bool fv4 = a.vec4;
 #define PMSST_FIN(FX, V4)                                                                                        \
   hipLaunchKernelGGL((bs_dx_finish_kernel<T, FX, V4>), grid, dim3(256), 0, stream, tbuf, pn, inv_norm, pdot, \
                      static_cast<T*>(dx), pitch, max_ichunks, xg, sc, a)
-    if (from_x) {
-      if (fv4) PMSST_FIN(true, true); else PMSST_FIN(true, false);
-    } else {
-      if (fv4) PMSST_FIN(false, true); else PMSST_FIN(false, false);
-    }
+      if (from_x) {
+        if (fv4) PMSST_FIN(true, true); else PMSST_FIN(true, false);
+      } else {
+        if (fv4) PMSST_FIN(false, true); else PMSST_FIN(false, false);
+      }
 #undef PMSST_FIN
-    rc = check_launch("bs_dx_finish_kernel");
-    if (rc != PMSST_OK) return rc;
+      rc = check_launch("bs_dx_finish_kernel");
+      if (rc != PMSST_OK) return rc;
+    }
   }
   bool dw_done = false;
   if constexpr (sizeof(T) == 2) {
-    // DMA-ring dW: 16-bit, 4-aligned widths and pointers, O % 8 == 0 with 16-byte aligned dy rows
-    constexpr int KR = PMSST_BS_DWD_KS * kChunkK;
-    const int otiles = static_cast<int>((O + kBdT - 1) / kBdT);
-    BandSched sc;
-    uint32_t per_xcd = 0;
-    if (PMSST_BS_DW_DMA && M >= KR && a.vec4 && O % 8 == 0 && aligned_to(dy, 16) &&
-        (static_cast<int64_t>(KR) * hb.F + hb.F) * 2 < (int64_t{1} << 31) &&
-        (static_cast<int64_t>(KR) * hb.NB * O + O) * 2 < (int64_t{1} << 31) &&
-        build_band_sched(hb.NB, 1, [&](int b) { return (dim_inputs[b] + kBdT - 1) / kBdT * otiles; }, &sc,
-                         &per_xcd)) {
-      // + one tail block per 16 columns of dgamma (the partials' column sums)
-      const uint32_t main_blocks = per_xcd * kXcds;
-      const dim3 grid(main_blocks + static_cast<uint32_t>((hb.F + kColSumCols - 1) / kColSumCols));
+    if (dma_dw) {
+      // + the finish's blocks (when folded) and one block per 16 columns of dgamma
+      const uint32_t main_blocks = w_per_xcd * kXcds;
+      const uint32_t fin_blocks = fold_finish ? per_xcd * kXcds : 0;
+      const BandSched& fsc = fold_finish ? sc : wsc;  // unused without fin_blocks
+      const dim3 grid(main_blocks + fin_blocks + static_cast<uint32_t>((hb.F + kColSumCols - 1) / kColSumCols));
       T* pdg = static_cast<T*>(dgamma);
+      T* pdx = static_cast<T*>(dx);
       if (from_x)
         hipLaunchKernelGGL((bs_bwd_dw_dma_kernel<T, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pn, inv_norm,
-                           pg, static_cast<T*>(dw), static_cast<T*>(db), sc, a, otiles, partial, m_tiles, pdg,
-                           main_blocks);
+                           pg, static_cast<T*>(dw), static_cast<T*>(db), wsc, a, otiles, partial, m_tiles, pdg,
+                           main_blocks, tbuf, pdot, pdx, pitch, fsc, fin_blocks);
       else
         hipLaunchKernelGGL((bs_bwd_dw_dma_kernel<T, false>), grid, dim3(kGemmThreads), 0, stream, pdy, pn,
-                           inv_norm, pg, static_cast<T*>(dw), static_cast<T*>(db), sc, a, otiles, partial, m_tiles,
-                           pdg, main_blocks);
+                           inv_norm, pg, static_cast<T*>(dw), static_cast<T*>(db), wsc, a, otiles, partial, m_tiles,
+                           pdg, main_blocks, tbuf, pdot, pdx, pitch, fsc, fin_blocks);
       const int rc = check_launch("bs_bwd_dw_dma_kernel");
       if (rc != PMSST_OK) return rc;
       dw_done = true;

@@ -152,11 +152,14 @@ struct BandSched {
 // Decodes this block: band, row tile, and index inside the (band, row tile) unit.  With
 // LAST_FIRST an XCD dispatches its range from the end (in canonical order the costly wide
 // bands come last, and starting them first keeps them out of the tail).
+// sched_block_at decodes block `blk` of the schedule: a kernel whose scheduled blocks start at a
+// multiple of kXcds past its own first block passes blockIdx.x minus that offset (the XCD stays
+// blk % kXcds).
 template <bool LAST_FIRST = false>
-__device__ __forceinline__ bool sched_block(const BandSched& sc, int& band, uint32_t& mt, uint32_t& sub,
-                                            uint32_t& per_unit) {
-  const uint32_t xcd = blockIdx.x % kXcds;
-  const uint32_t local = blockIdx.x / kXcds;
+__device__ __forceinline__ bool sched_block_at(const BandSched& sc, uint32_t blk, int& band, uint32_t& mt,
+                                               uint32_t& sub, uint32_t& per_unit) {
+  const uint32_t xcd = blk % kXcds;
+  const uint32_t local = blk / kXcds;
   if (sc.gs[xcd] + local >= sc.gs[xcd + 1]) return false;
   const uint32_t gb = LAST_FIRST ? sc.gs[xcd + 1] - 1 - local : sc.gs[xcd] + local;
   uint32_t b = sc.bstart[xcd];
@@ -167,6 +170,12 @@ __device__ __forceinline__ bool sched_block(const BandSched& sc, int& band, uint
   mt = within / per_unit;
   sub = within % per_unit;
   return true;
+}
+
+template <bool LAST_FIRST = false>
+__device__ __forceinline__ bool sched_block(const BandSched& sc, int& band, uint32_t& mt, uint32_t& sub,
+                                            uint32_t& per_unit) {
+  return sched_block_at<LAST_FIRST>(sc, blockIdx.x, band, mt, sub, per_unit);
 }
 
 // Host: schedule for per-band unit sizes units(b) (blocks per (band, row tile)) and per-block

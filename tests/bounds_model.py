@@ -476,7 +476,9 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
                         for r in range(4):
                             bnd.touch("workspace", (mtile * F + off + il + r) * 4, 4,
                                       ((lane & 15) == 0) & (il + r < I))
-        # -- finish: the dx kernel's blocks (band, 64-wide chunk, 64 rows)
+        # -- finish: the dx kernel's blocks (band, 64-wide chunk, 64 rows); with the DMA dW kernel and the
+        # dx schedule they are that kernel's tail blocks, decoded at blockIdx.x minus its scheduled
+        # blocks (a multiple of 8): the same decode and addresses
         if norm:
             for band in range(nb):
                 off, I = int(offs[band]), int(widths[band])
