@@ -216,7 +216,8 @@ class MaskEstimator(nn.Module):
         key = (tuple(indices), device.type, device.index)
         hit = self._index_cache.get(key)
         if hit is None:
-            hit = torch.as_tensor(indices, dtype=torch.long, device=device)
+            with torch.inference_mode(False):  # cached for training steps too
+                hit = torch.as_tensor(indices, dtype=torch.long, device=device)
             self._index_cache[key] = hit
         return hit
 

@@ -64,12 +64,15 @@ class RotaryEmbedding(nn.Module):
         hit = self._cache.get(key)
         if hit is not None:
             return hit
-        pos = torch.arange(seq_len, dtype=torch.float64)
-        inv = 1.0 / (self.theta ** (torch.arange(0, self.dim, 2, dtype=torch.float64)[: self.dim // 2] / self.dim))
-        ang = pos[:, None] * inv[None, :]
-        ang = ang.repeat_interleave(2, dim=-1)
-        cos = ang.cos().to(device=device, dtype=dtype).reshape(1, seq_len, 1, self.dim)
-        sin = ang.sin().to(device=device, dtype=dtype).reshape(1, seq_len, 1, self.dim)
+        # cached tables are normal tensors even when first built in inference mode (validation), so a
+        # later training step can save them for its backward
+        with torch.inference_mode(False):
+            pos = torch.arange(seq_len, dtype=torch.float64)
+            inv = 1.0 / (self.theta ** (torch.arange(0, self.dim, 2, dtype=torch.float64)[: self.dim // 2] / self.dim))
+            ang = pos[:, None] * inv[None, :]
+            ang = ang.repeat_interleave(2, dim=-1)
+            cos = ang.cos().to(device=device, dtype=dtype).reshape(1, seq_len, 1, self.dim)
+            sin = ang.sin().to(device=device, dtype=dtype).reshape(1, seq_len, 1, self.dim)
         self._cache[key] = (cos, sin)
         return cos, sin
 

@@ -4,10 +4,10 @@ The harness a user of the reference runs as ``pymsst compare-direct`` to show th
 the fused backend trains like the stock modules:
 
 * ``seed_everything`` - src/pymsst/validation/direct_compare.py:472-477;
-* ``run_manual_steps`` - the manual loop of direct_compare.py:335-392: autocast,
-  GradScaler (enabled for fp16 only; bf16 needs none), gradient accumulation,
-  optional clipping, loss recorded on steps 1, N and every ``interval``
-  (direct_compare.py:408-409);
+* ``run_manual_steps`` - the behaviour of the manual loop of direct_compare.py:335-392:
+  autocast, GradScaler (enabled for fp16 only; bf16 needs none), gradient
+  accumulation, optional clipping; ``loss_record_steps`` - the steps it records
+  (1, N and every ``interval``, direct_compare.py:407-408);
 * ``write_loss_curve`` / ``read_loss_curve`` - the CSV of direct_compare.py:411-440
   (header ``event,global_step,epoch,batch_idx,loss,val_loss,val_sdr``) and
   comparison.py:244-251;
@@ -45,8 +45,26 @@ def seed_everything(seed: int) -> None:
         torch.cuda.manual_seed_all(seed)
 
 
-def should_record_loss(step: int, total_steps: int, interval: int) -> bool:
-    return interval > 0 and (step == 1 or step == total_steps or step % interval == 0)
+def loss_record_steps(total_steps: int, interval: int) -> frozenset[int]:
+    """The 1-based steps whose loss goes into the curve.
+
+    ``interval`` 0 keeps none; otherwise the first step, the last step and every multiple of
+    ``interval`` are kept (the recording rule of direct_compare.py:407-408)."""
+    if interval < 0:
+        raise ValueError(f"loss_record_interval cannot be negative (got {interval})")
+    if interval == 0 or total_steps < 1:
+        return frozenset()
+    return frozenset(range(interval, total_steps + 1, interval)) | {1, total_steps}
+
+
+def _optimizer_update(model: torch.nn.Module, optimizer: torch.optim.Optimizer, scaler, grad_clip: float) -> None:
+    """One parameter update from the accumulated (possibly scaled) gradients: unscale, clip, step."""
+    scaler.unscale_(optimizer)
+    if grad_clip:
+        torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)
+    scaler.step(optimizer)  # skipped by the scaler when an fp16 gradient overflowed
+    scaler.update()
+    optimizer.zero_grad(set_to_none=True)
 
 
 def run_manual_steps(
@@ -62,36 +80,37 @@ def run_manual_steps(
     grad_clip: float = 0.0,
     loss_record_interval: int = 1,
 ) -> list[tuple[int, float]]:
-    """``loss_fn(model, mixture, target)`` -> scalar loss; returns ``[(step, loss)]``."""
-    if loss_record_interval < 0:
-        raise ValueError("loss_record_interval must be >= 0")
-    use_amp = amp_dtype is not None and device.type == "cuda"
-    scaler = torch.amp.GradScaler(device.type, enabled=use_amp and amp_dtype == torch.float16)
+    """Train ``steps`` steps on ``(target, mixture)`` pairs from ``batches`` and return the recorded
+    ``[(step, loss)]``.
+
+    Behaviour of the reference's manual loop (direct_compare.py:335-392): the forward runs under
+    autocast in ``amp_dtype`` on a GPU (none on the CPU or with ``amp_dtype=None``); fp16 losses are
+    scaled by a GradScaler (bf16 and fp32 need none); gradients of ``grad_accum`` consecutive steps are
+    summed (each loss divided by ``grad_accum``) before one optimizer update, and the last step always
+    updates; ``grad_clip`` > 0 clips the global gradient norm of the unscaled gradients; the recorded
+    loss is the unscaled, undivided one.  Fewer batches than ``steps`` is an error.
+    """
+    if grad_accum < 1:
+        raise ValueError(f"grad_accum must be a positive step count (got {grad_accum})")
+    record = loss_record_steps(steps, loss_record_interval)
+    autocast_on = amp_dtype is not None and device.type == "cuda"
+    scaler = torch.amp.GradScaler(device.type, enabled=autocast_on and amp_dtype == torch.float16)
+    source = iter(batches)
+    curve: list[tuple[int, float]] = []
     optimizer.zero_grad(set_to_none=True)
-    losses: list[tuple[int, float]] = []
-    completed = 0
-    for batch_idx, (target, mixture) in enumerate(batches):
-        if batch_idx >= steps:
-            break
-        step = batch_idx + 1
-        target = target.to(device, non_blocking=True)
-        mixture = mixture.to(device, non_blocking=True)
-        with torch.autocast(device_type=device.type, dtype=amp_dtype or torch.bfloat16, enabled=use_amp):
+    for step in range(1, steps + 1):
+        batch = next(source, None)
+        if batch is None:
+            raise RuntimeError(f"the batch source ran out after {step - 1} of {steps} steps")
+        target, mixture = (t.to(device, non_blocking=True) for t in batch)
+        with torch.autocast(device_type=device.type, dtype=amp_dtype or torch.bfloat16, enabled=autocast_on):
             loss = loss_fn(model, mixture, target)
-        if should_record_loss(step, steps, loss_record_interval):
-            losses.append((step, float(loss.detach().cpu())))
+        if step in record:
+            curve.append((step, float(loss.detach().cpu())))
         scaler.scale(loss / grad_accum).backward()
-        if (batch_idx + 1) % grad_accum == 0 or batch_idx + 1 == steps:
-            scaler.unscale_(optimizer)
-            if grad_clip:
-                torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)
-            scaler.step(optimizer)
-            scaler.update()
-            optimizer.zero_grad(set_to_none=True)
-        completed += 1
-    if completed != steps:
-        raise RuntimeError(f"expected {steps} train steps, got {completed}")
-    return losses
+        if step % grad_accum == 0 or step == steps:
+            _optimizer_update(model, optimizer, scaler, grad_clip)
+    return curve
 
 
 def write_loss_curve(path: str | Path, losses: list[tuple[int, float]]) -> Path:
@@ -250,7 +269,7 @@ __all__ = [
     "run_direct_loss_curve",
     "run_manual_steps",
     "seed_everything",
-    "should_record_loss",
+    "loss_record_steps",
     "summarize_comparisons",
     "write_loss_curve",
 ]

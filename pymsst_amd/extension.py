@@ -615,7 +615,8 @@ class HipFusedExtension:
             for d in dims:
                 offs.append(offs[-1] + d)
             host = (ctypes.c_int64 * len(dims))(*dims)
-            dev = torch.tensor(offs, dtype=torch.int64, device=device)
+            with torch.inference_mode(False):  # cached across modes
+                dev = torch.tensor(offs, dtype=torch.int64, device=device)
             ent = (host, dev, offs)
             self._band_cache[key] = ent
         return ent

@@ -841,7 +841,8 @@ def _dim_offsets_tensor(module, device) -> torch.Tensor:
     key = (device.type, device.index)
     hit = cache.get(key)
     if hit is None:
-        hit = cache[key] = torch.as_tensor(module._dim_offsets, dtype=torch.long, device=device)
+        with torch.inference_mode(False):  # a normal tensor, whichever mode builds the cache
+            hit = cache[key] = torch.as_tensor(module._dim_offsets, dtype=torch.long, device=device)
     return hit
 
 

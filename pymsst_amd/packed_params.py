@@ -9,8 +9,10 @@ step costs one copy per parameter kind per step, plus a cast under autocast.
 each ``nn.Parameter`` at its slice (``param.data`` becomes a view), so the parameters, their names in
 the state dict and the optimizer's view of them are unchanged while their bytes are contiguous.
 :meth:`FlatParams.flat` hands that storage to autograd as one tensor in the compute dtype (at most
-one cast per optimizer step, cached on the parameters' version counters) whose backward splits the
-flat gradient back into per-parameter gradients.  :meth:`FlatParams.group` does the same for a
+one cast per optimizer step, cached on the version counters of the parameters and the storage) whose
+backward splits the flat gradient back into per-parameter gradients.  Writes through ``param.data``
+bypass every version counter: after them, :meth:`FlatParams.invalidate` (or :func:`invalidate_casts` on
+the module) drops the cached casts.  :meth:`FlatParams.group` does the same for a
 contiguous run of equal-shaped parameters, stacked ``[G, ...]`` without a copy.
 
 If a parameter stops being a view of the storage (``module.to(...)`` after packing, a state dict
@@ -24,7 +26,7 @@ from typing import Sequence
 import torch
 from torch import nn
 
-__all__ = ["FlatParams", "pack", "band_split_packs", "mask_layer_packs"]
+__all__ = ["FlatParams", "pack", "band_split_packs", "mask_layer_packs", "invalidate_casts"]
 
 
 class FlatParams:
@@ -43,12 +45,15 @@ class FlatParams:
         self.starts = [0]
         for n in self.sizes:
             self.starts.append(self.starts[-1] + n)
-        storage = torch.empty(self.starts[-1], device=dev, dtype=dt)
-        with torch.no_grad():
-            for p, a, n in zip(params, self.starts, self.sizes):
-                storage[a : a + n].copy_(p.detach().reshape(-1))
-        for p, a, n, shape in zip(params, self.starts, self.sizes, self.shapes):
-            p.data = storage[a : a + n].view(shape)
+        # a pack first built under torch.inference_mode() (a validation pass) must still hold normal
+        # tensors: the parameters are re-pointed at this storage for good, and training saves them
+        with torch.inference_mode(False):
+            storage = torch.empty(self.starts[-1], device=dev, dtype=dt)
+            with torch.no_grad():
+                for p, a, n in zip(params, self.starts, self.sizes):
+                    storage[a : a + n].copy_(p.detach().reshape(-1))
+            for p, a, n, shape in zip(params, self.starts, self.sizes, self.shapes):
+                p.data = storage[a : a + n].view(shape)
         self.storage = storage
         self._casts: dict = {}
 
@@ -63,17 +68,26 @@ class FlatParams:
         return True
 
     def _values(self, dtype: torch.dtype) -> torch.Tensor:
-        """The storage in ``dtype``: the storage itself, or a cast cached until a parameter changes (an
-        in-place update of a parameter -- the optimizer step, ``load_state_dict`` -- bumps that
-        parameter's version counter)."""
+        """The storage in ``dtype``: the storage itself, or a cast cached until the values change.
+
+        The cache key holds the version counters of the storage and of every parameter: an in-place
+        update of a parameter (the optimizer step, ``load_state_dict``) or of the storage bumps one of
+        them.  A write through ``param.data`` bumps none; code that writes that way calls
+        :meth:`invalidate` afterwards.  The cast is made outside inference mode, so one made during an
+        inference-mode validation pass can serve the next training step."""
         if dtype == self.storage.dtype:
             return self.storage.detach()
-        key = (dtype, tuple(p._version for p in self.params))
+        key = (dtype, self.storage._version, tuple(p._version for p in self.params))
         hit = self._casts.get(dtype)
         if hit is None or hit[0] != key:
-            hit = (key, self.storage.detach().to(dtype))
+            with torch.inference_mode(False):
+                hit = (key, self.storage.detach().to(dtype))
             self._casts = {dtype: hit}
         return hit[1]
+
+    def invalidate(self) -> None:
+        """Drop the cached casts (after writes that bypass the version counters, such as ``p.data.copy_``)."""
+        self._casts = {}
 
     def flat(self, dtype: torch.dtype | None = None) -> torch.Tensor:
         """All parameters as one flat tensor in ``dtype`` (default: theirs), differentiable with respect
@@ -137,3 +151,10 @@ def mask_layer_packs(module, layer_index: int) -> tuple[FlatParams, FlatParams |
     if all(l.bias is not None for l in lins):
         bias = pack(module, f"mask.{layer_index}.bias", [l.bias for l in lins])
     return weight, bias
+
+
+def invalidate_casts(module: nn.Module) -> None:
+    """Drop the cached compute-dtype casts of every pack under ``module`` (after ``param.data`` writes)."""
+    for sub in module.modules():
+        for fp in sub.__dict__.get("_pymsst_packs", {}).values():
+            fp.invalidate()

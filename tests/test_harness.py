@@ -75,10 +75,13 @@ def test_summarize_comparisons_thresholds(tmp_path):
         dc.summarize_comparisons([])
 
 
-def test_should_record_loss():
-    rec = [s for s in range(1, 11) if dc.should_record_loss(s, 10, 4)]
-    assert rec == [1, 4, 8, 10]
-    assert not any(dc.should_record_loss(s, 10, 0) for s in range(1, 11))
+def test_loss_record_steps():
+    assert sorted(dc.loss_record_steps(10, 4)) == [1, 4, 8, 10]
+    assert sorted(dc.loss_record_steps(10, 1)) == list(range(1, 11))
+    assert sorted(dc.loss_record_steps(3, 5)) == [1, 3]
+    assert dc.loss_record_steps(10, 0) == frozenset()
+    with pytest.raises(ValueError):
+        dc.loss_record_steps(10, -1)
 
 
 def test_one_stem_waveform_loss_is_per_item():
@@ -146,3 +149,42 @@ def test_manual_loop_is_seeded_and_deterministic_on_cpu():
     assert [s for s, _ in first] == [1, 2, 3]
     assert first == second
     assert all(torch.isfinite(torch.tensor(v)) for _, v in first)
+
+
+def test_manual_loop_accumulates_and_checks_batches():
+    """grad_accum 2 over 3 steps updates after steps 2 and 3 (the last step always updates); each loss is
+    recorded undivided; a batch source shorter than ``steps`` is an error."""
+    updates = []
+
+    class CountingSGD(torch.optim.SGD):
+        def step(self, closure=None):
+            updates.append([p.grad.clone() for p in self.param_groups[0]["params"] if p.grad is not None])
+            return super().step(closure)
+
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(3, 1)
+    batches = [(torch.randn(2, 1), torch.randn(2, 3)) for _ in range(3)]
+
+    def loss_fn(model, mixture, target):
+        return ((model(mixture) - target) ** 2).mean()
+
+    ref = torch.nn.Linear(3, 1)
+    ref.load_state_dict(lin.state_dict())
+    curve = dc.run_manual_steps(model=lin, batches=batches, optimizer=CountingSGD(lin.parameters(), lr=0.1),
+                                device=torch.device("cpu"), steps=3, loss_fn=loss_fn, grad_accum=2)
+    assert len(updates) == 2
+    # the first update's gradient is the mean of the two steps' gradients at the initial weights
+    g = [torch.zeros_like(p) for p in ref.parameters()]
+    for target, mixture in batches[:2]:
+        ref.zero_grad()
+        (loss_fn(ref, mixture, target) / 2).backward()
+        g = [a + p.grad for a, p in zip(g, ref.parameters())]
+    assert all(torch.allclose(a, b) for a, b in zip(updates[0], g))
+    assert [s for s, _ in curve] == [1, 2, 3]
+    assert curve[0][1] == approx(loss_fn(ref, batches[0][1], batches[0][0]).item(), rel=1e-6)
+    with pytest.raises(RuntimeError, match="ran out after 3 of 4"):
+        dc.run_manual_steps(model=lin, batches=batches, optimizer=torch.optim.SGD(lin.parameters(), lr=0.1),
+                            device=torch.device("cpu"), steps=4, loss_fn=loss_fn)
+    with pytest.raises(ValueError):
+        dc.run_manual_steps(model=lin, batches=batches, optimizer=torch.optim.SGD(lin.parameters(), lr=0.1),
+                            device=torch.device("cpu"), steps=3, loss_fn=loss_fn, grad_accum=0)

@@ -218,6 +218,69 @@ def test_flat_params_cast_follows_optimizer_updates_and_device_moves():
     assert pk2 is not pk and pk2.intact() and isinstance(pk2, FlatParams)
 
 
+def _spec_batch(model):
+    g = torch.Generator().manual_seed(1)
+    mix = 0.1 * torch.randn(1, 2, 2048, generator=g)
+    return mix, 0.1 * torch.randn(1, 1, 2, 2048, generator=g)
+
+
+@pytest.mark.parametrize("first", ["inference", "train"])
+def test_packed_params_survive_inference_mode_validation(monkeypatch, first):
+    """The packs and their casts are normal tensors even when first built under torch.inference_mode()
+    (a validation pass): a train step after an inference-mode pass, and one before it, both work, and a
+    cast made during the inference pass is not handed to the training step."""
+    monkeypatch.setenv(fr.EXPERIMENTAL_LAYOUT_REDUCE_COPY_ENV, "1")
+    model = _small_model()
+    fr.apply_roformer_fused_training_backend(model, "cuda_ext", extension=object())
+    mix, target = _spec_batch(model)
+
+    def validate():
+        model.eval()
+        with torch.no_grad():  # an optimizer-like update: the next cast request misses the cache
+            model.band_split.to_features[0][1].weight.add_(0.0)
+        with torch.inference_mode():
+            model(mix)
+            # a bf16 cast made in inference mode
+            bs = model.band_split
+            bs._get_group_params(0, 2, torch.device("cpu"), torch.bfloat16)
+        model.train()
+
+    def train_step():
+        model.train()
+        model(mix, target).backward()
+        bs = model.band_split
+        w = bs._get_group_params(0, 2, torch.device("cpu"), torch.bfloat16)[1]
+        assert not w.is_inference()
+        w.float().sum().backward()  # the cached cast is saved for backward without error
+
+    steps = [validate, train_step, validate, train_step] if first == "inference" else [train_step, validate, train_step]
+    for fn in steps:
+        fn()
+    packs = model.band_split.__dict__["_pymsst_packs"]
+    assert packs and not any(fp.storage.is_inference() for fp in packs.values())
+    assert all(not p.is_inference() for p in model.parameters())
+
+
+def test_flat_params_cast_follows_storage_writes_and_invalidate():
+    """A write to the shared storage refreshes the cached cast by itself; a write through ``param.data``
+    bypasses every version counter and needs ``invalidate``."""
+    from pymsst_amd.packed_params import FlatParams, invalidate_casts
+
+    params = [torch.nn.Parameter(torch.randn(4)) for _ in range(2)]
+    pk = FlatParams(params)
+    c1 = pk.flat(torch.bfloat16).detach().clone()
+    with torch.no_grad():
+        pk.storage.mul_(2)
+    c2 = pk.flat(torch.bfloat16).detach().clone()
+    assert torch.equal(c2, (2 * c1.float()).bfloat16())
+    params[0].data.add_(1)
+    assert torch.equal(pk.flat(torch.bfloat16), c2)  # stale: documented
+    mod = torch.nn.Module()
+    mod.__dict__["_pymsst_packs"] = {"k": pk}
+    invalidate_casts(mod)
+    assert torch.equal(pk.flat(torch.bfloat16), torch.cat([p.detach() for p in params]).bfloat16())
+
+
 def test_packed_band_split_keeps_state_dict_and_is_zero_copy(monkeypatch):
     monkeypatch.setenv(fr.EXPERIMENTAL_LAYOUT_REDUCE_COPY_ENV, "1")
     model = _small_model()
