@@ -187,6 +187,32 @@ int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, in
                                      void* grad_weight, void* grad_bias, int dtype, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
+/* The ragged band split with an fp32 input and a 16-bit projection: fused_band_split.cpp:271-363
+ * band_split_ragged_forward / _backward (.cu:589-1003) called, as fr.py:827-857 does under autocast, with
+ * the fp32 STFT input x (the norm, inv_norm and grad_gamma in fp32, as the reference computes them),
+ * the projection's operands in `dtype` (F16 or BF16) where the stock module rounds them (RMSNorm in
+ * fp32, then nn.Linear in the autocast dtype).  x[rows, x_row_stride] fp32, gamma[F] fp32, weight
+ * and bias in `dtype` (packed as above); features[rows, F] (`dtype`) = x * inv_norm * sqrt(I_b) *
+ * gamma, the projection's input, written for the backward; out[rows, NB, O] (`dtype`);
+ * inv_norm[rows, NB] fp32. */
+int pmsst_band_split_mixed_forward(const float* x, int64_t x_row_stride, const float* gamma, const void* weight,
+                                   const void* bias, const int64_t* dim_offsets, const int64_t* dim_inputs,
+                                   int64_t band_count, int64_t rows, int64_t out_features, void* features, void* out,
+                                   float* inv_norm, int dtype, void* stream);
+/* Workspace bytes of the backward below: the projection's input gradient g[rows, F] (`dtype`),
+ * the per-(row, band) dots and the dgamma partials of every 16 rows (0 when rows == 0). */
+size_t pmsst_band_split_mixed_backward_workspace_size(int64_t rows, int64_t total_in, int64_t band_count);
+/* Backward of pmsst_band_split_mixed_forward: g = grad_out W_b rounded to `dtype` (the stock Linear's
+ * input gradient), then the fp32 RMSNorm backward grad_x[rows, F] = inv (sqrt(I) g gamma - n inv
+ * sum_i g gamma x) with n = x inv sqrt(I), grad_gamma[F] = sum_m g n (fp32); grad_weight = grad_out^T
+ * features, grad_bias = sum_m grad_out (`dtype`; grad_bias may be NULL). */
+int pmsst_band_split_mixed_backward(const void* grad_out, const float* x, int64_t x_row_stride, const void* features,
+                                    const float* inv_norm, const float* gamma, const void* weight,
+                                    const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
+                                    int64_t rows, int64_t out_features, float* grad_x, float* grad_gamma,
+                                    void* grad_weight, void* grad_bias, int dtype, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ grouped linear
  * fused_band_split.cpp:365-388 grouped_linear_forward (.cu:1005-1074):
  * out[m, g, :] = act(W_g x[m, g, :] + b_g) for x[rows, groups, in_features] with row pitch

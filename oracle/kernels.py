@@ -39,6 +39,8 @@ __all__ = [
     "band_split_ragged_forward",
     "band_split_ragged_backward",
     "band_split_ragged_backward_lean",
+    "band_split_mixed_forward",
+    "band_split_mixed_backward",
     "grouped_linear_forward",
     "grouped_linear_backward",
     "mask_estimator_final_forward",
@@ -314,6 +316,54 @@ def band_split_ragged_backward_lean(grad_out, x, inv_norm, gammas, weights, dim_
     return band_split_ragged_backward(grad_out, n, inv_norm, gammas, weights, dim_inputs, dt, acc)
 
 
+def band_split_mixed_forward(x, gammas, weights, biases, dim_inputs, dt: str, acc=np.float64):
+    """The ragged band split of an fp32 input with a 16-bit projection: the call fr.py:827-857 makes under
+    autocast (the STFT input is fp32, so the reference's norm runs in fp32, .cu:589-652), with the
+    projection rounded where the stock module's autocast nn.Linear rounds it: its input
+    ``u = dt(n * gamma)`` and weight in ``dt``, its output ``dt(u W^T + bias)``.
+
+    ``x`` fp32 values, ``gammas`` fp32, ``weights`` / ``biases`` in ``dt``.
+    Returns ``(out[M,NB,O] in dt, u[M,F] in dt, inv[M,NB] fp32)``."""
+    x = _f(x, acc)
+    off = _offsets(dim_inputs)
+    outs, feats, invs = [], [], []
+    for b in range(len(dim_inputs)):
+        xb = x[:, off[b] : off[b + 1]]
+        inv = _inv_norm(xb, acc)
+        n = xb * inv[:, None] * acc(math.sqrt(off[b + 1] - off[b]))
+        u = round_to(n * _f(gammas[b], acc)[None], dt)
+        outs.append(round_to(u @ _f(weights[b], acc).T + _f(biases[b], acc)[None], dt))
+        feats.append(u)
+        invs.append(_inv_out(inv, "f32"))
+    return np.stack(outs, axis=1), np.concatenate(feats, axis=1), np.stack(invs, axis=1)
+
+
+def band_split_mixed_backward(grad_out, x, features, inv_norm, gammas, weights, dim_inputs, dt: str, acc=np.float64):
+    """Backward of :func:`band_split_mixed_forward`: the stock autocast Linear's input gradient
+    ``g = dt(dy W)``, then the fp32 RMSNorm backward of .cu:741-879 (``gn = g gamma``,
+    ``dx = inv (gn sqrt(I) - n (gn . n) / sqrt(I))``, ``dgamma = sum_m g n``); ``dW = dt(dy^T u)``,
+    ``db = dt(sum_m dy)``.  Returns ``(dx fp32, [dgamma_b] fp32, [dW_b] dt, [db_b] dt)``."""
+    dy = _f(grad_out, acc)
+    x = _f(x, acc)
+    u = _f(features, acc)
+    inv = _f(inv_norm, acc)
+    off = _offsets(dim_inputs)
+    dxs, dgs, dws, dbs = [], [], [], []
+    for b in range(len(dim_inputs)):
+        w = off[b + 1] - off[b]
+        scale = acc(math.sqrt(w))
+        xb = x[:, off[b] : off[b + 1]]
+        n = xb * inv[:, b : b + 1] * scale
+        g = round_to(dy[:, b] @ _f(weights[b], acc), dt)
+        gn = g * _f(gammas[b], acc)[None]
+        dot = np.sum(gn * n, axis=-1, keepdims=True)
+        dxs.append(round_to(inv[:, b : b + 1] * (gn * scale - n * (dot / scale)), "f32"))
+        dgs.append(round_to(np.sum(g * n, axis=0), "f32"))
+        dws.append(round_to(dy[:, b].T @ u[:, off[b] : off[b + 1]], dt))
+        dbs.append(round_to(dy[:, b].sum(axis=0), dt))
+    return np.concatenate(dxs, axis=1), dgs, dws, dbs
+
+
 # --------------------------------------------------------------------------- grouped linear
 
 
@@ -383,7 +433,9 @@ def mask_estimator_final_backward(grad_out, x, pre, weights, dim_inputs, dt: str
     ``dbias = sum_m dpre``, ``dx_b = dpre_b W_b``, ``dW_b = dpre_b^T x_b``.
     ``grad_pre_dt``: the grouped mode stores ``dpre`` in the tensor dtype before its GEMMs
     (.cu:2343-2344, ``static_cast<scalar_t>``) while ``dbias`` sums the unrounded values
-    (.cu:2345-2346); ``None`` keeps ``dpre`` unrounded (the direct mode, .cu:2620-2635).
+    (.cu:2345-2346); ``None`` is the direct mode: ``dx`` and ``dbias`` from the unrounded ``dpre``
+    (.cu:2620-2635, 2645-2655), ``dW`` from the ``grad_pre`` it stored in the tensor dtype
+    (.cu:2618-2619 written, .cu:2697-2700 read).
     ``input_act="tanh"``: ``x`` is a tanh output and the first result is the gradient of its
     pre-activation, ``dx * (1 - x^2)`` (chain rule through ``inference_tanh``).
     Returns ``(dx[M,NB,H], dbias[2F], [dW_b])``.
@@ -405,7 +457,8 @@ def mask_estimator_final_backward(grad_out, x, pre, weights, dim_inputs, dt: str
         if grad_pre_dt is not None:
             dpre = round_to(dpre, grad_pre_dt)
         dx[:, b, :] = dpre @ _f(weights[b], acc)
-        dws.append(round_to(dpre.T @ x[:, b, :], dt))
+        dpre_stored = dpre if grad_pre_dt is not None else round_to(dpre, dt)
+        dws.append(round_to(dpre_stored.T @ x[:, b, :], dt))
     if input_act == "tanh":
         # dh in the tensor dtype (the stored product of the grouped form), then tanh's backward
         dx = round_to(dx, dt) * (1.0 - x * x)

@@ -889,6 +889,156 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_dma_kernel(
   }
 }
 
+// ------------------------------------------------------------------ fp32 input, 16-bit projection
+// The band split under autocast: the input is the fp32 STFT, the norm runs in fp32 and only the
+// projection's operands are 16-bit, at the point where the stock module rounds them (its RMSNorm
+// in fp32, then nn.Linear casts its input and weight to the autocast dtype):
+//   forward:  inv = 1 / max(|x_b|, 1e-12) (fp32), u = T(x inv sqrt(I_b) gamma), out = T(u W_b^T + bias)
+//   backward: g = T(dy W_b) (the Linear's input gradient in the autocast dtype), then the fp32
+//             RMSNorm backward dx = inv (sqrt(I) g gamma - n inv sum_i(g gamma x)), n = x inv sqrt(I),
+//             dgamma = sum_m g n (fp32); dW = T(dy^T u), dbias = T(sum_m dy).
+// The GEMMs are the norm-free band kernels above; the two kernels below are the fp32 row
+// reductions and the column-wise elementwise passes around them.
+
+// One wave per (64-row tile, band), one lane per row: lane m sums over its row's band
+//   MODE 0: x^2                     -> out[m, b] = inv = 1 / max(sqrt(sum), 1e-12)
+//   MODE 1: g * gamma * x (g in T)  -> out[m, b] = sum
+// The waves of a block are four row tiles of one band (equal trip counts); the widest bands come
+// first.  Rows past M are clamped to the last row and not stored.
+template <int MODE, typename T, bool V4>
+__global__ __launch_bounds__(256) void band_rowsum_kernel(const float* __restrict__ x, int64_t x_stride,
+                                                          const T* __restrict__ g, const float* __restrict__ gamma,
+                                                          const int64_t* __restrict__ offsets, int NB, int F,
+                                                          int64_t M, int m_tiles, float* __restrict__ out) {
+  const int wave = static_cast<int>(threadIdx.x >> 6), lane = static_cast<int>(threadIdx.x & 63);
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  const int band = NB - 1 - static_cast<int>(w / m_tiles);
+  if (band < 0) return;
+  const int64_t m = (w % m_tiles) * kWave + lane;
+  const int64_t mr = m < M ? m : M - 1;
+  const int off = static_cast<int>(offsets[band]);
+  const int I = static_cast<int>(offsets[band + 1]) - off;
+  const float* xr = x + mr * x_stride + off;
+  const T* gr = MODE == 1 ? g + mr * F + off : nullptr;
+  const float* gm = gamma + off;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (V4) {
+    for (int i = 0; i < I; i += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(xr + i);
+      if constexpr (MODE == 0) {
+        acc[0] += v.x * v.x;
+        acc[1] += v.y * v.y;
+        acc[2] += v.z * v.z;
+        acc[3] += v.w * v.w;
+      } else {
+        float gv[4];
+        load_pack<T, 4>(gr + i, gv);
+        const float4 c = *reinterpret_cast<const float4*>(gm + i);
+        acc[0] += gv[0] * c.x * v.x;
+        acc[1] += gv[1] * c.y * v.y;
+        acc[2] += gv[2] * c.z * v.z;
+        acc[3] += gv[3] * c.w * v.w;
+      }
+    }
+  } else {
+    for (int i = 0; i < I; ++i) {
+      const float v = xr[i];
+      acc[i & 3] += MODE == 0 ? v * v : to_f32(gr[i]) * gm[i] * v;
+    }
+  }
+  const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  if (m < M) out[m * NB + band] = MODE == 0 ? 1.0f / fmaxf(sqrtf(sum), 1.0e-12f) : sum;
+}
+
+// Band of column i: the largest b with offsets[b] <= i (binary search over the device offsets).
+__device__ __forceinline__ int band_of_column(const int64_t* __restrict__ offsets, int NB, int i) {
+  int lo = 0, hi = NB - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (offsets[mid] <= i) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+constexpr int kColRows = 16;  // rows per block of the column passes
+
+// Column-wise pass over a (kColRows-row, 1024-column) tile, 4 consecutive columns per thread (one
+// band: with V4 every band offset is a multiple of 4; else one column per thread):
+//   MODE 0: u[m, i] = T(x inv[m, b] sqrt(I_b) gamma_i)
+//   MODE 1: dx[m, i] = inv (sqrt(I) g gamma_i - n inv dot[m, b]), n = x inv sqrt(I) (fp32), and the
+//           dgamma partial sum_{rows of the tile} g n to partial[row tile, i]
+template <int MODE, typename T, bool V4>
+__global__ __launch_bounds__(256) void band_colpass_kernel(const float* __restrict__ x, int64_t x_stride,
+                                                           const T* __restrict__ g, const float* __restrict__ gamma,
+                                                           const float* __restrict__ inv, const float* __restrict__ dot,
+                                                           const int64_t* __restrict__ offsets, int NB, int F,
+                                                           int64_t M, T* __restrict__ u, float* __restrict__ dx,
+                                                           float* __restrict__ partial) {
+  constexpr int C = V4 ? 4 : 1;
+  const int i = (static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x)) * C;
+  if (i >= F) return;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kColRows;
+  const int band = band_of_column(offsets, NB, i);
+  const int I = static_cast<int>(offsets[band + 1] - offsets[band]);
+  const float root = sqrtf(static_cast<float>(I));
+  float gm[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) gm[c] = gamma[i + c];
+  float dg[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) dg[c] = 0.f;
+  const int rows = static_cast<int>(M - m0 < kColRows ? M - m0 : kColRows);
+  for (int r = 0; r < rows; ++r) {
+    const int64_t m = m0 + r;
+    float xv[C];
+    if constexpr (V4) {
+      const float4 v = *reinterpret_cast<const float4*>(x + m * x_stride + i);
+      xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
+    } else {
+      xv[0] = x[m * x_stride + i];
+    }
+    const float iv = inv[m * NB + band];
+    if constexpr (MODE == 0) {
+      float o[C];
+#pragma unroll
+      for (int c = 0; c < C; ++c) o[c] = xv[c] * iv * root * gm[c];
+      if constexpr (V4) {
+        store_pack<T, 4>(u + m * F + i, o);
+      } else {
+        u[m * F + i] = from_f32<T>(o[0]);
+      }
+    } else {
+      float gv[C];
+      if constexpr (V4) {
+        load_pack<T, 4>(g + m * F + i, gv);
+      } else {
+        gv[0] = to_f32(g[m * F + i]);
+      }
+      const float c1 = iv * dot[m * NB + band];
+      float o[C];
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const float n = xv[c] * iv * root;
+        o[c] = iv * (root * gv[c] * gm[c] - n * c1);
+        dg[c] += gv[c] * n;
+      }
+      if constexpr (V4) {
+        *reinterpret_cast<float4*>(dx + m * F + i) = make_float4(o[0], o[1], o[2], o[3]);
+      } else {
+        dx[m * F + i] = o[0];
+      }
+    }
+  }
+  if constexpr (MODE == 1) {
+    float* pp = partial + static_cast<int64_t>(blockIdx.y) * F + i;
+    if constexpr (V4) {
+      *reinterpret_cast<float4*>(pp) = make_float4(dg[0], dg[1], dg[2], dg[3]);
+    } else {
+      pp[0] = dg[0];
+    }
+  }
+}
+
 // ------------------------------------------------------------------ host side
 
 struct HostBands {
@@ -1202,6 +1352,154 @@ int launch_grouped_bwd(const void* dy, const void* x, const void* weight, const 
   return PMSST_OK;
 }
 
+// ------------------------------------------------------------------ fp32 input, 16-bit projection
+
+bool mixed_vec4(const HostBands& hb, int64_t x_stride, const void* x) {
+  return hb.vec4 && x_stride % 4 == 0 && aligned_to(x, 16);
+}
+
+// Row sums of band_rowsum_kernel<MODE> into out[M, NB].
+template <int MODE, typename T>
+int launch_rowsum(const float* x, int64_t x_stride, const T* g, const float* gamma, const int64_t* offsets,
+                  const HostBands& hb, int64_t M, bool v4, float* out, hipStream_t stream) {
+  const int m_tiles = static_cast<int>((M + kWave - 1) / kWave);
+  const int64_t waves = static_cast<int64_t>(m_tiles) * hb.NB;
+  const dim3 grid(static_cast<unsigned>((waves + 3) / 4));
+  if (v4)
+    hipLaunchKernelGGL((band_rowsum_kernel<MODE, T, true>), grid, dim3(256), 0, stream, x, x_stride, g, gamma, offsets,
+                       hb.NB, hb.F, M, m_tiles, out);
+  else
+    hipLaunchKernelGGL((band_rowsum_kernel<MODE, T, false>), grid, dim3(256), 0, stream, x, x_stride, g, gamma,
+                       offsets, hb.NB, hb.F, M, m_tiles, out);
+  return check_launch("band_rowsum_kernel");
+}
+
+template <int MODE, typename T>
+int launch_colpass(const float* x, int64_t x_stride, const T* g, const float* gamma, const float* inv,
+                   const float* dot, const int64_t* offsets, const HostBands& hb, int64_t M, bool v4, T* u, float* dx,
+                   float* partial, hipStream_t stream) {
+  const int per_block = 256 * (v4 ? 4 : 1);
+  const dim3 grid(static_cast<unsigned>((hb.F + per_block - 1) / per_block),
+                  static_cast<unsigned>((M + kColRows - 1) / kColRows));
+  if (v4)
+    hipLaunchKernelGGL((band_colpass_kernel<MODE, T, true>), grid, dim3(256), 0, stream, x, x_stride, g, gamma, inv,
+                       dot, offsets, hb.NB, hb.F, M, u, dx, partial);
+  else
+    hipLaunchKernelGGL((band_colpass_kernel<MODE, T, false>), grid, dim3(256), 0, stream, x, x_stride, g, gamma, inv,
+                       dot, offsets, hb.NB, hb.F, M, u, dx, partial);
+  return check_launch("band_colpass_kernel");
+}
+
+template <typename T>
+int launch_mixed_fwd(const float* x, int64_t x_stride, const float* gamma, const void* weight, const void* bias,
+                     const int64_t* offsets, const HostBands& hb, int64_t M, int64_t O, void* features, void* out,
+                     float* inv_norm, hipStream_t stream) {
+  const char* op = "band_split_mixed_forward";
+  PMSST_REQUIRE(sizeof(T) == 2, "%s: the projection dtype must be float16 or bfloat16", op);
+  PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
+  PMSST_REQUIRE(O >= 1 && O <= 512, "%s: out_features must be in [1, 512] (got %lld)", op, (long long)O);
+  if (M == 0) return PMSST_OK;
+  PMSST_REQUIRE(x && gamma && weight && offsets && features && out && inv_norm, "%s: null pointer", op);
+  PMSST_REQUIRE(x_stride >= hb.F, "%s: x row stride %lld < total features %d", op, (long long)x_stride, hb.F);
+  PMSST_REQUIRE(gemm_stride_ok(x_stride, sizeof(float)), "%s: rows too long for 32-bit offsets", op);
+  const bool v4 = mixed_vec4(hb, x_stride, x) && aligned_to(gamma, 16) && aligned_to(features, 8);
+  int rc = launch_rowsum<0, T>(x, x_stride, nullptr, gamma, offsets, hb, M, v4, inv_norm, stream);
+  if (rc != PMSST_OK) return rc;
+  rc = launch_colpass<0, T>(x, x_stride, nullptr, gamma, inv_norm, nullptr, offsets, hb, M, v4,
+                            static_cast<T*>(features), nullptr, nullptr, stream);
+  if (rc != PMSST_OK) return rc;
+  return launch_fwd<T>(features, hb.F, nullptr, weight, bias, offsets, hb, M, O, out, nullptr, nullptr, false,
+                       PMSST_ACT_NONE, stream);
+}
+
+size_t mixed_g_bytes(int64_t M, int F) { return align_up(static_cast<size_t>(M) * F * 2, 256); }
+size_t mixed_dot_bytes(int64_t M, int NB) { return align_up(static_cast<size_t>(M) * NB * sizeof(float), 256); }
+size_t mixed_partial_bytes(int64_t M, int F) {
+  return align_up(static_cast<size_t>((M + kColRows - 1) / kColRows) * F * sizeof(float), 256);
+}
+// [g = T(dy W) (16-bit, [M, F]) | dot [M, NB] | dgamma partials [ceil(M / 16), F]]
+size_t mixed_bwd_workspace(int64_t M, int F, int NB) {
+  return M == 0 ? 0 : mixed_g_bytes(M, F) + mixed_dot_bytes(M, NB) + mixed_partial_bytes(M, F);
+}
+
+template <typename T>
+int launch_mixed_bwd(const void* dy, const float* x, int64_t x_stride, const void* features, const float* inv_norm,
+                     const float* gamma, const void* weight, const int64_t* offsets, const HostBands& hb, int64_t M,
+                     int64_t O, float* dx, float* dgamma, void* dw, void* db, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
+  const char* op = "band_split_mixed_backward";
+  PMSST_REQUIRE(sizeof(T) == 2, "%s: the projection dtype must be float16 or bfloat16", op);
+  PMSST_REQUIRE(M >= 0 && M < (int64_t{1} << 31), "%s: bad row count", op);
+  PMSST_REQUIRE(O >= 1 && O <= 512, "%s: out_features must be in [1, 512] (got %lld)", op, (long long)O);
+  PMSST_REQUIRE(gamma && weight && offsets && dgamma && dw && (M == 0 || (dy && x && features && inv_norm && dx)),
+                "%s: null pointer", op);
+  PMSST_REQUIRE(M == 0 || x_stride >= hb.F, "%s: x row stride %lld < total features %d", op, (long long)x_stride, hb.F);
+  PMSST_REQUIRE(gemm_stride_ok(hb.F, sizeof(float)) && gemm_stride_ok(x_stride, sizeof(float)) &&
+                    gemm_stride_ok(int64_t{hb.NB} * O, sizeof(T)),
+                "%s: rows too long for 32-bit tile offsets", op);
+  const size_t need = mixed_bwd_workspace(M, hb.F, hb.NB);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(PMSST_EWORKSPACE, "%s: workspace of %zu bytes needed", op, need);
+  BandArgs a{offsets, M, hb.NB, hb.F, hb.F, static_cast<int>(O), false, false, false};
+  a.vec4 = hb.vec4 && aligned_to(features, 4 * sizeof(T)) && aligned_to(weight, 4 * sizeof(T)) &&
+           aligned_to(dw, 4 * sizeof(T));
+  a.ovec4 = O % 4 == 0 && aligned_to(dy, 4 * sizeof(T));
+  const T* pdy = static_cast<const T*>(dy);
+  const T* pu = static_cast<const T*>(features);
+  const T* pw = static_cast<const T*>(weight);
+  char* ws = static_cast<char*>(workspace);
+  T* g = reinterpret_cast<T*>(ws);
+  float* dot = reinterpret_cast<float*>(ws + mixed_g_bytes(M, hb.F));
+  float* partial = reinterpret_cast<float*>(ws + mixed_g_bytes(M, hb.F) + mixed_dot_bytes(M, hb.NB));
+  if (M > 0) {
+    // g = T(dy W_b): the norm-free dx kernel, one block per existing (band, row tile, 64-wide chunk)
+    const int m_tiles = static_cast<int>((M + kBM - 1) / kBM);
+    const int max_ichunks = (hb.max_width + 63) / 64;
+    const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_ichunks), static_cast<uint32_t>(m_tiles)};
+    BandSched sc;
+    uint32_t per_xcd = 0;
+    const bool sched =
+        build_even_sched(hb.NB, m_tiles, [&](int b) { return (hb.widths[b] + 63) / 64; }, &sc, &per_xcd);
+    const dim3 grid(sched ? per_xcd * kXcds : xg.blocks());
+    const bool gv4 = a.vec4 && a.ovec4;
+    if (gv4)
+      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pu,
+                         nullptr, nullptr, pw, g, nullptr, nullptr, nullptr, 0, max_ichunks, xg, sc, a);
+    else
+      hipLaunchKernelGGL((bs_bwd_dx_kernel<T, false, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, pu,
+                         nullptr, nullptr, pw, g, nullptr, nullptr, nullptr, 0, max_ichunks, xg, sc, a);
+    int rc = check_launch("bs_bwd_dx_kernel");
+    if (rc != PMSST_OK) return rc;
+    // fp32 RMSNorm backward: dot = sum g gamma x per (row, band), then dx and the dgamma partials
+    const bool v4 = mixed_vec4(hb, x_stride, x) && aligned_to(gamma, 16) && aligned_to(dx, 16) &&
+                    aligned_to(g, 8);
+    rc = launch_rowsum<1, T>(x, x_stride, g, gamma, offsets, hb, M, v4, dot, stream);
+    if (rc != PMSST_OK) return rc;
+    rc = launch_colpass<1, T>(x, x_stride, g, gamma, inv_norm, dot, offsets, hb, M, v4, nullptr, dx, partial,
+                              stream);
+    if (rc != PMSST_OK) return rc;
+  }
+  // dW_b = T(dy_b^T u_b), dbias = T(sum_m dy_b): the norm-free register-staged dW kernel (it also
+  // runs for M == 0 and then writes zeros)
+  {
+    const int max_itiles = (hb.max_width + kDwBI - 1) / kDwBI;
+    const XcdGrid xg{static_cast<uint32_t>(hb.NB * max_itiles), static_cast<uint32_t>((O + kDwBO - 1) / kDwBO)};
+    BandSched wsc;
+    const dim3 grid(dw_grid(hb, O, xg, &wsc));
+    if (a.vec4 && a.ovec4)
+      hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false, true>), grid, dim3(kGemmThreads), 0, stream, pdy, pu,
+                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, wsc, a);
+    else
+      hipLaunchKernelGGL((bs_bwd_dw_kernel<T, false, false, false>), grid, dim3(kGemmThreads), 0, stream, pdy, pu,
+                         nullptr, nullptr, static_cast<T*>(dw), static_cast<T*>(db), max_itiles, xg, wsc, a);
+    const int rc = check_launch("bs_bwd_dw_kernel");
+    if (rc != PMSST_OK) return rc;
+  }
+  // dgamma = the column sums of the partials (parts == 0 writes zeros)
+  const int parts = static_cast<int>((M + kColRows - 1) / kColRows);
+  return launch_col_sum(partial, parts, hb.F, dgamma, PMSST_F32, stream);
+}
+
 template <typename F>
 int with_dtype(int dtype, const char* op, F&& f) {
   switch (dtype) {
@@ -1291,6 +1589,50 @@ int pmsst_band_split_ragged_backward(const void* grad_out, const void* saved, in
     return launch_bwd<T>(grad_out, saved, saved_is_input != 0, inv_norm, gamma, weight, dim_offsets, dim_inputs, hb,
                          rows, out_features, grad_x, grad_gamma, grad_weight, grad_bias, workspace, workspace_bytes,
                          static_cast<hipStream_t>(stream));
+  });
+}
+
+int pmsst_band_split_mixed_forward(const float* x, int64_t x_row_stride, const float* gamma, const void* weight,
+                                   const void* bias, const int64_t* dim_offsets, const int64_t* dim_inputs,
+                                   int64_t band_count, int64_t rows, int64_t out_features, void* features, void* out,
+                                   float* inv_norm, int dtype, void* stream) {
+  HostBands hb;
+  int rc = check_bands("band_split_mixed_forward", dim_inputs, band_count, &hb);
+  if (rc != PMSST_OK) return rc;
+  return with_dtype(dtype, "band_split_mixed_forward", [&](auto tag) {
+    using T = decltype(tag);
+    if constexpr (sizeof(T) != 2) {
+      return fail(PMSST_EDTYPE, "band_split_mixed_forward: the projection dtype must be float16 or bfloat16");
+    } else {
+      return launch_mixed_fwd<T>(x, x_row_stride, gamma, weight, bias, dim_offsets, hb, rows, out_features, features,
+                                 out, inv_norm, static_cast<hipStream_t>(stream));
+    }
+  });
+}
+
+size_t pmsst_band_split_mixed_backward_workspace_size(int64_t rows, int64_t total_in, int64_t band_count) {
+  if (rows < 0 || total_in <= 0 || band_count <= 0) return 0;
+  return mixed_bwd_workspace(rows, static_cast<int>(total_in), static_cast<int>(band_count));
+}
+
+int pmsst_band_split_mixed_backward(const void* grad_out, const float* x, int64_t x_row_stride, const void* features,
+                                    const float* inv_norm, const float* gamma, const void* weight,
+                                    const int64_t* dim_offsets, const int64_t* dim_inputs, int64_t band_count,
+                                    int64_t rows, int64_t out_features, float* grad_x, float* grad_gamma,
+                                    void* grad_weight, void* grad_bias, int dtype, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  HostBands hb;
+  int rc = check_bands("band_split_mixed_backward", dim_inputs, band_count, &hb);
+  if (rc != PMSST_OK) return rc;
+  return with_dtype(dtype, "band_split_mixed_backward", [&](auto tag) {
+    using T = decltype(tag);
+    if constexpr (sizeof(T) != 2) {
+      return fail(PMSST_EDTYPE, "band_split_mixed_backward: the projection dtype must be float16 or bfloat16");
+    } else {
+      return launch_mixed_bwd<T>(grad_out, x, x_row_stride, features, inv_norm, gamma, weight, dim_offsets, hb, rows,
+                                 out_features, grad_x, grad_gamma, grad_weight, grad_bias, workspace,
+                                 workspace_bytes, static_cast<hipStream_t>(stream));
+    }
   });
 }
 

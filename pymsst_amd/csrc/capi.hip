@@ -61,6 +61,6 @@ extern "C" {
 
 const char* pmsst_last_error(void) { return pmsst::g_last_error.c_str(); }
 
-int pmsst_abi_version(void) { return 5; }
+int pmsst_abi_version(void) { return 6; }
 
 }  // extern "C"

@@ -676,6 +676,69 @@ class HipFusedExtension:
         check(rc, "pmsst_band_split_ragged_backward")
         return [dx, dg, dw, db]
 
+    def band_split_mixed_forward(self, x, gamma_all, weight_all, bias_all, dim_inputs, dtype):
+        """Ragged band split of an fp32 input with the projection in ``dtype`` (fp16 / bf16): the call
+        fr.py:827-857 makes under autocast, where x is the fp32 STFT.  The norm and ``inv_norm`` are
+        fp32; ``features = dtype(x * inv * sqrt(I_b) * gamma)`` is the projection's input (what the
+        stock nn.Linear sees under autocast) and is returned for the backward.
+
+        ``x[M, >=F]`` fp32 (any row pitch), ``gamma_all[F]`` fp32, ``weight_all`` / ``bias_all`` packed
+        as in :meth:`band_split_ragged_forward_packed`, in ``dtype``.
+        Returns ``[out[M,NB,O] (dtype), features[M,F] (dtype), inv_norm[M,NB] fp32]``.
+        """
+        _req(x.dtype == torch.float32 and gamma_all.dtype == torch.float32, "x and gamma must be float32")
+        _req(dtype in (torch.float16, torch.bfloat16), "the projection dtype must be float16 or bfloat16")
+        _req(weight_all.dtype == dtype and (bias_all is None or bias_all.dtype == dtype),
+             "weight and bias must have the projection dtype")
+        _req(x.dim() == 2 and x.stride(1) == 1, "x must be [rows, features] with contiguous rows")
+        host, dev_offs, offs = self._bands(dim_inputs, x.device)
+        nb, total = len(offs) - 1, offs[-1]
+        _req(x.size(1) >= total, "x has fewer columns than the bands' total width")
+        m = x.size(0)
+        o = weight_all.numel() // total
+        _req(o * total == weight_all.numel(), "packed weight size must be a multiple of the total width")
+        out = torch.empty((m, nb, o), dtype=dtype, device=x.device)
+        feats = torch.empty((m, total), dtype=dtype, device=x.device)
+        inv = torch.empty((m, nb), dtype=torch.float32, device=x.device)
+        with _DeviceGuard(x.device):
+            rc = self._lib.pmsst_band_split_mixed_forward(
+                _ptr(x), x.stride(0), _ptr(gamma_all.contiguous()), _ptr(weight_all.contiguous()),
+                _ptr(None if bias_all is None else bias_all.contiguous()), _ptr(dev_offs), host, nb, m, o,
+                _ptr(feats), _ptr(out), _ptr(inv), dtype_code(dtype), _stream(x.device),
+            )
+        check(rc, "pmsst_band_split_mixed_forward")
+        return [out, feats, inv]
+
+    def band_split_mixed_backward(self, grad_out, x, features, inv_norm, gamma_all, weight_all, dim_inputs,
+                                  has_bias=True):
+        """Backward of :meth:`band_split_mixed_forward`.  ``grad_out[M, NB, O]`` in the projection dtype.
+        Returns ``[grad_x[M,F] fp32, grad_gamma[F] fp32, grad_weight (packed, dtype),
+        grad_bias[NB*O] (dtype) | None]``."""
+        dtype = features.dtype
+        _req(grad_out.dtype == dtype and weight_all.dtype == dtype, "grad_out and weight must have the features' dtype")
+        _req(x.dtype == torch.float32 and gamma_all.dtype == torch.float32, "x and gamma must be float32")
+        _req(x.dim() == 2 and x.stride(1) == 1, "x must be [rows, features] with contiguous rows")
+        host, dev_offs, offs = self._bands(dim_inputs, grad_out.device)
+        nb, total = len(offs) - 1, offs[-1]
+        grad_out = grad_out.contiguous()
+        features = features.contiguous()
+        m = grad_out.size(0)
+        o = grad_out.size(-1)
+        dev = grad_out.device
+        dx = torch.empty((m, total), dtype=torch.float32, device=dev)
+        dg = torch.empty((total,), dtype=torch.float32, device=dev)
+        dw = torch.empty((o * total,), dtype=dtype, device=dev)
+        db = torch.empty((nb * o,), dtype=dtype, device=dev) if has_bias else None
+        ws = _workspace(self._lib.pmsst_band_split_mixed_backward_workspace_size(m, total, nb), dev)
+        with _DeviceGuard(dev):
+            rc = self._lib.pmsst_band_split_mixed_backward(
+                _ptr(grad_out), _ptr(x), x.stride(0), _ptr(features), _ptr(inv_norm.contiguous()),
+                _ptr(gamma_all.contiguous()), _ptr(weight_all.contiguous()), _ptr(dev_offs), host, nb, m, o,
+                _ptr(dx), _ptr(dg), _ptr(dw), _ptr(db), dtype_code(dtype), _ptr(ws), ws.numel(), _stream(dev),
+            )
+        check(rc, "pmsst_band_split_mixed_backward")
+        return [dx, dg, dw, db]
+
     def band_split_ragged_forward(self, x, gammas, weights, biases, dim_inputs, dim_offsets):
         """``.cpp:271-314``: ``x[M, total]``, per-band ``gamma[I]``, ``weight[O, I]``, ``bias[O]`` lists.
 

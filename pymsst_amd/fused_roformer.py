@@ -860,16 +860,23 @@ def _forward_grouped_band_split_cuda_ext(self, x: torch.Tensor) -> torch.Tensor:
     ext = self._pymsst_fused_extension
     bwd_mode = getattr(self, "_pymsst_fused_band_split_bwd_mode", None)
     lead = x.shape[:-1]
-    # Under autocast the stock per-band Linear runs in the autocast dtype and returns it; the
-    # fused op does the same (the reference keeps x's dtype here), so the residual stream that
-    # follows has the stock dtype.
     ragged = _ragged_forward_enabled(ext)
     if ragged and any(net[1].bias is None for net in self.to_features):
         return self._pymsst_original_forward_grouped(x)
-    if torch.is_autocast_enabled("cuda"):
-        x = x.to(torch.get_autocast_dtype("cuda"))
+    # Under autocast the input is the fp32 STFT and the reference runs its kernels in x's dtype
+    # (fr.py:827-857: parameters fetched in x.dtype), so the norm and its gradients are fp32.  With
+    # the mixed op the projection then runs where the stock module's nn.Linear does: operands and
+    # output in the autocast dtype, so the residual stream that follows has the stock dtype.
+    amp = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
     if ragged:
         dims = tuple(int(d) for d in self.dim_inputs)
+        if (amp in (torch.float16, torch.bfloat16) and x.dtype == torch.float32
+                and _packed_band_split_ops(ext) and hasattr(ext, "band_split_mixed_forward")):
+            gamma_p, weight_p, bias_p = band_split_packs(self)
+            if gamma_p.storage.device == x.device and gamma_p.storage.dtype == torch.float32:
+                out = _FusedBandSplitMixed.apply(x.reshape(-1, x.shape[-1]), gamma_p.flat(torch.float32),
+                                                 weight_p.flat(amp), bias_p.flat(amp), ext, dims, amp)
+                return out.reshape(*lead, len(dims), -1)
         if _packed_band_split_ops(ext):
             gamma_p, weight_p, bias_p = band_split_packs(self)
             if gamma_p.storage.device == x.device:
@@ -1024,6 +1031,31 @@ class _FusedBandSplitPacked(torch.autograd.Function):
         dx, dg, dw, db = ctx.extension.band_split_ragged_backward_packed(
             grad_out, x, True, inv_norm, gamma_all, weight_all, ctx.dim_inputs, True)
         return dx, dg, dw, db, None, None
+
+
+class _FusedBandSplitMixed(torch.autograd.Function):
+    """The packed band split of an fp32 input under autocast (fr.py:827-857 with the fp32 STFT): the
+    norm, ``inv_norm``, dx and dgamma in fp32; the projection on ``dtype`` operands, rounded where the
+    stock nn.Linear rounds them (its input ``x * inv * sqrt(I) * gamma`` and its input gradient), with
+    its output and weight / bias gradients in ``dtype``.  Saves x, the projection input and inv_norm."""
+
+    @staticmethod
+    def forward(ctx, x, gamma_all, weight_all, bias_all, extension, dim_inputs, dtype):
+        x = x.contiguous()
+        out, feats, inv_norm = extension.band_split_mixed_forward(x, gamma_all, weight_all, bias_all, dim_inputs,
+                                                                  dtype)
+        ctx.extension, ctx.dim_inputs = extension, dim_inputs
+        ctx.save_for_backward(x, feats, inv_norm, gamma_all, weight_all)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, feats, inv_norm, gamma_all, weight_all = ctx.saved_tensors
+        nb = len(ctx.dim_inputs)
+        grad_out = grad_out.reshape(x.shape[0], nb, -1).to(feats.dtype).contiguous()
+        dx, dg, dw, db = ctx.extension.band_split_mixed_backward(grad_out, x, feats, inv_norm, gamma_all, weight_all,
+                                                                 ctx.dim_inputs, True)
+        return dx, dg, dw, db, None, None, None
 
 
 class _FusedMaskEstimatorFinalPacked(torch.autograd.Function):

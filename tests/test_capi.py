@@ -34,7 +34,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.pmsst_abi_version() == 5
+    assert lib.pmsst_abi_version() == 6
     assert isinstance(_lib.last_error(), str)
 
 
@@ -49,6 +49,12 @@ def test_workspace_queries(lib):
     assert lib.pmsst_mask_estimator_final_backward_workspace_size(1032, 4100, 2) == -(-1032 * 8200 * 2 // 256) * 256
     assert lib.pmsst_mask_estimator_final_backward_workspace_size(0, 4100, 2) == 0
     assert lib.pmsst_grouped_linear_backward_workspace_size(1032, 62, 768) == 0
+    # [g = T(dy W), 16-bit [M, F] | dots [M, NB] fp32 | dgamma partials of every 16 rows]
+    g = -(-1032 * 4100 * 2 // 256) * 256
+    dots = -(-1032 * 62 * 4 // 256) * 256
+    parts = -(-65 * 4100 * 4 // 256) * 256
+    assert lib.pmsst_band_split_mixed_backward_workspace_size(1032, 4100, 62) == g + dots + parts
+    assert lib.pmsst_band_split_mixed_backward_workspace_size(0, 4100, 62) == 0
 
 
 def test_argument_errors_need_no_device(lib):

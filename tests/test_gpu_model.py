@@ -8,12 +8,14 @@ Bars:
   ``1e-5 * max(1, max|g_stock|)`` max-abs (the fp32 bar) and 1e-4 relative L2.
 * bf16 autocast: loss within 2e-2 relative; every gradient within 2e-2 relative L2
   (both of the stock model evaluated at fp32).
-* 100-step seeded fp32 loss curve (AdamW): mean-abs diff <= 1e-4 (comparison.py:223-241
-  statistic).
+* 100-step seeded loss curves (AdamW): mean-abs diff <= 1e-4 (comparison.py:223-241 statistic)
+  at configs[0] in fp32 and in fp16 with a GradScaler (the reference's own curve precision,
+  direct_compare.py:369-382), and at configs[2] in bf16.
 """
 
 from __future__ import annotations
 
+import re
 import sys
 
 import pytest
@@ -46,6 +48,21 @@ def _count_fused_mask_core(monkeypatch) -> list:
         return original(*args)
 
     monkeypatch.setattr(fr._FusedMaskMLPApply, "apply", counted)
+    return calls
+
+
+def _count_mixed_band_split(monkeypatch) -> list:
+    """Counts the calls of the band split that takes the fp32 input under autocast (the reference's
+    precision for the norm, fr.py:827-857)."""
+    calls = []
+    original = fr._FusedBandSplitMixed.apply
+
+    def counted(*args):
+        assert args[0].dtype == torch.float32
+        calls.append(args[-1])
+        return original(*args)
+
+    monkeypatch.setattr(fr._FusedBandSplitMixed, "apply", counted)
     return calls
 
 
@@ -115,9 +132,11 @@ def test_fused_model_bf16_autocast_within_tolerance(hip_env, monkeypatch):
     l32, g32, _ = _loss_and_grads(_BF16_WL, False, target, mixture, None)
     ls, gs, _ = _loss_and_grads(_BF16_WL, False, target, mixture, torch.bfloat16)
     calls = _count_fused_mask_core(monkeypatch)
+    mixed = _count_mixed_band_split(monkeypatch)
     lf, gf, status = _loss_and_grads(_BF16_WL, True, target, mixture, torch.bfloat16, hip_env)
     assert status.active == "cuda_ext"
     assert calls, "the mask estimators did not run with the mask product in their epilogue"
+    assert mixed == [torch.bfloat16], "the band split did not take the fp32 input"
     assert abs(lf - l32) <= 2e-2 * abs(l32), (lf, l32)
     rel = lambda a, b: ((a - b).norm() / b.norm().clamp_min(1e-30)).item()  # noqa: E731
     worst_f, worst_s, bad = 0.0, 0.0, []
@@ -138,10 +157,13 @@ def test_fused_model_dim512_checkpointed(hip_env, amp, monkeypatch):
     target, mixture = workload_batch(_LARGE_WL, seed=0, device="cuda")
     l32, g32, _ = _loss_and_grads(_LARGE_WL, False, target, mixture, None)
     calls = _count_fused_mask_core(monkeypatch)
+    mixed = _count_mixed_band_split(monkeypatch)
     lf, gf, status = _loss_and_grads(_LARGE_WL, True, target, mixture, amp, hip_env)
     assert status.active == "cuda_ext" and status.patched_mask_mlp
-    # the one-pass MLP (and with it the fused mask product) is 16-bit only
+    # the one-pass MLP (and with it the fused mask product) is 16-bit only; under autocast the band
+    # split takes the fp32 input (norm and its gradients in fp32, the projection in bf16)
     assert bool(calls) == (amp is not None)
+    assert mixed == ([amp] if amp is not None else [])
     assert set(gf) == set(g32)
     rel = lambda a, b: ((a - b).norm() / b.norm().clamp_min(1e-30)).item()  # noqa: E731
     if amp is None:
@@ -154,11 +176,28 @@ def test_fused_model_dim512_checkpointed(hip_env, amp, monkeypatch):
         return
     ls, gs, _ = _loss_and_grads(_LARGE_WL, False, target, mixture, amp)
     assert abs(lf - l32) <= 2e-2 * abs(l32), (lf, l32)
-    # small-band gamma gradients (8 elements) are the noisiest statistic here: within 2e-2, or within
-    # twice the stock bf16 model's own error
-    bad = [f"{n}: fused {rel(gf[n], r):.3e} stock {rel(gs[n], r):.3e}" for n, r in g32.items()
-           if rel(gf[n], r) > max(2e-2, 2.0 * rel(gs[n], r))]
-    _report("bf16 dim512", f"loss fp32 {l32:.6f} stock bf16 {ls:.6f} fused bf16 {lf:.6f}")
+    # The configs[2] bar, within 2e-2 or within 1.5x the stock bf16 model's own error, per parameter
+    # tensor of at least 64 elements.  The 8- and 16-element band gammas (sums over ~1900 rows with
+    # 30-40x cancellation) are judged together per kind: measured at two seeds, the stock bf16 model
+    # is itself up to 3.2e-2 off on them, the fused model's median error over the 62 gammas is below
+    # the stock one (1.74e-2 vs 1.94e-2), and yet a few of the 62 land above 1.5x the stock sample
+    # and others far below: one 8-element relative error against another is a noise statistic.
+    small = [n for n, r in g32.items() if r.numel() < 64]
+    kinds: dict = {}
+    for n in small:
+        kinds.setdefault(re.sub(r"\.\d+\.", ".*.", n), []).append(n)
+    cat = lambda g, names: torch.cat([g[n].reshape(-1) for n in names])  # noqa: E731
+    checks = [(n, rel(gf[n], r), rel(gs[n], r)) for n, r in g32.items() if r.numel() >= 64]
+    checks += [(k, rel(cat(gf, v), cat(g32, v)), rel(cat(gs, v), cat(g32, v))) for k, v in kinds.items()]
+    bad = [f"{n}: fused {f:.3e} stock {st:.3e}" for n, f, st in checks if f > max(2e-2, 1.5 * st)]
+    worst = max(checks, key=lambda c: c[1] / max(2e-2, 1.5 * c[2]))
+    worst_small = max(small, key=lambda n: rel(gf[n], g32[n]) / rel(gs[n], g32[n]), default=None)
+    allp = list(g32)
+    _report("bf16 dim512", f"loss fp32 {l32:.6f} stock bf16 {ls:.6f} fused bf16 {lf:.6f}; all gradients: fused "
+            f"{rel(cat(gf, allp), cat(g32, allp)):.3e} stock {rel(cat(gs, allp), cat(g32, allp)):.3e}; closest to the "
+            f"bar: {worst[0]} fused {worst[1]:.3e} stock {worst[2]:.3e}"
+            + (f"; worst single small tensor {worst_small} fused {rel(gf[worst_small], g32[worst_small]):.3e} stock "
+               f"{rel(gs[worst_small], g32[worst_small]):.3e}" if worst_small else ""))
     assert not bad, "; ".join(bad[:5])
 
 
@@ -196,8 +235,26 @@ def test_loss_curve_100_steps_bf16_configs2(hip_env, tmp_path):
             f"fused vs stock bf16: mean abs {cmp.mean_abs_diff:.3e} max abs {cmp.max_abs_diff:.3e}; "
             f"stock bf16 vs stock fp32 (floor): mean abs {floor.mean_abs_diff:.3e} max abs {floor.max_abs_diff:.3e}; "
             f"stock bf16 {cmp.first_original_loss:.6f} -> {cmp.last_original_loss:.6f}")
-    assert cmp.mean_abs_diff <= max(1e-4, floor.mean_abs_diff), (cmp, floor)
+    assert cmp.mean_abs_diff <= 1e-4, (cmp, floor)
     assert cmp.last_original_loss < cmp.first_original_loss  # it trains
+
+
+def test_loss_curve_100_steps_fp16_gradscaler_configs0(hip_env, tmp_path):
+    """The reference's own curve precision (direct_compare.py:369-382): fp16 autocast with a GradScaler,
+    100 seeded AdamW steps at configs[0], fused vs stock, mean-abs loss difference <= 1e-4."""
+    wl = WORKLOADS["bsr_tiny"]
+    runs = {}
+    for impl in ("fused", "stock"):
+        runs[impl] = dc.run_direct_loss_curve(implementation=impl, workload=wl, steps=100, results_path=tmp_path / impl,
+                                              seed=0, amp_dtype=torch.float16, lr=5e-4)
+    assert runs["fused"]["fused_status"]["active"] == "cuda_ext"
+    cmp = dc.compare_loss_curves(runs["fused"]["loss_curve_path"], runs["stock"]["loss_curve_path"])
+    assert cmp.compared_points == 100
+    _report("loss curve bsr_tiny fp16+GradScaler 100 steps",
+            f"mean abs {cmp.mean_abs_diff:.3e} max abs {cmp.max_abs_diff:.3e} "
+            f"stock {cmp.first_original_loss:.6f}->{cmp.last_original_loss:.6f}")
+    assert cmp.mean_abs_diff <= 1e-4, cmp
+    assert cmp.last_original_loss < cmp.first_original_loss
 
 
 def test_eval_mode_and_cpu_inputs_use_stock_path(hip_env):

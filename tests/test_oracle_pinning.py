@@ -15,6 +15,7 @@ import pytest
 import torch
 
 import oracle
+from oracle import round_to
 from tests import torch_reference as tr
 
 TOL = 1e-10  # float64 vs float64
@@ -230,6 +231,74 @@ def test_band_split_ragged_vs_autograd(dim_inputs, m, o, seed):
             x[:, None, off[k] : off[k + 1]], gammas[k][None], weights[k][None], biases[k][None], "f64"
         )
         _close(out[:, k], ob[:, 0], what="ragged==group")
+
+
+@pytest.mark.parametrize("dt,tdt", [("bf16", torch.bfloat16), ("f16", torch.float16)])
+@pytest.mark.parametrize("dim_inputs,m,o,seed", [((3, 5, 2, 7), 5, 4, 7), ((8, 8, 16, 48), 6, 12, 1)])
+def test_band_split_mixed_vs_autocast_autograd(dim_inputs, m, o, seed, dt, tdt):
+    """The fp32-input band split with a 16-bit projection against torch float64 autograd of the stock
+    module under autocast (RMSNorm in fp32, nn.Linear on 16-bit operands), where the rounding of the
+    projection's input and of its input gradient comes from the casts' autograd, not from the oracle's
+    formula.  A backward that skips the rounding of the Linear's input gradient is caught."""
+    r = _rng(seed)
+    x = round_to(0.05 * r.standard_normal((m, sum(dim_inputs))), "f32")
+    x[0, : dim_inputs[0]] = 0.0  # a zero band row: inv = 1e12
+    gammas = [round_to(1 + 0.1 * r.standard_normal(d), "f32") for d in dim_inputs]
+    weights = [round_to(r.standard_normal((o, d)) / math.sqrt(d), dt) for d in dim_inputs]
+    biases = [round_to(0.1 * r.standard_normal(o), dt) for _ in dim_inputs]
+    out, feats, inv = oracle.band_split_mixed_forward(x, gammas, weights, biases, dim_inputs, dt)
+    tx = _t(x, True)
+    tg = [_t(v, True) for v in gammas]
+    tw = [_t(v, True) for v in weights]
+    tb = [_t(v, True) for v in biases]
+    ref = tr.band_split_ragged_autocast(tx, tg, tw, tb, dim_inputs, tdt)
+    eps16 = 2.0**-8 if dt == "bf16" else 2.0**-11
+    # the only difference is fp32 (oracle) vs float64 (reference) rounding before the 16-bit roundings
+    mism = np.abs(out - ref.detach().numpy()) > 1e-12
+    assert mism.mean() < 0.02, mism.mean()
+    _close(out, ref, tol=2 * eps16, what="out")
+    dy = round_to(r.standard_normal((m, len(dim_inputs), o)), dt)
+    ref.backward(_t(dy))
+    dx, dgs, dws, dbs = oracle.band_split_mixed_backward(dy, x, feats, inv, gammas, weights, dim_inputs, dt)
+    _close(dx, tx.grad, tol=1e-5, what="dx")
+    off = np.cumsum((0,) + tuple(dim_inputs))
+    for k in range(len(dim_inputs)):
+        _close(dgs[k], tg[k].grad, tol=1e-5, what=f"dgamma{k}")
+        _close(dws[k], tw[k].grad, tol=eps16, what=f"dW{k}")
+        _close(dbs[k], tb[k].grad, tol=eps16, what=f"db{k}")
+    # planted mistake: the Linear's input gradient left unrounded moves dx past the bar
+    n_all = np.concatenate([x[:, off[k]:off[k + 1]] * inv[:, k:k + 1] * math.sqrt(d)
+                            for k, d in enumerate(dim_inputs)], axis=1)
+    bad = []
+    for k, d in enumerate(dim_inputs):
+        g = dy[:, k] @ weights[k]  # not rounded
+        gn = g * gammas[k][None]
+        nk = n_all[:, off[k]:off[k + 1]]
+        dot = np.sum(gn * nk, axis=-1, keepdims=True)
+        bad.append(inv[:, k:k + 1] * (gn * math.sqrt(d) - nk * dot / math.sqrt(d)))
+    with pytest.raises(AssertionError):
+        _close(np.concatenate(bad, axis=1), tx.grad, tol=1e-5, what="planted")
+
+
+def test_mask_final_direct_mode_rounding_points():
+    """The direct mode (.cu:2585-2704) and the grouped mode (.cu:2312-2367) share dbias (fp32 sums of the
+    unrounded dpre) and dW (from the dpre stored in the tensor dtype); only dx differs: the direct mode
+    multiplies the unrounded dpre, the grouped mode the stored one."""
+    r = _rng(41)
+    dims = (3, 8, 5)
+    m, h = 7, 16
+    x = round_to(r.standard_normal((m, len(dims), h)), "bf16")
+    w = [round_to(r.standard_normal((2 * d, h)) / 4, "bf16") for d in dims]
+    pre = round_to(r.standard_normal((m, 2 * sum(dims))), "bf16")
+    g = round_to(r.standard_normal((m, sum(dims))), "bf16")
+    dx_d, db_d, dw_d = oracle.mask_estimator_final_backward(g, x, pre, w, dims, "bf16")
+    dx_g, db_g, dw_g = oracle.mask_estimator_final_backward(g, x, pre, w, dims, "bf16", grad_pre_dt="bf16")
+    assert np.array_equal(db_d, db_g)
+    assert all(np.array_equal(a, b) for a, b in zip(dw_d, dw_g))
+    assert not np.array_equal(dx_d, dx_g)
+    # the direct dx is the unrounded product: the f64 oracle (no rounding anywhere) rounded once
+    dx_exact, _, _ = oracle.mask_estimator_final_backward(g, x, pre, w, dims, "f64")
+    assert np.array_equal(dx_d, round_to(dx_exact, "bf16"))
 
 
 # ------------------------------------------------------------------ grouped linear / mask estimator

@@ -49,6 +49,43 @@ def band_split_ragged(x, gammas, weights, biases, dim_inputs):
     return torch.stack(outs, dim=-2)
 
 
+class _AutocastCast(torch.autograd.Function):
+    """An fp32 tensor entering a 16-bit autocast op, in float64: forward rounds to fp32 then to
+    ``dtype``; backward hands back the gradient the op produced, which is in ``dtype`` too."""
+
+    @staticmethod
+    def forward(ctx, t, dtype):
+        ctx.dtype = dtype
+        return t.float().to(dtype).double()
+
+    @staticmethod
+    def backward(ctx, grad):
+        return grad.to(ctx.dtype).double(), None
+
+
+class _OutputCast(torch.autograd.Function):
+    """The 16-bit output of an autocast op, in float64: forward rounds, backward passes through."""
+
+    @staticmethod
+    def forward(ctx, t, dtype):
+        return t.float().to(dtype).double()
+
+    @staticmethod
+    def backward(ctx, grad):
+        return grad, None
+
+
+def band_split_ragged_autocast(x, gammas, weights, biases, dim_inputs, dtype):
+    """The stock band split under autocast in ``dtype``: RMSNorm in fp32 on the fp32 input, then the
+    per-band nn.Linear on ``dtype`` operands (its input and weight cast by autocast) with a ``dtype``
+    output.  ``weights`` / ``biases`` hold ``dtype`` values."""
+    outs = []
+    for xb, g, w, b in zip(x.split(list(dim_inputs), dim=-1), gammas, weights, biases):
+        u = _AutocastCast.apply(rms_norm(xb, g), dtype)
+        outs.append(_OutputCast.apply(F.linear(u, w, b), dtype))
+    return torch.stack(outs, dim=-2)
+
+
 def grouped_linear(x, weight, bias):
     group_count, _, in_features = weight.shape
     leading = x.shape[:-2]
