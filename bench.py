@@ -443,9 +443,38 @@ _TRAIN = {
 }
 
 
-def _train_leg(torch, cfg: int, steps: int, warmup: int, impls=("stock", "fused")) -> dict:
+def _device_work_per_step(torch, train_step, nsteps: int) -> dict:
+    """Device copies, fills and kernel launches per steady-state train step (torch.profiler over ``nsteps``
+    untimed steps after the timed ones)."""
+    from torch.profiler import ProfilerActivity, profile
+
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+        for _ in range(nsteps):
+            train_step()
+        torch.cuda.synchronize()
+    rows = {r.key: r for r in prof.key_averages()}
+
+    def per(key):
+        r = rows.get(key)
+        return {"count": round(r.count / nsteps, 1), "ms": round(r.device_time_total / nsteps / 1e3, 3)} if r else \
+            {"count": 0, "ms": 0.0}
+
+    launch_apis = ("hipLaunchKernel", "hipExtModuleLaunchKernel", "hipModuleLaunchKernel")
+    return {
+        "memcpy_dtod": per("Memcpy DtoD (Device -> Device)"),
+        "memcpy_htod": per("Memcpy HtoD (Host -> Device)"),
+        "memcpy_dtoh": per("Memcpy DtoH (Device -> Host)"),
+        "memset": per("Memset (Device)"),
+        "kernel_launches": round(sum(rows[k].count for k in launch_apis if k in rows) / nsteps, 1),
+        "method": f"torch.profiler over {nsteps} steady-state steps after the timed ones",
+    }
+
+
+def _train_leg(torch, cfg: int, steps: int, warmup: int, impls=("stock", "fused"), profile_steps: int = 0) -> dict:
     """Samples/s of full training steps (forward, backward, AdamW step) = batch / median step time, for the
-    stock modules and for the model patched onto the HIP kernels (same seed, same batch)."""
+    stock modules and for the model patched onto the HIP kernels (same seed, same batch); the median time
+    the host takes to enqueue a step; with ``profile_steps`` the device copies and launches per step."""
     import statistics
 
     from pymsst_amd import fused_roformer as fr
@@ -469,23 +498,33 @@ def _train_leg(torch, cfg: int, steps: int, warmup: int, impls=("stock", "fused"
         else:
             os.environ[fr.CORE_GROUPED_TRAIN_ENV] = "1"
         opt = torch.optim.AdamW(model.parameters(), lr=wl.lr)
-        times, losses = [], []
-        for i in range(warmup + steps):
-            print(f"[train] configs[{cfg}] {impl} step {i}", file=sys.stderr, flush=True)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
+
+        def train_step():
             with torch.autocast("cuda", dtype=wl.amp_dtype or torch.float32, enabled=wl.amp_dtype is not None):
                 loss = model(mixture, target)
             loss.backward()
             opt.step()
             opt.zero_grad(set_to_none=True)
+            return loss
+
+        times, enqueue, losses = [], [], []
+        for i in range(warmup + steps):
+            print(f"[train] configs[{cfg}] {impl} step {i}", file=sys.stderr, flush=True)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            loss = train_step()
+            t_enq = time.perf_counter()
             torch.cuda.synchronize()
             if i >= warmup:
                 times.append(time.perf_counter() - t0)
+                enqueue.append(t_enq - t0)
                 losses.append(float(loss.detach()))
         med = statistics.median(times)
         out[impl] = {"ms_median": round(med * 1e3, 2), "samples_per_s": round(wl.batch / med, 3),
+                     "host_enqueue_ms_median": round(statistics.median(enqueue) * 1e3, 2),
                      "first_loss": round(losses[0], 6), "last_loss": round(losses[-1], 6)}
+        if profile_steps > 0:
+            out[impl]["per_step_device_work"] = _device_work_per_step(torch, train_step, profile_steps)
         fr.restore_stock_implementations(model)
         del model, opt
         torch.cuda.empty_cache()
@@ -577,7 +616,7 @@ def main(argv=None) -> int:
     if args.train_steps > 0:
         cfgs = [int(c) for c in args.train_configs.split(",") if c.strip()]
         head = 2 if 2 in cfgs else cfgs[0]
-        train = _train_leg(torch, head, args.train_steps, args.train_warmup, impls)
+        train = _train_leg(torch, head, args.train_steps, args.train_warmup, impls, profile_steps=2)
         others = {}
         for cfg in cfgs:
             if cfg != head:
