@@ -38,6 +38,19 @@ LOWP_TOL = 2e-2
 LOWP_FLOOR = 2e-2  # absolute floor of the 16-bit bar, as a fraction of the group's rms(ref)
 
 
+# fp32 checks whose bar was scaled above the flat 1e-5 (reference values larger than 1), reported at the
+# end of the session
+F32_SCALED: list = []
+
+
+def pytest_terminal_summary(terminalreporter):
+    if F32_SCALED:
+        worst = sorted(F32_SCALED, key=lambda v: -v[1])[:5]
+        terminalreporter.write_line(
+            f"fp32 parity bars scaled by max(1, max|ref|): {len(F32_SCALED)} checks, largest scales: "
+            + ", ".join(f"{w or '?'} x{sc:.3g}" for w, sc in worst))
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP GPU (MI355X) and the built libpymsst_amd.so")
 
@@ -113,7 +126,11 @@ def assert_parity(actual, ref, dtype_name: str, what: str = "", groups=None) -> 
     assert np.all(np.isfinite(a)), f"{what}: non-finite values"
     err, bound = parity_error(actual, ref, dtype_name, groups)
     if dtype_name == "f32":
-        assert err <= bound, f"{what}: max abs err {err:.3e} > bound {bound:.3e} ({dtype_name})"
+        scale = bound / FP32_TOL
+        if scale > 1.0:
+            F32_SCALED.append((what, scale))
+        assert err <= bound, (f"{what}: max abs err {err:.3e} > bound {bound:.3e} = 1e-5 x max(1, max|ref|) with "
+                              f"max|ref| = {float(np.max(np.abs(to_np(ref)))):.3e} (scale {scale:.3e}, {dtype_name})")
     else:
         r = to_np(ref)
         i = int(np.argmax(np.abs(a - r) / _lowp_bound(r, groups)))
