@@ -50,7 +50,7 @@ BSR_WIDTHS = tuple([8] * 24 + [16] * 12 + [48] * 8 + [96] * 8 + [192] * 8 + [512
 # ops of the step that are one kernel launched n times per op call: the roofline candidates
 SINGLE_KERNEL_OPS = {
     "band_split_fwd": ("bs_fwd_kernel", 1),
-    "qk_norm_rotary_fwd": ("norm_rot_fwd_kernel", 2),
+    "qk_norm_rotary_fwd": ("norm_rot_fwd_kernel", 1),
     "mask_hidden_fwd": ("bs_fwd_kernel", 1),
     "mask_final_fwd": ("me_fwd_dma_kernel", 1),
     "mask_mlp_fwd": ("mlp_fwd_kernel", 1),
@@ -153,13 +153,12 @@ class Workload:
         def bs_bwd():
             e.band_split_ragged_backward_packed(w.g_bs, w.x, True, st["bs"][2], w.gamma_bs, w.w_bs, w.dims, True)
 
-        def qk_fwd():
-            st["q"] = e.rms_norm_rotary_forward(w.q, w.gamma_q, w.cos, w.sin)
-            st["k"] = e.rms_norm_rotary_forward(w.k, w.gamma_k, w.cos, w.sin)
+        def qk_fwd():  # q and k in one launch
+            st["qk"] = e.rms_norm_rotary_pair_forward(w.q, w.k, w.gamma_q, w.gamma_k, w.cos, w.sin)
 
         def qk_bwd():
-            e.rms_norm_rotary_backward(w.g_q, w.q, st["q"][1], w.gamma_q, w.cos, w.sin)
-            e.rms_norm_rotary_backward(w.g_k, w.k, st["k"][1], w.gamma_k, w.cos, w.sin)
+            e.rms_norm_rotary_pair_backward(w.g_q, w.g_k, w.q, w.k, st["qk"][2], st["qk"][3], w.gamma_q, w.gamma_k,
+                                            w.cos, w.sin)
 
         def hid_fwd():
             st["hid"] = e.grouped_linear_forward_act(w.h, w.w1, w.b1, activation="tanh")

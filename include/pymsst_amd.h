@@ -149,6 +149,22 @@ int pmsst_rms_norm_rotary_backward(const void* grad_out, const void* x, const fl
                                    int64_t cs_stride_pair, int dtype, int gamma_dtype, void* workspace,
                                    size_t workspace_bytes, void* stream);
 
+/* The two ops above on q and k together (two tensors of one shape, each with its own gamma and
+ * inv_norm) in one launch each way: this build's addition, no reference counterpart (the reference
+ * calls rotary_forward / rotary_backward once per tensor, fr.py:722-727).  grad_gamma[2 * dim] holds
+ * q's dgamma, then k's; the workspace is pmsst_rms_norm_rotary_backward_workspace_size(rows, 2 * dim). */
+int pmsst_rms_norm_rotary_pair_forward(const void* x0, const void* x1, const void* gamma0, const void* gamma1,
+                                       const void* cos, const void* sin, void* out0, void* out1, float* inv_norm0,
+                                       float* inv_norm1, int64_t batch, int64_t seq, int64_t heads, int64_t dim,
+                                       int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype, int gamma_dtype,
+                                       void* stream);
+int pmsst_rms_norm_rotary_pair_backward(const void* grad_out0, const void* grad_out1, const void* x0, const void* x1,
+                                        const float* inv_norm0, const float* inv_norm1, const void* gamma0,
+                                        const void* gamma1, const void* cos, const void* sin, void* grad_x0,
+                                        void* grad_x1, void* grad_gamma, int64_t batch, int64_t seq, int64_t heads,
+                                        int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype,
+                                        int gamma_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ band split
  * Ragged per-band RMSNorm + Linear (BS-RoFormer / MBR front end).  Band b spans
  * columns [off_b, off_b + I_b) of x with off = exclusive prefix sum of

@@ -304,11 +304,29 @@ constexpr int kRowsPerSlot = PMSST_NR_ROWS;
 #define PMSST_NR_GRID 0
 #endif
 
+// One or two tensors of one shape (q and k) in one launch: blocks [0, per_tensor) take tensor 0, the
+// next per_tensor blocks tensor 1; each has its own input, gamma, output and inv_norm.
+template <typename T, typename TG>
+struct NormRotIO {
+  const T* x[2];
+  const TG* gamma[2];
+  T* out[2];         // forward output / backward dx
+  float* inv[2];     // inv_norm (the backward reads it)
+  const T* dy[2];    // backward only
+  int per_tensor;    // blocks per tensor
+};
+
 template <typename T, typename TG, int VEC, int NV, int TS>
-__global__ __launch_bounds__(kNormRotThreads) void norm_rot_fwd_kernel(
-    const T* __restrict__ x, const TG* __restrict__ gamma, const T* __restrict__ cosv, const T* __restrict__ sinv,
-    T* __restrict__ out, float* __restrict__ inv_norm, int64_t rows, int tpr_log2, float scale, FastDiv heads,
-    FastDiv seq, TableRef tab) {
+__global__ __launch_bounds__(kNormRotThreads) void norm_rot_fwd_kernel(NormRotIO<T, TG> io, const T* __restrict__ cosv,
+                                                                    const T* __restrict__ sinv, int64_t rows,
+                                                                    int tpr_log2, float scale, FastDiv heads,
+                                                                    FastDiv seq, TableRef tab) {
+  const int tsel = static_cast<int>(blockIdx.x) >= io.per_tensor ? 1 : 0;
+  const int blk = static_cast<int>(blockIdx.x) - tsel * io.per_tensor;
+  const T* __restrict__ x = io.x[tsel];
+  const TG* __restrict__ gamma = io.gamma[tsel];
+  T* __restrict__ out = io.out[tsel];
+  float* __restrict__ inv_norm = io.inv[tsel];
   const int tpr = 1 << tpr_log2;
   const int dim = VEC * NV * tpr;
   const int lane = threadIdx.x & (kWave - 1);
@@ -322,8 +340,8 @@ __global__ __launch_bounds__(kNormRotThreads) void norm_rot_fwd_kernel(
 #pragma unroll
   for (int v = 0; v < NV; ++v) load_pack<TG, VEC>(gamma + (v * tpr + t) * VEC, g[v]);
 
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block * kRowsPerSlot; base < rows;
-       base += static_cast<int64_t>(gridDim.x) * rows_per_block * kRowsPerSlot) {
+  for (int64_t base = static_cast<int64_t>(blk) * rows_per_block * kRowsPerSlot; base < rows;
+       base += static_cast<int64_t>(io.per_tensor) * rows_per_block * kRowsPerSlot) {
     // every load of the trip (x packs and the cos / sin of each row's position) is issued
     // before the first reduction; the packs stay raw until then
     u32x4_t xr[kRowsPerSlot][NV];
@@ -382,13 +400,21 @@ __global__ __launch_bounds__(kNormRotThreads) void norm_rot_fwd_kernel(
   }
 }
 
+// dgamma partials: block b of tensor t writes row b, columns t * dim .. of partial[per_tensor, ntensors * dim]
 template <typename T, typename TG, int VEC, int NV, int TS>
-__global__ __launch_bounds__(kRowBwdThreads) void norm_rot_bwd_kernel(
-    const T* __restrict__ dy, const T* __restrict__ x, const float* __restrict__ inv_norm,
-    const TG* __restrict__ gamma, const T* __restrict__ cosv, const T* __restrict__ sinv, T* __restrict__ dx,
-    float* __restrict__ partial, int64_t rows, int tpr_log2, float scale, FastDiv heads, FastDiv seq,
-    TableRef tab) {
+__global__ __launch_bounds__(kRowBwdThreads) void norm_rot_bwd_kernel(NormRotIO<T, TG> io, const T* __restrict__ cosv,
+                                                                      const T* __restrict__ sinv,
+                                                                      float* __restrict__ partial, int pitch,
+                                                                      int64_t rows, int tpr_log2, float scale,
+                                                                      FastDiv heads, FastDiv seq, TableRef tab) {
   extern __shared__ float red[];
+  const int tsel = static_cast<int>(blockIdx.x) >= io.per_tensor ? 1 : 0;
+  const int blk = static_cast<int>(blockIdx.x) - tsel * io.per_tensor;
+  const T* __restrict__ dy = io.dy[tsel];
+  const T* __restrict__ x = io.x[tsel];
+  const float* __restrict__ inv_norm = io.inv[tsel];
+  const TG* __restrict__ gamma = io.gamma[tsel];
+  T* __restrict__ dx = io.out[tsel];
   const int tpr = 1 << tpr_log2;
   const int dim = VEC * NV * tpr;
   const int lane = threadIdx.x & (kWave - 1);
@@ -410,8 +436,8 @@ __global__ __launch_bounds__(kRowBwdThreads) void norm_rot_bwd_kernel(
   // the 256 registers of a wave and spill)
   constexpr int RPS = NV >= 3 ? 1 : kRowsPerSlot;
 
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * rows_per_block * RPS; base < rows;
-       base += static_cast<int64_t>(gridDim.x) * rows_per_block * RPS) {
+  for (int64_t base = static_cast<int64_t>(blk) * rows_per_block * RPS; base < rows;
+       base += static_cast<int64_t>(io.per_tensor) * rows_per_block * RPS) {
     // loads of all RPS rows first, held raw until every load of the trip has issued.
     // Rows past the end load the last row (no branch around the loads) and recompute it: their
     // dx stores write the bits the last row's own stores write, and only the dgamma
@@ -493,7 +519,7 @@ __global__ __launch_bounds__(kRowBwdThreads) void norm_rot_bwd_kernel(
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < kRowBwdThreads / kWave; ++w) s += red[w * dim + c];
-    partial[static_cast<int64_t>(blockIdx.x) * dim + c] = s;
+    partial[static_cast<int64_t>(blk) * pitch + tsel * dim + c] = s;
   }
 }
 
@@ -514,32 +540,40 @@ inline int norm_rot_check(const char* op, const NormRotArgs& a, int vec, const v
   return PMSST_OK;
 }
 
+// nt = 1 or 2 tensors of one shape (x[t], gamma[t], out[t], inv_norm[t]), one launch.
 template <typename T, typename TG>
-int launch_norm_rot_fwd(const void* x, const void* gamma, const void* cosv, const void* sinv, void* out,
-                        float* inv_norm, const NormRotArgs& a, hipStream_t stream) {
+int launch_norm_rot_fwd(int nt, const void* const* x, const void* const* gamma, const void* cosv, const void* sinv,
+                        void* const* out, float* const* inv_norm, const NormRotArgs& a, hipStream_t stream) {
   if (a.batch * a.seq * a.heads == 0 && a.dim > 0) return PMSST_OK;
-  PMSST_REQUIRE(x && gamma && cosv && sinv && out && inv_norm, "rms_norm_rotary_forward: null pointer");
   constexpr int kVec = 16 / sizeof(T);
-  const void* ptrs[] = {x, gamma, out};
-  const size_t sizes[] = {sizeof(T), sizeof(TG), sizeof(T)};
-  RowGeom geo;
-  int rc = norm_rot_check("rms_norm_rotary_forward", a, kVec, ptrs, sizes, 3, &geo);
-  if (rc != PMSST_OK) return rc;
+  NormRotIO<T, TG> io{};
+  RowGeom geo{};
+  for (int t = 0; t < nt; ++t) {
+    PMSST_REQUIRE(x[t] && gamma[t] && cosv && sinv && out[t] && inv_norm[t], "rms_norm_rotary_forward: null pointer");
+    const void* ptrs[] = {x[t], gamma[t], out[t]};
+    const size_t sizes[] = {sizeof(T), sizeof(TG), sizeof(T)};
+    const int rc = norm_rot_check("rms_norm_rotary_forward", a, kVec, ptrs, sizes, 3, &geo);
+    if (rc != PMSST_OK) return rc;
+    io.x[t] = static_cast<const T*>(x[t]);
+    io.gamma[t] = static_cast<const TG*>(gamma[t]);
+    io.out[t] = static_cast<T*>(out[t]);
+    io.inv[t] = inv_norm[t];
+  }
   const int64_t rows = a.batch * a.seq * a.heads;
   if (rows == 0) return PMSST_OK;
   const int rpb = (kWave >> geo.tpr_log2) * (kNormRotThreads / kWave) * kRowsPerSlot;
   int64_t blocks64 = (rows + rpb - 1) / rpb;
   if (PMSST_NR_GRID > 0 && blocks64 > static_cast<int64_t>(PMSST_NR_GRID) * num_cus())
     blocks64 = static_cast<int64_t>(PMSST_NR_GRID) * num_cus();
-  const int blocks = static_cast<int>(blocks64 < 65536 ? blocks64 : 65536);
+  io.per_tensor = static_cast<int>(blocks64 < 32768 ? blocks64 : 32768);
+  const int blocks = io.per_tensor * nt;
   const float scale = sqrtf(static_cast<float>(a.dim));
   const FastDiv fh(static_cast<uint32_t>(a.heads)), fs(static_cast<uint32_t>(a.seq));
   const TableRef tab{a.cs_seq, a.cs_pair};
   const int ts = table_mode(cosv, sinv, a.cs_seq, a.cs_pair, kVec, sizeof(T));
 #define PMSST_NRF1(NV, TS)                                                                                        \
   hipLaunchKernelGGL((norm_rot_fwd_kernel<T, TG, kVec, NV, TS>), dim3(blocks), dim3(kNormRotThreads), 0, stream, \
-                     static_cast<const T*>(x), static_cast<const TG*>(gamma), static_cast<const T*>(cosv),        \
-                     static_cast<const T*>(sinv), static_cast<T*>(out), inv_norm, rows, geo.tpr_log2, scale,     \
+                     io, static_cast<const T*>(cosv), static_cast<const T*>(sinv), rows, geo.tpr_log2, scale,    \
                      fh, fs, tab)
 #define PMSST_NRF(NV)                                          \
   do {                                                         \
@@ -559,26 +593,39 @@ int launch_norm_rot_fwd(const void* x, const void* gamma, const void* cosv, cons
   return check_launch("norm_rot_fwd_kernel");
 }
 
+// nt = 1 or 2 tensors of one shape; dgamma[nt * dim] holds tensor t's dgamma at t * dim.
 template <typename T, typename TG>
-int launch_norm_rot_bwd(const void* dy, const void* x, const float* inv_norm, const void* gamma, const void* cosv,
-                        const void* sinv, void* dx, void* dgamma, int gamma_dtype, const NormRotArgs& a,
-                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+int launch_norm_rot_bwd(int nt, const void* const* dy, const void* const* x, const float* const* inv_norm,
+                        const void* const* gamma, const void* cosv, const void* sinv, void* const* dx, void* dgamma,
+                        int gamma_dtype, const NormRotArgs& a, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
   const bool empty = a.batch * a.seq * a.heads == 0;
-  PMSST_REQUIRE(dgamma && gamma && (empty || (dy && x && inv_norm && cosv && sinv && dx)),
-                "rms_norm_rotary_backward: null pointer");
   constexpr int kVec = 16 / sizeof(T);
-  const void* ptrs[] = {dy, x, gamma, dx};
-  const size_t sizes[] = {sizeof(T), sizeof(T), sizeof(TG), sizeof(T)};
-  RowGeom geo;
-  int rc = norm_rot_check("rms_norm_rotary_backward", a, kVec, ptrs, sizes, 4, &geo);
-  if (rc != PMSST_OK) return rc;
+  NormRotIO<T, TG> io{};
+  RowGeom geo{};
+  PMSST_REQUIRE(dgamma != nullptr, "rms_norm_rotary_backward: null pointer");
+  for (int t = 0; t < nt; ++t) {
+    PMSST_REQUIRE(gamma[t] && (empty || (dy[t] && x[t] && inv_norm[t] && cosv && sinv && dx[t])),
+                  "rms_norm_rotary_backward: null pointer");
+    const void* ptrs[] = {dy[t], x[t], gamma[t], dx[t]};
+    const size_t sizes[] = {sizeof(T), sizeof(T), sizeof(TG), sizeof(T)};
+    const int rc = norm_rot_check("rms_norm_rotary_backward", a, kVec, ptrs, sizes, 4, &geo);
+    if (rc != PMSST_OK) return rc;
+    io.dy[t] = static_cast<const T*>(dy[t]);
+    io.x[t] = static_cast<const T*>(x[t]);
+    io.inv[t] = const_cast<float*>(inv_norm[t]);
+    io.gamma[t] = static_cast<const TG*>(gamma[t]);
+    io.out[t] = static_cast<T*>(dx[t]);
+  }
+  int rc = PMSST_OK;
   const int64_t rows = a.batch * a.seq * a.heads;
-  const size_t need = row_bwd_workspace(a.dim);
+  const size_t need = row_bwd_workspace(nt * a.dim);
   if (workspace == nullptr || workspace_bytes < need) {
     return fail(PMSST_EWORKSPACE, "rms_norm_rotary_backward: workspace of %zu bytes needed", need);
   }
   float* partial = static_cast<float*>(workspace);
   const int parts = row_bwd_parts(rows, geo.tpr_log2);
+  io.per_tensor = parts;
   const float scale = sqrtf(static_cast<float>(a.dim));
   const FastDiv fh(static_cast<uint32_t>(a.heads > 0 ? a.heads : 1)), fs(static_cast<uint32_t>(a.seq > 0 ? a.seq : 1));
   const TableRef tab{a.cs_seq, a.cs_pair};
@@ -586,10 +633,9 @@ int launch_norm_rot_bwd(const void* dy, const void* x, const float* inv_norm, co
   if (parts > 0) {
     const int ts = table_mode(cosv, sinv, a.cs_seq, a.cs_pair, kVec, sizeof(T));
 #define PMSST_NRB1(NV, TS)                                                                                           \
-  hipLaunchKernelGGL((norm_rot_bwd_kernel<T, TG, kVec, NV, TS>), dim3(parts), dim3(kRowBwdThreads), shmem, stream, \
-                     static_cast<const T*>(dy), static_cast<const T*>(x), inv_norm, static_cast<const TG*>(gamma),     \
-                     static_cast<const T*>(cosv), static_cast<const T*>(sinv), static_cast<T*>(dx), partial,         \
-                     rows, geo.tpr_log2, scale, fh, fs, tab)
+  hipLaunchKernelGGL((norm_rot_bwd_kernel<T, TG, kVec, NV, TS>), dim3(parts * nt), dim3(kRowBwdThreads), shmem,   \
+                     stream, io, static_cast<const T*>(cosv), static_cast<const T*>(sinv), partial,                   \
+                     static_cast<int>(nt * a.dim), rows, geo.tpr_log2, scale, fh, fs, tab)
 #define PMSST_NRB(NV)                                          \
   do {                                                         \
     if (ts == kTabRepeated) PMSST_NRB1(NV, kTabRepeated);      \
@@ -608,7 +654,7 @@ int launch_norm_rot_bwd(const void* dy, const void* x, const float* inv_norm, co
     rc = check_launch("norm_rot_bwd_kernel");
     if (rc != PMSST_OK) return rc;
   }
-  return launch_col_sum(partial, parts, static_cast<int>(a.dim), dgamma, gamma_dtype, stream);
+  return launch_col_sum(partial, parts, static_cast<int>(nt * a.dim), dgamma, gamma_dtype, stream);
 }
 
 template <typename F>
@@ -692,10 +738,36 @@ int pmsst_rms_norm_rotary_forward(const void* x, const void* gamma, const void* 
   const NormRotArgs a{batch, seq, heads, dim, cs_stride_seq, cs_stride_pair};
   return with_dtype(dtype, "rms_norm_rotary_forward", [&](auto tag) {
     using T = decltype(tag);
+    const void* xs[] = {x};
+    const void* gs[] = {gamma};
+    void* os[] = {out};
+    float* is[] = {inv_norm};
     if (gamma_dtype == PMSST_F32) {
-      return launch_norm_rot_fwd<T, float>(x, gamma, cos, sin, out, inv_norm, a, static_cast<hipStream_t>(stream));
+      return launch_norm_rot_fwd<T, float>(1, xs, gs, cos, sin, os, is, a, static_cast<hipStream_t>(stream));
     }
-    return launch_norm_rot_fwd<T, T>(x, gamma, cos, sin, out, inv_norm, a, static_cast<hipStream_t>(stream));
+    return launch_norm_rot_fwd<T, T>(1, xs, gs, cos, sin, os, is, a, static_cast<hipStream_t>(stream));
+  });
+}
+
+int pmsst_rms_norm_rotary_pair_forward(const void* x0, const void* x1, const void* gamma0, const void* gamma1,
+                                       const void* cos, const void* sin, void* out0, void* out1, float* inv_norm0,
+                                       float* inv_norm1, int64_t batch, int64_t seq, int64_t heads, int64_t dim,
+                                       int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype, int gamma_dtype,
+                                       void* stream) {
+  if (gamma_dtype != dtype && gamma_dtype != PMSST_F32) {
+    return fail(PMSST_EDTYPE, "rms_norm_rotary_forward: gamma dtype must equal x dtype or be fp32");
+  }
+  const NormRotArgs a{batch, seq, heads, dim, cs_stride_seq, cs_stride_pair};
+  return with_dtype(dtype, "rms_norm_rotary_forward", [&](auto tag) {
+    using T = decltype(tag);
+    const void* xs[] = {x0, x1};
+    const void* gs[] = {gamma0, gamma1};
+    void* os[] = {out0, out1};
+    float* is[] = {inv_norm0, inv_norm1};
+    if (gamma_dtype == PMSST_F32) {
+      return launch_norm_rot_fwd<T, float>(2, xs, gs, cos, sin, os, is, a, static_cast<hipStream_t>(stream));
+    }
+    return launch_norm_rot_fwd<T, T>(2, xs, gs, cos, sin, os, is, a, static_cast<hipStream_t>(stream));
   });
 }
 
@@ -715,11 +787,42 @@ int pmsst_rms_norm_rotary_backward(const void* grad_out, const void* x, const fl
   const NormRotArgs a{batch, seq, heads, dim, cs_stride_seq, cs_stride_pair};
   return with_dtype(dtype, "rms_norm_rotary_backward", [&](auto tag) {
     using T = decltype(tag);
+    const void* dys[] = {grad_out};
+    const void* xs[] = {x};
+    const float* is[] = {inv_norm};
+    const void* gs[] = {gamma};
+    void* dxs[] = {grad_x};
     if (gamma_dtype == PMSST_F32) {
-      return launch_norm_rot_bwd<T, float>(grad_out, x, inv_norm, gamma, cos, sin, grad_x, grad_gamma, PMSST_F32, a,
-                                           workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+      return launch_norm_rot_bwd<T, float>(1, dys, xs, is, gs, cos, sin, dxs, grad_gamma, PMSST_F32, a, workspace,
+                                           workspace_bytes, static_cast<hipStream_t>(stream));
     }
-    return launch_norm_rot_bwd<T, T>(grad_out, x, inv_norm, gamma, cos, sin, grad_x, grad_gamma, dtype, a, workspace,
+    return launch_norm_rot_bwd<T, T>(1, dys, xs, is, gs, cos, sin, dxs, grad_gamma, dtype, a, workspace,
+                                     workspace_bytes, static_cast<hipStream_t>(stream));
+  });
+}
+
+int pmsst_rms_norm_rotary_pair_backward(const void* grad_out0, const void* grad_out1, const void* x0, const void* x1,
+                                        const float* inv_norm0, const float* inv_norm1, const void* gamma0,
+                                        const void* gamma1, const void* cos, const void* sin, void* grad_x0,
+                                        void* grad_x1, void* grad_gamma, int64_t batch, int64_t seq, int64_t heads,
+                                        int64_t dim, int64_t cs_stride_seq, int64_t cs_stride_pair, int dtype,
+                                        int gamma_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  if (gamma_dtype != dtype && gamma_dtype != PMSST_F32) {
+    return fail(PMSST_EDTYPE, "rms_norm_rotary_backward: gamma dtype must equal x dtype or be fp32");
+  }
+  const NormRotArgs a{batch, seq, heads, dim, cs_stride_seq, cs_stride_pair};
+  return with_dtype(dtype, "rms_norm_rotary_backward", [&](auto tag) {
+    using T = decltype(tag);
+    const void* dys[] = {grad_out0, grad_out1};
+    const void* xs[] = {x0, x1};
+    const float* is[] = {inv_norm0, inv_norm1};
+    const void* gs[] = {gamma0, gamma1};
+    void* dxs[] = {grad_x0, grad_x1};
+    if (gamma_dtype == PMSST_F32) {
+      return launch_norm_rot_bwd<T, float>(2, dys, xs, is, gs, cos, sin, dxs, grad_gamma, PMSST_F32, a, workspace,
+                                           workspace_bytes, static_cast<hipStream_t>(stream));
+    }
+    return launch_norm_rot_bwd<T, T>(2, dys, xs, is, gs, cos, sin, dxs, grad_gamma, dtype, a, workspace,
                                      workspace_bytes, static_cast<hipStream_t>(stream));
   });
 }

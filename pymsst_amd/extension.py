@@ -389,6 +389,53 @@ class HipFusedExtension:
         return [dx, dgamma]
 
 
+    def rms_norm_rotary_pair_forward(self, q, k, gamma_q, gamma_k, cos, sin):
+        """:meth:`rms_norm_rotary_forward` on q and k (one shape, own gammas) in one launch.
+        Returns ``[q_out, k_out, inv_q, inv_k]``."""
+        _req(q.shape == k.shape and q.dtype == k.dtype and q.device == k.device, "q and k must match")
+        _req(gamma_q.dtype == gamma_k.dtype and gamma_q.shape == gamma_k.shape, "gamma_q and gamma_k must match")
+        self._rot_check(q, cos, sin, "q")
+        _req(gamma_q.is_cuda and gamma_q.dim() == 1 and gamma_q.size(0) == q.size(3), "gamma must have shape [D]")
+        _req(gamma_q.dtype in (q.dtype, torch.float32), "gamma dtype must match x or be float32")
+        q, k = q.contiguous(), k.contiguous()
+        gamma_q, gamma_k = gamma_q.contiguous(), gamma_k.contiguous()
+        cos, sin, s_seq, s_pair = self._tables(cos, sin)
+        b, n, h, d = q.shape
+        qo, ko = torch.empty_like(q), torch.empty_like(k)
+        inv = torch.empty((2, b * n * h), dtype=torch.float32, device=q.device)
+        with _DeviceGuard(q.device):
+            rc = self._lib.pmsst_rms_norm_rotary_pair_forward(
+                _ptr(q), _ptr(k), _ptr(gamma_q), _ptr(gamma_k), _ptr(cos), _ptr(sin), _ptr(qo), _ptr(ko),
+                _ptr(inv[0]), _ptr(inv[1]), b, n, h, d, s_seq, s_pair, dtype_code(q.dtype),
+                dtype_code(gamma_q.dtype), _stream(q.device),
+            )
+        check(rc, "pmsst_rms_norm_rotary_pair_forward")
+        return [qo, ko, inv[0], inv[1]]
+
+    def rms_norm_rotary_pair_backward(self, grad_q, grad_k, q, k, inv_q, inv_k, gamma_q, gamma_k, cos, sin):
+        """Backward of :meth:`rms_norm_rotary_pair_forward` in one launch (and one dgamma reduction).
+        Returns ``[grad_q_in, grad_k_in, grad_gamma_q, grad_gamma_k]``."""
+        _req(grad_q.shape == grad_k.shape == q.shape == k.shape, "q, k and their gradients must have one shape")
+        _req(grad_q.dtype == grad_k.dtype == q.dtype == k.dtype, "q, k and their gradients must have one dtype")
+        self._rot_check(grad_q, cos, sin, "grad_out")
+        _req(inv_q.dtype == torch.float32 and inv_k.dtype == torch.float32 and inv_q.numel() * q.size(3) == q.numel()
+             and inv_k.numel() == inv_q.numel(), "inv_norm length must match flattened rows")
+        grad_q, grad_k, q, k = grad_q.contiguous(), grad_k.contiguous(), q.contiguous(), k.contiguous()
+        gamma_q, gamma_k = gamma_q.contiguous(), gamma_k.contiguous()
+        cos, sin, s_seq, s_pair = self._tables(cos, sin)
+        b, n, h, d = q.shape
+        dq, dk = torch.empty_like(q), torch.empty_like(k)
+        dgamma = torch.empty((2, d), dtype=gamma_q.dtype, device=q.device)
+        ws = _workspace(self._lib.pmsst_rms_norm_rotary_backward_workspace_size(b * n * h, 2 * d), q.device)
+        with _DeviceGuard(q.device):
+            rc = self._lib.pmsst_rms_norm_rotary_pair_backward(
+                _ptr(grad_q), _ptr(grad_k), _ptr(q), _ptr(k), _ptr(inv_q.contiguous()), _ptr(inv_k.contiguous()),
+                _ptr(gamma_q), _ptr(gamma_k), _ptr(cos), _ptr(sin), _ptr(dq), _ptr(dk), _ptr(dgamma), b, n, h, d,
+                s_seq, s_pair, dtype_code(q.dtype), dtype_code(gamma_q.dtype), _ptr(ws), ws.numel(), _stream(q.device),
+            )
+        check(rc, "pmsst_rms_norm_rotary_pair_backward")
+        return [dq, dk, dgamma[0], dgamma[1]]
+
     # ------------------------------------------------------------------ attention gate
 
     @staticmethod

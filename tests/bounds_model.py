@@ -389,7 +389,7 @@ def replay_band_split_forward(widths, M, O, esz, *, norm=True, x_stride=None, ha
     return bnd
 
 
-def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=False):
+def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=False, even_dx=False):
     """band_split.hip launch_bwd (saved input: the split dx kernel writing t = gs * gamma and the dot
     partials, bs_dx_finish_kernel, the DMA-ring or register dW kernel, col_sum) or launch_grouped_bwd
     (grouped=True: the norm-free dx and dW kernels)."""
@@ -423,7 +423,7 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
     if M_dx > 0:
         # norm: the even schedule over the existing (band, row tile, chunk) blocks (the XcdGrid of
         # NB * max_ichunks groups past 256 bands); grouped: the XcdGrid (all groups one width)
-        sc = build_even_sched(nb, m_tiles, lambda b: cdiv(widths[b], 64)) if norm else None
+        sc = build_even_sched(nb, m_tiles, lambda b: cdiv(widths[b], 64)) if norm or even_dx else None
         if sc is not None:
             sched_decode(sc, nb, lambda b: cdiv(widths[b], 64), True, bnd, "bs_bwd_dx")
         else:
@@ -534,6 +534,103 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
         # col_sum_kernel over the m_tiles x F partials -> dgamma
         _replay_col_sum(bnd, "workspace", m_tiles, F, "dgamma", esz)
     return bnd
+
+
+def _replay_band_rowsum(bnd, widths, offs, M, x_stride, mode, gbuf):
+    """band_split.hip band_rowsum_kernel: one wave per (64-row tile, band), lane = row (clamped to the
+    last row); MODE 0 reads x, MODE 1 also g (16-bit, pitch F) and gamma; writes out[m, b] for m < M."""
+    nb, F = len(widths), int(sum(widths))
+    v4 = all(w % 4 == 0 for w in widths) and x_stride % 4 == 0
+    m_tiles = cdiv(M, 64)
+    waves = m_tiles * nb
+    wid = np.arange(cdiv(waves, 4) * 4)
+    band = nb - 1 - wid // m_tiles
+    live_w = band >= 0
+    if np.any(wid[live_w] // m_tiles >= nb):
+        bnd.fail("rowsum: band out of range")
+    lane = np.arange(64)
+    for w in [(nb - 1 - b) * m_tiles + mt for b in range(nb) for mt in sorted({0, m_tiles - 1})]:
+        b = nb - 1 - int(w) // m_tiles
+        mt = int(w) % m_tiles
+        m = mt * 64 + lane
+        mr = np.minimum(m, M - 1)
+        off, I = int(offs[b]), int(widths[b])
+        bnd.touch("offsets", np.array([b, b + 1]) * 8, 8)
+        step = 4 if v4 else 1
+        for i in sorted({0, I - step}):
+            bnd.touch("x", (mr * x_stride + off + i) * 4, 4 * step)
+            if mode == 1:
+                bnd.touch(gbuf, (mr * F + off + i) * 2, 2 * step)
+                bnd.touch("gamma", (off + i) * 4, 4 * step)
+        bnd.touch("inv_norm" if mode == 0 else "dot", (m * nb + b) * 4, 4, m < M)
+    # every (band, row tile) is one wave's: the decode is a bijection
+    seen = {(nb - 1 - int(w) // m_tiles, int(w) % m_tiles) for w in wid[live_w]}
+    if len(seen) != waves:
+        bnd.fail("rowsum: a (band, row tile) is missed or run twice")
+
+
+def _replay_band_colpass(bnd, widths, offs, M, x_stride, mode):
+    """band_split.hip band_colpass_kernel: thread = 4 columns (V4, one band) or 1, block = 16 rows;
+    reads x, inv (and g, dot); writes features (MODE 0) or dx and the partials (MODE 1)."""
+    nb, F = len(widths), int(sum(widths))
+    v4 = all(w % 4 == 0 for w in widths) and x_stride % 4 == 0
+    C = 4 if v4 else 1
+    blocks_x = cdiv(F, 256 * C)
+    parts = cdiv(M, 16)
+    t = np.arange(256)
+    for bx in sorted({0, blocks_x - 1}):
+        i = (bx * 256 + t) * C
+        ok = i < F
+        band = np.searchsorted(offs, np.minimum(i, F - 1), side="right") - 1
+        if np.any(band[ok] < 0) or np.any(band[ok] >= nb):
+            bnd.fail("colpass: band lookup out of range")
+        bk = np.clip(band[ok], 0, nb - 1)
+        if C == 4 and np.any((offs[bk + 1] < i[ok] + 4) | (offs[bk] > i[ok])):
+            bnd.fail("colpass: a 4-column group crosses a band")
+        bnd.touch("gamma", i * 4, 4 * C, ok)
+        for by in sorted({0, parts - 1}):
+            m0 = by * 16
+            for r in sorted({0, min(16, M - m0) - 1}):
+                m = m0 + r
+                bnd.touch("x", (m * x_stride + i) * 4, 4 * C, ok)
+                bnd.touch("inv_norm", (m * nb + np.clip(band, 0, nb - 1)) * 4, 4, ok)
+                if mode == 0:
+                    bnd.touch("features", (m * F + i) * 2, 2 * C, ok)
+                else:
+                    bnd.touch("g", (m * F + i) * 2, 2 * C, ok)
+                    bnd.touch("dot", (m * nb + np.clip(band, 0, nb - 1)) * 4, 4, ok)
+                    bnd.touch("dx", (m * F + i) * 4, 4 * C, ok)
+            if mode == 1:
+                bnd.touch("partial", (by * F + i) * 4, 4 * C, ok)
+
+
+def replay_band_split_mixed(widths, M, O, *, x_stride=None):
+    """band_split.hip launch_mixed_fwd / launch_mixed_bwd (the fp32-input band split, 16-bit projection):
+    rowsum and column passes around the norm-free band GEMMs.  Yields (label, Bounds)."""
+    nb, F = len(widths), int(sum(widths))
+    offs = _offs(widths)
+    x_stride = F if x_stride is None else x_stride
+    fsizes = {"x": ((M - 1) * x_stride + F) * 4, "gamma": F * 4, "inv_norm": M * nb * 4, "features": M * F * 2,
+              "offsets": (nb + 1) * 8}
+    fwd = Bounds(dict(fsizes))
+    _replay_band_rowsum(fwd, widths, offs, M, x_stride, 0, None)
+    _replay_band_colpass(fwd, widths, offs, M, x_stride, 0)
+    yield "band_split_mixed_fwd_norm", fwd
+    # the norm-free GEMM on the 16-bit features (row pitch F)
+    yield "band_split_mixed_fwd_gemm", replay_band_split_forward(widths, M, O, 2, norm=False)
+    gb = cdiv(M * F * 2, 256) * 256
+    db_ = cdiv(M * nb * 4, 256) * 256
+    pb = cdiv(cdiv(M, 16) * F * 4, 256) * 256
+    bsizes = {"x": ((M - 1) * x_stride + F) * 4, "gamma": F * 4, "inv_norm": M * nb * 4, "g": gb, "dot": db_,
+              "partial": pb, "dx": M * F * 4, "dgamma": F * 4, "offsets": (nb + 1) * 8}
+    bwd = Bounds(bsizes)
+    _replay_band_rowsum(bwd, widths, offs, M, x_stride, 1, "g")
+    _replay_band_colpass(bwd, widths, offs, M, x_stride, 1)
+    _replay_col_sum(bwd, "partial", cdiv(M, 16), F, "dgamma", 4)
+    yield "band_split_mixed_bwd_norm", bwd
+    # g = T(dy W) on the norm-free dx kernel and dW / dbias on the norm-free register dW kernel: the
+    # grouped-linear replay of those two kernels (dx = g here, x = the features)
+    yield "band_split_mixed_bwd_gemm", replay_band_split_backward(widths, M, O, 2, grouped=True, even_dx=True)
 
 
 GDX_TILES = {64: (4, 4), 128: (8, 4), 192: (12, 2), 256: (16, 2)}
@@ -1621,6 +1718,8 @@ def all_replays(name: str, esz: int):
     nb = len(widths)
     yield "band_split_fwd", replay_band_split_forward(widths, M, dim, esz)
     yield "band_split_bwd", replay_band_split_backward(widths, M, dim, esz)
+    if esz == 2 and name != "configs0":  # autocast configs: the band split of the fp32 STFT input
+        yield from replay_band_split_mixed(widths, M, dim)
     yield "grouped_linear_fwd", replay_band_split_forward([dim] * nb, M, hidden, esz, norm=False, act_tanh=True)
     yield "grouped_linear_bwd", replay_band_split_backward([dim] * nb, M, hidden, esz, grouped=True)
     yield "mask_final_fwd", replay_mask_final_forward(widths, M, hidden, esz)

@@ -291,3 +291,28 @@ def test_rms_norm_rotary_fused(hip_ext, dtype, gamma_fp32, shape):
     r_dx, r_dg = oracle.rms_norm_rotary_backward(to_np(dy), to_np(x), to_np(inv), to_np(gamma), cn, sn, dn, gdt)
     assert_parity(dx, r_dx, dn, "norm-rot dx")
     assert_parity(dg, r_dg, gdt, "norm-rot dgamma")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("gamma_fp32", [False, True])
+@pytest.mark.parametrize("shape", [(4, 65, 4, 32), (248, 258, 8, 64), (2, 3, 1, 128)])
+def test_rms_norm_rotary_pair_equals_single(hip_ext, dtype, gamma_fp32, shape):
+    """q and k in one launch each way (the configs[1] microbench op): every output bit for bit the
+    single-tensor op's, dgamma included (the pair's column sums run over the same partial rows)."""
+    b, n, h, d = shape
+    q, k = _rand(shape, dtype, 71), _rand(shape, dtype, 72)
+    gq = 1 + 0.1 * _rand((d,), torch.float32, 73)
+    gk = 1 + 0.1 * _rand((d,), torch.float32, 74)
+    if not gamma_fp32:
+        gq, gk = gq.to(dtype), gk.to(dtype)
+    cos, sin = _tables(n, d, dtype)
+    qo, ko, iq, ik = hip_ext.rms_norm_rotary_pair_forward(q, k, gq, gk, cos, sin)
+    sq, siq = hip_ext.rms_norm_rotary_forward(q, gq, cos, sin)
+    sk, sik = hip_ext.rms_norm_rotary_forward(k, gk, cos, sin)
+    assert torch.equal(qo, sq) and torch.equal(ko, sk) and torch.equal(iq, siq) and torch.equal(ik, sik)
+    dq_, dk_ = _rand(shape, dtype, 75), _rand(shape, dtype, 76)
+    dq, dk, dgq, dgk = hip_ext.rms_norm_rotary_pair_backward(dq_, dk_, q, k, iq, ik, gq, gk, cos, sin)
+    sdq, sdgq = hip_ext.rms_norm_rotary_backward(dq_, q, siq, gq, cos, sin)
+    sdk, sdgk = hip_ext.rms_norm_rotary_backward(dk_, k, sik, gk, cos, sin)
+    assert torch.equal(dq, sdq) and torch.equal(dk, sdk)
+    assert torch.equal(dgq, sdgq) and torch.equal(dgk, sdgk)

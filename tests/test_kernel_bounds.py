@@ -72,3 +72,20 @@ def test_replay_flags_an_unclamped_row():
     assert not b.violations()
     bm.krow_loader(b, "x", 2, 64 * 64, 64, 64, 64, 64, True, 0, 2, tid)
     assert b.violations()
+
+
+def test_mixed_band_split_replay_covers_its_buffers_and_flags_mistakes(monkeypatch):
+    """The fp32-input band split's row-sum and column passes touch exactly their buffers at configs[1];
+    a short features buffer and a band lookup that returns the next band are caught."""
+    reps = dict(bm.replay_band_split_mixed(bm.BSR_WIDTHS, 1032, 192))
+    for label, b in reps.items():
+        assert not b.violations(), (label, b.violations())
+    norm = reps["band_split_mixed_fwd_norm"]
+    assert norm.hi["features"] == norm.sizes["features"] and norm.hi["x"] == norm.sizes["x"]
+    b = dict(bm.replay_band_split_mixed(bm.BSR_WIDTHS, 1032, 192))["band_split_mixed_fwd_norm"]
+    b.sizes["features"] -= 2
+    assert any(v.startswith("features:") for v in b.violations())
+    real = bm.np.searchsorted
+    monkeypatch.setattr(bm.np, "searchsorted", lambda a, v, side="left": real(a, v, side=side) + 1)
+    v = dict(bm.replay_band_split_mixed(bm.BSR_WIDTHS, 1032, 192))["band_split_mixed_fwd_norm"].violations()
+    assert v
