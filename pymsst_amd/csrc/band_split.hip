@@ -420,7 +420,7 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dx_kernel(const T* __rest
     if (lane < 16) sdot[wave][j * 16 + lane] = v;
   }
 #pragma unroll
-  for (int r = 0; r < 4; ++r) dgp[r] = group_sum(dgp[r], 16);
+  for (int r = 0; r < 4; ++r) dgp[r] = row16_sum(dgp[r]);
   if ((lane & 15) == 0) {
     float* dst = dg_partial + mtile * a.F + off;
 #pragma unroll
@@ -950,6 +950,60 @@ __global__ __launch_bounds__(256) void band_rowsum_kernel(const float* __restric
   if (m < M) out[m * NB + band] = MODE == 0 ? 1.0f / fmaxf(sqrtf(sum), 1.0e-12f) : sum;
 }
 
+// The same row sums with coalesced loads, one block per row (4-aligned widths, F <= kRowSumMaxF):
+// thread t forms the sums of the row's 4-column quads t, t + 256, ... into LDS; thread p then adds
+// the (at most 16) quads of piece p, the c-th 64-column stretch of band b at p = off_b / 64 + b + c
+// (injective over (b, c < ceil(I_b / 64))), and thread b adds its band's pieces in order.  Every
+// sum runs in a fixed order.
+constexpr int kRowSumMaxF = 16384;
+
+template <int MODE, typename T>
+__global__ __launch_bounds__(256) void band_rowsum_row_kernel(const float* __restrict__ x, int64_t x_stride,
+                                                              const T* __restrict__ g, const float* __restrict__ gamma,
+                                                              const int64_t* __restrict__ offsets, int NB, int F,
+                                                              float* __restrict__ out) {
+  __shared__ float qsum[kRowSumMaxF / 4];
+  __shared__ float psum[kRowSumMaxF / 64 + kSchedMaxBands + 1];
+  __shared__ int soff[kSchedMaxBands + 1];
+  const int64_t m = blockIdx.x;
+  for (int b = threadIdx.x; b <= NB; b += 256) soff[b] = static_cast<int>(offsets[b]);
+  const float* xr = x + m * x_stride;
+  const int nq = F >> 2;
+  for (int q = threadIdx.x; q < nq; q += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(xr + 4 * q);
+    if constexpr (MODE == 0) {
+      qsum[q] = (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    } else {
+      float gv[4];
+      load_pack<T, 4>(g + m * F + 4 * q, gv);
+      const float4 c = *reinterpret_cast<const float4*>(gamma + 4 * q);
+      qsum[q] = (gv[0] * c.x * v.x + gv[1] * c.y * v.y) + (gv[2] * c.z * v.z + gv[3] * c.w * v.w);
+    }
+  }
+  __syncthreads();
+  const int npieces = F / 64 + NB + 1;
+  for (int p = threadIdx.x; p < npieces; p += 256) {
+    int lo = 0, hi = NB - 1;  // the largest b with off_b / 64 + b <= p
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (soff[mid] / 64 + mid <= p) lo = mid; else hi = mid - 1;
+    }
+    const int q0 = soff[lo] / 4 + 16 * (p - soff[lo] / 64 - lo);
+    const int q1 = q0 + 16 < soff[lo + 1] / 4 ? q0 + 16 : soff[lo + 1] / 4;  // none past the band's end
+    float s = 0.f;
+    for (int q = q0; q < q1; ++q) s += qsum[q];
+    psum[p] = s;
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < NB; b += 256) {
+    const int p0 = soff[b] / 64 + b;
+    const int pieces = (soff[b + 1] - soff[b] + 63) / 64;
+    float s = 0.f;
+    for (int c = 0; c < pieces; ++c) s += psum[p0 + c];
+    out[m * NB + b] = MODE == 0 ? 1.0f / fmaxf(sqrtf(s), 1.0e-12f) : s;
+  }
+}
+
 // Band of column i: the largest b with offsets[b] <= i (binary search over the device offsets).
 __device__ __forceinline__ int band_of_column(const int64_t* __restrict__ offsets, int NB, int i) {
   int lo = 0, hi = NB - 1;
@@ -1358,10 +1412,15 @@ bool mixed_vec4(const HostBands& hb, int64_t x_stride, const void* x) {
   return hb.vec4 && x_stride % 4 == 0 && aligned_to(x, 16);
 }
 
-// Row sums of band_rowsum_kernel<MODE> into out[M, NB].
+// Row sums of band_rowsum_row_kernel<MODE> (band_rowsum_kernel<MODE> past its shapes) into out[M, NB].
 template <int MODE, typename T>
 int launch_rowsum(const float* x, int64_t x_stride, const T* g, const float* gamma, const int64_t* offsets,
                   const HostBands& hb, int64_t M, bool v4, float* out, hipStream_t stream) {
+  if (v4 && hb.F <= kRowSumMaxF && hb.NB <= kSchedMaxBands && M < (int64_t{1} << 31)) {
+    hipLaunchKernelGGL((band_rowsum_row_kernel<MODE, T>), dim3(static_cast<unsigned>(M)), dim3(256), 0, stream, x,
+                       x_stride, g, gamma, offsets, hb.NB, hb.F, out);
+    return check_launch("band_rowsum_row_kernel");
+  }
   const int m_tiles = static_cast<int>((M + kWave - 1) / kWave);
   const int64_t waves = static_cast<int64_t>(m_tiles) * hb.NB;
   const dim3 grid(static_cast<unsigned>((waves + 3) / 4));

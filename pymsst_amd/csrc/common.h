@@ -78,6 +78,23 @@ __device__ __forceinline__ float group_sum(float v, int width) {
   return v;
 }
 
+// Sum over each aligned group of 16 lanes (one DPP row) with four DPP moves and no LDS traffic:
+// quad permutes [1,0,3,2] and [2,3,0,1] (xor 1, xor 2), then the mirror within 8 lanes and within
+// the row.  Each step adds two partial sums that every lane of the pair holds, so all 16 lanes end
+// with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  return v;
+}
+
 // Sum over the lanes that share (lane % width): offsets width, 2*width, ..., 32.
 __device__ __forceinline__ float cross_group_sum(float v, int width) {
   for (int off = width; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);

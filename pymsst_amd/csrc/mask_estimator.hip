@@ -378,7 +378,7 @@ __global__ __launch_bounds__(kGemmThreads) void me_fwd_dma_kernel(const T* __res
 // ------------------------------------------------------------------ backward
 
 constexpr int kDpreRows = 64;
-constexpr int kDpreFlatRows = 8;
+constexpr int kDpreFlatRows = 4;  // 4 rows: 10.9 us at configs[1] against 12.5 us with 8
 constexpr int kDpreFlatMaxBands = 4096;  // band offsets in LDS, 16 KB
 
 // dpre over whole rows (aligned case): thread t takes column quad t % (F / 4) of the

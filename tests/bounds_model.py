@@ -536,11 +536,53 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
     return bnd
 
 
+ROWSUM_MAX_F = 16384  # band_split.hip kRowSumMaxF
+
+
+def _replay_band_rowsum_row(bnd, widths, offs, M, x_stride, mode, gbuf):
+    """band_split.hip band_rowsum_row_kernel: one block per row; thread t's quads t + 256 k (x, and g,
+    gamma for MODE 1), the quad sums and piece sums in LDS (piece p of band b at off_b / 64 + b + c),
+    out[m, b].  Rows 0 and M - 1 bound every block's offsets."""
+    nb, F = len(widths), int(sum(widths))
+    nq = F // 4
+    npieces = F // 64 + nb + 1
+    bnd.sizes.setdefault("lds_qsum", ROWSUM_MAX_F)
+    bnd.sizes.setdefault("lds_psum", (ROWSUM_MAX_F // 64 + 256 + 1) * 4)
+    q = np.arange(nq)
+    p = np.arange(npieces)
+    key = offs[:-1] // 64 + np.arange(nb)
+    band = np.searchsorted(key, p, side="right") - 1
+    if np.any(band < 0) or np.any(band >= nb):
+        bnd.fail("rowsum_row: piece band lookup out of range")
+    band = np.clip(band, 0, nb - 1)
+    q0 = offs[band] // 4 + 16 * (p - key[band])
+    q1 = np.minimum(q0 + 16, offs[band + 1] // 4)
+    if np.any(q0[q1 > q0] < 0) or np.any(q1 > nq):
+        bnd.fail("rowsum_row: a piece reads quads outside the row")
+    covered = np.zeros(nq, dtype=np.int64)
+    for a_, b_ in zip(q0, q1):
+        covered[a_:b_] += 1
+    if np.any(covered != 1):
+        bnd.fail("rowsum_row: the pieces do not cover every quad exactly once")
+    bnd.touch("lds_psum", p * 4, 4)
+    bnd.touch("lds_qsum", q * 4, 4)
+    for m in sorted({0, M - 1}):
+        bnd.touch("x", (m * x_stride + 4 * q) * 4, 16)
+        if mode == 1:
+            bnd.touch(gbuf, (m * F + 4 * q) * 2, 8)
+            bnd.touch("gamma", 4 * q * 4, 16)
+        bnd.touch("inv_norm" if mode == 0 else "dot", (m * nb + np.arange(nb)) * 4, 4)
+
+
 def _replay_band_rowsum(bnd, widths, offs, M, x_stride, mode, gbuf):
-    """band_split.hip band_rowsum_kernel: one wave per (64-row tile, band), lane = row (clamped to the
-    last row); MODE 0 reads x, MODE 1 also g (16-bit, pitch F) and gamma; writes out[m, b] for m < M."""
+    """band_split.hip launch_rowsum: band_rowsum_row_kernel where it fits, else band_rowsum_kernel: one
+    wave per (64-row tile, band), lane = row (clamped to the last row); MODE 0 reads x, MODE 1 also g
+    (16-bit, pitch F) and gamma; writes out[m, b] for m < M."""
     nb, F = len(widths), int(sum(widths))
     v4 = all(w % 4 == 0 for w in widths) and x_stride % 4 == 0
+    if v4 and F <= ROWSUM_MAX_F and nb <= 256:
+        _replay_band_rowsum_row(bnd, widths, offs, M, x_stride, mode, gbuf)
+        return
     m_tiles = cdiv(M, 64)
     waves = m_tiles * nb
     wid = np.arange(cdiv(waves, 4) * 4)
@@ -1106,19 +1148,20 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
     dma_dw = esz == 2 and M >= CHUNK_K and H % 128 == 0
     # -- dpre over whole rows
     nq = F // 4
-    flat_threads = cdiv(M, 8) * nq
+    rows = 4  # kDpreFlatRows
+    flat_threads = cdiv(M, rows) * nq
     nblk = cdiv(flat_threads, 256)
     tid = np.arange(256)
     for blk in sorted({0, 1, nblk - 1}):
         t = blk * 256 + tid
-        m0 = t // nq * 8
+        m0 = t // nq * rows
         live = m0 < M
         q = t % nq
         band = np.searchsorted(offs[:-1], 4 * q, side="right") - 1
         off = offs[band]
         I = offs[band + 1] - off
         l = 4 * q - off
-        for r in range(8):
+        for r in range(rows):
             m = np.minimum(m0 + r, M - 1)
             bnd.touch("gout", (m * F + 4 * q) * esz, 4 * esz, live)
             bnd.touch("pre", (m * 2 * F + 2 * off + l) * esz, 4 * esz, live)
