@@ -2,12 +2,13 @@
 //   dx[m, g, :] = dy[m, g, :] W_g          (K = out_features = O, the mask MLP's hidden size)
 // dy[M, G, O], W[G, O, I] (group g's [O, I] weight), dx[M, G, I].
 //
-// Block = (group g, row tile): 4 waves x 16 NT rows.  Each wave accumulates dx^T[I x 16 NT] for its
-// rows over the whole K = O in registers.  Per 32-wide K chunk c a ring stage receives, by global ->
-// LDS DMA, the weight slab W_g[32 c .. 32 c + 31][0 .. I) (shared by the 4 waves; read as transposed
-// A fragments, ds_read_b64_tr_b16) and the block's dy tile dy[rows][g][32 c .. + 31] (each wave moves
-// and reads its own rows; K-contiguous B fragments).  Four stages keep three chunks of both in
-// flight, which the short per-chunk MFMA work needs to cover HBM latency.  dy is read once and dx
+// Block = (group g, row tile): 4 waves x 16 NT rows (NT 2 or 3 at I = 192, picked per shape).  Each
+// wave accumulates dx^T[I x 16 NT] for its rows over the whole K = O in registers.  Per 32-wide K
+// chunk c a ring stage receives, by global -> LDS DMA, the weight slab W_g[32 c .. 32 c + 31][0 .. I)
+// (shared by the 4 waves; read as transposed A fragments, ds_read_b64_tr_b16) and the block's dy tile
+// dy[rows][g][32 c .. + 31] (each wave moves and reads its own rows; K-contiguous B fragments).
+// S stages keep S - 1 chunks of both in flight (S = 4, or 3 for 48-row waves to stay at two blocks
+// per CU), which the short per-chunk MFMA work needs to cover HBM latency.  dy is read once and dx
 // written once; the weight comes from L2.  No atomics.
 #include "common.h"
 #include "dma_gemm.h"
@@ -17,17 +18,14 @@
 namespace pmsst {
 namespace {
 
-constexpr int kGdxStages = 4;
-
 struct GdxArgs {
   int64_t M;
   int G, O, I;
 };
 
-template <typename T, int DT, int NT>
-__global__ __launch_bounds__(256) void glin_dx_kernel(const T* __restrict__ dy, const T* __restrict__ w,
+template <typename T, int DT, int NT, int S>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void glin_dx_kernel(const T* __restrict__ dy, const T* __restrict__ w,
                                                       T* __restrict__ dx, GdxArgs a, BandSched sc) {
-  constexpr int S = kGdxStages;
   constexpr int I = 16 * DT;               // input features
   constexpr int kUnits = I / 8;            // 16-byte units per weight row
   constexpr int kSlab = 32 * 2 * I;        // weight slab bytes
@@ -157,14 +155,14 @@ __global__ __launch_bounds__(256) void glin_dx_kernel(const T* __restrict__ dy, 
   }
 }
 
-template <typename T, int DT, int NT>
+template <typename T, int DT, int NT, int S>
 int launch(const void* dy, const void* w, void* dx, const GdxArgs& a, hipStream_t stream) {
   BandSched sc;
   uint32_t per_xcd = 0;
   const int64_t rows = 64 * NT;
   if (!build_even_sched(a.G, (a.M + rows - 1) / rows, [](int) { return int64_t{1}; }, &sc, &per_xcd))
     return fail(PMSST_EINVAL, "grouped_linear_backward: too many groups or rows for the block schedule");
-  hipLaunchKernelGGL((glin_dx_kernel<T, DT, NT>), dim3(per_xcd * kXcds), dim3(256), 0, stream,
+  hipLaunchKernelGGL((glin_dx_kernel<T, DT, NT, S>), dim3(per_xcd * kXcds), dim3(256), 0, stream,
                      static_cast<const T*>(dy), static_cast<const T*>(w), static_cast<T*>(dx), a, sc);
   return check_launch("glin_dx_kernel");
 }
@@ -185,10 +183,22 @@ int launch_grouped_dx(const void* dy, const void* w, void* dx, int64_t groups, i
                       int64_t out_features, int64_t rows, hipStream_t stream) {
   const GdxArgs a{rows, static_cast<int>(groups), static_cast<int>(out_features), static_cast<int>(in_features)};
   switch (in_features) {
-    case 64: return launch<T, 4, 4>(dy, w, dx, a, stream);
-    case 128: return launch<T, 8, 4>(dy, w, dx, a, stream);
-    case 192: return launch<T, 12, 2>(dy, w, dx, a, stream);
-    case 256: return launch<T, 16, 2>(dy, w, dx, a, stream);
+    case 64: return launch<T, 4, 4, 4>(dy, w, dx, a, stream);
+    case 128: return launch<T, 8, 4, 4>(dy, w, dx, a, stream);
+    case 192: {
+      // 4 waves of 32 rows (4 ring stages) or of 48 rows (3 stages), both two blocks per CU: the form
+      // with fewer block rounds x rows per wave (48 on a tie).  A grid a few blocks past the CUs' slots
+      // pays a whole block time for its last round (configs[1], M = 1032: 558 blocks of 32-row waves
+      // took 43.4 us, 372 of 48-row waves 39.2 us; M = 1024: 496 blocks, 32.0 against 39.2 us).
+      const int64_t slots = 2 * static_cast<int64_t>(num_cus());
+      auto rounds = [&](int64_t block_rows) {
+        const int64_t blocks = groups * ((rows + block_rows - 1) / block_rows);
+        return (blocks + slots - 1) / slots;
+      };
+      if (rounds(192) * 3 <= rounds(128) * 2) return launch<T, 12, 3, 3>(dy, w, dx, a, stream);
+      return launch<T, 12, 2, 4>(dy, w, dx, a, stream);
+    }
+    case 256: return launch<T, 16, 2, 4>(dy, w, dx, a, stream);
     default: return fail(PMSST_EINVAL, "grouped_linear_backward: in_features %lld not supported by glin_dx_kernel",
                          static_cast<long long>(in_features));
   }

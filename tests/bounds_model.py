@@ -675,14 +675,24 @@ def replay_band_split_mixed(widths, M, O, *, x_stride=None):
     yield "band_split_mixed_bwd_gemm", replay_band_split_backward(widths, M, O, 2, grouped=True, even_dx=True)
 
 
-GDX_TILES = {64: (4, 4), 128: (8, 4), 192: (12, 2), 256: (16, 2)}
+GDX_TILES = {64: (4, 4, 4), 128: (8, 4, 4), 192: (12, 2, 4), 256: (16, 2, 4)}  # grouped_dx.hip launch_grouped_dx: DT, NT, stages
+GDX_SLOTS = 2 * 256  # two blocks per CU on the 256 CUs of an MI355X
+
+
+def gdx_tiles(I, G, M):
+    """grouped_dx.hip launch_grouped_dx: (DT, NT, stages); at I = 192 the 48-row form when its block
+    rounds x rows per wave are at most the 32-row form's."""
+    if I != 192:
+        return GDX_TILES[I]
+    rounds = lambda rows: cdiv(G * cdiv(M, rows), GDX_SLOTS)  # noqa: E731
+    return (12, 3, 3) if rounds(192) * 3 <= rounds(128) * 2 else GDX_TILES[192]
 
 
 def _replay_glin_dx(bnd, G, I, O, M):
     """grouped_dx.hip glin_dx_kernel: the DMA ring of weight slabs and dy tiles, the transposed weight
     fragments, the dy B fragments and the dx stores, on the even block schedule."""
-    DT, NT = GDX_TILES[I]
-    S, kUnits, kSlab = 4, I // 8, 32 * 2 * I
+    DT, NT, S = gdx_tiles(I, G, M)
+    kUnits, kSlab = I // 8, 32 * 2 * I
     kInstr = kSlab // 1024
     wave_rows = 16 * NT
     kStage = kSlab + 4 * wave_rows * 64

@@ -85,6 +85,8 @@ def test_mask_mlp_forward_matches_two_kernel_path(hip_ext):
 
 @pytest.mark.parametrize("m,groups,i,o,dtype", [
     (1032, 62, 192, 768, torch.bfloat16),
+    (1100, 62, 192, 768, torch.bfloat16),  # 48-row waves, the last tile's third wave part-filled
+    (1160, 62, 192, 768, torch.float16),   # 48-row waves, an 8-row last tile
     (77, 5, 128, 96, torch.float16),
     (300, 7, 256, 64, torch.bfloat16),
     (1, 3, 192, 768, torch.bfloat16),
@@ -92,7 +94,8 @@ def test_mask_mlp_forward_matches_two_kernel_path(hip_ext):
 ])
 def test_grouped_dx_register_kernel_vs_oracle(hip_ext, m, groups, i, o, dtype):
     """The grouped linear's input gradient on glin_dx_kernel (16-bit, in_features 64-256): full and
-    partial row tiles, a single row, and the mask MLP's configs[1] hidden layer."""
+    partial row tiles, a single row, and the mask MLP's configs[1] hidden layer; at in_features 192
+    both block forms (32-row waves at m = 1, 48-row waves at m >= 1032, chosen by the launcher)."""
     dn = dt_name(dtype)
     print(f"grouped dx m={m} groups={groups} i={i} o={o} {dn}", flush=True)
     g = torch.Generator().manual_seed(41)
