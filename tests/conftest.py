@@ -38,17 +38,34 @@ LOWP_TOL = 2e-2
 LOWP_FLOOR = 2e-2  # absolute floor of the 16-bit bar, as a fraction of the group's rms(ref)
 
 
-# fp32 checks whose bar was scaled above the flat 1e-5 (reference values larger than 1), reported at the
-# end of the session
+# fp32 checks whose bar was scaled above the flat 1e-5 (reference values larger than 1), and the
+# model-level figures the tests report (loss-curve statistics, relative errors), printed at the end
+# of the session
 F32_SCALED: list = []
+REPORTS: list = []
+
+
+def _session_lists(name: str) -> list:
+    """The list ``name`` of this module and of its other instance: pytest imports this file as
+    ``conftest`` while the test modules import ``tests.conftest``."""
+    out, seen = [], set()
+    for mod in (sys.modules.get(__name__), sys.modules.get("conftest"), sys.modules.get("tests.conftest")):
+        lst = getattr(mod, name, None)
+        if lst is not None and id(lst) not in seen:
+            seen.add(id(lst))
+            out += lst
+    return out
 
 
 def pytest_terminal_summary(terminalreporter):
-    if F32_SCALED:
-        worst = sorted(F32_SCALED, key=lambda v: -v[1])[:5]
+    scaled = _session_lists("F32_SCALED")
+    if scaled:
+        worst = sorted(scaled, key=lambda v: -v[1])[:5]
         terminalreporter.write_line(
-            f"fp32 parity bars scaled by max(1, max|ref|): {len(F32_SCALED)} checks, largest scales: "
+            f"fp32 parity bars scaled by max(1, max|ref|): {len(scaled)} checks, largest scales: "
             + ", ".join(f"{w or '?'} x{sc:.3g}" for w, sc in worst))
+    for tag, text in _session_lists("REPORTS"):
+        terminalreporter.write_line(f"[model-parity] {tag}: {text}")
 
 
 def pytest_configure(config):

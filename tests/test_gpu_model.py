@@ -24,6 +24,7 @@ import torch
 from pymsst_amd import direct_compare as dc
 from pymsst_amd import fused_roformer as fr
 from pymsst_amd.workloads import WORKLOADS, TrainWorkload, workload_batch
+from tests.conftest import REPORTS
 
 pytestmark = pytest.mark.gpu
 
@@ -85,6 +86,8 @@ def _loss_and_grads(workload, fused, target, mixture, amp_dtype, ext=None):
 
 
 def _report(tag, text):
+    """Print now (seen with -s) and keep for the session's terminal summary."""
+    REPORTS.append((tag, text))
     sys.stderr.write(f"[model-parity] {tag}: {text}\n")
     sys.stderr.flush()
 
