@@ -133,20 +133,15 @@ __device__ __forceinline__ void mlp_fwd_block(const T* __restrict__ x, const T* 
   for (int i = tid; i < H; i += 64 * WV) sb1[i] = to_f32(b1[static_cast<int64_t>(band) * H + i]);
   __syncthreads();
 
-  // ---- DMA plan.  Instruction k of a chunk: k < 2 DK moves GEMM1 row tile k % 2 of W1 K slice
-  // k / 2 (1 KB: hidden rows mlp_hid_row(k % 2, r), r < 16); the next 2 nv2 move 16-row groups of
-  // the W2 chunk (left rows j0 + 16 q + r, then gate rows I + j0 + 16 q + r; rows past the band
-  // clamped to its last row).  Groups wholly past the band are not moved (their products are never
-  // stored).  Every piece is stored fragment-major: lane l moves row r = l % 16, K unit l / 16 to
-  // byte 16 l of the piece, so the MFMA fragment of the piece (lane l: row l % 16, unit l / 16) is
-  // one contiguous 1 KB read, free of LDS bank conflicts (the 64-byte rows with XOR-swizzled units
-  // took half of the LDS-active cycles in conflicts, this layout a third: 11.1 M -> 5.5 M conflict
-  // cycles per launch at configs[1], 95.9 -> 94.0 us).  Wave w issues k = w, w + WV, ... and, with
-  // kLean, pads its share to kMaxPW with piece k = w again (same source, same LDS bytes).
+  // ---- DMA plan.  Instruction k of a chunk: k < 2 DK moves rows 16 (k % 2) .. + 15 of W1 K slice
+  // k / 2 (1 KB); the next 2 nv2 move 16-row groups of the W2 chunk (left rows j0 + 16 q + r, then
+  // gate rows I + j0 + 16 q + r; rows past the band clamped to its last row).  Groups wholly past
+  // the band are not moved (their products are never stored).  Wave w issues k = w, w + WV, ...
+  // and, with kLean, pads its share to kMaxPW with piece k = w again (same source, same LDS bytes).
   const int nv2 = (I - j0 + 15) / 16 < NV ? (I - j0 + 15) / 16 : NV;
   const int ntot = 2 * DK + 2 * nv2;
   const int npw = kLean ? kMaxPW : (ntot - wave + WV - 1) / WV;
-  const int fu = lane >> 4, fr = lane & 15;  // fragment-major piece: K unit fu of row position fr
+  const int u = (lane & 3) ^ swz_k(lane >> 2);  // logical 16-byte unit this lane moves
   const char* w1b = reinterpret_cast<const char*>(w1 + static_cast<int64_t>(band) * H * D);
   const char* w2b = reinterpret_cast<const char*>(w2 + static_cast<int64_t>(2) * off * H);
   uint32_t gsrc[kMaxPW];
@@ -157,20 +152,20 @@ __device__ __forceinline__ void mlp_fwd_block(const T* __restrict__ x, const T* 
     const int k = wave + WV * q;
     w1k[q] = k < 2 * DK || k >= ntot;
     if (kLean && k >= ntot) {  // padding: piece k = wave (wave < WV <= 2 DK, a W1 piece)
-      const int r = mlp_hid_row(wave & 1, fr);
-      gsrc[q] = static_cast<uint32_t>((r * D + 32 * (wave >> 1) + 8 * fu) * 2);
+      const int r = 16 * (wave & 1) + (lane >> 2);
+      gsrc[q] = static_cast<uint32_t>((r * D + 32 * (wave >> 1) + 8 * u) * 2);
       ldst[q] = static_cast<uint32_t>((wave >> 1) * 2048 + (wave & 1) * 1024);
     } else if (k < 2 * DK) {
-      const int r = mlp_hid_row(k & 1, fr);
-      gsrc[q] = static_cast<uint32_t>((r * D + 32 * (k >> 1) + 8 * fu) * 2);
+      const int r = 16 * (k & 1) + (lane >> 2);
+      gsrc[q] = static_cast<uint32_t>((r * D + 32 * (k >> 1) + 8 * u) * 2);
       ldst[q] = static_cast<uint32_t>((k >> 1) * 2048 + (k & 1) * 1024);
     } else {
       const int k2 = k - 2 * DK;
       const int half = k2 / (nv2 > 0 ? nv2 : 1), grp = k2 - half * nv2;
-      const int jr = j0 + 16 * grp + fr;
+      const int jr = j0 + 16 * grp + (lane >> 2);
       const int jc = jr < I ? jr : I - 1;
       const int prow = half ? I + jc : jc;
-      gsrc[q] = static_cast<uint32_t>((static_cast<int64_t>(prow) * H + 8 * fu) * 2);
+      gsrc[q] = static_cast<uint32_t>((static_cast<int64_t>(prow) * H + 8 * u) * 2);
       ldst[q] = static_cast<uint32_t>(DK * 2048 + (4 * half + grp) * 1024);
     }
   }
@@ -224,8 +219,11 @@ __device__ __forceinline__ void mlp_fwd_block(const T* __restrict__ x, const T* 
   // fragment offsets inside a stage
   uint32_t a1off[2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) a1off[t] = static_cast<uint32_t>(t * 1024 + lane * 16);
-  const uint32_t a2off = static_cast<uint32_t>(DK * 2048 + lane * 16);
+  for (int t = 0; t < 2; ++t) {
+    const int r = mlp_hid_row(t, rr);
+    a1off[t] = static_cast<uint32_t>(r * 64 + 16 * (g ^ swz_k(r & 15)));
+  }
+  const uint32_t a2off = static_cast<uint32_t>(DK * 2048 + rr * 64 + 16 * (g ^ swz_k(rr)));
   // GEMM2 row tiles: left 0 .. NV - 1 and gate NV .. 2 NV - 1 (acc2 index), the stage's W2 groups
   // t and 4 + t; tiles t >= nv2 (NV = 4 with 3 groups) hold stale LDS data and feed accumulators
   // that are never stored

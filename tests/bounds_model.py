@@ -1303,6 +1303,7 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
     tid = np.arange(64 * WV)
     lane = tid & 63
     g, rr = lane >> 4, lane & 15
+    u = (lane & 3) ^ swz_k(lane >> 2)
     nc = H // 32
     for band, mt, pss in sorted({(b, m, p) for b, m, p in decoded if m in (0, mtiles - 1)}):
         off, I = int(offs[band]), int(widths[band])
@@ -1330,18 +1331,18 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
             pad = DK != 8  # kLean
             for q in range(kmax_pw if pad else npw):
                 k = wave + WV * q if q < npw else wave
-                if k < 2 * DK:  # fragment-major pieces: lane l moves row l % 16, K unit l / 16
-                    r = 8 * (rr >> 2) + 4 * (k & 1) + (rr & 3)  # mlp_hid_row(k % 2, l % 16)
-                    gsrc = (r * D + 32 * (k >> 1) + 8 * g) * 2
+                if k < 2 * DK:
+                    r = 16 * (k & 1) + (lane >> 2)
+                    gsrc = (r * D + 32 * (k >> 1) + 8 * u) * 2
                     ldst = (k >> 1) * 2048 + (k & 1) * 1024
                     base, stride, buf = band * H * D * esz, 64 * D, "w1"
                 else:
                     k2 = k - 2 * DK
                     half, grp = k2 // nv2, k2 % nv2
-                    jr = j0 + 16 * grp + rr
+                    jr = j0 + 16 * grp + (lane >> 2)
                     jc = np.minimum(jr, I - 1)
                     prow = I + jc if half else jc
-                    gsrc = (prow * H + 8 * g) * 2
+                    gsrc = (prow * H + 8 * u) * 2
                     ldst = DK * 2048 + (4 * half + grp) * 1024
                     base, stride, buf = 2 * off * H * esz, 64, "w2"
                     if ldst + 1024 > kStage:
@@ -1364,10 +1365,11 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
             for stage in range(S):
                 sb = stage * kStage
                 for t in range(2):
-                    a1 = t * 1024 + lane * 16
+                    r = 8 * (rr >> 2) + 4 * t + (rr & 3)
+                    a1 = r * 64 + 16 * (g ^ swz_k(r & 15))
                     for s_ in range(DK):
                         bnd.touch("lds", sb + a1 + 2048 * s_, 16)
-                a2 = DK * 2048 + lane * 16
+                a2 = DK * 2048 + rr * 64 + 16 * (g ^ swz_k(rr))
                 for t in range(2 * NV):  # the instance's 2 NV GEMM2 row tiles (W2 groups t, 4 + t)
                     bnd.touch("lds", sb + a2 + 1024 * (t if t < NV else 4 + t - NV), 16)
             for c in steps(nc):
