@@ -29,6 +29,7 @@
 #include "gemm.h"
 #include "rowgeom.h"
 #include "grouped_dx.h"
+#include "ring.h"
 
 namespace pmsst {
 namespace {
@@ -832,20 +833,29 @@ __global__ __launch_bounds__(kGemmThreads) void me_bwd_dw_kernel(const T* __rest
 #ifndef PMSST_ME_DW_HT
 #define PMSST_ME_DW_HT 128
 #endif
-constexpr int kDwT = 128;  // j columns per block
+constexpr int kDwT = 128;  // j columns per block (the final layer's dW; the grouped dW may take 192)
+constexpr int64_t kLdsBytes = 160 * 1024;  // LDS per CU (gfx950)
 
-template <typename T, int HT>
+template <typename T, int HT, int JT = kDwT>
 __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict__ dpre, const T* __restrict__ x,
                                                            T* __restrict__ dw, T* __restrict__ dbias, BandSched sc,
                                                            MaskArgs a) {
   constexpr int S = HT == 128 ? PMSST_ME_DW_STAGES : PMSST_ME_DW256_STAGES;
   static_assert(S >= 3 && S <= 8, "stages");
   static_assert(HT == 64 || HT == 128 || HT == 256, "hidden columns per block");
-  constexpr int NW = HT / 32;              // waves: (HT / 64) x 2
-  constexpr int kU = HT / 8;               // 16-byte units per x K-row
-  constexpr int kXTile = kChunkK * HT * 2;  // x tile bytes; the dpre tile (32 K-rows x 128 j) follows
-  constexpr int kStage = kXTile + 8192;
-  constexpr int kDI = 8 / NW;               // dpre DMAs per wave and stage (2 x DMAs each)
+  static_assert(JT == 128 || JT == 192, "j columns per block");
+  constexpr int WJ = JT / 64;               // wave columns (64 j each)
+  constexpr int NW = HT / 64 * WJ;          // waves: (HT / 64) x WJ tiles of 64 x 64
+  constexpr int kU = HT / 8;                // 16-byte units per x K-row
+  constexpr int kJU = JT / 8;               // 16-byte units per dpre K-row
+  constexpr int kXTile = kChunkK * HT * 2;  // x tile bytes; the dpre tile (32 K-rows x JT j) follows
+  constexpr int kStage = kXTile + kChunkK * JT * 2;
+  constexpr int kPX = kXTile / 1024;        // 1 KB DMA pieces of the x tile, then of the dpre tile
+  constexpr int kPT = kPX + kChunkK * JT * 2 / 1024;
+  constexpr int kMaxPW = (kPT + NW - 1) / NW;  // pieces per wave and stage, at most
+  // both tiles' pieces split evenly over the waves: each wave's first kPX / NW pieces are x pieces
+  // and its count is kMaxPW, both known at compile time
+  constexpr bool kEven = kPX % NW == 0 && (kPT - kPX) % NW == 0;
   __shared__ __attribute__((aligned(1024))) char lds[S * kStage];
   int band;
   uint32_t mt0, sub, per_unit;
@@ -853,7 +863,7 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
   const int H = a.H;
   const int htiles = H / HT;
   const int h0 = static_cast<int>(sub % htiles) * HT;
-  const int j0 = static_cast<int>(sub / htiles) * kDwT;
+  const int j0 = static_cast<int>(sub / htiles) * JT;
   const int off = a.uniform_I > 0 ? band * a.uniform_I : static_cast<int>(a.offsets[band]);
   const int I = a.uniform_I > 0 ? a.uniform_I : static_cast<int>(a.offsets[band + 1]) - off;
   const int K2 = 2 * I;
@@ -862,31 +872,34 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
   const int64_t xstride = static_cast<int64_t>(a.NB) * H;  // elements between rows m of x
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int wr = wave >> 1, wc = wave & 1;  // hidden columns 64 wr .., j columns 64 wc ..
+  const int wr = wave / WJ, wc = wave % WJ;  // hidden columns 64 wr .., j columns 64 wc ..
   const int nk = (M + kChunkK - 1) / kChunkK;
   const int kbeg = M - nk * kChunkK;
 
-  // DMA pieces.  x instruction t (of 2) of wave w is q = w + NW t: K-rows (64 / kU) q + lane / kU,
-  // unit lane % kU of the row (logical unit ^ swz_mn).  dpre instruction t (of kDI) is q = w + NW t:
-  // K-rows 4 q + lane / 16, unit lane % 16 (columns past 2 I clamped to the band's last 8).
-  uint32_t aoff[2], aoff0[2], boff[kDI], boff0[kDI];
-  bool aok0[2], bok0[kDI];
+  // DMA pieces: piece k < kPX moves flattened units 64 k + lane of the x tile (K-row U / kU,
+  // physical unit U % kU <- logical unit (U % kU) ^ swz_mn(K-row)); piece k >= kPX the same of the
+  // dpre tile with kJU units per K-row (columns past 2 I clamped to the band's last 8).  Wave w
+  // issues pieces w, w + NW, ... < kPT.
+  const int npw = kEven ? kMaxPW : (kPT - wave + NW - 1) / NW;
+  uint32_t goff[kMaxPW], goff0[kMaxPW];
+  bool ok0[kMaxPW], isx[kMaxPW];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int kr = (64 / kU) * (wave + NW * t) + lane / kU;
-    const int u = (lane % kU) ^ swz_mn(kr);
-    aoff[t] = static_cast<uint32_t>((kr * xstride + 8 * u) * 2);
-    aok0[t] = kbeg + kr >= 0;
-    aoff0[t] = aok0[t] ? aoff[t] : static_cast<uint32_t>((-kbeg * xstride + 8 * u) * 2);  // row m = 0
-  }
-#pragma unroll
-  for (int t = 0; t < kDI; ++t) {
-    const int kr = 4 * (wave + NW * t) + (lane >> 4);
-    const int u = (lane & 15) ^ swz_mn(kr);
-    const int jc = j0 + 8 * u < K2 ? j0 + 8 * u : K2 - 8;
-    boff[t] = static_cast<uint32_t>((kr * pitch2 + jc) * 2);
-    bok0[t] = kbeg + kr >= 0;
-    boff0[t] = bok0[t] ? boff[t] : static_cast<uint32_t>((-kbeg * pitch2 + jc) * 2);
+  for (int t = 0; t < kMaxPW; ++t) {
+    const int k = wave + NW * t;
+    isx[t] = kEven ? t < kPX / NW : k < kPX;
+    const int units = isx[t] ? kU : kJU;
+    const int U = 64 * (isx[t] ? k : k - kPX) + lane;
+    const int kr = U / units;
+    const int u = (U % units) ^ swz_mn(kr);
+    ok0[t] = kbeg + kr >= 0;
+    if (isx[t]) {
+      goff[t] = static_cast<uint32_t>((kr * xstride + 8 * u) * 2);
+      goff0[t] = ok0[t] ? goff[t] : static_cast<uint32_t>((-kbeg * xstride + 8 * u) * 2);  // row m = 0
+    } else {
+      const int jc = j0 + 8 * u < K2 ? j0 + 8 * u : K2 - 8;
+      goff[t] = static_cast<uint32_t>((kr * pitch2 + jc) * 2);
+      goff0[t] = ok0[t] ? goff[t] : static_cast<uint32_t>((-kbeg * pitch2 + jc) * 2);
+    }
   }
   const char* xsrc0 = reinterpret_cast<const char*>(x + (static_cast<int64_t>(kbeg) * a.NB + band) * H + h0);
   const char* dsrc0 = reinterpret_cast<const char*>(dpre + static_cast<int64_t>(kbeg) * pitch2 + 2 * off);
@@ -897,10 +910,8 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
     const char* ds = dsrc0 + static_cast<int64_t>(kc) * kChunkK * pitch2 * 2;
     char* st = lds + stage * kStage;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) dma_lds16(xs + (kc == 0 ? aoff0[t] : aoff[t]), st + (wave + NW * t) * 1024);
-#pragma unroll
-    for (int t = 0; t < kDI; ++t)
-      dma_lds16(ds + (kc == 0 ? boff0[t] : boff[t]), st + kXTile + (wave + NW * t) * 1024);
+    for (int t = 0; t < kMaxPW; ++t)
+      if (t < npw) dma_lds16((isx[t] ? xs : ds) + (kc == 0 ? goff0[t] : goff[t]), st + (wave + NW * t) * 1024);
   };
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
@@ -910,14 +921,14 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     fa[i] = frag_mn_addr(lds0, 64 * wr + 16 * i, 2 * HT, lane);
-    fb[i] = frag_mn_addr(lds0 + kXTile, 64 * wc + 16 * i, 2 * kDwT, lane);
+    fb[i] = frag_mn_addr(lds0 + kXTile, 64 * wc + 16 * i, 2 * JT, lane);
   }
   f32x4_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // dbias = ones^T dpre: the two waves of the first hidden tile's first 64 columns also multiply
+  // dbias = ones^T dpre: the waves of the first hidden tile's first 64 columns also multiply
   // their dpre fragments by an all-ones A fragment (every row of the product is the column sum)
   const bool do_bias = h0 == 0 && wr == 0 && dbias != nullptr;
   const uint32_t one2 = std::is_same<T, bf16>::value ? 0x3F803F80u : 0x3C003C00u;
@@ -927,26 +938,27 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
   for (int j = 0; j < 4; ++j) accb[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int s = 0; s < nk; ++s) {
-    // chunk s landed once at most (2 + kDI) nd DMAs are outstanding, nd = chunks issued after it
+    // chunk s landed once at most npw nd DMAs are outstanding, nd = chunks issued after it
     const int nd = nk - 1 - s < S - 2 ? nk - 1 - s : S - 2;
-    static_assert(S - 2 <= 6, "wait table");
-    switch (nd) {
-      case 0: vm_wait<0>(); break;
-      case 1: vm_wait<2 + kDI>(); break;
-      case 2: vm_wait<2 * (2 + kDI)>(); break;
-      case 3: vm_wait<3 * (2 + kDI)>(); break;
-      case 4: vm_wait<4 * (2 + kDI)>(); break;
-      case 5: vm_wait<5 * (2 + kDI)>(); break;
-      default: vm_wait<6 * (2 + kDI)>(); break;
+    if constexpr (kEven) {
+      static_assert(S - 2 <= 6, "wait table");
+      switch (nd) {
+        case 0: vm_wait<0>(); break;
+        case 1: vm_wait<kMaxPW>(); break;
+        case 2: vm_wait<2 * kMaxPW>(); break;
+        case 3: vm_wait<3 * kMaxPW>(); break;
+        case 4: vm_wait<4 * kMaxPW>(); break;
+        case 5: vm_wait<5 * kMaxPW>(); break;
+        default: vm_wait<6 * kMaxPW>(); break;
+      }
+    } else {
+      ring_vm_wait<(S - 2) * kMaxPW>(nd * npw);
     }
     if (s == 0 && kbeg < 0) {  // zero this wave's own pieces of chunk 0 that lie before row 0
       const u32x4_t z{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-        if (!aok0[t]) *reinterpret_cast<u32x4_t*>(lds + (wave + NW * t) * 1024 + lane * 16) = z;
-#pragma unroll
-      for (int t = 0; t < kDI; ++t)
-        if (!bok0[t]) *reinterpret_cast<u32x4_t*>(lds + kXTile + (wave + NW * t) * 1024 + lane * 16) = z;
+      for (int t = 0; t < kMaxPW; ++t)
+        if (t < npw && !ok0[t]) *reinterpret_cast<u32x4_t*>(lds + (wave + NW * t) * 1024 + lane * 16) = z;
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     __builtin_amdgcn_s_barrier();
@@ -957,7 +969,7 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
 #pragma unroll
     for (int i = 0; i < 4; ++i) af[i] = lds_read_tr_pair(fa[i] + so, 4 * 2 * HT);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bfr[j] = lds_read_tr_pair(fb[j] + so, 4 * 2 * kDwT);
+    for (int j = 0; j < 4; ++j) bfr[j] = lds_read_tr_pair(fb[j] + so, 4 * 2 * JT);
     lds_wait(af, bfr);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -969,7 +981,7 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
     }
   }
 
-  const int jv = K2 - j0 < kDwT ? K2 - j0 : kDwT;
+  const int jv = K2 - j0 < JT ? K2 - j0 : JT;
   if (do_bias && lane < 16) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -979,10 +991,10 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
   }
 
   // epilogue through LDS: lane holds h = 64 wr + 16 i + 4 (lane / 16) + r of columns
-  // j = 64 wc + 16 jj + lane % 16; staged as [128 j][HT h] (row pitch 2 HT + 16 bytes)
+  // j = 64 wc + 16 jj + lane % 16; staged as [JT j][HT h] (row pitch 2 HT + 16 bytes)
   __syncthreads();  // every wave is done with the ring (its last wait was vmcnt(0))
   constexpr int kOP = HT + 8;
-  static_assert(kDwT * kOP * 2 <= S * kStage, "staging tile");
+  static_assert(JT * kOP * 2 <= S * kStage, "staging tile");
   T* ot = reinterpret_cast<T*>(lds);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -995,10 +1007,12 @@ __global__ __launch_bounds__(512) void me_bwd_dw_dma_kernel(const T* __restrict_
   }
   __syncthreads();
   T* dwb = dw + (static_cast<int64_t>(2) * off + j0) * H + h0;  // rows j of dW_b
+  constexpr int kRowsPerPass = 64 * NW / kU;  // rows j written per pass, kU threads each
+  static_assert(64 * NW % kU == 0 && JT % kRowsPerPass == 0, "write-out passes");
   const int c8 = static_cast<int>(threadIdx.x % kU) * 8;
 #pragma unroll
-  for (int p = 0; p < kDwT / 16; ++p) {
-    const int jj = static_cast<int>(threadIdx.x / kU) + 16 * p;
+  for (int p = 0; p < JT / kRowsPerPass; ++p) {
+    const int jj = static_cast<int>(threadIdx.x / kU) + kRowsPerPass * p;
     if (jj < jv)
       *reinterpret_cast<u32x4_t*>(dwb + static_cast<int64_t>(jj) * H + c8) =
           *reinterpret_cast<const u32x4_t*>(ot + jj * kOP + c8);
@@ -1240,12 +1254,27 @@ int launch_uniform_dw_impl(const void* dy, const void* x, void* dw, void* db, in
   BandSched wsc;
   uint32_t per_xcd = 0;
   const int64_t htl = in_features / 64;
+  // j tile: 192 columns (3 waves, 48 KB of ring: three blocks per CU) when that takes fewer rounds
+  // of resident blocks than 128 (2 waves, 36 KB: four per CU); each x tile is then re-read for 4
+  // instead of 6 column tiles at out_features 768
+  auto rounds = [&](int64_t jt, int64_t ring_bytes) {
+    const int64_t blocks = groups * htl * ((out_features + jt - 1) / jt);
+    const int64_t slots = static_cast<int64_t>(num_cus()) * (kLdsBytes / ring_bytes);
+    return (blocks + slots - 1) / slots;
+  };
+  const int64_t ring128 = 3 * kChunkK * 2 * (64 + 128), ring192 = 3 * kChunkK * 2 * (64 + 192);
+  const int jt = rounds(192, ring192) < rounds(128, ring128) ? 192 : 128;
   if (!build_band_sched(static_cast<int>(groups), 1,
-                        [&](int) { return htl * ((out_features + kDwT - 1) / kDwT); }, &wsc, &per_xcd))
+                        [&](int) { return htl * ((out_features + jt - 1) / jt); }, &wsc, &per_xcd))
     return fail(PMSST_EINVAL, "grouped_linear_backward: too many groups for the dW schedule");
-  hipLaunchKernelGGL((me_bwd_dw_dma_kernel<T, 64>), dim3(per_xcd * kXcds), dim3(128), 0, stream,
-                     static_cast<const T*>(dy), static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(db),
-                     wsc, a);
+  if (jt == 192)
+    hipLaunchKernelGGL((me_bwd_dw_dma_kernel<T, 64, 192>), dim3(per_xcd * kXcds), dim3(192), 0, stream,
+                       static_cast<const T*>(dy), static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(db),
+                       wsc, a);
+  else
+    hipLaunchKernelGGL((me_bwd_dw_dma_kernel<T, 64>), dim3(per_xcd * kXcds), dim3(128), 0, stream,
+                       static_cast<const T*>(dy), static_cast<const T*>(x), static_cast<T*>(dw), static_cast<T*>(db),
+                       wsc, a);
   return check_launch("me_bwd_dw_dma_kernel");
 }
 

@@ -527,7 +527,7 @@ def replay_band_split_backward(widths, M, O, esz, *, has_bias=True, grouped=Fals
         _replay_bs_dw_dma(bnd, widths, offs, M, O, esz, has_bias)
     elif uniform_dw:  # the mask-estimator DMA dW kernel with HT = 64 on bands of width 2 I_b = O
         _replay_me_dw_dma(bnd, [O // 2] * nb, _offs([O // 2] * nb), M, widths[0], esz, 64, "dy", "x", "dw",
-                          "db" if has_bias else None, "lds_dw")
+                          "db" if has_bias else None, "lds_dw", JT=dw_jt(nb, widths[0], O))
     else:
         _replay_bs_dw_reg(bnd, widths, offs, M, O, esz, has_bias, norm, vec4 and ovec4)
     if norm:
@@ -985,24 +985,44 @@ def replay_mask_final_forward(widths, M, H, esz):
     return bnd
 
 
-def _replay_me_dw_dma(bnd, widths, offs, M, H, esz, HT, dpre_buf, x_buf, dw_buf, db_buf, lds_buf):
-    """mask_estimator.hip me_bwd_dw_dma_kernel<T, HT> (HT hidden columns x 128 j per block, HT / 32
-    waves) on its band schedule, over a dpre-like buffer of row pitch 2 F."""
+DW_CUS = 256        # CUs of the device the dW tile choice is replayed for
+LDS_PER_CU = 160 * 1024
+
+
+def dw_jt(groups, in_features, out_features):
+    """mask_estimator.hip launch_uniform_dw_impl: the j tile (192 when it takes fewer rounds of
+    resident blocks than 128, with rings of 3 stages of 32 K-rows x (64 + JT) columns)."""
+    htl = in_features // 64
+
+    def rounds(jt):
+        ring = 3 * CHUNK_K * 2 * (64 + jt)
+        return cdiv(groups * htl * cdiv(out_features, jt), DW_CUS * (LDS_PER_CU // ring))
+
+    return 192 if rounds(192) < rounds(128) else 128
+
+
+def _replay_me_dw_dma(bnd, widths, offs, M, H, esz, HT, dpre_buf, x_buf, dw_buf, db_buf, lds_buf, JT=128):
+    """mask_estimator.hip me_bwd_dw_dma_kernel<T, HT, JT> (HT hidden columns x JT j per block,
+    (HT / 64) x (JT / 64) waves, the x and dpre tiles moved as one list of 1 KB pieces dealt to the
+    waves in turn) on its band schedule, over a dpre-like buffer of row pitch 2 F."""
     nb, F = len(widths), int(sum(widths))
-    kDwT, S2 = 128, 3
-    NW2 = HT // 32
-    kU2 = HT // 8
+    S2 = 3
+    WJ = JT // 64
+    NW2 = HT // 64 * WJ
+    kU2, kJU = HT // 8, JT // 8
     kXTile = CHUNK_K * HT * 2
-    kStage2 = kXTile + 8192
-    kDI2 = 8 // NW2
+    kStage2 = kXTile + CHUNK_K * JT * 2
+    PX = kXTile // 1024
+    PT = PX + CHUNK_K * JT * 2 // 1024
+    kMaxPW = cdiv(PT, NW2)
     bnd.sizes[lds_buf] = max(bnd.sizes.get(lds_buf, 0), S2 * kStage2)
     htl = H // HT
-    units2 = lambda b: htl * cdiv(2 * widths[b], kDwT)  # noqa: E731
+    units2 = lambda b: htl * cdiv(2 * widths[b], JT)  # noqa: E731
     sc2 = build_band_sched(nb, 1, units2)
     decoded2 = sched_decode(sc2, nb, units2, False, bnd, "me_bwd_dw_dma")
     tid = np.arange(NW2 * 64)
     lane, wave = tid & 63, tid >> 6
-    wr, wc = wave >> 1, wave & 1
+    wr, wc = wave // WJ, wave % WJ
     nk = cdiv(M, CHUNK_K)
     kbeg = M - nk * CHUNK_K
     xstride = nb * H
@@ -1010,45 +1030,45 @@ def _replay_me_dw_dma(bnd, widths, offs, M, H, esz, HT, dpre_buf, x_buf, dw_buf,
         off, I = int(offs[band]), int(widths[band])
         K2 = 2 * I
         h0 = (sub % htl) * HT
-        j0 = (sub // htl) * kDwT
+        j0 = (sub // htl) * JT
         for c in steps(nk):
             st = (c % S2) * kStage2
-            for t in range(2):
-                kr = (64 // kU2) * (wave + NW2 * t) + lane // kU2
-                uu = (lane % kU2) ^ swz_mn(kr)
+            for t in range(kMaxPW):
+                k = wave + NW2 * t
+                valid = k < PT
+                isx = k < PX
+                units = np.where(isx, kU2, kJU)
+                U = 64 * np.where(isx, k, k - PX) + lane
+                kr = U // units
+                uu = (U % units) ^ swz_mn(kr)
                 row = kbeg + c * CHUNK_K + kr
                 row = np.where((c == 0) & (row < 0), 0, row)
-                bnd.touch(x_buf, (row * xstride + band * H + h0 + 8 * uu) * esz, 16)
-                bnd.touch(lds_buf, st + (wave + NW2 * t) * 1024 + 16 * lane, 16)
-            for t in range(kDI2):
-                kr = 4 * (wave + NW2 * t) + (lane >> 4)
-                uu = (lane & 15) ^ swz_mn(kr)
+                bnd.touch(x_buf, (row * xstride + band * H + h0 + 8 * uu) * esz, 16, valid & isx)
                 jc = np.minimum(j0 + 8 * uu, K2 - 8)
-                row = kbeg + c * CHUNK_K + kr
-                row = np.where((c == 0) & (row < 0), 0, row)
-                bnd.touch(dpre_buf, (row * 2 * F + 2 * off + jc) * esz, 16)
-                bnd.touch(lds_buf, st + kXTile + (wave + NW2 * t) * 1024 + 16 * lane, 16)
+                bnd.touch(dpre_buf, (row * 2 * F + 2 * off + jc) * esz, 16, valid & ~isx)
+                bnd.touch(lds_buf, st + k * 1024 + 16 * lane, 16, valid)
             for i in range(4):
                 fa = frag_mn_addr(0, 64 * wr + 16 * i, 2 * HT, lane) + st
-                fb = frag_mn_addr(kXTile, 64 * wc + 16 * i, 2 * kDwT, lane) + st
-                for a_, p in ((fa, 2 * HT), (fb, 2 * kDwT)):
+                fb = frag_mn_addr(kXTile, 64 * wc + 16 * i, 2 * JT, lane) + st
+                for a_, p in ((fa, 2 * HT), (fb, 2 * JT)):
                     bnd.touch(lds_buf, a_, 8)
                     bnd.touch(lds_buf, a_ + 4 * p, 8)
-        jv = min(K2 - j0, kDwT)
+        jv = min(K2 - j0, JT)
         if db_buf is not None:
             for j in range(4):
                 jj = 64 * wc + 16 * j + lane
                 bnd.touch(db_buf, (2 * off + j0 + jj) * esz, esz, (h0 == 0) & (wr == 0) & (lane < 16) & (jj < jv))
         kop = HT + 8
-        if kDwT * kop * 2 > S2 * kStage2:
+        if JT * kop * 2 > S2 * kStage2:
             bnd.fail("me_bwd_dw_dma: staging tile larger than the ring")
         for j in range(4):
             jj = 64 * wc + 16 * j + (lane & 15)
             for i in range(4):
                 bnd.touch(lds_buf, (jj * kop + 64 * wr + 16 * i + 4 * (lane >> 4)) * esz, 4 * esz)
+        rows_per_pass = 64 * NW2 // kU2
         c8 = (tid % kU2) * 8
-        for p in range(kDwT // 16):
-            jj = tid // kU2 + 16 * p
+        for p in range(JT // rows_per_pass):
+            jj = tid // kU2 + rows_per_pass * p
             ok = jj < jv
             bnd.touch(lds_buf, (jj * kop + c8) * esz, 16, ok)
             bnd.touch(dw_buf, ((2 * off + j0 + jj) * H + h0 + c8) * esz, 16, ok)
