@@ -12,7 +12,7 @@
 // fragments); K values past 2 I_b are zeroed in the B fragments (I_b is a multiple of 4, so whole
 // 8-value units are in or out), the weight rows past it are clamped reads multiplied by those
 // zeros.  The accumulators stay in registers over the whole K; the epilogue stages the tile in LDS
-// and streams dz out along whole rows, with x read along whole rows before the K loop.  Blocks of wide bands (long K) are dispatched first.
+// and streams x in and dz out along whole rows.  Blocks of wide bands (long K) are dispatched first.
 #include "common.h"
 #include "dma_gemm.h"
 #include "grouped_dx.h"
@@ -30,7 +30,7 @@ struct DzArgs {
 };
 
 template <typename T, int DT, int NT, bool TANH>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void me_dz_kernel(const T* __restrict__ dpre, const T* __restrict__ w,
+__global__ __launch_bounds__(256) void me_dz_kernel(const T* __restrict__ dpre, const T* __restrict__ w,
                                                     const T* __restrict__ xin, T* __restrict__ dz, DzArgs a,
                                                     BandSched sc) {
   constexpr int S = kDzStages;
@@ -102,27 +102,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
   for (int c = 0; c < S - 1; ++c)
     if (c < nc) dma(c, c);
 
-  // the epilogue's x units (whole rows of the tile, 16 bytes per thread and unit), loaded right after
-  // the ring's first chunks: they land while the K loop runs, so a block of a narrow band (one or two
-  // chunks) waits for one memory round trip instead of two
-  const int64_t m0 = static_cast<int64_t>(mt) * (4 * kWaveRows);
-  constexpr int kRowUnits = HT / 8;
-  constexpr int kUnitsPerThread = 4 * kWaveRows * kRowUnits / 256;
-  static_assert(4 * kWaveRows * kRowUnits % 256 == 0, "units per thread");
-  constexpr int kXLoads = TANH ? kUnitsPerThread : 0;
-  const int tid = threadIdx.x;
-  uint4 xin_u[kUnitsPerThread];
-  if constexpr (TANH) {
-#pragma unroll
-    for (int k = 0; k < kUnitsPerThread; ++k) {
-      const int q = tid + 256 * k;
-      const int r = q / kRowUnits, u = q % kRowUnits;
-      int64_t m = m0 + r;
-      m = m < a.M ? m : a.M - 1;
-      xin_u[k] = *reinterpret_cast<const uint4*>(xin + (m * a.NB + band) * H + h0 + 8 * u);
-    }
-  }
-
   f32x4_t acc[DT][NT];
 #pragma unroll
   for (int d = 0; d < DT; ++d)
@@ -140,12 +119,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
   const uint32_t boff = static_cast<uint32_t>(kSlab + wave * NT * 1024 + rr * 64 + 16 * (gq ^ swz_k(rr)));
 
   const int per_chunk = npw + nvt;
-  // chunk c landed once at most (chunks issued after it) x per_chunk DMAs are outstanding, plus the
-  // x loads for the chunks issued before them (c < S - 1); only chunks < nc are moved (short bands
-  // have fewer than S - 1)
+  // chunk c landed once at most (chunks issued after it) x per_chunk DMAs are outstanding; only
+  // chunks < nc are moved (short bands have fewer than S - 1)
   auto ring_step = [&](int c) {
     const int after = nc - 1 - c < S - 2 ? nc - 1 - c : S - 2;
-    ring_vm_wait<(S - 2) * (kMaxPW + NT) + kXLoads>(after * per_chunk + (c < S - 1 ? kXLoads : 0));
+    ring_vm_wait<(S - 2) * (kMaxPW + NT)>(after * per_chunk);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -193,6 +171,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     }
   }
   __syncthreads();
+  const int64_t m0 = static_cast<int64_t>(mt) * (4 * kWaveRows);
+  constexpr int kRowUnits = HT / 8;
+  constexpr int kUnitsPerThread = 4 * kWaveRows * kRowUnits / 256;
+  static_assert(4 * kWaveRows * kRowUnits % 256 == 0, "units per thread");
+  const int tid = threadIdx.x;
+  uint4 xin_u[kUnitsPerThread];
+  if constexpr (TANH) {
+#pragma unroll
+    for (int k = 0; k < kUnitsPerThread; ++k) {
+      const int q = tid + 256 * k;
+      const int r = q / kRowUnits, u = q % kRowUnits;
+      int64_t m = m0 + r;
+      m = m < a.M ? m : a.M - 1;
+      xin_u[k] = *reinterpret_cast<const uint4*>(xin + (m * a.NB + band) * H + h0 + 8 * u);
+    }
+  }
 #pragma unroll
   for (int k = 0; k < kUnitsPerThread; ++k) {
     const int q = tid + 256 * k;
