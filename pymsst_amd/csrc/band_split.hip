@@ -614,7 +614,9 @@ __global__ __launch_bounds__(kGemmThreads) void bs_bwd_dw_kernel(const T* __rest
 // multiply their dy fragments by an all-ones A fragment (every row of that product is the
 // column sum).  The tile leaves through LDS as rows o of dW_b.
 constexpr int kBdT = 64;
-constexpr int kBdWinRows = 2048;
+// 1024 rows (4 KB) keep the kernel at 52 KB of LDS, three blocks per CU, so the dx finish and
+// dgamma tail blocks run beside the dW blocks' row loops (2048 rows: 56 KB, two per CU)
+constexpr int kBdWinRows = 1024;
 #ifndef PMSST_BS_DW_DMA
 #define PMSST_BS_DW_DMA 1
 #endif
