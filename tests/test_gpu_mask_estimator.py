@@ -127,10 +127,13 @@ def test_empty_rows(hip_ext):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(129, 62, 192, 768), (37, 3, 6, 10), (130, 62, 64, 256), (65, 4, 512, 2048)])
+@pytest.mark.parametrize("shape", [(129, 62, 192, 768), (37, 3, 6, 10), (130, 62, 64, 256), (65, 4, 512, 2048),
+                                   (100, 100, 192, 776)])
 def test_grouped_linear_tanh_forward_and_backward(hip_ext, dtype, shape):
     """Mask-MLP hidden layer: grouped linear with the tanh epilogue, and the grouped-linear backward
-    (dx, dW, db) against the oracle; odd widths (6 -> 10) take the unaligned paths."""
+    (dx, dW, db) against the oracle; odd widths (6 -> 10) take the unaligned paths.  At 100 groups of
+    192 -> 776 the 16-bit dW takes 192 output columns per block (fewer rounds of resident blocks than
+    128) with a last column tile of 8."""
     dn = dt_name(dtype)
     m, groups, i, o = shape
     g = torch.Generator().manual_seed(21)

@@ -89,3 +89,12 @@ def test_mixed_band_split_replay_covers_its_buffers_and_flags_mistakes(monkeypat
     monkeypatch.setattr(bm.np, "searchsorted", lambda a, v, side="left": real(a, v, side=side) + 1)
     v = dict(bm.replay_band_split_mixed(bm.BSR_WIDTHS, 1032, 192))["band_split_mixed_fwd_norm"].violations()
     assert v
+
+
+def test_grouped_dw_192_column_tiles_stay_in_bounds():
+    """The grouped-linear dW on 192 output columns per block (chosen when it takes fewer rounds of
+    resident blocks), with a partly filled last column tile (776 = 4 x 192 + 8)."""
+    assert bm.dw_jt(100, 192, 776) == 192 and bm.dw_jt(62, 192, 768) == 192 and bm.dw_jt(62, 512, 2048) == 128
+    b = bm.replay_band_split_backward([192] * 100, 100, 776, 2, grouped=True)
+    assert b.sizes["lds_dw"] == 3 * 32 * 2 * (64 + 192)
+    assert not b.violations()
