@@ -158,3 +158,91 @@ def test_mask_mlp_and_band_split_write_inside_their_outputs(hip_ext, guarded, dt
     assert not guarded.damaged(), "mask_estimator_final_backward_packed"
     hip_ext.grouped_linear_backward(dz, hx, w1, has_bias=True)
     assert not guarded.damaged(), "grouped_linear_backward"
+
+
+def _rotary_tables(n, d, dtype):
+    import oracle
+
+    c, s = oracle.rotary_tables(n, d)
+    c = torch.from_numpy(c).to(dtype).cuda().repeat_interleave(2, dim=-1).reshape(1, n, 1, d)[..., ::2]
+    s = torch.from_numpy(s).to(dtype).cuda().repeat_interleave(2, dim=-1).reshape(1, n, 1, d)[..., ::2]
+    return c, s
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_train_path_ops_write_inside_their_outputs(hip_ext, guarded, dtype):
+    """The other ops of the patched training step: RMSNorm (aligned and guarded-scalar widths),
+    rotary on q/k views and the fused qkv split, the attention gate in both layouts, the mask
+    application, the mixed-precision band split of an fp32 input and the mel band gather/scatter."""
+    import numpy as np
+
+    from pymsst_amd.core.mel_band_roformer import mel_band_bins
+
+    g = torch.Generator().manual_seed(5)
+
+    def rnd(*shape, dt=dtype):
+        return torch.randn(*shape, generator=g).to(dt).cuda()
+
+    for rows, dim in ((257, 192), (65, 100), (33, 6)):
+        print(f"[guard] rms_norm {rows}x{dim}", flush=True)
+        x, gamma, dy = rnd(rows, dim), 1 + 0.1 * rnd(dim), rnd(rows, dim)
+        out, normed, inv = hip_ext.rms_norm_forward(x, gamma)
+        hip_ext.rms_norm_backward(dy, normed, inv, gamma)
+        hip_ext.rms_norm_backward_from_input(dy, x, inv, gamma)
+        assert not guarded.damaged(), f"rms_norm {rows}x{dim}"
+
+    b, n, h, d = 2, 62, 8, 64
+    print("[guard] rotary", flush=True)
+    qkv = rnd(b, n, 3 * h * d)
+    cos, sin = _rotary_tables(n, d, dtype)
+    q, k, _ = qkv.view(b, n, 3, h, d).unbind(dim=2)
+    for t in (q, k):
+        for layout in ("bnhd", "bhnd"):
+            hip_ext.rotary_forward(t, cos, sin, out_layout=layout)
+    hip_ext.rotary_backward(rnd(b, n, h, d), cos, sin)
+    hip_ext.rotary_qkv_forward(qkv, h, cos, sin)
+    gq, gk, gv = (rnd(b, h, n, d).transpose(1, 2) for _ in range(3))
+    hip_ext.rotary_qkv_backward(gq, gk, gv, cos, sin)
+    assert not guarded.damaged(), "rotary"
+
+    print("[guard] attention gate", flush=True)
+    m, dm = b * n, 192
+    attn, xg, wg, bg, gout = rnd(m, h, d), rnd(m, dm), rnd(h, dm) / dm**0.5, 0.5 * rnd(h), rnd(m, h * d)
+    _, gate, sa, sx = hip_ext.attention_gate_forward(attn, xg, wg, bg)
+    hip_ext.attention_gate_backward(gout, sa, sx, wg, gate)
+    attn_t = rnd(b, h, n, d).transpose(1, 2)
+    _, gate, sa, sx = hip_ext.attention_gate_forward_bnhd(attn_t, xg, wg, bg)
+    hip_ext.attention_gate_backward_bnhd(gout, sa, sx, wg, gate)
+    hip_ext.attention_gate_backward_bnhd(gout, sa, sx, wg, gate, out_layout="bnhd")
+    assert not guarded.damaged(), "attention gate"
+
+    print("[guard] mask apply", flush=True)
+    bs, s, c, f, t = 2, 3, 2, 33, 70
+    spec = torch.complex(torch.randn(bs, f * c, t, generator=g), torch.randn(bs, f * c, t, generator=g)).cuda()
+    mask = rnd(bs, s, t, 2 * f * c)
+    est = hip_ext.mask_apply_forward(spec, mask, c, True)
+    hip_ext.mask_apply_backward(torch.randn_like(est), spec, mask, c, True, need_spec_grad=True)
+    assert not guarded.damaged(), "mask apply"
+
+    print("[guard] band split mixed", flush=True)
+    dims = bench.BSR_WIDTHS
+    fb, ob = sum(dims), 192
+    xb = torch.randn(130, fb, generator=g).cuda()
+    gb = (1 + 0.1 * torch.randn(fb, generator=g)).cuda()
+    pdt = dtype if dtype != torch.float32 else torch.bfloat16  # the projection runs in 16-bit only
+    wb = torch.cat([(torch.randn(ob, i, generator=g) / i**0.5).reshape(-1) for i in dims]).to(pdt).cuda()
+    bb = (0.1 * torch.randn(len(dims) * ob, generator=g)).to(pdt).cuda()
+    out, feats, inv = hip_ext.band_split_mixed_forward(xb, gb, wb, bb, dims, pdt)
+    hip_ext.band_split_mixed_backward(torch.randn_like(out), xb, feats, inv, gb, wb, dims, True)
+    assert not guarded.damaged(), "band split mixed"
+
+    print("[guard] mel band rows", flush=True)
+    bins = mel_band_bins(44100, 2048, 60)
+    rows = np.concatenate([(bb_[:, None] * 2 + np.arange(2)[None, :]).reshape(-1) for bb_ in bins])
+    plan = hip_ext.band_rows_plan(rows, 1025 * 2, "cuda")
+    xr = torch.randn(2, 1025 * 2, 65, 2, generator=g).cuda()
+    yr = hip_ext.band_rows_gather(xr, plan, out_dtype=dtype)
+    hip_ext.band_rows_scatter(yr.float(), plan)
+    hip_ext.band_rows_scatter(yr.float(), plan, mean=True)
+    assert not guarded.damaged(), "mel band rows"
