@@ -207,7 +207,10 @@ __global__ __launch_bounds__(256) void me_dz_kernel(const T* __restrict__ dpre, 
       for (int e = 0; e < 8; ++e) pk.v[e] = from_f32<T>(o[e]);
       v = __builtin_bit_cast(uint4, pk);
     }
-    *reinterpret_cast<uint4*>(dz + ((m0 + r) * a.NB + band) * H + h0 + 8 * u) = v;
+    // non-temporal: dz (M x NB x H, far larger than the L2s) would otherwise displace the weight slabs,
+    // dpre rows and x lines this kernel is still reading; the stores are whole 16-byte units along rows
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v),
+                                reinterpret_cast<u32x4_t*>(dz + ((m0 + r) * a.NB + band) * H + h0 + 8 * u));
   }
 }
 
