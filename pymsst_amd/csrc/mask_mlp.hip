@@ -67,6 +67,7 @@ struct MlpArgs {
   int64_t M;
   int NB, H, F;
   MlpApply ap;             // used by the APPLY kernels only
+  int rb;                  // rows of a block's row tile (a multiple of 16, at most 16 NT WV)
 };
 
 template <int DK>
@@ -126,8 +127,9 @@ __device__ __forceinline__ void mlp_fwd_block(const T* __restrict__ x, const T* 
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 4, rr = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t wrow0 = static_cast<int64_t>(mt) * (WV * kWaveRows) + wave * kWaveRows;
-  const int64_t rows_left = a.M - wrow0;
+  const int64_t wrow0 = static_cast<int64_t>(mt) * a.rb + wave * kWaveRows;
+  const int64_t tile_end = static_cast<int64_t>(mt + 1) * a.rb < a.M ? static_cast<int64_t>(mt + 1) * a.rb : a.M;
+  const int64_t rows_left = tile_end - wrow0;
   const int nvt = rows_left <= 0 ? 0 : (rows_left >= kWaveRows ? NT : static_cast<int>((rows_left + 15) / 16));
 
   for (int i = tid; i < H; i += 64 * WV) sb1[i] = to_f32(b1[static_cast<int64_t>(band) * H + i]);
@@ -536,12 +538,26 @@ int tanh_tables(hipStream_t stream, const uint16_t** out) {
   return PMSST_OK;
 }
 
+// Rows of a block's row tile.  The blocks run in rounds of one per CU, so a last row tile of a few
+// rows costs a dispatch slot for little work: where the full tile leaves at most an eighth of itself
+// in the last tile and one wave's rows less (full - 32) needs no extra tile, the tiles take full - 32
+// rows (configs[1]: M = 1032 in 4 x 224 + 136 rows instead of 4 x 256 + 8: 1 to 3 us less per launch
+// on each of three boxes, 96-98 -> 93-96 us; 208 and 240 rows were no faster than 256).
+int64_t mlp_row_tile(int64_t M, int64_t full) {
+  const int64_t tiles = (M + full - 1) / full, tail = M - (tiles - 1) * full;
+  const int64_t alt = full - 32;
+  if (M > full && tail <= full / 8 && (M + alt - 1) / alt == tiles) return alt;
+  return full;
+}
+
 template <typename T, int DK, int NT, int WV = 4>
 int launch_dk(const void* x, const void* w1, const void* b1, const void* w2, const void* b2, void* pre, void* out,
               void* hid, const MlpArgs& a, const int64_t* dim_inputs, hipStream_t stream) {
   BandSched sc;
   uint32_t per_xcd = 0;
-  const int64_t rows_per_block = 16 * NT * WV;
+  const int64_t rows_per_block = mlp_row_tile(a.M, 16 * NT * WV);
+  MlpArgs ar = a;
+  ar.rb = static_cast<int>(rows_per_block);
   // an even split of the blocks over the XCDs (units of one band stay contiguous, so its weight chunks
   // are shared in one L2 but at the seams).  Narrow passes (NV 1 or 2) run fewer GEMM2 tiles, but
   // measured they take nearly the time of full ones (a split weighted by MFMA count was slower).
@@ -556,7 +572,7 @@ int launch_dk(const void* x, const void* w1, const void* b1, const void* w2, con
   const T* b2p = static_cast<const T*>(b2);
   auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, dim3(64 * WV), 0, stream, xp, w1p, b1p, w2p, b2p, static_cast<T*>(pre),
-                       static_cast<T*>(out), static_cast<T*>(hid), a, sc);
+                       static_cast<T*>(out), static_cast<T*>(hid), ar, sc);
   };
   if (a.ap.est != nullptr) {
     if (hid != nullptr) go(mlp_fwd_kernel<T, DK, NT, WV, true, true>);

@@ -1283,7 +1283,19 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
 MLP_TILES = {64: (2, 4, 4), 128: (4, 4, 4), 192: (6, 2, 8), 256: (8, 4, 4), 384: (12, 2, 4), 512: (16, 2, 4)}
 
 
-def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, apply=None):
+def mlp_row_tile(M, NT, WV):
+    """mask_mlp.hip mlp_row_tile: the rows of a block's row tile (full - 32 where the full tile would
+    leave at most an eighth of itself in the last tile and full - 32 needs no extra tile)."""
+    full = 16 * NT * WV
+    tiles = cdiv(M, full)
+    tail = M - (tiles - 1) * full
+    alt = full - 32
+    if M > full and tail <= full // 8 and cdiv(M, alt) == tiles:
+        return alt
+    return full
+
+
+def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, apply=None, rb=None):
     """mask_mlp.hip mlp_fwd_kernel (whole depth-2 mask MLP, 16-bit) on its band schedule: the b1 fill,
     the x fragments, the W1 / W2 DMA ring, the LDS fragment reads, the hidden stores and the GLU
     epilogue."""
@@ -1311,7 +1323,12 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
         bnd.fail("mask_mlp: shape outside the host check")
         return bnd
     wave_rows = 16 * NT
-    mtiles = cdiv(M, WV * wave_rows)
+    if rb is None:
+        rb = mlp_row_tile(M, NT, WV)
+    if rb % 16 or not 0 < rb <= WV * wave_rows:
+        bnd.fail("mlp_fwd: row tile not a multiple of 16 within the block's waves")
+        return bnd
+    mtiles = cdiv(M, rb)
     units = lambda b: cdiv(widths[b], J)  # noqa: E731
 
     def nv_of(b, p):  # the kernel's instance: 1, 2 or 4 16-row output groups per half
@@ -1373,8 +1390,8 @@ def replay_mask_mlp_forward(widths, M, D, H, esz, *, write_h=True, wv=None, appl
                     bnd.touch(buf, base + gsrc + c * stride, 16)
                 for stage in range(S):
                     bnd.touch("lds", stage * kStage + ldst + lane * 16, 16)
-            wrow0 = mt * WV * wave_rows + wave * wave_rows
-            left = M - wrow0
+            wrow0 = mt * rb + wave * wave_rows
+            left = min((mt + 1) * rb, M) - wrow0
             nvt = 0 if left <= 0 else (NT if left >= wave_rows else cdiv(left, 16))
             for n in range(NT):
                 m = np.minimum(wrow0 + 16 * n + rr, M - 1)

@@ -47,6 +47,9 @@ CASES = [
     pytest.param(BSR_WIDTHS, 300, 512, 2048, torch.bfloat16, id="configs4-dims-bf16"),
     pytest.param("mel", 700, 192, 768, torch.bfloat16, id="mel60-bf16"),
     pytest.param((4, 8, 12, 400, 64, 128, 4), 77, 128, 96, torch.float16, id="ragged-fp16"),
+    # row tiles one wave shorter than the block (224 + 33 rows at dim 192, 96 + 44 at dim 512)
+    pytest.param(BSR_WIDTHS, 257, 192, 768, torch.bfloat16, id="row-tile-224-bf16"),
+    pytest.param(BSR_WIDTHS, 140, 512, 2048, torch.float16, id="row-tile-96-dim512-fp16"),
 ]
 
 

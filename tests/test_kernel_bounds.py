@@ -98,3 +98,20 @@ def test_grouped_dw_192_column_tiles_stay_in_bounds():
     b = bm.replay_band_split_backward([192] * 100, 100, 776, 2, grouped=True)
     assert b.sizes["lds_dw"] == 3 * 32 * 2 * (64 + 192)
     assert not b.violations()
+
+
+def test_mask_mlp_row_tiles_stay_in_bounds():
+    """The one-pass MLP's row tile: one wave's rows less than the block where the full tile would
+    leave a last tile of at most an eighth (M = 1032 at dim 192: 4 x 224 + 136 rows), the full
+    tile elsewhere; every tile height that is a multiple of 16 replays clean, others are refused."""
+    widths = [8] * 24 + [16] * 12 + [48] * 8 + [96] * 8 + [192] * 8 + [512, 516]
+    assert bm.mlp_row_tile(1032, 2, 8) == 224 and bm.mlp_row_tile(1033, 2, 8) == 224
+    assert bm.mlp_row_tile(1024, 2, 8) == 256 and bm.mlp_row_tile(1896, 2, 8) == 256
+    assert bm.mlp_row_tile(4104, 2, 8) == 256  # 224-row tiles would need two more
+    assert bm.mlp_row_tile(140, 2, 4) == 96 and bm.mlp_row_tile(300, 2, 4) == 128
+    for M, D, H in ((1032, 192, 768), (257, 192, 768), (140, 512, 2048), (31, 192, 768)):
+        assert not bm.replay_mask_mlp_forward(widths, M, D, H, 2).violations(), (M, D)
+    for rb in (160, 176, 192, 208, 224, 240, 256):
+        assert not bm.replay_mask_mlp_forward(widths, 1032, 192, 768, 2, rb=rb).violations(), rb
+    assert bm.replay_mask_mlp_forward(widths, 1032, 192, 768, 2, rb=200).violations()
+    assert bm.replay_mask_mlp_forward(widths, 1032, 192, 768, 2, rb=272).violations()
