@@ -2,7 +2,9 @@
 //   dx[m, g, :] = dy[m, g, :] W_g          (K = out_features = O, the mask MLP's hidden size)
 // dy[M, G, O], W[G, O, I] (group g's [O, I] weight), dx[M, G, I].
 //
-// Block = (group g, row tile): 4 waves x 16 NT rows (NT 2 or 3 at I = 192, picked per shape).  Each
+// Block = (group g, row tile): 4 waves x 16 NT rows (NT 2 or 3 at I = 192, picked per shape); a row
+// tile may be shorter than the block's 64 NT rows (a multiple of 16: the waves past its end only move
+// weight slabs, see gdx_row_tile).  Each
 // wave accumulates dx^T[I x 16 NT] for its rows over the whole K = O in registers.  Per 32-wide K
 // chunk c a ring stage receives, by global -> LDS DMA, the weight slab W_g[32 c .. 32 c + 31][0 .. I)
 // (shared by the 4 waves; read as transposed A fragments, ds_read_b64_tr_b16) and the block's dy tile
@@ -21,6 +23,7 @@ namespace {
 struct GdxArgs {
   int64_t M;
   int G, O, I;
+  int rb;  // rows of a block's row tile (a multiple of 16, at most 64 NT)
 };
 
 template <typename T, int DT, int NT, int S>
@@ -41,8 +44,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   const int O = a.O;
   const int lane = threadIdx.x & 63, gq = lane >> 4, rr = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int64_t wrow0 = static_cast<int64_t>(mt) * (4 * kWaveRows) + wave * kWaveRows;
-  const int64_t left = a.M - wrow0;
+  const int64_t wrow0 = static_cast<int64_t>(mt) * a.rb + wave * kWaveRows;
+  const int64_t tile_end = static_cast<int64_t>(mt + 1) * a.rb < a.M ? static_cast<int64_t>(mt + 1) * a.rb : a.M;
+  const int64_t left = tile_end - wrow0;
   const int nvt = left <= 0 ? 0 : (left >= kWaveRows ? NT : static_cast<int>((left + 15) / 16));
   const int nc = O / 32;
 
@@ -155,15 +159,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   }
 }
 
+// Row tile of the 48-row-wave form: the smallest multiple of 16 rows that keeps the grid in the block
+// rounds the full tile (192 rows) needs.  Every block costs the same K loop, and a round lasts as
+// long as its longest blocks, so shorter tiles on the same rounds shorten the kernel (configs[1],
+// M = 1032, 62 groups: 8 tiles of 144 rows instead of 6 of 192 (5 x 192 + 72), 496 blocks against
+// 372 in one round of two per CU: 50.2-50.5 -> 43.1 us on two boxes; 160 rows 45.6-46.1 us).
+int64_t gdx_row_tile(int64_t M, int64_t groups, int64_t full, int64_t slots) {
+  const int64_t rounds = (groups * ((M + full - 1) / full) + slots - 1) / slots;
+  const int64_t tiles = rounds * slots / groups;  // row tiles that fit in those rounds
+  if (tiles <= 0) return full;
+  const int64_t rb = ((M + tiles - 1) / tiles + 15) / 16 * 16;
+  return rb < full ? rb : full;
+}
+
 template <typename T, int DT, int NT, int S>
-int launch(const void* dy, const void* w, void* dx, const GdxArgs& a, hipStream_t stream) {
+int launch(const void* dy, const void* w, void* dx, const GdxArgs& a, int64_t rows, hipStream_t stream) {
   BandSched sc;
   uint32_t per_xcd = 0;
-  const int64_t rows = 64 * NT;
+  if (rows <= 0 || rows > 64 * NT || rows % 16 != 0)
+    return fail(PMSST_EINVAL, "grouped_linear_backward: row tile %lld outside the block", (long long)rows);
+  GdxArgs ar = a;
+  ar.rb = static_cast<int>(rows);
   if (!build_even_sched(a.G, (a.M + rows - 1) / rows, [](int) { return int64_t{1}; }, &sc, &per_xcd))
     return fail(PMSST_EINVAL, "grouped_linear_backward: too many groups or rows for the block schedule");
   hipLaunchKernelGGL((glin_dx_kernel<T, DT, NT, S>), dim3(per_xcd * kXcds), dim3(256), 0, stream,
-                     static_cast<const T*>(dy), static_cast<const T*>(w), static_cast<T*>(dx), a, sc);
+                     static_cast<const T*>(dy), static_cast<const T*>(w), static_cast<T*>(dx), ar, sc);
   return check_launch("glin_dx_kernel");
 }
 
@@ -183,8 +203,8 @@ int launch_grouped_dx(const void* dy, const void* w, void* dx, int64_t groups, i
                       int64_t out_features, int64_t rows, hipStream_t stream) {
   const GdxArgs a{rows, static_cast<int>(groups), static_cast<int>(out_features), static_cast<int>(in_features)};
   switch (in_features) {
-    case 64: return launch<T, 4, 4, 4>(dy, w, dx, a, stream);
-    case 128: return launch<T, 8, 4, 4>(dy, w, dx, a, stream);
+    case 64: return launch<T, 4, 4, 4>(dy, w, dx, a, 256, stream);
+    case 128: return launch<T, 8, 4, 4>(dy, w, dx, a, 256, stream);
     case 192: {
       // 4 waves of 32 rows (4 ring stages) or of 48 rows (3 stages), both two blocks per CU: the form
       // with fewer block rounds x rows per wave (48 on a tie).  A grid a few blocks past the CUs' slots
@@ -195,10 +215,11 @@ int launch_grouped_dx(const void* dy, const void* w, void* dx, int64_t groups, i
         const int64_t blocks = groups * ((rows + block_rows - 1) / block_rows);
         return (blocks + slots - 1) / slots;
       };
-      if (rounds(192) * 3 <= rounds(128) * 2) return launch<T, 12, 3, 3>(dy, w, dx, a, stream);
-      return launch<T, 12, 2, 4>(dy, w, dx, a, stream);
+      if (rounds(192) * 3 <= rounds(128) * 2)
+        return launch<T, 12, 3, 3>(dy, w, dx, a, gdx_row_tile(rows, groups, 192, slots), stream);
+      return launch<T, 12, 2, 4>(dy, w, dx, a, 128, stream);
     }
-    case 256: return launch<T, 16, 2, 4>(dy, w, dx, a, stream);
+    case 256: return launch<T, 16, 2, 4>(dy, w, dx, a, 128, stream);
     default: return fail(PMSST_EINVAL, "grouped_linear_backward: in_features %lld not supported by glin_dx_kernel",
                          static_cast<long long>(in_features));
   }

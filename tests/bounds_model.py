@@ -688,7 +688,21 @@ def gdx_tiles(I, G, M):
     return (12, 3, 3) if rounds(192) * 3 <= rounds(128) * 2 else GDX_TILES[192]
 
 
-def _replay_glin_dx(bnd, G, I, O, M):
+def gdx_row_tile(M, G, NT):
+    """grouped_dx.hip launch_grouped_dx: the row tile (gdx_row_tile for the 48-row-wave form: the
+    smallest multiple of 16 rows keeping the grid in the full tile's block rounds; the full 64 NT
+    rows otherwise)."""
+    full = 64 * NT
+    if NT != 3:
+        return full
+    rounds = cdiv(G * cdiv(M, full), GDX_SLOTS)
+    tiles = rounds * GDX_SLOTS // G
+    if tiles <= 0:
+        return full
+    return min(full, cdiv(cdiv(M, tiles), 16) * 16)
+
+
+def _replay_glin_dx(bnd, G, I, O, M, rb=None):
     """grouped_dx.hip glin_dx_kernel: the DMA ring of weight slabs and dy tiles, the transposed weight
     fragments, the dy B fragments and the dx stores, on the even block schedule."""
     DT, NT, S = gdx_tiles(I, G, M)
@@ -699,7 +713,12 @@ def _replay_glin_dx(bnd, G, I, O, M):
     bnd.sizes["lds_gdx"] = S * kStage
     if S * kStage > 160 * 1024:
         bnd.fail("glin_dx: more than 160 KB of LDS")
-    mtiles = cdiv(M, 4 * wave_rows)
+    if rb is None:
+        rb = gdx_row_tile(M, G, NT)
+    if rb % 16 or not 0 < rb <= 4 * wave_rows:
+        bnd.fail("glin_dx: row tile not a multiple of 16 within the block's waves")
+        return
+    mtiles = cdiv(M, rb)
     units = lambda b: 1  # noqa: E731
     sc = build_even_sched(G, mtiles, units)
     decoded = sched_decode(sc, G, units, True, bnd, "glin_dx")
@@ -720,8 +739,8 @@ def _replay_glin_dx(bnd, G, I, O, M):
                     bnd.touch("weight", g * O * I * 2 + ((32 * c + kr) * I + 8 * u) * 2, 16)
                 for stage in range(S):
                     bnd.touch("lds_gdx", stage * kStage + t * 1024 + lane * 16, 16)
-            wrow0 = mt * 4 * wave_rows + wave * wave_rows
-            left = M - wrow0
+            wrow0 = mt * rb + wave * wave_rows
+            left = min((mt + 1) * rb, M) - wrow0
             nvt = 0 if left <= 0 else (NT if left >= wave_rows else cdiv(left, 16))
             u = (lane & 3) ^ swz_k(lane >> 2)
             for n in range(nvt):

@@ -128,7 +128,10 @@ def test_empty_rows(hip_ext):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(129, 62, 192, 768), (37, 3, 6, 10), (130, 62, 64, 256), (65, 4, 512, 2048),
-                                   (100, 100, 192, 776)])
+                                   (100, 100, 192, 776),
+                                   # 16-bit dx on 48-row waves with row tiles of 144 (7 x 144 + 25) and
+                                   # 176 rows (15 x 176 + 120) instead of the block's 192
+                                   (1033, 62, 192, 768), (2760, 60, 192, 768)])
 def test_grouped_linear_tanh_forward_and_backward(hip_ext, dtype, shape):
     """Mask-MLP hidden layer: grouped linear with the tanh epilogue, and the grouped-linear backward
     (dx, dW, db) against the oracle; odd widths (6 -> 10) take the unaligned paths.  At 100 groups of

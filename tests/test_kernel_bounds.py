@@ -115,3 +115,24 @@ def test_mask_mlp_row_tiles_stay_in_bounds():
         assert not bm.replay_mask_mlp_forward(widths, 1032, 192, 768, 2, rb=rb).violations(), rb
     assert bm.replay_mask_mlp_forward(widths, 1032, 192, 768, 2, rb=200).violations()
     assert bm.replay_mask_mlp_forward(widths, 1032, 192, 768, 2, rb=272).violations()
+
+
+def test_grouped_dx_row_tiles_stay_in_bounds():
+    """glin_dx's 48-row-wave form takes the smallest multiple of 16 rows that keeps the grid in the
+    full tile's block rounds (configs[1]: 8 tiles of 144 rows in one round of 2 x 256 blocks); every
+    tile height up to the block's 192 rows replays clean, others are refused."""
+    assert bm.gdx_tiles(192, 62, 1032)[1] == 3 and bm.gdx_row_tile(1032, 62, 3) == 144
+    assert 62 * bm.cdiv(1032, 144) <= bm.GDX_SLOTS < 62 * bm.cdiv(1032, 128)
+    assert bm.gdx_row_tile(2760, 60, 3) == 176 and bm.gdx_row_tile(1032, 62, 2) == 128
+
+    def replay(M, G, rb=None):
+        b = bm.Bounds({"dy": M * G * 768 * 2, "weight": G * 768 * 192 * 2, "dx": M * G * 192 * 2,
+                       "lds_gdx": 0})
+        bm._replay_glin_dx(b, G, 192, 768, M, rb=rb)
+        return b.violations()
+
+    for M, G in ((1032, 62), (1033, 62), (2760, 60)):
+        assert not replay(M, G), (M, G)
+    for rb in range(16, 193, 16):
+        assert not replay(1032, 62, rb), rb
+    assert replay(1032, 62, 200) and replay(1032, 62, 208)
