@@ -382,52 +382,55 @@ constexpr int kDpreRows = 64;
 constexpr int kDpreFlatRows = 4;  // 4 rows: 10.9 us at configs[1] against 12.5 us with 8
 constexpr int kDpreFlatMaxBands = 4096;  // band offsets in LDS, 16 KB
 
-// dpre over whole rows (aligned case): thread t takes column quad t % (F / 4) of the
-// kDpreFlatRows rows of row group t / (F / 4), so consecutive threads read consecutive quads of
-// the same rows whatever the band widths (band offsets are multiples of 4, so a quad lies in one
-// band, found by binary search over the offsets staged in LDS).  The rows past M are clamped
-// reads (issued with the others, no branch before the arithmetic) whose results are not stored.
+// dpre over whole rows (aligned case): thread t takes column quad t % (F / 4) of the kDpreFlatRows
+// rows of row group t / (F / 4), so consecutive threads read consecutive quads of the same rows
+// whatever the band widths (band offsets are multiples of 4, so a quad lies in one band, found by
+// binary search over the offsets staged in LDS).  The thread index fits 32 bits (host check), so the
+// row group and quad come from one 32-bit division (a 64-bit one took 0.3 us more at configs[1]).  The
+// rows past M are clamped reads (issued with the others, no branch before the arithmetic) whose
+// results are not stored.
 template <typename T>
 __global__ __launch_bounds__(256) void me_dpre_flat_kernel(const T* __restrict__ gout, const T* __restrict__ pre,
                                                            T* __restrict__ dpre, MaskArgs a) {
   __shared__ int soff[kDpreFlatMaxBands + 1];
   for (int b = threadIdx.x; b <= a.NB; b += 256) soff[b] = static_cast<int>(a.offsets[b]);
   __syncthreads();
-  const int nq = a.F / 4;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t m0 = t / nq * kDpreFlatRows;
+  constexpr int V = 4;
+  const uint32_t nq = static_cast<uint32_t>(a.F / V);
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  const int64_t m0 = static_cast<int64_t>(t / nq) * kDpreFlatRows;
   if (m0 >= a.M) return;
-  const int q = static_cast<int>(t % nq);
-  int lo = 0, hi = a.NB - 1;  // last band with soff[b] <= 4q
+  const int c0 = V * static_cast<int>(t % nq);
+  int lo = 0, hi = a.NB - 1;  // last band with soff[b] <= c0
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (soff[mid] <= 4 * q) lo = mid; else hi = mid - 1;
+    if (soff[mid] <= c0) lo = mid; else hi = mid - 1;
   }
   const int off = soff[lo];
   const int I = soff[lo + 1] - off;
-  const int l = 4 * q - off;
+  const int l = c0 - off;
   const int64_t pitch2 = 2 * static_cast<int64_t>(a.F);
-  float g[kDpreFlatRows][4], L[kDpreFlatRows][4], G[kDpreFlatRows][4];
+  float g[kDpreFlatRows][V], L[kDpreFlatRows][V], G[kDpreFlatRows][V];
 #pragma unroll
   for (int r = 0; r < kDpreFlatRows; ++r) {
     const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;
-    load_pack<T, 4>(gout + m * a.F + 4 * q, g[r]);
-    load_pack<T, 4>(pre + m * pitch2 + 2 * off + l, L[r]);
-    load_pack<T, 4>(pre + m * pitch2 + 2 * off + l + I, G[r]);
+    load_pack<T, V>(gout + m * a.F + c0, g[r]);
+    load_pack<T, V>(pre + m * pitch2 + 2 * off + l, L[r]);
+    load_pack<T, V>(pre + m * pitch2 + 2 * off + l + I, G[r]);
   }
 #pragma unroll
   for (int r = 0; r < kDpreFlatRows; ++r) {
-    float ol[4], og[4];
+    float ol[V], og[V];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < V; ++j) {
       const float sg = sigmoidf_(G[r][j]);
       ol[j] = g[r][j] * sg;
       og[j] = g[r][j] * L[r][j] * sg * (1.0f - sg);
     }
     if (m0 + r < a.M) {
       T* dl = dpre + (m0 + r) * pitch2 + 2 * off + l;
-      store_pack<T, 4>(dl, ol);
-      store_pack<T, 4>(dl + I, og);
+      store_pack<T, V>(dl, ol);
+      store_pack<T, V>(dl + I, og);
     }
   }
 }
@@ -1133,7 +1136,7 @@ int launch_me_bwd(const void* gout, const void* x, const void* pre, const void* 
   if (M > 0) {
     const dim3 g1(static_cast<unsigned>((M + kDpreRows - 1) / kDpreRows), static_cast<unsigned>(hm.NB));
     const int64_t flat_threads = (M + kDpreFlatRows - 1) / kDpreFlatRows * (hm.F / 4);
-    if (a.vec4 && hm.NB <= kDpreFlatMaxBands && (flat_threads + 255) / 256 < (int64_t{1} << 31)) {
+    if (a.vec4 && hm.NB <= kDpreFlatMaxBands && flat_threads + 255 < (int64_t{1} << 31)) {
       hipLaunchKernelGGL((me_dpre_flat_kernel<T>), dim3(static_cast<unsigned>((flat_threads + 255) / 256)), dim3(256),
                          0, stream, static_cast<const T*>(gout), static_cast<const T*>(pre), dpre, a);
     } else

@@ -1195,29 +1195,34 @@ def replay_mask_final_backward(widths, M, H, esz, *, tanh_in=False):
     dz_ring = esz == 2 and (H % 192 == 0 or H % 128 == 0)  # mask_dz.hip me_dz_kernel
     dma_dx = esz == 2 and H % 128 == 0 and not dz_ring
     dma_dw = esz == 2 and M >= CHUNK_K and H % 128 == 0
-    # -- dpre over whole rows
-    nq = F // 4
+    # -- dpre over whole rows: 4 columns per thread
+    V = 4
+    nq = F // V
     rows = 4  # kDpreFlatRows
     flat_threads = cdiv(M, rows) * nq
+    if flat_threads + 255 >= 1 << 31:
+        bnd.fail("dpre: thread index past 32 bits")
     nblk = cdiv(flat_threads, 256)
     tid = np.arange(256)
     for blk in sorted({0, 1, nblk - 1}):
         t = blk * 256 + tid
         m0 = t // nq * rows
         live = m0 < M
-        q = t % nq
-        band = np.searchsorted(offs[:-1], 4 * q, side="right") - 1
+        c0 = V * (t % nq)
+        band = np.searchsorted(offs[:-1], c0, side="right") - 1
         off = offs[band]
         I = offs[band + 1] - off
-        l = 4 * q - off
+        l = c0 - off
+        if np.any(l + V > I):
+            bnd.fail("dpre: a column group crosses a band")
         for r in range(rows):
             m = np.minimum(m0 + r, M - 1)
-            bnd.touch("gout", (m * F + 4 * q) * esz, 4 * esz, live)
-            bnd.touch("pre", (m * 2 * F + 2 * off + l) * esz, 4 * esz, live)
-            bnd.touch("pre", (m * 2 * F + 2 * off + l + I) * esz, 4 * esz, live)
+            bnd.touch("gout", (m * F + c0) * esz, V * esz, live)
+            bnd.touch("pre", (m * 2 * F + 2 * off + l) * esz, V * esz, live)
+            bnd.touch("pre", (m * 2 * F + 2 * off + l + I) * esz, V * esz, live)
             okw = live & (m0 + r < M)
-            bnd.touch("workspace", ((m0 + r) * 2 * F + 2 * off + l) * esz, 4 * esz, okw)
-            bnd.touch("workspace", ((m0 + r) * 2 * F + 2 * off + l + I) * esz, 4 * esz, okw)
+            bnd.touch("workspace", ((m0 + r) * 2 * F + 2 * off + l) * esz, V * esz, okw)
+            bnd.touch("workspace", ((m0 + r) * 2 * F + 2 * off + l + I) * esz, V * esz, okw)
     bnd.touch("lds_flat", np.arange(nb + 1) * 4, 4)
     if dz_ring:
         _replay_me_dz(bnd, widths, offs, M, H, esz, tanh_in)
