@@ -126,7 +126,7 @@ def test_empty_rows(hip_ext):
     assert all(torch.count_nonzero(t).item() == 0 for t in res[1:])
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(129, 62, 192, 768), (37, 3, 6, 10), (130, 62, 64, 256), (65, 4, 512, 2048),
                                    (100, 100, 192, 776),
                                    # 16-bit dx on 48-row waves with row tiles of 144 (7 x 144 + 25) and
